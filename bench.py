@@ -1,0 +1,223 @@
+"""Benchmark of the persistent GRU scan forward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--kinds 0,1,2,3,4] [--no-cpu]
+
+A step is one forward scan (the drop-in ``gru_scan_*`` call) over one batch
+of synthetic input already resident in HBM. The headline line is the dense
+fp32 scan at T=64, B=32, H=512 (config 1, the configuration the metric is
+quoted on); the other four configurations are measured in the same run and
+reported under "kinds".
+
+Per kind:
+  ms_per_step  host wall time of K back-to-back calls / K (synchronised on
+               both sides), i.e. what a caller of the Python API sees;
+  kernel_ms    average device duration of one launch, from HIP events around
+               each launch while the queue is kept ahead of the GPU, so host
+               overhead is not counted (this feeds the roofline);
+  roofline     algorithmic bytes or FLOPs per launch / kernel_ms against the
+               MI355X peak (HBM 8 TB/s; fp32 MFMA 157.3 TFLOP/s);
+  cpu_baseline the oracle (the reference's per-step PyTorch CPU path) timed on
+               this host's cores on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "gru-triton_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+# Algorithmic work per launch at the benchmark shapes (bytes: gi + out + hidden
+# weights + h0 + bias; FLOPs: the hidden projection only).
+WORK = {
+    0: {"bytes": 16_855_040, "flops": 3 * 64 * 32 * 512, "bound": "hbm"},
+    1: {"bytes": 19_994_624, "flops": 3_221_225_472, "bound": "mfma"},
+    2: {"bytes": 19_994_624, "flops": 3_221_225_472, "bound": "mfma"},
+    3: {"bytes": 17_635_328, "flops": 805_306_368, "bound": "mfma"},
+    4: {"bytes": 537_391_104, "flops": 3_019_898_880, "bound": "hbm"},
+}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def roofline(idx: int, kernel_ms: float) -> dict:
+    w = WORK[idx]
+    traffic = None
+    try:
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get(str(idx))
+    except (OSError, ValueError):
+        traffic = None
+    if w["bound"] == "hbm":
+        achieved = w["bytes"] / (kernel_ms * 1e-3) / 1e9
+        return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic}
+    achieved = w["flops"] / (kernel_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 4), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 5), "traffic": traffic}
+
+
+def time_kind(idx: int, steps: int, warmup: int, dev) -> dict:
+    import torch
+
+    from gru_qat_amd.configs import NAMES, SHAPES, make_config, run_config
+
+    cfg = make_config(idx, device=dev)
+    for _ in range(warmup):
+        run_config(cfg)
+    torch.cuda.synchronize(dev)
+
+    # Whole-call time as a caller sees it.
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run_config(cfg)
+    torch.cuda.synchronize(dev)
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+
+    # Device time per launch: keep the queue ahead of the GPU with a sleep
+    # kernel, then bracket every launch with events on the launch stream.
+    stream = torch.cuda.current_stream(dev)
+    durs = []
+    reps = max(steps, 30)
+    done = 0
+    while done < reps:
+        n = min(50, reps - done)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        torch.cuda._sleep(int(2e7))
+        for a, b in ev:
+            a.record(stream)
+            run_config(cfg)
+            b.record(stream)
+        torch.cuda.synchronize(dev)
+        durs += [a.elapsed_time(b) for a, b in ev]
+        done += n
+    kernel_ms = statistics.mean(durs)
+    T, B, H = SHAPES[idx]
+    return {
+        "name": NAMES[idx],
+        "shape": {"T": T, "B": B, "H": H},
+        "ms_per_step": round(wall_ms, 5),
+        "kernel_ms": round(kernel_ms, 5),
+        "kernel_ms_median": round(statistics.median(durs), 5),
+        "tokens_per_s": round(T * B / (wall_ms * 1e-3), 1),
+        "kernel_tokens_per_s": round(T * B / (kernel_ms * 1e-3), 1),
+        "roofline": roofline(idx, kernel_ms),
+    }
+
+
+def cpu_baseline(idx: int, budget_s: float) -> dict:
+    import torch
+
+    from gru_qat_amd.configs import make_config
+    from oracle import gru_oracle as O
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    cfg = make_config(idx)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        O.scan_config(cfg)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s or len(times) >= 50:
+            break
+    ms = statistics.median(times) * 1e3
+    return {"value": round(ms, 3), "unit": "ms/iter", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{len(times)} full iterations of config {idx} (median), torch CPU restatement of the "
+                      f"reference per-step path"}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--kinds", default="0,1,2,3,4")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=4.0, help="seconds of CPU baseline per kind")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(batch sharding across GPUs is not part of this build); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import gru_qat_amd
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    gru_qat_amd.load_library()
+    kinds = [int(k) for k in args.kinds.split(",") if k.strip()]
+
+    results = {}
+    for idx in kinds:
+        print(f"[bench] config {idx} ...", file=sys.stderr, flush=True)
+        results[idx] = time_kind(idx, args.steps, args.warmup, dev)
+        print(f"[bench] config {idx}: {json.dumps(results[idx])}", file=sys.stderr, flush=True)
+    faults = gru_qat_amd.workspace_faults(dev)
+
+    cpu = {}
+    if not args.no_cpu:
+        for idx in kinds:
+            print(f"[bench] cpu baseline config {idx} ...", file=sys.stderr, flush=True)
+            cpu[idx] = cpu_baseline(idx, args.cpu_budget)
+            results[idx]["cpu_baseline"] = cpu[idx]
+
+    head = 1 if 1 in results else kinds[0]
+    r = results[head]
+    props = torch.cuda.get_device_properties(dev)
+    line = {
+        "metric": "ms/iter scan fwd at T=64,B=32,H=512 per kind; % of HBM/MFMA roofline",
+        "value": r["ms_per_step"],
+        "unit": "ms/iter",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": r["ms_per_step"],
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded CPU generator, BASELINE.json config distributions)",
+        "config": {"workload": f"config {head}: {r['name']} T={r['shape']['T']} B={r['shape']['B']} "
+                               f"H={r['shape']['H']}", "kind": r["name"], **r["shape"]},
+        "tokens_per_s": r["tokens_per_s"],
+        "kernel_ms": r["kernel_ms"],
+        "roofline": r["roofline"],
+        "cpu_baseline": cpu.get(head),
+        "kinds": {str(k): v for k, v in results.items()},
+        "device": {"name": props.name, "cus": props.multi_processor_count, "host_cpu": cpu_model(),
+                   "host_cores": os.cpu_count()},
+        "barrier_faults": faults,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if faults == 0 else 1
+
+
+if __name__ == "__main__":
+    sys.exit(main())

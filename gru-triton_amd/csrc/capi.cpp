@@ -1,0 +1,112 @@
+// C-ABI plumbing of libgruscan.so: error text, validation, workspace sizing and
+// the workspace fault-word readback. The kernels and their launchers live in
+// scan_*.hip.
+#include <cstring>
+
+#include "gs_host.h"
+
+namespace gs {
+
+static thread_local std::string g_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error.assign(buf);
+  return code;
+}
+
+const char* last_error() { return g_error.c_str(); }
+void clear_error() { g_error.clear(); }
+
+int validate_quant(const gs_quant& q, const char* name, const char* who) {
+  if (!q.enabled) return GS_OK;
+  if (!(std::isfinite(q.scale) && q.scale > 0.0f))
+    return set_error(GS_ERR_INVALID, "%s: %s scale must be finite and > 0; got %g", who, name,
+                     (double)q.scale);
+  if (q.qmin > q.qmax)
+    return set_error(GS_ERR_INVALID, "%s: %s qmin (%d) must be <= qmax (%d)", who, name, q.qmin,
+                     q.qmax);
+  return GS_OK;
+}
+
+int validate_common(const gs_args* a, const char* who) {
+  if (a == nullptr) return set_error(GS_ERR_INVALID, "%s: args is NULL", who);
+  if (a->T < 1) return set_error(GS_ERR_INVALID, "%s: seq length T must be > 0; got T=%lld", who, (long long)a->T);
+  if (a->B < 1) return set_error(GS_ERR_INVALID, "%s: batch size B must be > 0; got B=%lld", who, (long long)a->B);
+  if (a->H < 1) return set_error(GS_ERR_INVALID, "%s: hidden size H must be > 0; got H=%lld", who, (long long)a->H);
+  if (a->T > (1ll << 30) || a->B > (1ll << 24) || a->H > (1ll << 20))
+    return set_error(GS_ERR_INVALID, "%s: T/B/H out of supported range (T=%lld, B=%lld, H=%lld)", who,
+                     (long long)a->T, (long long)a->B, (long long)a->H);
+  if (!a->gi || !a->h0 || !a->w || !a->bh || !a->out)
+    return set_error(GS_ERR_INVALID, "%s: gi, h0, w, bh and out must be non-NULL device pointers", who);
+  // Rows of one step must not overlap, and steps must not overlap each other.
+  if ((a->B > 1 && a->sg_b < 3 * a->H) || (a->T > 1 && a->sg_t < a->sg_b * (a->B - 1) + 3 * a->H))
+    return set_error(GS_ERR_INVALID, "%s: gi strides (sg_t=%lld, sg_b=%lld) do not describe a [T, B, 3H] tensor", who,
+                     (long long)a->sg_t, (long long)a->sg_b);
+  if ((a->B > 1 && a->so_b < a->H) || (a->T > 1 && a->so_t < a->so_b * (a->B - 1) + a->H))
+    return set_error(GS_ERR_INVALID, "%s: out strides (so_t=%lld, so_b=%lld) do not describe a [T, B, H] tensor", who,
+                     (long long)a->so_t, (long long)a->so_b);
+  if (a->sh0_b < a->H && a->B > 1)
+    return set_error(GS_ERR_INVALID, "%s: h0 stride sh0_b=%lld < H=%lld", who, (long long)a->sh0_b, (long long)a->H);
+  int rc = validate_quant(a->q_in, "h_in_quant", who);
+  if (rc) return rc;
+  return validate_quant(a->q_out, "h_out_quant", who);
+}
+
+int check_workspace(const gs_args* a, int64_t need, const char* who) {
+  if (need <= 0) return GS_OK;
+  if (a->workspace == nullptr || a->workspace_bytes < need)
+    return set_error(GS_ERR_INVALID, "%s: workspace of %lld bytes required; got %lld at %p", who,
+                     (long long)need, (long long)a->workspace_bytes, a->workspace);
+  if ((reinterpret_cast<uintptr_t>(a->workspace) & 255u) != 0)
+    return set_error(GS_ERR_INVALID, "%s: workspace must be 256-byte aligned", who);
+  return GS_OK;
+}
+
+}  // namespace gs
+
+// Defined in the kernel translation units.
+namespace gs {
+int64_t dense_workspace_bytes(const gs_args* a);
+int64_t monarch_workspace_bytes(const gs_args* a);
+}  // namespace gs
+
+extern "C" {
+
+int64_t gs_workspace_bytes(int kind, const gs_args* a) {
+  if (a == nullptr) return gs::set_error(GS_ERR_INVALID, "gs_workspace_bytes: args is NULL");
+  switch (kind) {
+    case GS_KIND_DENSE:
+      return gs::dense_workspace_bytes(a);
+    case GS_KIND_MONARCH:
+      return gs::monarch_workspace_bytes(a);
+    case GS_KIND_DIAGONAL:
+    case GS_KIND_BUTTERFLY:
+      return gs::kCtrlBytes;
+    default:
+      return gs::set_error(GS_ERR_INVALID, "gs_workspace_bytes: unknown kind %d", kind);
+  }
+}
+
+int gs_workspace_status(void* ws, int64_t bytes, hipStream_t stream) {
+  if (ws == nullptr || bytes < gs::kCtrlBytes)
+    return gs::set_error(GS_ERR_INVALID, "gs_workspace_status: workspace too small or NULL");
+  GS_CHECK_HIP(hipStreamSynchronize(stream));
+  uint32_t word = 0;
+  GS_CHECK_HIP(hipMemcpy(&word, ws, sizeof(word), hipMemcpyDeviceToHost));
+  if (word != 0) {
+    const uint32_t zero = 0;
+    GS_CHECK_HIP(hipMemcpy(ws, &zero, sizeof(zero), hipMemcpyHostToDevice));
+  }
+  return (int)word;
+}
+
+const char* gs_last_error(void) { return gs::last_error(); }
+
+int gs_abi_version(void) { return GS_ABI_VERSION; }
+
+}  // extern "C"

@@ -1,0 +1,60 @@
+// Host-side helpers shared by the C-ABI entry points: per-thread error text,
+// argument validation and the workspace layout.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/gruscan.h"
+#include "gs_device.h"
+
+namespace gs {
+
+int set_error(int code, const char* fmt, ...);
+const char* last_error();
+void clear_error();
+
+#define GS_CHECK_HIP(expr)                                                                  \
+  do {                                                                                      \
+    hipError_t _e = (expr);                                                                 \
+    if (_e != hipSuccess)                                                                   \
+      return ::gs::set_error(GS_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(_e));   \
+  } while (0)
+
+// Workspace layout (bytes from the start):
+//   [0, 256)                 control words: fault flag at word 0, exit count at word 32
+//   [256, 256 + 256*ngroups) one arrival counter per group, 256 B apart
+//   then float exchange buffers, each starting on a 256-byte boundary.
+constexpr int64_t kCtrlBytes = 256;
+constexpr int64_t kCounterBytes = 4 * kCounterStride;
+
+inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
+
+inline Ctrl ctrl_of(void* ws) {
+  uint32_t* w = static_cast<uint32_t*>(ws);
+  return Ctrl{w, w + 32, w + kCtrlBytes / 4};
+}
+
+inline Quant to_quant(const gs_quant& q) {
+  return Quant{q.scale, (float)q.qmin, (float)q.qmax, q.enabled != 0};
+}
+
+// The two quantizers are the same map when both are on with equal parameters.
+// Then q_in(q_out(x)) == q_out(x) bit for bit: for |code| <= 2^22 the product
+// code*s divided by s rounds back to the code, so the carried h can be read as
+// the matmul-side h without applying q_in again.
+inline bool same_quant(const gs_quant& a, const gs_quant& b) {
+  return a.enabled && b.enabled && a.scale == b.scale && a.qmin == b.qmin && a.qmax == b.qmax &&
+         std::fabs((double)a.qmin) <= 4194304.0 && std::fabs((double)a.qmax) <= 4194304.0;
+}
+
+int validate_common(const gs_args* a, const char* who);
+int validate_quant(const gs_quant& q, const char* name, const char* who);
+int check_workspace(const gs_args* a, int64_t need, const char* who);
+
+}  // namespace gs

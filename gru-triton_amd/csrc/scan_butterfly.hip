@@ -1,0 +1,329 @@
+// Butterfly-hidden GRU scan forward (gfx950).
+//
+// Reference: LarocheC/gru-triton src/gru_qat/triton_kernels/scan_butterfly.py:168-366
+// (kernel) and :369-459 (launcher). Twiddles are [3, nchains, L, N/2, 2, 2]
+// with N = 2^L >= H. Chain c runs L stages; stage s uses stride 2^ls with
+// ls = s for even c and L-1-s for odd c (scan_butterfly.py:276-283). Element i
+// of a stage mixes with its partner i ^ stride:
+//   m    = (i >> ls) & 1,  pair = (i >> (ls+1)) * stride + (i & (stride-1))
+//   y[i] = tw[g, c, s, pair, m, m] * x[i] + tw[g, c, s, pair, m, 1-m] * x[i ^ stride]
+// (scan_butterfly.py:284-312). The input is q_in(h) zero-padded to N; gh is
+// the first H outputs plus bh. Batch rows are independent, so one workgroup
+// owns one batch row for all T steps and no grid barrier is needed.
+//
+// Unlike the reference kernel, which updates its scratch in place inside a
+// stage, every stage here reads the previous stage's values only (register
+// copies or a separate LDS buffer), so no stage can observe a partly updated
+// vector.
+#include "gs_host.h"
+
+namespace gs {
+namespace {
+
+struct BParams {
+  const float* gi;
+  const float* h0;
+  const float* tw;
+  const float* bh;
+  float* out;
+  int64_t sg_t, sg_b, sh0_b, so_t, so_b;
+  int T, B, H;
+  int logn, nchains;
+  Quant qin, qout;
+  int qin_after_first;
+};
+
+__device__ __forceinline__ int pair_index(int i, int ls) {
+  return ((i >> (ls + 1)) << ls) | (i & ((1 << ls) - 1));
+}
+
+// ---------------------------------------------------------------------------------
+// Generic kernel: any N = 2^logn <= 4096, any number of chains. The three gate
+// vectors live in LDS (ping-pong between stages); twiddles are read from
+// global memory (they stay in L1/L2: 24*N*L*nchains bytes in total).
+// ---------------------------------------------------------------------------------
+constexpr int kGenericThreads = 256;
+
+__global__ __launch_bounds__(kGenericThreads) void butterfly_generic_kernel(BParams p) {
+  extern __shared__ float lds[];
+  const int N = 1 << p.logn;
+  const int L = p.logn;
+  float* buf0 = lds;              // [3][N]
+  float* buf1 = lds + 3 * N;      // [3][N]
+  float* hraw = lds + 6 * N;      // [N] raw h of this row
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int H = p.H;
+
+  for (int i = tid; i < N; i += kGenericThreads) {
+    float h = (i < H) ? p.h0[(int64_t)b * p.sh0_b + i] : 0.0f;
+    hraw[i] = h;
+    const float hq = (i < H && p.qin.on) ? fake_quant(h, p.qin) : h;
+    buf0[i] = hq;
+    buf0[N + i] = hq;
+    buf0[2 * N + i] = hq;
+  }
+  __syncthreads();
+
+  float* cur = buf0;
+  float* nxt = buf1;
+  for (int t = 0; t < p.T; ++t) {
+    for (int c = 0; c < p.nchains; ++c) {
+      for (int s = 0; s < L; ++s) {
+        const int ls = (c & 1) ? (L - 1 - s) : s;
+        const int stride = 1 << ls;
+        for (int idx = tid; idx < 3 * N; idx += kGenericThreads) {
+          const int g = idx >> L;
+          const int i = idx & (N - 1);
+          const int m = (i >> ls) & 1;
+          const int64_t base =
+              ((((int64_t)g * p.nchains + c) * L + s) * (N / 2) + pair_index(i, ls)) * 4 + 2 * m;
+          const float tss = p.tw[base + m];
+          const float tsp = p.tw[base + 1 - m];
+          nxt[g * N + i] = tss * cur[g * N + i] + tsp * cur[g * N + (i ^ stride)];
+        }
+        __syncthreads();
+        float* tmp = cur;
+        cur = nxt;
+        nxt = tmp;
+      }
+    }
+    // Gate epilogue; writes next step's matmul-side h into nxt.
+    for (int i = tid; i < N; i += kGenericThreads) {
+      float hq = 0.0f;
+      if (i < H) {
+        const float* g = p.gi + (int64_t)t * p.sg_t + (int64_t)b * p.sg_b + i;
+        const float ghr = cur[i] + p.bh[i];
+        const float ghz = cur[N + i] + p.bh[H + i];
+        const float ghn = cur[2 * N + i] + p.bh[2 * H + i];
+        float hn = gru_update(g[0], g[H], g[2 * H], ghr, ghz, ghn, hraw[i]);
+        if (p.qout.on) hn = fake_quant(hn, p.qout);
+        p.out[(int64_t)t * p.so_t + (int64_t)b * p.so_b + i] = hn;
+        hraw[i] = hn;
+        hq = (p.qin.on && p.qin_after_first) ? fake_quant(hn, p.qin) : hn;
+      }
+      nxt[i] = hq;
+      nxt[N + i] = hq;
+      nxt[2 * N + i] = hq;
+    }
+    __syncthreads();
+    float* tmp = cur;
+    cur = nxt;
+    nxt = tmp;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Register kernel: one chain, N in {256, 512, 1024}. Each gate's vector is
+// spread over WPG = N/256 waves; lane l of gate wave w holds elements
+// i = l + 64*r + 256*w for r = 0..3. Stages with stride < 64 swap across
+// lanes, strides 64 and 128 pair registers inside a lane, strides >= 256 go
+// through LDS between the gate's waves. Each lane keeps the two twiddles of
+// each of its 4 elements for all L stages in registers (8L values), loaded
+// once. The gate epilogue for element i runs on the gate-r wave that holds i,
+// which reads gh_z and gh_n from LDS and broadcasts the next q_in(h) back.
+// ---------------------------------------------------------------------------------
+template <int LOGN>
+__global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BParams p) {
+  constexpr int N = 1 << LOGN;
+  constexpr int L = LOGN;
+  constexpr int WPG = N / 256;
+  __shared__ float xch[2][3][N];
+  __shared__ float ghs[3][N];
+  __shared__ float hqs[N];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int g = wv / WPG;
+  const int w = wv - g * WPG;
+  const int b = blockIdx.x;
+  const int H = p.H;
+
+  int idx[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) idx[r] = lane + 64 * r + 256 * w;
+
+  float tss[L][4], tsp[L][4];
+#pragma unroll
+  for (int s = 0; s < L; ++s) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = idx[r];
+      const int m = (i >> s) & 1;
+      const int64_t base = (((int64_t)g * L + s) * (N / 2) + pair_index(i, s)) * 4 + 2 * m;
+      tss[s][r] = p.tw[base + m];
+      tsp[s][r] = p.tw[base + 1 - m];
+    }
+  }
+
+  float x[4], hraw[4], bias[3][4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = idx[r];
+    const float h = (i < H) ? p.h0[(int64_t)b * p.sh0_b + i] : 0.0f;
+    hraw[r] = h;
+    x[r] = (i < H && p.qin.on) ? fake_quant(h, p.qin) : h;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) bias[q][r] = (i < H) ? p.bh[q * H + i] : 0.0f;
+  }
+
+  for (int t = 0; t < p.T; ++t) {
+    float gir[4], giz[4], gin[4];
+    if (g == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = idx[r];
+        if (i < H) {
+          const float* gp = p.gi + (int64_t)t * p.sg_t + (int64_t)b * p.sg_b + i;
+          gir[r] = gp[0];
+          giz[r] = gp[H];
+          gin[r] = gp[2 * H];
+        } else {
+          gir[r] = giz[r] = gin[r] = 0.0f;
+        }
+      }
+    }
+    int xsel = 0;
+#pragma unroll
+    for (int s = 0; s < L; ++s) {
+      float y[4];
+      if (s < 6) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = lane_xor(x[r], 1 << s);
+      } else if (s < 8) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = x[r ^ (1 << (s - 6))];
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xch[xsel][g][idx[r]] = x[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = xch[xsel][g][idx[r] ^ (1 << s)];
+        xsel ^= 1;
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = tss[s][r] * x[r] + tsp[s][r] * y[r];
+    }
+    if (g != 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ghs[g][idx[r]] = x[r];
+    }
+    __syncthreads();
+    if (g == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = idx[r];
+        const float ghr = x[r] + bias[0][r];
+        const float ghz = ghs[1][i] + bias[1][r];
+        const float ghn = ghs[2][i] + bias[2][r];
+        float hn = gru_update(gir[r], giz[r], gin[r], ghr, ghz, ghn, hraw[r]);
+        if (p.qout.on) hn = fake_quant(hn, p.qout);
+        float hq = 0.0f;
+        if (i < H) {
+          p.out[(int64_t)t * p.so_t + (int64_t)b * p.so_b + i] = hn;
+          hraw[r] = hn;
+          hq = (p.qin.on && p.qin_after_first) ? fake_quant(hn, p.qin) : hn;
+        }
+        hqs[i] = hq;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = hqs[idx[r]];
+  }
+}
+
+int launch_generic(const BParams& p, hipStream_t stream) {
+  const size_t lds = (size_t)7 * ((size_t)1 << p.logn) * sizeof(float);
+  if (lds > 65536)
+    GS_CHECK_HIP(hipFuncSetAttribute((const void*)butterfly_generic_kernel,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+  hipLaunchKernelGGL(butterfly_generic_kernel, dim3((unsigned)p.B), dim3(kGenericThreads), lds, stream, p);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_butterfly_fwd(const gs_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_butterfly_fwd";
+  int rc = validate_common(a, who);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the butterfly kind", who);
+  if (a->log_n < 1 || a->log_n > 12 || (int64_t(1) << a->log_n) < a->H)
+    return set_error(GS_ERR_INVALID,
+                     "%s: twiddles imply H_PAD=2^%lld, which must be >= H=%lld, >= 2 and <= 4096", who,
+                     (long long)a->log_n, (long long)a->H);
+  if (a->bfly_nblocks < 1 || a->bfly_nblocks > 64)
+    return set_error(GS_ERR_INVALID, "%s: butterfly nblocks must be in [1, 64]; got %lld", who,
+                     (long long)a->bfly_nblocks);
+
+  BParams p;
+  p.gi = a->gi;
+  p.h0 = a->h0;
+  p.tw = a->w;
+  p.bh = a->bh;
+  p.out = a->out;
+  p.sg_t = a->sg_t;
+  p.sg_b = a->sg_b;
+  p.sh0_b = a->sh0_b;
+  p.so_t = a->so_t;
+  p.so_b = a->so_b;
+  p.T = (int)a->T;
+  p.B = (int)a->B;
+  p.H = (int)a->H;
+  p.logn = (int)a->log_n;
+  p.nchains = (int)a->bfly_nblocks;
+  p.qin = to_quant(a->q_in);
+  p.qout = to_quant(a->q_out);
+  p.qin_after_first = !same_quant(a->q_in, a->q_out);
+
+  const dim3 grid((unsigned)a->B);
+  if (p.nchains == 1 && p.logn == 10) {
+    hipLaunchKernelGGL(butterfly_reg_kernel<10>, grid, dim3(768), 0, stream, p);
+  } else if (p.nchains == 1 && p.logn == 9) {
+    hipLaunchKernelGGL(butterfly_reg_kernel<9>, grid, dim3(384), 0, stream, p);
+  } else if (p.nchains == 1 && p.logn == 8) {
+    hipLaunchKernelGGL(butterfly_reg_kernel<8>, grid, dim3(192), 0, stream, p);
+  } else {
+    return launch_generic(p, stream);
+  }
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
+
+// Test hook: forces the generic kernel regardless of shape, so tests can run
+// both implementations on one input. Same contract as gs_butterfly_fwd.
+extern "C" int gs_butterfly_fwd_generic(const gs_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_butterfly_fwd_generic";
+  int rc = validate_common(a, who);
+  if (rc) return rc;
+  if (a->log_n < 1 || a->log_n > 12 || (int64_t(1) << a->log_n) < a->H || a->bfly_nblocks < 1 ||
+      a->bfly_nblocks > 64 || a->w2 != nullptr)
+    return set_error(GS_ERR_INVALID, "%s: bad butterfly shape", who);
+  BParams p;
+  p.gi = a->gi;
+  p.h0 = a->h0;
+  p.tw = a->w;
+  p.bh = a->bh;
+  p.out = a->out;
+  p.sg_t = a->sg_t;
+  p.sg_b = a->sg_b;
+  p.sh0_b = a->sh0_b;
+  p.so_t = a->so_t;
+  p.so_b = a->so_b;
+  p.T = (int)a->T;
+  p.B = (int)a->B;
+  p.H = (int)a->H;
+  p.logn = (int)a->log_n;
+  p.nchains = (int)a->bfly_nblocks;
+  p.qin = to_quant(a->q_in);
+  p.qout = to_quant(a->q_out);
+  p.qin_after_first = !same_quant(a->q_in, a->q_out);
+  return launch_generic(p, stream);
+}

@@ -1,0 +1,129 @@
+// Diagonal-hidden GRU scan forward (gfx950).
+//
+// Reference: LarocheC/gru-triton src/gru_qat/triton_kernels/scan_diagonal.py:127-223
+// (kernel) and :226-282 (launcher); math of the PyTorch oracle :79-124.
+//
+// gh_g = w_g * q_in(h) + b_g is elementwise, so every (b, j) lane is an
+// independent scalar GRU: one thread owns one lane for all T steps and keeps h
+// in a register. There is no cross-thread traffic at all. The step chain is
+// latency bound (a few dozen dependent VALU ops), so the kernel's job is to
+// keep HBM latency off that chain: gi for the next kDepth steps is always in
+// flight while the current kDepth steps compute, and out[t] stores are
+// fire-and-forget. Loads of gi[t, b, g*H + j] for consecutive threads are
+// consecutive floats, so each wave reads 256 contiguous bytes per gate.
+#include "gs_host.h"
+
+namespace gs {
+namespace {
+
+constexpr int kDepth = 8;    // steps of gi prefetched ahead
+constexpr int kThreads = 256;
+
+struct DiagParams {
+  const float* gi;
+  const float* h0;
+  const float* w;
+  const float* bh;
+  float* out;
+  int64_t sg_t, sg_b, sh0_b, so_t, so_b;
+  int T, B, H;
+  Quant qin, qout;
+  int qin_after_first;  // 0: q_in is the identity on carried h for t >= 1
+};
+
+__global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
+  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (e >= (int64_t)p.B * p.H) return;
+  const int b = (int)(e / p.H);
+  const int j = (int)(e - (int64_t)b * p.H);
+  const int H = p.H;
+
+  const float wr = p.w[j], wz = p.w[H + j], wn = p.w[2 * H + j];
+  const float br = p.bh[j], bz = p.bh[H + j], bn = p.bh[2 * H + j];
+  float h = p.h0[(int64_t)b * p.sh0_b + j];
+
+  const float* gib = p.gi + (int64_t)b * p.sg_b + j;
+  float* outb = p.out + (int64_t)b * p.so_b + j;
+
+  float cr[kDepth], cz[kDepth], cn[kDepth];
+#pragma unroll
+  for (int i = 0; i < kDepth; ++i) {
+    if (i < p.T) {
+      const float* g = gib + (int64_t)i * p.sg_t;
+      cr[i] = g[0];
+      cz[i] = g[H];
+      cn[i] = g[2 * H];
+    }
+  }
+
+  for (int t0 = 0; t0 < p.T; t0 += kDepth) {
+    float nr[kDepth], nz[kDepth], nn[kDepth];
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      const int t = t0 + kDepth + i;
+      if (t < p.T) {
+        const float* g = gib + (int64_t)t * p.sg_t;
+        nr[i] = g[0];
+        nz[i] = g[H];
+        nn[i] = g[2 * H];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      const int t = t0 + i;
+      if (t < p.T) {
+        float hq = h;
+        if (p.qin.on && (t == 0 || p.qin_after_first)) hq = fake_quant(h, p.qin);
+        const float ghr = mul_add_nofma(wr, hq, br);
+        const float ghz = mul_add_nofma(wz, hq, bz);
+        const float ghn = mul_add_nofma(wn, hq, bn);
+        float hn = gru_update(cr[i], cz[i], cn[i], ghr, ghz, ghn, h);
+        if (p.qout.on) hn = fake_quant(hn, p.qout);
+        outb[(int64_t)t * p.so_t] = hn;
+        h = hn;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      cr[i] = nr[i];
+      cz[i] = nz[i];
+      cn[i] = nn[i];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_diagonal_fwd(const gs_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_diagonal_fwd";
+  int rc = validate_common(a, who);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the diagonal kind", who);
+
+  DiagParams p;
+  p.gi = a->gi;
+  p.h0 = a->h0;
+  p.w = a->w;
+  p.bh = a->bh;
+  p.out = a->out;
+  p.sg_t = a->sg_t;
+  p.sg_b = a->sg_b;
+  p.sh0_b = a->sh0_b;
+  p.so_t = a->so_t;
+  p.so_b = a->so_b;
+  p.T = (int)a->T;
+  p.B = (int)a->B;
+  p.H = (int)a->H;
+  p.qin = to_quant(a->q_in);
+  p.qout = to_quant(a->q_out);
+  p.qin_after_first = !(same_quant(a->q_in, a->q_out));
+
+  const int64_t n = a->B * a->H;
+  const dim3 grid((unsigned)((n + kThreads - 1) / kThreads));
+  hipLaunchKernelGGL(diagonal_fwd_kernel, grid, dim3(kThreads), 0, stream, p);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}

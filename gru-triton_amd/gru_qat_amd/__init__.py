@@ -1,0 +1,46 @@
+"""gru_qat_amd: MI355X-native persistent GRU scan (forward on hand-written
+gfx950 HIP kernels behind the C ABI of libgruscan.so).
+
+Drop-in replacements for the scan entry points of LarocheC/gru-triton
+(gru_qat.triton_kernels.scan*), keeping their names, signatures and error
+types.
+"""
+
+from .scan import (
+    GRUScanFunction,
+    GRUScanPersistentFunction,
+    gru_scan,
+    gru_scan_forward,
+    gru_scan_forward_persistent,
+    gru_scan_persistent,
+)
+from .scan_butterfly import (
+    extract_butterfly_twiddles,
+    gru_scan_butterfly_forward,
+    gru_scan_butterfly_persistent,
+    gru_scan_butterfly_triton,
+)
+from .scan_diagonal import extract_diagonal_factors, gru_scan_diagonal, gru_scan_diagonal_forward
+from .scan_monarch import extract_monarch_factors, gru_scan_monarch, gru_scan_monarch_forward
+from ._lib import load as load_library, workspace_faults
+
+__all__ = [
+    "GRUScanFunction",
+    "GRUScanPersistentFunction",
+    "extract_butterfly_twiddles",
+    "extract_diagonal_factors",
+    "extract_monarch_factors",
+    "gru_scan",
+    "gru_scan_butterfly_forward",
+    "gru_scan_butterfly_persistent",
+    "gru_scan_butterfly_triton",
+    "gru_scan_diagonal",
+    "gru_scan_diagonal_forward",
+    "gru_scan_forward",
+    "gru_scan_forward_persistent",
+    "gru_scan_monarch",
+    "gru_scan_monarch_forward",
+    "gru_scan_persistent",
+    "load_library",
+    "workspace_faults",
+]

@@ -1,0 +1,70 @@
+"""Argument validation shared by the scan wrappers.
+
+Errors are ``ValueError`` (device, dtype, shape, quant tuple) or
+``RuntimeError`` (capacity, HIP), never ``AssertionError``, so they survive
+``python -O`` (reference contract: tests/test_scan_wrapper_validation.py:47-49).
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+QuantTuple = Optional[Tuple[float, int, int]]
+
+
+def require_cuda(who: str, **tensors: torch.Tensor) -> None:
+    bad = {k: v.device for k, v in tensors.items() if not (isinstance(v, torch.Tensor) and v.is_cuda)}
+    if bad:
+        devs = ", ".join(f"{k}={v.device if isinstance(v, torch.Tensor) else type(v).__name__}"
+                         for k, v in tensors.items())
+        names = ", ".join(tensors)
+        raise ValueError(f"{who}: {names} must all be CUDA (HIP) tensors; got devices {devs}")
+    dev = next(iter(tensors.values())).device
+    other = {k: v.device for k, v in tensors.items() if v.device != dev}
+    if other:
+        raise ValueError(f"{who}: all tensors must be on {dev}; got {other}")
+
+
+def require_f32(who: str, **tensors: torch.Tensor) -> None:
+    for k, v in tensors.items():
+        if v.dtype != torch.float32:
+            raise ValueError(f"{who}: {k} dtype must be float32; got {v.dtype}")
+
+
+def split_gi(who: str, gi: torch.Tensor) -> Tuple[int, int, int]:
+    if gi.dim() != 3:
+        raise ValueError(f"{who}: gi must be [T, B, 3H]; got shape {tuple(gi.shape)}")
+    T, B, three_h = gi.shape
+    if three_h % 3 != 0 or three_h == 0:
+        raise ValueError(f"{who}: gi last dim must be 3*H with H > 0; got {three_h}")
+    if T == 0:
+        raise ValueError(f"seq length T must be > 0; got T={T}")
+    if B == 0:
+        raise ValueError(f"batch size B must be > 0; got B={B}")
+    return T, B, three_h // 3
+
+
+def check_common(who: str, gi: torch.Tensor, h0: torch.Tensor, bh_cat: torch.Tensor) -> Tuple[int, int, int]:
+    T, B, H = split_gi(who, gi)
+    if tuple(h0.shape) != (B, H):
+        raise ValueError(f"h0 shape must be (B, H)=({B}, {H}); got {tuple(h0.shape)}")
+    if tuple(bh_cat.shape) != (3 * H,):
+        raise ValueError(f"bh_cat shape must be (3H,)=({3 * H},); got {tuple(bh_cat.shape)}")
+    return T, B, H
+
+
+def check_quant(q: QuantTuple, name: str) -> QuantTuple:
+    if q is None:
+        return None
+    try:
+        scale, qmin, qmax = q
+    except (TypeError, ValueError):
+        raise ValueError(f"{name} must be None or a (scale, qmin, qmax) tuple; got {q!r}") from None
+    scale = float(scale)
+    if not (scale > 0.0 and scale != float("inf")):
+        raise ValueError(f"{name} scale must be finite and > 0; got {scale}")
+    if int(qmin) > int(qmax):
+        raise ValueError(f"{name} qmin must be <= qmax; got {qmin} > {qmax}")
+    return (scale, int(qmin), int(qmax))

@@ -1,0 +1,217 @@
+"""ctypes binding of libgruscan.so (the C ABI declared in include/gruscan.h).
+
+The library is built in-tree by ``make -C gru-triton_amd/csrc`` (or
+``__graft_entry__.build()``). There is no fallback: if the library is missing
+or cannot be loaded, every scan entry point raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional, Tuple
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libgruscan.so")
+
+GS_OK = 0
+GS_ERR_INVALID = -1
+GS_ERR_CAPACITY = -2
+GS_ERR_HIP = -3
+
+KIND_DENSE = 0
+KIND_DIAGONAL = 1
+KIND_MONARCH = 2
+KIND_BUTTERFLY = 3
+
+# Every symbol include/gruscan.h declares.
+EXPORTS = (
+    "gs_dense_fwd",
+    "gs_diagonal_fwd",
+    "gs_monarch_fwd",
+    "gs_butterfly_fwd",
+    "gs_butterfly_fwd_generic",
+    "gs_workspace_bytes",
+    "gs_workspace_status",
+    "gs_last_error",
+    "gs_abi_version",
+)
+
+ABI_VERSION = 1
+
+QuantTuple = Optional[Tuple[float, int, int]]
+
+
+class GsQuant(ctypes.Structure):
+    _fields_ = [
+        ("enabled", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("qmin", ctypes.c_int32),
+        ("qmax", ctypes.c_int32),
+    ]
+
+
+class GsArgs(ctypes.Structure):
+    _fields_ = [
+        ("gi", ctypes.c_void_p),
+        ("h0", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("bh", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
+        ("T", ctypes.c_int64),
+        ("B", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("sg_t", ctypes.c_int64),
+        ("sg_b", ctypes.c_int64),
+        ("sh0_b", ctypes.c_int64),
+        ("so_t", ctypes.c_int64),
+        ("so_b", ctypes.c_int64),
+        ("nblocks", ctypes.c_int64),
+        ("blksz", ctypes.c_int64),
+        ("log_n", ctypes.c_int64),
+        ("bfly_nblocks", ctypes.c_int64),
+        ("q_in", GsQuant),
+        ("q_out", GsQuant),
+    ]
+
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def load() -> ctypes.CDLL:
+    """Load libgruscan.so once (after torch, so it binds torch's HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"libgruscan.so not found at {LIB_PATH}; build it with "
+                "`make -C gru-triton_amd/csrc` or __graft_entry__.build()"
+            )
+        lib = ctypes.CDLL(LIB_PATH)
+        for name in ("gs_dense_fwd", "gs_diagonal_fwd", "gs_monarch_fwd", "gs_butterfly_fwd",
+                     "gs_butterfly_fwd_generic"):
+            fn = getattr(lib, name)
+            fn.argtypes = [ctypes.POINTER(GsArgs), ctypes.c_void_p]
+            fn.restype = ctypes.c_int
+        lib.gs_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsArgs)]
+        lib.gs_workspace_bytes.restype = ctypes.c_int64
+        lib.gs_workspace_status.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+        lib.gs_workspace_status.restype = ctypes.c_int
+        lib.gs_last_error.argtypes = []
+        lib.gs_last_error.restype = ctypes.c_char_p
+        lib.gs_abi_version.argtypes = []
+        lib.gs_abi_version.restype = ctypes.c_int
+        if lib.gs_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"libgruscan.so ABI version {lib.gs_abi_version()} != expected {ABI_VERSION}; rebuild it"
+            )
+        _lib = lib
+        return lib
+
+
+def make_quant(q: QuantTuple, name: str) -> GsQuant:
+    if q is None:
+        return GsQuant(0, 1.0, -(2**31), 2**31 - 1)
+    try:
+        scale, qmin, qmax = q
+    except (TypeError, ValueError):
+        raise ValueError(f"{name} must be None or a (scale, qmin, qmax) tuple; got {q!r}") from None
+    return GsQuant(1, float(scale), int(qmin), int(qmax))
+
+
+def raise_for(rc: int, lib: ctypes.CDLL) -> None:
+    if rc == GS_OK:
+        return
+    msg = lib.gs_last_error().decode("utf-8", "replace")
+    if rc == GS_ERR_INVALID:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+# ---- per-(device, stream) workspace cache ----------------------------------------
+# A workspace is zeroed once when allocated; every kernel leaves it zeroed
+# again, so launches ordered on one stream can share it. Distinct streams get
+# distinct workspaces.
+_ws_cache: dict = {}
+_ws_lock = threading.Lock()
+
+
+def workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor:
+    key = (device.index, stream_handle)
+    with _ws_lock:
+        ws = _ws_cache.get(key)
+        if ws is None or ws.numel() < nbytes:
+            size = max(nbytes, 4096)
+            if ws is not None:
+                size = max(size, 2 * ws.numel())
+            ws = torch.zeros(size, dtype=torch.uint8, device=device)
+            _ws_cache[key] = ws
+        return ws
+
+
+def workspace_faults(device: Optional[torch.device] = None) -> int:
+    """Read and clear the fault word of every cached workspace (synchronises).
+
+    Nonzero means a persistent kernel hit its barrier time-out and the output
+    of that launch is invalid.
+    """
+    lib = load()
+    total = 0
+    with _ws_lock:
+        items = list(_ws_cache.items())
+    for (dev, stream_handle), ws in items:
+        if device is not None and device.index != dev:
+            continue
+        rc = lib.gs_workspace_status(ctypes.c_void_p(ws.data_ptr()), ws.numel(),
+                                     ctypes.c_void_p(stream_handle))
+        if rc < 0:
+            raise_for(rc, lib)
+        total += rc
+    return total
+
+
+def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,
+           w2: Optional[torch.Tensor], bh: torch.Tensor, out: torch.Tensor,
+           h_in_quant: QuantTuple, h_out_quant: QuantTuple, nblocks: int = 0, blksz: int = 0,
+           log_n: int = 0, bfly_nblocks: int = 0) -> None:
+    """Fill gs_args from contiguous fp32 device tensors and call the entry point
+    on the current torch stream of gi's device."""
+    lib = load()
+    T, B, threeH = gi.shape
+    H = threeH // 3
+    a = GsArgs()
+    a.gi = gi.data_ptr()
+    a.h0 = h0.data_ptr()
+    a.w = w.data_ptr()
+    a.w2 = w2.data_ptr() if w2 is not None else None
+    a.bh = bh.data_ptr()
+    a.out = out.data_ptr()
+    a.T, a.B, a.H = T, B, H
+    a.sg_t, a.sg_b = gi.stride(0), gi.stride(1)
+    a.sh0_b = h0.stride(0)
+    a.so_t, a.so_b = out.stride(0), out.stride(1)
+    a.nblocks, a.blksz = nblocks, blksz
+    a.log_n, a.bfly_nblocks = log_n, bfly_nblocks
+    a.q_in = make_quant(h_in_quant, "h_in_quant")
+    a.q_out = make_quant(h_out_quant, "h_out_quant")
+
+    need = lib.gs_workspace_bytes(kind, ctypes.byref(a))
+    if need < 0:
+        raise_for(int(need), lib)
+    with torch.cuda.device(gi.device):
+        handle = torch.cuda.current_stream(gi.device).cuda_stream
+        ws = workspace(gi.device, handle, int(need))
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws.numel()
+        rc = getattr(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
+    raise_for(rc, lib)

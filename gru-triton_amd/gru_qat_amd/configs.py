@@ -1,0 +1,131 @@
+"""Synthetic inputs of the five benchmark configurations.
+
+Every tensor is drawn on the CPU from one ``torch.Generator`` seeded with
+``seed`` (default 0) in a fixed order, then moved to ``device``, so a GPU run
+and a CPU run see bit-identical inputs. Draw order per config: hidden
+weights, hidden bias, gi, h0.
+
+* cfg0 diagonal fp32: T=64 B=32 H=512; w_h, b_h ~ U(-1/sqrt(H), 1/sqrt(H)) of
+  shape (3H,), w_h viewed [3, H]; gi ~ N(0, 1); h0 = 0.
+* cfg1 dense fp32: W_cfg (H, 3H) and bh ~ U(+-1/sqrt(H)); gi ~ N(0, 1);
+  h0 ~ N(0, 0.1^2). The kernel takes the reference layout
+  Wh_cat = W_cfg.T (3H, H), gh = h @ Wh_cat.T + bh.
+* cfg2 dense int8 QAT: cfg1 with per-output-row symmetric int8 weight
+  fake-quant of Wh_cat (scale = max|row| / 127, clamped at 1e-8) and hidden
+  quant (fp32(1/127), -127, 127) on both sides.
+* cfg3 Monarch, nblocks=8, blksz=64: two factors [3, 8, 64, 64] ~ U(-1/8, 1/8)
+  (first factor then second), bh ~ U(+-1/sqrt(H)), gi ~ N(0, 1), h0 = 0,
+  hidden quant as cfg2.
+* cfg4 butterfly: T=512 B=64 H=1024; twiddles [3, 1, 10, 512, 2, 2] ~
+  N(0, 1/2); bh ~ U(+-1/sqrt(H)); gi ~ N(0, 1); h0 = 0.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import torch
+
+Q_INT8_HIDDEN: Tuple[float, int, int] = (float(torch.tensor(1.0 / 127.0, dtype=torch.float32).item()), -127, 127)
+
+NAMES = {
+    0: "diagonal_fp32",
+    1: "dense_fp32",
+    2: "dense_int8_qat",
+    3: "monarch_nb8_two_factor_int8",
+    4: "butterfly_fp32",
+}
+
+SHAPES = {0: (64, 32, 512), 1: (64, 32, 512), 2: (64, 32, 512), 3: (64, 32, 512), 4: (512, 64, 1024)}
+
+
+def _uniform(gen: torch.Generator, shape, bound: float) -> torch.Tensor:
+    return (torch.rand(shape, generator=gen, dtype=torch.float32) * 2.0 - 1.0) * bound
+
+
+def per_row_int8_fake_quant(W: torch.Tensor) -> torch.Tensor:
+    """Symmetric per-output-row int8 fake-quant of a [rows, cols] weight
+    (reference quantizers.py:124-134, 188-199; ste.py:65-95 with zp = 0)."""
+    absmax = torch.maximum(W.amax(dim=1, keepdim=True).abs(), W.amin(dim=1, keepdim=True).abs()).clamp(min=1e-8)
+    scale = absmax / 127.0
+    zp = torch.zeros_like(scale)
+    q = torch.round(W / scale + zp).clamp(-127.0, 127.0)
+    return (q - zp) * scale
+
+
+def make_config(idx: int, device: Optional[torch.device] = None, seed: int = 0,
+                shape: Optional[Tuple[int, int, int]] = None) -> Dict[str, object]:
+    """Returns a dict with kind, tensors and quant tuples for config ``idx``.
+
+    ``shape`` = (T, B, H) overrides the benchmark shape (same distributions),
+    which tests use to build small instances of each config.
+    """
+    T, B, H = shape if shape is not None else SHAPES[idx]
+    gen = torch.Generator().manual_seed(seed)
+    k = 1.0 / math.sqrt(H)
+    d: Dict[str, object] = {"name": NAMES[idx], "T": T, "B": B, "H": H, "h_in_quant": None, "h_out_quant": None}
+    if idx == 0:
+        d["kind"] = "diagonal"
+        d["w"] = _uniform(gen, (3 * H,), k).view(3, H)
+        d["bh"] = _uniform(gen, (3 * H,), k)
+        d["gi"] = torch.randn((T, B, 3 * H), generator=gen, dtype=torch.float32)
+        d["h0"] = torch.zeros((B, H), dtype=torch.float32)
+    elif idx in (1, 2):
+        d["kind"] = "dense"
+        W_cfg = _uniform(gen, (H, 3 * H), k)
+        d["bh"] = _uniform(gen, (3 * H,), k)
+        d["gi"] = torch.randn((T, B, 3 * H), generator=gen, dtype=torch.float32)
+        d["h0"] = torch.randn((B, H), generator=gen, dtype=torch.float32) * 0.1
+        Wh_cat = W_cfg.t().contiguous()
+        if idx == 2:
+            Wh_cat = per_row_int8_fake_quant(Wh_cat)
+            d["h_in_quant"] = Q_INT8_HIDDEN
+            d["h_out_quant"] = Q_INT8_HIDDEN
+        d["w"] = Wh_cat
+    elif idx == 3:
+        d["kind"] = "monarch"
+        nb = 8 if H % 8 == 0 else 1
+        bs = H // nb
+        d["w"] = _uniform(gen, (3, nb, bs, bs), 1.0 / 8.0)
+        d["w2"] = _uniform(gen, (3, nb, bs, bs), 1.0 / 8.0)
+        d["bh"] = _uniform(gen, (3 * H,), k)
+        d["gi"] = torch.randn((T, B, 3 * H), generator=gen, dtype=torch.float32)
+        d["h0"] = torch.zeros((B, H), dtype=torch.float32)
+        d["h_in_quant"] = Q_INT8_HIDDEN
+        d["h_out_quant"] = Q_INT8_HIDDEN
+    elif idx == 4:
+        d["kind"] = "butterfly"
+        n_pad = 1 << max(1, (H - 1).bit_length())
+        L = n_pad.bit_length() - 1
+        d["w"] = torch.randn((3, 1, L, n_pad // 2, 2, 2), generator=gen, dtype=torch.float32) * math.sqrt(0.5)
+        d["bh"] = _uniform(gen, (3 * H,), k)
+        d["gi"] = torch.randn((T, B, 3 * H), generator=gen, dtype=torch.float32)
+        d["h0"] = torch.zeros((B, H), dtype=torch.float32)
+    else:
+        raise ValueError(f"unknown config {idx}")
+    if device is not None:
+        for key in ("w", "w2", "bh", "gi", "h0"):
+            if key in d:
+                d[key] = d[key].to(device)  # type: ignore[union-attr]
+    return d
+
+
+def run_config(d: Dict[str, object]) -> torch.Tensor:
+    """Runs the HIP scan of a config dict (tensors on a GPU); returns out."""
+    from .scan import gru_scan_forward_persistent
+    from .scan_butterfly import gru_scan_butterfly_forward
+    from .scan_diagonal import gru_scan_diagonal_forward
+    from .scan_monarch import gru_scan_monarch_forward
+
+    kw = dict(h_in_quant=d["h_in_quant"], h_out_quant=d["h_out_quant"])
+    kind = d["kind"]
+    if kind == "dense":
+        return gru_scan_forward_persistent(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    if kind == "diagonal":
+        return gru_scan_diagonal_forward(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    if kind == "monarch":
+        return gru_scan_monarch_forward(d["gi"], d["h0"], d["w"], d["bh"], Wh_struct2=d.get("w2"), **kw)
+    if kind == "butterfly":
+        return gru_scan_butterfly_forward(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    raise ValueError(kind)

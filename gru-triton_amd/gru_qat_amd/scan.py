@@ -1,0 +1,135 @@
+"""Dense-hidden persistent GRU scan (drop-in for gru_qat.triton_kernels.scan).
+
+Entry points keep the reference signatures
+(LarocheC/gru-triton src/gru_qat/triton_kernels/scan.py):
+
+* ``gru_scan_persistent(gi, h0, Wh_cat, bh_cat, *, h_in_quant, h_out_quant)``
+  (scan.py:1667-1685) and its autograd Function (scan.py:1630-1664);
+* ``gru_scan(...)`` (scan.py:1607-1627), same contract;
+* ``gru_scan_forward_persistent`` / ``gru_scan_forward`` (scan.py:213-293,
+  1688-1765), the forward-only launchers.
+
+``Wh_cat`` is ``[3H, H]`` with rows ordered r, z, n and ``gh = hq @ Wh_cat.T +
+bh_cat``. ``h_in_quant`` / ``h_out_quant`` are optional frozen per-tensor
+symmetric ``(scale, qmin, qmax)`` tuples. The forward runs the gfx950 kernel
+``gs_dense_fwd`` of libgruscan.so (one persistent launch, Wh resident in
+registers, fp32 MFMA); the reference's tile and warp knobs have no meaning
+there and are accepted only as keywords that are ignored.
+"""
+
+from __future__ import annotations
+
+from typing import Any, cast
+
+import torch
+
+from . import _lib
+from ._backward import scan_backward
+from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
+
+
+def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.Tensor,
+                   bh_cat: torch.Tensor, h_in_quant: QuantTuple, h_out_quant: QuantTuple) -> torch.Tensor:
+    require_cuda(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
+    require_f32(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
+    T, B, H = check_common(who, gi, h0, bh_cat)
+    if tuple(Wh_cat.shape) != (3 * H, H):
+        raise ValueError(f"Wh_cat shape must be (3H, H)=({3 * H}, {H}); got {tuple(Wh_cat.shape)}")
+    h_in_quant = check_quant(h_in_quant, "h_in_quant")
+    h_out_quant = check_quant(h_out_quant, "h_out_quant")
+    gi = gi.contiguous()
+    h0 = h0.contiguous()
+    Wh_cat = Wh_cat.contiguous()
+    bh_cat = bh_cat.contiguous()
+    out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
+    _lib.launch(_lib.KIND_DENSE, "gs_dense_fwd", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat, out=out,
+                h_in_quant=h_in_quant, h_out_quant=h_out_quant)
+    return out
+
+
+def gru_scan_forward_persistent(
+    gi: torch.Tensor,
+    h0: torch.Tensor,
+    Wh_cat: torch.Tensor,
+    bh_cat: torch.Tensor,
+    *,
+    h_in_quant: QuantTuple = None,
+    h_out_quant: QuantTuple = None,
+    **_ignored_tiling: Any,
+) -> torch.Tensor:
+    """Forward of the dense scan; returns out [T, B, H] (h_T = out[-1])."""
+    return _dense_forward("gru_scan_forward_persistent", gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant)
+
+
+def gru_scan_forward(
+    gi: torch.Tensor,
+    h0: torch.Tensor,
+    Wh_cat: torch.Tensor,
+    bh_cat: torch.Tensor,
+    *,
+    h_in_quant: QuantTuple = None,
+    h_out_quant: QuantTuple = None,
+) -> torch.Tensor:
+    """Same contract as the reference's autotuned launcher (scan.py:1688-1765)."""
+    return _dense_forward("gru_scan_forward", gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant)
+
+
+def _dense_gh(hq: torch.Tensor, Wh_cat: torch.Tensor) -> torch.Tensor:
+    return hq @ Wh_cat.t()
+
+
+def gru_scan_backward(gi, h0, Wh_cat, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None):
+    """(dgi, dh0, dWh_cat, dbh_cat); semantics of scan.py:1460-1550."""
+    dgi, dh0, (dW,), dbh = scan_backward(gi, h0, out, dout, _dense_gh, [Wh_cat], bh_cat,
+                                         h_in_quant, h_out_quant)
+    return dgi, dh0, dW, dbh
+
+
+class GRUScanPersistentFunction(torch.autograd.Function):
+    """autograd wrapper; saves (gi, h0, Wh_cat, bh_cat, out) like scan.py:1650."""
+
+    @staticmethod
+    def forward(ctx: Any, gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant):  # type: ignore[override]
+        out = gru_scan_forward_persistent(gi, h0, Wh_cat, bh_cat, h_in_quant=h_in_quant,
+                                          h_out_quant=h_out_quant)
+        ctx.save_for_backward(gi, h0, Wh_cat, bh_cat, out)
+        ctx.h_in_quant = check_quant(h_in_quant, "h_in_quant")
+        ctx.h_out_quant = check_quant(h_out_quant, "h_out_quant")
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, dout: torch.Tensor):  # type: ignore[override]
+        gi, h0, Wh_cat, bh_cat, out = ctx.saved_tensors
+        grads = gru_scan_backward(gi, h0, Wh_cat, bh_cat, out, dout, h_in_quant=ctx.h_in_quant,
+                                  h_out_quant=ctx.h_out_quant)
+        return (*grads, None, None)
+
+
+GRUScanFunction = GRUScanPersistentFunction
+
+
+def gru_scan_persistent(
+    gi: torch.Tensor,
+    h0: torch.Tensor,
+    Wh_cat: torch.Tensor,
+    bh_cat: torch.Tensor,
+    *,
+    h_in_quant: QuantTuple = None,
+    h_out_quant: QuantTuple = None,
+) -> torch.Tensor:
+    """Differentiable dense persistent GRU scan; returns out [T, B, H]."""
+    return cast(torch.Tensor, GRUScanPersistentFunction.apply(gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant))
+
+
+def gru_scan(
+    gi: torch.Tensor,
+    h0: torch.Tensor,
+    Wh_cat: torch.Tensor,
+    bh_cat: torch.Tensor,
+    *,
+    h_in_quant: QuantTuple = None,
+    h_out_quant: QuantTuple = None,
+) -> torch.Tensor:
+    """Differentiable dense GRU scan (reference scan.py:1607-1627); same kernel
+    as ``gru_scan_persistent`` on MI355X."""
+    return cast(torch.Tensor, GRUScanPersistentFunction.apply(gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant))

@@ -1,0 +1,145 @@
+"""Butterfly-hidden GRU scan (drop-in for the persistent path of
+gru_qat.triton_kernels.scan_butterfly).
+
+Twiddles are ``[3, nblocks, log_n, 2^log_n / 2, 2, 2]`` (gates r, z, n; the
+torch-structured ``Butterfly.twiddle`` with nstacks squeezed), and the hidden
+map is the chain of strided 2x2 stages described in
+LarocheC/gru-triton src/gru_qat/triton_kernels/scan_butterfly.py:276-317
+applied to q_in(h) zero-padded to 2^log_n, truncated to H, plus bh.
+Signatures: ``gru_scan_butterfly_triton`` (:1115-1139), its forward launcher
+(:369-459) and ``extract_butterfly_twiddles`` (:1142-1182). The forward is
+``gs_butterfly_fwd`` of libgruscan.so.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Tuple, cast
+
+import torch
+
+from . import _lib
+from ._backward import scan_backward
+from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
+
+
+def extract_butterfly_twiddles(cell: Any) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Stack the three ``struct_Wh_*.b.twiddle`` tensors ([1, nblocks, log_n,
+    n/2, 2, 2] each) into [3, nblocks, log_n, n/2, 2, 2]."""
+    if getattr(cell, "_hidden_dense", False):
+        raise ValueError("cell hidden side is dense; nothing to extract")
+    tws = [layer.b.twiddle.squeeze(0) for layer in (cell.struct_Wh_r, cell.struct_Wh_z, cell.struct_Wh_n)]
+    twiddles = torch.stack(tws, dim=0)
+    if getattr(cell, "b_hr", None) is None:
+        bh_cat = torch.zeros(3 * cell.hidden_size, device=twiddles.device, dtype=twiddles.dtype)
+    else:
+        bh_cat = torch.cat([cell.b_hr, cell.b_hz, cell.b_hn])
+    return twiddles, bh_cat
+
+
+def check_twiddles(twiddles: torch.Tensor, H: int) -> Tuple[int, int]:
+    """Validates the twiddle shape (scan_butterfly.py:403-420); returns (nblocks, log_n)."""
+    if twiddles.dim() != 6:
+        raise ValueError(f"twiddles shape must be (3, nblocks, log_H, H//2, 2, 2); got {tuple(twiddles.shape)}")
+    n_gates, nblocks, log_n, n_div_2, two1, two2 = twiddles.shape
+    if not (n_gates == 3 and two1 == 2 and two2 == 2 and nblocks >= 1):
+        raise ValueError(f"twiddles shape must be (3, nblocks, log_H, H//2, 2, 2); got {tuple(twiddles.shape)}")
+    h_pad = 2 * n_div_2
+    if not (h_pad >= H and h_pad >= 2 and (h_pad & (h_pad - 1)) == 0):
+        raise ValueError(f"twiddles imply H_PAD={h_pad}, which must be >= H={H} and a power of two "
+                         f"(shape {tuple(twiddles.shape)})")
+    if (1 << log_n) != h_pad:
+        raise ValueError(f"twiddles log_H={log_n} inconsistent with H_PAD={h_pad}: expected 1 << log_H == H_PAD "
+                         f"(shape {tuple(twiddles.shape)})")
+    return nblocks, log_n
+
+
+def _forward(fn_name: str, who: str, gi, h0, twiddles, bh_cat, h_in_quant, h_out_quant) -> torch.Tensor:
+    require_cuda(who, gi=gi, h0=h0, twiddles=twiddles, bh_cat=bh_cat)
+    require_f32(who, gi=gi, h0=h0, twiddles=twiddles, bh_cat=bh_cat)
+    T, B, H = check_common(who, gi, h0, bh_cat)
+    nblocks, log_n = check_twiddles(twiddles, H)
+    h_in_quant = check_quant(h_in_quant, "h_in_quant")
+    h_out_quant = check_quant(h_out_quant, "h_out_quant")
+    gi, h0, twiddles, bh_cat = gi.contiguous(), h0.contiguous(), twiddles.contiguous(), bh_cat.contiguous()
+    out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
+    _lib.launch(_lib.KIND_BUTTERFLY, fn_name, gi=gi, h0=h0, w=twiddles, w2=None, bh=bh_cat, out=out,
+                h_in_quant=h_in_quant, h_out_quant=h_out_quant, log_n=log_n, bfly_nblocks=nblocks)
+    return out
+
+
+def gru_scan_butterfly_forward(gi, h0, twiddles, bh_cat, *, h_in_quant: QuantTuple = None,
+                               h_out_quant: QuantTuple = None, **_ignored_tiling: Any) -> torch.Tensor:
+    return _forward("gs_butterfly_fwd", "gru_scan_butterfly_forward", gi, h0, twiddles, bh_cat,
+                    h_in_quant, h_out_quant)
+
+
+gru_scan_butterfly_forward_triton = gru_scan_butterfly_forward
+
+
+def gru_scan_butterfly_forward_generic(gi, h0, twiddles, bh_cat, *, h_in_quant: QuantTuple = None,
+                                       h_out_quant: QuantTuple = None) -> torch.Tensor:
+    """Same result from the general LDS kernel (used to cross-check the register kernel)."""
+    return _forward("gs_butterfly_fwd_generic", "gru_scan_butterfly_forward_generic", gi, h0, twiddles,
+                    bh_cat, h_in_quant, h_out_quant)
+
+
+def butterfly_gh(hq: torch.Tensor, twiddles: torch.Tensor) -> torch.Tensor:
+    """Hidden projection without bias, [B, 3H], as torch ops (for the backward)."""
+    B, H = hq.shape
+    _, nblocks, L, n2, _, _ = twiddles.shape
+    N = 2 * n2
+    x = torch.zeros(B, 3, N, dtype=hq.dtype, device=hq.device)
+    x = x + torch.nn.functional.pad(hq, (0, N - H)).unsqueeze(1)
+    i = torch.arange(N, device=hq.device)
+    for c in range(nblocks):
+        for s in range(L):
+            ls = s if c % 2 == 0 else L - 1 - s
+            stride = 1 << ls
+            m = (i >> ls) & 1
+            pair = (i >> (ls + 1)) * stride + (i & (stride - 1))
+            tw = twiddles[:, c, s]  # [3, N/2, 2, 2]
+            t_ss = tw[:, pair, m, m]
+            t_sp = tw[:, pair, m, 1 - m]
+            x = t_ss.unsqueeze(0) * x + t_sp.unsqueeze(0) * x[:, :, i ^ stride]
+    return x[:, :, :H].reshape(B, 3 * H)
+
+
+def gru_scan_butterfly_backward(gi, h0, twiddles, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None):
+    dgi, dh0, (dtw,), dbh = scan_backward(gi, h0, out, dout, butterfly_gh, [twiddles], bh_cat,
+                                          h_in_quant, h_out_quant)
+    return dgi, dh0, dtw, dbh
+
+
+class GRUScanButterflyTritonFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, gi, h0, twiddles, bh_cat, h_in_quant, h_out_quant):  # type: ignore[override]
+        out = gru_scan_butterfly_forward(gi, h0, twiddles, bh_cat, h_in_quant=h_in_quant, h_out_quant=h_out_quant)
+        ctx.save_for_backward(gi, h0, twiddles, bh_cat, out)
+        ctx.h_in_quant = check_quant(h_in_quant, "h_in_quant")
+        ctx.h_out_quant = check_quant(h_out_quant, "h_out_quant")
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, dout: torch.Tensor):  # type: ignore[override]
+        gi, h0, twiddles, bh_cat, out = ctx.saved_tensors
+        grads = gru_scan_butterfly_backward(gi, h0, twiddles, bh_cat, out, dout, h_in_quant=ctx.h_in_quant,
+                                            h_out_quant=ctx.h_out_quant)
+        return (*grads, None, None)
+
+
+def gru_scan_butterfly_triton(
+    gi: torch.Tensor,
+    h0: torch.Tensor,
+    twiddles: torch.Tensor,
+    bh_cat: torch.Tensor,
+    *,
+    h_in_quant: QuantTuple = None,
+    h_out_quant: QuantTuple = None,
+) -> torch.Tensor:
+    """Differentiable butterfly-hidden GRU scan; returns out [T, B, H]. The
+    name is the reference's; the kernel is hand-written HIP, not Triton."""
+    return cast(torch.Tensor, GRUScanButterflyTritonFunction.apply(gi, h0, twiddles, bh_cat, h_in_quant,
+                                                                   h_out_quant))
+
+
+gru_scan_butterfly_persistent = gru_scan_butterfly_triton

@@ -1,0 +1,144 @@
+"""Monarch (block-diagonal) hidden GRU scan (drop-in for
+gru_qat.triton_kernels.scan_monarch).
+
+Single factor, as in the reference (LarocheC/gru-triton
+src/gru_qat/triton_kernels/scan_monarch.py:74-127, 927-952):
+``gh[b, g, n, o] = sum_i q_in(h)[b, n*blksz + i] * Wh_struct[g, n, o, i] + bh``.
+
+Two factors (keyword-only ``Wh_struct2``, no reference counterpart): with
+R_g = Wh_struct[g], L_g = Wh_struct2[g] (both block-diagonal, blocks stored as
+(out, in)) and P the stride-``nblocks`` permutation
+``(P z)[c * nblocks + a] = z[a * blksz + c]``, the hidden map is
+``gh_g = P^T L_g P R_g q_in(h) + bh_g``. With identity blocks in Wh_struct2
+it is exactly the single-factor map.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional, Tuple, cast
+
+import torch
+
+from . import _lib
+from ._backward import scan_backward
+from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
+
+
+def extract_monarch_factors(cell: Any) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Stack ``struct_Wh_{r,z,n}.weight`` ([nblocks, out, in] each) into
+    [3, nblocks, blksz, blksz] and the hidden biases into [3H]
+    (scan_monarch.py:22-58)."""
+    if getattr(cell, "_hidden_dense", False):
+        raise ValueError("cell hidden side is dense; nothing to extract")
+    Wh_struct = torch.stack([cell.struct_Wh_r.weight, cell.struct_Wh_z.weight, cell.struct_Wh_n.weight], dim=0)
+    if getattr(cell, "b_hr", None) is None:
+        bh_cat = torch.zeros(3 * cell.hidden_size, device=Wh_struct.device, dtype=Wh_struct.dtype)
+    else:
+        bh_cat = torch.cat([cell.b_hr, cell.b_hz, cell.b_hn])
+    return Wh_struct, bh_cat
+
+
+def _check_struct(name: str, W: torch.Tensor, H: int) -> Tuple[int, int]:
+    if W.dim() != 4:
+        raise ValueError(f"{name} must be [3, nblocks, blksz, blksz]; got shape {tuple(W.shape)}")
+    n_gates, nblocks, out_blksz, in_blksz = W.shape
+    if n_gates != 3:
+        raise ValueError(f"{name} dim 0 (n_gates) must be 3; got {n_gates} (shape {tuple(W.shape)})")
+    if nblocks < 1 or not (out_blksz == in_blksz == H // nblocks) or nblocks * out_blksz != H:
+        raise ValueError(
+            f"{name} block dims must be square and tile H: expected out_blksz == in_blksz == "
+            f"H // nblocks == {H // max(nblocks, 1)}; got out_blksz={out_blksz}, in_blksz={in_blksz}, "
+            f"H={H}, nblocks={nblocks}"
+        )
+    return nblocks, out_blksz
+
+
+def gru_scan_monarch_forward(
+    gi: torch.Tensor,
+    h0: torch.Tensor,
+    Wh_struct: torch.Tensor,
+    bh_cat: torch.Tensor,
+    *,
+    h_in_quant: QuantTuple = None,
+    h_out_quant: QuantTuple = None,
+    Wh_struct2: Optional[torch.Tensor] = None,
+    **_ignored_tiling: Any,
+) -> torch.Tensor:
+    who = "gru_scan_monarch_forward"
+    tensors = dict(gi=gi, h0=h0, Wh_struct=Wh_struct, bh_cat=bh_cat)
+    if Wh_struct2 is not None:
+        tensors["Wh_struct2"] = Wh_struct2
+    require_cuda(who, **tensors)
+    require_f32(who, **tensors)
+    T, B, H = check_common(who, gi, h0, bh_cat)
+    nblocks, blksz = _check_struct("Wh_struct", Wh_struct, H)
+    if Wh_struct2 is not None:
+        if tuple(Wh_struct2.shape) != tuple(Wh_struct.shape):
+            raise ValueError(f"Wh_struct2 shape {tuple(Wh_struct2.shape)} must equal Wh_struct shape "
+                             f"{tuple(Wh_struct.shape)}")
+        Wh_struct2 = Wh_struct2.contiguous()
+    h_in_quant = check_quant(h_in_quant, "h_in_quant")
+    h_out_quant = check_quant(h_out_quant, "h_out_quant")
+    gi, h0, Wh_struct, bh_cat = gi.contiguous(), h0.contiguous(), Wh_struct.contiguous(), bh_cat.contiguous()
+    out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
+    _lib.launch(_lib.KIND_MONARCH, "gs_monarch_fwd", gi=gi, h0=h0, w=Wh_struct, w2=Wh_struct2, bh=bh_cat,
+                out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, nblocks=nblocks, blksz=blksz)
+    return out
+
+
+gru_scan_monarch_forward_triton = gru_scan_monarch_forward
+
+
+def monarch_gh(hq: torch.Tensor, Wh_struct: torch.Tensor, Wh_struct2: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Hidden projection without bias, [B, 3H] (device-agnostic torch ops)."""
+    B, H = hq.shape
+    _, nb, bs, _ = Wh_struct.shape
+    z = torch.einsum("bni,gnoi->bgno", hq.reshape(B, nb, bs), Wh_struct)  # [B, 3, nb, bs]
+    if Wh_struct2 is None:
+        return z.reshape(B, 3 * H)
+    u = z.reshape(B, 3, nb, bs).transpose(2, 3).reshape(B, 3, nb, bs)  # P z, viewed as blocks
+    v = torch.einsum("bgni,gnoi->bgno", u, Wh_struct2)
+    y = v.reshape(B, 3, bs, nb).transpose(2, 3).reshape(B, 3 * H)  # P^T v
+    return y
+
+
+def gru_scan_monarch_backward(gi, h0, Wh_struct, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None,
+                              Wh_struct2=None):
+    params = [Wh_struct] if Wh_struct2 is None else [Wh_struct, Wh_struct2]
+    dgi, dh0, dps, dbh = scan_backward(gi, h0, out, dout, monarch_gh, params, bh_cat, h_in_quant, h_out_quant)
+    return dgi, dh0, dps, dbh
+
+
+class GRUScanMonarchFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, gi, h0, Wh_struct, bh_cat, h_in_quant, h_out_quant, Wh_struct2):  # type: ignore[override]
+        out = gru_scan_monarch_forward(gi, h0, Wh_struct, bh_cat, h_in_quant=h_in_quant,
+                                       h_out_quant=h_out_quant, Wh_struct2=Wh_struct2)
+        ctx.save_for_backward(gi, h0, Wh_struct, bh_cat, out, Wh_struct2)
+        ctx.h_in_quant = check_quant(h_in_quant, "h_in_quant")
+        ctx.h_out_quant = check_quant(h_out_quant, "h_out_quant")
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, dout: torch.Tensor):  # type: ignore[override]
+        gi, h0, Wh_struct, bh_cat, out, Wh_struct2 = ctx.saved_tensors
+        dgi, dh0, dps, dbh = gru_scan_monarch_backward(gi, h0, Wh_struct, bh_cat, out, dout,
+                                                       h_in_quant=ctx.h_in_quant, h_out_quant=ctx.h_out_quant,
+                                                       Wh_struct2=Wh_struct2)
+        dW2 = dps[1] if Wh_struct2 is not None else None
+        return dgi, dh0, dps[0], dbh, None, None, dW2
+
+
+def gru_scan_monarch(
+    gi: torch.Tensor,
+    h0: torch.Tensor,
+    Wh_struct: torch.Tensor,
+    bh_cat: torch.Tensor,
+    *,
+    h_in_quant: QuantTuple = None,
+    h_out_quant: QuantTuple = None,
+    Wh_struct2: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Differentiable Monarch-hidden GRU scan; returns out [T, B, H]."""
+    return cast(torch.Tensor, GRUScanMonarchFunction.apply(gi, h0, Wh_struct, bh_cat, h_in_quant, h_out_quant,
+                                                           Wh_struct2))

@@ -1,0 +1,124 @@
+/*
+ * gruscan.h -- C ABI of libgruscan.so, the MI355X (gfx950) persistent GRU scan.
+ *
+ * One entry point per hidden-weight kind. Each runs the whole T-step GRU
+ * recurrence forward in one kernel launch on the given HIP stream:
+ *
+ *   hq_t   = q_in(h_{t-1})                     (optional frozen fake-quant)
+ *   gh     = Wh(hq_t) + bh                     (dense / diagonal / Monarch / butterfly)
+ *   r      = sigmoid(gi_r[t] + gh_r)
+ *   z      = sigmoid(gi_z[t] + gh_z)
+ *   n      = tanh(gi_n[t] + r * gh_n)
+ *   h_t    = q_out((1 - z) * n + z * h_{t-1})   (raw h_{t-1} on the carry side)
+ *   out[t] = h_t
+ *
+ * Gate order along the 3H axis is r, z, n. All tensors are fp32, device
+ * resident, with unit stride along their last axis; the other strides are
+ * given in elements. The library never allocates device memory: the caller
+ * passes `out` and a scratch `workspace` of gs_workspace_bytes() bytes, zeroed
+ * once when it is first allocated. Every entry point leaves the workspace
+ * zeroed again when its kernel ends, so one workspace serves any number of
+ * calls issued in order on one stream; calls that overlap in time (two
+ * streams) need distinct workspaces.
+ *
+ * Return codes: GS_OK, or a negative GS_ERR_* value; gs_last_error() then
+ * returns a message for the calling thread.
+ *
+ * Reference interfaces replaced (LarocheC/gru-triton, src/gru_qat/triton_kernels/):
+ *   gs_dense_fwd     <- scan.py:76-210 (gru_scan_fwd_persistent_kernel), launched by
+ *                       gru_scan_forward_persistent scan.py:213-293 and, with the same
+ *                       contract, gru_scan_forward scan.py:1688-1765
+ *   gs_diagonal_fwd  <- scan_diagonal.py:127-223, launched by scan_diagonal.py:226-282
+ *   gs_monarch_fwd   <- scan_monarch.py:130-291, launched by scan_monarch.py:320-406
+ *                       (w2 != NULL selects the two-factor form, which has no
+ *                       reference counterpart; see gs_args.w2)
+ *   gs_butterfly_fwd <- scan_butterfly.py:168-366, launched by scan_butterfly.py:369-459
+ * The quant triple mirrors the (scale, qmin, qmax) tuples of those wrappers
+ * (scan.py:269-270); the in-kernel fake-quant mirrors scan.py:136-139, 176-179.
+ */
+#ifndef GRUSCAN_H
+#define GRUSCAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GS_ABI_VERSION 1
+
+#define GS_OK 0
+#define GS_ERR_INVALID (-1)  /* bad pointer, shape, stride or quant parameter (Python: ValueError) */
+#define GS_ERR_CAPACITY (-2) /* persistent grid does not fit co-resident on the device (RuntimeError) */
+#define GS_ERR_HIP (-3)      /* HIP runtime error; message carries hipGetErrorString (RuntimeError) */
+
+#define GS_KIND_DENSE 0
+#define GS_KIND_DIAGONAL 1
+#define GS_KIND_MONARCH 2
+#define GS_KIND_BUTTERFLY 3
+
+/* Frozen per-tensor symmetric fake-quant: q = clamp(rint(x / scale), qmin, qmax) * scale,
+ * with IEEE division and round-half-to-even. enabled == 0 turns it off. */
+typedef struct gs_quant {
+  int32_t enabled;
+  float scale;
+  int32_t qmin;
+  int32_t qmax;
+} gs_quant;
+
+typedef struct gs_args {
+  const float* gi;  /* [T, B, 3H]; strides sg_t, sg_b, 1                                   */
+  const float* h0;  /* [B, H];     strides sh0_b, 1                                         */
+  const float* w;   /* dense: Wh_cat [3H, H] (rows r,z,n; gh = hq @ w^T), contiguous
+                       diagonal: Wh_diag [3, H], contiguous
+                       Monarch: Wh_struct [3, nblocks, blksz, blksz] as (out, in), contiguous
+                       butterfly: twiddles [3, bfly_nblocks, log_n, 2^log_n / 2, 2, 2], contiguous */
+  const float* w2;  /* Monarch only: second block-diagonal factor, same shape as w, or NULL.
+                       With w2 the hidden map is gh_g = P^T L_g P R_g hq, where R_g = w[g],
+                       L_g = w2[g] and P is the stride-nblocks permutation
+                       (P z)[c * nblocks + a] = z[a * blksz + c]. w2 = identity blocks
+                       gives back the single-factor map. Must be NULL for other kinds. */
+  const float* bh;  /* [3H], contiguous                                                     */
+  float* out;       /* [T, B, H];  strides so_t, so_b, 1                                    */
+  void* workspace;  /* gs_workspace_bytes() bytes, 256-byte aligned, zero on first use     */
+  int64_t workspace_bytes;
+  int64_t T, B, H;
+  int64_t sg_t, sg_b, sh0_b, so_t, so_b;
+  int64_t nblocks, blksz;      /* Monarch: nblocks * blksz == H                             */
+  int64_t log_n, bfly_nblocks; /* butterfly: 2^log_n >= H                                   */
+  gs_quant q_in;  /* applied to the matmul-side h only                                      */
+  gs_quant q_out; /* applied to h_t before it is stored and carried                         */
+} gs_args;
+
+int gs_dense_fwd(const gs_args* args, hipStream_t stream);
+int gs_diagonal_fwd(const gs_args* args, hipStream_t stream);
+int gs_monarch_fwd(const gs_args* args, hipStream_t stream);
+int gs_butterfly_fwd(const gs_args* args, hipStream_t stream);
+
+/* Same contract as gs_butterfly_fwd, but always runs the general LDS kernel
+ * (any 2^log_n <= 4096, any bfly_nblocks) instead of the register kernel that
+ * gs_butterfly_fwd picks for one chain at 2^log_n in {256, 512, 1024}. No
+ * reference counterpart: it lets tests cross-check the two implementations. */
+int gs_butterfly_fwd_generic(const gs_args* args, hipStream_t stream);
+
+/* Scratch bytes the kind needs for these arguments (barrier counters, exchange
+ * buffers). Pure host arithmetic; never touches the device. Negative on error. */
+int64_t gs_workspace_bytes(int kind, const gs_args* args);
+
+/* Reads and clears the device-side fault word of a workspace (nonzero means a
+ * persistent kernel hit its barrier time-out and its output is invalid).
+ * Synchronises the stream. Returns the word, or a negative GS_ERR_* value. */
+int gs_workspace_status(void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* gs_last_error(void);
+
+int gs_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GRUSCAN_H */

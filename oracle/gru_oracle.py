@@ -1,0 +1,212 @@
+"""CPU oracle for the persistent GRU scan -- TEST INFRASTRUCTURE ONLY.
+
+This module restates, in plain PyTorch on the CPU, the reference path that
+the HIP kernels must match (LarocheC/gru-triton, the per-step
+``GRUCellQuant`` path). Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker
+or the timed CPU baseline; the product path (``gru_qat_amd``) never calls it.
+
+Functions and what they follow (reference file:line):
+  fake_quant       src/gru_qat/ste.py:65-95 (q = round(x/s + zp), clamp, (q - zp)*s,
+                   zp = 0) as used by FakeQuantize.forward, quantizers.py:89-96
+  gru_step         src/gru_qat/gru_cell.py:437-464 (step_with_gi), gate order r, z, n,
+                   raw h on the carry side, q_out before the carry
+  gh_dense         gru_cell.py:453 (F.linear(hq, Wh_cat, bh_cat)), scan.py:1500
+  gh_diagonal      triton_kernels/scan_diagonal.py:110-115, structure.py:213-217
+  gh_monarch       triton_kernels/scan_monarch.py:107-113
+  gh_monarch2      build-defined two-factor form P^T L P R (no reference counterpart)
+  butterfly_apply  triton_kernels/scan_butterfly.py:276-317 (stage order, stride
+                   direction per chain, pair index and twiddle element selection)
+  scan             the T-step loops of scan_diagonal.py:79-124 / scan_monarch.py:74-127 /
+                   gru_layer.py:212-223
+
+Pins (tests/test_oracle.py): round-half-even and clipping known answers
+(tests/test_ste.py:12-61 of the reference), an exhaustive boundary sweep of
+fake_quant against exact rational arithmetic, nn.GRUCell closed forms for the
+dense, diagonal and Monarch maps (weight_ih = I, weight_hh = the materialised
+hidden map), an independent permutation-matrix construction of the
+two-factor Monarch map and its reduction to the single-factor map, identity
+and single-stage closed forms of the butterfly, float64 brute force, and
+golden vectors produced from the reference's own butterfly kernel
+(tests/golden/).
+"""
+
+from __future__ import annotations
+
+from typing import Callable, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+QuantTuple = Optional[Tuple[float, int, int]]
+
+
+def fake_quant(x: torch.Tensor, q: QuantTuple) -> torch.Tensor:
+    """Frozen per-tensor symmetric fake-quant with the reference's op order."""
+    if q is None:
+        return x
+    scale, qmin, qmax = q
+    s = torch.tensor(scale, dtype=x.dtype)
+    zp = torch.tensor(0.0, dtype=x.dtype)
+    v = torch.round(x / s + zp)
+    v = torch.clamp(v, qmin, qmax)
+    return (v - zp) * s
+
+
+def quant_codes(x: torch.Tensor, q: Tuple[float, int, int]) -> torch.Tensor:
+    """Integer codes clamp(round(x / s)) as fp32 (the reference never
+    materialises int8; codes are integer-valued floats)."""
+    scale, qmin, qmax = q
+    s = torch.tensor(scale, dtype=x.dtype)
+    return torch.clamp(torch.round(x / s), qmin, qmax)
+
+
+def gru_step(gi_t: torch.Tensor, h: torch.Tensor, gh: torch.Tensor) -> torch.Tensor:
+    """One GRU update from the two projections; returns the pre-q_out h."""
+    gi_r, gi_z, gi_n = gi_t.chunk(3, dim=-1)
+    gh_r, gh_z, gh_n = gh.chunk(3, dim=-1)
+    r = torch.sigmoid(gi_r + gh_r)
+    z = torch.sigmoid(gi_z + gh_z)
+    n = torch.tanh(gi_n + r * gh_n)
+    return (1.0 - z) * n + z * h
+
+
+# ---- hidden maps (include bias) -----------------------------------------------------
+
+def gh_dense(hq: torch.Tensor, Wh_cat: torch.Tensor, bh: torch.Tensor) -> torch.Tensor:
+    return F.linear(hq, Wh_cat, bh)
+
+
+def gh_diagonal(hq: torch.Tensor, Wh_diag: torch.Tensor, bh: torch.Tensor) -> torch.Tensor:
+    H = hq.shape[-1]
+    b = bh.view(3, H)
+    return torch.cat([Wh_diag[0] * hq + b[0], Wh_diag[1] * hq + b[1], Wh_diag[2] * hq + b[2]], dim=-1)
+
+
+def gh_monarch(hq: torch.Tensor, Wh_struct: torch.Tensor, bh: torch.Tensor) -> torch.Tensor:
+    B, H = hq.shape
+    _, nb, bs, _ = Wh_struct.shape
+    gh = torch.einsum("bni,gnoi->bgno", hq.view(B, nb, bs), Wh_struct)
+    return (gh.reshape(B, 3, H) + bh.view(3, H)).reshape(B, 3 * H)
+
+
+def monarch_perm(nb: int, bs: int) -> torch.Tensor:
+    """perm[c * nb + a] = a * bs + c, so (P z) = z[perm]."""
+    c = torch.arange(bs).repeat_interleave(nb)
+    a = torch.arange(nb).repeat(bs)
+    return a * bs + c
+
+
+def gh_monarch2(hq: torch.Tensor, R: torch.Tensor, L: torch.Tensor, bh: torch.Tensor) -> torch.Tensor:
+    B, H = hq.shape
+    _, nb, bs, _ = R.shape
+    perm = monarch_perm(nb, bs)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(H)
+    z = torch.einsum("bni,gnoi->bgno", hq.view(B, nb, bs), R).reshape(B, 3, H)
+    u = z[:, :, perm]
+    v = torch.einsum("bgni,gnoi->bgno", u.reshape(B, 3, nb, bs), L).reshape(B, 3, H)
+    y = v[:, :, inv]
+    return (y + bh.view(3, H)).reshape(B, 3 * H)
+
+
+def butterfly_apply(x: torch.Tensor, tw_g: torch.Tensor) -> torch.Tensor:
+    """One gate's butterfly on rows of x [B, N]; tw_g is [nchains, L, N/2, 2, 2]."""
+    nchains, L, n2 = tw_g.shape[0], tw_g.shape[1], tw_g.shape[2]
+    N = 2 * n2
+    i = torch.arange(N)
+    for c in range(nchains):
+        for s in range(L):
+            ls = s if c % 2 == 0 else L - 1 - s
+            stride = 1 << ls
+            partner = i ^ stride
+            m = (i >> ls) & 1
+            pair = (i >> (ls + 1)) * stride + (i & (stride - 1))
+            t_ss = tw_g[c, s, pair, m, m]
+            t_sp = tw_g[c, s, pair, m, 1 - m]
+            x = t_ss * x + t_sp * x[:, partner]
+    return x
+
+
+def gh_butterfly(hq: torch.Tensor, twiddles: torch.Tensor, bh: torch.Tensor) -> torch.Tensor:
+    B, H = hq.shape
+    N = 2 * twiddles.shape[3]
+    xp = F.pad(hq, (0, N - H))
+    parts = [butterfly_apply(xp, twiddles[g])[:, :H] for g in range(3)]
+    return torch.cat(parts, dim=-1) + bh
+
+
+# ---- scans --------------------------------------------------------------------------
+
+GhFn = Callable[[torch.Tensor], torch.Tensor]
+
+
+def scan(gi: torch.Tensor, h0: torch.Tensor, gh_fn: GhFn, h_in_quant: QuantTuple = None,
+         h_out_quant: QuantTuple = None) -> torch.Tensor:
+    T = gi.shape[0]
+    out = torch.empty(T, *h0.shape, dtype=gi.dtype)
+    h = h0
+    for t in range(T):
+        h_new = gru_step(gi[t], h, gh_fn(fake_quant(h, h_in_quant)))
+        h_new = fake_quant(h_new, h_out_quant)
+        out[t] = h_new
+        h = h_new
+    return out
+
+
+def gh_fn_for(cfg: dict) -> GhFn:
+    kind = cfg["kind"]
+    w, bh = cfg["w"], cfg["bh"]
+    if kind == "dense":
+        return lambda hq: gh_dense(hq, w, bh)
+    if kind == "diagonal":
+        return lambda hq: gh_diagonal(hq, w, bh)
+    if kind == "monarch":
+        if cfg.get("w2") is not None:
+            w2 = cfg["w2"]
+            return lambda hq: gh_monarch2(hq, w, w2, bh)
+        return lambda hq: gh_monarch(hq, w, bh)
+    if kind == "butterfly":
+        return lambda hq: gh_butterfly(hq, w, bh)
+    raise ValueError(kind)
+
+
+def _cpu(cfg: dict) -> dict:
+    return {k: (v.detach().cpu() if isinstance(v, torch.Tensor) else v) for k, v in cfg.items()}
+
+
+def scan_config(cfg: dict) -> torch.Tensor:
+    """Runs the oracle on a config dict (see gru_qat_amd.configs); CPU tensors."""
+    c = _cpu(cfg)
+    return scan(c["gi"], c["h0"], gh_fn_for(c), c.get("h_in_quant"), c.get("h_out_quant"))
+
+
+def teacher_forced_prequant(cfg: dict, out_kernel: torch.Tensor) -> torch.Tensor:
+    """Pre-q_out hidden state of every step, computed by the oracle from the
+    kernel's own previous output (h_{t-1} = out_kernel[t-1], h_{-1} = h0).
+
+    Comparing quant codes of this against the kernel's codes checks every step
+    in isolation, so one boundary flip cannot propagate into later steps.
+    """
+    c = _cpu(cfg)
+    gi, h0 = c["gi"], c["h0"]
+    ok = out_kernel.detach().cpu()
+    gh_fn = gh_fn_for(c)
+    T = gi.shape[0]
+    pre = torch.empty_like(ok)
+    for t in range(T):
+        h = h0 if t == 0 else ok[t - 1]
+        pre[t] = gru_step(gi[t], h, gh_fn(fake_quant(h, c.get("h_in_quant"))))
+    return pre
+
+
+def materialize_hidden(cfg: dict) -> torch.Tensor:
+    """The hidden map of a config as a dense [3H, H] matrix (gh = hq @ M.T + bh),
+    obtained by pushing identity rows through the oracle's map."""
+    c = _cpu(cfg)
+    H = c["H"] if "H" in c else c["h0"].shape[-1]
+    eye = torch.eye(H, dtype=c["bh"].dtype)
+    zero_b = torch.zeros_like(c["bh"])
+    cz = dict(c)
+    cz["bh"] = zero_b
+    return gh_fn_for(cz)(eye).t().contiguous()

@@ -1,0 +1,148 @@
+"""C-ABI and wrapper checks that need no GPU: the library loads, exports every
+symbol include/gruscan.h declares, sizes workspaces, and rejects bad
+arguments with ValueError (never AssertionError) before any device work."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from gru_qat_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "gruscan.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(gs_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    assert _declared_symbols() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.gs_abi_version() == _lib.ABI_VERSION
+
+
+def _args(T=4, B=3, H=8, **kw):
+    a = _lib.GsArgs()
+    a.T, a.B, a.H = T, B, H
+    a.sg_t, a.sg_b = B * 3 * H, 3 * H
+    a.sh0_b = H
+    a.so_t, a.so_b = B * H, H
+    a.q_in = _lib.make_quant(kw.pop("q_in", None), "q_in")
+    a.q_out = _lib.make_quant(kw.pop("q_out", None), "q_out")
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+FAKE = 0x1000  # never dereferenced: validation fails before any device access
+
+
+@pytest.mark.parametrize("fn", ["gs_dense_fwd", "gs_diagonal_fwd", "gs_monarch_fwd", "gs_butterfly_fwd",
+                                "gs_butterfly_fwd_generic"])
+def test_null_pointers_rejected(fn):
+    lib = _lib.load()
+    a = _args()
+    rc = getattr(lib, fn)(ctypes.byref(a), None)
+    assert rc == _lib.GS_ERR_INVALID
+    assert b"non-NULL" in lib.gs_last_error()
+
+
+@pytest.mark.parametrize("field,msg", [("T", b"T must be > 0"), ("B", b"B must be > 0"), ("H", b"H must be > 0")])
+def test_empty_dims_rejected(field, msg):
+    lib = _lib.load()
+    a = _args(gi=FAKE, h0=FAKE, w=FAKE, bh=FAKE, out=FAKE)
+    setattr(a, field, 0)
+    assert lib.gs_dense_fwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert msg in lib.gs_last_error()
+
+
+def test_bad_quant_rejected():
+    lib = _lib.load()
+    a = _args(gi=FAKE, h0=FAKE, w=FAKE, bh=FAKE, out=FAKE, q_in=(0.0, -127, 127))
+    assert lib.gs_diagonal_fwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    a = _args(gi=FAKE, h0=FAKE, w=FAKE, bh=FAKE, out=FAKE, q_out=(0.1, 5, -5))
+    assert lib.gs_diagonal_fwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+
+
+def test_missing_workspace_rejected():
+    lib = _lib.load()
+    a = _args(gi=FAKE, h0=FAKE, w=FAKE, bh=FAKE, out=FAKE)
+    assert lib.gs_dense_fwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"workspace" in lib.gs_last_error()
+
+
+def test_monarch_shape_rejected():
+    lib = _lib.load()
+    a = _args(H=8, gi=FAKE, h0=FAKE, w=FAKE, bh=FAKE, out=FAKE, nblocks=3, blksz=3)
+    assert lib.gs_monarch_fwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"tile H" in lib.gs_last_error()
+
+
+def test_butterfly_shape_rejected():
+    lib = _lib.load()
+    a = _args(H=8, gi=FAKE, h0=FAKE, w=FAKE, bh=FAKE, out=FAKE, log_n=2, bfly_nblocks=1)
+    assert lib.gs_butterfly_fwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"H_PAD" in lib.gs_last_error()
+
+
+def test_workspace_sizes():
+    lib = _lib.load()
+    a = _args(T=64, B=32, H=512)
+    n = lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a))
+    assert 256 <= n <= 256 + 8 * 256 + 4096
+    q = (1.0 / 127, -127, 127)
+    a_same = _args(T=64, B=32, H=512, q_in=q, q_out=q)
+    assert lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a_same)) == n
+    a_diff = _args(T=64, B=32, H=512, q_in=q)
+    assert lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a_diff)) >= n + 2 * 32 * 512 * 4
+    a_m2 = _args(T=64, B=32, H=512, nblocks=8, blksz=64, w2=FAKE)
+    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m2)) >= 3 * 32 * 512 * 4
+    assert lib.gs_workspace_bytes(9, ctypes.byref(a)) == _lib.GS_ERR_INVALID
+
+
+# ---- Python wrappers: CPU tensors are rejected before any device work -----------------
+
+def _cpu_inputs(T=4, B=3, H=8):
+    gi = torch.randn(T, B, 3 * H)
+    h0 = torch.zeros(B, H)
+    bh = torch.zeros(3 * H)
+    return gi, h0, bh
+
+
+def test_wrappers_reject_cpu_tensors():
+    import gru_qat_amd as G
+
+    gi, h0, bh = _cpu_inputs()
+    cases = [
+        (G.gru_scan_persistent, torch.zeros(24, 8)),
+        (G.gru_scan, torch.zeros(24, 8)),
+        (G.gru_scan_diagonal, torch.zeros(3, 8)),
+        (G.gru_scan_monarch, torch.zeros(3, 2, 4, 4)),
+        (G.gru_scan_butterfly_triton, torch.zeros(3, 1, 3, 4, 2, 2)),
+    ]
+    for fn, w in cases:
+        with pytest.raises(ValueError) as ei:
+            fn(gi, h0, w, bh)
+        assert not isinstance(ei.value, AssertionError)
+        assert "CUDA" in str(ei.value)
+
+
+def test_bad_quant_tuple_rejected_on_cpu():
+    from gru_qat_amd._common import check_quant
+
+    with pytest.raises(ValueError):
+        check_quant((0.1, 1), "h_in_quant")
+    with pytest.raises(ValueError):
+        check_quant((-1.0, -127, 127), "h_in_quant")
+    assert check_quant((0.5, -127, 127), "h_in_quant") == (0.5, -127, 127)

@@ -1,0 +1,95 @@
+"""Run-to-run and structural invariants of the HIP scans on the GPU.
+
+Mirrors the reference's regression tests: 50-run determinism of the
+persistent kernel (tests/test_triton_scan_strict.py:490-528), batch
+invariance (tests/test_edge_cases.py:520-586), and adds workspace reuse
+across shapes and streams (the self-resetting barrier counters) and the
+barrier fault word.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import gru_qat_amd as G
+from gru_qat_amd.configs import make_config, run_config
+from parity_util import log, small_cfg, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("idx", [1, 2, 3])
+def test_determinism_50_runs(dev, idx):
+    cfg = to_dev(make_config(idx), dev)
+    log(f"[inv] determinism cfg{idx}")
+    first = run_config(cfg)
+    for _ in range(49):
+        assert torch.equal(run_config(cfg), first)
+    assert G.workspace_faults(dev) == 0
+
+
+@pytest.mark.parametrize("idx", [0, 1, 2, 3, 4])
+def test_batch_invariance(dev, idx):
+    T, B, H = (16, 8, 512) if idx != 4 else (8, 6, 1024)
+    cfg = make_config(idx, shape=(T, 1, H))
+    rep = dict(cfg)
+    rep["gi"] = cfg["gi"].expand(T, B, 3 * H).contiguous()
+    rep["h0"] = cfg["h0"].expand(B, H).contiguous()
+    rep["B"] = B
+    log(f"[inv] batch invariance cfg{idx}")
+    out = run_config(to_dev(rep, dev)).cpu()
+    for b in range(1, B):
+        assert torch.equal(out[:, b], out[:, 0]), f"row {b} differs"
+
+
+def test_workspace_reuse_across_shapes(dev):
+    """Alternating shapes and kinds on one stream must keep producing the
+    same results: every persistent launch leaves its counters zeroed."""
+    cfgs = [to_dev(small_cfg(1, s), dev) for s in [(5, 32, 512), (7, 4, 64), (3, 64, 256)]]
+    cfgs.append(to_dev(make_config(3, shape=(6, 16, 512)), dev))
+    firsts = [run_config(c) for c in cfgs]
+    for _ in range(5):
+        for c, f in zip(cfgs, firsts):
+            assert torch.equal(run_config(c), f)
+    assert G.workspace_faults(dev) == 0
+
+
+def test_side_stream_matches_default(dev):
+    cfg = to_dev(make_config(1), dev)
+    ref = run_config(cfg)
+    s = torch.cuda.Stream(dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        out = run_config(cfg)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(out, ref)
+
+
+def test_noncontiguous_inputs(dev):
+    cfg = small_cfg(1, (6, 8, 64))
+    d = to_dev(cfg, dev)
+    ref = run_config(d)
+    gi_nc = d["gi"].transpose(0, 1).contiguous().transpose(0, 1)  # [T, B, 3H] view with batch-major storage
+    assert not gi_nc.is_contiguous()
+    out = G.gru_scan_forward_persistent(gi_nc, d["h0"], d["w"], d["bh"])
+    assert torch.equal(out, ref)
+
+
+def test_wrapper_errors_on_gpu(dev):
+    d = to_dev(small_cfg(1, (4, 3, 8)), dev)
+    with pytest.raises(ValueError):
+        G.gru_scan_persistent(d["gi"], d["h0"][:, :7], d["w"], d["bh"])
+    with pytest.raises(ValueError):
+        G.gru_scan_persistent(d["gi"], d["h0"], d["w"][:, :7], d["bh"])
+    with pytest.raises(ValueError):
+        G.gru_scan_persistent(d["gi"].double(), d["h0"], d["w"], d["bh"])
+    with pytest.raises(ValueError):
+        G.gru_scan_diagonal(d["gi"], d["h0"], d["w"][:3, :8], d["bh"])
+    with pytest.raises(ValueError):
+        G.gru_scan_monarch(d["gi"], d["h0"], torch.zeros(3, 3, 3, 3, device=dev), d["bh"])
+    with pytest.raises(ValueError):
+        G.gru_scan_butterfly_triton(d["gi"], d["h0"], torch.zeros(3, 1, 2, 2, 2, 2, device=dev), d["bh"])
+    with pytest.raises(ValueError):
+        G.gru_scan_persistent(d["gi"][:0], d["h0"], d["w"], d["bh"])

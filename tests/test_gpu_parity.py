@@ -1,0 +1,174 @@
+"""Parity of the HIP kernels (through the C ABI) with the CPU oracle.
+
+fp32: max |out - oracle| <= 1e-5 on every element and on h_T.
+Quant: integer codes bit-exact wherever the pre-quant fp32 values agree (see
+parity_util.assert_quant_parity).
+Shapes cover the reference tests' grids (tests/test_triton_*.py,
+tests/test_edge_cases.py: T=1, B=1, H in {1, 2, 8}, partial batch tiles,
+non-multiple-of-4 sizes) and the five benchmark configurations.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gru_qat_amd.configs import Q_INT8_HIDDEN, make_config
+from parity_util import assert_fp32_parity, assert_quant_parity, small_cfg
+
+pytestmark = pytest.mark.gpu
+
+Q = Q_INT8_HIDDEN
+Q2 = (0.02, -100, 100)
+
+# ---- diagonal -----------------------------------------------------------------------------
+
+DIAG_SHAPES = [(8, 4, 32), (16, 8, 64), (8, 32, 64), (16, 32, 256), (1, 4, 8), (5, 1, 1), (5, 1, 2),
+               (3, 4, 1), (9, 3, 7), (13, 33, 100)]
+
+
+@pytest.mark.parametrize("shape", DIAG_SHAPES)
+def test_diagonal_fp32(dev, shape):
+    assert_fp32_parity(small_cfg(0, shape), dev)
+
+
+@pytest.mark.parametrize("qin,qout", [(Q, Q), (None, Q), (Q, None), (Q2, Q)])
+def test_diagonal_quant(dev, qin, qout):
+    cfg = small_cfg(0, (16, 8, 64), h_in_quant=qin, h_out_quant=qout)
+    if qout is None:
+        assert_fp32_parity(cfg, dev)
+    else:
+        assert_quant_parity(cfg, dev)
+
+
+def test_diagonal_cfg0(dev):
+    assert_fp32_parity(make_config(0), dev)
+
+
+# ---- dense --------------------------------------------------------------------------------
+
+DENSE_SHAPES = [(8, 16, 128), (16, 32, 256), (7, 4, 16), (16, 8, 32), (1, 4, 8), (5, 1, 1), (5, 1, 2),
+                (3, 4, 1), (3, 4, 2), (9, 3, 24), (6, 5, 17), (4, 33, 64), (3, 6, 300)]
+
+
+@pytest.mark.parametrize("shape", DENSE_SHAPES)
+def test_dense_fp32(dev, shape):
+    assert_fp32_parity(small_cfg(1, shape), dev)
+
+
+@pytest.mark.parametrize("qin,qout", [(Q, Q), (None, Q), (Q, None), (Q2, Q)])
+def test_dense_quant(dev, qin, qout):
+    cfg = small_cfg(1, (8, 4, 64), h_in_quant=qin, h_out_quant=qout)
+    if qout is None:
+        assert_fp32_parity(cfg, dev)
+    else:
+        assert_quant_parity(cfg, dev)
+
+
+def test_dense_cfg1(dev):
+    assert_fp32_parity(make_config(1), dev)
+
+
+def test_dense_cfg2_quant(dev):
+    assert_quant_parity(make_config(2), dev)
+
+
+def test_dense_h1024(dev):
+    assert_fp32_parity(small_cfg(1, (4, 8, 1024)), dev)
+
+
+# ---- Monarch ------------------------------------------------------------------------------
+
+def _monarch(shape, nb, two=False, seed=0, **over):
+    T, B, H = shape
+    cfg = make_config(3, shape=shape, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    bs = H // nb
+    cfg["w"] = (torch.rand((3, nb, bs, bs), generator=g) * 2 - 1) / bs ** 0.5
+    cfg["w2"] = ((torch.rand((3, nb, bs, bs), generator=g) * 2 - 1) / bs ** 0.5) if two else None
+    cfg["h_in_quant"] = None
+    cfg["h_out_quant"] = None
+    cfg.update(over)
+    return cfg
+
+
+MONARCH_CASES = [((8, 4, 32), 4), ((16, 8, 64), 4), ((8, 32, 64), 4), ((16, 32, 256), 4), ((6, 3, 30), 5),
+                 ((5, 4, 256), 2), ((4, 5, 8), 8), ((1, 4, 8), 2)]
+
+
+@pytest.mark.parametrize("shape,nb", MONARCH_CASES)
+def test_monarch_single_fp32(dev, shape, nb):
+    assert_fp32_parity(_monarch(shape, nb), dev)
+
+
+@pytest.mark.parametrize("shape,nb", [((5, 3, 32), 8), ((6, 5, 64), 4), ((4, 4, 256), 2), ((6, 3, 30), 5)])
+def test_monarch_two_factor_fp32(dev, shape, nb):
+    assert_fp32_parity(_monarch(shape, nb, two=True), dev)
+
+
+def test_monarch_two_factor_identity_equals_single(dev):
+    cfg = _monarch((6, 8, 64), 4)
+    eye = torch.eye(16).expand(3, 4, 16, 16).contiguous()
+    from parity_util import run_both, to_dev
+    from gru_qat_amd.configs import run_config
+
+    one = run_config(to_dev(cfg, dev))
+    two = run_config(to_dev(dict(cfg, w2=eye), dev))
+    assert torch.equal(one.cpu(), two.cpu())
+
+
+@pytest.mark.parametrize("two", [False, True])
+def test_monarch_quant(dev, two):
+    cfg = _monarch((16, 8, 64), 4, two=two, h_in_quant=Q, h_out_quant=Q)
+    assert_quant_parity(cfg, dev)
+
+
+def test_monarch_cfg3_single_factor_fp32(dev):
+    cfg = make_config(3)
+    cfg.update(w2=None, h_in_quant=None, h_out_quant=None)
+    assert_fp32_parity(cfg, dev)
+
+
+def test_monarch_cfg3(dev):
+    assert_quant_parity(make_config(3), dev)
+
+
+# ---- butterfly ----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(8, 4, 256), (8, 5, 512), (8, 3, 1024), (6, 4, 1000), (5, 3, 12),
+                                   (4, 2, 2), (3, 3, 64), (3, 2, 2048)])
+def test_butterfly_fp32(dev, shape):
+    assert_fp32_parity(small_cfg(4, shape), dev)
+
+
+@pytest.mark.parametrize("B", [1, 3, 5, 7, 9, 17, 33])
+def test_butterfly_partial_batch_sweep(dev, B):
+    # Reference tests/test_edge_cases.py:521-586 sweeps these B at (T=16, H=512).
+    assert_fp32_parity(small_cfg(4, (16, B, 512)), dev)
+
+
+def test_butterfly_two_chains(dev):
+    cfg = small_cfg(4, (6, 4, 64))
+    g = torch.Generator().manual_seed(3)
+    cfg["w"] = torch.randn((3, 2, 6, 32, 2, 2), generator=g) * 0.5 ** 0.5
+    assert_fp32_parity(cfg, dev)
+
+
+def test_butterfly_register_equals_generic(dev):
+    import gru_qat_amd.scan_butterfly as SB
+    from parity_util import to_dev
+
+    for shape in [(12, 6, 1024), (12, 6, 512), (12, 6, 256)]:
+        cfg = to_dev(small_cfg(4, shape), dev)
+        a = SB.gru_scan_butterfly_forward(cfg["gi"], cfg["h0"], cfg["w"], cfg["bh"])
+        b = SB.gru_scan_butterfly_forward_generic(cfg["gi"], cfg["h0"], cfg["w"], cfg["bh"])
+        assert (a - b).abs().max().item() <= 1e-5
+
+
+@pytest.mark.parametrize("qin,qout", [(Q, Q), (None, Q), (Q2, Q)])
+def test_butterfly_quant(dev, qin, qout):
+    assert_quant_parity(small_cfg(4, (16, 4, 1024), h_in_quant=qin, h_out_quant=qout), dev)
+
+
+def test_butterfly_cfg4(dev):
+    assert_fp32_parity(make_config(4), dev)
