@@ -66,57 +66,84 @@ __device__ __forceinline__ float lane_xor(float x, int m) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ m) << 2, __float_as_int(x)));
 }
 
-// ---- group barrier ----------------------------------------------------------------
-// All workgroups of one group share a monotonically increasing arrival counter;
-// the barrier of step t waits for count >= nwg_in_group * (t + 1). Agent-scope
-// release/acquire makes every store issued before the barrier (by any wave of
-// any arriving workgroup) visible to every load issued after it, whichever XCD
-// each workgroup runs on. The spin is bounded: if the counter has not moved for
-// kSpinLimit polls, the workgroup raises the fault word and every other
-// spinning workgroup leaves too, so a broken launch always drains instead of
-// hanging the device.
+// ---- tagged exchange --------------------------------------------------------------
+// Persistent kernels exchange hidden state between workgroups as 64-bit words
+// {fp32 value (low half), 32-bit step tag (high half)}, written and read with
+// relaxed agent-scope atomics. A consumer polls exactly the words it needs
+// until each carries the tag of the step it wants; an aligned 8-byte atomic is
+// single-copy atomic and coherent across the XCDs, so the value it returns is
+// the one stored with that tag. No fence, counter or grid barrier is needed,
+// and every wave proceeds as soon as its own inputs exist.
+//
+// Tags are tag_base + t + 1 for step t; tag_base lives in the workspace and
+// advances by T at the end of every launch, so a word left over from an
+// earlier launch (or a zeroed workspace, tag 0) never matches a tag the
+// current launch waits for until the 32-bit tag space wraps, after 2^32
+// steps on one workspace. Polls are bounded: after kSpinLimit polls the
+// waiter raises the fault word and every waiter gives up, so a broken launch
+// drains instead of hanging the device.
 constexpr uint32_t kSpinLimit = 1u << 22;
-constexpr int kCounterStride = 64;  // uint32 words between group counters (256 B)
 
 struct Ctrl {
-  uint32_t* fault;  // nonzero after a barrier time-out
-  uint32_t* exit_count;
-  uint32_t* counters;
+  uint32_t* fault;       // nonzero after a poll time-out
+  uint32_t* exit_count;  // workgroups that have finished this launch
+  uint32_t* tag_base;    // tags of this launch are tag_base + t + 1
 };
 
-__device__ __forceinline__ void group_barrier(const Ctrl& c, int group, uint32_t target) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t* cnt = c.counters + (size_t)group * kCounterStride;
-    __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t polls = 0;
-    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      if (__hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) break;
-      if (++polls > kSpinLimit) {
-        __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(1);
-    }
-  }
-  __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+__device__ __forceinline__ uint64_t ld_tagged(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Called once by every workgroup of a cooperative launch after its last
-// barrier. The last workgroup to leave zeroes the group counters and the exit
-// count, so the workspace is ready for the next launch on the stream. By then
-// every other workgroup has finished polling, so the reset cannot be observed
-// by a waiter.
-__device__ __forceinline__ void leave_grid(const Ctrl& c, int ngroups, uint32_t nwg) {
+__device__ __forceinline__ void st_tagged(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint32_t tag_of(uint64_t w) { return (uint32_t)(w >> 32); }
+__device__ __forceinline__ float value_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
+// Polls N words until every valid one carries `tag`. addr(i) returns the
+// word's address or nullptr for "no word" (value 0). Returns the values.
+template <int N, typename Addr>
+__device__ __forceinline__ void poll_tagged(const Ctrl& c, uint32_t tag, Addr addr, float (&out)[N]) {
+  uint64_t v[N];
+  const uint64_t ready_zero = (uint64_t)tag << 32;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const uint64_t* q = addr(i);
+    v[i] = q ? ld_tagged(q) : ready_zero;
+  }
+  uint32_t polls = 0;
+  while (true) {
+    bool ready = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) ready = ready && tag_of(v[i]) == tag;
+    if (ready) break;
+    if (++polls > kSpinLimit) {
+      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      break;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (tag_of(v[i]) != tag) v[i] = ld_tagged(addr(i));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = value_of(v[i]);
+}
+
+// Called once by every workgroup after its last exchange. The last one to
+// leave advances tag_base by the launch's step count (every workgroup read
+// tag_base before it incremented exit_count) and rearms exit_count.
+__device__ __forceinline__ void leave_grid(const Ctrl& c, uint32_t nwg, uint32_t base, uint32_t steps) {
   if (threadIdx.x == 0) {
     const uint32_t prev =
         __hip_atomic_fetch_add(c.exit_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == nwg - 1u) {
-      for (int g = 0; g < ngroups; ++g)
-        __hip_atomic_store(c.counters + (size_t)g * kCounterStride, 0u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(c.tag_base, base + steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(c.exit_count, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }
   }

@@ -27,17 +27,19 @@ void clear_error();
   } while (0)
 
 // Workspace layout (bytes from the start):
-//   [0, 256)                 control words: fault flag at word 0, exit count at word 32
-//   [256, 256 + 256*ngroups) one arrival counter per group, 256 B apart
-//   then float exchange buffers, each starting on a 256-byte boundary.
+//   [0, 256)        control words: fault flag (word 0), exit count (word 32),
+//                   tag base (word 48); zero on first use
+//   [256, ...)      tagged exchange words (uint64), 256-byte aligned regions
+// Every launch leaves the exit count at zero and the tag base advanced, and
+// only ever compares exchange words against tags newer than any word an
+// earlier launch wrote, so regions of differently shaped launches may overlap.
 constexpr int64_t kCtrlBytes = 256;
-constexpr int64_t kCounterBytes = 4 * kCounterStride;
 
 inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 inline Ctrl ctrl_of(void* ws) {
   uint32_t* w = static_cast<uint32_t*>(ws);
-  return Ctrl{w, w + 32, w + kCtrlBytes / 4};
+  return Ctrl{w, w + 32, w + 48};
 }
 
 inline Quant to_quant(const gs_quant& q) {

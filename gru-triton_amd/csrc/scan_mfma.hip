@@ -4,25 +4,35 @@
 //   dense    scan.py:76-210 (persistent kernel), scan.py:213-293 (launcher)
 //   Monarch  scan_monarch.py:130-291 (kernel), :320-406 (launcher), math :74-127
 //
-// Decomposition. The hidden units are split into quads of 4 consecutive units;
-// one wave owns one quad (all three gates, i.e. 12 rows of Wh) for the whole
-// scan. Its slice of Wh lives in VGPRs, loaded once. A *group* is the set of
-// workgroups that together cover every quad that a batch row depends on
+// Decomposition. Hidden units are split into quads of 4 consecutive units; one
+// wave owns one quad (all three gates: 12 rows of Wh) for the whole scan and
+// keeps that slice of Wh in VGPRs, loaded once. A *group* is the set of
+// workgroups that together produce every unit a batch row's next step needs
 // (dense: all of H; single-factor Monarch: one block; two-factor Monarch: all
-// of H); each group handles its own row-blocks of 4 batch rows and
-// synchronises only with itself, once per step (twice for two-factor
-// Monarch). Groups are interleaved in blockIdx (gid = blockIdx % ngroups), so
-// with round-robin workgroup placement the members of one group share an XCD.
+// of H). Each group owns RB row-blocks of 4 batch rows. Groups are
+// interleaved in blockIdx (gid = blockIdx % ngroups), so under round-robin
+// workgroup placement the members of a group share an XCD. All waves of a
+// workgroup read the same K range (Monarch: the same block).
 //
-// Per step and row-block, each wave computes gh[4 rows][4 units] for 3 gates
-// as 3 chains of v_mfma_f32_4x4x1_16b_f32: the instruction's 16 blocks are 16
-// interleaved slices of K (block b covers k = KC*b + m, m < KC), so KC
-// instructions per gate cover K = 16*KC. A is q_in(h)[row = lane&3][k], B is
-// Wh[unit = lane&3][k], D block b holds the partial dot products of slice b
-// (row = vgpr index, unit = lane&3). The 16 partials are summed with two DPP
-// row rotations and two cross-row swaps; afterwards lane l holds the full
-// gh[row = (l>>2)&3][unit = l&3], and the 16 lanes of row 0 run the gate
-// epilogue and store out[t].
+// Exchange. Every unit's matmul-side state q_in(h_t) is published as a
+// tagged 64-bit word (gs_device.h); consumers poll exactly the words they
+// need. Each workgroup stages the 4 x K slice of q_in(h_{t-1}) its waves read
+// into LDS (double-buffered), so one workgroup-local barrier per step and
+// phase is the only synchronisation; there is no grid barrier.
+//
+// Per step and row-block each wave computes gh[4 rows][4 units] for 3 gates
+// with v_mfma_f32_4x4x1_16b_f32 chains: the instruction's 16 blocks are 16
+// slices of K. A is q_in(h)[row = lane&3][k], B is Wh[unit = lane&3][k] and
+// D block b holds slice b's partial dot products (row = vgpr index,
+// unit = lane&3), with k(m, b) = 64*(m/4) + 4*b + m%4 so that each lane
+// reads its A operand as float4s from LDS. The 16 partials are summed with
+// two DPP row rotations and two cross-row swaps; lane l then holds
+// gh[row = (l>>2)&3][unit = l&3] and the 16 lanes of row 0 run the gate
+// epilogue, store out[t] and publish q_in(h_t).
+//
+// Two-factor Monarch runs two such phases per step: phase 1 publishes
+// z_g = R_g q_in(h) (tagged, per gate), phase 2 stages the workgroup's block
+// of P z_g, multiplies by L_g and lands the result on y = P^T v.
 #include <mutex>
 
 #include "gs_host.h"
@@ -41,24 +51,25 @@ struct MParams {
   const float* w2;
   const float* bh;
   float* out;
-  float* hqbuf;  // [2][B][H]: q_in(h_t) when the two quantizers differ
-  float* zbuf;   // two-factor Monarch: [3][B][H] output of the first factor
+  uint64_t* xh;  // [2][B][H] tagged q_in(h_t)
+  uint64_t* xz;  // two-factor Monarch: [2][3][B][H] tagged first-factor output
   Ctrl ctrl;
   int64_t sg_t, sg_b, sh0_b, so_t, so_b;
   int T, B, H;
-  int nb, bs;     // Monarch blocks (dense: nb = 1, bs = H)
-  int qpb;        // quads per block = ceil(bs / 4)
-  int ngroups;    // groups in the grid
-  int G;          // row-block sets (ngroups = G, or G * nb for single-factor Monarch)
-  int RB;         // row-blocks per set
-  int nrb;        // row-blocks = ceil(B / 4)
-  int P;          // workgroups per group
-  int nwg;        // workgroups in the grid
+  int nb, bs;   // Monarch blocks (dense: nb = 1, bs = H)
+  int qpb;      // quads per block = ceil(bs / 4)
+  int ngroups;  // groups in the grid
+  int G;        // row-block sets (ngroups = G, or G * nb for single-factor Monarch)
+  int RB;       // row-blocks per set
+  int nrb;      // row-blocks = ceil(B / 4)
+  int nwg;      // workgroups in the grid
+  int rs;       // LDS row stride (floats) of the staging buffers
   Quant qin, qout;
-  int hq_scratch;  // 1: matmul-side h of step t >= 1 comes from hqbuf, else from out
-  int vec_ok;      // rows of out / hqbuf may be read as float4
-  int coop;        // 1: groups span several workgroups (global barrier)
+  int qin_after_first;  // q_in must be applied to h_t before it is published
 };
+
+// k index of MFMA instruction m in k-slice b (see the header comment).
+__device__ __forceinline__ int kmap(int m, int b) { return 64 * (m >> 2) + 4 * b + (m & 3); }
 
 __device__ __forceinline__ float reduce16(f4 acc, int s) {
   // Sum the 4 k-slices that share this 16-lane row (lane bits 2..3) ...
@@ -75,47 +86,8 @@ __device__ __forceinline__ float reduce16(f4 acc, int s) {
   return v;
 }
 
-// Loads this lane's A operand: q_in(h)[row][kbase + KC*kb4 + m], m < KC, zero
-// outside [0, klen) or for rows >= B.
-template <int KC>
-__device__ __forceinline__ void load_hq(const MParams& p, int t, int row, int kbase, int klen,
-                                        int kb4, float (&a)[KC]) {
-  const int k0 = KC * kb4;
-  const bool row_ok = row < p.B;
-  if (t == 0) {
-    const float* src = p.h0 + (int64_t)row * p.sh0_b + kbase;
-#pragma unroll
-    for (int m = 0; m < KC; ++m) {
-      float v = 0.0f;
-      if (row_ok && k0 + m < klen) {
-        v = src[k0 + m];
-        if (p.qin.on) v = fake_quant(v, p.qin);
-      }
-      a[m] = v;
-    }
-    return;
-  }
-  const float* src = p.hq_scratch
-                         ? p.hqbuf + (int64_t)((t - 1) & 1) * p.B * p.H + (int64_t)row * p.H + kbase
-                         : p.out + (int64_t)(t - 1) * p.so_t + (int64_t)row * p.so_b + kbase;
-  if (p.vec_ok && row_ok && k0 + KC <= klen) {
-    const f4* v4 = reinterpret_cast<const f4*>(src + k0);
-#pragma unroll
-    for (int q = 0; q < KC / 4; ++q) {
-      const f4 v = v4[q];
-      a[4 * q + 0] = v[0];
-      a[4 * q + 1] = v[1];
-      a[4 * q + 2] = v[2];
-      a[4 * q + 3] = v[3];
-    }
-  } else {
-#pragma unroll
-    for (int m = 0; m < KC; ++m) a[m] = (row_ok && k0 + m < klen) ? src[k0 + m] : 0.0f;
-  }
-}
-
 // Loads Wh slice: w[((gate*nb + blk)*bs + o)*bs + k] for o = o0 + (lane&3),
-// k = KC*kb4 + m; zero where o >= bs or k >= bs.
+// k = kmap(m, kb4); zero where o >= bs or k >= bs.
 template <int KC>
 __device__ __forceinline__ void load_w(const float* w, int nb, int bs, int blk, int o0, int j,
                                        int kb4, bool blk_ok, float (&wr)[3][KC]) {
@@ -126,14 +98,29 @@ __device__ __forceinline__ void load_w(const float* w, int nb, int bs, int blk, 
     const float* row = w + ((int64_t)(g * nb + blk) * bs + o) * bs;
 #pragma unroll
     for (int m = 0; m < KC; ++m) {
-      const int k = KC * kb4 + m;
+      const int k = kmap(m, kb4);
       wr[g][m] = (ok && k < bs) ? row[k] : 0.0f;
     }
   }
 }
 
+// A operand from an LDS staging row: a[m] = row[kmap(m, kb4)].
 template <int KC>
-__device__ __forceinline__ void mfma3(const float (&a)[KC], const float (&wr)[3][KC], f4 (&acc)[3]) {
+__device__ __forceinline__ void lds_a(const float* row, int kb4, float (&a)[KC]) {
+#pragma unroll
+  for (int q = 0; q < KC / 4; ++q) {
+    const f4 v = *reinterpret_cast<const f4*>(row + 64 * q + 4 * kb4);
+    a[4 * q + 0] = v[0];
+    a[4 * q + 1] = v[1];
+    a[4 * q + 2] = v[2];
+    a[4 * q + 3] = v[3];
+  }
+}
+
+// Three MFMA chains (one per gate), two accumulators each for issue overlap.
+// With SHARED_A all gates multiply the same A operand (a[0]).
+template <int KC, bool SHARED_A>
+__device__ __forceinline__ void mfma3(const float (&a)[3][KC], const float (&wr)[3][KC], f4 (&acc)[3]) {
   f4 acc0[3], acc1[3];
 #pragma unroll
   for (int g = 0; g < 3; ++g) {
@@ -143,70 +130,110 @@ __device__ __forceinline__ void mfma3(const float (&a)[KC], const float (&wr)[3]
 #pragma unroll
   for (int m = 0; m < KC; m += 2) {
 #pragma unroll
-    for (int g = 0; g < 3; ++g) acc0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[m], wr[g][m], acc0[g], 0, 0, 0);
+    for (int g = 0; g < 3; ++g)
+      acc0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[SHARED_A ? 0 : g][m], wr[g][m], acc0[g], 0, 0, 0);
 #pragma unroll
     for (int g = 0; g < 3; ++g)
-      acc1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[m + 1], wr[g][m + 1], acc1[g], 0, 0, 0);
+      acc1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[SHARED_A ? 0 : g][m + 1], wr[g][m + 1], acc1[g], 0, 0, 0);
   }
 #pragma unroll
   for (int g = 0; g < 3; ++g) acc[g] = acc0[g] + acc1[g];
 }
 
-// Per-gate MFMA chain for the second Monarch factor (each gate has its own A).
-template <int KC>
-__device__ __forceinline__ void mfma3_sep(const float (&a)[3][KC], const float (&wr)[3][KC],
-                                          f4 (&acc)[3]) {
-  f4 acc0[3], acc1[3];
-#pragma unroll
-  for (int g = 0; g < 3; ++g) {
-    acc0[g] = f4{0.f, 0.f, 0.f, 0.f};
-    acc1[g] = f4{0.f, 0.f, 0.f, 0.f};
+// Stages q_in(h_{t-1})[rows 4rb..4rb+3][klo, klo + klen) into LDS rows of
+// stride rs (rows >= B become zeros). t == 0 reads h0 and applies q_in;
+// later steps poll the tagged words published at step t-1.
+template <int MW>
+__device__ __forceinline__ void stage_h(const MParams& p, int t, int rb, int klo, int klen, float* dst,
+                                        uint32_t tag_prev) {
+  const int words = 4 * klen;
+  const int tid = threadIdx.x;
+  const int nth = blockDim.x;
+  if (t == 0) {
+    for (int w = tid; w < words; w += nth) {
+      const int r = w / klen, k = w - r * klen;
+      const int row = 4 * rb + r;
+      float v = 0.0f;
+      if (row < p.B) {
+        v = p.h0[(int64_t)row * p.sh0_b + klo + k];
+        if (p.qin.on) v = fake_quant(v, p.qin);
+      }
+      dst[r * p.rs + k] = v;
+    }
+    return;
   }
+  const uint64_t* src = p.xh + (int64_t)((t - 1) & 1) * p.B * p.H;
+  for (int c0 = 0; c0 < words; c0 += MW * nth) {
+    float v[MW];
+    poll_tagged<MW>(
+        p.ctrl, tag_prev,
+        [&](int i) -> const uint64_t* {
+          const int w = c0 + tid + i * nth;
+          if (w >= words) return nullptr;
+          const int r = w / klen, k = w - r * klen;
+          const int row = 4 * rb + r;
+          return row < p.B ? src + (int64_t)row * p.H + klo + k : nullptr;
+        },
+        v);
 #pragma unroll
-  for (int m = 0; m < KC; m += 2) {
-#pragma unroll
-    for (int g = 0; g < 3; ++g)
-      acc0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[g][m], wr[g][m], acc0[g], 0, 0, 0);
-#pragma unroll
-    for (int g = 0; g < 3; ++g)
-      acc1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[g][m + 1], wr[g][m + 1], acc1[g], 0, 0, 0);
+    for (int i = 0; i < MW; ++i) {
+      const int w = c0 + tid + i * nth;
+      if (w < words) {
+        const int r = w / klen, k = w - r * klen;
+        dst[r * p.rs + k] = v[i];
+      }
+    }
   }
-#pragma unroll
-  for (int g = 0; g < 3; ++g) acc[g] = acc0[g] + acc1[g];
 }
 
-// Gate epilogue for (row, unit): all lanes compute, lanes 0..15 store.
-__device__ __forceinline__ void epilogue(const MParams& p, int t, int row, int unit, bool store,
-                                         const float (&gh)[3], const float (&bias)[3], float gir,
-                                         float giz, float gin, float hprev) {
-  float hn = gru_update(gir, giz, gin, gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
-  if (p.qout.on) hn = fake_quant(hn, p.qout);
-  if (store) {
-    p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
-    if (p.hq_scratch)
-      p.hqbuf[(int64_t)(t & 1) * p.B * p.H + (int64_t)row * p.H + unit] = fake_quant(hn, p.qin);
-  }
-}
-
-__device__ __forceinline__ void step_sync(const MParams& p, int gid, int t) {
-  if (p.coop) {
-    group_barrier(p.ctrl, gid, (uint32_t)p.P * (uint32_t)(t + 1));
-  } else {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+// Two-factor Monarch: stages (P z_g)[blk*bs + i] for i < bs, 3 gates, rows
+// 4rb..4rb+3 (LDS row g*4 + r), from the tagged first-factor outputs of step t.
+template <int MW>
+__device__ __forceinline__ void stage_z(const MParams& p, int t, int rb, int blk, float* dst, uint32_t tag) {
+  const int bs = p.bs;
+  const int words = 12 * bs;
+  const int tid = threadIdx.x;
+  const int nth = blockDim.x;
+  const uint64_t* src = p.xz + (int64_t)(t & 1) * 3 * p.B * p.H;
+  for (int c0 = 0; c0 < words; c0 += MW * nth) {
+    float v[MW];
+    poll_tagged<MW>(
+        p.ctrl, tag,
+        [&](int i) -> const uint64_t* {
+          const int w = c0 + tid + i * nth;
+          if (w >= words) return nullptr;
+          const int gr = w / bs, k = w - gr * bs;  // gr = g * 4 + r
+          const int g = gr >> 2, r = gr & 3;
+          const int row = 4 * rb + r;
+          if (row >= p.B) return nullptr;
+          const int idx = blk * bs + k;                     // position in P z
+          const int zpos = (idx % p.nb) * bs + idx / p.nb;  // position in z
+          return src + ((int64_t)g * p.B + row) * p.H + zpos;
+        },
+        v);
+#pragma unroll
+    for (int i = 0; i < MW; ++i) {
+      const int w = c0 + tid + i * nth;
+      if (w < words) {
+        const int gr = w / bs, k = w - gr * bs;
+        dst[gr * p.rs + k] = v[i];
+      }
+    }
   }
 }
 
 template <int KIND, int KC, int NT>
 __global__ __launch_bounds__(NT) void mfma_scan_kernel(MParams p) {
+  extern __shared__ float lds[];
+  constexpr int MWH = (4 * 16 * KC + NT - 1) / NT;   // staged h words per thread and pass
+  constexpr int MWZ = (12 * 16 * KC + NT - 1) / NT;  // staged z words per thread and pass
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
-  const int j = lane & 3;          // unit within the quad (B and D column)
-  const int kb4 = lane >> 2;       // k-slice (MFMA block)
-  const int s = (lane >> 2) & 3;   // D row owned after the reduction
-  const bool lead = lane < 16;     // lanes that store
+  const int j = lane & 3;         // unit within the quad (B and D column), A row
+  const int kb4 = lane >> 2;      // k-slice (MFMA block)
+  const int s = (lane >> 2) & 3;  // D row owned after the reduction
+  const bool lead = lane < 16;    // lanes that store
 
   const int gid = blockIdx.x % p.ngroups;
   const int pw = blockIdx.x / p.ngroups;
@@ -222,7 +249,15 @@ __global__ __launch_bounds__(NT) void mfma_scan_kernel(MParams p) {
     o0 = 4 * (quad - blk * p.qpb);
   }
   const bool blk_ok = blk < p.nb && o0 < p.bs;
-  const int kbase = blk * p.bs;
+  // The K range every wave of this workgroup reads: [klo, klo + bs).
+  const int wg_blk = (KIND == kDense) ? 0 : ((KIND == kMonarch1) ? blk : (pw * nw) / p.qpb);
+  const bool wg_ok = wg_blk < p.nb;
+  const int klo = wg_blk * p.bs;
+
+  float* hst = lds;             // [2][4][rs]
+  float* zst = lds + 8 * p.rs;  // two-factor Monarch: [2][12][rs]
+  for (int i = threadIdx.x; i < (KIND == kMonarch2 ? 32 : 8) * p.rs; i += blockDim.x) lds[i] = 0.0f;
+  __syncthreads();
 
   float wr[3][KC];
   load_w<KC>(p.w, p.nb, p.bs, blk, o0, j, kb4, blk_ok, wr);
@@ -231,95 +266,76 @@ __global__ __launch_bounds__(NT) void mfma_scan_kernel(MParams p) {
 
   // Epilogue unit of this lane. Two-factor Monarch: the second factor's row
   // vi = blk*bs + o0 + j lands on y[(vi % nb) * bs + vi / nb] (P^T).
-  const int vi = kbase + o0 + j;
+  const int vi = blk * p.bs + o0 + j;
   const bool unit_ok = blk_ok && (o0 + j) < p.bs;
   const int unit = (KIND == kMonarch2) ? (vi % p.nb) * p.bs + vi / p.nb : vi;
   float bias[3];
 #pragma unroll
   for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? p.bh[g * p.H + unit] : 0.0f;
 
+  const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int rb_begin = set * p.RB;
   const int rb_end = min(rb_begin + p.RB, p.nrb);
+  int hbuf = 0, zbuf = 0;
 
   for (int t = 0; t < p.T; ++t) {
-    if (KIND != kMonarch2) {
-      for (int rb = rb_begin; rb < rb_end; ++rb) {
-        const int row = 4 * rb + s;
-        const bool row_ok = row < p.B;
-        const bool store = lead && row_ok && unit_ok;
-        float gir = 0.f, giz = 0.f, gin = 0.f, hprev = 0.f;
-        if (row_ok && unit_ok) {
-          const float* g = p.gi + (int64_t)t * p.sg_t + (int64_t)row * p.sg_b + unit;
-          gir = g[0];
-          giz = g[p.H];
-          gin = g[2 * p.H];
-          hprev = (t == 0) ? p.h0[(int64_t)row * p.sh0_b + unit]
-                           : p.out[(int64_t)(t - 1) * p.so_t + (int64_t)row * p.so_b + unit];
-        }
-        float a[KC];
-        load_hq<KC>(p, t, 4 * rb + j, kbase, p.bs, kb4, a);
-        f4 acc[3];
-        mfma3<KC>(a, wr, acc);
-        float gh[3];
-#pragma unroll
-        for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
-        epilogue(p, t, row, unit, store, gh, bias, gir, giz, gin, hprev);
+    const uint32_t tag = base + (uint32_t)t + 1u;
+    const bool publish = t + 1 < p.T;
+    for (int rb = rb_begin; rb < rb_end; ++rb) {
+      const int row = 4 * rb + s;
+      const bool mine = lead && row < p.B && unit_ok;
+      // Epilogue operands first, so their latency overlaps the staging polls.
+      float gir = 0.f, giz = 0.f, gin = 0.f, hprev = 0.f;
+      if (mine) {
+        const float* g = p.gi + (int64_t)t * p.sg_t + (int64_t)row * p.sg_b + unit;
+        gir = g[0];
+        giz = g[p.H];
+        gin = g[2 * p.H];
+        hprev = (t == 0) ? p.h0[(int64_t)row * p.sh0_b + unit]
+                         : p.out[(int64_t)(t - 1) * p.so_t + (int64_t)row * p.so_b + unit];
       }
-    } else {
-      // Phase 1: z_g = R_g q_in(h), block-local.
-      for (int rb = rb_begin; rb < rb_end; ++rb) {
-        const int row = 4 * rb + s;
-        float a[KC];
-        load_hq<KC>(p, t, 4 * rb + j, kbase, p.bs, kb4, a);
-        f4 acc[3];
-        mfma3<KC>(a, wr, acc);
-        float z[3];
+      float* hs = hst + hbuf * 4 * p.rs;
+      hbuf ^= 1;
+      if (wg_ok) stage_h<MWH>(p, t, rb, klo, p.bs, hs, tag - 1u);
+      __syncthreads();
+      float a[3][KC];
+      lds_a<KC>(hs + j * p.rs, kb4, a[0]);
+      f4 acc[3];
+      mfma3<KC, true>(a, wr, acc);
+      float gh[3];
 #pragma unroll
-        for (int g = 0; g < 3; ++g) z[g] = reduce16(acc[g], s);
+      for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
+
+      if (KIND == kMonarch2) {
+        // Publish z_g = R_g q_in(h), then stage P z_g for this workgroup's block.
         if (lead && row < p.B && unit_ok) {
 #pragma unroll
           for (int g = 0; g < 3; ++g)
-            p.zbuf[((int64_t)g * p.B + row) * p.H + vi] = z[g];
+            st_tagged(p.xz + ((int64_t)((t & 1) * 3 + g) * p.B + row) * p.H + vi, gh[g], tag);
         }
-      }
-      step_sync(p, gid, 2 * t);
-      // Phase 2: v_g = L_g (P z_g); gh lands at y = P^T v.
-      for (int rb = rb_begin; rb < rb_end; ++rb) {
-        const int row = 4 * rb + s;
-        const bool row_ok = row < p.B;
-        const bool store = lead && row_ok && unit_ok;
-        float gir = 0.f, giz = 0.f, gin = 0.f, hprev = 0.f;
-        if (row_ok && unit_ok) {
-          const float* g = p.gi + (int64_t)t * p.sg_t + (int64_t)row * p.sg_b + unit;
-          gir = g[0];
-          giz = g[p.H];
-          gin = g[2 * p.H];
-          hprev = (t == 0) ? p.h0[(int64_t)row * p.sh0_b + unit]
-                           : p.out[(int64_t)(t - 1) * p.so_t + (int64_t)row * p.so_b + unit];
-        }
-        const int arow = 4 * rb + j;
-        float a[3][KC];
+        float* zs = zst + zbuf * 12 * p.rs;
+        zbuf ^= 1;
+        if (wg_ok) stage_z<MWZ>(p, t, rb, wg_blk, zs, tag);
+        __syncthreads();
 #pragma unroll
-        for (int m = 0; m < KC; ++m) {
-          const int k = KC * kb4 + m;
-          const bool ok = arow < p.B && k < p.bs && blk_ok;
-          const int idx = kbase + k;                       // position in P z
-          const int src = (idx % p.nb) * p.bs + idx / p.nb;  // position in z
-#pragma unroll
-          for (int g = 0; g < 3; ++g)
-            a[g][m] = ok ? p.zbuf[((int64_t)g * p.B + arow) * p.H + src] : 0.0f;
-        }
-        f4 acc[3];
-        mfma3_sep<KC>(a, wl, acc);
-        float gh[3];
+        for (int g = 0; g < 3; ++g) lds_a<KC>(zs + (g * 4 + j) * p.rs, kb4, a[g]);
+        mfma3<KC, false>(a, wl, acc);
 #pragma unroll
         for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
-        epilogue(p, t, row, unit, store, gh, bias, gir, giz, gin, hprev);
+      }
+
+      float hn = gru_update(gir, giz, gin, gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
+      if (p.qout.on) hn = fake_quant(hn, p.qout);
+      if (mine) {
+        p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
+        if (publish) {
+          const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
+          st_tagged(p.xh + ((int64_t)(t & 1) * p.B + row) * p.H + unit, hq, tag);
+        }
       }
     }
-    if (t + 1 < p.T) step_sync(p, gid, KIND == kMonarch2 ? 2 * t + 1 : t);
   }
-  if (p.coop) leave_grid(p.ctrl, p.ngroups, (uint32_t)p.nwg);
+  leave_grid(p.ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T);
 }
 
 // ---- host side --------------------------------------------------------------------
@@ -348,11 +364,22 @@ int device_info(DevInfo* out) {
 
 typedef void (*KernelFn)(MParams);
 
+// Workgroup size bound per instance: small reduction lengths keep few
+// registers per wave, so up to 16 waves share a workgroup; from KC = 16 on
+// (8 for the two-factor form, which holds two weight slices) a wave needs
+// more than 128 VGPRs and the workgroup is capped at 4 waves, one per SIMD.
 template <int KIND>
 KernelFn pick_kernel(int KC, int* nt) {
   switch (KC) {
     case 4: *nt = 1024; return mfma_scan_kernel<KIND, 4, 1024>;
-    case 8: *nt = 1024; return mfma_scan_kernel<KIND, 8, 1024>;
+    case 8:
+      if constexpr (KIND == kMonarch2) {
+        *nt = 256;
+        return mfma_scan_kernel<KIND, 8, 256>;
+      } else {
+        *nt = 1024;
+        return mfma_scan_kernel<KIND, 8, 1024>;
+      }
     case 16: *nt = 256; return mfma_scan_kernel<KIND, 16, 256>;
     case 32: *nt = 256; return mfma_scan_kernel<KIND, 32, 256>;
     case 64: *nt = 256; return mfma_scan_kernel<KIND, 64, 256>;
@@ -374,8 +401,9 @@ int choose_kc(int klen) {
 }
 
 struct Plan {
-  int kind, KC, nt, nw, P, G, RB, nrb, ngroups, nwg, coop, nb, bs, qpb;
-  int64_t counters_bytes, hq_bytes, z_bytes;
+  int kind, KC, nt, nw, P, G, RB, nrb, ngroups, nwg, nb, bs, qpb, rs;
+  int64_t xh_bytes, xz_bytes;
+  size_t lds_bytes;
 };
 
 // Static part of the plan (no device query): used for workspace sizing too.
@@ -396,17 +424,24 @@ int plan_static(int kind, const gs_args* a, Plan* pl, const char* who) {
   if (pl->KC < 0)
     return set_error(GS_ERR_INVALID, "%s: reduction length %d exceeds the supported maximum of 1024", who, pl->bs);
   pl->qpb = (pl->bs + 3) / 4;
-  const int quads = (kind == kMonarch1) ? pl->qpb : pl->nb * pl->qpb;
-  const int nwmax = pl->KC >= 16 ? 4 : 16;
-  pl->nw = quads < nwmax ? quads : nwmax;
-  pl->P = (quads + pl->nw - 1) / pl->nw;
-  pl->coop = pl->P > 1;
+  if (!pick(kind, pl->KC, &pl->nt)) return set_error(GS_ERR_INVALID, "%s: no kernel for KC=%d", who, pl->KC);
+  const int nwmax = pl->nt / 64;
+  if (kind == kDense) {
+    pl->nw = pl->qpb < nwmax ? pl->qpb : nwmax;
+    pl->P = (pl->qpb + pl->nw - 1) / pl->nw;
+  } else {
+    // The waves of a workgroup must share one Monarch block, so the wave count
+    // divides the quads per block.
+    int nw = pl->qpb < nwmax ? pl->qpb : nwmax;
+    while (pl->qpb % nw != 0) --nw;
+    pl->nw = nw;
+    pl->P = (kind == kMonarch1 ? pl->qpb : pl->nb * pl->qpb) / nw;
+  }
   pl->nrb = (int)((a->B + 3) / 4);
-  const int64_t max_groups = (int64_t)pl->nrb * (kind == kMonarch1 ? pl->nb : 1);
-  pl->counters_bytes = pl->coop ? align256(max_groups * kCounterBytes) : 0;
-  const bool hq_scratch = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
-  pl->hq_bytes = hq_scratch ? align256(2 * a->B * a->H * 4) : 0;
-  pl->z_bytes = (kind == kMonarch2) ? align256(3 * a->B * a->H * 4) : 0;
+  pl->rs = 16 * pl->KC + 4;  // one full MFMA K span per staged row (+4 floats of skew)
+  pl->lds_bytes = (size_t)(kind == kMonarch2 ? 32 : 8) * pl->rs * sizeof(float);
+  pl->xh_bytes = align256(2 * a->B * a->H * 8);
+  pl->xz_bytes = (kind == kMonarch2) ? align256(6 * a->B * a->H * 8) : 0;
   return GS_OK;
 }
 
@@ -414,7 +449,7 @@ int64_t workspace_bytes_for(int kind, const gs_args* a) {
   Plan pl;
   const int rc = plan_static(kind, a, &pl, "gs_workspace_bytes");
   if (rc) return rc;
-  return kCtrlBytes + pl.counters_bytes + pl.hq_bytes + pl.z_bytes;
+  return kCtrlBytes + pl.xh_bytes + pl.xz_bytes;
 }
 
 int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
@@ -426,23 +461,27 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   Plan pl;
   rc = plan_static(kind, a, &pl, who);
   if (rc) return rc;
-  const int64_t need = kCtrlBytes + pl.counters_bytes + pl.hq_bytes + pl.z_bytes;
-  rc = check_workspace(a, need, who);
+  rc = check_workspace(a, kCtrlBytes + pl.xh_bytes + pl.xz_bytes, who);
   if (rc) return rc;
 
   KernelFn fn = pick(kind, pl.KC, &pl.nt);
-  if (!fn) return set_error(GS_ERR_INVALID, "%s: no kernel for KC=%d", who, pl.KC);
   const int threads = pl.nw * 64;
+  if (pl.lds_bytes > 65536)
+    GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)pl.lds_bytes));
 
+  // Groups that span several workgroups wait on each other's published state,
+  // so all of their workgroups must be resident at once (cooperative launch).
+  const bool coop = pl.P > 1;
   const int per_set = pl.P * (kind == kMonarch1 ? pl.nb : 1);
   int G = pl.nrb;
-  if (pl.coop) {
+  if (coop) {
     DevInfo di;
     rc = device_info(&di);
     if (rc) return rc;
     if (!di.coop) return set_error(GS_ERR_CAPACITY, "%s: device does not support cooperative launch", who);
     int occ = 0;
-    GS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)fn, threads, 0));
+    GS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)fn, threads, pl.lds_bytes));
     const int64_t resident = (int64_t)occ * di.cus;
     if (resident < per_set)
       return set_error(GS_ERR_CAPACITY,
@@ -465,10 +504,9 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.bh = a->bh;
   p.out = a->out;
   char* ws = static_cast<char*>(a->workspace);
-  p.ctrl = ctrl_of(ws ? ws : nullptr);
-  p.hqbuf = pl.hq_bytes ? reinterpret_cast<float*>(ws + kCtrlBytes + pl.counters_bytes) : nullptr;
-  p.zbuf = pl.z_bytes ? reinterpret_cast<float*>(ws + kCtrlBytes + pl.counters_bytes + pl.hq_bytes)
-                      : nullptr;
+  p.ctrl = ctrl_of(ws);
+  p.xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
+  p.xz = pl.xz_bytes ? reinterpret_cast<uint64_t*>(ws + kCtrlBytes + pl.xh_bytes) : nullptr;
   p.sg_t = a->sg_t;
   p.sg_b = a->sg_b;
   p.sh0_b = a->sh0_b;
@@ -484,21 +522,18 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.G = pl.G;
   p.RB = pl.RB;
   p.nrb = pl.nrb;
-  p.P = pl.P;
   p.nwg = pl.nwg;
+  p.rs = pl.rs;
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
-  p.hq_scratch = pl.hq_bytes != 0;
-  const bool out_aligned = (reinterpret_cast<uintptr_t>(a->out) & 15u) == 0 && a->so_b % 4 == 0 &&
-                           a->so_t % 4 == 0;
-  p.vec_ok = (pl.bs % 4 == 0) && (a->H % 4 == 0) && (p.hq_scratch || out_aligned);
-  p.coop = pl.coop;
+  p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
 
-  if (pl.coop) {
+  if (coop) {
     void* kargs[] = {&p};
-    GS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)fn, dim3(pl.nwg), dim3(threads), kargs, 0, stream));
+    GS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)fn, dim3(pl.nwg), dim3(threads), kargs,
+                                            (unsigned)pl.lds_bytes, stream));
   } else {
-    hipLaunchKernelGGL(fn, dim3(pl.nwg), dim3(threads), 0, stream, p);
+    hipLaunchKernelGGL(fn, dim3(pl.nwg), dim3(threads), pl.lds_bytes, stream, p);
     GS_CHECK_HIP(hipGetLastError());
   }
   return GS_OK;

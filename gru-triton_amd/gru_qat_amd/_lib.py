@@ -139,14 +139,19 @@ def raise_for(rc: int, lib: ctypes.CDLL) -> None:
 
 
 # ---- per-(device, stream) workspace cache ----------------------------------------
-# A workspace is zeroed once when allocated; every kernel leaves it zeroed
-# again, so launches ordered on one stream can share it. Distinct streams get
-# distinct workspaces.
+# A workspace is zeroed once when allocated. Every launch leaves its control
+# words ready for the next launch ordered after it on the same stream, so
+# launches on one stream share a workspace; distinct streams get distinct
+# workspaces. The persistent kernels tag exchanged words with a 32-bit step
+# counter kept in the workspace; before that counter could wrap, the
+# workspace is zeroed again (the host mirrors the step count it has issued).
 _ws_cache: dict = {}
+_ws_steps: dict = {}
 _ws_lock = threading.Lock()
+_TAG_LIMIT = (1 << 32) - (1 << 24)
 
 
-def workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Tensor:
+def workspace(device: torch.device, stream_handle: int, nbytes: int, steps: int = 0) -> torch.Tensor:
     key = (device.index, stream_handle)
     with _ws_lock:
         ws = _ws_cache.get(key)
@@ -156,6 +161,12 @@ def workspace(device: torch.device, stream_handle: int, nbytes: int) -> torch.Te
                 size = max(size, 2 * ws.numel())
             ws = torch.zeros(size, dtype=torch.uint8, device=device)
             _ws_cache[key] = ws
+            _ws_steps[key] = 0
+        if steps:
+            if _ws_steps[key] + steps + 1 >= _TAG_LIMIT:
+                ws.zero_()
+                _ws_steps[key] = 0
+            _ws_steps[key] += steps
         return ws
 
 
@@ -210,7 +221,8 @@ def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: to
         raise_for(int(need), lib)
     with torch.cuda.device(gi.device):
         handle = torch.cuda.current_stream(gi.device).cuda_stream
-        ws = workspace(gi.device, handle, int(need))
+        tagged = kind in (KIND_DENSE, KIND_MONARCH)
+        ws = workspace(gi.device, handle, int(need), steps=T if tagged else 0)
         a.workspace = ws.data_ptr()
         a.workspace_bytes = ws.numel()
         rc = getattr(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))

@@ -97,17 +97,23 @@ def test_butterfly_shape_rejected():
 
 
 def test_workspace_sizes():
+    """Control words plus double-buffered tagged exchange words (8 bytes per
+    unit and row; two-factor Monarch adds 3 gates of first-factor words)."""
     lib = _lib.load()
     a = _args(T=64, B=32, H=512)
     n = lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a))
-    assert 256 <= n <= 256 + 8 * 256 + 4096
+    xh = 2 * 32 * 512 * 8
+    assert n == 256 + xh
     q = (1.0 / 127, -127, 127)
-    a_same = _args(T=64, B=32, H=512, q_in=q, q_out=q)
-    assert lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a_same)) == n
-    a_diff = _args(T=64, B=32, H=512, q_in=q)
-    assert lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a_diff)) >= n + 2 * 32 * 512 * 4
+    for kw in ({"q_in": q, "q_out": q}, {"q_in": q}):
+        assert lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(_args(T=64, B=32, H=512, **kw))) == n
+    a_m1 = _args(T=64, B=32, H=512, nblocks=8, blksz=64)
+    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m1)) == n
     a_m2 = _args(T=64, B=32, H=512, nblocks=8, blksz=64, w2=FAKE)
-    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m2)) >= 3 * 32 * 512 * 4
+    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m2)) == n + 3 * xh
+    # diagonal and butterfly kernels use no workspace beyond the control words
+    assert lib.gs_workspace_bytes(_lib.KIND_DIAGONAL, ctypes.byref(a)) == 256
+    assert lib.gs_workspace_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) == 256
     assert lib.gs_workspace_bytes(9, ctypes.byref(a)) == _lib.GS_ERR_INVALID
 
 

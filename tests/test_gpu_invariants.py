@@ -55,6 +55,22 @@ def test_workspace_reuse_across_shapes(dev):
     assert G.workspace_faults(dev) == 0
 
 
+def test_scratch_writes_never_reach_barrier_counters(dev):
+    """Regression: a call that uses the exchange buffer (q_in != q_out) and a
+    call that uses the two-factor Monarch z buffer, followed by cooperative
+    calls with many groups on the same workspace. The exchange data must not
+    land on the later calls' barrier counters (it once did: barriers then
+    released early and results went wrong only after such a call)."""
+    from parity_util import assert_fp32_parity
+
+    q = (0.02, -100, 100)
+    run_config(to_dev(small_cfg(1, (8, 4, 64), h_in_quant=q, h_out_quant=(1.0 / 127, -127, 127)), dev))
+    assert_fp32_parity(make_config(1), dev)
+    run_config(to_dev(make_config(3, shape=(6, 16, 512)), dev))
+    assert_fp32_parity(make_config(1), dev)
+    assert G.workspace_faults(dev) == 0
+
+
 def test_side_stream_matches_default(dev):
     cfg = to_dev(make_config(1), dev)
     ref = run_config(cfg)
@@ -86,7 +102,7 @@ def test_wrapper_errors_on_gpu(dev):
     with pytest.raises(ValueError):
         G.gru_scan_persistent(d["gi"].double(), d["h0"], d["w"], d["bh"])
     with pytest.raises(ValueError):
-        G.gru_scan_diagonal(d["gi"], d["h0"], d["w"][:3, :8], d["bh"])
+        G.gru_scan_diagonal(d["gi"], d["h0"], d["w"][:3, :7], d["bh"])
     with pytest.raises(ValueError):
         G.gru_scan_monarch(d["gi"], d["h0"], torch.zeros(3, 3, 3, 3, device=dev), d["bh"])
     with pytest.raises(ValueError):
