@@ -66,6 +66,21 @@ __device__ __forceinline__ float lane_xor(float x, int m) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ m) << 2, __float_as_int(x)));
 }
 
+// x[l] + x[l ^ 16] + x[l ^ 32] + x[l ^ 48] in every lane, with gfx950's VALU
+// row swaps: permlane16_swap(x, x) returns (x with odd rows replaced by the
+// even rows below them, x with even rows replaced by the odd rows above
+// them), so the sum of its two results is x[l] + x[l ^ 16] in every lane (the
+// two operands are the same in both lanes of a pair, and fp32 addition
+// commutes, so both lanes hold bitwise the same sum); permlane32_swap does
+// the same for l ^ 32.
+__device__ __forceinline__ float sum_across_rows(float x) {
+  typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+  const u2 a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const u2 b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // ---- tagged exchange --------------------------------------------------------------
 // Persistent kernels exchange hidden state between workgroups as 64-bit words
 // {fp32 value (low half), 32-bit step tag (high half)}, written and read with
@@ -133,6 +148,39 @@ __device__ __forceinline__ void poll_tagged(const Ctrl& c, uint32_t tag, Addr ad
   }
 #pragma unroll
   for (int i = 0; i < N; ++i) out[i] = value_of(v[i]);
+}
+
+// Polls MW words base[src[i]] (those with bit i of `valid`) until each
+// carries `tag`, then stores their values to dst_lds[dst[i]]. Offsets are
+// precomputed by the caller, so the loop is loads, compares and a sleep.
+template <int MW>
+__device__ __forceinline__ void poll_to_lds(const Ctrl& c, const uint64_t* base, const int (&src)[MW],
+                                            const int (&dst)[MW], uint32_t valid, uint32_t tag,
+                                            float* dst_lds) {
+  uint64_t v[MW];
+#pragma unroll
+  for (int i = 0; i < MW; ++i) v[i] = ld_tagged(base + src[i]);
+  uint32_t polls = 0;
+  while (true) {
+    uint32_t pending = 0;
+#pragma unroll
+    for (int i = 0; i < MW; ++i) pending |= (tag_of(v[i]) != tag ? 1u : 0u) << i;
+    pending &= valid;
+    if (pending == 0u) break;
+    if (++polls > kSpinLimit) {
+      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      break;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int i = 0; i < MW; ++i)
+      if ((pending >> i) & 1u) v[i] = ld_tagged(base + src[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < MW; ++i)
+    if ((valid >> i) & 1u) dst_lds[dst[i]] = value_of(v[i]);
 }
 
 // Called once by every workgroup after its last exchange. The last one to

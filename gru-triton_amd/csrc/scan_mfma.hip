@@ -26,7 +26,7 @@
 // D block b holds slice b's partial dot products (row = vgpr index,
 // unit = lane&3), with k(m, b) = 64*(m/4) + 4*b + m%4 so that each lane
 // reads its A operand as float4s from LDS. The 16 partials are summed with
-// two DPP row rotations and two cross-row swaps; lane l then holds
+// two DPP row rotations and two permlane row swaps; lane l then holds
 // gh[row = (l>>2)&3][unit = l&3] and the 16 lanes of row 0 run the gate
 // epilogue, store out[t] and publish q_in(h_t).
 //
@@ -51,8 +51,8 @@ struct MParams {
   const float* w2;
   const float* bh;
   float* out;
-  uint64_t* xh;  // [2][B][H] tagged q_in(h_t)
-  uint64_t* xz;  // two-factor Monarch: [2][3][B][H] tagged first-factor output
+  uint64_t* xh;  // [2][Bp][H] tagged q_in(h_t), Bp = 4 * nrb (padding rows hold finite filler)
+  uint64_t* xz;  // two-factor Monarch: [2][3][Bp][H] tagged first-factor output
   Ctrl ctrl;
   int64_t sg_t, sg_b, sh0_b, so_t, so_b;
   int T, B, H;
@@ -62,6 +62,7 @@ struct MParams {
   int G;        // row-block sets (ngroups = G, or G * nb for single-factor Monarch)
   int RB;       // row-blocks per set
   int nrb;      // row-blocks = ceil(B / 4)
+  int Bp;       // 4 * nrb: rows of the exchange buffers
   int nwg;      // workgroups in the grid
   int rs;       // LDS row stride (floats) of the staging buffers
   Quant qin, qout;
@@ -79,11 +80,9 @@ __device__ __forceinline__ float reduce16(f4 acc, int s) {
     acc[c] += row_ror<4>(acc[c]);
   }
   // ... keep the D row this lane will own (row index == lane bits 2..3) ...
-  float v = (s == 0) ? acc[0] : (s == 1) ? acc[1] : (s == 2) ? acc[2] : acc[3];
+  const float v = (s == 0) ? acc[0] : (s == 1) ? acc[1] : (s == 2) ? acc[2] : acc[3];
   // ... and add the other three 16-lane rows.
-  v += lane_xor(v, 16);
-  v += lane_xor(v, 32);
-  return v;
+  return sum_across_rows(v);
 }
 
 // Loads Wh slice: w[((gate*nb + blk)*bs + o)*bs + k] for o = o0 + (lane&3),
@@ -140,85 +139,105 @@ __device__ __forceinline__ void mfma3(const float (&a)[3][KC], const float (&wr)
   for (int g = 0; g < 3; ++g) acc[g] = acc0[g] + acc1[g];
 }
 
-// Stages q_in(h_{t-1})[rows 4rb..4rb+3][klo, klo + klen) into LDS rows of
-// stride rs (rows >= B become zeros). t == 0 reads h0 and applies q_in;
-// later steps poll the tagged words published at step t-1.
+// Staging. Each thread owns MW words of a workgroup's per-step slice; its
+// word offsets are computed once (StagePlan) and the per-step work is the
+// poll. A slice larger than MW * threads (only for workgroups smaller than
+// the instance's maximum) is staged in several passes with offsets computed
+// on the fly.
 template <int MW>
-__device__ __forceinline__ void stage_h(const MParams& p, int t, int rb, int klo, int klen, float* dst,
-                                        uint32_t tag_prev) {
-  const int words = 4 * klen;
-  const int tid = threadIdx.x;
-  const int nth = blockDim.x;
-  if (t == 0) {
-    for (int w = tid; w < words; w += nth) {
-      const int r = w / klen, k = w - r * klen;
-      const int row = 4 * rb + r;
-      float v = 0.0f;
-      if (row < p.B) {
-        v = p.h0[(int64_t)row * p.sh0_b + klo + k];
-        if (p.qin.on) v = fake_quant(v, p.qin);
-      }
-      dst[r * p.rs + k] = v;
-    }
-    return;
+struct StagePlan {
+  int src[MW];     // word offset from the row-block's slot base
+  int dst[MW];     // LDS offset (floats)
+  uint32_t valid;  // bit i: word i exists
+  bool single;     // the whole slice fits one pass
+};
+
+// q_in(h) slice: rows r < 4, k < klen -> src r*H + klo + k, dst r*rs + k.
+template <int MW>
+__device__ __forceinline__ StagePlan<MW> plan_h(const MParams& p, int klo, int klen) {
+  StagePlan<MW> pl;
+  const int words = 4 * klen, tid = threadIdx.x, nth = blockDim.x;
+  pl.valid = 0;
+  pl.single = words <= MW * nth;
+#pragma unroll
+  for (int i = 0; i < MW; ++i) {
+    const int w = tid + i * nth;
+    const int r = w / klen, k = w - r * klen;
+    const bool ok = w < words;
+    pl.src[i] = ok ? r * p.H + klo + k : 0;
+    pl.dst[i] = ok ? r * p.rs + k : 0;
+    pl.valid |= (ok ? 1u : 0u) << i;
   }
-  const uint64_t* src = p.xh + (int64_t)((t - 1) & 1) * p.B * p.H;
+  return pl;
+}
+
+// Two-factor Monarch: (P z_g)[blk*bs + k] for gates g, rows r < 4, k < bs
+// -> src g*Bp*H + r*H + zpos, dst (g*4 + r)*rs + k.
+__device__ __forceinline__ int zsrc(const MParams& p, int blk, int w) {
+  const int gr = w / p.bs, k = w - gr * p.bs;
+  const int idx = blk * p.bs + k;                      // position in P z
+  const int zpos = (idx % p.nb) * p.bs + idx / p.nb;   // position in z
+  return ((gr >> 2) * p.Bp + (gr & 3)) * p.H + zpos;
+}
+
+template <int MW>
+__device__ __forceinline__ StagePlan<MW> plan_z(const MParams& p, int blk) {
+  StagePlan<MW> pl;
+  const int words = 12 * p.bs, tid = threadIdx.x, nth = blockDim.x;
+  pl.valid = 0;
+  pl.single = words <= MW * nth;
+#pragma unroll
+  for (int i = 0; i < MW; ++i) {
+    const int w = tid + i * nth;
+    const bool ok = w < words;
+    const int gr = w / p.bs;
+    pl.src[i] = ok ? zsrc(p, blk, w) : 0;
+    pl.dst[i] = ok ? gr * p.rs + (w - gr * p.bs) : 0;
+    pl.valid |= (ok ? 1u : 0u) << i;
+  }
+  return pl;
+}
+
+// Multi-pass staging with offsets computed per word (rare shapes only).
+template <int MW, bool Z>
+__device__ __forceinline__ void stage_general(const MParams& p, const uint64_t* base, int klo, int klen, int blk,
+                                           float* dst, uint32_t tag) {
+  const int words = Z ? 12 * p.bs : 4 * klen;
+  const int tid = threadIdx.x, nth = blockDim.x;
   for (int c0 = 0; c0 < words; c0 += MW * nth) {
-    float v[MW];
-    poll_tagged<MW>(
-        p.ctrl, tag_prev,
-        [&](int i) -> const uint64_t* {
-          const int w = c0 + tid + i * nth;
-          if (w >= words) return nullptr;
-          const int r = w / klen, k = w - r * klen;
-          const int row = 4 * rb + r;
-          return row < p.B ? src + (int64_t)row * p.H + klo + k : nullptr;
-        },
-        v);
+    int src[MW], off[MW];
+    uint32_t valid = 0;
 #pragma unroll
     for (int i = 0; i < MW; ++i) {
       const int w = c0 + tid + i * nth;
-      if (w < words) {
+      const bool ok = w < words;
+      if (Z) {
+        const int gr = w / p.bs;
+        src[i] = ok ? zsrc(p, blk, w) : 0;
+        off[i] = ok ? gr * p.rs + (w - gr * p.bs) : 0;
+      } else {
         const int r = w / klen, k = w - r * klen;
-        dst[r * p.rs + k] = v[i];
+        src[i] = ok ? r * p.H + klo + k : 0;
+        off[i] = ok ? r * p.rs + k : 0;
       }
+      valid |= (ok ? 1u : 0u) << i;
     }
+    poll_to_lds<MW>(p.ctrl, base, src, off, valid, tag, dst);
   }
 }
 
-// Two-factor Monarch: stages (P z_g)[blk*bs + i] for i < bs, 3 gates, rows
-// 4rb..4rb+3 (LDS row g*4 + r), from the tagged first-factor outputs of step t.
-template <int MW>
-__device__ __forceinline__ void stage_z(const MParams& p, int t, int rb, int blk, float* dst, uint32_t tag) {
-  const int bs = p.bs;
-  const int words = 12 * bs;
-  const int tid = threadIdx.x;
-  const int nth = blockDim.x;
-  const uint64_t* src = p.xz + (int64_t)(t & 1) * 3 * p.B * p.H;
-  for (int c0 = 0; c0 < words; c0 += MW * nth) {
-    float v[MW];
-    poll_tagged<MW>(
-        p.ctrl, tag,
-        [&](int i) -> const uint64_t* {
-          const int w = c0 + tid + i * nth;
-          if (w >= words) return nullptr;
-          const int gr = w / bs, k = w - gr * bs;  // gr = g * 4 + r
-          const int g = gr >> 2, r = gr & 3;
-          const int row = 4 * rb + r;
-          if (row >= p.B) return nullptr;
-          const int idx = blk * bs + k;                     // position in P z
-          const int zpos = (idx % p.nb) * bs + idx / p.nb;  // position in z
-          return src + ((int64_t)g * p.B + row) * p.H + zpos;
-        },
-        v);
-#pragma unroll
-    for (int i = 0; i < MW; ++i) {
-      const int w = c0 + tid + i * nth;
-      if (w < words) {
-        const int gr = w / bs, k = w - gr * bs;
-        dst[gr * p.rs + k] = v[i];
-      }
+// Step 0 input: q_in(h0) rows 4rb..4rb+3 (zeros past B), cols [klo, klo+klen).
+__device__ __forceinline__ void stage_h0(const MParams& p, int rb, int klo, int klen, float* dst) {
+  const int words = 4 * klen;
+  for (int w = threadIdx.x; w < words; w += blockDim.x) {
+    const int r = w / klen, k = w - r * klen;
+    const int row = 4 * rb + r;
+    float v = 0.0f;
+    if (row < p.B) {
+      v = p.h0[(int64_t)row * p.sh0_b + klo + k];
+      if (p.qin.on) v = fake_quant(v, p.qin);
     }
+    dst[r * p.rs + k] = v;
   }
 }
 
@@ -273,6 +292,10 @@ __global__ __launch_bounds__(NT) void mfma_scan_kernel(MParams p) {
 #pragma unroll
   for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? p.bh[g * p.H + unit] : 0.0f;
 
+  const StagePlan<MWH> hplan = plan_h<MWH>(p, klo, p.bs);
+  StagePlan<MWZ> zplan;
+  if (KIND == kMonarch2) zplan = plan_z<MWZ>(p, wg_blk);
+
   const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int rb_begin = set * p.RB;
   const int rb_end = min(rb_begin + p.RB, p.nrb);
@@ -284,6 +307,7 @@ __global__ __launch_bounds__(NT) void mfma_scan_kernel(MParams p) {
     for (int rb = rb_begin; rb < rb_end; ++rb) {
       const int row = 4 * rb + s;
       const bool mine = lead && row < p.B && unit_ok;
+      const bool pub = lead && unit_ok;  // padding rows are published too (finite filler)
       // Epilogue operands first, so their latency overlaps the staging polls.
       float gir = 0.f, giz = 0.f, gin = 0.f, hprev = 0.f;
       if (mine) {
@@ -296,7 +320,17 @@ __global__ __launch_bounds__(NT) void mfma_scan_kernel(MParams p) {
       }
       float* hs = hst + hbuf * 4 * p.rs;
       hbuf ^= 1;
-      if (wg_ok) stage_h<MWH>(p, t, rb, klo, p.bs, hs, tag - 1u);
+      if (wg_ok) {
+        if (t == 0) {
+          stage_h0(p, rb, klo, p.bs, hs);
+        } else {
+          const uint64_t* hb = p.xh + ((int64_t)((t - 1) & 1) * p.Bp + 4 * rb) * p.H;
+          if (hplan.single)
+            poll_to_lds<MWH>(p.ctrl, hb, hplan.src, hplan.dst, hplan.valid, tag - 1u, hs);
+          else
+            stage_general<MWH, false>(p, hb, klo, p.bs, 0, hs, tag - 1u);
+        }
+      }
       __syncthreads();
       float a[3][KC];
       lds_a<KC>(hs + j * p.rs, kb4, a[0]);
@@ -308,14 +342,20 @@ __global__ __launch_bounds__(NT) void mfma_scan_kernel(MParams p) {
 
       if (KIND == kMonarch2) {
         // Publish z_g = R_g q_in(h), then stage P z_g for this workgroup's block.
-        if (lead && row < p.B && unit_ok) {
+        if (pub) {
 #pragma unroll
           for (int g = 0; g < 3; ++g)
-            st_tagged(p.xz + ((int64_t)((t & 1) * 3 + g) * p.B + row) * p.H + vi, gh[g], tag);
+            st_tagged(p.xz + ((int64_t)((t & 1) * 3 + g) * p.Bp + row) * p.H + vi, gh[g], tag);
         }
         float* zs = zst + zbuf * 12 * p.rs;
         zbuf ^= 1;
-        if (wg_ok) stage_z<MWZ>(p, t, rb, wg_blk, zs, tag);
+        if (wg_ok) {
+          const uint64_t* zb = p.xz + (int64_t)(t & 1) * 3 * p.Bp * p.H + (int64_t)4 * rb * p.H;
+          if (zplan.single)
+            poll_to_lds<MWZ>(p.ctrl, zb, zplan.src, zplan.dst, zplan.valid, tag, zs);
+          else
+            stage_general<MWZ, true>(p, zb, 0, 0, wg_blk, zs, tag);
+        }
         __syncthreads();
 #pragma unroll
         for (int g = 0; g < 3; ++g) lds_a<KC>(zs + (g * 4 + j) * p.rs, kb4, a[g]);
@@ -326,12 +366,10 @@ __global__ __launch_bounds__(NT) void mfma_scan_kernel(MParams p) {
 
       float hn = gru_update(gir, giz, gin, gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
       if (p.qout.on) hn = fake_quant(hn, p.qout);
-      if (mine) {
-        p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
-        if (publish) {
-          const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
-          st_tagged(p.xh + ((int64_t)(t & 1) * p.B + row) * p.H + unit, hq, tag);
-        }
+      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
+      if (pub && publish) {
+        const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
+        st_tagged(p.xh + ((int64_t)(t & 1) * p.Bp + row) * p.H + unit, hq, tag);
       }
     }
   }
@@ -440,8 +478,9 @@ int plan_static(int kind, const gs_args* a, Plan* pl, const char* who) {
   pl->nrb = (int)((a->B + 3) / 4);
   pl->rs = 16 * pl->KC + 4;  // one full MFMA K span per staged row (+4 floats of skew)
   pl->lds_bytes = (size_t)(kind == kMonarch2 ? 32 : 8) * pl->rs * sizeof(float);
-  pl->xh_bytes = align256(2 * a->B * a->H * 8);
-  pl->xz_bytes = (kind == kMonarch2) ? align256(6 * a->B * a->H * 8) : 0;
+  const int64_t Bp = 4 * (int64_t)pl->nrb;
+  pl->xh_bytes = align256(2 * Bp * a->H * 8);
+  pl->xz_bytes = (kind == kMonarch2) ? align256(6 * Bp * a->H * 8) : 0;
   return GS_OK;
 }
 
@@ -522,6 +561,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.G = pl.G;
   p.RB = pl.RB;
   p.nrb = pl.nrb;
+  p.Bp = 4 * pl.nrb;
   p.nwg = pl.nwg;
   p.rs = pl.rs;
   p.qin = to_quant(a->q_in);
