@@ -8,6 +8,8 @@
 // way torch's elementwise kernels round it).
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -114,6 +116,21 @@ __device__ __forceinline__ void st_tagged(uint64_t* p, float v, uint32_t tag) {
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Non-temporal form of st_tagged: the word is written into the writer's XCD L2
+// and not through to memory, which halves the time until an agent-scope load
+// from the same XCD sees it. Only valid when every reader of the word runs
+// on the writer's XCD (group_on_one_xcd); a reader elsewhere may not see the
+// word until it is evicted.
+__device__ __forceinline__ void st_tagged_xcd(uint64_t* p, float v, uint32_t tag) {
+  __builtin_nontemporal_store(((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v), p);
+}
+
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xfu;
+}
+
 __device__ __forceinline__ uint32_t tag_of(uint64_t w) { return (uint32_t)(w >> 32); }
 __device__ __forceinline__ float value_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
@@ -181,6 +198,101 @@ __device__ __forceinline__ void poll_to_lds(const Ctrl& c, const uint64_t* base,
 #pragma unroll
   for (int i = 0; i < MW; ++i)
     if ((valid >> i) & 1u) dst_lds[dst[i]] = value_of(v[i]);
+}
+
+// Calls f(integral_constant<int, I>) for I = 0 .. N-1 as straight-line code.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+// Polls R rows of tagged words into LDS: row r, word k = lane + 64 m
+// (m < MPR) at src[r * src_stride + k], stored to dst[r * dst_stride + k] for
+// k < klen. src and dst are wave-uniform; the loads address words up to
+// k = 64 MPR - 1 of every row, so the buffer behind src must extend that far
+// (words past klen are loaded but neither waited for nor stored). Only words
+// whose tag is still stale are loaded again.
+template <int R, int MPR>
+__device__ __forceinline__ void poll_rows(const Ctrl& c, const uint64_t* src, int src_stride, float* dst,
+                                          int dst_stride, int klen, uint32_t tag) {
+  constexpr int MW = R * MPR;
+  static_assert(MW <= 32, "poll mask is 32 bits");
+  const int lane = threadIdx.x & 63;
+  uint32_t valid = 0;
+#pragma unroll
+  for (int m = 0; m < MPR; ++m) {
+    const bool ok = lane + 64 * m < klen;
+#pragma unroll
+    for (int r = 0; r < R; ++r) valid |= (ok ? 1u : 0u) << (r * MPR + m);
+  }
+  uint64_t v[MW];
+  static_for<0, MW>([&](auto I) {
+    constexpr int r = I / MPR, m = I % MPR;
+    v[I] = ld_tagged(src + r * src_stride + lane + 64 * m);
+  });
+  uint32_t polls = 0;
+  while (true) {
+    uint32_t pending = 0;
+    static_for<0, MW>([&](auto I) { pending |= (tag_of(v[I]) != tag ? 1u : 0u) << I; });
+    pending &= valid;
+    if (pending == 0u) break;
+    if (++polls > kSpinLimit) {
+      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      break;
+    __builtin_amdgcn_s_sleep(1);
+    static_for<0, MW>([&](auto I) {
+      constexpr int r = I / MPR, m = I % MPR;
+      if ((pending >> I) & 1u) v[I] = ld_tagged(src + r * src_stride + lane + 64 * m);
+    });
+  }
+  static_for<0, MW>([&](auto I) {
+    constexpr int r = I / MPR, m = I % MPR;
+    if ((valid >> I) & 1u) dst[r * dst_stride + lane + 64 * m] = value_of(v[I]);
+  });
+}
+
+// Waits (bounded) until the LDS counter reaches target.
+__device__ __forceinline__ void wait_lds_count(const Ctrl& c, const int* cnt, int target) {
+  uint32_t polls = 0;
+  while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+    if (++polls > kSpinLimit) {
+      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Whether the n workgroups whose XCD words sit at words[0], words[stride], ...
+// all run on one XCD. Every workgroup stores its word (st_tagged of its
+// xcc_id with `tag`) at launch; one wave of each workgroup calls this and all
+// of them reach the same answer. n <= 64.
+__device__ __forceinline__ bool group_on_one_xcd(const Ctrl& c, const uint64_t* words, int stride, int n,
+                                                 uint32_t tag) {
+  const int lane = threadIdx.x & 63;
+  const bool mine = lane < n;
+  const uint64_t* src = words + (int64_t)(mine ? lane : 0) * stride;
+  uint64_t v = ld_tagged(src);
+  uint32_t polls = 0;
+  while (__ballot(mine && tag_of(v) != tag)) {
+    if (++polls > kSpinLimit) {
+      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      return false;
+    __builtin_amdgcn_s_sleep(1);
+    if (mine && tag_of(v) != tag) v = ld_tagged(src);
+  }
+  const uint32_t x = (uint32_t)v;
+  const uint32_t x0 = __builtin_amdgcn_readfirstlane(x);
+  return __ballot(mine && x != x0) == 0;
 }
 
 // Called once by every workgroup after its last exchange. The last one to

@@ -1,0 +1,154 @@
+// Building blocks shared by the MFMA scan kernels (dense, single- and
+// two-factor Monarch): the 4x4x1 MFMA chains over a wave's quad of hidden
+// units, the 16-way K-slice reduction, weight-slice loads and LDS operand
+// reads, the workgroup barrier used between exchange stages, and host-side
+// device queries.
+//
+// MFMA layout (v_mfma_f32_4x4x1_16b_f32, checked on the device): lane l
+// supplies A[block l/4][row l%4] and B[block l/4][col l%4]; D block b, row v,
+// col j is VGPR v of lane 4b + j. The kernels use the 16 blocks as 16 slices
+// of K: instruction m of a chain covers k = kmap(m, b) for block b.
+#pragma once
+
+#include <mutex>
+
+#include "gs_host.h"
+
+namespace gs {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// k index of MFMA instruction m in k-slice b: float4-contiguous per lane, so a
+// lane reads its A operand from an LDS row with KC/4 ds_read_b128.
+__device__ __forceinline__ int kmap(int m, int b) { return 64 * (m >> 2) + 4 * b + (m & 3); }
+
+// Sums the 16 K-slice partials of one gate. Input: the chain's D (lane 4b+j,
+// VGPR v = slice b's partial for row v, unit j). Output in lane l: the full
+// sum for row s = (l >> 2) & 3, unit l & 3.
+__device__ __forceinline__ float reduce16(f4 acc, int s) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    acc[c] += row_ror<8>(acc[c]);
+    acc[c] += row_ror<4>(acc[c]);
+  }
+  const float v = (s == 0) ? acc[0] : (s == 1) ? acc[1] : (s == 2) ? acc[2] : acc[3];
+  return sum_across_rows(v);
+}
+
+// Wh slice of a quad: w[((gate*nb + blk)*bs + o)*bs + k] for o = o0 + j,
+// k = kmap(m, kb4); zero where o >= bs or k >= bs.
+template <int KC>
+__device__ __forceinline__ void load_w(const float* w, int nb, int bs, int blk, int o0, int j, int kb4, bool ok_blk,
+                                       float (&wr)[3][KC]) {
+  const int o = o0 + j;
+  const bool ok = ok_blk && o < bs;
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    const float* row = w + ((int64_t)(g * nb + blk) * bs + o) * bs;
+#pragma unroll
+    for (int m = 0; m < KC; ++m) {
+      const int k = kmap(m, kb4);
+      wr[g][m] = (ok && k < bs) ? row[k] : 0.0f;
+    }
+  }
+}
+
+// A operand from an LDS staging row: a[m] = row[kmap(m, kb4)].
+template <int KC>
+__device__ __forceinline__ void lds_a(const float* row, int kb4, float (&a)[KC]) {
+#pragma unroll
+  for (int q = 0; q < KC / 4; ++q) {
+    const f4 v = *reinterpret_cast<const f4*>(row + 64 * q + 4 * kb4);
+    a[4 * q + 0] = v[0];
+    a[4 * q + 1] = v[1];
+    a[4 * q + 2] = v[2];
+    a[4 * q + 3] = v[3];
+  }
+}
+
+// Three MFMA chains (one per gate), two accumulators each for issue overlap.
+// SHARED_A: every gate multiplies a[0].
+template <int KC, bool SHARED_A>
+__device__ __forceinline__ void mfma3(const float (&a)[3][KC], const float (&wr)[3][KC], f4 (&acc)[3]) {
+  f4 acc0[3], acc1[3];
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    acc0[g] = f4{0.f, 0.f, 0.f, 0.f};
+    acc1[g] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int m = 0; m < KC; m += 2) {
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+      acc0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[SHARED_A ? 0 : g][m], wr[g][m], acc0[g], 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 3; ++g)
+      acc1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[SHARED_A ? 0 : g][m + 1], wr[g][m + 1], acc1[g], 0, 0, 0);
+  }
+#pragma unroll
+  for (int g = 0; g < 3; ++g) acc[g] = acc0[g] + acc1[g];
+}
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS
+// operations, then s_barrier. Unlike __syncthreads it does not wait for the
+// wave's global stores, whose acknowledgement (for coherent stores, a round
+// trip to the device coherence point) would otherwise sit on the critical path.
+// The asm memory clobber keeps the compiler from moving memory operations
+// across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ---- host side --------------------------------------------------------------------
+
+struct DevInfo {
+  int cus = 0;
+  int coop = 0;
+};
+
+inline int device_info(DevInfo* out) {
+  static std::mutex mu;
+  static DevInfo cache[64];
+  static bool have[64] = {};
+  int dev = 0;
+  GS_CHECK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return set_error(GS_ERR_HIP, "device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lk(mu);
+  if (!have[dev]) {
+    GS_CHECK_HIP(hipDeviceGetAttribute(&cache[dev].cus, hipDeviceAttributeMultiprocessorCount, dev));
+    GS_CHECK_HIP(hipDeviceGetAttribute(&cache[dev].coop, hipDeviceAttributeCooperativeLaunch, dev));
+    have[dev] = true;
+  }
+  *out = cache[dev];
+  return GS_OK;
+}
+
+inline int choose_kc(int klen) {
+  const int need = (klen + 15) / 16;
+  for (int kc : {4, 8, 16, 32, 64})
+    if (kc >= need) return kc;
+  return -1;
+}
+
+// Largest number of groups a cooperative launch can hold: workgroups of
+// `threads` threads and `lds` bytes, `per_group` workgroups per group.
+inline int coop_groups(const void* fn, int threads, size_t lds, int per_group, int want, int* out, const char* who) {
+  DevInfo di;
+  int rc = device_info(&di);
+  if (rc) return rc;
+  if (!di.coop) return set_error(GS_ERR_CAPACITY, "%s: device does not support cooperative launch", who);
+  int occ = 0;
+  GS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, threads, lds));
+  const int64_t resident = (int64_t)occ * di.cus;
+  if (resident < per_group)
+    return set_error(GS_ERR_CAPACITY,
+                     "%s: persistent grid needs %d co-resident workgroups of %d threads per batch group; "
+                     "the device holds %lld",
+                     who, per_group, threads, (long long)resident);
+  const int64_t gmax = resident / per_group;
+  *out = (int)(gmax < want ? gmax : want);
+  return GS_OK;
+}
+
+int64_t monarch2_workspace_bytes(const gs_args* a);
+int run_monarch2(const gs_args* a, hipStream_t stream, const char* who);
+
+}  // namespace gs

@@ -1,0 +1,414 @@
+// Dense and single-factor Monarch GRU scan forward on fp32 MFMA (gfx950).
+//
+// References (LarocheC/gru-triton src/gru_qat/triton_kernels/):
+//   dense    scan.py:76-210 (persistent kernel), scan.py:213-293 (launcher)
+//   Monarch  scan_monarch.py:130-291 (kernel), :320-406 (launcher), math :74-127
+//
+// Work split. Hidden units come in quads of 4; each compute wave owns one quad
+// (3 gates x 4 units = 12 rows of Wh, K = H for dense or the block for Monarch)
+// and keeps that weight slice in VGPRs for the whole scan. A *group* is the set
+// of workgroups that produce every unit a batch row's next step reads (dense:
+// all of H; Monarch: one block). Groups own RB row-blocks of 4 batch rows and
+// are interleaved in blockIdx (gid = blockIdx % ngroups), which places a group
+// on one XCD under round-robin workgroup dispatch.
+//
+// Per step and row-block a compute wave reads its A operand q_in(h)[4 rows][K]
+// and the gate inputs from LDS, runs 3 chains of v_mfma_f32_4x4x1_16b_f32
+// (gs_mfma.h), sums the 16 K-slice partials, and the 16 lanes of row 0 run the
+// gate epilogue, store out[t] and pass q_in(h_t) on.
+//
+// Local mode (a group fits in one workgroup): compute waves write q_in(h_t)
+// straight into the LDS staging buffer of the next step.
+// Remote mode (a group spans workgroups): compute waves publish q_in(h_t) as
+// tagged 64-bit words (gs_device.h) and never load from global memory inside
+// the loop. Four poller waves per workgroup, one per batch row of the
+// row-block, poll the words the next iteration needs and stage them, with the
+// next gate inputs, into LDS while the compute waves work. The two roles meet
+// at one LDS-only barrier per iteration, so no wave ever waits for its own
+// stores to be acknowledged. During the first exchange the pollers check that
+// their group runs on one XCD; if so, later steps publish with non-temporal
+// stores that stay in that XCD's L2, which the group's agent-scope loads see
+// sooner than stores written through to memory.
+#include "gs_mfma.h"
+
+namespace gs {
+namespace {
+
+enum : int { kDense = 0, kMonarch1 = 1 };
+constexpr int kPollers = 4;  // remote mode: poller waves per workgroup, one per row
+
+struct DParams {
+  const float* gi;
+  const float* h0;
+  const float* w;
+  const float* bh;
+  float* out;
+  uint64_t* xh;  // remote mode: [2][Bp][H] tagged q_in(h_t)
+  uint64_t* xw;  // remote mode: [nwg] tagged XCD ids
+  Ctrl ctrl;
+  int64_t sg_t, sg_b, sh0_b, so_t, so_b;
+  int T, B, H;
+  int nb, bs, qpb;  // dense: nb = 1, bs = H
+  int ngroups, G, RB, nrb, Bp, nwg, P;
+  int nwc;  // compute waves per workgroup
+  int rs;   // LDS staging row stride (floats)
+  Quant qin, qout;
+  int qin_after_first;
+};
+
+template <int KIND, int KC, int NT, bool REMOTE>
+__global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwc = p.nwc;
+  const bool poller = REMOTE && wave >= nwc;
+  const int j = lane & 3, kb4 = lane >> 2, s = (lane >> 2) & 3;
+  const bool lead = lane < 16;
+
+  const int gid = blockIdx.x % p.ngroups;
+  const int pw = blockIdx.x / p.ngroups;
+  const int set = (KIND == kMonarch1) ? gid % p.G : gid;
+  const int blk_g = (KIND == kMonarch1) ? gid / p.G : 0;  // the group's block (dense: 0)
+  const int klo = blk_g * p.bs;                           // K range [klo, klo + bs)
+  const int quad = pw * nwc + wave;                       // within the group's K range
+  const int o0 = 4 * quad;
+  const bool quad_ok = !poller && o0 < p.bs;
+  const int U = 4 * nwc;               // units per workgroup
+  const int ulo = klo + 4 * pw * nwc;  // first unit of this workgroup
+  const int unit = ulo + 4 * wave + j;
+  const bool unit_ok = quad_ok && (o0 + j) < p.bs;
+
+  const int rb_begin = set * p.RB;
+  const int rb_end = min(rb_begin + p.RB, p.nrb);
+  const int nrbm = rb_end - rb_begin;
+
+  float* hst = lds;                  // [2][4][rs]   staged q_in(h) of the K range
+  float* hk = hst + 8 * p.rs;        // [RB][4][U]   raw h of this workgroup's units
+  float* gst = hk + p.RB * 4 * U;    // [2][4][3][U] staged gi (remote mode)
+  int* flags = reinterpret_cast<int*>(gst + 24 * U);  // remote mode: [0] compute-wave iterations
+                                                      // published, [1] group on one XCD
+  const int lds_floats = 8 * p.rs + p.RB * 4 * U + (REMOTE ? 24 * U + 4 : 0);
+  for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
+
+  const uint32_t base = REMOTE ? __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+  if (REMOTE && threadIdx.x == 0) st_tagged(p.xw + blockIdx.x, __uint_as_float(xcc_id()), base + 1u);
+  const int niter = p.T * nrbm;
+
+  // Prologue (all waves): step-0 inputs of the first row-block, raw h0 of all.
+  lds_barrier();
+  {
+    const int rb = rb_begin;
+    for (int w = threadIdx.x; w < 4 * p.bs; w += blockDim.x) {
+      const int r = w / p.bs, k = w - r * p.bs;
+      const int row = 4 * rb + r;
+      float v = 0.0f;
+      if (row < p.B) {
+        v = p.h0[(int64_t)row * p.sh0_b + klo + k];
+        if (p.qin.on) v = fake_quant(v, p.qin);
+      }
+      hst[r * p.rs + k] = v;
+    }
+    for (int w = threadIdx.x; w < nrbm * 4 * U; w += blockDim.x) {
+      const int rbl = w / (4 * U), rem = w - rbl * 4 * U, r = rem / U, u = rem - r * U;
+      const int row = 4 * (rb_begin + rbl) + r;
+      const bool ok = row < p.B && (ulo + u - klo) < p.bs;
+      hk[w] = ok ? p.h0[(int64_t)row * p.sh0_b + ulo + u] : 0.0f;
+    }
+    if (REMOTE) {
+      for (int w = threadIdx.x; w < 12 * U; w += blockDim.x) {
+        const int r = w / (3 * U), rem = w - r * 3 * U, g = rem / U, u = rem - g * U;
+        const int row = 4 * rb + r;
+        const bool ok = row < p.B && (ulo + u - klo) < p.bs;
+        gst[w] = ok ? p.gi[(int64_t)row * p.sg_b + g * p.H + ulo + u] : 0.0f;
+      }
+    }
+  }
+  lds_barrier();
+
+  // The compute waves and the poller waves run separate loops with the same
+  // number of iterations and one barrier each, so each role's registers are
+  // allocated only for its own live values.
+  if (!poller) {
+    float wr[3][KC];
+    load_w<KC>(p.w, p.nb, p.bs, blk_g, o0, j, kb4, quad_ok, wr);
+    float bias[3];
+#pragma unroll
+    for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? p.bh[g * p.H + unit] : 0.0f;
+    for (int it = 0; it < niter; ++it) {
+      const int t = it / nrbm;
+      const int rbl = it - t * nrbm;
+      const int rb = rb_begin + rbl;
+      const int buf = it & 1;
+      const int row = 4 * rb + s;
+      const bool mine = lead && row < p.B && unit_ok;
+      float gir = 0.f, giz = 0.f, gin = 0.f;
+      if (REMOTE) {
+        const float* gs_ = gst + buf * 12 * U + s * 3 * U + 4 * wave + j;
+        gir = gs_[0];
+        giz = gs_[U];
+        gin = gs_[2 * U];
+      } else if (mine) {
+        const float* g = p.gi + (int64_t)t * p.sg_t + (int64_t)row * p.sg_b + unit;
+        gir = g[0];
+        giz = g[p.H];
+        gin = g[2 * p.H];
+      }
+      float* hkp = hk + (rbl * 4 + s) * U + 4 * wave + j;
+      const float hprev = *hkp;
+      float a[3][KC];
+      lds_a<KC>(hst + buf * 4 * p.rs + j * p.rs, kb4, a[0]);
+      f4 acc[3];
+      mfma3<KC, true>(a, wr, acc);
+      float gh[3];
+#pragma unroll
+      for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
+      float hn = gru_update(gir, giz, gin, gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
+      if (p.qout.on) hn = fake_quant(hn, p.qout);
+      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
+      const bool xcd_local = REMOTE && t >= 1 && __builtin_amdgcn_readfirstlane(flags[1]) != 0;
+      if (lead && unit_ok) {
+        *hkp = hn;
+        if (t + 1 < p.T) {
+          const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
+          if (REMOTE) {
+            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + row) * p.H + unit;
+            if (xcd_local)
+              st_tagged_xcd(dst, hq, base + (uint32_t)t + 1u);
+            else
+              st_tagged(dst, hq, base + (uint32_t)t + 1u);
+          } else {
+            hst[(buf ^ 1) * 4 * p.rs + s * p.rs + (unit - klo)] = hq;  // local mode: RB == 1
+          }
+        }
+      }
+      if (REMOTE && lane == 0) __hip_atomic_fetch_add(&flags[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      lds_barrier();
+    }
+  } else if (REMOTE) {
+    // Poller wave pr stages row pr of iteration it + 1's inputs while the
+    // compute waves run iteration it. The gate-input loads are issued first so
+    // that their latency overlaps the polls, which start once this
+    // workgroup's compute waves have published iteration it: the other
+    // workgroups publish at about the same time, and polling earlier only
+    // loads the memory system that carries their stores.
+    const int pr = wave - nwc;
+    constexpr int NGI = NT / 64 > kPollers ? (3 * 4 * (NT / 64 - kPollers) + 63) / 64 : 1;  // gi words per lane
+    for (int it = 0; it < niter; ++it) {
+      const int nx = it + 1;
+      if (nx < niter) {
+        const int t2 = nx / nrbm;
+        const int rb2 = rb_begin + (nx - t2 * nrbm);
+        const int row = 4 * rb2 + pr;
+        float gv[NGI];
+#pragma unroll
+        for (int i = 0; i < NGI; ++i) {
+          const int w = lane + 64 * i;
+          const int g = w / U, u = w - g * U;
+          const bool ok = w < 3 * U && row < p.B && (ulo + u - klo) < p.bs;
+          gv[i] = ok ? p.gi[(int64_t)t2 * p.sg_t + (int64_t)row * p.sg_b + g * p.H + ulo + u] : 0.0f;
+        }
+        float* hs = hst + (nx & 1) * 4 * p.rs + pr * p.rs;
+        if (t2 == 0) {
+          for (int k = lane; k < p.bs; k += 64) {
+            float v = 0.0f;
+            if (row < p.B) {
+              v = p.h0[(int64_t)row * p.sh0_b + klo + k];
+              if (p.qin.on) v = fake_quant(v, p.qin);
+            }
+            hs[k] = v;
+          }
+        } else {
+          if (pr == 0 && nx == nrbm)  // first exchange of the launch
+            flags[1] = (p.P <= 64 && group_on_one_xcd(p.ctrl, p.xw + gid, p.ngroups, p.P, base + 1u)) ? 1 : 0;
+          wait_lds_count(p.ctrl, &flags[0], nwc * (it + 1));
+          // bs words of the row; lane takes k = lane + 64 m, m < KC/4 (bs <= 16 KC)
+          const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * p.H + klo;
+          poll_rows<1, KC / 4>(p.ctrl, hb, 0, hs, 0, p.bs, base + (uint32_t)t2);
+        }
+        float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
+#pragma unroll
+        for (int i = 0; i < NGI; ++i) {
+          const int w = lane + 64 * i;
+          if (w < 3 * U) gs_[w] = gv[i];
+        }
+      }
+      lds_barrier();
+    }
+  }
+  if (REMOTE) leave_grid(p.ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T);
+}
+
+typedef void (*DFn)(DParams);
+
+template <int KIND, bool REMOTE>
+DFn pick_kernel(int KC, int* nt) {
+  // Remote instances add 4 poller waves to 4 compute waves (KC >= 16) or up
+  // to 12 (KC <= 8); local instances hold up to 16 compute waves.
+  switch (KC) {
+    case 4: *nt = 1024; return scan_kernel<KIND, 4, 1024, REMOTE>;
+    case 8: *nt = 1024; return scan_kernel<KIND, 8, 1024, REMOTE>;
+    case 16: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 16, REMOTE ? 512 : 256, REMOTE>;
+    case 32: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 32, REMOTE ? 512 : 256, REMOTE>;
+    case 64: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 64, REMOTE ? 512 : 256, REMOTE>;
+    default: return nullptr;
+  }
+}
+
+DFn pick(int kind, bool remote, int KC, int* nt) {
+  if (kind == kDense) return remote ? pick_kernel<kDense, true>(KC, nt) : pick_kernel<kDense, false>(KC, nt);
+  return remote ? pick_kernel<kMonarch1, true>(KC, nt) : pick_kernel<kMonarch1, false>(KC, nt);
+}
+
+struct DPlan {
+  int KC, nt, nwc, P, nrb, Bp, rs, nb, bs, qpb;
+  bool remote;
+  int64_t xh_bytes, xw_bytes;
+};
+
+int plan_dense(int kind, const gs_args* a, DPlan* pl, const char* who) {
+  if (kind == kDense) {
+    pl->nb = 1;
+    pl->bs = (int)a->H;
+  } else {
+    if (a->nblocks < 1 || a->blksz < 1 || a->nblocks * a->blksz != a->H)
+      return set_error(GS_ERR_INVALID, "%s: Wh_struct block dims must tile H: nblocks=%lld, blksz=%lld, H=%lld", who,
+                       (long long)a->nblocks, (long long)a->blksz, (long long)a->H);
+    pl->nb = (int)a->nblocks;
+    pl->bs = (int)a->blksz;
+  }
+  pl->KC = choose_kc(pl->bs);
+  if (pl->KC < 0)
+    return set_error(GS_ERR_INVALID, "%s: reduction length %d exceeds the supported maximum of 1024", who, pl->bs);
+  pl->qpb = (pl->bs + 3) / 4;
+  pl->remote = pl->qpb > 16;
+  if (!pl->remote) {
+    pl->nwc = pl->qpb;
+    pl->P = 1;
+  } else {
+    const int nwmax = pl->KC >= 16 ? 4 : 12;
+    int nwc = pl->qpb < nwmax ? pl->qpb : nwmax;
+    if (kind == kMonarch1)
+      while (pl->qpb % nwc != 0) --nwc;
+    pl->nwc = nwc;
+    pl->P = (pl->qpb + nwc - 1) / nwc;
+  }
+  pick(kind, pl->remote, pl->KC, &pl->nt);
+  pl->nrb = (int)((a->B + 3) / 4);
+  pl->Bp = 4 * pl->nrb;
+  pl->rs = 16 * pl->KC + 4;
+  // The pollers load 16 KC words per row from the row's first unit; the pad
+  // keeps the reads past the last row inside the workspace.
+  pl->xh_bytes = pl->remote ? align256(2 * (int64_t)pl->Bp * a->H * 8 + 16 * pl->KC * 8) : 0;
+  // one XCD-id word per workgroup of the largest grid the launch can use
+  pl->xw_bytes = pl->remote ? align256((int64_t)pl->nrb * pl->nb * pl->P * 8) : 0;
+  return GS_OK;
+}
+
+int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
+  DPlan pl;
+  int rc = plan_dense(kind, a, &pl, who);
+  if (rc) return rc;
+  rc = check_workspace(a, kCtrlBytes + pl.xh_bytes + pl.xw_bytes, who);
+  if (rc) return rc;
+  DFn fn = pick(kind, pl.remote, pl.KC, &pl.nt);
+  const int threads = 64 * (pl.nwc + (pl.remote ? kPollers : 0));
+  const int per_set = pl.P * (kind == kMonarch1 ? pl.nb : 1);
+
+  int G = pl.nrb, RB = 1;
+  size_t lds = 0;
+  // Local mode keeps RB = 1 (a workgroup's LDS staging holds one row-block);
+  // remote mode shrinks the group count until the cooperative grid fits.
+  for (int pass = 0; pass < 2; ++pass) {
+    RB = (pl.nrb + G - 1) / G;
+    G = (pl.nrb + RB - 1) / RB;
+    const int U = 4 * pl.nwc;
+    lds = sizeof(float) * (size_t)(8 * pl.rs + RB * 4 * U + (pl.remote ? 24 * U + 4 : 0));
+    if (lds > 65536)
+      GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    if (!pl.remote) break;
+    int gfit = 0;
+    rc = coop_groups((const void*)fn, threads, lds, per_set, pl.nrb, &gfit, who);
+    if (rc) return rc;
+    if (gfit >= G) break;
+    G = gfit;
+  }
+
+  DParams p;
+  p.gi = a->gi;
+  p.h0 = a->h0;
+  p.w = a->w;
+  p.bh = a->bh;
+  p.out = a->out;
+  char* ws = static_cast<char*>(a->workspace);
+  p.ctrl = ctrl_of(ws);
+  p.xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
+  p.xw = reinterpret_cast<uint64_t*>(ws + kCtrlBytes + pl.xh_bytes);
+  p.sg_t = a->sg_t;
+  p.sg_b = a->sg_b;
+  p.sh0_b = a->sh0_b;
+  p.so_t = a->so_t;
+  p.so_b = a->so_b;
+  p.T = (int)a->T;
+  p.B = (int)a->B;
+  p.H = (int)a->H;
+  p.nb = pl.nb;
+  p.bs = pl.bs;
+  p.qpb = pl.qpb;
+  p.G = G;
+  p.RB = RB;
+  p.nrb = pl.nrb;
+  p.Bp = pl.Bp;
+  p.ngroups = G * (kind == kMonarch1 ? pl.nb : 1);
+  p.nwg = p.ngroups * pl.P;
+  p.P = pl.P;
+  p.nwc = pl.nwc;
+  p.rs = pl.rs;
+  p.qin = to_quant(a->q_in);
+  p.qout = to_quant(a->q_out);
+  p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
+  if (pl.remote) {
+    void* kargs[] = {&p};
+    GS_CHECK_HIP(
+        hipLaunchCooperativeKernel((const void*)fn, dim3(p.nwg), dim3(threads), kargs, (unsigned)lds, stream));
+  } else {
+    hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), lds, stream, p);
+    GS_CHECK_HIP(hipGetLastError());
+  }
+  return GS_OK;
+}
+
+int64_t ws_bytes(int kind, const gs_args* a) {
+  DPlan pl;
+  const int rc = plan_dense(kind, a, &pl, "gs_workspace_bytes");
+  if (rc) return rc;
+  return kCtrlBytes + pl.xh_bytes + pl.xw_bytes;
+}
+
+}  // namespace
+
+int64_t dense_workspace_bytes(const gs_args* a) { return ws_bytes(kDense, a); }
+
+int64_t monarch_workspace_bytes(const gs_args* a) {
+  return a->w2 ? monarch2_workspace_bytes(a) : ws_bytes(kMonarch1, a);
+}
+
+}  // namespace gs
+
+extern "C" int gs_dense_fwd(const gs_args* a, hipStream_t stream) {
+  gs::clear_error();
+  const char* who = "gs_dense_fwd";
+  int rc = gs::validate_common(a, who);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
+  return gs::run(gs::kDense, a, stream, who);
+}
+
+extern "C" int gs_monarch_fwd(const gs_args* a, hipStream_t stream) {
+  gs::clear_error();
+  const char* who = "gs_monarch_fwd";
+  int rc = gs::validate_common(a, who);
+  if (rc) return rc;
+  if (a->w2) return gs::run_monarch2(a, stream, who);
+  return gs::run(gs::kMonarch1, a, stream, who);
+}

@@ -1,0 +1,289 @@
+// Two-factor Monarch GRU scan forward on fp32 MFMA (gfx950).
+//
+// Hidden map (no reference counterpart; the single-factor form is
+// LarocheC/gru-triton src/gru_qat/triton_kernels/scan_monarch.py:74-127):
+//   gh_g = P^T L_g P R_g q_in(h) + bh_g,   (P z)[c * nb + a] = z[a * bs + c],
+// with R_g = w[g], L_g = w2[g] block-diagonal ([nb, bs, bs] as (out, in)).
+//
+// monarch2_split_kernel (any nb, bs). A group covers all H units for its
+// row-blocks. Phase 1: each wave's quad of R rows gives z_g = R_g q_in(h) for 4
+// units, published as tagged words. Phase 2: each workgroup stages P z_g for
+// its block (polling the z words), multiplies by L_g and lands the result on
+// y = P^T v. Two exchanges per step.
+#include "gs_mfma.h"
+
+namespace gs {
+namespace {
+
+struct M2Params {
+  const float* gi;
+  const float* h0;
+  const float* w;
+  const float* w2;
+  const float* bh;
+  float* out;
+  uint64_t* xh;  // [2][Bp][H] tagged q_in(h_t)
+  uint64_t* xz;  // [2][3][Bp][H] tagged first-factor output
+  Ctrl ctrl;
+  int64_t sg_t, sg_b, sh0_b, so_t, so_b;
+  int T, B, H;
+  int nb, bs, qpb;
+  int nrb, Bp, RB, nwg, ngroups;
+  int rs;  // LDS row stride (floats)
+  Quant qin, qout;
+  int qin_after_first;
+};
+
+// Polls `words` tagged words of one exchange slice into LDS, MW per thread and pass.
+// Word w maps to (src offset, LDS offset) through addr(w, &src, &dst).
+template <int MW, typename Map>
+__device__ __forceinline__ void stage_words(const Ctrl& c, const uint64_t* base, int words, uint32_t tag, float* lds,
+                                            Map map) {
+  const int tid = threadIdx.x, nth = blockDim.x;
+  for (int c0 = 0; c0 < words; c0 += MW * nth) {
+    int src[MW], dst[MW];
+    uint32_t valid = 0;
+#pragma unroll
+    for (int i = 0; i < MW; ++i) {
+      const int w = c0 + tid + i * nth;
+      const bool ok = w < words;
+      map(ok ? w : 0, src[i], dst[i]);
+      valid |= (ok ? 1u : 0u) << i;
+    }
+    poll_to_lds<MW>(c, base, src, dst, valid, tag, lds);
+  }
+}
+
+template <int KC, int NT>
+__global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
+  extern __shared__ float lds[];
+  constexpr int MWH = (4 * 16 * KC + NT - 1) / NT;
+  constexpr int MWZ = (12 * 16 * KC + NT - 1) / NT;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nw = blockDim.x >> 6;
+  const int j = lane & 3, kb4 = lane >> 2, s = (lane >> 2) & 3;
+  const bool lead = lane < 16;
+
+  const int gid = blockIdx.x % p.ngroups;
+  const int pw = blockIdx.x / p.ngroups;
+  const int quad = pw * nw + wave;
+  const int blk = quad / p.qpb;
+  const int o0 = 4 * (quad - blk * p.qpb);
+  const bool blk_ok = blk < p.nb && o0 < p.bs;
+  const int wg_blk = (pw * nw) / p.qpb;  // waves per workgroup divide quads per block
+  const int klo = wg_blk * p.bs;
+
+  float* hst = lds;             // [2][4][rs]
+  float* zst = lds + 8 * p.rs;  // [2][12][rs]
+  for (int i = threadIdx.x; i < 32 * p.rs; i += blockDim.x) lds[i] = 0.0f;
+  lds_barrier();
+
+  float wr[3][KC], wl[3][KC];
+  load_w<KC>(p.w, p.nb, p.bs, blk, o0, j, kb4, blk_ok, wr);
+  load_w<KC>(p.w2, p.nb, p.bs, blk, o0, j, kb4, blk_ok, wl);
+
+  const int vi = blk * p.bs + o0 + j;
+  const bool unit_ok = blk_ok && (o0 + j) < p.bs;
+  const int unit = (vi % p.nb) * p.bs + vi / p.nb;
+  float bias[3];
+#pragma unroll
+  for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? p.bh[g * p.H + unit] : 0.0f;
+
+  const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int rb_begin = gid * p.RB;
+  const int rb_end = min(rb_begin + p.RB, p.nrb);
+  int hbuf = 0, zbuf = 0;
+  const int bs = p.bs, H = p.H, nb = p.nb, rs = p.rs, Bp = p.Bp;
+
+  for (int t = 0; t < p.T; ++t) {
+    const uint32_t tag = base + (uint32_t)t + 1u;
+    for (int rb = rb_begin; rb < rb_end; ++rb) {
+      const int row = 4 * rb + s;
+      const bool mine = lead && row < p.B && unit_ok;
+      const bool pub = lead && unit_ok;
+      float gir = 0.f, giz = 0.f, gin = 0.f, hprev = 0.f;
+      if (mine) {
+        const float* g = p.gi + (int64_t)t * p.sg_t + (int64_t)row * p.sg_b + unit;
+        gir = g[0];
+        giz = g[H];
+        gin = g[2 * H];
+        hprev = (t == 0) ? p.h0[(int64_t)row * p.sh0_b + unit]
+                         : p.out[(int64_t)(t - 1) * p.so_t + (int64_t)row * p.so_b + unit];
+      }
+      // Phase 1 input: q_in(h_{t-1}) rows 4rb.., cols of this workgroup's block.
+      float* hs = hst + hbuf * 4 * rs;
+      hbuf ^= 1;
+      if (t == 0) {
+        for (int w = threadIdx.x; w < 4 * bs; w += blockDim.x) {
+          const int r = w / bs, k = w - r * bs;
+          const int row_r = 4 * rb + r;
+          float v = 0.0f;
+          if (row_r < p.B) {
+            v = p.h0[(int64_t)row_r * p.sh0_b + klo + k];
+            if (p.qin.on) v = fake_quant(v, p.qin);
+          }
+          hs[r * rs + k] = v;
+        }
+      } else {
+        const uint64_t* hb = p.xh + ((int64_t)((t - 1) & 1) * Bp + 4 * rb) * H;
+        stage_words<MWH>(p.ctrl, hb, 4 * bs, tag - 1u, hs, [&](int w, int& src, int& dst) {
+          const int r = w / bs, k = w - r * bs;
+          src = r * H + klo + k;
+          dst = r * rs + k;
+        });
+      }
+      lds_barrier();
+      float a[3][KC];
+      lds_a<KC>(hs + j * rs, kb4, a[0]);
+      f4 acc[3];
+      mfma3<KC, true>(a, wr, acc);
+      float gh[3];
+#pragma unroll
+      for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
+      if (pub) {
+#pragma unroll
+        for (int g = 0; g < 3; ++g) st_tagged(p.xz + ((int64_t)((t & 1) * 3 + g) * Bp + row) * H + vi, gh[g], tag);
+      }
+      // Phase 2 input: (P z_g)[wg_blk*bs + k], 3 gates x 4 rows.
+      float* zs = zst + zbuf * 12 * rs;
+      zbuf ^= 1;
+      const uint64_t* zb = p.xz + (int64_t)(t & 1) * 3 * Bp * H + (int64_t)4 * rb * H;
+      stage_words<MWZ>(p.ctrl, zb, 12 * bs, tag, zs, [&](int w, int& src, int& dst) {
+        const int gr = w / bs, k = w - gr * bs;
+        const int idx = wg_blk * bs + k;
+        const int zpos = (idx % nb) * bs + idx / nb;
+        src = ((gr >> 2) * Bp + (gr & 3)) * H + zpos;
+        dst = gr * rs + k;
+      });
+      lds_barrier();
+#pragma unroll
+      for (int g = 0; g < 3; ++g) lds_a<KC>(zs + (g * 4 + j) * rs, kb4, a[g]);
+      mfma3<KC, false>(a, wl, acc);
+#pragma unroll
+      for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
+
+      float hn = gru_update(gir, giz, gin, gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
+      if (p.qout.on) hn = fake_quant(hn, p.qout);
+      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
+      if (pub && t + 1 < p.T) {
+        const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
+        st_tagged(p.xh + ((int64_t)(t & 1) * Bp + row) * H + unit, hq, tag);
+      }
+    }
+  }
+  leave_grid(p.ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T);
+}
+
+typedef void (*M2Fn)(M2Params);
+
+M2Fn pick_split(int KC, int* nt) {
+  switch (KC) {
+    case 4: *nt = 1024; return monarch2_split_kernel<4, 1024>;
+    case 8: *nt = 256; return monarch2_split_kernel<8, 256>;
+    case 16: *nt = 256; return monarch2_split_kernel<16, 256>;
+    case 32: *nt = 256; return monarch2_split_kernel<32, 256>;
+    case 64: *nt = 256; return monarch2_split_kernel<64, 256>;
+    default: return nullptr;
+  }
+}
+
+struct M2Plan {
+  int KC, nt, nw, P, nrb, Bp, rs;
+  int64_t xh_bytes, xz_bytes;
+  size_t lds;
+};
+
+int plan_m2(const gs_args* a, M2Plan* pl, const char* who) {
+  if (a->nblocks < 1 || a->blksz < 1 || a->nblocks * a->blksz != a->H)
+    return set_error(GS_ERR_INVALID, "%s: Wh_struct block dims must tile H: nblocks=%lld, blksz=%lld, H=%lld", who,
+                     (long long)a->nblocks, (long long)a->blksz, (long long)a->H);
+  const int bs = (int)a->blksz, nb = (int)a->nblocks;
+  pl->KC = choose_kc(bs);
+  if (pl->KC < 0) return set_error(GS_ERR_INVALID, "%s: block size %d exceeds the supported maximum of 1024", who, bs);
+  if (!pick_split(pl->KC, &pl->nt)) return set_error(GS_ERR_INVALID, "%s: no kernel for KC=%d", who, pl->KC);
+  const int qpb = (bs + 3) / 4;
+  int nw = qpb < pl->nt / 64 ? qpb : pl->nt / 64;
+  while (qpb % nw != 0) --nw;
+  pl->nw = nw;
+  pl->P = nb * qpb / nw;
+  pl->nrb = (int)((a->B + 3) / 4);
+  pl->Bp = 4 * pl->nrb;
+  pl->rs = 16 * pl->KC + 4;
+  pl->lds = (size_t)32 * pl->rs * sizeof(float);
+  pl->xh_bytes = align256(2 * (int64_t)pl->Bp * a->H * 8);
+  pl->xz_bytes = align256(6 * (int64_t)pl->Bp * a->H * 8);
+  return GS_OK;
+}
+
+}  // namespace
+
+int64_t monarch2_workspace_bytes(const gs_args* a) {
+  M2Plan pl;
+  const int rc = plan_m2(a, &pl, "gs_workspace_bytes");
+  if (rc) return rc;
+  return kCtrlBytes + pl.xh_bytes + pl.xz_bytes;
+}
+
+int run_monarch2(const gs_args* a, hipStream_t stream, const char* who) {
+  M2Plan pl;
+  int rc = plan_m2(a, &pl, who);
+  if (rc) return rc;
+  rc = check_workspace(a, kCtrlBytes + pl.xh_bytes + pl.xz_bytes, who);
+  if (rc) return rc;
+  M2Fn fn = pick_split(pl.KC, &pl.nt);
+  const int threads = pl.nw * 64;
+  if (pl.lds > 65536)
+    GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.lds));
+  int G = pl.nrb;
+  const bool coop = pl.P > 1;
+  if (coop) {
+    rc = coop_groups((const void*)fn, threads, pl.lds, pl.P, pl.nrb, &G, who);
+    if (rc) return rc;
+  }
+  const int RB = (pl.nrb + G - 1) / G;
+  G = (pl.nrb + RB - 1) / RB;
+
+  M2Params p;
+  p.gi = a->gi;
+  p.h0 = a->h0;
+  p.w = a->w;
+  p.w2 = a->w2;
+  p.bh = a->bh;
+  p.out = a->out;
+  char* ws = static_cast<char*>(a->workspace);
+  p.ctrl = ctrl_of(ws);
+  p.xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
+  p.xz = reinterpret_cast<uint64_t*>(ws + kCtrlBytes + pl.xh_bytes);
+  p.sg_t = a->sg_t;
+  p.sg_b = a->sg_b;
+  p.sh0_b = a->sh0_b;
+  p.so_t = a->so_t;
+  p.so_b = a->so_b;
+  p.T = (int)a->T;
+  p.B = (int)a->B;
+  p.H = (int)a->H;
+  p.nb = (int)a->nblocks;
+  p.bs = (int)a->blksz;
+  p.qpb = (p.bs + 3) / 4;
+  p.nrb = pl.nrb;
+  p.Bp = pl.Bp;
+  p.RB = RB;
+  p.nwg = G * pl.P;
+  p.ngroups = G;
+  p.rs = pl.rs;
+  p.qin = to_quant(a->q_in);
+  p.qout = to_quant(a->q_out);
+  p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
+  if (coop) {
+    void* kargs[] = {&p};
+    GS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)fn, dim3(p.nwg), dim3(threads), kargs, (unsigned)pl.lds,
+                                            stream));
+  } else {
+    hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), pl.lds, stream, p);
+    GS_CHECK_HIP(hipGetLastError());
+  }
+  return GS_OK;
+}
+
+}  // namespace gs

@@ -98,19 +98,27 @@ def test_butterfly_shape_rejected():
 
 def test_workspace_sizes():
     """Control words plus double-buffered tagged exchange words (8 bytes per
-    unit and row; two-factor Monarch adds 3 gates of first-factor words)."""
+    unit and row) when a batch row's step spans workgroups; two-factor Monarch
+    adds 3 gates of first-factor words. A Monarch block of <= 64 units is
+    produced by one workgroup, which exchanges through LDS only."""
     lib = _lib.load()
     a = _args(T=64, B=32, H=512)
     n = lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a))
     xh = 2 * 32 * 512 * 8
-    assert n == 256 + xh
+    # pollers read 16 * KC words per row (KC = 32 for a 512-long reduction),
+    # so the exchange area is padded by as many words past its last row; one
+    # XCD-id word follows per workgroup (8 row-blocks x 32 workgroups)
+    assert n == 256 + xh + 16 * 32 * 8 + 8 * 32 * 8
     q = (1.0 / 127, -127, 127)
     for kw in ({"q_in": q, "q_out": q}, {"q_in": q}):
         assert lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(_args(T=64, B=32, H=512, **kw))) == n
     a_m1 = _args(T=64, B=32, H=512, nblocks=8, blksz=64)
-    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m1)) == n
+    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m1)) == 256
+    a_m1 = _args(T=64, B=32, H=512, nblocks=4, blksz=128)
+    # 4 blocks x 4 workgroups of 8 compute waves per row-block
+    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m1)) == 256 + xh + 16 * 8 * 8 + 8 * 16 * 8
     a_m2 = _args(T=64, B=32, H=512, nblocks=8, blksz=64, w2=FAKE)
-    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m2)) == n + 3 * xh
+    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m2)) == 256 + 4 * xh
     # diagonal and butterfly kernels use no workspace beyond the control words
     assert lib.gs_workspace_bytes(_lib.KIND_DIAGONAL, ctypes.byref(a)) == 256
     assert lib.gs_workspace_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) == 256
