@@ -5,6 +5,17 @@
 //   gh_g = P^T L_g P R_g q_in(h) + bh_g,   (P z)[c * nb + a] = z[a * bs + c],
 // with R_g = w[g], L_g = w2[g] block-diagonal ([nb, bs, bs] as (out, in)).
 //
+// monarch2_fused_kernel (bs <= 64, nb | bs, bs / nb a multiple of 4). One
+// workgroup per block b of L and set of row-blocks. Block b of y = P z reads
+// z[a * bs + c] for every first-factor block a and c in [b cpb, (b + 1) cpb),
+// cpb = bs / nb, so the workgroup computes exactly those bs entries of z_g
+// itself (phase 1, quads of 4 consecutive c under one a), stages them in LDS
+// in y order, multiplies by L_g[b] (phase 2) and runs the gate epilogue for
+// the units y = P^T v places its outputs on. One exchange per step, of
+// q_in(h_t), exactly as in the dense kernel: compute waves publish tagged
+// words and four poller waves, one per batch row, stage the next step's
+// q_in(h) and gate inputs into LDS.
+//
 // monarch2_split_kernel (any nb, bs). A group covers all H units for its
 // row-blocks. Phase 1: each wave's quad of R rows gives z_g = R_g q_in(h) for 4
 // units, published as tagged words. Phase 2: each workgroup stages P z_g for
@@ -14,6 +25,231 @@
 
 namespace gs {
 namespace {
+
+constexpr int kPollers = 4;  // fused kernel: poller waves per workgroup, one per row
+
+struct M2FParams {
+  const float* gi;
+  const float* h0;
+  const float* w;
+  const float* w2;
+  const float* bh;
+  float* out;
+  uint64_t* xh;  // [2][Bp][H] tagged q_in(h_t)
+  uint64_t* xw;  // [nwg] tagged XCD ids
+  Ctrl ctrl;
+  int64_t sg_t, sg_b, sh0_b, so_t, so_b;
+  int T, B, H;
+  int nb, bs, cpb, nq;  // nq = bs / 4 quads per phase
+  int ngroups, RB, nrb, Bp, nwg;
+  int nwc;       // compute waves per workgroup
+  int rsh, rsz;  // LDS row strides: staged q_in(h) rows, staged z rows
+  Quant qin, qout;
+  int qin_after_first;
+};
+
+// Unit of H that output i of L-block b lands on: y = P^T v, v index m = b bs + i.
+__device__ __forceinline__ int m2_unit(int m, int nb, int bs) { return (m % nb) * bs + m / nb; }
+
+template <int QW, int NT>
+__global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
+  constexpr int KC = 4;  // bs <= 64
+  extern __shared__ float lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwc = p.nwc;
+  const bool poller = wave >= nwc;
+  const int j = lane & 3, kb4 = lane >> 2, s = (lane >> 2) & 3;
+  const int bs = p.bs, H = p.H, nb = p.nb;
+
+  const int gid = blockIdx.x % p.ngroups;
+  const int b = blockIdx.x / p.ngroups;  // block of L
+  const int rb_begin = gid * p.RB;
+  const int rb_end = min(rb_begin + p.RB, p.nrb);
+  const int nrbm = rb_end - rb_begin;
+  const int U = bs;  // units per workgroup, in y order i = 0 .. bs-1
+
+  float* hst = lds;                     // [2][4][rsh]  staged q_in(h), all H
+  float* zst = hst + 8 * p.rsh;         // [3][4][rsz]  z_g in y order of block b
+  float* hk = zst + 12 * p.rsz;         // [RB][4][U]   raw h of this workgroup's units
+  float* gst = hk + p.RB * 4 * U;       // [2][4][3][U] staged gi
+  int* flags = reinterpret_cast<int*>(gst + 24 * U);  // [0] compute-wave iterations published,
+                                                      // [1] group on one XCD
+  const int lds_floats = 8 * p.rsh + 12 * p.rsz + p.RB * 4 * U + 24 * U + 4;
+  for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
+
+  const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) st_tagged(p.xw + blockIdx.x, __uint_as_float(xcc_id()), base + 1u);
+  const int niter = p.T * nrbm;
+  lds_barrier();
+
+  // Prologue: q_in(h0) of the first row-block, raw h0 and step-0 gate inputs.
+  {
+    const int rb = rb_begin;
+    for (int w = threadIdx.x; w < 4 * H; w += blockDim.x) {
+      const int r = w / H, k = w - r * H;
+      const int row = 4 * rb + r;
+      float v = 0.0f;
+      if (row < p.B) {
+        v = p.h0[(int64_t)row * p.sh0_b + k];
+        if (p.qin.on) v = fake_quant(v, p.qin);
+      }
+      hst[r * p.rsh + k] = v;
+    }
+    for (int w = threadIdx.x; w < nrbm * 4 * U; w += blockDim.x) {
+      const int rbl = w / (4 * U), rem = w - rbl * 4 * U, r = rem / U, i = rem - r * U;
+      const int row = 4 * (rb_begin + rbl) + r;
+      hk[w] = row < p.B ? p.h0[(int64_t)row * p.sh0_b + m2_unit(b * bs + i, nb, bs)] : 0.0f;
+    }
+    for (int w = threadIdx.x; w < 12 * U; w += blockDim.x) {
+      const int r = w / (3 * U), rem = w - r * 3 * U, g = rem / U, i = rem - g * U;
+      const int row = 4 * rb + r;
+      gst[w] = row < p.B ? p.gi[(int64_t)row * p.sg_b + g * H + m2_unit(b * bs + i, nb, bs)] : 0.0f;
+    }
+  }
+  lds_barrier();
+
+  if (!poller) {
+    // Phase-1 quad q of this wave: qd = wave + nwc q -> first-factor block
+    // a = qd / (cpb / 4), rows c0 .. c0 + 3 of R_g[a]. Phase-2 quad: rows
+    // 4 qd .. 4 qd + 3 of L_g[b].
+    const int qpa = p.cpb / 4;
+    float wr[QW][3][KC], wl[QW][3][KC];
+    int ablk[QW], zpos[QW];
+    bool ok[QW];
+#pragma unroll
+    for (int q = 0; q < QW; ++q) {
+      const int qd = wave + nwc * q;
+      ok[q] = qd < p.nq;
+      const int a = ok[q] ? qd / qpa : 0;
+      const int c0 = b * p.cpb + 4 * (qd - a * qpa);
+      ablk[q] = a;
+      zpos[q] = (c0 + j) * nb + a - b * bs;  // this lane's z entry in y order (lane < 16)
+      load_w<KC>(p.w, nb, bs, a, c0, j, kb4, ok[q], wr[q]);
+      load_w<KC>(p.w2, nb, bs, b, 4 * qd, j, kb4, ok[q], wl[q]);
+    }
+    // Epilogue lanes: lanes 16 q .. 16 q + 15 take phase-2 quad q.
+    const int qe = lane >> 4;
+    const int qde = wave + nwc * (qe < QW ? qe : 0);
+    const bool lead = lane < 16 * QW && qde < p.nq;
+    const int ie = 4 * qde + j;  // this lane's output in y order
+    const int unit = m2_unit(b * bs + ie, nb, bs);
+    float bias[3];
+#pragma unroll
+    for (int g = 0; g < 3; ++g) bias[g] = lead ? p.bh[g * H + unit] : 0.0f;
+
+    for (int it = 0; it < niter; ++it) {
+      const int t = it / nrbm;
+      const int rbl = it - t * nrbm;
+      const int rb = rb_begin + rbl;
+      const int buf = it & 1;
+      const float* hs = hst + buf * 4 * p.rsh + j * p.rsh;
+      // phase 1: z_g entries of this wave's quads -> zst (y order)
+#pragma unroll
+      for (int q = 0; q < QW; ++q) {
+        float a1[3][KC];
+        lds_a<KC>(hs + ablk[q] * bs, kb4, a1[0]);
+        f4 acc[3];
+        mfma3<KC, true>(a1, wr[q], acc);
+#pragma unroll
+        for (int g = 0; g < 3; ++g) {
+          const float z = reduce16(acc[g], s);
+          if (lane < 16 && ok[q]) zst[g * 4 * p.rsz + s * p.rsz + zpos[q]] = z;
+        }
+      }
+      lds_barrier();
+      // phase 2: L_g[b] times the staged z_g
+      float a2[3][KC];
+#pragma unroll
+      for (int g = 0; g < 3; ++g) lds_a<KC>(zst + g * 4 * p.rsz + j * p.rsz, kb4, a2[g]);
+      float gh[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < QW; ++q) {
+        f4 acc[3];
+        mfma3<KC, false>(a2, wl[q], acc);
+#pragma unroll
+        for (int g = 0; g < 3; ++g) {
+          const float v = reduce16(acc[g], s);
+          gh[g] = (qe == q) ? v : gh[g];
+        }
+      }
+      const int row = 4 * rb + s;
+      const float* gs_ = gst + buf * 12 * U + s * 3 * U + ie;
+      float* hkp = hk + (rbl * 4 + s) * U + ie;
+      if (lead) {
+        const float hprev = *hkp;
+        float hn = gru_update(gs_[0], gs_[U], gs_[2 * U], gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
+        if (p.qout.on) hn = fake_quant(hn, p.qout);
+        if (row < p.B) p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
+        *hkp = hn;
+        if (t + 1 < p.T) {
+          const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
+          uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + row) * H + unit;
+          if (t >= 1 && flags[1] != 0)
+            st_tagged_xcd(dst, hq, base + (uint32_t)t + 1u);
+          else
+            st_tagged(dst, hq, base + (uint32_t)t + 1u);
+        }
+      }
+      if (lane == 0) __hip_atomic_fetch_add(&flags[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      lds_barrier();
+    }
+  } else {
+    // Poller wave pr stages row pr of iteration it + 1 (see the dense kernel).
+    const int pr = wave - nwc;
+    constexpr int NGI = (3 * 64 + 63) / 64;  // 3 U <= 192 gate inputs per row
+    for (int it = 0; it < niter; ++it) {
+      const int nx = it + 1;
+      const bool more = nx < niter;
+      const int t2 = nx / nrbm;
+      const int rb2 = rb_begin + (nx - t2 * nrbm);
+      const int row = 4 * rb2 + pr;
+      float gv[NGI];
+#pragma unroll
+      for (int i = 0; i < NGI; ++i) {
+        const int w = lane + 64 * i;
+        const int g = w / U, ii = w - g * U;
+        const bool okw = more && w < 3 * U && row < p.B;
+        gv[i] = okw ? p.gi[(int64_t)t2 * p.sg_t + (int64_t)row * p.sg_b + g * H + m2_unit(b * bs + ii, nb, bs)] : 0.0f;
+      }
+      lds_barrier();  // the compute waves' phase-1/phase-2 barrier
+      if (more) {
+        float* hs = hst + (nx & 1) * 4 * p.rsh + pr * p.rsh;
+        if (t2 == 0) {
+          for (int k = lane; k < H; k += 64) {
+            float v = 0.0f;
+            if (row < p.B) {
+              v = p.h0[(int64_t)row * p.sh0_b + k];
+              if (p.qin.on) v = fake_quant(v, p.qin);
+            }
+            hs[k] = v;
+          }
+        } else {
+          if (pr == 0 && nx == nrbm)  // first exchange of the launch
+            flags[1] = (nb <= 64 && group_on_one_xcd(p.ctrl, p.xw + gid, p.ngroups, nb, base + 1u)) ? 1 : 0;
+          wait_lds_count(p.ctrl, &flags[0], nwc * (it + 1));
+          const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * H;
+          const uint32_t tag = base + (uint32_t)t2;
+          // H words of the row in chunks of 512 (lane k = lane + 64 m)
+          if (H <= 256) {
+            poll_rows<1, 4>(p.ctrl, hb, 0, hs, 0, H, tag);
+          } else {
+            for (int k0 = 0; k0 < H; k0 += 512)
+              poll_rows<1, 8>(p.ctrl, hb + k0, 0, hs + k0, 0, min(512, H - k0), tag);
+          }
+        }
+        float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
+#pragma unroll
+        for (int i = 0; i < NGI; ++i) {
+          const int w = lane + 64 * i;
+          if (w < 3 * U) gs_[w] = gv[i];
+        }
+      }
+      lds_barrier();
+    }
+  }
+  leave_grid(p.ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T);
+}
 
 struct M2Params {
   const float* gi;
@@ -216,9 +452,104 @@ int plan_m2(const gs_args* a, M2Plan* pl, const char* who) {
   return GS_OK;
 }
 
+// ---- fused kernel: host side ---------------------------------------------------
+
+typedef void (*M2FFn)(M2FParams);
+
+struct M2FPlan {
+  int QW, nt, nwc, nrb, Bp, rsh, rsz;
+  int64_t xh_bytes, xw_bytes;
+  M2FFn fn;
+};
+
+// The fused kernel covers bs <= 64 with nb | bs and bs / nb a multiple of 4,
+// for H <= 2048.
+bool plan_fused(const gs_args* a, M2FPlan* pl) {
+  const int nb = (int)a->nblocks, bs = (int)a->blksz, H = (int)a->H;
+  if (bs > 64 || bs % nb != 0 || (bs / nb) % 4 != 0 || H > 2048) return false;
+  const int nq = bs / 4;
+  pl->QW = nq <= 12 ? 1 : 2;
+  pl->nwc = (nq + pl->QW - 1) / pl->QW;
+  if (pl->QW == 1) {
+    pl->nt = 1024;
+    pl->fn = monarch2_fused_kernel<1, 1024>;
+  } else {
+    pl->nt = 768;
+    pl->fn = monarch2_fused_kernel<2, 768>;
+  }
+  pl->nrb = (int)((a->B + 3) / 4);
+  pl->Bp = 4 * pl->nrb;
+  pl->rsh = H + 68;  // phase-1 operand reads run up to 63 words past a block start
+  pl->rsz = 68;
+  // pollers load up to 511 words past the last chunk start of a row
+  pl->xh_bytes = align256(2 * (int64_t)pl->Bp * H * 8 + 512 * 8);
+  pl->xw_bytes = align256((int64_t)pl->nrb * nb * 8);
+  return true;
+}
+
+int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const char* who) {
+  const int nb = (int)a->nblocks, bs = (int)a->blksz;
+  const int threads = 64 * (pl.nwc + kPollers);
+  const int U = bs;
+  int G = pl.nrb, RB = 1;
+  size_t lds = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    RB = (pl.nrb + G - 1) / G;
+    G = (pl.nrb + RB - 1) / RB;
+    lds = sizeof(float) * (size_t)(8 * pl.rsh + 12 * pl.rsz + RB * 4 * U + 24 * U + 4);
+    if (lds > 65536)
+      GS_CHECK_HIP(hipFuncSetAttribute((const void*)pl.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    int gfit = 0;
+    const int rc = coop_groups((const void*)pl.fn, threads, lds, nb, pl.nrb, &gfit, who);
+    if (rc) return rc;
+    if (gfit >= G) break;
+    G = gfit;
+  }
+  M2FParams p;
+  p.gi = a->gi;
+  p.h0 = a->h0;
+  p.w = a->w;
+  p.w2 = a->w2;
+  p.bh = a->bh;
+  p.out = a->out;
+  char* ws = static_cast<char*>(a->workspace);
+  p.ctrl = ctrl_of(ws);
+  p.xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
+  p.xw = reinterpret_cast<uint64_t*>(ws + kCtrlBytes + pl.xh_bytes);
+  p.sg_t = a->sg_t;
+  p.sg_b = a->sg_b;
+  p.sh0_b = a->sh0_b;
+  p.so_t = a->so_t;
+  p.so_b = a->so_b;
+  p.T = (int)a->T;
+  p.B = (int)a->B;
+  p.H = (int)a->H;
+  p.nb = nb;
+  p.bs = bs;
+  p.cpb = bs / nb;
+  p.nq = bs / 4;
+  p.ngroups = G;
+  p.RB = RB;
+  p.nrb = pl.nrb;
+  p.Bp = pl.Bp;
+  p.nwg = G * nb;
+  p.nwc = pl.nwc;
+  p.rsh = pl.rsh;
+  p.rsz = pl.rsz;
+  p.qin = to_quant(a->q_in);
+  p.qout = to_quant(a->q_out);
+  p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
+  void* kargs[] = {&p};
+  GS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)pl.fn, dim3(p.nwg), dim3(threads), kargs, (unsigned)lds, stream));
+  return GS_OK;
+}
+
 }  // namespace
 
 int64_t monarch2_workspace_bytes(const gs_args* a) {
+  M2FPlan fp;
+  if (a->nblocks >= 1 && a->blksz >= 1 && a->nblocks * a->blksz == a->H && plan_fused(a, &fp))
+    return kCtrlBytes + fp.xh_bytes + fp.xw_bytes;
   M2Plan pl;
   const int rc = plan_m2(a, &pl, "gs_workspace_bytes");
   if (rc) return rc;
@@ -229,6 +560,12 @@ int run_monarch2(const gs_args* a, hipStream_t stream, const char* who) {
   M2Plan pl;
   int rc = plan_m2(a, &pl, who);
   if (rc) return rc;
+  M2FPlan fp;
+  if (plan_fused(a, &fp)) {
+    rc = check_workspace(a, kCtrlBytes + fp.xh_bytes + fp.xw_bytes, who);
+    if (rc) return rc;
+    return run_fused(a, fp, stream, who);
+  }
   rc = check_workspace(a, kCtrlBytes + pl.xh_bytes + pl.xz_bytes, who);
   if (rc) return rc;
   M2Fn fn = pick_split(pl.KC, &pl.nt);

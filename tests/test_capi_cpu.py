@@ -118,6 +118,11 @@ def test_workspace_sizes():
     # 4 blocks x 4 workgroups of 8 compute waves per row-block
     assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m1)) == 256 + xh + 16 * 8 * 8 + 8 * 16 * 8
     a_m2 = _args(T=64, B=32, H=512, nblocks=8, blksz=64, w2=FAKE)
+    # fused two-factor kernel (bs = 64, nb = 8): one exchange of q_in(h) padded
+    # by 512 words, plus one XCD-id word per workgroup (8 row-blocks x 8 blocks)
+    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m2)) == 256 + xh + 512 * 8 + 8 * 8 * 8
+    # split two-factor kernel (bs = 128 > 64): q_in(h) plus 3 gates of z words
+    a_m2 = _args(T=64, B=32, H=512, nblocks=4, blksz=128, w2=FAKE)
     assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m2)) == 256 + 4 * xh
     # diagonal and butterfly kernels use no workspace beyond the control words
     assert lib.gs_workspace_bytes(_lib.KIND_DIAGONAL, ctypes.byref(a)) == 256
