@@ -1,6 +1,7 @@
 """Benchmark of the persistent GRU scan forward on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--kinds 0,1,2,3,4] [--no-cpu]
+    python bench.py --copy-mib N [--steps K]   # counter calibration, see below
 
 A step is one forward scan (the drop-in ``gru_scan_*`` call) over one batch
 of synthetic input already resident in HBM. The headline line is the dense
@@ -18,6 +19,12 @@ Per kind:
                MI355X peak (HBM 8 TB/s; fp32 MFMA 157.3 TFLOP/s);
   cpu_baseline the oracle (the reference's per-step PyTorch CPU path) timed on
                this host's cores on a bounded sample.
+
+--copy-mib N runs K launches of a plain elementwise copy (out = x * 1, fp32)
+of N MiB and exits. Under rocprofv3 --pmc it calibrates the FETCH_SIZE and
+WRITE_SIZE counters: the copy reads and writes exactly N MiB per launch, so
+the counters' ratio to N MiB scales the scan kernels' counter readings to HBM
+bytes (the "traffic" field, read from profiles/traffic.json).
 """
 
 from __future__ import annotations
@@ -156,6 +163,7 @@ def main() -> int:
     ap.add_argument("--kinds", default="0,1,2,3,4")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=4.0, help="seconds of CPU baseline per kind")
+    ap.add_argument("--copy-mib", type=int, default=0, help="run a plain N MiB copy K times and exit")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -171,6 +179,17 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda", 0)
+    if args.copy_mib > 0:
+        n = args.copy_mib * (1 << 20) // 4
+        x = torch.rand(n, device=dev)
+        y = torch.empty_like(x)
+        torch.cuda.synchronize(dev)
+        for _ in range(args.steps):
+            torch.mul(x, 1.0, out=y)
+        torch.cuda.synchronize(dev)
+        print(json.dumps({"copy_mib": args.copy_mib, "launches": args.steps,
+                          "bytes_read_per_launch": 4 * n, "bytes_written_per_launch": 4 * n}), flush=True)
+        return 0
     gru_qat_amd.load_library()
     kinds = [int(k) for k in args.kinds.split(",") if k.strip()]
 

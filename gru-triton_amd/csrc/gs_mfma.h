@@ -101,7 +101,6 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 struct DevInfo {
   int cus = 0;
-  int coop = 0;
 };
 
 inline int device_info(DevInfo* out) {
@@ -114,7 +113,6 @@ inline int device_info(DevInfo* out) {
   std::lock_guard<std::mutex> lk(mu);
   if (!have[dev]) {
     GS_CHECK_HIP(hipDeviceGetAttribute(&cache[dev].cus, hipDeviceAttributeMultiprocessorCount, dev));
-    GS_CHECK_HIP(hipDeviceGetAttribute(&cache[dev].coop, hipDeviceAttributeCooperativeLaunch, dev));
     have[dev] = true;
   }
   *out = cache[dev];
@@ -128,13 +126,23 @@ inline int choose_kc(int klen) {
   return -1;
 }
 
-// Largest number of groups a cooperative launch can hold: workgroups of
+// Persistent grids. Workgroups of one group wait for each other's exchange
+// words, so a group's workgroups must run at the same time. The grid is sized
+// to what the device holds at once (occupancy x CUs) and launched as an
+// ordinary kernel: on an otherwise idle device every workgroup of such a grid
+// is resident from the start. A kernel on another stream that holds CUs delays
+// the rest of the grid until it ends; every wait in these kernels is bounded,
+// so a delay beyond the poll bound ends the launch with the workspace fault
+// word set instead of hanging. (hipLaunchCooperativeKernel would add about
+// 16 us of dispatch overhead per call on this stack.)
+//
+// Largest number of groups the device holds at once: workgroups of
 // `threads` threads and `lds` bytes, `per_group` workgroups per group.
-inline int coop_groups(const void* fn, int threads, size_t lds, int per_group, int want, int* out, const char* who) {
+inline int resident_groups(const void* fn, int threads, size_t lds, int per_group, int want, int* out,
+                           const char* who) {
   DevInfo di;
   int rc = device_info(&di);
   if (rc) return rc;
-  if (!di.coop) return set_error(GS_ERR_CAPACITY, "%s: device does not support cooperative launch", who);
   int occ = 0;
   GS_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, threads, lds));
   const int64_t resident = (int64_t)occ * di.cus;

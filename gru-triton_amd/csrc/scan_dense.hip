@@ -318,7 +318,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   int G = pl.nrb, RB = 1;
   size_t lds = 0;
   // Local mode keeps RB = 1 (a workgroup's LDS staging holds one row-block);
-  // remote mode shrinks the group count until the cooperative grid fits.
+  // remote mode shrinks the group count until the grid is resident at once.
   for (int pass = 0; pass < 2; ++pass) {
     RB = (pl.nrb + G - 1) / G;
     G = (pl.nrb + RB - 1) / RB;
@@ -328,7 +328,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
       GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     if (!pl.remote) break;
     int gfit = 0;
-    rc = coop_groups((const void*)fn, threads, lds, per_set, pl.nrb, &gfit, who);
+    rc = resident_groups((const void*)fn, threads, lds, per_set, pl.nrb, &gfit, who);
     if (rc) return rc;
     if (gfit >= G) break;
     G = gfit;
@@ -367,14 +367,8 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
   p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
-  if (pl.remote) {
-    void* kargs[] = {&p};
-    GS_CHECK_HIP(
-        hipLaunchCooperativeKernel((const void*)fn, dim3(p.nwg), dim3(threads), kargs, (unsigned)lds, stream));
-  } else {
-    hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), lds, stream, p);
-    GS_CHECK_HIP(hipGetLastError());
-  }
+  hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), lds, stream, p);
+  GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }
 

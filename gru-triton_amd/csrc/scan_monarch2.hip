@@ -500,7 +500,7 @@ int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const cha
     if (lds > 65536)
       GS_CHECK_HIP(hipFuncSetAttribute((const void*)pl.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     int gfit = 0;
-    const int rc = coop_groups((const void*)pl.fn, threads, lds, nb, pl.nrb, &gfit, who);
+    const int rc = resident_groups((const void*)pl.fn, threads, lds, nb, pl.nrb, &gfit, who);
     if (rc) return rc;
     if (gfit >= G) break;
     G = gfit;
@@ -539,8 +539,8 @@ int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const cha
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
   p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
-  void* kargs[] = {&p};
-  GS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)pl.fn, dim3(p.nwg), dim3(threads), kargs, (unsigned)lds, stream));
+  hipLaunchKernelGGL(pl.fn, dim3(p.nwg), dim3(threads), lds, stream, p);
+  GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }
 
@@ -573,11 +573,8 @@ int run_monarch2(const gs_args* a, hipStream_t stream, const char* who) {
   if (pl.lds > 65536)
     GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl.lds));
   int G = pl.nrb;
-  const bool coop = pl.P > 1;
-  if (coop) {
-    rc = coop_groups((const void*)fn, threads, pl.lds, pl.P, pl.nrb, &G, who);
-    if (rc) return rc;
-  }
+  rc = resident_groups((const void*)fn, threads, pl.lds, pl.P, pl.nrb, &G, who);
+  if (rc) return rc;
   const int RB = (pl.nrb + G - 1) / G;
   G = (pl.nrb + RB - 1) / RB;
 
@@ -612,14 +609,8 @@ int run_monarch2(const gs_args* a, hipStream_t stream, const char* who) {
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
   p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
-  if (coop) {
-    void* kargs[] = {&p};
-    GS_CHECK_HIP(hipLaunchCooperativeKernel((const void*)fn, dim3(p.nwg), dim3(threads), kargs, (unsigned)pl.lds,
-                                            stream));
-  } else {
-    hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), pl.lds, stream, p);
-    GS_CHECK_HIP(hipGetLastError());
-  }
+  hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), pl.lds, stream, p);
+  GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }
 
