@@ -232,7 +232,7 @@ def main() -> int:
         "kinds": {str(k): v for k, v in results.items()},
         "device": {"name": props.name, "cus": props.multi_processor_count, "host_cpu": cpu_model(),
                    "host_cores": os.cpu_count()},
-        "barrier_faults": faults,
+        "exchange_faults": faults,
     }
     print(json.dumps(line), flush=True)
     return 0 if faults == 0 else 1

@@ -173,7 +173,7 @@ def workspace(device: torch.device, stream_handle: int, nbytes: int, steps: int 
 def workspace_faults(device: Optional[torch.device] = None) -> int:
     """Read and clear the fault word of every cached workspace (synchronises).
 
-    Nonzero means a persistent kernel hit its barrier time-out and the output
+    Nonzero means a persistent kernel ran out of its bounded wait and the output
     of that launch is invalid.
     """
     lib = load()

@@ -16,10 +16,19 @@
  * resident, with unit stride along their last axis; the other strides are
  * given in elements. The library never allocates device memory: the caller
  * passes `out` and a scratch `workspace` of gs_workspace_bytes() bytes, zeroed
- * once when it is first allocated. Every entry point leaves the workspace
- * zeroed again when its kernel ends, so one workspace serves any number of
- * calls issued in order on one stream; calls that overlap in time (two
- * streams) need distinct workspaces.
+ * once when it is first allocated. The dense and Monarch kernels exchange the
+ * hidden state between workgroups through words tagged with a step counter
+ * that lives in the workspace and advances by T per call, so one workspace
+ * serves any number of calls issued in order on one stream, up to 2^32 - 2^24
+ * total scan steps, after which the caller zeroes it again; calls that overlap
+ * in time (two streams) need distinct workspaces.
+ *
+ * Those kernels are persistent: the workgroups of a batch group wait for each
+ * other's words every step. The grid is capped at what the device holds at
+ * once (occupancy x CUs) and launched as an ordinary kernel. A kernel on
+ * another stream that holds CUs delays part of the grid; every wait is
+ * bounded, and a wait that runs out sets the workspace fault word (see
+ * gs_workspace_status) instead of hanging.
  *
  * Return codes: GS_OK, or a negative GS_ERR_* value; gs_last_error() then
  * returns a message for the calling thread.
@@ -103,12 +112,12 @@ int gs_butterfly_fwd(const gs_args* args, hipStream_t stream);
  * reference counterpart: it lets tests cross-check the two implementations. */
 int gs_butterfly_fwd_generic(const gs_args* args, hipStream_t stream);
 
-/* Scratch bytes the kind needs for these arguments (barrier counters, exchange
- * buffers). Pure host arithmetic; never touches the device. Negative on error. */
+/* Scratch bytes the kind needs for these arguments (control words, exchange
+ * words). Pure host arithmetic; never touches the device. Negative on error. */
 int64_t gs_workspace_bytes(int kind, const gs_args* args);
 
 /* Reads and clears the device-side fault word of a workspace (nonzero means a
- * persistent kernel hit its barrier time-out and its output is invalid).
+ * persistent kernel ran out of its bounded wait and its output is invalid).
  * Synchronises the stream. Returns the word, or a negative GS_ERR_* value. */
 int gs_workspace_status(void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
