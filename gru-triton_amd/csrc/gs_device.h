@@ -3,9 +3,12 @@
 // Numerics follow the reference PyTorch cell (LarocheC/gru-triton
 // src/gru_qat/gru_cell.py:437-464): r = sigmoid(gi_r + gh_r),
 // z = sigmoid(gi_z + gh_z), n = tanh(gi_n + r * gh_n), h' = (1 - z) * n + z * h,
-// evaluated as separately rounded fp32 operations in that order (FMA
-// contraction is switched off in the gate epilogue so each product rounds the
-// way torch's elementwise kernels round it).
+// evaluated in that order as separately rounded fp32 operations (FMA
+// contraction is off in the gate epilogue). sigmoid and tanh use the hardware
+// base-2 exponential and reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each);
+// their deviation from torch's CPU functions is a few 1e-8 absolute, far inside
+// the 1e-5 parity bar, and the fake-quant division stays IEEE so integer codes
+// depend only on the pre-quant value.
 #pragma once
 
 #include <type_traits>
@@ -33,9 +36,21 @@ __device__ __forceinline__ float fake_quant(float x, const Quant& q) {
   return v * q.scale;
 }
 
-// torch's CPU sigmoid is 1 / (1 + exp(-x)) with a 1-ulp exp and an exact
-// division; this is the same expression on the ROCm device library's expf.
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+constexpr float kLog2e = 1.4426950408889634f;
+
+// sigmoid(x) = 1 / (1 + e^-x) with e^y = 2^(y log2 e). Saturates correctly:
+// x -> -inf gives rcp(inf) = 0, x -> +inf gives rcp(1) = 1.
+__device__ __forceinline__ float sigmoid(float x) {
+#pragma clang fp contract(off)
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -kLog2e));
+}
+
+// tanh(x) = 1 - 2 / (1 + e^2x). Absolute error stays at the fp32 rounding of
+// values near 1 (a few 1e-8), including near 0 where the form cancels.
+__device__ __forceinline__ float tanh_fast(float x) {
+#pragma clang fp contract(off)
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * (2.0f * kLog2e)));
+}
 
 // One GRU gate epilogue. Inputs are the gate pre-activations' two halves; h is
 // the raw (unquantized) previous state.
@@ -44,7 +59,7 @@ __device__ __forceinline__ float gru_update(float gir, float giz, float gin, flo
 #pragma clang fp contract(off)
   const float r = sigmoid(gir + ghr);
   const float z = sigmoid(giz + ghz);
-  const float n = tanhf(gin + r * ghn);
+  const float n = tanh_fast(gin + r * ghn);
   return (1.0f - z) * n + z * h;
 }
 
@@ -134,39 +149,6 @@ __device__ __forceinline__ uint32_t xcc_id() {
 __device__ __forceinline__ uint32_t tag_of(uint64_t w) { return (uint32_t)(w >> 32); }
 __device__ __forceinline__ float value_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
 
-// Polls N words until every valid one carries `tag`. addr(i) returns the
-// word's address or nullptr for "no word" (value 0). Returns the values.
-template <int N, typename Addr>
-__device__ __forceinline__ void poll_tagged(const Ctrl& c, uint32_t tag, Addr addr, float (&out)[N]) {
-  uint64_t v[N];
-  const uint64_t ready_zero = (uint64_t)tag << 32;
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    const uint64_t* q = addr(i);
-    v[i] = q ? ld_tagged(q) : ready_zero;
-  }
-  uint32_t polls = 0;
-  while (true) {
-    bool ready = true;
-#pragma unroll
-    for (int i = 0; i < N; ++i) ready = ready && tag_of(v[i]) == tag;
-    if (ready) break;
-    if (++polls > kSpinLimit) {
-      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
-    }
-    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-      break;
-    __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      if (tag_of(v[i]) != tag) v[i] = ld_tagged(addr(i));
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < N; ++i) out[i] = value_of(v[i]);
-}
-
 // Polls MW words base[src[i]] (those with bit i of `valid`) until each
 // carries `tag`, then stores their values to dst_lds[dst[i]]. Offsets are
 // precomputed by the caller, so the loop is loads, compares and a sleep.
@@ -207,54 +189,6 @@ __device__ __forceinline__ void static_for(F&& f) {
     f(std::integral_constant<int, I>{});
     static_for<I + 1, N>(f);
   }
-}
-
-// Polls R rows of tagged words into LDS: row r, word k = lane + 64 m
-// (m < MPR) at src[r * src_stride + k], stored to dst[r * dst_stride + k] for
-// k < klen. src and dst are wave-uniform; the loads address words up to
-// k = 64 MPR - 1 of every row, so the buffer behind src must extend that far
-// (words past klen are loaded but neither waited for nor stored). Only words
-// whose tag is still stale are loaded again.
-template <int R, int MPR>
-__device__ __forceinline__ void poll_rows(const Ctrl& c, const uint64_t* src, int src_stride, float* dst,
-                                          int dst_stride, int klen, uint32_t tag) {
-  constexpr int MW = R * MPR;
-  static_assert(MW <= 32, "poll mask is 32 bits");
-  const int lane = threadIdx.x & 63;
-  uint32_t valid = 0;
-#pragma unroll
-  for (int m = 0; m < MPR; ++m) {
-    const bool ok = lane + 64 * m < klen;
-#pragma unroll
-    for (int r = 0; r < R; ++r) valid |= (ok ? 1u : 0u) << (r * MPR + m);
-  }
-  uint64_t v[MW];
-  static_for<0, MW>([&](auto I) {
-    constexpr int r = I / MPR, m = I % MPR;
-    v[I] = ld_tagged(src + r * src_stride + lane + 64 * m);
-  });
-  uint32_t polls = 0;
-  while (true) {
-    uint32_t pending = 0;
-    static_for<0, MW>([&](auto I) { pending |= (tag_of(v[I]) != tag ? 1u : 0u) << I; });
-    pending &= valid;
-    if (pending == 0u) break;
-    if (++polls > kSpinLimit) {
-      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
-    }
-    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-      break;
-    __builtin_amdgcn_s_sleep(1);
-    static_for<0, MW>([&](auto I) {
-      constexpr int r = I / MPR, m = I % MPR;
-      if ((pending >> I) & 1u) v[I] = ld_tagged(src + r * src_stride + lane + 64 * m);
-    });
-  }
-  static_for<0, MW>([&](auto I) {
-    constexpr int r = I / MPR, m = I % MPR;
-    if ((valid >> I) & 1u) dst[r * dst_stride + lane + 64 * m] = value_of(v[I]);
-  });
 }
 
 // Waits (bounded) until the LDS counter reaches target.

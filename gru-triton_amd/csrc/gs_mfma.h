@@ -31,8 +31,10 @@ __device__ __forceinline__ float reduce16(f4 acc, int s) {
     acc[c] += row_ror<8>(acc[c]);
     acc[c] += row_ror<4>(acc[c]);
   }
-  const float v = (s == 0) ? acc[0] : (s == 1) ? acc[1] : (s == 2) ? acc[2] : acc[3];
-  return sum_across_rows(v);
+  // branch-free pick of acc[s] (lane-varying s)
+  const float lo = (s & 1) ? acc[1] : acc[0];
+  const float hi = (s & 1) ? acc[3] : acc[2];
+  return sum_across_rows((s & 2) ? hi : lo);
 }
 
 // Wh slice of a quad: w[((gate*nb + blk)*bs + o)*bs + k] for o = o0 + j,
@@ -51,6 +53,65 @@ __device__ __forceinline__ void load_w(const float* w, int nb, int bs, int blk, 
       wr[g][m] = (ok && k < bs) ? row[k] : 0.0f;
     }
   }
+}
+
+// Interleaved staging layout of a 4-row operand block: element (row r, k) sits
+// at il_index(r, k) = (k / 4) * 16 + 4 r + k % 4. The A operand of lane l for
+// K-chunk q (k = 64 q + 4 (l / 4) + e, row l % 4) is then the float4 at
+// 256 q + 4 l: a wave's operand reads cover contiguous LDS, free of bank
+// conflicts. A block holding K values per row takes 4 K floats.
+__device__ __forceinline__ int il_index(int r, int k) { return ((k >> 2) << 4) + (r << 2) + (k & 3); }
+
+template <int KC>
+__device__ __forceinline__ void lds_a_il(const float* blk, int lane, float (&a)[KC]) {
+#pragma unroll
+  for (int q = 0; q < KC / 4; ++q) {
+    const f4 v = *reinterpret_cast<const f4*>(blk + 256 * q + 4 * lane);
+    a[4 * q + 0] = v[0];
+    a[4 * q + 1] = v[1];
+    a[4 * q + 2] = v[2];
+    a[4 * q + 3] = v[3];
+  }
+}
+
+// Polls one row of tagged words into an interleaved LDS block: lane l takes
+// k = 64 m + l (m < MPR) from src[k] and stores dst[il_index(r, k)] for
+// k < klen. Each load instruction reads 64 consecutive words (polling 4 rows
+// x 16 words per instruction instead measured 25 % slower exchanges). Loads
+// address k up to 64 MPR - 1, so the buffer behind src must extend that far
+// (words past klen are loaded but neither waited for nor stored). Only stale
+// words are loaded again.
+template <int MPR>
+__device__ __forceinline__ void poll_row_il(const Ctrl& c, const uint64_t* src, float* dst, int r, int klen,
+                                            uint32_t tag) {
+  static_assert(MPR <= 32, "poll mask is 32 bits");
+  const int lane = threadIdx.x & 63;
+  const uint64_t* s0 = src + lane;
+  uint32_t valid = 0;
+#pragma unroll
+  for (int m = 0; m < MPR; ++m) valid |= (lane + 64 * m < klen ? 1u : 0u) << m;
+  uint64_t v[MPR];
+  static_for<0, MPR>([&](auto I) { v[I] = ld_tagged(s0 + 64 * I); });
+  uint32_t polls = 0;
+  while (true) {
+    uint32_t pending = 0;
+    static_for<0, MPR>([&](auto I) { pending |= (tag_of(v[I]) != tag ? 1u : 0u) << I; });
+    pending &= valid;
+    if (pending == 0u) break;
+    if (++polls > kSpinLimit) {
+      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      break;
+    __builtin_amdgcn_s_sleep(1);
+    static_for<0, MPR>([&](auto I) {
+      if ((pending >> I) & 1u) v[I] = ld_tagged(s0 + 64 * I);
+    });
+  }
+  static_for<0, MPR>([&](auto I) {
+    if ((valid >> I) & 1u) dst[il_index(r, lane + 64 * I)] = value_of(v[I]);
+  });
 }
 
 // A operand from an LDS staging row: a[m] = row[kmap(m, kb4)].

@@ -51,7 +51,7 @@ struct DParams {
   int nb, bs, qpb;  // dense: nb = 1, bs = H
   int ngroups, G, RB, nrb, Bp, nwg, P;
   int nwc;  // compute waves per workgroup
-  int rs;   // LDS staging row stride (floats)
+  int hsz;  // floats per LDS staging block (4 rows x 16 KC, interleaved)
   Quant qin, qout;
   int qin_after_first;
 };
@@ -83,12 +83,12 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   const int rb_end = min(rb_begin + p.RB, p.nrb);
   const int nrbm = rb_end - rb_begin;
 
-  float* hst = lds;                  // [2][4][rs]   staged q_in(h) of the K range
-  float* hk = hst + 8 * p.rs;        // [RB][4][U]   raw h of this workgroup's units
+  float* hst = lds;                  // [2][hsz]     staged q_in(h) of the K range (il_index)
+  float* hk = hst + 2 * p.hsz;       // [RB][4][U]   raw h of this workgroup's units
   float* gst = hk + p.RB * 4 * U;    // [2][4][3][U] staged gi (remote mode)
   int* flags = reinterpret_cast<int*>(gst + 24 * U);  // remote mode: [0] compute-wave iterations
                                                       // published, [1] group on one XCD
-  const int lds_floats = 8 * p.rs + p.RB * 4 * U + (REMOTE ? 24 * U + 4 : 0);
+  const int lds_floats = 2 * p.hsz + p.RB * 4 * U + (REMOTE ? 24 * U + 4 : 0);
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
   const uint32_t base = REMOTE ? __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
@@ -107,7 +107,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
         v = p.h0[(int64_t)row * p.sh0_b + klo + k];
         if (p.qin.on) v = fake_quant(v, p.qin);
       }
-      hst[r * p.rs + k] = v;
+      hst[il_index(r, k)] = v;
     }
     for (int w = threadIdx.x; w < nrbm * 4 * U; w += blockDim.x) {
       const int rbl = w / (4 * U), rem = w - rbl * 4 * U, r = rem / U, u = rem - r * U;
@@ -135,6 +135,9 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
     float bias[3];
 #pragma unroll
     for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? p.bh[g * p.H + unit] : 0.0f;
+    // lane parts of the out / exchange-word offsets (row = 4 rb + s)
+    const int64_t lane_out = (int64_t)s * p.so_b + unit;
+    const int64_t lane_xh = (int64_t)s * p.H + unit;
     for (int it = 0; it < niter; ++it) {
       const int t = it / nrbm;
       const int rbl = it - t * nrbm;
@@ -157,7 +160,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       float* hkp = hk + (rbl * 4 + s) * U + 4 * wave + j;
       const float hprev = *hkp;
       float a[3][KC];
-      lds_a<KC>(hst + buf * 4 * p.rs + j * p.rs, kb4, a[0]);
+      lds_a_il<KC>(hst + buf * p.hsz, lane, a[0]);
       f4 acc[3];
       mfma3<KC, true>(a, wr, acc);
       float gh[3];
@@ -165,20 +168,20 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
       float hn = gru_update(gir, giz, gin, gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
       if (p.qout.on) hn = fake_quant(hn, p.qout);
-      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
+      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = hn;
       const bool xcd_local = REMOTE && t >= 1 && __builtin_amdgcn_readfirstlane(flags[1]) != 0;
       if (lead && unit_ok) {
         *hkp = hn;
         if (t + 1 < p.T) {
           const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
           if (REMOTE) {
-            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + row) * p.H + unit;
+            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * p.H + lane_xh;
             if (xcd_local)
               st_tagged_xcd(dst, hq, base + (uint32_t)t + 1u);
             else
               st_tagged(dst, hq, base + (uint32_t)t + 1u);
           } else {
-            hst[(buf ^ 1) * 4 * p.rs + s * p.rs + (unit - klo)] = hq;  // local mode: RB == 1
+            hst[(buf ^ 1) * p.hsz + il_index(s, unit - klo)] = hq;  // local mode: RB == 1
           }
         }
       }
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
           const bool ok = w < 3 * U && row < p.B && (ulo + u - klo) < p.bs;
           gv[i] = ok ? p.gi[(int64_t)t2 * p.sg_t + (int64_t)row * p.sg_b + g * p.H + ulo + u] : 0.0f;
         }
-        float* hs = hst + (nx & 1) * 4 * p.rs + pr * p.rs;
+        float* hs = hst + (nx & 1) * p.hsz;
         if (t2 == 0) {
           for (int k = lane; k < p.bs; k += 64) {
             float v = 0.0f;
@@ -216,15 +219,15 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
               v = p.h0[(int64_t)row * p.sh0_b + klo + k];
               if (p.qin.on) v = fake_quant(v, p.qin);
             }
-            hs[k] = v;
+            hs[il_index(pr, k)] = v;
           }
         } else {
           if (pr == 0 && nx == nrbm)  // first exchange of the launch
             flags[1] = (p.P <= 64 && group_on_one_xcd(p.ctrl, p.xw + gid, p.ngroups, p.P, base + 1u)) ? 1 : 0;
           wait_lds_count(p.ctrl, &flags[0], nwc * (it + 1));
-          // bs words of the row; lane takes k = lane + 64 m, m < KC/4 (bs <= 16 KC)
+          // bs words of row pr, k < 16 KC
           const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * p.H + klo;
-          poll_rows<1, KC / 4>(p.ctrl, hb, 0, hs, 0, p.bs, base + (uint32_t)t2);
+          poll_row_il<KC / 4>(p.ctrl, hb, hs, pr, p.bs, base + (uint32_t)t2);
         }
         float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
 #pragma unroll
@@ -261,7 +264,7 @@ DFn pick(int kind, bool remote, int KC, int* nt) {
 }
 
 struct DPlan {
-  int KC, nt, nwc, P, nrb, Bp, rs, nb, bs, qpb;
+  int KC, nt, nwc, P, nrb, Bp, hsz, nb, bs, qpb;
   bool remote;
   int64_t xh_bytes, xw_bytes;
 };
@@ -296,7 +299,7 @@ int plan_dense(int kind, const gs_args* a, DPlan* pl, const char* who) {
   pick(kind, pl->remote, pl->KC, &pl->nt);
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
-  pl->rs = 16 * pl->KC + 4;
+  pl->hsz = 64 * pl->KC;
   // The pollers load 16 KC words per row from the row's first unit; the pad
   // keeps the reads past the last row inside the workspace.
   pl->xh_bytes = pl->remote ? align256(2 * (int64_t)pl->Bp * a->H * 8 + 16 * pl->KC * 8) : 0;
@@ -323,7 +326,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
     RB = (pl.nrb + G - 1) / G;
     G = (pl.nrb + RB - 1) / RB;
     const int U = 4 * pl.nwc;
-    lds = sizeof(float) * (size_t)(8 * pl.rs + RB * 4 * U + (pl.remote ? 24 * U + 4 : 0));
+    lds = sizeof(float) * (size_t)(2 * pl.hsz + RB * 4 * U + (pl.remote ? 24 * U + 4 : 0));
     if (lds > 65536)
       GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     if (!pl.remote) break;
@@ -363,7 +366,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.nwg = p.ngroups * pl.P;
   p.P = pl.P;
   p.nwc = pl.nwc;
-  p.rs = pl.rs;
+  p.hsz = pl.hsz;
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
   p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);

@@ -43,7 +43,7 @@ struct M2FParams {
   int nb, bs, cpb, nq;  // nq = bs / 4 quads per phase
   int ngroups, RB, nrb, Bp, nwg;
   int nwc;       // compute waves per workgroup
-  int rsh, rsz;  // LDS row strides: staged q_in(h) rows, staged z rows
+  int hsz;       // floats per staged q_in(h) block (4 rows x H interleaved, plus read-over pad)
   Quant qin, qout;
   int qin_after_first;
 };
@@ -69,13 +69,13 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
   const int nrbm = rb_end - rb_begin;
   const int U = bs;  // units per workgroup, in y order i = 0 .. bs-1
 
-  float* hst = lds;                     // [2][4][rsh]  staged q_in(h), all H
-  float* zst = hst + 8 * p.rsh;         // [3][4][rsz]  z_g in y order of block b
-  float* hk = zst + 12 * p.rsz;         // [RB][4][U]   raw h of this workgroup's units
+  float* hst = lds;                     // [2][hsz]     staged q_in(h), all H (il_index)
+  float* zst = hst + 2 * p.hsz;         // [3][256]     z_g in y order of block b (il_index)
+  float* hk = zst + 3 * 256;            // [RB][4][U]   raw h of this workgroup's units
   float* gst = hk + p.RB * 4 * U;       // [2][4][3][U] staged gi
   int* flags = reinterpret_cast<int*>(gst + 24 * U);  // [0] compute-wave iterations published,
                                                       // [1] group on one XCD
-  const int lds_floats = 8 * p.rsh + 12 * p.rsz + p.RB * 4 * U + 24 * U + 4;
+  const int lds_floats = 2 * p.hsz + 3 * 256 + p.RB * 4 * U + 24 * U + 4;
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
   const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
         v = p.h0[(int64_t)row * p.sh0_b + k];
         if (p.qin.on) v = fake_quant(v, p.qin);
       }
-      hst[r * p.rsh + k] = v;
+      hst[il_index(r, k)] = v;
     }
     for (int w = threadIdx.x; w < nrbm * 4 * U; w += blockDim.x) {
       const int rbl = w / (4 * U), rem = w - rbl * 4 * U, r = rem / U, i = rem - r * U;
@@ -137,31 +137,33 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
     float bias[3];
 #pragma unroll
     for (int g = 0; g < 3; ++g) bias[g] = lead ? p.bh[g * H + unit] : 0.0f;
+    const int64_t lane_out = (int64_t)s * p.so_b + unit;  // row = 4 rb + s
+    const int64_t lane_xh = (int64_t)s * H + unit;
 
     for (int it = 0; it < niter; ++it) {
       const int t = it / nrbm;
       const int rbl = it - t * nrbm;
       const int rb = rb_begin + rbl;
       const int buf = it & 1;
-      const float* hs = hst + buf * 4 * p.rsh + j * p.rsh;
+      const float* hs = hst + buf * p.hsz;
       // phase 1: z_g entries of this wave's quads -> zst (y order)
 #pragma unroll
       for (int q = 0; q < QW; ++q) {
         float a1[3][KC];
-        lds_a<KC>(hs + ablk[q] * bs, kb4, a1[0]);
+        lds_a_il<KC>(hs + 4 * ablk[q] * bs, lane, a1[0]);  // block a starts at k = a bs, bs % 4 == 0
         f4 acc[3];
         mfma3<KC, true>(a1, wr[q], acc);
 #pragma unroll
         for (int g = 0; g < 3; ++g) {
           const float z = reduce16(acc[g], s);
-          if (lane < 16 && ok[q]) zst[g * 4 * p.rsz + s * p.rsz + zpos[q]] = z;
+          if (lane < 16 && ok[q]) zst[g * 256 + il_index(s, zpos[q])] = z;
         }
       }
       lds_barrier();
       // phase 2: L_g[b] times the staged z_g
       float a2[3][KC];
 #pragma unroll
-      for (int g = 0; g < 3; ++g) lds_a<KC>(zst + g * 4 * p.rsz + j * p.rsz, kb4, a2[g]);
+      for (int g = 0; g < 3; ++g) lds_a_il<KC>(zst + g * 256, lane, a2[g]);
       float gh[3] = {0.f, 0.f, 0.f};
 #pragma unroll
       for (int q = 0; q < QW; ++q) {
@@ -180,11 +182,11 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
         const float hprev = *hkp;
         float hn = gru_update(gs_[0], gs_[U], gs_[2 * U], gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
         if (p.qout.on) hn = fake_quant(hn, p.qout);
-        if (row < p.B) p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
+        if (row < p.B) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = hn;
         *hkp = hn;
         if (t + 1 < p.T) {
           const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
-          uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + row) * H + unit;
+          uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * H + lane_xh;
           if (t >= 1 && flags[1] != 0)
             st_tagged_xcd(dst, hq, base + (uint32_t)t + 1u);
           else
@@ -214,7 +216,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       }
       lds_barrier();  // the compute waves' phase-1/phase-2 barrier
       if (more) {
-        float* hs = hst + (nx & 1) * 4 * p.rsh + pr * p.rsh;
+        float* hs = hst + (nx & 1) * p.hsz;
         if (t2 == 0) {
           for (int k = lane; k < H; k += 64) {
             float v = 0.0f;
@@ -222,7 +224,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
               v = p.h0[(int64_t)row * p.sh0_b + k];
               if (p.qin.on) v = fake_quant(v, p.qin);
             }
-            hs[k] = v;
+            hs[il_index(pr, k)] = v;
           }
         } else {
           if (pr == 0 && nx == nrbm)  // first exchange of the launch
@@ -230,12 +232,13 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
           wait_lds_count(p.ctrl, &flags[0], nwc * (it + 1));
           const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * H;
           const uint32_t tag = base + (uint32_t)t2;
-          // H words of the row in chunks of 512 (lane k = lane + 64 m)
+          // H words of row pr in chunks of 512 (a chunk starting at k0 fills
+          // the interleaved block from il_index(0, k0) = 4 k0)
           if (H <= 256) {
-            poll_rows<1, 4>(p.ctrl, hb, 0, hs, 0, H, tag);
+            poll_row_il<4>(p.ctrl, hb, hs, pr, H, tag);
           } else {
             for (int k0 = 0; k0 < H; k0 += 512)
-              poll_rows<1, 8>(p.ctrl, hb + k0, 0, hs + k0, 0, min(512, H - k0), tag);
+              poll_row_il<8>(p.ctrl, hb + k0, hs + 4 * k0, pr, min(512, H - k0), tag);
           }
         }
         float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
@@ -457,7 +460,7 @@ int plan_m2(const gs_args* a, M2Plan* pl, const char* who) {
 typedef void (*M2FFn)(M2FParams);
 
 struct M2FPlan {
-  int QW, nt, nwc, nrb, Bp, rsh, rsz;
+  int QW, nt, nwc, nrb, Bp, hsz;
   int64_t xh_bytes, xw_bytes;
   M2FFn fn;
 };
@@ -479,8 +482,8 @@ bool plan_fused(const gs_args* a, M2FPlan* pl) {
   }
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
-  pl->rsh = H + 68;  // phase-1 operand reads run up to 63 words past a block start
-  pl->rsz = 68;
+  // phase-1 operand reads cover 64 k from a block start: up to 64 - bs past H
+  pl->hsz = 4 * H + 256;
   // pollers load up to 511 words past the last chunk start of a row
   pl->xh_bytes = align256(2 * (int64_t)pl->Bp * H * 8 + 512 * 8);
   pl->xw_bytes = align256((int64_t)pl->nrb * nb * 8);
@@ -496,7 +499,7 @@ int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const cha
   for (int pass = 0; pass < 2; ++pass) {
     RB = (pl.nrb + G - 1) / G;
     G = (pl.nrb + RB - 1) / RB;
-    lds = sizeof(float) * (size_t)(8 * pl.rsh + 12 * pl.rsz + RB * 4 * U + 24 * U + 4);
+    lds = sizeof(float) * (size_t)(2 * pl.hsz + 3 * 256 + RB * 4 * U + 24 * U + 4);
     if (lds > 65536)
       GS_CHECK_HIP(hipFuncSetAttribute((const void*)pl.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     int gfit = 0;
@@ -534,8 +537,7 @@ int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const cha
   p.Bp = pl.Bp;
   p.nwg = G * nb;
   p.nwc = pl.nwc;
-  p.rsh = pl.rsh;
-  p.rsz = pl.rsz;
+  p.hsz = pl.hsz;
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
   p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
