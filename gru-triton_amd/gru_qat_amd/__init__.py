@@ -23,6 +23,7 @@ from .scan_butterfly import (
 from .scan_diagonal import extract_diagonal_factors, gru_scan_diagonal, gru_scan_diagonal_forward
 from .scan_monarch import extract_monarch_factors, gru_scan_monarch, gru_scan_monarch_forward
 from ._lib import load as load_library, workspace_faults
+from .gru_layer import fast_dispatch_eligible, forward_fast_dispatch, resolve_use_triton
 
 __all__ = [
     "GRUScanFunction",
@@ -30,6 +31,8 @@ __all__ = [
     "extract_butterfly_twiddles",
     "extract_diagonal_factors",
     "extract_monarch_factors",
+    "fast_dispatch_eligible",
+    "forward_fast_dispatch",
     "gru_scan",
     "gru_scan_butterfly_forward",
     "gru_scan_butterfly_persistent",
@@ -42,5 +45,6 @@ __all__ = [
     "gru_scan_monarch_forward",
     "gru_scan_persistent",
     "load_library",
+    "resolve_use_triton",
     "workspace_faults",
 ]

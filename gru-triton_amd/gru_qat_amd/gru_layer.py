@@ -1,0 +1,130 @@
+"""Scan dispatch of the reference ``GRULayer`` (LarocheC/gru-triton
+src/gru_qat/gru_layer.py), restated around this build's scans.
+
+The reference layer sends a forward to ``_forward_fast_dispatch``
+(gru_layer.py:234-302) when ``use_triton`` resolves to True
+(gru_layer.py:110-124): the input projection builds ``gi [T, B, 3H]`` and one
+scan entry point consumes it with the hidden quantizers' frozen parameters.
+This module keeps the parts of that path that decide and feed the scan:
+
+* ``_extract_h_quant_params`` -- gru_layer.py:30-48;
+* ``fast_dispatch_eligible`` and ``resolve_use_triton`` -- the eligibility
+  rule and the ``use_triton`` argument contract of gru_layer.py:110-124;
+* ``forward_fast_dispatch`` -- gru_layer.py:183-192 (T/B checks, zero h0)
+  and :260-302 (kind switch, ``h_T = out[-1]`` taken before the batch_first
+  transpose).
+
+The cell, quantizer modules, calibration and the input projection that
+produces ``gi`` are not part of this build; callers pass ``gi`` and the
+extracted hidden weights (``extract_*`` helpers of the scan modules).
+"""
+
+from __future__ import annotations
+
+from typing import Any, Optional, Tuple
+
+import torch
+
+from ._common import QuantTuple
+
+FAST_DISPATCH_KINDS = ("diagonal", "monarch", "butterfly")
+
+
+def _extract_h_quant_params(quantizer: Any) -> QuantTuple:
+    """``(scale, qmin, qmax)`` of a frozen, per-tensor, symmetric quantizer,
+    else None (the scan then runs without in-kernel fake-quant).
+
+    Mirrors gru_layer.py:30-48. The reference tests
+    ``isinstance(quantizer, FakeQuantizePerTensor)``; the quantizer classes
+    are not part of this build, so per-tensor is read from the quantizer's
+    config (``config.axis is None``, the reference's per-tensor config) and a
+    one-element scale. Like the reference, this reads the scale with
+    ``.item()`` (a device-to-host sync for a device scale).
+    """
+    cfg = quantizer.config
+    if cfg.mode != "frozen":
+        return None
+    if getattr(cfg, "axis", None) is not None or quantizer.scale.numel() != 1:
+        return None
+    if not cfg.symmetric:
+        return None
+    return (float(quantizer.scale.item()), int(quantizer.qmin), int(quantizer.qmax))
+
+
+def fast_dispatch_eligible(kind: Optional[str], gate_layout: str) -> bool:
+    """gru_layer.py:110-113: the hidden structure kind is diagonal, monarch or
+    butterfly and the gate layout is fused (gi is one [T, B, 3H] tensor)."""
+    return kind in FAST_DISPATCH_KINDS and gate_layout == "fused"
+
+
+def resolve_use_triton(use_triton: Any, kind: Optional[str], gate_layout: str) -> bool:
+    """gru_layer.py:115-124: "auto" follows eligibility; a truthy value on an
+    ineligible configuration raises ValueError; falsy disables dispatch."""
+    eligible = fast_dispatch_eligible(kind, gate_layout)
+    if use_triton == "auto":
+        return eligible
+    use = bool(use_triton)
+    if use and not eligible:
+        raise ValueError(
+            "use_triton=True requires structure_hidden.kind in {'diagonal', 'monarch', 'butterfly'} "
+            "and gate_layout='fused'."
+        )
+    return use
+
+
+def forward_fast_dispatch(
+    kind: str,
+    gi: torch.Tensor,
+    h0: Optional[torch.Tensor],
+    hidden: torch.Tensor,
+    bh_cat: torch.Tensor,
+    *,
+    h_in_quant: QuantTuple = None,
+    h_out_quant: QuantTuple = None,
+    batch_first: bool = False,
+    hidden2: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Runs the scan of ``kind`` on ``gi [T, B, 3H]`` (time-major, as the
+    reference builds it after its batch_first transpose) and returns
+    ``(out, h_T)``: out is [T, B, H], or [B, T, H] when ``batch_first``;
+    h_T = out[-1] of the time-major result.
+
+    ``hidden`` is Wh_diag [3, H] (diagonal), Wh_struct [3, nb, bs, bs]
+    (monarch; ``hidden2`` the optional second factor), twiddles (butterfly),
+    or Wh_cat [3H, H] for kind "dense", which this build adds (the reference
+    routes dense hidden weights to its per-step loop). ``h0`` None means
+    zeros, as in gru_layer.py:191-192. An unknown kind raises RuntimeError
+    (gru_layer.py:294-297).
+    """
+    if gi.dim() != 3:
+        raise ValueError(f"gi must be [T, B, 3H]; got shape {tuple(gi.shape)}")
+    T, B, threeH = gi.shape
+    if T == 0:
+        raise ValueError(f"seq length T must be > 0; got T={T}")
+    if B == 0:
+        raise ValueError(f"batch size B must be > 0; got B={B}")
+    if h0 is None:
+        h0 = gi.new_zeros(B, threeH // 3)
+    kw = dict(h_in_quant=h_in_quant, h_out_quant=h_out_quant)
+    if kind == "diagonal":
+        from .scan_diagonal import gru_scan_diagonal
+
+        out = gru_scan_diagonal(gi, h0, hidden, bh_cat, **kw)
+    elif kind == "monarch":
+        from .scan_monarch import gru_scan_monarch
+
+        out = gru_scan_monarch(gi, h0, hidden, bh_cat, Wh_struct2=hidden2, **kw)
+    elif kind == "butterfly":
+        from .scan_butterfly import gru_scan_butterfly_triton
+
+        out = gru_scan_butterfly_triton(gi, h0, hidden, bh_cat, **kw)
+    elif kind == "dense":
+        from .scan import gru_scan_persistent
+
+        out = gru_scan_persistent(gi, h0, hidden, bh_cat, **kw)
+    else:
+        raise RuntimeError(f"unexpected dispatch kind {kind!r}")
+    h_T = out[-1]
+    if batch_first:
+        out = out.transpose(0, 1)
+    return out, h_T
