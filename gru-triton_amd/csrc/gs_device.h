@@ -83,6 +83,44 @@ __device__ __forceinline__ float lane_xor(float x, int m) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ m) << 2, __float_as_int(x)));
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// x[l ^ M] for M in {1, 2, 4, 8, 16, 32} with VALU lane moves instead of an
+// LDS permute: quad permutes for 1 and 2; for 4, the half-row mirror
+// (l -> l ^ 7 inside 8 lanes) followed by the quad reversal (l -> l ^ 3);
+// for 8, a row rotation by 8 (either direction); for 16 and 32, the gfx950
+// row swaps, whose two results hold the partner row in odd and even rows
+// respectively (see sum_across_rows).
+template <int M>
+__device__ __forceinline__ float lane_xor_c(float x) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane_xor_c stride");
+  if constexpr (M == 1) {
+    return dpp_mov<0xB1>(x);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (M == 2) {
+    return dpp_mov<0x4E>(x);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (M == 4) {
+    return dpp_mov<0x1B>(dpp_mov<0x141>(x));  // row_half_mirror, then quad_perm [3, 2, 1, 0]
+  } else if constexpr (M == 8) {
+    return dpp_mov<0x128>(x);  // row_ror:8
+  } else {
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    const u2 a = (M == 16) ? __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false)
+                           : __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((__lane_id() & M) ? a[0] : a[1]);
+  }
+}
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS
+// operations, then s_barrier. Unlike __syncthreads it does not wait for the
+// wave's global stores, whose acknowledgement (for coherent stores, a round
+// trip to the device coherence point) would otherwise sit on the critical path.
+// The asm memory clobber keeps the compiler from moving memory operations
+// across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // x[l] + x[l ^ 16] + x[l ^ 32] + x[l ^ 48] in every lane, with gfx950's VALU
 // row swaps: permlane16_swap(x, x) returns (x with odd rows replaced by the
 // even rows below them, x with even rows replaced by the odd rows above

@@ -150,13 +150,6 @@ __device__ __forceinline__ void mfma3(const float (&a)[3][KC], const float (&wr)
   for (int g = 0; g < 3; ++g) acc[g] = acc0[g] + acc1[g];
 }
 
-// Workgroup barrier that orders LDS only: waits for this wave's LDS
-// operations, then s_barrier. Unlike __syncthreads it does not wait for the
-// wave's global stores, whose acknowledgement (for coherent stores, a round
-// trip to the device coherence point) would otherwise sit on the critical path.
-// The asm memory clobber keeps the compiler from moving memory operations
-// across it.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ---- host side --------------------------------------------------------------------
 

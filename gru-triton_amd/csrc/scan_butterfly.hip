@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kGenericThreads) void butterfly_generic_kernel(BPar
     buf0[N + i] = hq;
     buf0[2 * N + i] = hq;
   }
-  __syncthreads();
+  lds_barrier();
 
   float* cur = buf0;
   float* nxt = buf1;
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(kGenericThreads) void butterfly_generic_kernel(BPar
           const float tsp = p.tw[base + 1 - m];
           nxt[g * N + i] = tss * cur[g * N + i] + tsp * cur[g * N + (i ^ stride)];
         }
-        __syncthreads();
+        lds_barrier();
         float* tmp = cur;
         cur = nxt;
         nxt = tmp;
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kGenericThreads) void butterfly_generic_kernel(BPar
       nxt[N + i] = hq;
       nxt[2 * N + i] = hq;
     }
-    __syncthreads();
+    lds_barrier();
     float* tmp = cur;
     cur = nxt;
     nxt = tmp;
@@ -117,9 +117,13 @@ __global__ __launch_bounds__(kGenericThreads) void butterfly_generic_kernel(BPar
 // Register kernel: one chain, N in {256, 512, 1024}. Each gate's vector is
 // spread over WPG = N/256 waves; lane l of gate wave w holds elements
 // i = l + 64*r + 256*w for r = 0..3. Stages with stride < 64 swap across
-// lanes, strides 64 and 128 pair registers inside a lane, strides >= 256 go
-// through LDS between the gate's waves. Each lane keeps the two twiddles of
-// each of its 4 elements for all L stages in registers (8L values), loaded
+// lanes: strides 1, 2, 4 and 8 with DPP moves that fold into the multiply
+// (stride 4 needs one extra move), 16 and 32 with ds_bpermute, which keeps
+// them off the VALU, the bound at three waves per SIMD (moving them to the
+// permlane swaps measured 5 % slower). Strides 64 and 128 pair registers
+// inside a lane, strides >= 256 go through LDS between the gate's waves.
+// Each lane keeps the two twiddles of each of its 4 elements for all L stages
+// in registers (8L values), loaded
 // once. The gate epilogue for element i runs on the gate-r wave that holds i,
 // which reads gh_z and gh_n from LDS and broadcasts the next q_in(h) back.
 // ---------------------------------------------------------------------------------
@@ -184,31 +188,37 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
       }
     }
     int xsel = 0;
-#pragma unroll
-    for (int s = 0; s < L; ++s) {
+    static_for<0, L>([&](auto S) {
+      constexpr int s = S;
       float y[4];
-      if (s < 6) {
+      if constexpr (s <= 3) {
+        // strides 1, 2, 4, 8: DPP lane moves (one folds into the multiply)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = lane_xor_c<1 << s>(x[r]);
+      } else if constexpr (s < 6) {
+        // strides 16, 32: through the LDS crossbar, which keeps these moves
+        // off the VALU (the kernel's bound at three waves per SIMD)
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = lane_xor(x[r], 1 << s);
-      } else if (s < 8) {
+      } else if constexpr (s < 8) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = x[r ^ (1 << (s - 6))];
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) xch[xsel][g][idx[r]] = x[r];
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = xch[xsel][g][idx[r] ^ (1 << s)];
         xsel ^= 1;
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] = tss[s][r] * x[r] + tsp[s][r] * y[r];
-    }
+    });
     if (g != 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) ghs[g][idx[r]] = x[r];
     }
-    __syncthreads();
+    lds_barrier();
     if (g == 0) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -227,7 +237,7 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
         hqs[i] = hq;
       }
     }
-    __syncthreads();
+    lds_barrier();
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[r] = hqs[idx[r]];
   }
