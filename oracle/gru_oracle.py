@@ -19,8 +19,14 @@ Functions and what they follow (reference file:line):
                    direction per chain, pair index and twiddle element selection)
   scan             the T-step loops of scan_diagonal.py:79-124 / scan_monarch.py:74-127 /
                    gru_layer.py:212-223
+  scan_backward    triton_kernels/scan.py:1450-1550 (_fake_quant and the recompute-based
+                   _gru_scan_backward_pytorch): reverse walk, gates recomputed from
+                   out[t-1], clipped-STE masks on q_out and q_in, dW accumulated against hq
+  scan_ste         the forward with ste.py:17-95's STERound/STEClamp gradients, the
+                   independent derivation scan_backward is pinned against (autograd)
 
-Pins (tests/test_oracle.py): round-half-even and clipping known answers
+Pins (tests/test_oracle.py; the backward in tests/test_oracle_backward.py
+against torch.autograd through scan_ste, in float64): round-half-even and clipping known answers
 (tests/test_ste.py:12-61 of the reference), an exhaustive boundary sweep of
 fake_quant against exact rational arithmetic, nn.GRUCell closed forms for the
 dense, diagonal and Monarch maps (weight_ih = I, weight_hh = the materialised
@@ -210,3 +216,147 @@ def materialize_hidden(cfg: dict) -> torch.Tensor:
     cz = dict(c)
     cz["bh"] = zero_b
     return gh_fn_for(cz)(eye).t().contiguous()
+
+
+# ---- backward ---------------------------------------------------------------------
+
+def fake_quant_mask(x: torch.Tensor, q: Tuple[float, int, int]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Forward fake-quant and the clipped-STE mask (scan.py:1450-1457):
+    mask = round(x / s) inside [qmin, qmax]."""
+    scale, qmin, qmax = q
+    s = torch.tensor(scale, dtype=x.dtype)
+    qu = torch.round(x / s)
+    mask = (qu >= qmin) & (qu <= qmax)
+    return qu.clamp(qmin, qmax) * s, mask
+
+
+class _FakeQuantSTE(torch.autograd.Function):
+    """fake_quant with the reference's gradient: STERound is the identity and
+    STEClamp passes the gradient where round(x / s) lies in [qmin, qmax]
+    (ste.py:17-63), so d out / d x = mask."""
+
+    @staticmethod
+    def forward(ctx, x, scale, qmin, qmax):  # type: ignore[override]
+        xq, mask = fake_quant_mask(x, (scale, qmin, qmax))
+        ctx.save_for_backward(mask)
+        return xq
+
+    @staticmethod
+    def backward(ctx, g):  # type: ignore[override]
+        (mask,) = ctx.saved_tensors
+        return g * mask, None, None, None
+
+
+def fake_quant_ste(x: torch.Tensor, q: QuantTuple) -> torch.Tensor:
+    return x if q is None else _FakeQuantSTE.apply(x, *q)
+
+
+def hidden_params(cfg: dict) -> Tuple[str, ...]:
+    """Keys of the hidden-map parameters of a config (w, and w2 for two-factor Monarch)."""
+    return ("w", "w2") if cfg.get("w2") is not None else ("w",)
+
+
+def gh_map_nobias(cfg: dict) -> Callable[..., torch.Tensor]:
+    """The hidden map without bias as a function of (hq, *params) for the keys
+    of hidden_params(cfg); differentiable in every argument."""
+    kind = cfg["kind"]
+    if kind == "dense":
+        return lambda hq, w: hq @ w.t()
+    if kind == "diagonal":
+        return lambda hq, w: (w.unsqueeze(1) * hq.unsqueeze(0)).permute(1, 0, 2).reshape(hq.shape[0], -1)
+    if kind == "monarch":
+        zero = torch.zeros(3 * cfg["h0"].shape[-1], dtype=cfg["gi"].dtype)
+        if cfg.get("w2") is not None:
+            return lambda hq, w, w2: gh_monarch2(hq, w, w2, zero)
+        return lambda hq, w: gh_monarch(hq, w, zero)
+    if kind == "butterfly":
+        zero = torch.zeros(3 * cfg["h0"].shape[-1], dtype=cfg["gi"].dtype)
+        return lambda hq, w: gh_butterfly(hq, w, zero)
+    raise ValueError(kind)
+
+
+def scan_ste(cfg: dict) -> torch.Tensor:
+    """Differentiable forward (STE on both quantizers): the autograd pin for
+    scan_backward. cfg tensors may require grad."""
+    gi, h0, bh = cfg["gi"], cfg["h0"], cfg["bh"]
+    params = [cfg[k] for k in hidden_params(cfg)]
+    gmap = gh_map_nobias(cfg)
+    qin, qout = cfg.get("h_in_quant"), cfg.get("h_out_quant")
+    h = h0
+    outs = []
+    for t in range(gi.shape[0]):
+        hq = fake_quant_ste(h, qin)
+        h_new = gru_step(gi[t], h, gmap(hq, *params) + bh)
+        h = fake_quant_ste(h_new, qout)
+        outs.append(h)
+    return torch.stack(outs, dim=0)
+
+
+def scan_backward(cfg: dict, out: torch.Tensor, dout: torch.Tensor, _mutation: str = "") -> dict:
+    """Restates _gru_scan_backward_pytorch (scan.py:1460-1550) for every hidden
+    kind: walk t from T-1 to 0, recompute the gates from h_{t-1} = out[t-1]
+    (h0 at t = 0), push dout[t] plus the carried gradient through q_out's mask,
+    the gate derivatives and the hidden map, and carry
+    dh_{t-1} = dh_t * z + mask_in * (d gh / d hq)^T dgh. The hidden map's
+    vector-Jacobian products (with respect to hq and to its parameters) come
+    from autograd on the map, which for the dense kind are dgh @ Wh_cat and
+    dgh^T @ hq exactly as in the reference.
+
+    Returns {"dgi", "dh0", "dbh", "d<param key>" ...}; CPU tensors.
+    ``_mutation`` plants a known mistake for the tests that show the autograd
+    pin catches it: "dgh_n_without_r" or "ignore_mask_in".
+    """
+    c = _cpu(cfg)
+    gi, h0, bh = c["gi"], c["h0"], c["bh"]
+    out = out.detach().cpu()
+    dout = dout.detach().cpu()
+    keys = hidden_params(c)
+    params = [c[k] for k in keys]
+    gmap = gh_map_nobias(c)
+    qin, qout = c.get("h_in_quant"), c.get("h_out_quant")
+    T = gi.shape[0]
+    H = h0.shape[-1]
+    dgi = torch.zeros_like(gi)
+    dparams = [torch.zeros_like(p) for p in params]
+    dbh = torch.zeros_like(bh)
+    dh_acc = torch.zeros_like(h0)
+    for t in reversed(range(T)):
+        h_prev = h0 if t == 0 else out[t - 1]
+        if qin is not None:
+            hq, mask_in = fake_quant_mask(h_prev, qin)
+        else:
+            hq, mask_in = h_prev, None
+        with torch.enable_grad():
+            hq_req = hq.detach().requires_grad_(True)
+            p_req = [p.detach().requires_grad_(True) for p in params]
+            gh_nob = gmap(hq_req, *p_req)
+        gh = gh_nob.detach() + bh
+        gi_r, gi_z, gi_n = gi[t].split(H, dim=-1)
+        gh_r, gh_z, gh_n = gh.split(H, dim=-1)
+        r = torch.sigmoid(gi_r + gh_r)
+        z = torch.sigmoid(gi_z + gh_z)
+        n = torch.tanh(gi_n + r * gh_n)
+        h_raw = (1.0 - z) * n + z * h_prev
+        dh_t = dout[t] + dh_acc
+        if qout is not None:
+            dh_t = dh_t * fake_quant_mask(h_raw, qout)[1]
+        dn = dh_t * (1.0 - z)
+        dz = dh_t * (h_prev - n)
+        dh_direct = dh_t * z
+        dgn = dn * (1.0 - n * n)
+        dr = dgn * gh_n
+        dgh_n = dgn if _mutation == "dgh_n_without_r" else dgn * r
+        dgz = dz * z * (1.0 - z)
+        dgr = dr * r * (1.0 - r)
+        dgi[t] = torch.cat([dgr, dgz, dgn], dim=-1)
+        dgh = torch.cat([dgr, dgz, dgh_n], dim=-1)
+        grads = torch.autograd.grad(gh_nob, [hq_req] + p_req, dgh)
+        dh_via = grads[0] if (mask_in is None or _mutation == "ignore_mask_in") else grads[0] * mask_in
+        for acc, g in zip(dparams, grads[1:]):
+            acc += g
+        dbh += dgh.sum(dim=0)
+        dh_acc = dh_direct + dh_via
+    res = {"dgi": dgi, "dh0": dh_acc, "dbh": dbh}
+    for k, d in zip(keys, dparams):
+        res["d" + k] = d
+    return res

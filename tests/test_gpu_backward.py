@@ -1,0 +1,71 @@
+"""Backward of the differentiable scan entry points on the GPU against the
+oracle's restatement of the reference backward (scan.py:1450-1550), computed
+from the kernel's own forward output so that both walk the same trajectory.
+
+Bar: every gradient within 1e-4 x max(1, max |oracle|) (fp32 recomputation of
+the gates on the device vs the CPU, accumulated over T steps)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gru_qat_amd.configs import Q_INT8_HIDDEN, make_config
+from oracle import gru_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+COARSE = (0.05, -10, 10)
+
+
+def _cfg(idx, shape, nb=None, two=False, q=None, seed=0):
+    cfg = make_config(idx, shape=shape, seed=seed)
+    T, B, H = shape
+    if idx == 3:
+        g = torch.Generator().manual_seed(seed + 7)
+        bs = H // nb
+        cfg["w"] = (torch.rand((3, nb, bs, bs), generator=g) * 2 - 1) / bs ** 0.5
+        cfg["w2"] = ((torch.rand((3, nb, bs, bs), generator=g) * 2 - 1) / bs ** 0.5) if two else None
+    cfg["h0"] = torch.randn(B, H, generator=torch.Generator().manual_seed(seed + 3)) * 0.3
+    cfg["h_in_quant"] = q
+    cfg["h_out_quant"] = q
+    return cfg
+
+
+def _run(cfg, dev, leaves):
+    import gru_qat_amd as G
+
+    kw = dict(h_in_quant=cfg["h_in_quant"], h_out_quant=cfg["h_out_quant"])
+    kind = cfg["kind"]
+    if kind == "dense":
+        return G.gru_scan_persistent(leaves["gi"], leaves["h0"], leaves["w"], leaves["bh"], **kw)
+    if kind == "diagonal":
+        return G.gru_scan_diagonal(leaves["gi"], leaves["h0"], leaves["w"], leaves["bh"], **kw)
+    if kind == "monarch":
+        return G.gru_scan_monarch(leaves["gi"], leaves["h0"], leaves["w"], leaves["bh"],
+                                  Wh_struct2=leaves.get("w2"), **kw)
+    return G.gru_scan_butterfly_triton(leaves["gi"], leaves["h0"], leaves["w"], leaves["bh"], **kw)
+
+
+CASES = [
+    (1, (8, 5, 64), None, False), (1, (6, 4, 300), None, False), (0, (8, 5, 64), None, False),
+    (3, (6, 4, 64), 4, False), (3, (6, 4, 64), 4, True), (4, (5, 3, 256), None, False),
+    (4, (5, 3, 100), None, False),
+]
+
+
+@pytest.mark.parametrize("idx,shape,nb,two", CASES)
+@pytest.mark.parametrize("q", [None, COARSE, Q_INT8_HIDDEN])
+def test_backward_matches_oracle(dev, idx, shape, nb, two, q):
+    cfg = _cfg(idx, shape, nb=nb, two=two, q=q)
+    keys = ["gi", "h0", "bh"] + list(O.hidden_params(cfg))
+    leaves = {k: cfg[k].to(dev).requires_grad_(True) for k in keys}
+    out = _run(cfg, dev, leaves)
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(13)).to(dev)
+    grads = torch.autograd.grad(out, [leaves[k] for k in keys], dout)
+    ref = O.scan_backward(cfg, out.detach(), dout)
+    for k, g in zip(keys, grads):
+        r = ref["d" + k]
+        err = (g.cpu() - r).abs().max().item()
+        print(f"[bwd] {cfg['name']} {shape} q={q is not None} d{k}: max err {err:.3e} (|ref| {r.abs().max().item():.3e})")
+        assert err <= 1e-4 * max(1.0, r.abs().max().item()), k
