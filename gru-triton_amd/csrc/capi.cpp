@@ -57,6 +57,44 @@ int validate_common(const gs_args* a, const char* who) {
   return validate_quant(a->q_out, "h_out_quant", who);
 }
 
+gs_args fwd_view(const gs_bwd_args& a) {
+  gs_args f;
+  memset(&f, 0, sizeof f);
+  f.gi = a.gi;
+  f.h0 = a.h0;
+  f.w = a.w;
+  f.w2 = a.w2;
+  f.bh = a.bh;
+  f.out = const_cast<float*>(a.out);
+  f.workspace = a.workspace;
+  f.workspace_bytes = a.workspace_bytes;
+  f.T = a.T;
+  f.B = a.B;
+  f.H = a.H;
+  f.sg_t = a.sg_t;
+  f.sg_b = a.sg_b;
+  f.sh0_b = a.sh0_b;
+  f.so_t = a.so_t;
+  f.so_b = a.so_b;
+  f.nblocks = a.nblocks;
+  f.blksz = a.blksz;
+  f.log_n = a.log_n;
+  f.bfly_nblocks = a.bfly_nblocks;
+  f.q_in = a.q_in;
+  f.q_out = a.q_out;
+  return f;
+}
+
+int validate_bwd_common(const gs_bwd_args* a, const char* who) {
+  if (a == nullptr) return set_error(GS_ERR_INVALID, "%s: args is NULL", who);
+  const gs_args f = fwd_view(*a);
+  const int rc = validate_common(&f, who);
+  if (rc) return rc;
+  if (!a->dout || !a->dgi || !a->dh0 || !a->dbh_part)
+    return set_error(GS_ERR_INVALID, "%s: dout, dgi, dh0 and dbh_part must be non-NULL device pointers", who);
+  return GS_OK;
+}
+
 int check_workspace(const gs_args* a, int64_t need, const char* who) {
   if (need <= 0) return GS_OK;
   if (a->workspace == nullptr || a->workspace_bytes < need)

@@ -63,6 +63,42 @@ __device__ __forceinline__ float gru_update(float gir, float giz, float gin, flo
   return (1.0f - z) * n + z * h;
 }
 
+// Backward of one GRU step (reference src/gru_qat/triton_kernels/scan.py:1498-1540):
+// recomputes r, z, n from the step's inputs with the forward's arithmetic,
+// applies q_out's clipped-STE mask (round(h_raw / s) inside [qmin, qmax]) to
+// the incoming gradient, and returns the gate-input gradients dg* (dgi), the
+// n-gate hidden gradient dghn = dgn * r (dgh = (dgr, dgz, dghn)) and the
+// direct carry dh * z.
+struct GateGrad {
+  float dgr, dgz, dgn, dghn, dh_direct;
+};
+
+__device__ __forceinline__ bool quant_keeps(float x, const Quant& q) {
+  const float v = __builtin_rintf(x / q.scale);
+  return v >= q.qmin && v <= q.qmax;
+}
+
+__device__ __forceinline__ GateGrad gru_backward(float gir, float giz, float gin, float ghr, float ghz, float ghn,
+                                                 float h_prev, float dh, const Quant& qout) {
+#pragma clang fp contract(off)
+  const float r = sigmoid(gir + ghr);
+  const float z = sigmoid(giz + ghz);
+  const float n = tanh_fast(gin + r * ghn);
+  if (qout.on) {
+    const float h_raw = (1.0f - z) * n + z * h_prev;
+    if (!quant_keeps(h_raw, qout)) dh = 0.0f;
+  }
+  GateGrad gg;
+  const float dn = dh * (1.0f - z);
+  const float dz = dh * (h_prev - n);
+  gg.dh_direct = dh * z;
+  gg.dgn = dn * (1.0f - n * n);
+  gg.dghn = gg.dgn * r;
+  gg.dgz = dz * z * (1.0f - z);
+  gg.dgr = gg.dgn * ghn * r * (1.0f - r);
+  return gg;
+}
+
 // Diagonal hidden projection w * hq + b, rounded twice like torch's
 // `w_hr * h + bh` (reference scan_diagonal.py:113-115).
 __device__ __forceinline__ float mul_add_nofma(float w, float x, float b) {

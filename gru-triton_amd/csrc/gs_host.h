@@ -56,6 +56,10 @@ inline bool same_quant(const gs_quant& a, const gs_quant& b) {
 }
 
 int validate_common(const gs_args* a, const char* who);
+// gs_args view of the forward fields of a backward call.
+gs_args fwd_view(const gs_bwd_args& a);
+// validate_common on the forward fields plus the gradient pointers.
+int validate_bwd_common(const gs_bwd_args* a, const char* who);
 int validate_quant(const gs_quant& q, const char* name, const char* who);
 int check_workspace(const gs_args* a, int64_t need, const char* who);
 

@@ -92,8 +92,164 @@ __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
   }
 }
 
+// ---- backward ---------------------------------------------------------------------
+// Reference: scan_diagonal.py:285-561 (Triton backward kernel and launcher) and
+// its PyTorch restatement :564-647. Every (b, j) lane is again independent: one
+// thread walks t from T-1 to 0 carrying dh in a register, recomputes the
+// gates from h_{t-1} = out[t-1] (h0 at t = 0) with the forward's arithmetic,
+// and accumulates its lane's contribution to dWh_diag and dbh in registers;
+// the per-row partials go to dw_part / dbh_part at the end. gi, out[t-1] and
+// dout[t] of the next kDepth steps (in reverse) are in flight while the
+// current kDepth steps compute.
+struct DiagBwdParams {
+  const float* gi;
+  const float* h0;
+  const float* w;
+  const float* bh;
+  const float* out;
+  const float* dout;
+  float* dgi;
+  float* dh0;
+  float* dw_part;
+  float* dbh_part;
+  int64_t sg_t, sg_b, sh0_b, so_t, so_b;
+  int T, B, H;
+  Quant qin, qout;
+};
+
+__global__ __launch_bounds__(kThreads) void diagonal_bwd_kernel(DiagBwdParams p) {
+  const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (e >= (int64_t)p.B * p.H) return;
+  const int b = (int)(e / p.H);
+  const int j = (int)(e - (int64_t)b * p.H);
+  const int H = p.H;
+
+  const float wr = p.w[j], wz = p.w[H + j], wn = p.w[2 * H + j];
+  const float br = p.bh[j], bz = p.bh[H + j], bn = p.bh[2 * H + j];
+  const float h0 = p.h0[(int64_t)b * p.sh0_b + j];
+
+  const float* gib = p.gi + (int64_t)b * p.sg_b + j;
+  const float* outb = p.out + (int64_t)b * p.so_b + j;
+  const float* doutb = p.dout + ((int64_t)b * H + j);
+  float* dgib = p.dgi + ((int64_t)b * 3 * H + j);
+  const int64_t sd_t = (int64_t)p.B * H, sdg_t = (int64_t)p.B * 3 * H;
+
+  // step s of a chunk is t = t0 - s; loads of step t: gi[t], out[t-1] (h0 at 0), dout[t]
+  float cr[kDepth], cz[kDepth], cn[kDepth], ch[kDepth], cd[kDepth];
+  auto load = [&](int t, float& gr, float& gz, float& gn, float& hp, float& dd) {
+    const float* g = gib + (int64_t)t * p.sg_t;
+    gr = g[0];
+    gz = g[H];
+    gn = g[2 * H];
+    hp = t > 0 ? outb[(int64_t)(t - 1) * p.so_t] : h0;
+    dd = doutb[(int64_t)t * sd_t];
+  };
+#pragma unroll
+  for (int i = 0; i < kDepth; ++i)
+    if (p.T - 1 - i >= 0) load(p.T - 1 - i, cr[i], cz[i], cn[i], ch[i], cd[i]);
+
+  float dh = 0.0f;
+  float dwr = 0.f, dwz = 0.f, dwn = 0.f, dbr = 0.f, dbz = 0.f, dbn = 0.f;
+  for (int t0 = p.T - 1; t0 >= 0; t0 -= kDepth) {
+    float nr[kDepth], nz[kDepth], nn[kDepth], nh[kDepth], nd[kDepth];
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      const int t = t0 - kDepth - i;
+      if (t >= 0) load(t, nr[i], nz[i], nn[i], nh[i], nd[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      const int t = t0 - i;
+      if (t >= 0) {
+        const float h_prev = ch[i];
+        float hq = h_prev;
+        bool keep_in = true;
+        if (p.qin.on) {
+          keep_in = quant_keeps(h_prev, p.qin);
+          hq = fake_quant(h_prev, p.qin);
+        }
+        const float ghr = mul_add_nofma(wr, hq, br);
+        const float ghz = mul_add_nofma(wz, hq, bz);
+        const float ghn = mul_add_nofma(wn, hq, bn);
+        const GateGrad gg = gru_backward(cr[i], cz[i], cn[i], ghr, ghz, ghn, h_prev, cd[i] + dh, p.qout);
+        float* dg = dgib + (int64_t)t * sdg_t;
+        dg[0] = gg.dgr;
+        dg[H] = gg.dgz;
+        dg[2 * H] = gg.dgn;
+        {
+#pragma clang fp contract(off)
+          float via = gg.dgr * wr + gg.dgz * wz + gg.dghn * wn;
+          if (!keep_in) via = 0.0f;
+          dh = gg.dh_direct + via;
+          dwr += gg.dgr * hq;
+          dwz += gg.dgz * hq;
+          dwn += gg.dghn * hq;
+          dbr += gg.dgr;
+          dbz += gg.dgz;
+          dbn += gg.dghn;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      cr[i] = nr[i];
+      cz[i] = nz[i];
+      cn[i] = nn[i];
+      ch[i] = nh[i];
+      cd[i] = nd[i];
+    }
+  }
+  p.dh0[(int64_t)b * H + j] = dh;
+  float* dwp = p.dw_part + (int64_t)b * 3 * H + j;
+  dwp[0] = dwr;
+  dwp[H] = dwz;
+  dwp[2 * H] = dwn;
+  float* dbp = p.dbh_part + (int64_t)b * 3 * H + j;
+  dbp[0] = dbr;
+  dbp[H] = dbz;
+  dbp[2 * H] = dbn;
+}
+
 }  // namespace
 }  // namespace gs
+
+extern "C" int gs_diagonal_bwd(const gs_bwd_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_diagonal_bwd";
+  int rc = validate_bwd_common(a, who);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the diagonal kind", who);
+  if (a->dw_part == nullptr) return set_error(GS_ERR_INVALID, "%s: dw_part must be a non-NULL device pointer", who);
+
+  DiagBwdParams p;
+  p.gi = a->gi;
+  p.h0 = a->h0;
+  p.w = a->w;
+  p.bh = a->bh;
+  p.out = a->out;
+  p.dout = a->dout;
+  p.dgi = a->dgi;
+  p.dh0 = a->dh0;
+  p.dw_part = a->dw_part;
+  p.dbh_part = a->dbh_part;
+  p.sg_t = a->sg_t;
+  p.sg_b = a->sg_b;
+  p.sh0_b = a->sh0_b;
+  p.so_t = a->so_t;
+  p.so_b = a->so_b;
+  p.T = (int)a->T;
+  p.B = (int)a->B;
+  p.H = (int)a->H;
+  p.qin = to_quant(a->q_in);
+  p.qout = to_quant(a->q_out);
+
+  const int64_t n = a->B * a->H;
+  const dim3 grid((unsigned)((n + kThreads - 1) / kThreads));
+  hipLaunchKernelGGL(diagonal_bwd_kernel, grid, dim3(kThreads), 0, stream, p);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
 
 extern "C" int gs_diagonal_fwd(const gs_args* a, hipStream_t stream) {
   using namespace gs;

@@ -33,6 +33,7 @@ EXPORTS = (
     "gs_monarch_fwd",
     "gs_butterfly_fwd",
     "gs_butterfly_fwd_generic",
+    "gs_diagonal_bwd",
     "gs_workspace_bytes",
     "gs_workspace_status",
     "gs_last_error",
@@ -80,6 +81,38 @@ class GsArgs(ctypes.Structure):
     ]
 
 
+class GsBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("gi", ctypes.c_void_p),
+        ("h0", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("bh", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("dout", ctypes.c_void_p),
+        ("dgi", ctypes.c_void_p),
+        ("dh0", ctypes.c_void_p),
+        ("dw_part", ctypes.c_void_p),
+        ("dbh_part", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
+        ("T", ctypes.c_int64),
+        ("B", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("sg_t", ctypes.c_int64),
+        ("sg_b", ctypes.c_int64),
+        ("sh0_b", ctypes.c_int64),
+        ("so_t", ctypes.c_int64),
+        ("so_b", ctypes.c_int64),
+        ("nblocks", ctypes.c_int64),
+        ("blksz", ctypes.c_int64),
+        ("log_n", ctypes.c_int64),
+        ("bfly_nblocks", ctypes.c_int64),
+        ("q_in", GsQuant),
+        ("q_out", GsQuant),
+    ]
+
+
 _lib = None
 _lib_lock = threading.Lock()
 
@@ -102,6 +135,10 @@ def load() -> ctypes.CDLL:
                      "gs_butterfly_fwd_generic"):
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(GsArgs), ctypes.c_void_p]
+            fn.restype = ctypes.c_int
+        for name in ("gs_diagonal_bwd",):
+            fn = getattr(lib, name)
+            fn.argtypes = [ctypes.POINTER(GsBwdArgs), ctypes.c_void_p]
             fn.restype = ctypes.c_int
         lib.gs_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsArgs)]
         lib.gs_workspace_bytes.restype = ctypes.c_int64
@@ -225,5 +262,36 @@ def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: to
         ws = workspace(gi.device, handle, int(need), steps=T if tagged else 0)
         a.workspace = ws.data_ptr()
         a.workspace_bytes = ws.numel()
+        rc = getattr(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
+    raise_for(rc, lib)
+
+
+def launch_bwd(fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,
+               w2: Optional[torch.Tensor], bh: torch.Tensor, out: torch.Tensor, dout: torch.Tensor,
+               dgi: torch.Tensor, dh0: torch.Tensor, dw_part: Optional[torch.Tensor],
+               dbh_part: torch.Tensor, h_in_quant: QuantTuple, h_out_quant: QuantTuple,
+               nblocks: int = 0, blksz: int = 0, log_n: int = 0, bfly_nblocks: int = 0) -> None:
+    """Fill gs_bwd_args from fp32 device tensors (dout, dgi, dh0 and the
+    partials contiguous) and call a backward entry point on the current torch
+    stream of gi's device."""
+    lib = load()
+    T, B, threeH = gi.shape
+    a = GsBwdArgs()
+    a.gi, a.h0, a.w = gi.data_ptr(), h0.data_ptr(), w.data_ptr()
+    a.w2 = w2.data_ptr() if w2 is not None else None
+    a.bh, a.out, a.dout = bh.data_ptr(), out.data_ptr(), dout.data_ptr()
+    a.dgi, a.dh0 = dgi.data_ptr(), dh0.data_ptr()
+    a.dw_part = dw_part.data_ptr() if dw_part is not None else None
+    a.dbh_part = dbh_part.data_ptr()
+    a.T, a.B, a.H = T, B, threeH // 3
+    a.sg_t, a.sg_b = gi.stride(0), gi.stride(1)
+    a.sh0_b = h0.stride(0)
+    a.so_t, a.so_b = out.stride(0), out.stride(1)
+    a.nblocks, a.blksz = nblocks, blksz
+    a.log_n, a.bfly_nblocks = log_n, bfly_nblocks
+    a.q_in = make_quant(h_in_quant, "h_in_quant")
+    a.q_out = make_quant(h_out_quant, "h_out_quant")
+    with torch.cuda.device(gi.device):
+        handle = torch.cuda.current_stream(gi.device).cuda_stream
         rc = getattr(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
     raise_for(rc, lib)

@@ -14,7 +14,6 @@ from typing import Any, Tuple, cast
 import torch
 
 from . import _lib
-from ._backward import scan_backward
 from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
 
 
@@ -60,14 +59,33 @@ def gru_scan_diagonal_forward(
 gru_scan_diagonal_forward_triton = gru_scan_diagonal_forward
 
 
-def _diag_gh(hq: torch.Tensor, Wh_diag: torch.Tensor) -> torch.Tensor:
-    return torch.cat([hq * Wh_diag[0], hq * Wh_diag[1], hq * Wh_diag[2]], dim=-1)
-
-
 def gru_scan_diagonal_backward(gi, h0, Wh_diag, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None):
-    dgi, dh0, (dW,), dbh = scan_backward(gi, h0, out, dout, _diag_gh, [Wh_diag], bh_cat,
-                                         h_in_quant, h_out_quant)
-    return dgi, dh0, dW, dbh
+    """Gradients (dgi, dh0, dWh_diag, dbh_cat) of the diagonal scan.
+
+    Mirrors the reference's backward launcher (scan_diagonal.py:285-561):
+    ``gs_diagonal_bwd`` walks t in reverse per (b, j) and writes dgi, dh0 and
+    per-row partials of dWh_diag [B, 3, H] and dbh [B, 3H]; the partials are
+    summed over B here.
+    """
+    who = "gru_scan_diagonal_backward"
+    require_cuda(who, gi=gi, h0=h0, Wh_diag=Wh_diag, bh_cat=bh_cat, out=out, dout=dout)
+    require_f32(who, gi=gi, h0=h0, Wh_diag=Wh_diag, bh_cat=bh_cat, out=out, dout=dout)
+    T, B, H = check_common(who, gi, h0, bh_cat)
+    if tuple(out.shape) != (T, B, H) or tuple(dout.shape) != (T, B, H):
+        raise ValueError(f"out and dout must be (T, B, H)=({T}, {B}, {H})")
+    if tuple(Wh_diag.shape) != (3, H):
+        raise ValueError(f"Wh_diag shape must be (3, H)=(3, {H}); got {tuple(Wh_diag.shape)}")
+    gi, h0, out = gi.contiguous(), h0.contiguous(), out.contiguous()
+    Wh_diag, bh_cat, dout = Wh_diag.contiguous(), bh_cat.contiguous(), dout.contiguous()
+    dgi = torch.empty((T, B, 3 * H), device=gi.device, dtype=gi.dtype)
+    dh0 = torch.empty((B, H), device=gi.device, dtype=gi.dtype)
+    dw_part = torch.empty((B, 3, H), device=gi.device, dtype=gi.dtype)
+    dbh_part = torch.empty((B, 3 * H), device=gi.device, dtype=gi.dtype)
+    _lib.launch_bwd("gs_diagonal_bwd", gi=gi, h0=h0, w=Wh_diag, w2=None, bh=bh_cat, out=out, dout=dout,
+                    dgi=dgi, dh0=dh0, dw_part=dw_part, dbh_part=dbh_part,
+                    h_in_quant=check_quant(h_in_quant, "h_in_quant"),
+                    h_out_quant=check_quant(h_out_quant, "h_out_quant"))
+    return dgi, dh0, dw_part.sum(0), dbh_part.sum(0)
 
 
 class GRUScanDiagonalFunction(torch.autograd.Function):

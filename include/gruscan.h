@@ -121,6 +121,41 @@ int64_t gs_workspace_bytes(int kind, const gs_args* args);
  * Synchronises the stream. Returns the word, or a negative GS_ERR_* value. */
 int gs_workspace_status(void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* ---- backward ------------------------------------------------------------------
+ * Gradients of the scan (reference: the recompute-based backward of
+ * src/gru_qat/triton_kernels/scan.py:1460-1550 and its per-kind Triton kernels,
+ * scan.py:296-752, scan_diagonal.py:285-561, scan_monarch.py:409-884,
+ * scan_butterfly.py:462-1075). Walks t from T-1 to 0, recomputes the gates from
+ * h_{t-1} = out[t-1] (h0 at t = 0) and pushes dout[t] plus the carried gradient
+ * through q_out's clipped-STE mask, the gates and the hidden map; q_in's mask
+ * gates the carry through the map. Weight and bias gradients are returned as
+ * per-batch-row partials (sum them over rows), which keeps the kernels free of
+ * atomics and their results deterministic, as the reference's partial
+ * buffers do (scan.py:1445-1446).
+ */
+typedef struct gs_bwd_args {
+  const float* gi;    /* forward inputs and output as in gs_args                      */
+  const float* h0;
+  const float* w;
+  const float* w2;
+  const float* bh;
+  const float* out;   /* [T, B, H] the forward's output                               */
+  const float* dout;  /* [T, B, H] contiguous: upstream gradient of out               */
+  float* dgi;         /* [T, B, 3H] contiguous: gradient of gi                        */
+  float* dh0;         /* [B, H] contiguous: gradient of h0                            */
+  float* dw_part;     /* diagonal: [B, 3, H] per-row partial gradient of Wh_diag      */
+  float* dbh_part;    /* [B, 3H] per-row partial gradient of bh                       */
+  void* workspace;
+  int64_t workspace_bytes;
+  int64_t T, B, H;
+  int64_t sg_t, sg_b, sh0_b, so_t, so_b; /* strides of gi, h0, out (elements)      */
+  int64_t nblocks, blksz, log_n, bfly_nblocks;
+  gs_quant q_in;
+  gs_quant q_out;
+} gs_bwd_args;
+
+int gs_diagonal_bwd(const gs_bwd_args* args, hipStream_t stream);
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* gs_last_error(void);
 

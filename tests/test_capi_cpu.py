@@ -96,6 +96,43 @@ def test_butterfly_shape_rejected():
     assert b"H_PAD" in lib.gs_last_error()
 
 
+def _bwd_args(T=4, B=3, H=8, **kw):
+    a = _lib.GsBwdArgs()
+    a.T, a.B, a.H = T, B, H
+    a.sg_t, a.sg_b = B * 3 * H, 3 * H
+    a.sh0_b = H
+    a.so_t, a.so_b = B * H, H
+    a.q_in = _lib.make_quant(kw.pop("q_in", None), "q_in")
+    a.q_out = _lib.make_quant(kw.pop("q_out", None), "q_out")
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+BWD_PTRS = ("gi", "h0", "w", "bh", "out", "dout", "dgi", "dh0", "dw_part", "dbh_part")
+
+
+@pytest.mark.parametrize("missing", BWD_PTRS)
+def test_diagonal_bwd_null_pointer_rejected(missing):
+    lib = _lib.load()
+    a = _bwd_args(**{k: FAKE for k in BWD_PTRS if k != missing})
+    assert lib.gs_diagonal_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"non-NULL" in lib.gs_last_error()
+
+
+def test_diagonal_bwd_rejects_w2_and_bad_quant():
+    lib = _lib.load()
+    a = _bwd_args(w2=FAKE, **{k: FAKE for k in BWD_PTRS})
+    assert lib.gs_diagonal_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"w2" in lib.gs_last_error()
+    a = _bwd_args(q_out=(0.1, 5, -5), **{k: FAKE for k in BWD_PTRS})
+    assert lib.gs_diagonal_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    a = _bwd_args(**{k: FAKE for k in BWD_PTRS})
+    a.T = 0
+    assert lib.gs_diagonal_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"T must be > 0" in lib.gs_last_error()
+
+
 def test_workspace_sizes():
     """Control words plus double-buffered tagged exchange words (8 bytes per
     unit and row) when a batch row's step spans workgroups; two-factor Monarch

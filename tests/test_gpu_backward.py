@@ -51,6 +51,7 @@ CASES = [
     (1, (8, 5, 64), None, False), (1, (6, 4, 300), None, False), (0, (8, 5, 64), None, False),
     (3, (6, 4, 64), 4, False), (3, (6, 4, 64), 4, True), (4, (5, 3, 256), None, False),
     (4, (5, 3, 100), None, False),
+    (0, (67, 9, 200), None, False), (0, (1, 2, 8), None, False),
 ]
 
 
