@@ -111,6 +111,7 @@ int check_workspace(const gs_args* a, int64_t need, const char* who) {
 namespace gs {
 int64_t dense_workspace_bytes(const gs_args* a);
 int64_t monarch_workspace_bytes(const gs_args* a);
+int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a);
 }  // namespace gs
 
 extern "C" {
@@ -127,6 +128,18 @@ int64_t gs_workspace_bytes(int kind, const gs_args* a) {
       return gs::kCtrlBytes;
     default:
       return gs::set_error(GS_ERR_INVALID, "gs_workspace_bytes: unknown kind %d", kind);
+  }
+}
+
+int64_t gs_bwd_workspace_bytes(int kind, const gs_bwd_args* a) {
+  if (a == nullptr) return gs::set_error(GS_ERR_INVALID, "gs_bwd_workspace_bytes: args is NULL");
+  switch (kind) {
+    case GS_KIND_DENSE:
+      return gs::dense_bwd_workspace_bytes(a);
+    case GS_KIND_DIAGONAL:
+      return 0;
+    default:
+      return gs::set_error(GS_ERR_INVALID, "gs_bwd_workspace_bytes: no backward for kind %d", kind);
   }
 }
 

@@ -34,7 +34,9 @@ EXPORTS = (
     "gs_butterfly_fwd",
     "gs_butterfly_fwd_generic",
     "gs_diagonal_bwd",
+    "gs_dense_bwd",
     "gs_workspace_bytes",
+    "gs_bwd_workspace_bytes",
     "gs_workspace_status",
     "gs_last_error",
     "gs_abi_version",
@@ -136,12 +138,14 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(GsArgs), ctypes.c_void_p]
             fn.restype = ctypes.c_int
-        for name in ("gs_diagonal_bwd",):
+        for name in ("gs_diagonal_bwd", "gs_dense_bwd"):
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(GsBwdArgs), ctypes.c_void_p]
             fn.restype = ctypes.c_int
         lib.gs_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsArgs)]
         lib.gs_workspace_bytes.restype = ctypes.c_int64
+        lib.gs_bwd_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsBwdArgs)]
+        lib.gs_bwd_workspace_bytes.restype = ctypes.c_int64
         lib.gs_workspace_status.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
         lib.gs_workspace_status.restype = ctypes.c_int
         lib.gs_last_error.argtypes = []
@@ -266,14 +270,15 @@ def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: to
     raise_for(rc, lib)
 
 
-def launch_bwd(fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,
+def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,
                w2: Optional[torch.Tensor], bh: torch.Tensor, out: torch.Tensor, dout: torch.Tensor,
                dgi: torch.Tensor, dh0: torch.Tensor, dw_part: Optional[torch.Tensor],
                dbh_part: torch.Tensor, h_in_quant: QuantTuple, h_out_quant: QuantTuple,
                nblocks: int = 0, blksz: int = 0, log_n: int = 0, bfly_nblocks: int = 0) -> None:
     """Fill gs_bwd_args from fp32 device tensors (dout, dgi, dh0 and the
     partials contiguous) and call a backward entry point on the current torch
-    stream of gi's device."""
+    stream of gi's device, with the stream's cached workspace when the kind
+    needs one."""
     lib = load()
     T, B, threeH = gi.shape
     a = GsBwdArgs()
@@ -291,7 +296,14 @@ def launch_bwd(fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Ten
     a.log_n, a.bfly_nblocks = log_n, bfly_nblocks
     a.q_in = make_quant(h_in_quant, "h_in_quant")
     a.q_out = make_quant(h_out_quant, "h_out_quant")
+    need = lib.gs_bwd_workspace_bytes(kind, ctypes.byref(a))
+    if need < 0:
+        raise_for(int(need), lib)
     with torch.cuda.device(gi.device):
         handle = torch.cuda.current_stream(gi.device).cuda_stream
+        if need > 0:
+            ws = workspace(gi.device, handle, int(need), steps=T)
+            a.workspace = ws.data_ptr()
+            a.workspace_bytes = ws.numel()
         rc = getattr(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
     raise_for(rc, lib)

@@ -24,7 +24,6 @@ from typing import Any, cast
 import torch
 
 from . import _lib
-from ._backward import scan_backward
 from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
 
 
@@ -74,15 +73,39 @@ def gru_scan_forward(
     return _dense_forward("gru_scan_forward", gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant)
 
 
-def _dense_gh(hq: torch.Tensor, Wh_cat: torch.Tensor) -> torch.Tensor:
-    return hq @ Wh_cat.t()
+def gru_scan_backward_persistent(gi, h0, Wh_cat, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None,
+                                 **_ignored_tiling: Any):
+    """Gradients (dgi, dh0, dWh_cat, dbh_cat) of the dense scan.
+
+    Same contract as the reference's gru_scan_backward_persistent
+    (scan.py:646-752): ``gs_dense_bwd`` recomputes gh for every step with one
+    GEMM, runs the reverse recurrence as one persistent launch and forms dWh
+    with a second GEMM; dbh comes back as per-row partials summed here.
+    """
+    who = "gru_scan_backward_persistent"
+    require_cuda(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat, out=out, dout=dout)
+    require_f32(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat, out=out, dout=dout)
+    T, B, H = check_common(who, gi, h0, bh_cat)
+    if tuple(Wh_cat.shape) != (3 * H, H):
+        raise ValueError(f"Wh_cat shape must be (3H, H)=({3 * H}, {H}); got {tuple(Wh_cat.shape)}")
+    if tuple(out.shape) != (T, B, H) or tuple(dout.shape) != (T, B, H):
+        raise ValueError(f"out and dout must be (T, B, H)=({T}, {B}, {H})")
+    gi, h0, out = gi.contiguous(), h0.contiguous(), out.contiguous()
+    Wh_cat, bh_cat, dout = Wh_cat.contiguous(), bh_cat.contiguous(), dout.contiguous()
+    dgi = torch.empty((T, B, 3 * H), device=gi.device, dtype=gi.dtype)
+    dh0 = torch.empty((B, H), device=gi.device, dtype=gi.dtype)
+    dW = torch.empty((3 * H, H), device=gi.device, dtype=gi.dtype)
+    dbh_part = torch.empty((B, 3 * H), device=gi.device, dtype=gi.dtype)
+    _lib.launch_bwd(_lib.KIND_DENSE, "gs_dense_bwd", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat, out=out,
+                    dout=dout, dgi=dgi, dh0=dh0, dw_part=dW, dbh_part=dbh_part,
+                    h_in_quant=check_quant(h_in_quant, "h_in_quant"),
+                    h_out_quant=check_quant(h_out_quant, "h_out_quant"))
+    return dgi, dh0, dW, dbh_part.sum(0)
 
 
-def gru_scan_backward(gi, h0, Wh_cat, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None):
-    """(dgi, dh0, dWh_cat, dbh_cat); semantics of scan.py:1460-1550."""
-    dgi, dh0, (dW,), dbh = scan_backward(gi, h0, out, dout, _dense_gh, [Wh_cat], bh_cat,
-                                         h_in_quant, h_out_quant)
-    return dgi, dh0, dW, dbh
+# The reference's names for the dense backward launchers (scan.py:1355, :646).
+gru_scan_backward_triton = gru_scan_backward_persistent
+gru_scan_backward = gru_scan_backward_persistent
 
 
 class GRUScanPersistentFunction(torch.autograd.Function):

@@ -81,7 +81,7 @@ def gru_scan_diagonal_backward(gi, h0, Wh_diag, bh_cat, out, dout, *, h_in_quant
     dh0 = torch.empty((B, H), device=gi.device, dtype=gi.dtype)
     dw_part = torch.empty((B, 3, H), device=gi.device, dtype=gi.dtype)
     dbh_part = torch.empty((B, 3 * H), device=gi.device, dtype=gi.dtype)
-    _lib.launch_bwd("gs_diagonal_bwd", gi=gi, h0=h0, w=Wh_diag, w2=None, bh=bh_cat, out=out, dout=dout,
+    _lib.launch_bwd(_lib.KIND_DIAGONAL, "gs_diagonal_bwd", gi=gi, h0=h0, w=Wh_diag, w2=None, bh=bh_cat, out=out, dout=dout,
                     dgi=dgi, dh0=dh0, dw_part=dw_part, dbh_part=dbh_part,
                     h_in_quant=check_quant(h_in_quant, "h_in_quant"),
                     h_out_quant=check_quant(h_out_quant, "h_out_quant"))

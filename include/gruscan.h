@@ -128,10 +128,11 @@ int gs_workspace_status(void* workspace, int64_t workspace_bytes, hipStream_t st
  * scan_butterfly.py:462-1075). Walks t from T-1 to 0, recomputes the gates from
  * h_{t-1} = out[t-1] (h0 at t = 0) and pushes dout[t] plus the carried gradient
  * through q_out's clipped-STE mask, the gates and the hidden map; q_in's mask
- * gates the carry through the map. Weight and bias gradients are returned as
- * per-batch-row partials (sum them over rows), which keeps the kernels free of
- * atomics and their results deterministic, as the reference's partial
- * buffers do (scan.py:1445-1446).
+ * gates the carry through the map. Bias gradients (and the diagonal kind's
+ * weight gradient) are returned as per-batch-row partials (sum them over
+ * rows), which keeps the kernels free of atomics and their results
+ * deterministic, as the reference's partial buffers do (scan.py:1445-1446);
+ * the dense kind's weight gradient comes out whole.
  */
 typedef struct gs_bwd_args {
   const float* gi;    /* forward inputs and output as in gs_args                      */
@@ -143,7 +144,8 @@ typedef struct gs_bwd_args {
   const float* dout;  /* [T, B, H] contiguous: upstream gradient of out               */
   float* dgi;         /* [T, B, 3H] contiguous: gradient of gi                        */
   float* dh0;         /* [B, H] contiguous: gradient of h0                            */
-  float* dw_part;     /* diagonal: [B, 3, H] per-row partial gradient of Wh_diag      */
+  float* dw_part;     /* diagonal: [B, 3, H] per-row partial gradient of Wh_diag;      *
+                       * dense: [3H, H] gradient of Wh_cat                             */
   float* dbh_part;    /* [B, 3H] per-row partial gradient of bh                       */
   void* workspace;
   int64_t workspace_bytes;
@@ -155,6 +157,17 @@ typedef struct gs_bwd_args {
 } gs_bwd_args;
 
 int gs_diagonal_bwd(const gs_bwd_args* args, hipStream_t stream);
+
+/* Dense backward (reference gru_scan_backward_persistent, scan.py:646-752, and
+ * its kernel, scan.py:296-643). `out` must hold its steps back to back
+ * (so_t == B * so_b). Needs a workspace of gs_bwd_workspace_bytes(GS_KIND_DENSE,
+ * args) bytes, 256-byte aligned, zeroed before its first use (like the
+ * forward's, it may be shared with forward launches on the same stream). */
+int gs_dense_bwd(const gs_bwd_args* args, hipStream_t stream);
+
+/* Scratch bytes a backward entry point needs (0 for the diagonal kind). Pure
+ * host arithmetic. Negative on error. */
+int64_t gs_bwd_workspace_bytes(int kind, const gs_bwd_args* args);
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* gs_last_error(void);

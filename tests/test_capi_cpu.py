@@ -133,6 +133,47 @@ def test_diagonal_bwd_rejects_w2_and_bad_quant():
     assert b"T must be > 0" in lib.gs_last_error()
 
 
+@pytest.mark.parametrize("missing", BWD_PTRS)
+def test_dense_bwd_null_pointer_rejected(missing):
+    lib = _lib.load()
+    a = _bwd_args(**{k: FAKE for k in BWD_PTRS if k != missing})
+    assert lib.gs_dense_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"non-NULL" in lib.gs_last_error()
+
+
+def test_dense_bwd_rejects_strided_out_and_missing_workspace():
+    lib = _lib.load()
+    a = _bwd_args(**{k: FAKE for k in BWD_PTRS})
+    a.so_t = a.so_t + 8  # steps not back to back
+    assert lib.gs_dense_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"so_t == B * so_b" in lib.gs_last_error()
+    a = _bwd_args(**{k: FAKE for k in BWD_PTRS})
+    assert lib.gs_dense_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"workspace" in lib.gs_last_error()
+
+
+def test_bwd_workspace_sizes():
+    """Dense: control words, double-buffered tagged dgh rows (3H words per
+    padded row) plus pad, one XCD word per workgroup, gh [T B, 3H], dgh_n
+    [T B, H] and the K-split partials of dWh; diagonal needs none."""
+    lib = _lib.load()
+    al = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    T, B, H = 64, 32, 512
+    a = _bwd_args(T=T, B=B, H=H)
+    kc = 32
+    nwc, P = 4, 128 // 4
+    tiles = (3 * H // 64) * (H // 64)
+    split = min(-(-512 // tiles), -(-(T * B) // 256))
+    want = (256 + al(2 * B * 3 * H * 8 + 16 * kc * 8) + al((B // 4) * P * 8) + al(T * B * 3 * H * 4)
+            + al(T * B * H * 4) + (al(split * 3 * H * H * 4) if split > 1 else 0))
+    assert nwc == 4
+    assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == want
+    assert lib.gs_bwd_workspace_bytes(_lib.KIND_DIAGONAL, ctypes.byref(a)) == 0
+    assert lib.gs_bwd_workspace_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) == _lib.GS_ERR_INVALID
+    a = _bwd_args(T=2, B=3, H=2048)
+    assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == _lib.GS_ERR_INVALID
+
+
 def test_workspace_sizes():
     """Control words plus double-buffered tagged exchange words (8 bytes per
     unit and row) when a batch row's step spans workgroups; two-factor Monarch

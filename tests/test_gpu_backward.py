@@ -52,6 +52,8 @@ CASES = [
     (3, (6, 4, 64), 4, False), (3, (6, 4, 64), 4, True), (4, (5, 3, 256), None, False),
     (4, (5, 3, 100), None, False),
     (0, (67, 9, 200), None, False), (0, (1, 2, 8), None, False),
+    (1, (64, 32, 512), None, False), (1, (5, 37, 1000), None, False), (1, (3, 2, 8), None, False),
+    (1, (1, 3, 16), None, False), (1, (7, 6, 128), None, False),
 ]
 
 
