@@ -1,80 +1,145 @@
 // fp32 GEMM on v_mfma_f32_16x16x4f32 (gfx950) for the products around the
 // scans: the backward's recomputation of the hidden projection for all steps
-// at once, gh = q_in([h0; out[0..T-2]]) Wh^T + bh, and the weight gradient
-// dWh = dgh^T q_in([h0; out[0..T-2]]) (the per-step products of the
-// reference backward, src/gru_qat/triton_kernels/scan.py:388-421 and
-// :576-619, batched over every step because neither depends on the reverse
-// recurrence).
+// at once, gh = q_in([h0; out[0..T-2]]) Wh^T + bh (NT), and the weight
+// gradient dWh = dgh^T q_in([h0; out[0..T-2]]) (TN) -- the per-step products
+// of the reference backward (src/gru_qat/triton_kernels/scan.py:388-421 and
+// :576-619), batched over every step because neither depends on the reverse
+// recurrence.
 //
 // Tiling: a workgroup of 4 waves computes a 64 x 64 tile of C; wave (wy, wx)
-// owns the 32 x 32 quarter as 2 x 2 MFMA tiles of 16 x 16. K advances in
-// slices of 32 staged through LDS as [k][i] and [k][j] (a column of 16
-// consecutive i or j per MFMA operand read, conflict-free), double-buffered:
-// the next slice's global loads are in flight while the current one feeds
-// the MFMAs. Global loads run along each operand's unit-stride dimension.
+// owns a 32 x 32 quarter as 2 x 2 MFMA tiles of 16 x 16. K advances in slices
+// of 32, staged through LDS and double-buffered: the next slice's global
+// loads are in flight while the current one feeds the MFMAs. Global loads are
+// float4 along each operand's contiguous dimension when the shapes allow it
+// (scalar otherwise), and land in LDS without transposition:
+//   NT: S[row][k], row stride 36. The 16 lanes of k-group q read
+//       k = 8 q + s (s < 8) of their row as two float4 (36 = 4 mod 64 x 9
+//       puts the 16 rows x 4 words in distinct banks).
+//   TN: S[k][row], row stride 80. MFMA s reads k = q + 4 s: the four
+//       k-groups sit 80 = 16 mod 64 words apart, so the 64 lanes' reads hit
+//       64 distinct banks.
+// Any bijection between (MFMA step, k-group) and k is valid as long as A and
+// B use the same one; each layout picks the one its LDS order reads
+// conflict-free.
 //
-// MFMA operand layout (16x16x4 f32): lane l supplies A[i = l % 16][k = l / 16]
-// and B[k = l / 16][j = l % 16]; D VGPR v of lane l is C[4 (l / 16) + v][l % 16].
+// MFMA operand layout (16x16x4 f32): lane l supplies A[i = l % 16][k-group
+// l / 16] and B[k-group l / 16][j = l % 16]; D VGPR v of lane l is
+// C[4 (l / 16) + v][l % 16].
 #include "gs_gemm.h"
 #include "gs_mfma.h"
 
 namespace gs {
 namespace {
 
-constexpr int BM = 64, BN = 64, BK = 32, kGemmThreads = 256, kPad = 1;
-constexpr int kPerThread = BM * BK / kGemmThreads;  // elements of each operand per thread per slice
-static_assert(BM * BK == BK * BN, "both operands stage the same element count");
+constexpr int BM = 64, BN = 64, BK = 32, kGemmThreads = 256;
+constexpr int kNTStride = BK + 4;  // NT: floats per LDS row (one row of the tile, 32 k)
+constexpr int kTNStride = 64 + 16; // TN: floats per LDS row (one k, 64 rows of the tile)
+constexpr int kStageFloats = (BM * kNTStride > BK * kTNStride) ? BM * kNTStride : BK * kTNStride;
 
-// Element (r, c) of an operand whose column stride is 1 (CUNIT) or whose row
-// stride is 1 (!CUNIT).
-template <bool CUNIT>
-__device__ __forceinline__ float operand_at(const GemmOperand& o, int r, int c) {
-  const float* src;
-  if (r < o.rows0)
-    src = o.p0 + (int64_t)r * o.s0r;
-  else
-    src = o.p + (CUNIT ? (int64_t)(r - o.rows0) * o.sr : (int64_t)(r - o.rows0));
-  float v = src[CUNIT ? (int64_t)c : (int64_t)c * o.sc];
-  if (o.q.on) v = fake_quant(v, o.q);
-  return v;
-}
+typedef float f4v __attribute__((ext_vector_type(4)));
 
-// A_KFAST: A's column (k) stride is 1, else its row (i) stride is 1.
-// B_NFAST: B's column (j) stride is 1, else its row (k) stride is 1.
-template <bool A_KFAST, bool B_NFAST>
+// Loads of one operand tile (64 rows of the output dimension x 32 k) into
+// registers, then into LDS. KC: the operand is contiguous along k.
+template <bool KC, bool VEC>
+struct TileLoader {
+  // VEC: 2 float4 per thread; scalar: 8 floats per thread.
+  static constexpr int N = VEC ? 2 : 8;
+  float r[VEC ? 8 : 8];
+  const float* base;
+  int64_t ld;
+  int lim_row, lim_k;  // rows < lim_row, k < lim_k (absolute)
+  int row0;
+
+  __device__ __forceinline__ void init(const float* p, int64_t ld_, int row0_, int lim_row_, int lim_k_) {
+    base = p;
+    ld = ld_;
+    row0 = row0_;
+    lim_row = lim_row_;
+    lim_k = lim_k_;
+  }
+  __device__ __forceinline__ void load(int k0) {
+    const int tid = threadIdx.x;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int idx = tid + kGemmThreads * e;
+        int row, k;
+        if constexpr (KC) {
+          row = idx >> 3;
+          k = (idx & 7) * 4;
+        } else {
+          k = idx >> 4;
+          row = (idx & 15) * 4;
+        }
+        const int R = row0 + row, Kk = k0 + k;
+        f4v v = f4v{0.f, 0.f, 0.f, 0.f};
+        // Shapes are multiples of 4 along the contiguous dimension, so a
+        // float4 is either wholly inside or wholly outside.
+        if (R < lim_row && Kk < lim_k)
+          v = *reinterpret_cast<const f4v*>(KC ? base + (int64_t)R * ld + Kk : base + (int64_t)Kk * ld + R);
+        r[4 * e + 0] = v[0];
+        r[4 * e + 1] = v[1];
+        r[4 * e + 2] = v[2];
+        r[4 * e + 3] = v[3];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int idx = tid + kGemmThreads * e;
+        int row, k;
+        if constexpr (KC) {
+          row = idx >> 5;
+          k = idx & 31;
+        } else {
+          k = idx >> 6;
+          row = idx & 63;
+        }
+        const int R = row0 + row, Kk = k0 + k;
+        r[e] = (R < lim_row && Kk < lim_k) ? (KC ? base[(int64_t)R * ld + Kk] : base[(int64_t)Kk * ld + R]) : 0.0f;
+      }
+    }
+  }
+  __device__ __forceinline__ void stage(float* s) const {
+    const int tid = threadIdx.x;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int idx = tid + kGemmThreads * e;
+        float* d;
+        if constexpr (KC)
+          d = s + (idx >> 3) * kNTStride + (idx & 7) * 4;
+        else
+          d = s + (idx >> 4) * kTNStride + (idx & 15) * 4;
+        *reinterpret_cast<f4v*>(d) = f4v{r[4 * e], r[4 * e + 1], r[4 * e + 2], r[4 * e + 3]};
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int idx = tid + kGemmThreads * e;
+        if constexpr (KC)
+          s[(idx >> 5) * kNTStride + (idx & 31)] = r[e];
+        else
+          s[(idx >> 6) * kTNStride + (idx & 63)] = r[e];
+      }
+    }
+  }
+};
+
+template <int LAYOUT, bool VEC>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
-  __shared__ float As[2][BK][BM + kPad];
-  __shared__ float Bs[2][BK][BN + kPad];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr bool KC = LAYOUT == kGemmNT;
+  __shared__ __attribute__((aligned(16))) float As[2][kStageFloats];
+  __shared__ __attribute__((aligned(16))) float Bs[2][kStageFloats];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wy = wave >> 1, wx = wave & 1;
   const int i0 = blockIdx.x * BM, j0 = blockIdx.y * BN;
   const int kper = ((g.K + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
   const int kbeg = blockIdx.z * kper;
   const int kend = min(g.K, kbeg + kper);
 
-  float ra[kPerThread], rb[kPerThread];
-  auto load = [&](int k0) {
-#pragma unroll
-    for (int e = 0; e < kPerThread; ++e) {
-      const int idx = tid + kGemmThreads * e;
-      const int ai = A_KFAST ? idx / BK : idx % BM, ak = A_KFAST ? idx % BK : idx / BM;
-      const int i = i0 + ai, k = k0 + ak;
-      ra[e] = (i < g.M && k < kend) ? operand_at<A_KFAST>(g.a, i, k) : 0.0f;
-      const int bj = B_NFAST ? idx % BN : idx / BK, bk = B_NFAST ? idx / BN : idx % BK;
-      const int j = j0 + bj, kb = k0 + bk;
-      rb[e] = (j < g.N && kb < kend) ? operand_at<B_NFAST>(g.b, kb, j) : 0.0f;
-    }
-  };
-  auto stage = [&](int buf) {
-#pragma unroll
-    for (int e = 0; e < kPerThread; ++e) {
-      const int idx = tid + kGemmThreads * e;
-      const int ai = A_KFAST ? idx / BK : idx % BM, ak = A_KFAST ? idx % BK : idx / BM;
-      As[buf][ak][ai] = ra[e];
-      const int bj = B_NFAST ? idx % BN : idx / BK, bk = B_NFAST ? idx / BN : idx % BK;
-      Bs[buf][bk][bj] = rb[e];
-    }
-  };
+  TileLoader<KC, VEC> la, lb;
+  la.init(g.a, g.lda, i0, g.M, kend);
+  lb.init(g.b, g.ldb, j0, g.N, kend);
 
   f4 acc[2][2];
 #pragma unroll
@@ -85,24 +150,55 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   const int r16 = lane & 15, kq = lane >> 4;
   int buf = 0;
   if (kbeg < kend) {
-    load(kbeg);
-    stage(0);
+    la.load(kbeg);
+    lb.load(kbeg);
+    la.stage(As[0]);
+    lb.stage(Bs[0]);
   }
   __syncthreads();
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     const bool more = k0 + BK < kend;
-    if (more) load(k0 + BK);
-#pragma unroll
-    for (int k4 = 0; k4 < BK; k4 += 4) {
-      const float* ar = &As[buf][k4 + kq][32 * wy + r16];
-      const float* br = &Bs[buf][k4 + kq][32 * wx + r16];
-      const float a0 = ar[0], a1 = ar[16], b0 = br[0], b1 = br[16];
-      acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
-      acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
-      acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
-      acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+    if (more) {
+      la.load(k0 + BK);
+      lb.load(k0 + BK);
     }
-    if (more) stage(buf ^ 1);
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
+    if constexpr (KC) {
+      // lane: rows 32 wy + 16 ti + r16 (A) and 32 wx + 16 tj + r16 (B), k = 8 kq + s
+      f4v a[2][2], b[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          a[t][h] = *reinterpret_cast<const f4v*>(as + (32 * wy + 16 * t + r16) * kNTStride + 8 * kq + 4 * h);
+          b[t][h] = *reinterpret_cast<const f4v*>(bs + (32 * wx + 16 * t + r16) * kNTStride + 8 * kq + 4 * h);
+        }
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+          for (int tj = 0; tj < 2; ++tj)
+            acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti][s >> 2][s & 3], b[tj][s >> 2][s & 3],
+                                                               acc[ti][tj], 0, 0, 0);
+    } else {
+      // k = kq + 4 s
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float* ar = as + (kq + 4 * s) * kTNStride + 32 * wy + r16;
+        const float* br = bs + (kq + 4 * s) * kTNStride + 32 * wx + r16;
+        const float a0 = ar[0], a1 = ar[16], b0 = br[0], b1 = br[16];
+        acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b1, acc[1][1], 0, 0, 0);
+      }
+    }
+    if (more) {
+      la.stage(As[buf ^ 1]);
+      lb.stage(Bs[buf ^ 1]);
+    }
     __syncthreads();
     buf ^= 1;
   }
@@ -132,14 +228,28 @@ __global__ void sum_partials_kernel(float* dst, const float* src, int64_t n, int
   }
 }
 
+__global__ void prev_state_kernel(float* hq, const float* h0, int64_t sh0_b, const float* out, int64_t so_b,
+                                  int64_t rows, int B, int H, Quant q) {
+  const int64_t n = rows * H;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = e / H;
+    const int k = (int)(e - m * H);
+    float v = m < B ? h0[m * sh0_b + k] : out[(m - B) * so_b + k];
+    if (q.on) v = fake_quant(v, q);
+    hq[e] = v;
+  }
+}
+
 typedef void (*GemmFn)(GemmArgs);
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 
 int gemm_pick_split(int M, int N, int K) {
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-  int s = (512 + tiles - 1) / tiles;       // about two workgroups per CU
-  const int smax = (K + 255) / 256;        // at least 256 terms per split
+  int s = (512 + tiles - 1) / tiles;  // about two workgroups per CU
+  const int smax = (K + 255) / 256;   // at least 256 terms per split
   if (s > smax) s = smax;
   return s < 1 ? 1 : s;
 }
@@ -148,11 +258,13 @@ int gemm_f32(const GemmArgs& g, hipStream_t stream, const char* who) {
   if (g.M < 1 || g.N < 1 || g.K < 1 || g.ksplit < 1)
     return set_error(GS_ERR_INVALID, "%s: GEMM dims must be positive (M=%d, N=%d, K=%d, ksplit=%d)", who, g.M, g.N,
                      g.K, g.ksplit);
-  const bool a_kfast = g.a.sc == 1, b_nfast = g.b.sc == 1;
-  if ((!a_kfast && g.a.sr != 1) || (!b_nfast && g.b.sr != 1))
-    return set_error(GS_ERR_INVALID, "%s: GEMM operands need a unit stride", who);
-  GemmFn fn = a_kfast ? (b_nfast ? gemm_kernel<true, true> : gemm_kernel<true, false>)
-                      : (b_nfast ? gemm_kernel<false, true> : gemm_kernel<false, false>);
+  // float4 loads need 16-byte aligned bases, leading dimensions that keep
+  // rows aligned, and contiguous extents that are multiples of 4.
+  const bool nt = g.layout == kGemmNT;
+  const bool vec = aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+                   (nt ? g.K % 4 == 0 : (g.M % 4 == 0 && g.N % 4 == 0));
+  GemmFn fn = nt ? (vec ? gemm_kernel<kGemmNT, true> : gemm_kernel<kGemmNT, false>)
+                 : (vec ? gemm_kernel<kGemmTN, true> : gemm_kernel<kGemmTN, false>);
   const dim3 grid((unsigned)((g.M + BM - 1) / BM), (unsigned)((g.N + BN - 1) / BN), (unsigned)g.ksplit);
   hipLaunchKernelGGL(fn, grid, dim3(kGemmThreads), 0, stream, g);
   GS_CHECK_HIP(hipGetLastError());
@@ -165,6 +277,17 @@ int sum_partials(float* dst, const float* src, int64_t n, int parts, int64_t str
   const int64_t blocks = (n + 255) / 256;
   hipLaunchKernelGGL(sum_partials_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, stream, dst,
                      src, n, parts, stride);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
+
+int build_prev_state(float* hq, const float* h0, int64_t sh0_b, const float* out, int64_t so_b, int T, int B, int H,
+                     const Quant& q, hipStream_t stream, const char* who) {
+  (void)who;
+  const int64_t n = (int64_t)T * B * H;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(prev_state_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, stream, hq, h0,
+                     sh0_b, out, so_b, (int64_t)T * B, B, H, q);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }

@@ -74,36 +74,29 @@ __device__ __forceinline__ void lds_a_il(const float* blk, int lane, float (&a)[
   }
 }
 
-// Polls one row of tagged words into interleaved LDS blocks: segment g of
-// the row starts at src + g * src_seg and lands in the block at
-// dst + g * dst_seg; lane l takes k = 64 m + l (m < MPR) of every segment and
-// stores block[il_index(r, k)] for k < klen. Each load instruction reads 64
-// consecutive words (polling 4 rows x 16 words per instruction instead
-// measured 25 % slower exchanges). Loads address k up to 64 MPR - 1, so the
-// buffer behind the last segment must extend that far (words past klen are
-// loaded but neither waited for nor stored). Only stale words are loaded
-// again.
-template <int MPR, int NSEG>
-__device__ __forceinline__ void poll_row_segs(const Ctrl& c, const uint64_t* src, int64_t src_seg, float* dst,
-                                              int dst_seg, int r, int klen, uint32_t tag) {
-  constexpr int NW = MPR * NSEG;
-  static_assert(NW <= 64, "poll mask is 64 bits");
-  typedef typename std::conditional<(NW > 32), uint64_t, uint32_t>::type Mask;
+// Polls one row of tagged words: lane l waits for src[64 m + l] (m < MPR,
+// 64 m + l < klen) to carry `tag` and returns the words in v[m]. Each load
+// instruction reads 64 consecutive words (polling 4 rows x 16 words per
+// instruction instead measured 25 % slower exchanges). Loads address up to
+// src[64 MPR - 1], so the buffer must extend that far (words past klen are
+// loaded but not waited for). Only stale words are loaded again. Returns the
+// mask of valid m.
+template <int MPR>
+__device__ __forceinline__ uint32_t poll_row_words(const Ctrl& c, const uint64_t* src, int klen, uint32_t tag,
+                                                   uint64_t (&v)[MPR]) {
+  static_assert(MPR <= 32, "poll mask is 32 bits");
   const int lane = threadIdx.x & 63;
   const uint64_t* s0 = src + lane;
-  Mask valid = 0;
+  uint32_t valid = 0;
 #pragma unroll
-  for (int m = 0; m < MPR; ++m)
-#pragma unroll
-    for (int g = 0; g < NSEG; ++g) valid |= (Mask)(lane + 64 * m < klen ? 1u : 0u) << (g * MPR + m);
-  uint64_t v[NW];
-  static_for<0, NW>([&](auto I) { v[I] = ld_tagged(s0 + (I / MPR) * src_seg + 64 * (I % MPR)); });
+  for (int m = 0; m < MPR; ++m) valid |= (lane + 64 * m < klen ? 1u : 0u) << m;
+  static_for<0, MPR>([&](auto I) { v[I] = ld_tagged(s0 + 64 * I); });
   uint32_t polls = 0;
   while (true) {
-    Mask pending = 0;
-    static_for<0, NW>([&](auto I) { pending |= (Mask)(tag_of(v[I]) != tag ? 1u : 0u) << I; });
+    uint32_t pending = 0;
+    static_for<0, MPR>([&](auto I) { pending |= (tag_of(v[I]) != tag ? 1u : 0u) << I; });
     pending &= valid;
-    if (pending == 0) break;
+    if (pending == 0u) break;
     if (++polls > kSpinLimit) {
       __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       break;
@@ -111,20 +104,49 @@ __device__ __forceinline__ void poll_row_segs(const Ctrl& c, const uint64_t* src
     if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
       break;
     __builtin_amdgcn_s_sleep(1);
-    static_for<0, NW>([&](auto I) {
-      if ((pending >> I) & 1u) v[I] = ld_tagged(s0 + (I / MPR) * src_seg + 64 * (I % MPR));
+    static_for<0, MPR>([&](auto I) {
+      if ((pending >> I) & 1u) v[I] = ld_tagged(s0 + 64 * I);
     });
   }
-  static_for<0, NW>([&](auto I) {
-    if ((valid >> I) & 1u) dst[(I / MPR) * dst_seg + il_index(r, lane + 64 * (I % MPR))] = value_of(v[I]);
-  });
+  return valid;
 }
 
-// One-segment form: one row of klen words into one interleaved block.
+// Polls one row of tagged words into an interleaved LDS block: lane l takes
+// k = 64 m + l (m < MPR) from src[k] and stores dst[il_index(r, k)] for
+// k < klen, with the loads, waits and bounds of poll_row_words. (The wait loop
+// is written out here rather than shared: the forward kernels' code around
+// this inlined loop is tuned, and the shared form schedules differently.)
 template <int MPR>
 __device__ __forceinline__ void poll_row_il(const Ctrl& c, const uint64_t* src, float* dst, int r, int klen,
                                             uint32_t tag) {
-  poll_row_segs<MPR, 1>(c, src, 0, dst, 0, r, klen, tag);
+  static_assert(MPR <= 32, "poll mask is 32 bits");
+  const int lane = threadIdx.x & 63;
+  const uint64_t* s0 = src + lane;
+  uint32_t valid = 0;
+#pragma unroll
+  for (int m = 0; m < MPR; ++m) valid |= (lane + 64 * m < klen ? 1u : 0u) << m;
+  uint64_t v[MPR];
+  static_for<0, MPR>([&](auto I) { v[I] = ld_tagged(s0 + 64 * I); });
+  uint32_t polls = 0;
+  while (true) {
+    uint32_t pending = 0;
+    static_for<0, MPR>([&](auto I) { pending |= (tag_of(v[I]) != tag ? 1u : 0u) << I; });
+    pending &= valid;
+    if (pending == 0u) break;
+    if (++polls > kSpinLimit) {
+      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+      break;
+    __builtin_amdgcn_s_sleep(1);
+    static_for<0, MPR>([&](auto I) {
+      if ((pending >> I) & 1u) v[I] = ld_tagged(s0 + 64 * I);
+    });
+  }
+  static_for<0, MPR>([&](auto I) {
+    if ((valid >> I) & 1u) dst[il_index(r, lane + 64 * I)] = value_of(v[I]);
+  });
 }
 
 // A operand from an LDS staging row: a[m] = row[kmap(m, kb4)].

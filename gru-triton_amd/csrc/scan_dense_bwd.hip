@@ -1,32 +1,36 @@
-// Dense GRU scan backward (gfx950): the persistent reverse recurrence on fp32
-// MFMA, framed by two GEMMs.
+// Dense GRU scan backward (gfx950): a linear reverse recurrence on fp32 MFMA,
+// framed by parallel passes and two GEMMs.
 //
 // Reference: gru_scan_backward_persistent and its kernel
 // (LarocheC/gru-triton src/gru_qat/triton_kernels/scan.py:646-752, :296-643),
 // whose math is the PyTorch backward at scan.py:1460-1550. Per step t, walking
-// t from T-1 to 0 with h_{t-1} = out[t-1] (h0 at t = 0):
-//   gh_t    = q_in(h_{t-1}) Wh^T + bh                 (recomputed)
-//   dh_t    = dout[t] + dh_carry, masked by q_out's clipped STE on h_t's raw value
-//   dgi_t   = (dgr, dgz, dgn), dgh_t = (dgr, dgz, dgn * r)   (gru_backward)
-//   dh_carry <- dh_t * z + mask_in(h_{t-1}) * (dgh_t Wh)
-//   dWh += dgh_t^T q_in(h_{t-1}),  dbh += sum_b dgh_t
-// Only the dgh_t Wh product sits on the recurrence. The launcher runs
-//   1. gemm: gh for every step at once, into the workspace;
-//   2. dense_bwd_kernel: the recurrence, writing dgi, dh0, dgh's n part
-//      (dgi holds its r and z parts) and per-row dbh sums;
-//   3. gemm: dWh = dgh^T q_in([h0; out[0..T-2]]), K split over T*B, then a sum.
+// t from T-1 to 0 with h_{t-1} = out[t-1] (h0 at t = 0), D_t = dout[t] + the
+// carry from step t+1 is the gradient reaching h_t, and the step's gradients
+// (gru_backward) are linear in D_t with coefficients fixed by the forward:
+//   (dgr, dgz, dgn, dgh_n, dh_direct) = D_t * (Cr, Cz, Cgn, Chn, Zm)_t
+// (q_out's clipped-STE mask is folded into the coefficients), dgh_t =
+// (dgr, dgz, dgh_n), and
+//   D_{t-1} = dout[t-1] + Zm_t D_t + Mi_t (dgh_t Wh),   Mi_t = q_in's mask on h_{t-1}
+//   dh0 = Zm_0 D_0 + Mi_0 (dgh_0 Wh)
+//   dWh = sum_t dgh_t^T q_in(h_{t-1}),  dbh = sum_t sum_b dgh_t
+// Only D_t sits on the recurrence. The launcher runs
+//   0. hq = q_in([h0; out[0..T-2]]) as one [T B, H] block;
+//   1. gemm: gh = hq Wh^T + bh for every step at once;
+//   2. coef_kernel: the coefficient planes from gi, gh and h_{t-1}
+//      (Cr, Cz, Chn overwrite gh in place; Cgn, Zm, Mi in planes of their own);
+//   3. dense_bwd_kernel: the recurrence, writing D_t for every t and dh0;
+//   4. grad_kernel: dgi, dgh_n and per-row dbh sums from D and the planes;
+//   5. gemm: dWh = dgh^T hq, K split over T B, then a sum.
 //
-// The recurrence kernel mirrors the forward's exchange (scan_dense.hip) with
-// the roles of K and the output swapped: the exchanged vector is dgh_t
-// (3H words per batch row) and each compute wave owns a quad of units u of
-// dh_{t-1}, holding the Wh columns of those units over all 3H rows in VGPRs
-// (wt[g][m] = Wh[g H + kmap(m)][u]). Per iteration a compute wave runs one
-// MFMA chain over the three staged dgh segments, reduces the K slices, and
-// the 16 lanes of row 0 finish the step: carry, gate gradients of step t-1,
-// stores, and the tagged publish of dgh_{t-1}. Four poller waves per
-// workgroup stage the next iteration's dgh row (polled) and the per-unit
-// step inputs (gi, gh, dout, out, h0) into LDS. dgh_{T-1} needs no exchange:
-// it depends only on inputs, so the stagers compute it for the whole row.
+// The recurrence kernel has the forward's shape (scan_dense.hip) with the
+// reduction over 3H: the exchanged vector is D_t (H tagged words per batch
+// row, as the forward exchanges h) and each compute wave owns a quad of units
+// u of D_{t-1}, holding the Wh columns of those units over all 3H rows in
+// VGPRs (wt[g][m] = Wh[g H + kmap(m)][u]). The poller waves poll D_t, scale
+// it by the step's coefficients (prefetched while the compute waves work) and
+// stage dgh_t = D_t (Cr, Cz, Chn) into LDS; a compute wave runs one MFMA chain
+// over the three staged segments, reduces the K slices, and the 16 lanes of
+// row 0 form D_{t-1} and publish it.
 #include "gs_gemm.h"
 #include "gs_mfma.h"
 
@@ -34,46 +38,84 @@ namespace gs {
 namespace {
 
 constexpr int kPollers = 4;
-// Per-unit values staged for one iteration (consuming dgh_t):
-//   0 h_{t-1} (q_in mask), 1 dout[t-1], 2..4 gi[t-1] (r, z, n),
-//   5..7 gh[t-1] (r, z, n), 8 h_{t-2}
-constexpr int kNV = 9;
+// Per-unit values staged for the iteration that consumes D_t: 0 Zm_t, 1 Mi_t, 2 dout[t-1]
+constexpr int kNV = 3;
+
+// ---- parallel passes ---------------------------------------------------------------
+
+// For every (t, b, k): gradients of step t per unit D_t (gru_backward with
+// dh = 1). cg [T B, 3H] holds gh on entry and (Cr, Cz, Chn) on exit.
+__global__ void coef_kernel(const float* gi, int64_t sg_t, int64_t sg_b, const float* h0, int64_t sh0_b,
+                            const float* out, int64_t so_t, int64_t so_b, float* cg, float* cgn, float* zm, float* mi,
+                            int T, int B, int H, Quant qin, Quant qout) {
+  const int64_t n = (int64_t)T * B * H;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = e / H;
+    const int k = (int)(e - m * H);
+    const int t = (int)(m / B), b = (int)(m - (int64_t)t * B);
+    const float* g = gi + (int64_t)t * sg_t + (int64_t)b * sg_b + k;
+    float* c = cg + m * 3 * H + k;
+    const float hp = t > 0 ? out[(int64_t)(t - 1) * so_t + (int64_t)b * so_b + k] : h0[(int64_t)b * sh0_b + k];
+    const GateGrad gg = gru_backward(g[0], g[H], g[2 * H], c[0], c[H], c[2 * H], hp, 1.0f, qout);
+    c[0] = gg.dgr;
+    c[H] = gg.dgz;
+    c[2 * H] = gg.dghn;
+    cgn[e] = gg.dgn;
+    zm[e] = gg.dh_direct;
+    mi[e] = (qin.on && !quant_keeps(hp, qin)) ? 0.0f : 1.0f;
+  }
+}
+
+// dgi, dgh_n and per-row partial dbh sums over chunks of kGradSteps steps:
+// thread (chunk, b, k) walks the chunk's steps t.
+constexpr int kGradSteps = 8;
+__global__ void grad_kernel(const float* dsum, const float* cg, const float* cgn, float* dgi, float* dghn,
+                            float* dbh_chunks, int T, int B, int H) {
+  const int64_t per_chunk = (int64_t)B * H;
+  const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int nchunks = (T + kGradSteps - 1) / kGradSteps;
+  if (e >= per_chunk * nchunks) return;
+  const int chunk = (int)(e / per_chunk);
+  const int64_t bk = e - chunk * per_chunk;
+  const int b = (int)(bk / H), k = (int)(bk - (int64_t)b * H);
+  float sr = 0.f, sz = 0.f, sn = 0.f;
+  const int t1 = min(T, (chunk + 1) * kGradSteps);
+  for (int t = chunk * kGradSteps; t < t1; ++t) {
+    const int64_t m = (int64_t)t * B + b;
+    const float D = dsum[m * H + k];
+    const float* c = cg + m * 3 * H + k;
+    float* d = dgi + m * 3 * H + k;
+    const float gr = D * c[0], gz = D * c[H], ghn = D * c[2 * H];
+    d[0] = gr;
+    d[H] = gz;
+    d[2 * H] = D * cgn[m * H + k];
+    dghn[m * H + k] = ghn;
+    sr += gr;
+    sz += gz;
+    sn += ghn;
+  }
+  float* o = dbh_chunks + ((int64_t)chunk * B + b) * 3 * H + k;
+  o[0] = sr;
+  o[H] = sz;
+  o[2 * H] = sn;
+}
+
+// ---- the recurrence ----------------------------------------------------------------
 
 struct BParams {
-  const float* gi;
-  const float* h0;
   const float* w;
-  const float* out;
   const float* dout;  // [T, B, H] contiguous
-  const float* gh;    // [T, B, 3H] contiguous, bias included
-  float* dgi;         // [T, B, 3H] contiguous
-  float* dghn;        // [T, B, H] contiguous
+  const float* cg;    // [T, B, 3H] (Cr, Cz, Chn)
+  const float* zm;    // [T, B, H]
+  const float* mi;    // [T, B, H]
+  float* dsum;        // [T, B, H] D_t
   float* dh0;         // [B, H] contiguous
-  float* dbh_part;    // [B, 3H] contiguous
-  uint64_t* xh;       // [2][Bp][3H] tagged dgh
+  uint64_t* xh;       // [2][Bp][H] tagged D_t
   uint64_t* xw;       // [nwg] tagged XCD ids
   Ctrl ctrl;
-  int64_t sg_t, sg_b, sh0_b, so_t, so_b;
   int T, B, H;
   int ngroups, RB, nrb, Bp, nwg, P, nwc, hsz;
-  Quant qin, qout;
 };
-
-// h_t of row `row` (t >= 0) or h0 (t == -1), unit k.
-__device__ __forceinline__ float h_at(const BParams& p, int t, int row, int k) {
-  return t >= 0 ? p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + k] : p.h0[(int64_t)row * p.sh0_b + k];
-}
-
-// Staged value v of unit k for the iteration that consumes dgh_t.
-__device__ __forceinline__ float step_value(const BParams& p, int t, int row, int k, int v) {
-  if (v == 0) return h_at(p, t - 1, row, k);
-  if (t == 0) return 0.0f;
-  const int tp = t - 1;
-  if (v == 1) return p.dout[((int64_t)tp * p.B + row) * p.H + k];
-  if (v <= 4) return p.gi[(int64_t)tp * p.sg_t + (int64_t)row * p.sg_b + (v - 2) * p.H + k];
-  if (v <= 7) return p.gh[((int64_t)tp * p.B + row) * 3 * p.H + (v - 5) * p.H + k];
-  return h_at(p, t - 2, row, k);
-}
 
 template <int KC>
 __device__ __forceinline__ void load_wt(const float* w, int H, int o0, int j, int kb4, bool ok_q,
@@ -99,6 +141,7 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
   const int j = lane & 3, kb4 = lane >> 2, s = (lane >> 2) & 3;
   const bool lead = lane < 16;
   const int H = p.H, T = p.T;
+  constexpr int MPR = KC / 4;  // polled words per lane per row
 
   const int gid = blockIdx.x % p.ngroups;
   const int pw = blockIdx.x / p.ngroups;
@@ -113,46 +156,41 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
   const int rb_end = min(rb_begin + p.RB, p.nrb);
   const int nrbm = rb_end - rb_begin;
 
-  float* hst = lds;                              // [2][3][hsz] staged dgh (il_index per gate block)
-  float* sti = hst + 6 * p.hsz;                  // [2][4][kNV][U] staged per-unit step inputs
-  float* dd = sti + 2 * 4 * kNV * U;             // [RB][4][U] dh_t * z_t carried to the next step
-  float* dacc = dd + p.RB * 4 * U;               // [RB][4][3][U] running sums of dgh (dbh)
-  int* flags = reinterpret_cast<int*>(dacc + p.RB * 12 * U);  // [0] compute-wave iterations published,
-                                                               // [1] group on one XCD
-  const int lds_floats = 6 * p.hsz + 8 * kNV * U + p.RB * 16 * U + 4;
+  float* hst = lds;                   // [2][3][hsz] staged dgh_t (il_index per gate block)
+  float* sti = hst + 6 * p.hsz;       // [2][4][kNV][U] staged per-unit values
+  float* dd = sti + 2 * 4 * kNV * U;  // [RB][4][U] D_t of this workgroup's units
+  int* flags = reinterpret_cast<int*>(dd + p.RB * 4 * U);  // [0] compute-wave iterations published,
+                                                          // [1] group on one XCD
+  const int lds_floats = 6 * p.hsz + 8 * kNV * U + p.RB * 4 * U + 4;
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
   const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (threadIdx.x == 0) st_tagged(p.xw + blockIdx.x, __uint_as_float(xcc_id()), base + 1u);
   const int niter = T * nrbm;
+  const int64_t BH = (int64_t)p.B * H;
 
-  // dgh_{T-1} of unit k of local row r for iteration nx (< nrbm): computed
-  // from inputs; the owner of unit k also stores its dgi / dgh_n, seeds the
-  // dbh sums and keeps dh_{T-1} z_{T-1}.
+  // Staged value v of unit k of `row` for the iteration consuming D_t.
+  auto step_value = [&](int t, int row, int k, int v) -> float {
+    const int64_t e = (int64_t)t * BH + (int64_t)row * H + k;
+    if (v == 0) return p.zm[e];
+    if (v == 1) return p.mi[e];
+    return t > 0 ? p.dout[e - BH] : 0.0f;
+  };
+  // First iteration of row-block nx: D_{T-1} = dout[T-1] needs no exchange.
   auto stage_first = [&](int nx, int r, int k) {
     const int row = 4 * (rb_begin + nx) + r;
     if (row >= p.B) return;
-    const int t = T - 1;
-    const float* g = p.gi + (int64_t)t * p.sg_t + (int64_t)row * p.sg_b + k;
-    const float* h = p.gh + ((int64_t)t * p.B + row) * 3 * H + k;
-    const float dh = p.dout[((int64_t)t * p.B + row) * H + k];
-    const GateGrad gg = gru_backward(g[0], g[H], g[2 * H], h[0], h[H], h[2 * H], h_at(p, t - 1, row, k), dh, p.qout);
+    const int64_t e = (int64_t)(T - 1) * BH + (int64_t)row * H + k;
+    const float D = p.dout[e];
+    const float* c = p.cg + ((int64_t)(T - 1) * p.B + row) * 3 * H + k;
     float* hs = hst + (nx & 1) * 3 * p.hsz + il_index(r, k);
-    hs[0] = gg.dgr;
-    hs[p.hsz] = gg.dgz;
-    hs[2 * p.hsz] = gg.dghn;
+    hs[0] = D * c[0];
+    hs[p.hsz] = D * c[H];
+    hs[2 * p.hsz] = D * c[2 * H];
     const int u = k - ulo;
     if (u >= 0 && u < U) {
-      float* dgo = p.dgi + ((int64_t)t * p.B + row) * 3 * H + k;
-      dgo[0] = gg.dgr;
-      dgo[H] = gg.dgz;
-      dgo[2 * H] = gg.dgn;
-      p.dghn[((int64_t)t * p.B + row) * H + k] = gg.dghn;
-      dd[(nx * 4 + r) * U + u] = gg.dh_direct;
-      float* da = dacc + (nx * 4 + r) * 3 * U + u;
-      da[0] = gg.dgr;
-      da[U] = gg.dgz;
-      da[2 * U] = gg.dghn;
+      dd[(nx * 4 + r) * U + u] = D;
+      p.dsum[e] = D;
     }
   };
 
@@ -162,7 +200,7 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
   for (int w = threadIdx.x; w < 4 * kNV * U; w += blockDim.x) {
     const int r = w / (kNV * U), rem = w - r * kNV * U, v = rem / U, u = rem - v * U;
     const int row = 4 * rb_begin + r;
-    sti[w] = (row < p.B && ulo + u < H) ? step_value(p, T - 1, row, ulo + u, v) : 0.0f;
+    sti[w] = (row < p.B && ulo + u < H) ? step_value(T - 1, row, ulo + u, v) : 0.0f;
   }
   lds_barrier();
 
@@ -186,41 +224,27 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
           acc1 = __builtin_amdgcn_mfma_f32_4x4x1f32(a[m + 1], wt[G][m + 1], acc1, 0, 0, 0);
         }
       });
-      float via_w = reduce16(acc0 + acc1, s);
+      const float via_w = reduce16(acc0 + acc1, s);
       const bool xcd_local = st >= 1 && __builtin_amdgcn_readfirstlane(flags[1]) != 0;
       if (lead && unit_ok && row < p.B) {
         const float* sv = sti + (buf * 4 + s) * kNV * U + uo;
         float* ddp = dd + (rbl * 4 + s) * U + uo;
-        if (p.qin.on && !quant_keeps(sv[0], p.qin)) via_w = 0.0f;
-        const float carry = *ddp + via_w;
+        float carry;
+        {
+#pragma clang fp contract(off)
+          carry = sv[0] * *ddp + sv[U] * via_w;
+        }
         if (t == 0) {
           p.dh0[(int64_t)row * H + unit] = carry;
         } else {
-          const float dh = sv[U] + carry;
-          const GateGrad gg = gru_backward(sv[2 * U], sv[3 * U], sv[4 * U], sv[5 * U], sv[6 * U], sv[7 * U],
-                                           sv[8 * U], dh, p.qout);
-          const int64_t rowt = (int64_t)(t - 1) * p.B + row;
-          const uint32_t tag = base + (uint32_t)st + 1u;
-          uint64_t* dst = p.xh + ((int64_t)(st & 1) * p.Bp + row) * 3 * H + unit;
-          if (xcd_local) {
-            st_tagged_xcd(dst, gg.dgr, tag);
-            st_tagged_xcd(dst + H, gg.dgz, tag);
-            st_tagged_xcd(dst + 2 * H, gg.dghn, tag);
-          } else {
-            st_tagged(dst, gg.dgr, tag);
-            st_tagged(dst + H, gg.dgz, tag);
-            st_tagged(dst + 2 * H, gg.dghn, tag);
-          }
-          float* dgo = p.dgi + rowt * 3 * H + unit;
-          dgo[0] = gg.dgr;
-          dgo[H] = gg.dgz;
-          dgo[2 * H] = gg.dgn;
-          p.dghn[rowt * H + unit] = gg.dghn;
-          float* da = dacc + (rbl * 4 + s) * 3 * U + uo;
-          da[0] += gg.dgr;
-          da[U] += gg.dgz;
-          da[2 * U] += gg.dghn;
-          *ddp = gg.dh_direct;
+          const float dn = sv[2 * U] + carry;  // D_{t-1}
+          uint64_t* dst = p.xh + ((int64_t)(st & 1) * p.Bp + row) * H + unit;
+          if (xcd_local)
+            st_tagged_xcd(dst, dn, base + (uint32_t)st + 1u);
+          else
+            st_tagged(dst, dn, base + (uint32_t)st + 1u);
+          p.dsum[(int64_t)(t - 1) * BH + (int64_t)row * H + unit] = dn;
+          *ddp = dn;
         }
       }
       if (lane == 0) __hip_atomic_fetch_add(&flags[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -228,9 +252,10 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
     }
   } else {
     // Poller wave pr stages row pr of iteration it + 1 while the compute
-    // waves run iteration it: the per-unit step inputs first (their loads
-    // overlap the poll), then the dgh row, polled once this workgroup's
-    // compute waves have published iteration it.
+    // waves run iteration it: per-unit values and the row's coefficients are
+    // loaded first (their latency overlaps the poll), then D_t is polled once
+    // this workgroup's compute waves have published iteration it, and dgh_t
+    // = D_t (Cr, Cz, Chn) goes to LDS.
     const int pr = wave - nwc;
     constexpr int NWC_MAX = NT / 64 - kPollers;
     constexpr int NSV = (kNV * 4 * NWC_MAX + 63) / 64;  // staged values per lane
@@ -246,18 +271,35 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
         for (int i = 0; i < NSV; ++i) {
           const int w = lane + 64 * i;
           const int v = w / U, u = w - v * U;
-          sv[i] = (w < kNV * U && row < p.B && ulo + u < H) ? step_value(p, t2, row, ulo + u, v) : 0.0f;
+          sv[i] = (w < kNV * U && row < p.B && ulo + u < H) ? step_value(t2, row, ulo + u, v) : 0.0f;
         }
         if (st2 == 0) {
           for (int k = lane; k < H; k += 64) stage_first(nx, pr, k);
         } else if (row < p.B) {
+          const float* crow = p.cg + ((int64_t)t2 * p.B + row) * 3 * H + lane;
+          float cf[3][MPR];
+#pragma unroll
+          for (int m = 0; m < MPR; ++m) {
+            const bool ok = lane + 64 * m < H;
+#pragma unroll
+            for (int g = 0; g < 3; ++g) cf[g][m] = ok ? crow[g * H + 64 * m] : 0.0f;
+          }
           if (pr == 0 && nx == nrbm)  // first exchange of the launch
             flags[1] = (p.P <= 64 && group_on_one_xcd(p.ctrl, p.xw + gid, p.ngroups, p.P, base + 1u)) ? 1 : 0;
           wait_lds_count(p.ctrl, &flags[0], nwc * (it + 1));
-          const uint64_t* hb = p.xh + ((int64_t)((st2 - 1) & 1) * p.Bp + row) * 3 * H;
-          poll_row_segs<KC / 4, 3>(p.ctrl, hb, H, hst + (nx & 1) * 3 * p.hsz, p.hsz, pr, H, base + (uint32_t)st2);
-        } else if (pr == 0 && nx == nrbm) {
-          flags[1] = (p.P <= 64 && group_on_one_xcd(p.ctrl, p.xw + gid, p.ngroups, p.P, base + 1u)) ? 1 : 0;
+          uint64_t v[MPR];
+          const uint32_t valid =
+              poll_row_words<MPR>(p.ctrl, p.xh + ((int64_t)((st2 - 1) & 1) * p.Bp + row) * H, H, base + (uint32_t)st2, v);
+          float* hs = hst + (nx & 1) * 3 * p.hsz;
+          static_for<0, MPR>([&](auto I) {
+            if ((valid >> I) & 1u) {
+              const float D = value_of(v[I]);
+              const int li = il_index(pr, lane + 64 * I);
+              hs[li] = D * cf[0][I];
+              hs[p.hsz + li] = D * cf[1][I];
+              hs[2 * p.hsz + li] = D * cf[2][I];
+            }
+          });
         }
         float* sd = sti + ((nx & 1) * 4 + pr) * kNV * U;
 #pragma unroll
@@ -268,15 +310,6 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
       }
       lds_barrier();
     }
-  }
-
-  // Per-row dbh sums of this workgroup's units.
-  lds_barrier();
-  for (int w = threadIdx.x; w < nrbm * 12 * U; w += blockDim.x) {
-    const int rbl = w / (12 * U), rem = w - rbl * 12 * U, r = rem / (3 * U), rem2 = rem - r * 3 * U;
-    const int g = rem2 / U, u = rem2 - g * U;
-    const int row = 4 * (rb_begin + rbl) + r;
-    if (row < p.B && ulo + u < H) p.dbh_part[(int64_t)row * 3 * H + g * H + ulo + u] = dacc[w];
   }
   leave_grid(p.ctrl, (uint32_t)p.nwg, base, (uint32_t)T);
 }
@@ -294,10 +327,15 @@ BFn pick_bwd(int KC, int* nt) {
   }
 }
 
+// Workspace after the control words, each region 256-byte aligned:
+//   xh [2][Bp][H] tagged D | xw [nrb P] | cg [T B, 3H] | hq, cgn, zm, mi,
+//   dsum, dghn [T B, H] each | dbh chunks [nchunks][B][3H] | dWh split partials
 struct BPlan {
-  int KC, nt, nwc, P, nrb, Bp, hsz, split;
-  int64_t xh_bytes, xw_bytes, gh_bytes, dghn_bytes, part_bytes;
-  int64_t total() const { return kCtrlBytes + xh_bytes + xw_bytes + gh_bytes + dghn_bytes + part_bytes; }
+  int KC, nt, nwc, P, nrb, Bp, hsz, split, nchunks;
+  int64_t xh_bytes, xw_bytes, cg_bytes, plane_bytes, chunk_bytes, part_bytes;
+  int64_t total() const {
+    return kCtrlBytes + xh_bytes + xw_bytes + cg_bytes + 6 * plane_bytes + chunk_bytes + part_bytes;
+  }
 };
 
 int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
@@ -314,12 +352,16 @@ int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
   pl->Bp = 4 * pl->nrb;
   pl->hsz = 64 * pl->KC;
   const int64_t TB = a->T * a->B;
-  if (TB > INT32_MAX) return set_error(GS_ERR_INVALID, "%s: T*B = %lld exceeds 2^31 - 1", who, (long long)TB);
+  if (TB > INT32_MAX / 4) return set_error(GS_ERR_INVALID, "%s: T*B = %lld is too large", who, (long long)TB);
   pl->split = gemm_pick_split(3 * H, H, (int)TB);
-  pl->xh_bytes = align256(2 * (int64_t)pl->Bp * 3 * H * 8 + 16 * pl->KC * 8);
+  pl->nchunks = (int)((a->T + kGradSteps - 1) / kGradSteps);
+  // The pollers load 16 KC words per row from the row's start; the pad keeps
+  // the reads past the last row inside the workspace.
+  pl->xh_bytes = align256(2 * (int64_t)pl->Bp * H * 8 + 16 * pl->KC * 8);
   pl->xw_bytes = align256((int64_t)pl->nrb * pl->P * 8);
-  pl->gh_bytes = align256(TB * 3 * H * 4);
-  pl->dghn_bytes = align256(TB * H * 4);
+  pl->cg_bytes = align256(TB * 3 * H * 4);
+  pl->plane_bytes = align256(TB * H * 4);
+  pl->chunk_bytes = align256((int64_t)pl->nchunks * a->B * 3 * H * 4);
   pl->part_bytes = pl->split > 1 ? align256((int64_t)pl->split * 3 * H * H * 4) : 0;
   return GS_OK;
 }
@@ -355,20 +397,38 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
 
   const int T = (int)a->T, B = (int)a->B, H = (int)a->H, TB = T * B;
   char* ws = static_cast<char*>(a->workspace);
-  uint64_t* xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
-  uint64_t* xw = reinterpret_cast<uint64_t*>(ws + kCtrlBytes + pl.xh_bytes);
-  float* gh = reinterpret_cast<float*>(ws + kCtrlBytes + pl.xh_bytes + pl.xw_bytes);
-  float* dghn = reinterpret_cast<float*>(reinterpret_cast<char*>(gh) + pl.gh_bytes);
-  float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(dghn) + pl.dghn_bytes);
+  char* cur = ws + kCtrlBytes;
+  auto take = [&](int64_t bytes) {
+    char* r = cur;
+    cur += bytes;
+    return r;
+  };
+  uint64_t* xh = reinterpret_cast<uint64_t*>(take(pl.xh_bytes));
+  uint64_t* xw = reinterpret_cast<uint64_t*>(take(pl.xw_bytes));
+  float* cg = reinterpret_cast<float*>(take(pl.cg_bytes));
+  float* hq = reinterpret_cast<float*>(take(pl.plane_bytes));
+  float* cgn = reinterpret_cast<float*>(take(pl.plane_bytes));
+  float* zm = reinterpret_cast<float*>(take(pl.plane_bytes));
+  float* mi = reinterpret_cast<float*>(take(pl.plane_bytes));
+  float* dsum = reinterpret_cast<float*>(take(pl.plane_bytes));
+  float* dghn = reinterpret_cast<float*>(take(pl.plane_bytes));
+  float* chunks = reinterpret_cast<float*>(take(pl.chunk_bytes));
+  float* part = reinterpret_cast<float*>(take(pl.part_bytes));
+  const Quant qin = to_quant(a->q_in), qout = to_quant(a->q_out);
+  const int64_t n_plane = (int64_t)TB * H;
+  auto grid1d = [](int64_t n) { return dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)); };
 
-  // q_in([h0; out[0..T-2]]) as rows m = t B + b of a [T B, H] matrix.
-  GemmOperand hq{a->out, a->so_b, 1, a->h0, a->sh0_b, B, to_quant(a->q_in)};
+  // 0. hq = q_in([h0; out[0..T-2]]): rows m = t B + b of a [T B, H] matrix
+  rc = build_prev_state(hq, a->h0, a->sh0_b, a->out, a->so_b, T, B, H, qin, stream, who);
+  if (rc) return rc;
 
-  // 1. gh = hq Wh^T + bh  -> [T B, 3H]
+  // 1. gh = hq Wh^T + bh  -> cg [T B, 3H]
   GemmArgs g1;
   g1.a = hq;
-  g1.b = plain_operand(a->w, 1, H);  // B(k, n) = Wh[n][k]
-  g1.c = gh;
+  g1.lda = H;
+  g1.b = a->w;  // B(k, n) = Wh[n][k]
+  g1.ldb = H;
+  g1.c = cg;
   g1.ldc = 3 * H;
   g1.split_stride = 0;
   g1.bias = a->bh;
@@ -376,10 +436,16 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
   g1.N = 3 * H;
   g1.K = H;
   g1.ksplit = 1;
+  g1.layout = kGemmNT;
   rc = gemm_f32(g1, stream, who);
   if (rc) return rc;
 
-  // 2. the recurrence
+  // 2. coefficient planes
+  hipLaunchKernelGGL(coef_kernel, grid1d(n_plane), dim3(256), 0, stream, a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b,
+                     a->out, a->so_t, a->so_b, cg, cgn, zm, mi, T, B, H, qin, qout);
+  GS_CHECK_HIP(hipGetLastError());
+
+  // 3. the recurrence
   int nt = 0;
   BFn fn = pick_bwd(pl.KC, &nt);
   const int threads = 64 * (pl.nwc + kPollers);
@@ -389,7 +455,7 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
     RB = (pl.nrb + G - 1) / G;
     G = (pl.nrb + RB - 1) / RB;
     const int U = 4 * pl.nwc;
-    lds = sizeof(float) * (size_t)(6 * pl.hsz + 8 * kNV * U + RB * 16 * U + 4);
+    lds = sizeof(float) * (size_t)(6 * pl.hsz + 8 * kNV * U + RB * 4 * U + 4);
     if (lds > 65536)
       GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     int gfit = 0;
@@ -399,24 +465,16 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
     G = gfit;
   }
   BParams p;
-  p.gi = a->gi;
-  p.h0 = a->h0;
   p.w = a->w;
-  p.out = a->out;
   p.dout = a->dout;
-  p.gh = gh;
-  p.dgi = a->dgi;
-  p.dghn = dghn;
+  p.cg = cg;
+  p.zm = zm;
+  p.mi = mi;
+  p.dsum = dsum;
   p.dh0 = a->dh0;
-  p.dbh_part = a->dbh_part;
   p.xh = xh;
   p.xw = xw;
   p.ctrl = ctrl_of(ws);
-  p.sg_t = a->sg_t;
-  p.sg_b = a->sg_b;
-  p.sh0_b = a->sh0_b;
-  p.so_t = a->so_t;
-  p.so_b = a->so_b;
   p.T = T;
   p.B = B;
   p.H = H;
@@ -428,18 +486,26 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
   p.nwg = G * pl.P;
   p.nwc = pl.nwc;
   p.hsz = pl.hsz;
-  p.qin = to_quant(a->q_in);
-  p.qout = to_quant(a->q_out);
   hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), lds, stream, p);
   GS_CHECK_HIP(hipGetLastError());
 
-  // 3. dWh[n][k] = sum_m dgh[m][n] hq[m][k]: rows [0, 2H) from dgi's r and z
+  // 4. dgi, dgh_n, per-row dbh
+  const int64_t n_grad = (int64_t)pl.nchunks * B * H;
+  hipLaunchKernelGGL(grad_kernel, dim3((unsigned)((n_grad + 255) / 256)), dim3(256), 0, stream, dsum, cg, cgn, a->dgi,
+                     dghn, chunks, T, B, H);
+  GS_CHECK_HIP(hipGetLastError());
+  rc = sum_partials(a->dbh_part, chunks, (int64_t)B * 3 * H, pl.nchunks, (int64_t)B * 3 * H, stream, who);
+  if (rc) return rc;
+
+  // 5. dWh[n][k] = sum_m dgh[m][n] hq[m][k]: rows [0, 2H) from dgi's r and z
   //    parts, rows [2H, 3H) from dgh_n.
   float* dst = pl.split > 1 ? part : a->dw_part;
   const int64_t split_stride = (int64_t)3 * H * H;
   GemmArgs g3;
-  g3.a = plain_operand(a->dgi, 1, 3 * H);  // A(n, m) = dgi[m][n]
-  g3.b = hq;
+  g3.a = a->dgi;  // A(n, m) = dgi[m][n]
+  g3.lda = 3 * H;
+  g3.b = hq;  // B(m, k) = hq[m][k]
+  g3.ldb = H;
   g3.c = dst;
   g3.ldc = H;
   g3.split_stride = split_stride;
@@ -448,9 +514,11 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
   g3.N = H;
   g3.K = TB;
   g3.ksplit = pl.split;
+  g3.layout = kGemmTN;
   rc = gemm_f32(g3, stream, who);
   if (rc) return rc;
-  g3.a = plain_operand(dghn, 1, H);
+  g3.a = dghn;
+  g3.lda = H;
   g3.c = dst + (int64_t)2 * H * H;
   g3.M = H;
   rc = gemm_f32(g3, stream, who);

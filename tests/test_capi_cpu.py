@@ -153,20 +153,21 @@ def test_dense_bwd_rejects_strided_out_and_missing_workspace():
 
 
 def test_bwd_workspace_sizes():
-    """Dense: control words, double-buffered tagged dgh rows (3H words per
-    padded row) plus pad, one XCD word per workgroup, gh [T B, 3H], dgh_n
-    [T B, H] and the K-split partials of dWh; diagonal needs none."""
+    """Dense: control words, double-buffered tagged D rows (H words per padded
+    row) plus pad, one XCD word per workgroup, the coefficient block
+    [T B, 3H], six [T B, H] planes, per-chunk dbh sums and the K-split
+    partials of dWh; diagonal needs none."""
     lib = _lib.load()
     al = lambda x: (x + 255) // 256 * 256  # noqa: E731
     T, B, H = 64, 32, 512
     a = _bwd_args(T=T, B=B, H=H)
     kc = 32
-    nwc, P = 4, 128 // 4
+    P = 128 // 4
     tiles = (3 * H // 64) * (H // 64)
     split = min(-(-512 // tiles), -(-(T * B) // 256))
-    want = (256 + al(2 * B * 3 * H * 8 + 16 * kc * 8) + al((B // 4) * P * 8) + al(T * B * 3 * H * 4)
-            + al(T * B * H * 4) + (al(split * 3 * H * H * 4) if split > 1 else 0))
-    assert nwc == 4
+    nchunks = -(-T // 8)
+    want = (256 + al(2 * B * H * 8 + 16 * kc * 8) + al((B // 4) * P * 8) + al(T * B * 3 * H * 4)
+            + 6 * al(T * B * H * 4) + al(nchunks * B * 3 * H * 4) + (al(split * 3 * H * H * 4) if split > 1 else 0))
     assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == want
     assert lib.gs_bwd_workspace_bytes(_lib.KIND_DIAGONAL, ctypes.byref(a)) == 0
     assert lib.gs_bwd_workspace_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) == _lib.GS_ERR_INVALID
