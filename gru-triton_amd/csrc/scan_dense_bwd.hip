@@ -368,28 +368,24 @@ int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
 
 }  // namespace
 
-int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a) {
+int64_t dense_bwd_core_bytes(const gs_bwd_args* a, const char* who) {
   BPlan pl;
-  const int rc = plan_bwd(a, &pl, "gs_bwd_workspace_bytes");
+  const int rc = plan_bwd(a, &pl, who);
   if (rc) return rc;
   return pl.total();
 }
 
-}  // namespace gs
+int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a) { return dense_bwd_core_bytes(a, "gs_bwd_workspace_bytes"); }
 
-extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
-  using namespace gs;
-  clear_error();
-  const char* who = "gs_dense_bwd";
-  int rc = validate_bwd_common(a, who);
-  if (rc) return rc;
-  if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
-  if (a->dw_part == nullptr) return set_error(GS_ERR_INVALID, "%s: dw_part must be a non-NULL device pointer", who);
+// The dense backward of a hidden map given as the matrix w [3H, H] (rows r,
+// z, n); writes dgi, dh0 and dbh_part of `a` and the map's gradient dw
+// [3H, H]. Uses the first dense_bwd_core_bytes(a) bytes of a->workspace.
+int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t stream, const char* who) {
   if (a->T > 1 && a->so_t != a->B * a->so_b)
     return set_error(GS_ERR_INVALID, "%s: out must hold its steps back to back (so_t == B * so_b); got so_t=%lld, so_b=%lld",
                      who, (long long)a->so_t, (long long)a->so_b);
   BPlan pl;
-  rc = plan_bwd(a, &pl, who);
+  int rc = plan_bwd(a, &pl, who);
   if (rc) return rc;
   const gs_args f = fwd_view(*a);
   rc = check_workspace(&f, pl.total(), who);
@@ -426,7 +422,7 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
   GemmArgs g1;
   g1.a = hq;
   g1.lda = H;
-  g1.b = a->w;  // B(k, n) = Wh[n][k]
+  g1.b = w;  // B(k, n) = Wh[n][k]
   g1.ldb = H;
   g1.c = cg;
   g1.ldc = 3 * H;
@@ -465,7 +461,7 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
     G = gfit;
   }
   BParams p;
-  p.w = a->w;
+  p.w = w;
   p.dout = a->dout;
   p.cg = cg;
   p.zm = zm;
@@ -499,7 +495,7 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
 
   // 5. dWh[n][k] = sum_m dgh[m][n] hq[m][k]: rows [0, 2H) from dgi's r and z
   //    parts, rows [2H, 3H) from dgh_n.
-  float* dst = pl.split > 1 ? part : a->dw_part;
+  float* dst = pl.split > 1 ? part : dw;
   const int64_t split_stride = (int64_t)3 * H * H;
   GemmArgs g3;
   g3.a = a->dgi;  // A(n, m) = dgi[m][n]
@@ -523,6 +519,19 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
   g3.M = H;
   rc = gemm_f32(g3, stream, who);
   if (rc) return rc;
-  if (pl.split > 1) return sum_partials(a->dw_part, part, split_stride, pl.split, split_stride, stream, who);
+  if (pl.split > 1) return sum_partials(dw, part, split_stride, pl.split, split_stride, stream, who);
   return GS_OK;
+}
+
+}  // namespace gs
+
+extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_dense_bwd";
+  int rc = validate_bwd_common(a, who);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
+  if (a->dw_part == nullptr) return set_error(GS_ERR_INVALID, "%s: dw_part must be a non-NULL device pointer", who);
+  return dense_bwd_core(a, a->w, a->dw_part, stream, who);
 }

@@ -35,6 +35,8 @@ EXPORTS = (
     "gs_butterfly_fwd_generic",
     "gs_diagonal_bwd",
     "gs_dense_bwd",
+    "gs_monarch_bwd",
+    "gs_butterfly_bwd",
     "gs_workspace_bytes",
     "gs_bwd_workspace_bytes",
     "gs_workspace_status",
@@ -95,6 +97,7 @@ class GsBwdArgs(ctypes.Structure):
         ("dgi", ctypes.c_void_p),
         ("dh0", ctypes.c_void_p),
         ("dw_part", ctypes.c_void_p),
+        ("dw2_part", ctypes.c_void_p),
         ("dbh_part", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_int64),
@@ -138,7 +141,7 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(GsArgs), ctypes.c_void_p]
             fn.restype = ctypes.c_int
-        for name in ("gs_diagonal_bwd", "gs_dense_bwd"):
+        for name in ("gs_diagonal_bwd", "gs_dense_bwd", "gs_monarch_bwd", "gs_butterfly_bwd"):
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(GsBwdArgs), ctypes.c_void_p]
             fn.restype = ctypes.c_int
@@ -274,6 +277,7 @@ def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w
                w2: Optional[torch.Tensor], bh: torch.Tensor, out: torch.Tensor, dout: torch.Tensor,
                dgi: torch.Tensor, dh0: torch.Tensor, dw_part: Optional[torch.Tensor],
                dbh_part: torch.Tensor, h_in_quant: QuantTuple, h_out_quant: QuantTuple,
+               dw2_part: Optional[torch.Tensor] = None,
                nblocks: int = 0, blksz: int = 0, log_n: int = 0, bfly_nblocks: int = 0) -> None:
     """Fill gs_bwd_args from fp32 device tensors (dout, dgi, dh0 and the
     partials contiguous) and call a backward entry point on the current torch
@@ -287,6 +291,7 @@ def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w
     a.bh, a.out, a.dout = bh.data_ptr(), out.data_ptr(), dout.data_ptr()
     a.dgi, a.dh0 = dgi.data_ptr(), dh0.data_ptr()
     a.dw_part = dw_part.data_ptr() if dw_part is not None else None
+    a.dw2_part = dw2_part.data_ptr() if dw2_part is not None else None
     a.dbh_part = dbh_part.data_ptr()
     a.T, a.B, a.H = T, B, threeH // 3
     a.sg_t, a.sg_b = gi.stride(0), gi.stride(1)

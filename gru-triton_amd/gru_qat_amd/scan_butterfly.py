@@ -18,7 +18,6 @@ from typing import Any, Tuple, cast
 import torch
 
 from . import _lib
-from ._backward import scan_backward
 from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
 
 
@@ -83,31 +82,32 @@ def gru_scan_butterfly_forward_generic(gi, h0, twiddles, bh_cat, *, h_in_quant: 
                     bh_cat, h_in_quant, h_out_quant)
 
 
-def butterfly_gh(hq: torch.Tensor, twiddles: torch.Tensor) -> torch.Tensor:
-    """Hidden projection without bias, [B, 3H], as torch ops (for the backward)."""
-    B, H = hq.shape
-    _, nblocks, L, n2, _, _ = twiddles.shape
-    N = 2 * n2
-    x = torch.zeros(B, 3, N, dtype=hq.dtype, device=hq.device)
-    x = x + torch.nn.functional.pad(hq, (0, N - H)).unsqueeze(1)
-    i = torch.arange(N, device=hq.device)
-    for c in range(nblocks):
-        for s in range(L):
-            ls = s if c % 2 == 0 else L - 1 - s
-            stride = 1 << ls
-            m = (i >> ls) & 1
-            pair = (i >> (ls + 1)) * stride + (i & (stride - 1))
-            tw = twiddles[:, c, s]  # [3, N/2, 2, 2]
-            t_ss = tw[:, pair, m, m]
-            t_sp = tw[:, pair, m, 1 - m]
-            x = t_ss.unsqueeze(0) * x + t_sp.unsqueeze(0) * x[:, :, i ^ stride]
-    return x[:, :, :H].reshape(B, 3 * H)
-
-
 def gru_scan_butterfly_backward(gi, h0, twiddles, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None):
-    dgi, dh0, (dtw,), dbh = scan_backward(gi, h0, out, dout, butterfly_gh, [twiddles], bh_cat,
-                                          h_in_quant, h_out_quant)
-    return dgi, dh0, dtw, dbh
+    """Gradients (dgi, dh0, dtwiddles, dbh_cat) of the butterfly scan
+    (reference backward: scan_butterfly.py:462-1075).
+
+    ``gs_butterfly_bwd`` materializes the map as a [3H, H] matrix, runs the
+    dense backward with it and carries the matrix gradient back through the
+    twiddle stages; dbh comes back as per-row partials summed here.
+    """
+    who = "gru_scan_butterfly_backward"
+    require_cuda(who, gi=gi, h0=h0, twiddles=twiddles, bh_cat=bh_cat, out=out, dout=dout)
+    require_f32(who, gi=gi, h0=h0, twiddles=twiddles, bh_cat=bh_cat, out=out, dout=dout)
+    T, B, H = check_common(who, gi, h0, bh_cat)
+    nblocks, log_n = check_twiddles(twiddles, H)
+    if tuple(out.shape) != (T, B, H) or tuple(dout.shape) != (T, B, H):
+        raise ValueError(f"out and dout must be (T, B, H)=({T}, {B}, {H})")
+    gi, h0, out = gi.contiguous(), h0.contiguous(), out.contiguous()
+    twiddles, bh_cat, dout = twiddles.contiguous(), bh_cat.contiguous(), dout.contiguous()
+    dgi = torch.empty((T, B, 3 * H), device=gi.device, dtype=gi.dtype)
+    dh0 = torch.empty((B, H), device=gi.device, dtype=gi.dtype)
+    dtw = torch.empty_like(twiddles)
+    dbh_part = torch.empty((B, 3 * H), device=gi.device, dtype=gi.dtype)
+    _lib.launch_bwd(_lib.KIND_BUTTERFLY, "gs_butterfly_bwd", gi=gi, h0=h0, w=twiddles, w2=None, bh=bh_cat, out=out,
+                    dout=dout, dgi=dgi, dh0=dh0, dw_part=dtw, dbh_part=dbh_part,
+                    h_in_quant=check_quant(h_in_quant, "h_in_quant"),
+                    h_out_quant=check_quant(h_out_quant, "h_out_quant"), log_n=log_n, bfly_nblocks=nblocks)
+    return dgi, dh0, dtw, dbh_part.sum(0)
 
 
 class GRUScanButterflyTritonFunction(torch.autograd.Function):

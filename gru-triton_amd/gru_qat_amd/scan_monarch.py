@@ -20,7 +20,6 @@ from typing import Any, Optional, Tuple, cast
 import torch
 
 from . import _lib
-from ._backward import scan_backward
 from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
 
 
@@ -89,24 +88,42 @@ def gru_scan_monarch_forward(
 gru_scan_monarch_forward_triton = gru_scan_monarch_forward
 
 
-def monarch_gh(hq: torch.Tensor, Wh_struct: torch.Tensor, Wh_struct2: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Hidden projection without bias, [B, 3H] (device-agnostic torch ops)."""
-    B, H = hq.shape
-    _, nb, bs, _ = Wh_struct.shape
-    z = torch.einsum("bni,gnoi->bgno", hq.reshape(B, nb, bs), Wh_struct)  # [B, 3, nb, bs]
-    if Wh_struct2 is None:
-        return z.reshape(B, 3 * H)
-    u = z.reshape(B, 3, nb, bs).transpose(2, 3).reshape(B, 3, nb, bs)  # P z, viewed as blocks
-    v = torch.einsum("bgni,gnoi->bgno", u, Wh_struct2)
-    y = v.reshape(B, 3, bs, nb).transpose(2, 3).reshape(B, 3 * H)  # P^T v
-    return y
-
-
 def gru_scan_monarch_backward(gi, h0, Wh_struct, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None,
                               Wh_struct2=None):
-    params = [Wh_struct] if Wh_struct2 is None else [Wh_struct, Wh_struct2]
-    dgi, dh0, dps, dbh = scan_backward(gi, h0, out, dout, monarch_gh, params, bh_cat, h_in_quant, h_out_quant)
-    return dgi, dh0, dps, dbh
+    """Gradients (dgi, dh0, [dWh_struct(, dWh_struct2)], dbh_cat) of the
+    Monarch scan (reference backward: scan_monarch.py:409-884 and :955-1053).
+
+    ``gs_monarch_bwd`` materializes the (one- or two-factor) map as a [3H, H]
+    matrix, runs the dense backward with it and carries the matrix gradient
+    onto the factors; dbh comes back as per-row partials summed here.
+    """
+    who = "gru_scan_monarch_backward"
+    require_cuda(who, gi=gi, h0=h0, Wh_struct=Wh_struct, bh_cat=bh_cat, out=out, dout=dout)
+    require_f32(who, gi=gi, h0=h0, Wh_struct=Wh_struct, bh_cat=bh_cat, out=out, dout=dout)
+    T, B, H = check_common(who, gi, h0, bh_cat)
+    nblocks, blksz = _check_struct("Wh_struct", Wh_struct, H)
+    if Wh_struct2 is not None:
+        require_cuda(who, gi=gi, Wh_struct2=Wh_struct2)
+        require_f32(who, Wh_struct2=Wh_struct2)
+        if tuple(Wh_struct2.shape) != tuple(Wh_struct.shape):
+            raise ValueError(f"Wh_struct2 shape must equal Wh_struct's {tuple(Wh_struct.shape)}; "
+                             f"got {tuple(Wh_struct2.shape)}")
+        Wh_struct2 = Wh_struct2.contiguous()
+    if tuple(out.shape) != (T, B, H) or tuple(dout.shape) != (T, B, H):
+        raise ValueError(f"out and dout must be (T, B, H)=({T}, {B}, {H})")
+    gi, h0, out = gi.contiguous(), h0.contiguous(), out.contiguous()
+    Wh_struct, bh_cat, dout = Wh_struct.contiguous(), bh_cat.contiguous(), dout.contiguous()
+    dgi = torch.empty((T, B, 3 * H), device=gi.device, dtype=gi.dtype)
+    dh0 = torch.empty((B, H), device=gi.device, dtype=gi.dtype)
+    dW = torch.empty_like(Wh_struct)
+    dW2 = torch.empty_like(Wh_struct2) if Wh_struct2 is not None else None
+    dbh_part = torch.empty((B, 3 * H), device=gi.device, dtype=gi.dtype)
+    _lib.launch_bwd(_lib.KIND_MONARCH, "gs_monarch_bwd", gi=gi, h0=h0, w=Wh_struct, w2=Wh_struct2, bh=bh_cat,
+                    out=out, dout=dout, dgi=dgi, dh0=dh0, dw_part=dW, dw2_part=dW2, dbh_part=dbh_part,
+                    h_in_quant=check_quant(h_in_quant, "h_in_quant"),
+                    h_out_quant=check_quant(h_out_quant, "h_out_quant"), nblocks=nblocks, blksz=blksz)
+    dps = [dW] if dW2 is None else [dW, dW2]
+    return dgi, dh0, dps, dbh_part.sum(0)
 
 
 class GRUScanMonarchFunction(torch.autograd.Function):

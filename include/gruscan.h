@@ -145,7 +145,9 @@ typedef struct gs_bwd_args {
   float* dgi;         /* [T, B, 3H] contiguous: gradient of gi                        */
   float* dh0;         /* [B, H] contiguous: gradient of h0                            */
   float* dw_part;     /* diagonal: [B, 3, H] per-row partial gradient of Wh_diag;      *
-                       * dense: [3H, H] gradient of Wh_cat                             */
+                       * dense: [3H, H] gradient of Wh_cat; Monarch: [3, nb, bs, bs]   *
+                       * gradient of w; butterfly: gradient of the twiddles           */
+  float* dw2_part;    /* two-factor Monarch: [3, nb, bs, bs] gradient of w2, else NULL */
   float* dbh_part;    /* [B, 3H] per-row partial gradient of bh                       */
   void* workspace;
   int64_t workspace_bytes;
@@ -164,6 +166,14 @@ int gs_diagonal_bwd(const gs_bwd_args* args, hipStream_t stream);
  * args) bytes, 256-byte aligned, zeroed before its first use (like the
  * forward's, it may be shared with forward launches on the same stream). */
 int gs_dense_bwd(const gs_bwd_args* args, hipStream_t stream);
+
+/* Monarch and butterfly backward (reference scan_monarch.py:409-884 and
+ * scan_butterfly.py:462-1075). Both hidden maps are linear in q_in(h), so the
+ * map is materialized as a [3H, H] matrix and run through the dense backward;
+ * its [3H, H] gradient is then carried onto the structured parameters
+ * (dw_part, and dw2_part for a two-factor Monarch). H <= 1024. */
+int gs_monarch_bwd(const gs_bwd_args* args, hipStream_t stream);
+int gs_butterfly_bwd(const gs_bwd_args* args, hipStream_t stream);
 
 /* Scratch bytes a backward entry point needs (0 for the diagonal kind). Pure
  * host arithmetic. Negative on error. */

@@ -54,6 +54,8 @@ CASES = [
     (0, (67, 9, 200), None, False), (0, (1, 2, 8), None, False),
     (1, (64, 32, 512), None, False), (1, (5, 37, 1000), None, False), (1, (3, 2, 8), None, False),
     (1, (1, 3, 16), None, False), (1, (7, 6, 128), None, False),
+    (3, (16, 8, 512), 8, True), (3, (8, 6, 128), 8, False), (3, (5, 9, 96), 3, True),
+    (4, (8, 6, 512), None, False), (4, (3, 2, 1000), None, False),
 ]
 
 
