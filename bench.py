@@ -4,7 +4,9 @@
     python bench.py --copy-mib N [--steps K]   # counter calibration, see below
 
 A step is one forward scan (the drop-in ``gru_scan_*`` call) over one batch
-of synthetic input already resident in HBM. The headline line is the dense
+of synthetic input already resident in HBM. A second table, "train_step_ms",
+times full training steps (input GEMM, scan, loss, backward) per hidden kind
+at the shape of the reference's published train-step table. The headline line is the dense
 fp32 scan at T=64, B=32, H=512 (config 1, the configuration the metric is
 quoted on); the other four configurations are measured in the same run and
 reported under "kinds".
@@ -121,6 +123,77 @@ def time_kind(idx: int, steps: int, warmup: int, dev) -> dict:
     }
 
 
+# The reference's published train-step table (README.md:163-176; fp32 at
+# T=64, B=32, H=512 on an RTX 2000 Ada): variant -> ms/iter.
+PUBLISHED_TRAIN_MS = {"dense": 8.8, "monarch_nb4": 5.8, "monarch_nb8": 2.0, "butterfly": 20.3, "diagonal": 1.1}
+
+
+def train_steps(dev, iters: int, warmup: int) -> dict:
+    """One training step per variant, as the reference's bench_triton_train.py
+    (:125-137) times it: gi = F.linear(x, Wi, bi), the differentiable scan,
+    loss = sum(out^2), backward into Wi, bi and the hidden parameters; the
+    median over iterations of the synchronised host time. Shape (64, 32, 512),
+    fp32, input size H, random weights of the reference's initial ranges."""
+    import math
+
+    import torch
+    import torch.nn.functional as F
+
+    import gru_qat_amd as G
+    from gru_qat_amd.configs import Q_INT8_HIDDEN
+
+    T, B, H = 64, 32, 512
+    gen = torch.Generator().manual_seed(0)
+    k = 1.0 / math.sqrt(H)
+
+    def u(*shape, bound=k):
+        return ((torch.rand(shape, generator=gen) * 2 - 1) * bound).to(dev)
+
+    x = (torch.randn((T, B, H), generator=gen) * 0.1).to(dev)
+    h0 = (torch.randn((B, H), generator=gen) * 0.1).to(dev)
+    Wi, bi, bh = u(3 * H, H), u(3 * H), u(3 * H)
+    variants = {
+        "dense": ([u(3 * H, H)], lambda gi, p, q: G.gru_scan_persistent(gi, h0, p[0], p[-1], h_in_quant=q,
+                                                                         h_out_quant=q), None),
+        "dense_int8_qat": ([u(3 * H, H)], lambda gi, p, q: G.gru_scan_persistent(gi, h0, p[0], p[-1], h_in_quant=q,
+                                                                                  h_out_quant=q), Q_INT8_HIDDEN),
+        "monarch_nb4": ([u(3, 4, H // 4, H // 4, bound=1 / math.sqrt(H // 4))],
+                        lambda gi, p, q: G.gru_scan_monarch(gi, h0, p[0], p[-1], h_in_quant=q, h_out_quant=q), None),
+        "monarch_nb8": ([u(3, 8, H // 8, H // 8, bound=1 / math.sqrt(H // 8))],
+                        lambda gi, p, q: G.gru_scan_monarch(gi, h0, p[0], p[-1], h_in_quant=q, h_out_quant=q), None),
+        "butterfly": ([(torch.randn((3, 1, 9, H // 2, 2, 2), generator=gen) * math.sqrt(0.5)).to(dev)],
+                      lambda gi, p, q: G.gru_scan_butterfly_triton(gi, h0, p[0], p[-1], h_in_quant=q, h_out_quant=q),
+                      None),
+        "diagonal": ([u(3, H)], lambda gi, p, q: G.gru_scan_diagonal(gi, h0, p[0], p[-1], h_in_quant=q,
+                                                                       h_out_quant=q), None),
+    }
+    res = {}
+    for name, (hidden, scan, q) in variants.items():
+        params = [torch.nn.Parameter(t.clone()) for t in [Wi, bi] + hidden + [bh]]
+
+        def step():
+            for prm in params:
+                prm.grad = None
+            gi = F.linear(x, params[0], params[1])
+            out = scan(gi, params[2:], q)
+            out.pow(2).sum().backward()
+
+        for _ in range(warmup):
+            step()
+        samples = []
+        for _ in range(iters):
+            torch.cuda.synchronize(dev)
+            t0 = time.perf_counter()
+            step()
+            torch.cuda.synchronize(dev)
+            samples.append((time.perf_counter() - t0) * 1e3)
+        ms = statistics.median(samples)
+        pub = PUBLISHED_TRAIN_MS.get(name)
+        res[name] = {"ms": round(ms, 4), "reference_ms_rtx2000ada": pub,
+                     "speedup_vs_reference_hw": round(pub / ms, 1) if pub else None}
+    return res
+
+
 def cpu_baseline(idx: int, budget_s: float) -> dict:
     import torch
 
@@ -164,6 +237,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=4.0, help="seconds of CPU baseline per kind")
     ap.add_argument("--copy-mib", type=int, default=0, help="run a plain N MiB copy K times and exit")
+    ap.add_argument("--no-train", action="store_true", help="skip the train-step table")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -198,6 +272,11 @@ def main() -> int:
         print(f"[bench] config {idx} ...", file=sys.stderr, flush=True)
         results[idx] = time_kind(idx, args.steps, args.warmup, dev)
         print(f"[bench] config {idx}: {json.dumps(results[idx])}", file=sys.stderr, flush=True)
+    train = None
+    if not args.no_train:
+        print("[bench] train steps ...", file=sys.stderr, flush=True)
+        train = train_steps(dev, iters=30, warmup=10)
+        print(f"[bench] train steps: {json.dumps(train)}", file=sys.stderr, flush=True)
     faults = gru_qat_amd.workspace_faults(dev)
 
     cpu = {}
@@ -230,6 +309,7 @@ def main() -> int:
         "roofline": r["roofline"],
         "cpu_baseline": cpu.get(head),
         "kinds": {str(k): v for k, v in results.items()},
+        "train_step_ms": train,
         "device": {"name": props.name, "cus": props.multi_processor_count, "host_cpu": cpu_model(),
                    "host_cores": os.cpu_count()},
         "exchange_faults": faults,

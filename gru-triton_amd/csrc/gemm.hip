@@ -12,15 +12,16 @@
 // loads are in flight while the current one feeds the MFMAs. Global loads are
 // float4 along each operand's contiguous dimension when the shapes allow it
 // (scalar otherwise), and land in LDS without transposition:
-//   NT: S[row][k], row stride 36. The 16 lanes of k-group q read
-//       k = 8 q + s (s < 8) of their row as two float4 (36 = 4 mod 64 x 9
-//       puts the 16 rows x 4 words in distinct banks).
-//   TN: S[k][row], row stride 80. MFMA s reads k = q + 4 s: the four
-//       k-groups sit 80 = 16 mod 64 words apart, so the 64 lanes' reads hit
-//       64 distinct banks.
-// Any bijection between (MFMA step, k-group) and k is valid as long as A and
-// B use the same one; each layout picks the one its LDS order reads
-// conflict-free.
+//   k-contiguous operand: S[row][k], row stride 36;
+//   row-contiguous operand: S[k][row], row stride 80.
+// When both operands are k-contiguous (NT), the 16 lanes of k-group q read
+// k = 8 q + s (s < 8) of their row as two float4 (36 = 4 mod 64 x 9 puts the
+// 16 rows x 4 words in distinct banks). Otherwise MFMA s reads k = q + 4 s
+// as single words: from S[k][row] the four k-groups sit 80 = 16 mod 64 words
+// apart, and from S[row][k] the 16 rows x 4 k-groups land on 36 r + q, all
+// distinct mod 64; either way the 64 lanes hit 64 banks. Any bijection
+// between (MFMA step, k-group) and k is valid as long as A and B use the same
+// one.
 //
 // MFMA operand layout (16x16x4 f32): lane l supplies A[i = l % 16][k-group
 // l / 16] and B[k-group l / 16][j = l % 16]; D VGPR v of lane l is
@@ -40,7 +41,7 @@ typedef float f4v __attribute__((ext_vector_type(4)));
 
 // Loads of one operand tile (64 rows of the output dimension x 32 k) into
 // registers, then into LDS. KC: the operand is contiguous along k.
-template <bool KC, bool VEC>
+template <bool KC, bool VEC, bool QUANT>
 struct TileLoader {
   // VEC: 2 float4 per thread; scalar: 8 floats per thread.
   static constexpr int N = VEC ? 2 : 8;
@@ -49,6 +50,7 @@ struct TileLoader {
   int64_t ld;
   int lim_row, lim_k;  // rows < lim_row, k < lim_k (absolute)
   int row0;
+  Quant q;
 
   __device__ __forceinline__ void init(const float* p, int64_t ld_, int row0_, int lim_row_, int lim_k_) {
     base = p;
@@ -77,6 +79,13 @@ struct TileLoader {
         // float4 is either wholly inside or wholly outside.
         if (R < lim_row && Kk < lim_k)
           v = *reinterpret_cast<const f4v*>(KC ? base + (int64_t)R * ld + Kk : base + (int64_t)Kk * ld + R);
+        if constexpr (QUANT) {
+          // zero padding stays zero: fake_quant(0) == 0
+          v[0] = fake_quant(v[0], q);
+          v[1] = fake_quant(v[1], q);
+          v[2] = fake_quant(v[2], q);
+          v[3] = fake_quant(v[3], q);
+        }
         r[4 * e + 0] = v[0];
         r[4 * e + 1] = v[1];
         r[4 * e + 2] = v[2];
@@ -95,7 +104,9 @@ struct TileLoader {
           row = idx & 63;
         }
         const int R = row0 + row, Kk = k0 + k;
-        r[e] = (R < lim_row && Kk < lim_k) ? (KC ? base[(int64_t)R * ld + Kk] : base[(int64_t)Kk * ld + R]) : 0.0f;
+        float v = (R < lim_row && Kk < lim_k) ? (KC ? base[(int64_t)R * ld + Kk] : base[(int64_t)Kk * ld + R]) : 0.0f;
+        if constexpr (QUANT) v = fake_quant(v, q);
+        r[e] = v;
       }
     }
   }
@@ -125,9 +136,10 @@ struct TileLoader {
   }
 };
 
-template <int LAYOUT, bool VEC>
+template <int LAYOUT, bool VEC, bool QA, bool QB>
 __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
-  constexpr bool KC = LAYOUT == kGemmNT;
+  constexpr bool A_KC = LAYOUT != kGemmTN, B_KC = LAYOUT == kGemmNT;
+  constexpr bool VEC_A = VEC, VEC_B = VEC;
   __shared__ __attribute__((aligned(16))) float As[2][kStageFloats];
   __shared__ __attribute__((aligned(16))) float Bs[2][kStageFloats];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -137,9 +149,12 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   const int kbeg = blockIdx.z * kper;
   const int kend = min(g.K, kbeg + kper);
 
-  TileLoader<KC, VEC> la, lb;
+  TileLoader<A_KC, VEC_A, QA> la;
+  TileLoader<B_KC, VEC_B, QB> lb;
   la.init(g.a, g.lda, i0, g.M, kend);
   lb.init(g.b, g.ldb, j0, g.N, kend);
+  la.q = g.qa;
+  lb.q = g.qb;
 
   f4 acc[2][2];
 #pragma unroll
@@ -164,7 +179,7 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     }
     const float* as = As[buf];
     const float* bs = Bs[buf];
-    if constexpr (KC) {
+    if constexpr (A_KC && B_KC) {
       // lane: rows 32 wy + 16 ti + r16 (A) and 32 wx + 16 tj + r16 (B), k = 8 kq + s
       f4v a[2][2], b[2][2];
 #pragma unroll
@@ -186,9 +201,18 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
       // k = kq + 4 s
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        const float* ar = as + (kq + 4 * s) * kTNStride + 32 * wy + r16;
+        float a0, a1;
+        if constexpr (A_KC) {
+          const float* ar = as + (32 * wy + r16) * kNTStride + kq + 4 * s;
+          a0 = ar[0];
+          a1 = ar[16 * kNTStride];
+        } else {
+          const float* ar = as + (kq + 4 * s) * kTNStride + 32 * wy + r16;
+          a0 = ar[0];
+          a1 = ar[16];
+        }
         const float* br = bs + (kq + 4 * s) * kTNStride + 32 * wx + r16;
-        const float a0 = ar[0], a1 = ar[16], b0 = br[0], b1 = br[16];
+        const float b0 = br[0], b1 = br[16];
         acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
         acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);
         acc[1][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b0, acc[1][0], 0, 0, 0);
@@ -228,6 +252,18 @@ __global__ void sum_partials_kernel(float* dst, const float* src, int64_t n, int
   }
 }
 
+// Column sums in chunks of kColRows rows: partial[chunk][j].
+constexpr int kColRows = 256;
+__global__ void colsum_kernel(const float* src, int64_t ld, int rows, int cols, float* partial) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  const int chunk = blockIdx.y;
+  if (j >= cols) return;
+  const int r1 = min(rows, (chunk + 1) * kColRows);
+  float s = 0.0f;
+  for (int r = chunk * kColRows; r < r1; ++r) s += src[(int64_t)r * ld + j];
+  partial[(int64_t)chunk * cols + j] = s;
+}
+
 __global__ void prev_state_kernel(float* hq, const float* h0, int64_t sh0_b, const float* out, int64_t so_b,
                                   int64_t rows, int B, int H, Quant q) {
   const int64_t n = rows * H;
@@ -258,13 +294,23 @@ int gemm_f32(const GemmArgs& g, hipStream_t stream, const char* who) {
   if (g.M < 1 || g.N < 1 || g.K < 1 || g.ksplit < 1)
     return set_error(GS_ERR_INVALID, "%s: GEMM dims must be positive (M=%d, N=%d, K=%d, ksplit=%d)", who, g.M, g.N,
                      g.K, g.ksplit);
+  if (g.layout != kGemmNT && g.layout != kGemmTN && g.layout != kGemmNN)
+    return set_error(GS_ERR_INVALID, "%s: unknown GEMM layout %d", who, g.layout);
   // float4 loads need 16-byte aligned bases, leading dimensions that keep
   // rows aligned, and contiguous extents that are multiples of 4.
-  const bool nt = g.layout == kGemmNT;
+  const bool a_kc = g.layout != kGemmTN, b_kc = g.layout == kGemmNT;
   const bool vec = aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
-                   (nt ? g.K % 4 == 0 : (g.M % 4 == 0 && g.N % 4 == 0));
-  GemmFn fn = nt ? (vec ? gemm_kernel<kGemmNT, true> : gemm_kernel<kGemmNT, false>)
-                 : (vec ? gemm_kernel<kGemmTN, true> : gemm_kernel<kGemmTN, false>);
+                   (a_kc ? g.K % 4 == 0 : g.M % 4 == 0) && (b_kc ? g.K % 4 == 0 : g.N % 4 == 0);
+#define GS_GEMM_ROW(L, V) \
+  {{gemm_kernel<L, V, false, false>, gemm_kernel<L, V, false, true>}, \
+   {gemm_kernel<L, V, true, false>, gemm_kernel<L, V, true, true>}}
+  static const GemmFn table[3][2][2][2] = {
+      {GS_GEMM_ROW(kGemmNT, false), GS_GEMM_ROW(kGemmNT, true)},
+      {GS_GEMM_ROW(kGemmTN, false), GS_GEMM_ROW(kGemmTN, true)},
+      {GS_GEMM_ROW(kGemmNN, false), GS_GEMM_ROW(kGemmNN, true)},
+  };
+#undef GS_GEMM_ROW
+  GemmFn fn = table[g.layout][vec ? 1 : 0][g.qa.on ? 1 : 0][g.qb.on ? 1 : 0];
   const dim3 grid((unsigned)((g.M + BM - 1) / BM), (unsigned)((g.N + BN - 1) / BN), (unsigned)g.ksplit);
   hipLaunchKernelGGL(fn, grid, dim3(kGemmThreads), 0, stream, g);
   GS_CHECK_HIP(hipGetLastError());
@@ -279,6 +325,17 @@ int sum_partials(float* dst, const float* src, int64_t n, int parts, int64_t str
                      src, n, parts, stride);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
+}
+
+int64_t colsum_partial_floats(int rows, int cols) { return (int64_t)((rows + kColRows - 1) / kColRows) * cols; }
+
+int colsum(float* dst, const float* src, int64_t ld, int rows, int cols, float* partials, hipStream_t stream,
+           const char* who) {
+  const int chunks = (rows + kColRows - 1) / kColRows;
+  hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((cols + 255) / 256), (unsigned)chunks), dim3(256), 0, stream, src,
+                     ld, rows, cols, partials);
+  GS_CHECK_HIP(hipGetLastError());
+  return sum_partials(dst, partials, cols, chunks, cols, stream, who);
 }
 
 int build_prev_state(float* hq, const float* h0, int64_t sh0_b, const float* out, int64_t so_b, int T, int B, int H,

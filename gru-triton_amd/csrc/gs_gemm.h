@@ -1,27 +1,32 @@
 // fp32 GEMM on MFMA for the plain matrix products around the scans:
-//   C[i, j] = sum_k A(i, k) B(k, j) (+ bias[j])
-// in two layouts: NT, both operands contiguous along k
-// (A(i, k) = a[i lda + k], B(k, j) = b[j ldb + k]), and TN, both contiguous
-// along their output dimension (A(i, k) = a[k lda + i], B(k, j) = b[k ldb + j]).
+//   C[i, j] = sum_k qa(A(i, k)) qb(B(k, j)) (+ bias[j])
+// in three layouts: NT, both operands contiguous along k
+// (A(i, k) = a[i lda + k], B(k, j) = b[j ldb + k]); TN, both contiguous
+// along their output dimension (A(i, k) = a[k lda + i], B(k, j) = b[k ldb + j]);
+// NN, A along k and B along j (A(i, k) = a[i lda + k], B(k, j) = b[k ldb + j]).
+// qa and qb are optional per-tensor fake-quants applied to A and B as they are
+// loaded.
 #pragma once
 
 #include "gs_host.h"
 
 namespace gs {
 
-enum GemmLayout : int { kGemmNT = 0, kGemmTN = 1 };
+enum GemmLayout : int { kGemmNT = 0, kGemmTN = 1, kGemmNN = 2 };
 
 struct GemmArgs {
-  const float* a;
-  int64_t lda;
-  const float* b;
-  int64_t ldb;
-  float* c;  // C[i * ldc + j]; split s of a K-split product writes c + s * split_stride
-  int64_t ldc;
-  int64_t split_stride;
-  const float* bias;  // [N] added once (by split 0), or null
-  int M, N, K, ksplit;
-  int layout;  // GemmLayout
+  const float* a = nullptr;
+  int64_t lda = 0;
+  const float* b = nullptr;
+  int64_t ldb = 0;
+  float* c = nullptr;  // C[i * ldc + j]; split s of a K-split product writes c + s * split_stride
+  int64_t ldc = 0;
+  int64_t split_stride = 0;
+  const float* bias = nullptr;  // [N] added once (by split 0), or null
+  int M = 0, N = 0, K = 0, ksplit = 1;
+  int layout = kGemmNT;                 // GemmLayout
+  Quant qa{1.0f, 0.0f, 0.0f, 0};         // applied to A on load when qa.on
+  Quant qb{1.0f, 0.0f, 0.0f, 0};         // applied to B on load when qb.on
 };
 
 // Launches the product on `stream`. Every element of C (of every split) is written.
@@ -30,6 +35,12 @@ int gemm_f32(const GemmArgs& g, hipStream_t stream, const char* who);
 // dst[e] = sum_{s < parts} src[s * stride + e] for e < n.
 int sum_partials(float* dst, const float* src, int64_t n, int parts, int64_t stride, hipStream_t stream,
                  const char* who);
+
+// dst[j] = sum_{i < rows} src[i * ld + j] for j < cols; `partials` holds
+// colsum_partial_floats(rows, cols) floats of scratch.
+int64_t colsum_partial_floats(int rows, int cols);
+int colsum(float* dst, const float* src, int64_t ld, int rows, int cols, float* partials, hipStream_t stream,
+           const char* who);
 
 // Number of K splits that fills the device for an M x N output with K terms.
 int gemm_pick_split(int M, int N, int K);

@@ -1,0 +1,194 @@
+// Input projection that produces the scan's gate inputs (gfx950):
+//   gi = q_x(x) W_q^T + bi,   W_q = per-row int8 fake-quant of Wi_cat
+// and its backward.
+//
+// Reference: GRULayer._forward_fast_dispatch (LarocheC/gru-triton
+// src/gru_qat/gru_layer.py:249-255: xq = quant_x(x); Wi_cat, bi_cat =
+// cell.quantize_input_weights(); gi = F.linear(xq, Wi_cat, bi_cat)), the
+// weight quantizer FakeQuantizePerChannel (quantizers.py:188-199) with its
+// symmetric scale (quantizers.py:124-134: scale = max(|min|, |max|) clamped to
+// 1e-8, over qmax), and fake_quant_ste (ste.py:65-95) for both quantizers.
+//
+// The forward is one NT GEMM (gemm.hip) whose A loads apply q_x (the fake-
+// quant prologue) and whose epilogue adds bi; the weight is fake-quantized
+// once per call by a row kernel (a reduction for the row's absmax, then the
+// codes), which also returns the per-row scales. The backward follows the
+// straight-through estimator: dx = mask_x (dgi W_q) with q_x's clipped-STE
+// mask, dW = dgi^T q_x(x) (the gradient reaching W_q; the per-row clamp never
+// clips, since every |W / scale| <= qmax), dbi = column sums of dgi. The
+// scales are treated as constants, as in the reference's frozen mode.
+#include "gs_gemm.h"
+#include "gs_mfma.h"
+
+namespace gs {
+namespace {
+
+constexpr int kRowThreads = 256;
+
+// One workgroup per row of w [rows, cols].
+__global__ __launch_bounds__(kRowThreads) void weight_quant_rows(const float* w, int cols, float qmin, float qmax,
+                                                                 float* wq, float* scale_out) {
+  __shared__ float red[kRowThreads / 64];
+  const int64_t row = blockIdx.x;
+  const float* src = w + row * cols;
+  float m = 0.0f;
+  for (int k = threadIdx.x; k < cols; k += kRowThreads) m = fmaxf(m, fabsf(src[k]));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float absmax = red[0];
+  for (int i = 1; i < kRowThreads / 64; ++i) absmax = fmaxf(absmax, red[i]);
+  const float scale = fmaxf(absmax, 1e-8f) / qmax;
+  const Quant q{scale, qmin, qmax, 1};
+  for (int k = threadIdx.x; k < cols; k += kRowThreads) wq[row * cols + k] = fake_quant(src[k], q);
+  if (threadIdx.x == 0) scale_out[row] = scale;
+}
+
+// dx[m][i] = 0 where q_x clipped x[m][i].
+__global__ void mask_clipped(float* dx, int64_t sdx, const float* x, int64_t sx, int rows, int cols, Quant q) {
+  const int64_t n = (int64_t)rows * cols;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = e / cols;
+    const int i = (int)(e - m * cols);
+    if (!quant_keeps(x[m * sx + i], q)) dx[m * sdx + i] = 0.0f;
+  }
+}
+
+int validate_proj(int64_t M, int64_t N, int64_t I, const char* who) {
+  if (M < 1 || N < 1 || I < 1)
+    return set_error(GS_ERR_INVALID, "%s: M, N and I must be > 0; got M=%lld, N=%lld, I=%lld", who, (long long)M,
+                     (long long)N, (long long)I);
+  if (M > INT32_MAX / 4 || N > (1 << 20) || I > (1 << 20))
+    return set_error(GS_ERR_INVALID, "%s: dims out of supported range (M=%lld, N=%lld, I=%lld)", who, (long long)M,
+                     (long long)N, (long long)I);
+  return GS_OK;
+}
+
+int64_t proj_bwd_bytes(const gs_proj_bwd_args* a) {
+  const int split = gemm_pick_split((int)a->N, (int)a->I, (int)a->M);
+  return align256(colsum_partial_floats((int)a->M, (int)a->N) * 4) +
+         (split > 1 ? align256((int64_t)split * a->N * a->I * 4) : 0);
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_input_proj(const gs_proj_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_input_proj";
+  if (a == nullptr) return set_error(GS_ERR_INVALID, "%s: args is NULL", who);
+  int rc = validate_proj(a->M, a->N, a->I, who);
+  if (rc) return rc;
+  if (!a->x || !a->w || !a->gi)
+    return set_error(GS_ERR_INVALID, "%s: x, w and gi must be non-NULL device pointers", who);
+  if (a->sx < a->I || a->sgi < a->N)
+    return set_error(GS_ERR_INVALID, "%s: row strides (sx=%lld, sgi=%lld) shorter than the rows", who,
+                     (long long)a->sx, (long long)a->sgi);
+  rc = validate_quant(a->q_x, "x_quant", who);
+  if (rc) return rc;
+  const float* w = a->w;
+  if (a->q_w.enabled) {
+    if (!a->w_q || !a->w_scale)
+      return set_error(GS_ERR_INVALID, "%s: w_q and w_scale must be non-NULL when the weight quant is on", who);
+    if (!(a->q_w.qmax > 0) || a->q_w.qmin > a->q_w.qmax)
+      return set_error(GS_ERR_INVALID, "%s: weight quant needs qmax > 0 and qmin <= qmax; got [%d, %d]", who,
+                       a->q_w.qmin, a->q_w.qmax);
+    hipLaunchKernelGGL(weight_quant_rows, dim3((unsigned)a->N), dim3(kRowThreads), 0, stream, a->w, (int)a->I,
+                       (float)a->q_w.qmin, (float)a->q_w.qmax, a->w_q, a->w_scale);
+    GS_CHECK_HIP(hipGetLastError());
+    w = a->w_q;
+  }
+  GemmArgs g;
+  g.a = a->x;
+  g.lda = a->sx;
+  g.b = w;  // B(k, n) = W[n][k]
+  g.ldb = a->I;
+  g.c = a->gi;
+  g.ldc = a->sgi;
+  g.bias = a->bias;
+  g.M = (int)a->M;
+  g.N = (int)a->N;
+  g.K = (int)a->I;
+  g.layout = kGemmNT;
+  g.qa = to_quant(a->q_x);
+  return gemm_f32(g, stream, who);
+}
+
+extern "C" int64_t gs_input_proj_bwd_workspace_bytes(const gs_proj_bwd_args* a) {
+  using namespace gs;
+  if (a == nullptr) return set_error(GS_ERR_INVALID, "gs_input_proj_bwd_workspace_bytes: args is NULL");
+  const int rc = validate_proj(a->M, a->N, a->I, "gs_input_proj_bwd_workspace_bytes");
+  if (rc) return rc;
+  return proj_bwd_bytes(a);
+}
+
+extern "C" int gs_input_proj_bwd(const gs_proj_bwd_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_input_proj_bwd";
+  if (a == nullptr) return set_error(GS_ERR_INVALID, "%s: args is NULL", who);
+  int rc = validate_proj(a->M, a->N, a->I, who);
+  if (rc) return rc;
+  if (!a->x || !a->w || !a->dgi || !a->dx || !a->dw)
+    return set_error(GS_ERR_INVALID, "%s: x, w, dgi, dx and dw must be non-NULL device pointers", who);
+  if (a->sx < a->I || a->sdgi < a->N || a->sdx < a->I)
+    return set_error(GS_ERR_INVALID, "%s: row strides shorter than the rows", who);
+  rc = validate_quant(a->q_x, "x_quant", who);
+  if (rc) return rc;
+  const int64_t need = proj_bwd_bytes(a);
+  if (a->workspace == nullptr || a->workspace_bytes < need)
+    return set_error(GS_ERR_INVALID, "%s: workspace of %lld bytes required; got %lld", who, (long long)need,
+                     (long long)a->workspace_bytes);
+  const int M = (int)a->M, N = (int)a->N, I = (int)a->I;
+  const Quant qx = to_quant(a->q_x);
+  float* colp = static_cast<float*>(a->workspace);
+  float* part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + align256(colsum_partial_floats(M, N) * 4));
+
+  // dx = dgi W  (NN: A(m, n) = dgi[m][n], B(n, i) = W[n][i]), then q_x's mask
+  GemmArgs g;
+  g.a = a->dgi;
+  g.lda = a->sdgi;
+  g.b = a->w;
+  g.ldb = I;
+  g.c = a->dx;
+  g.ldc = a->sdx;
+  g.M = M;
+  g.N = I;
+  g.K = N;
+  g.layout = kGemmNN;
+  rc = gemm_f32(g, stream, who);
+  if (rc) return rc;
+  if (qx.on) {
+    const int64_t n = (int64_t)M * I;
+    hipLaunchKernelGGL(mask_clipped, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0, stream,
+                       a->dx, a->sdx, a->x, a->sx, M, I, qx);
+    GS_CHECK_HIP(hipGetLastError());
+  }
+
+  // dW = dgi^T q_x(x)  (TN: A(n, m) = dgi[m][n], B(m, i) = q_x(x[m][i]))
+  const int split = gemm_pick_split(N, I, M);
+  GemmArgs h;
+  h.a = a->dgi;
+  h.lda = a->sdgi;
+  h.b = a->x;
+  h.ldb = a->sx;
+  h.c = split > 1 ? part : a->dw;
+  h.ldc = I;
+  h.split_stride = (int64_t)N * I;
+  h.M = N;
+  h.N = I;
+  h.K = M;
+  h.ksplit = split;
+  h.layout = kGemmTN;
+  h.qb = qx;
+  rc = gemm_f32(h, stream, who);
+  if (rc) return rc;
+  if (split > 1) {
+    rc = sum_partials(a->dw, part, (int64_t)N * I, split, (int64_t)N * I, stream, who);
+    if (rc) return rc;
+  }
+  if (a->dbias) return colsum(a->dbias, a->dgi, a->sdgi, M, N, colp, stream, who);
+  return GS_OK;
+}

@@ -37,6 +37,9 @@ EXPORTS = (
     "gs_dense_bwd",
     "gs_monarch_bwd",
     "gs_butterfly_bwd",
+    "gs_input_proj",
+    "gs_input_proj_bwd",
+    "gs_input_proj_bwd_workspace_bytes",
     "gs_workspace_bytes",
     "gs_bwd_workspace_bytes",
     "gs_workspace_status",
@@ -118,6 +121,44 @@ class GsBwdArgs(ctypes.Structure):
     ]
 
 
+class GsProjArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("gi", ctypes.c_void_p),
+        ("w_q", ctypes.c_void_p),
+        ("w_scale", ctypes.c_void_p),
+        ("M", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("I", ctypes.c_int64),
+        ("sx", ctypes.c_int64),
+        ("sgi", ctypes.c_int64),
+        ("q_x", GsQuant),
+        ("q_w", GsQuant),
+    ]
+
+
+class GsProjBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("dgi", ctypes.c_void_p),
+        ("dx", ctypes.c_void_p),
+        ("dw", ctypes.c_void_p),
+        ("dbias", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
+        ("M", ctypes.c_int64),
+        ("N", ctypes.c_int64),
+        ("I", ctypes.c_int64),
+        ("sx", ctypes.c_int64),
+        ("sdgi", ctypes.c_int64),
+        ("sdx", ctypes.c_int64),
+        ("q_x", GsQuant),
+    ]
+
+
 _lib = None
 _lib_lock = threading.Lock()
 
@@ -145,6 +186,12 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(GsBwdArgs), ctypes.c_void_p]
             fn.restype = ctypes.c_int
+        lib.gs_input_proj.argtypes = [ctypes.POINTER(GsProjArgs), ctypes.c_void_p]
+        lib.gs_input_proj.restype = ctypes.c_int
+        lib.gs_input_proj_bwd.argtypes = [ctypes.POINTER(GsProjBwdArgs), ctypes.c_void_p]
+        lib.gs_input_proj_bwd.restype = ctypes.c_int
+        lib.gs_input_proj_bwd_workspace_bytes.argtypes = [ctypes.POINTER(GsProjBwdArgs)]
+        lib.gs_input_proj_bwd_workspace_bytes.restype = ctypes.c_int64
         lib.gs_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsArgs)]
         lib.gs_workspace_bytes.restype = ctypes.c_int64
         lib.gs_bwd_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsBwdArgs)]

@@ -179,6 +179,56 @@ int gs_butterfly_bwd(const gs_bwd_args* args, hipStream_t stream);
  * host arithmetic. Negative on error. */
 int64_t gs_bwd_workspace_bytes(int kind, const gs_bwd_args* args);
 
+/* ---- input projection ----------------------------------------------------------
+ * The producer of gi (reference GRULayer._forward_fast_dispatch,
+ * src/gru_qat/gru_layer.py:249-255: xq = quant_x(x); Wi_cat, bi_cat =
+ * cell.quantize_input_weights(); gi = F.linear(xq, Wi_cat, bi_cat)):
+ *   gi[m][n] = sum_i q_x(x[m][i]) W_q[n][i] + bias[n]
+ * with q_x a frozen per-tensor fake-quant (ste.py:65-95) and W_q the per-row
+ * symmetric fake-quant of w (FakeQuantizePerChannel, quantizers.py:188-199:
+ * scale[n] = max(max_i |w[n][i]|, 1e-8) / qmax, quantizers.py:124-134), or w
+ * itself when q_w is off. One fp32 MFMA GEMM with the x fake-quant applied as
+ * the operand is loaded and the bias added in its epilogue.
+ */
+typedef struct gs_proj_args {
+  const float* x;     /* [M, I] rows (M = T B), row stride sx                        */
+  const float* w;     /* [N, I] contiguous (Wi_cat, N = 3H)                          */
+  const float* bias;  /* [N] or NULL                                                 */
+  float* gi;          /* [M, N] output, row stride sgi                               */
+  float* w_q;         /* [N, I] the fake-quantized weight (q_w on), else NULL        */
+  float* w_scale;     /* [N] its per-row scales (q_w on), else NULL                  */
+  int64_t M, N, I;
+  int64_t sx, sgi;
+  gs_quant q_x;       /* per-tensor fake-quant of x                                  */
+  gs_quant q_w;       /* per-row weight fake-quant: enabled, qmin, qmax (scale unused) */
+} gs_proj_args;
+
+int gs_input_proj(const gs_proj_args* args, hipStream_t stream);
+
+/* Backward of gs_input_proj with the straight-through estimator (scales held
+ * constant, as in the reference's frozen mode): dx = mask_x (dgi w), with q_x's
+ * clipped-STE mask; dw = dgi^T q_x(x), the gradient reaching the weight that
+ * was used (w_q when q_w was on; the per-row clamp never clips); dbias = the
+ * column sums of dgi (skipped when NULL). No reference counterpart as one call:
+ * the reference gets these from autograd through F.linear and
+ * fake_quant_ste. */
+typedef struct gs_proj_bwd_args {
+  const float* x;     /* [M, I], row stride sx                                       */
+  const float* w;     /* [N, I] contiguous: the weight the forward used              */
+  const float* dgi;   /* [M, N], row stride sdgi                                     */
+  float* dx;          /* [M, I], row stride sdx                                      */
+  float* dw;          /* [N, I] contiguous                                           */
+  float* dbias;       /* [N] or NULL                                                 */
+  void* workspace;    /* gs_input_proj_bwd_workspace_bytes(args) bytes               */
+  int64_t workspace_bytes;
+  int64_t M, N, I;
+  int64_t sx, sdgi, sdx;
+  gs_quant q_x;
+} gs_proj_bwd_args;
+
+int64_t gs_input_proj_bwd_workspace_bytes(const gs_proj_bwd_args* args);
+int gs_input_proj_bwd(const gs_proj_bwd_args* args, hipStream_t stream);
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* gs_last_error(void);
 

@@ -24,6 +24,13 @@ Functions and what they follow (reference file:line):
                    out[t-1], clipped-STE masks on q_out and q_in, dW accumulated against hq
   scan_ste         the forward with ste.py:17-95's STERound/STEClamp gradients, the
                    independent derivation scan_backward is pinned against (autograd)
+  weight_fake_quant_rows
+                   quantizers.py:188-199 (per-channel min/max over every dim but axis 0)
+                   and :124-134 (symmetric: scale = max(|max|, |min|).clamp(1e-8) / qmax,
+                   zp = 0), then ste.py:65-95
+  input_projection gru_layer.py:249-255 (xq = quant_x(x); Wi_cat = quantize_input_weights();
+                   gi = F.linear(xq, Wi_cat, bi_cat)); with ste=True the straight-through
+                   gradients (clipped STE on x, scales held constant)
 
 Pins (tests/test_oracle.py; the backward in tests/test_oracle_backward.py
 against torch.autograd through scan_ste, in float64): round-half-even and clipping known answers
@@ -360,3 +367,29 @@ def scan_backward(cfg: dict, out: torch.Tensor, dout: torch.Tensor, _mutation: s
     for k, d in zip(keys, dparams):
         res["d" + k] = d
     return res
+
+
+# ---- input projection ----------------------------------------------------------------
+
+def weight_fake_quant_rows(W: torch.Tensor, qmin: int, qmax: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-output-row symmetric fake-quant of W [N, I]; returns (W_q, scale [N])."""
+    x_min = W.amin(dim=1, keepdim=True)
+    x_max = W.amax(dim=1, keepdim=True)
+    absmax = torch.maximum(x_max.abs(), x_min.abs()).clamp(min=1e-8)
+    scale = absmax / qmax
+    q = torch.round(W / scale).clamp(qmin, qmax)
+    return q * scale, scale.view(-1)
+
+
+def input_projection(x: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor], x_quant: QuantTuple = None,
+                     w_quant: Optional[Tuple[int, int]] = None, ste: bool = False) -> torch.Tensor:
+    """gi = F.linear(q_x(x), W_q, b) on x [..., I]."""
+    if x_quant is not None:
+        xq = fake_quant_ste(x, x_quant) if ste else fake_quant(x, x_quant)
+    else:
+        xq = x
+    if w_quant is not None:
+        wq, _ = weight_fake_quant_rows(W.detach(), w_quant[0], w_quant[1])
+        W = W + (wq - W).detach() if ste else wq
+    return F.linear(xq, W, b)
+

@@ -244,3 +244,59 @@ def test_bad_quant_tuple_rejected_on_cpu():
     with pytest.raises(ValueError):
         check_quant((-1.0, -127, 127), "h_in_quant")
     assert check_quant((0.5, -127, 127), "h_in_quant") == (0.5, -127, 127)
+
+
+def _proj_args(M=6, N=12, I=8, **kw):
+    a = _lib.GsProjArgs()
+    a.M, a.N, a.I = M, N, I
+    a.sx, a.sgi = I, N
+    a.q_x = _lib.make_quant(kw.pop("q_x", None), "q_x")
+    a.q_w = _lib.make_quant(kw.pop("q_w", None), "q_w")
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_input_proj_validation():
+    lib = _lib.load()
+    a = _proj_args(x=FAKE, w=FAKE)
+    assert lib.gs_input_proj(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"non-NULL" in lib.gs_last_error()
+    a = _proj_args(x=FAKE, w=FAKE, gi=FAKE, M=0)
+    assert lib.gs_input_proj(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    a = _proj_args(x=FAKE, w=FAKE, gi=FAKE)
+    a.sx = 4  # shorter than a row of I = 8
+    assert lib.gs_input_proj(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"stride" in lib.gs_last_error()
+    a = _proj_args(x=FAKE, w=FAKE, gi=FAKE, q_w=(1.0, -127, 127))
+    assert lib.gs_input_proj(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"w_q" in lib.gs_last_error()
+    a = _proj_args(x=FAKE, w=FAKE, gi=FAKE, q_x=(0.0, -127, 127))
+    assert lib.gs_input_proj(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+
+
+def test_input_proj_bwd_workspace_and_validation():
+    lib = _lib.load()
+    a = _lib.GsProjBwdArgs()
+    a.M, a.N, a.I = 2048, 1536, 512
+    a.sx, a.sdgi, a.sdx = 512, 1536, 512
+    al = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    tiles = (1536 // 64) * (512 // 64)
+    split = min(-(-512 // tiles), -(-2048 // 256))
+    want = al(-(-2048 // 256) * 1536 * 4) + (al(split * 1536 * 512 * 4) if split > 1 else 0)
+    assert lib.gs_input_proj_bwd_workspace_bytes(ctypes.byref(a)) == want
+    a.x, a.w, a.dgi, a.dx, a.dw = FAKE, FAKE, FAKE, FAKE, FAKE
+    assert lib.gs_input_proj_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"workspace" in lib.gs_last_error()
+    a.dw = None
+    assert lib.gs_input_proj_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"non-NULL" in lib.gs_last_error()
+
+
+def test_input_projection_rejects_cpu_tensors():
+    import gru_qat_amd as G
+
+    with pytest.raises(ValueError):
+        G.input_projection(torch.zeros(2, 3), torch.zeros(4, 3))
+    with pytest.raises(ValueError):
+        G.quantize_input_weights(torch.zeros(4, 3), (-127, 127))
