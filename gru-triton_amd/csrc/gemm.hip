@@ -252,16 +252,42 @@ __global__ void sum_partials_kernel(float* dst, const float* src, int64_t n, int
   }
 }
 
-// Column sums in chunks of kColRows rows: partial[chunk][j].
+// Column sums: a workgroup takes 64 columns x kColRows rows; its 256 threads
+// are 64 columns x 4 row lanes, each lane summing every 4th row (8 loads in
+// flight), and the 4 lanes are combined through LDS into partial[chunk][j].
 constexpr int kColRows = 256;
-__global__ void colsum_kernel(const float* src, int64_t ld, int rows, int cols, float* partial) {
-  const int j = blockIdx.x * blockDim.x + threadIdx.x;
-  const int chunk = blockIdx.y;
-  if (j >= cols) return;
-  const int r1 = min(rows, (chunk + 1) * kColRows);
+__global__ __launch_bounds__(256) void colsum_kernel(const float* src, int64_t ld, int rows, int cols,
+                                                     float* partial) {
+  __shared__ float red[4][64];
+  const int jl = threadIdx.x & 63, lane_r = threadIdx.x >> 6;
+  const int j = blockIdx.x * 64 + jl;
+  const int r0 = blockIdx.y * kColRows;
+  const int r1 = min(rows, r0 + kColRows);
   float s = 0.0f;
-  for (int r = chunk * kColRows; r < r1; ++r) s += src[(int64_t)r * ld + j];
-  partial[(int64_t)chunk * cols + j] = s;
+  if (j < cols) {
+    int r = r0 + lane_r;
+    for (; r + 28 < r1; r += 32) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = src[(int64_t)(r + 4 * u) * ld + j];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; r < r1; r += 4) s += src[(int64_t)r * ld + j];
+  }
+  red[lane_r][jl] = s;
+  __syncthreads();
+  if (lane_r == 0 && j < cols)
+    partial[(int64_t)blockIdx.y * cols + j] = ((red[0][jl] + red[1][jl]) + red[2][jl]) + red[3][jl];
+}
+
+__global__ void quant_copy_kernel(float* dst, const float* src, int64_t ld, int rows, int cols, Quant q) {
+  const int64_t n = (int64_t)rows * cols;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = e / cols;
+    const int i = (int)(e - m * cols);
+    dst[e] = fake_quant(src[m * ld + i], q);
+  }
 }
 
 __global__ void prev_state_kernel(float* hq, const float* h0, int64_t sh0_b, const float* out, int64_t so_b,
@@ -332,10 +358,20 @@ int64_t colsum_partial_floats(int rows, int cols) { return (int64_t)((rows + kCo
 int colsum(float* dst, const float* src, int64_t ld, int rows, int cols, float* partials, hipStream_t stream,
            const char* who) {
   const int chunks = (rows + kColRows - 1) / kColRows;
-  hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((cols + 255) / 256), (unsigned)chunks), dim3(256), 0, stream, src,
+  hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)((cols + 63) / 64), (unsigned)chunks), dim3(256), 0, stream, src,
                      ld, rows, cols, partials);
   GS_CHECK_HIP(hipGetLastError());
   return sum_partials(dst, partials, cols, chunks, cols, stream, who);
+}
+
+int quant_copy(float* dst, const float* src, int64_t ld, int rows, int cols, const Quant& q, hipStream_t stream,
+               const char* who) {
+  (void)who;
+  const int64_t n = (int64_t)rows * cols;
+  hipLaunchKernelGGL(quant_copy_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0, stream,
+                     dst, src, ld, rows, cols, q);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
 }
 
 int build_prev_state(float* hq, const float* h0, int64_t sh0_b, const float* out, int64_t so_b, int T, int B, int H,

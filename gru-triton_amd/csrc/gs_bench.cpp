@@ -12,6 +12,12 @@
 // keeps the queue ahead of the device, so host overhead is not counted), and
 // prints one JSON line with the mean and median launch duration.
 //
+// Items b0..b4 time the backward entry point of a configuration instead
+// (gs_*_bwd on the forward's own output and a random upstream gradient), and
+// "proj" times the input projection at the benchmark shape (x [2048, 512],
+// Wi_cat [1536, 512], int8 x and per-row weight fake-quant) forward and
+// backward.
+//
 // The copy item launches a plain copy kernel (float4 loads and stores) of
 // 256 MiB; it reads and writes exactly that many bytes per launch, which
 // calibrates byte counters (FETCH_SIZE, WRITE_SIZE) under rocprofv3 --pmc.
@@ -147,7 +153,7 @@ int run_copy(int mib, int launches) {
   return 0;
 }
 
-int run_config(int idx, int launches, int warmup) {
+int run_config(int idx, int launches, int warmup, bool backward) {
   const long long T = idx == 4 ? 512 : 64, B = idx == 4 ? 64 : 32, H = idx == 4 ? 1024 : 512;
   Rng g(idx + 1);
   const float k = 1.0f / std::sqrt((float)H);
@@ -199,20 +205,70 @@ int run_config(int idx, int launches, int warmup) {
     a.q_in = q;
     a.q_out = q;
   }
-  const int64_t need = gs_workspace_bytes(kind, &a);
+  int64_t need = gs_workspace_bytes(kind, &a);
   if (need < 0) {
     fprintf(stderr, "gs_bench: gs_workspace_bytes: %s\n", gs_last_error());
     return 1;
+  }
+  gs_bwd_args b;
+  memset(&b, 0, sizeof b);
+  if (backward) {
+    b.gi = a.gi;
+    b.h0 = a.h0;
+    b.w = a.w;
+    b.w2 = a.w2;
+    b.bh = a.bh;
+    b.out = a.out;
+    owned.push_back(upload(filled((size_t)T * B * H, g, 1.0f)));
+    b.dout = owned.back();
+    owned.push_back(upload(std::vector<float>((size_t)T * B * 3 * H, 0.0f)));
+    b.dgi = owned.back();
+    owned.push_back(upload(std::vector<float>((size_t)B * H, 0.0f)));
+    b.dh0 = owned.back();
+    const size_t nw = kind == GS_KIND_DENSE ? (size_t)3 * H * H
+                      : kind == GS_KIND_MONARCH ? (size_t)3 * H * a.blksz
+                      : kind == GS_KIND_DIAGONAL ? (size_t)B * 3 * H
+                                                 : (size_t)3 * 10 * 512 * 4;
+    owned.push_back(upload(std::vector<float>(nw, 0.0f)));
+    b.dw_part = owned.back();
+    if (a.w2) {
+      owned.push_back(upload(std::vector<float>(nw, 0.0f)));
+      b.dw2_part = owned.back();
+    }
+    owned.push_back(upload(std::vector<float>((size_t)B * 3 * H, 0.0f)));
+    b.dbh_part = owned.back();
+    b.T = T;
+    b.B = B;
+    b.H = H;
+    b.sg_t = a.sg_t;
+    b.sg_b = a.sg_b;
+    b.sh0_b = a.sh0_b;
+    b.so_t = a.so_t;
+    b.so_b = a.so_b;
+    b.nblocks = a.nblocks;
+    b.blksz = a.blksz;
+    b.log_n = a.log_n;
+    b.bfly_nblocks = a.bfly_nblocks;
+    b.q_in = a.q_in;
+    b.q_out = a.q_out;
+    const int64_t nb = gs_bwd_workspace_bytes(kind, &b);
+    if (nb < 0) {
+      fprintf(stderr, "gs_bench: gs_bwd_workspace_bytes: %s\n", gs_last_error());
+      return 1;
+    }
+    need = std::max(need, nb);
   }
   void* ws = nullptr;
   CHECK(hipMalloc(&ws, need));
   CHECK(hipMemset(ws, 0, need));
   a.workspace = ws;
   a.workspace_bytes = need;
+  b.workspace = ws;
+  b.workspace_bytes = need;
   hipStream_t st;
   CHECK(hipStreamCreate(&st));
   int rc = GS_OK;
-  auto launch = [&] {
+  auto forward = [&] {
     switch (kind) {
       case GS_KIND_DIAGONAL: rc = gs_diagonal_fwd(&a, st); break;
       case GS_KIND_DENSE: rc = gs_dense_fwd(&a, st); break;
@@ -224,15 +280,120 @@ int run_config(int idx, int launches, int warmup) {
       exit(1);
     }
   };
+  auto launch = [&] {
+    if (!backward) return forward();
+    switch (kind) {
+      case GS_KIND_DIAGONAL: rc = gs_diagonal_bwd(&b, st); break;
+      case GS_KIND_DENSE: rc = gs_dense_bwd(&b, st); break;
+      case GS_KIND_MONARCH: rc = gs_monarch_bwd(&b, st); break;
+      default: rc = gs_butterfly_bwd(&b, st); break;
+    }
+    if (rc != GS_OK) {
+      fprintf(stderr, "gs_bench: backward launch failed (%d): %s\n", rc, gs_last_error());
+      exit(1);
+    }
+  };
+  if (backward) forward();  // out for the backward
   auto ms = time_launches(launch, launches, warmup, st);
   rc = gs_workspace_status(ws, need, st);
   if (rc != GS_OK) {
     fprintf(stderr, "gs_bench: a poll timed out (workspace fault word set)\n");
     return 1;
   }
-  report(kNames[idx], idx, ms, T, B, H);
+  if (backward) {
+    char name[64];
+    snprintf(name, sizeof name, "%s_backward", kNames[idx]);
+    report(name, idx, ms, T, B, H);
+  } else {
+    report(kNames[idx], idx, ms, T, B, H);
+  }
   CHECK(hipFree(ws));
   for (float* p : owned) CHECK(hipFree(p));
+  CHECK(hipStreamDestroy(st));
+  return 0;
+}
+
+int run_proj(int launches, int warmup) {
+  const int64_t M = 2048, N = 1536, I = 512;
+  Rng g(11);
+  std::vector<float*> owned;
+  owned.push_back(upload(filled((size_t)M * I, g, 1.0f)));
+  float* x = owned.back();
+  owned.push_back(upload(filled((size_t)N * I, g, 0.044f)));
+  float* w = owned.back();
+  owned.push_back(upload(filled((size_t)N, g, 0.044f)));
+  float* bias = owned.back();
+  owned.push_back(upload(std::vector<float>((size_t)M * N, 0.0f)));
+  float* gi = owned.back();
+  owned.push_back(upload(std::vector<float>((size_t)N * I, 0.0f)));
+  float* wq = owned.back();
+  owned.push_back(upload(std::vector<float>((size_t)M * I, 0.0f)));
+  float* xq = owned.back();
+  owned.push_back(upload(std::vector<float>((size_t)N, 0.0f)));
+  float* sc = owned.back();
+  owned.push_back(upload(filled((size_t)M * N, g, 1.0f)));
+  float* dgi = owned.back();
+  owned.push_back(upload(std::vector<float>((size_t)M * I, 0.0f)));
+  float* dx = owned.back();
+  owned.push_back(upload(std::vector<float>((size_t)N * I, 0.0f)));
+  float* dw = owned.back();
+  owned.push_back(upload(std::vector<float>((size_t)N, 0.0f)));
+  float* db = owned.back();
+  gs_proj_args p;
+  memset(&p, 0, sizeof p);
+  p.x = x;
+  p.w = w;
+  p.bias = bias;
+  p.gi = gi;
+  p.x_q = xq;
+  p.w_q = wq;
+  p.w_scale = sc;
+  p.M = M;
+  p.N = N;
+  p.I = I;
+  p.sx = I;
+  p.sgi = N;
+  p.q_x = gs_quant{1, 0.02f, -127, 127};
+  p.q_w = gs_quant{1, 1.0f, -127, 127};
+  gs_proj_bwd_args q;
+  memset(&q, 0, sizeof q);
+  q.x = x;
+  q.w = wq;
+  q.x_q = xq;
+  q.dgi = dgi;
+  q.dx = dx;
+  q.dw = dw;
+  q.dbias = db;
+  q.M = M;
+  q.N = N;
+  q.I = I;
+  q.sx = I;
+  q.sdgi = N;
+  q.sdx = I;
+  q.q_x = p.q_x;
+  const int64_t need = gs_input_proj_bwd_workspace_bytes(&q);
+  void* ws = nullptr;
+  CHECK(hipMalloc(&ws, need));
+  q.workspace = ws;
+  q.workspace_bytes = need;
+  hipStream_t st;
+  CHECK(hipStreamCreate(&st));
+  auto fwd = [&] {
+    if (gs_input_proj(&p, st) != GS_OK) {
+      fprintf(stderr, "gs_bench: gs_input_proj: %s\n", gs_last_error());
+      exit(1);
+    }
+  };
+  auto bwd = [&] {
+    if (gs_input_proj_bwd(&q, st) != GS_OK) {
+      fprintf(stderr, "gs_bench: gs_input_proj_bwd: %s\n", gs_last_error());
+      exit(1);
+    }
+  };
+  report("input_projection", -1, time_launches(fwd, launches, warmup, st), 64, 32, 512);
+  report("input_projection_backward", -1, time_launches(bwd, launches, warmup, st), 64, 32, 512);
+  CHECK(hipFree(ws));
+  for (float* o : owned) CHECK(hipFree(o));
   CHECK(hipStreamDestroy(st));
   return 0;
 }
@@ -241,7 +402,8 @@ int run_config(int idx, int launches, int warmup) {
 
 int main(int argc, char** argv) {
   if (argc < 2) {
-    fprintf(stderr, "usage: gs_bench <items: configs 0..4 and/or copy, comma-separated> [launches] [warmup]\n");
+    fprintf(stderr, "usage: gs_bench <items: configs 0..4, b0..b4 (backward), proj, copy; comma-separated> "
+                    "[launches] [warmup]\n");
     return 2;
   }
   const int launches = argc > 2 ? atoi(argv[2]) : 30;
@@ -254,14 +416,18 @@ int main(int argc, char** argv) {
     int rc;
     if (!strcmp(tok, "copy")) {
       rc = run_copy(256, launches);
+    } else if (!strcmp(tok, "proj")) {
+      rc = run_proj(launches, warmup);
     } else {
+      const bool backward = tok[0] == 'b';
+      const char* num = backward ? tok + 1 : tok;
       char* end = nullptr;
-      const long idx = strtol(tok, &end, 10);
-      if (*tok == 0 || *end != 0 || idx < 0 || idx > 4) {
+      const long idx = strtol(num, &end, 10);
+      if (*num == 0 || *end != 0 || idx < 0 || idx > 4) {
         fprintf(stderr, "gs_bench: unknown item '%s'\n", tok);
         return 2;
       }
-      rc = run_config((int)idx, launches, warmup);
+      rc = run_config((int)idx, launches, warmup, backward);
     }
     if (rc) return rc;
   }

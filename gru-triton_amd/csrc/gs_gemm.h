@@ -45,6 +45,10 @@ int colsum(float* dst, const float* src, int64_t ld, int rows, int cols, float* 
 // Number of K splits that fills the device for an M x N output with K terms.
 int gemm_pick_split(int M, int N, int K);
 
+// dst[m][i] = fake_quant(src[m ld + i], q), dst contiguous [rows, cols].
+int quant_copy(float* dst, const float* src, int64_t ld, int rows, int cols, const Quant& q, hipStream_t stream,
+               const char* who);
+
 // hq[m][k] = q(m < B ? h0[m sh0_b + k] : out[(m - B) so_b + k]) for m < T B,
 // k < H: the previous-state matrix [h0; out[0..T-2]] (fake-quantized when
 // q.on) as a contiguous [T B, H] block.

@@ -9,11 +9,13 @@
 // symmetric scale (quantizers.py:124-134: scale = max(|min|, |max|) clamped to
 // 1e-8, over qmax), and fake_quant_ste (ste.py:65-95) for both quantizers.
 //
-// The forward is one NT GEMM (gemm.hip) whose A loads apply q_x (the fake-
-// quant prologue) and whose epilogue adds bi; the weight is fake-quantized
-// once per call by a row kernel (a reduction for the row's absmax, then the
-// codes), which also returns the per-row scales. The backward follows the
-// straight-through estimator: dx = mask_x (dgi W_q) with q_x's clipped-STE
+// The forward is one NT GEMM (gemm.hip) whose epilogue adds bi. q_x is applied
+// either by one elementwise pass into a caller buffer (x_q), which the
+// backward reuses, or as the GEMM loads x (the fake-quant prologue; that
+// repeats the quantization once per output tile and measured 25 % slower).
+// The weight is fake-quantized once per call by a row kernel (a reduction for
+// the row's absmax, then the codes), which also returns the per-row scales.
+// The backward follows the straight-through estimator: dx = mask_x (dgi W_q) with q_x's clipped-STE
 // mask, dW = dgi^T q_x(x) (the gradient reaching W_q; the per-row clamp never
 // clips, since every |W / scale| <= qmax), dbi = column sums of dgi. The
 // scales are treated as constants, as in the reference's frozen mode.
@@ -103,6 +105,15 @@ extern "C" int gs_input_proj(const gs_proj_args* a, hipStream_t stream) {
   GemmArgs g;
   g.a = a->x;
   g.lda = a->sx;
+  g.qa = to_quant(a->q_x);
+  if (a->q_x.enabled && a->x_q) {
+    // one fake-quant pass instead of one per output tile of the GEMM
+    rc = quant_copy(a->x_q, a->x, a->sx, (int)a->M, (int)a->I, g.qa, stream, who);
+    if (rc) return rc;
+    g.a = a->x_q;
+    g.lda = a->I;
+    g.qa.on = 0;
+  }
   g.b = w;  // B(k, n) = W[n][k]
   g.ldb = a->I;
   g.c = a->gi;
@@ -112,7 +123,6 @@ extern "C" int gs_input_proj(const gs_proj_args* a, hipStream_t stream) {
   g.N = (int)a->N;
   g.K = (int)a->I;
   g.layout = kGemmNT;
-  g.qa = to_quant(a->q_x);
   return gemm_f32(g, stream, who);
 }
 
@@ -172,8 +182,8 @@ extern "C" int gs_input_proj_bwd(const gs_proj_bwd_args* a, hipStream_t stream) 
   GemmArgs h;
   h.a = a->dgi;
   h.lda = a->sdgi;
-  h.b = a->x;
-  h.ldb = a->sx;
+  h.b = a->x_q ? a->x_q : a->x;
+  h.ldb = a->x_q ? I : a->sx;
   h.c = split > 1 ? part : a->dw;
   h.ldc = I;
   h.split_stride = (int64_t)N * I;
@@ -182,7 +192,7 @@ extern "C" int gs_input_proj_bwd(const gs_proj_bwd_args* a, hipStream_t stream) 
   h.K = M;
   h.ksplit = split;
   h.layout = kGemmTN;
-  h.qb = qx;
+  if (!a->x_q) h.qb = qx;
   rc = gemm_f32(h, stream, who);
   if (rc) return rc;
   if (split > 1) {

@@ -127,6 +127,7 @@ class GsProjArgs(ctypes.Structure):
         ("w", ctypes.c_void_p),
         ("bias", ctypes.c_void_p),
         ("gi", ctypes.c_void_p),
+        ("x_q", ctypes.c_void_p),
         ("w_q", ctypes.c_void_p),
         ("w_scale", ctypes.c_void_p),
         ("M", ctypes.c_int64),
@@ -143,6 +144,7 @@ class GsProjBwdArgs(ctypes.Structure):
     _fields_ = [
         ("x", ctypes.c_void_p),
         ("w", ctypes.c_void_p),
+        ("x_q", ctypes.c_void_p),
         ("dgi", ctypes.c_void_p),
         ("dx", ctypes.c_void_p),
         ("dw", ctypes.c_void_p),

@@ -39,8 +39,8 @@ def _check_wq(w_quant: WeightQuant) -> WeightQuant:
 
 
 def _project(x2: torch.Tensor, Wi_cat: torch.Tensor, bi_cat: Optional[torch.Tensor], x_quant: QuantTuple,
-             w_quant: WeightQuant) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor]]:
-    """gi [M, N], the weight used, and its per-row scales (or None)."""
+             w_quant: WeightQuant) -> Tuple[torch.Tensor, torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """gi [M, N], the weight used, its per-row scales (or None) and q_x(x) (or None)."""
     lib = _lib.load()
     M, I = x2.shape
     N = Wi_cat.shape[0]
@@ -51,6 +51,10 @@ def _project(x2: torch.Tensor, Wi_cat: torch.Tensor, bi_cat: Optional[torch.Tens
     a.M, a.N, a.I = M, N, I
     a.sx, a.sgi = x2.stride(0), gi.stride(0)
     a.q_x = _lib.make_quant(x_quant, "x_quant")
+    xq = None
+    if x_quant is not None:
+        xq = torch.empty((M, I), device=x2.device, dtype=x2.dtype)
+        a.x_q = xq.data_ptr()
     w_used, scales = Wi_cat, None
     if w_quant is not None:
         w_used = torch.empty_like(Wi_cat)
@@ -62,7 +66,7 @@ def _project(x2: torch.Tensor, Wi_cat: torch.Tensor, bi_cat: Optional[torch.Tens
     with torch.cuda.device(x2.device):
         rc = lib.gs_input_proj(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(x2.device).cuda_stream))
     _lib.raise_for(rc, lib)
-    return gi, w_used, scales
+    return gi, w_used, scales, xq
 
 
 def _validate(who: str, x: torch.Tensor, Wi_cat: torch.Tensor, bi_cat: Optional[torch.Tensor]) -> None:
@@ -87,7 +91,7 @@ def quantize_input_weights(Wi_cat: torch.Tensor, w_quant: WeightQuant = (-127, 1
         raise ValueError("quantize_input_weights needs a (qmin, qmax) weight quant")
     x = Wi_cat.new_zeros((1, Wi_cat.shape[1]))
     _validate("quantize_input_weights", x, Wi_cat, None)
-    _, wq, scales = _project(x, Wi_cat.contiguous(), None, None, w_quant)
+    _, wq, scales, _ = _project(x, Wi_cat.contiguous(), None, None, w_quant)
     return wq, cast(torch.Tensor, scales)
 
 
@@ -97,8 +101,8 @@ class InputProjectionFunction(torch.autograd.Function):
         x2 = x.reshape(-1, x.shape[-1])
         if x2.stride(-1) != 1:
             x2 = x2.contiguous()
-        gi, w_used, _ = _project(x2, Wi_cat, bi_cat, x_quant, w_quant)
-        ctx.save_for_backward(x2, w_used)
+        gi, w_used, _, xq = _project(x2, Wi_cat, bi_cat, x_quant, w_quant)
+        ctx.save_for_backward(x2, w_used, xq)
         ctx.x_quant = x_quant
         ctx.has_bias = bi_cat is not None
         ctx.x_shape = x.shape
@@ -106,7 +110,7 @@ class InputProjectionFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx: Any, dgi: torch.Tensor):  # type: ignore[override]
-        x2, w_used = ctx.saved_tensors
+        x2, w_used, xq = ctx.saved_tensors
         lib = _lib.load()
         M, I = x2.shape
         N = w_used.shape[0]
@@ -118,6 +122,7 @@ class InputProjectionFunction(torch.autograd.Function):
         dbias = torch.empty((N,), device=x2.device, dtype=x2.dtype) if ctx.has_bias else None
         a = _lib.GsProjBwdArgs()
         a.x, a.w, a.dgi, a.dx, a.dw = x2.data_ptr(), w_used.data_ptr(), dgi2.data_ptr(), dx.data_ptr(), dw.data_ptr()
+        a.x_q = xq.data_ptr() if xq is not None else None
         a.dbias = dbias.data_ptr() if dbias is not None else None
         a.M, a.N, a.I = M, N, I
         a.sx, a.sdgi, a.sdx = x2.stride(0), dgi2.stride(0), dx.stride(0)

@@ -195,6 +195,8 @@ typedef struct gs_proj_args {
   const float* w;     /* [N, I] contiguous (Wi_cat, N = 3H)                          */
   const float* bias;  /* [N] or NULL                                                 */
   float* gi;          /* [M, N] output, row stride sgi                               */
+  float* x_q;         /* [M, I] contiguous: q_x(x) is written here and fed to the GEMM *
+                       * (q_x on); NULL fake-quantizes x as the GEMM loads it        */
   float* w_q;         /* [N, I] the fake-quantized weight (q_w on), else NULL        */
   float* w_scale;     /* [N] its per-row scales (q_w on), else NULL                  */
   int64_t M, N, I;
@@ -215,6 +217,8 @@ int gs_input_proj(const gs_proj_args* args, hipStream_t stream);
 typedef struct gs_proj_bwd_args {
   const float* x;     /* [M, I], row stride sx                                       */
   const float* w;     /* [N, I] contiguous: the weight the forward used              */
+  const float* x_q;   /* [M, I] contiguous q_x(x) from the forward, or NULL (then    *
+                       * x is fake-quantized as it is loaded)                        */
   const float* dgi;   /* [M, N], row stride sdgi                                     */
   float* dx;          /* [M, I], row stride sdx                                      */
   float* dw;          /* [N, I] contiguous                                           */
