@@ -166,15 +166,19 @@ def train_steps(dev, iters: int, warmup: int) -> dict:
                       None),
         "diagonal": ([u(3, H)], lambda gi, p, q: G.gru_scan_diagonal(gi, h0, p[0], p[-1], h_in_quant=q,
                                                                        h_out_quant=q), None),
+        # the whole step on this build's kernels: gs_input_proj instead of F.linear
+        "dense_hip_projection": ([u(3 * H, H)], lambda gi, p, q: G.gru_scan_persistent(gi, h0, p[0], p[-1]), None),
     }
     res = {}
     for name, (hidden, scan, q) in variants.items():
         params = [torch.nn.Parameter(t.clone()) for t in [Wi, bi] + hidden + [bh]]
 
+        project = G.input_projection if name == "dense_hip_projection" else F.linear
+
         def step():
             for prm in params:
                 prm.grad = None
-            gi = F.linear(x, params[0], params[1])
+            gi = project(x, params[0], params[1])
             out = scan(gi, params[2:], q)
             out.pow(2).sum().backward()
 

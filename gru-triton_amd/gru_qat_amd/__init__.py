@@ -23,7 +23,7 @@ from .scan_butterfly import (
 from .scan_diagonal import extract_diagonal_factors, gru_scan_diagonal, gru_scan_diagonal_forward
 from .scan_monarch import extract_monarch_factors, gru_scan_monarch, gru_scan_monarch_forward
 from ._lib import load as load_library, workspace_faults
-from .gru_layer import fast_dispatch_eligible, forward_fast_dispatch, resolve_use_triton
+from .gru_layer import fast_dispatch_eligible, forward_fast_dispatch, layer_forward, resolve_use_triton
 from .input_proj import input_projection, quantize_input_weights
 
 __all__ = [
@@ -46,6 +46,7 @@ __all__ = [
     "gru_scan_monarch_forward",
     "gru_scan_persistent",
     "input_projection",
+    "layer_forward",
     "load_library",
     "quantize_input_weights",
     "resolve_use_triton",

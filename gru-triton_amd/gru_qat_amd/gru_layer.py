@@ -12,15 +12,19 @@ This module keeps the parts of that path that decide and feed the scan:
   rule and the ``use_triton`` argument contract of gru_layer.py:110-124;
 * ``forward_fast_dispatch`` -- gru_layer.py:183-192 (T/B checks, zero h0)
   and :260-302 (kind switch, ``h_T = out[-1]`` taken before the batch_first
-  transpose).
+  transpose);
+* ``layer_forward`` -- GRULayer.forward (gru_layer.py:153-200) with a dense
+  input side, through ``_forward_fast_dispatch`` (:234-302): x to time-major,
+  the input projection (``input_projection``, :249-255), the scan.
 
-The cell, quantizer modules, calibration and the input projection that
-produces ``gi`` are not part of this build; callers pass ``gi`` and the
-extracted hidden weights (``extract_*`` helpers of the scan modules).
+The cell and quantizer modules and calibration are not part of this build;
+callers pass the extracted weights (``extract_*`` helpers of the scan
+modules) and the frozen quant tuples.
 """
 
 from __future__ import annotations
 
+import weakref
 from typing import Any, Optional, Tuple
 
 import torch
@@ -28,6 +32,23 @@ import torch
 from ._common import QuantTuple
 
 FAST_DISPATCH_KINDS = ("diagonal", "monarch", "butterfly")
+
+
+_SCALE_CACHE: "weakref.WeakKeyDictionary[Any, Tuple[int, int, float]]" = weakref.WeakKeyDictionary()
+
+
+def _scale_value(scale: torch.Tensor) -> float:
+    """``float(scale.item())``, read once per version of the tensor: a frozen
+    scale is not written again, so later forwards skip the device-to-host
+    sync that the reference pays on every call (gru_layer.py:48). Any
+    in-place write bumps ``scale._version`` and forces a fresh read."""
+    key = (scale.data_ptr(), scale._version)
+    hit = _SCALE_CACHE.get(scale)
+    if hit is not None and hit[:2] == key:
+        return hit[2]
+    value = float(scale.item())
+    _SCALE_CACHE[scale] = (key[0], key[1], value)
+    return value
 
 
 def _extract_h_quant_params(quantizer: Any) -> QuantTuple:
@@ -38,8 +59,10 @@ def _extract_h_quant_params(quantizer: Any) -> QuantTuple:
     ``isinstance(quantizer, FakeQuantizePerTensor)``; the quantizer classes
     are not part of this build, so per-tensor is read from the quantizer's
     config (``config.axis is None``, the reference's per-tensor config) and a
-    one-element scale. Like the reference, this reads the scale with
-    ``.item()`` (a device-to-host sync for a device scale).
+    one-element scale. The reference reads the scale with ``.item()`` on
+    every forward; here the value is cached per tensor version
+    (``_scale_value``), so a frozen device scale costs one sync, not one per
+    call.
     """
     cfg = quantizer.config
     if cfg.mode != "frozen":
@@ -48,7 +71,9 @@ def _extract_h_quant_params(quantizer: Any) -> QuantTuple:
         return None
     if not cfg.symmetric:
         return None
-    return (float(quantizer.scale.item()), int(quantizer.qmin), int(quantizer.qmax))
+    scale = quantizer.scale
+    value = _scale_value(scale) if isinstance(scale, torch.Tensor) else float(scale)
+    return (value, int(quantizer.qmin), int(quantizer.qmax))
 
 
 def fast_dispatch_eligible(kind: Optional[str], gate_layout: str) -> bool:
@@ -128,3 +153,45 @@ def forward_fast_dispatch(
     if batch_first:
         out = out.transpose(0, 1)
     return out, h_T
+
+
+def layer_forward(
+    kind: str,
+    x: torch.Tensor,
+    h0: Optional[torch.Tensor],
+    Wi_cat: torch.Tensor,
+    bi_cat: Optional[torch.Tensor],
+    hidden: torch.Tensor,
+    bh_cat: torch.Tensor,
+    *,
+    x_quant: QuantTuple = None,
+    w_quant: Optional[Tuple[int, int]] = None,
+    h_in_quant: QuantTuple = None,
+    h_out_quant: QuantTuple = None,
+    batch_first: bool = False,
+    hidden2: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """GRULayer's forward on the fast dispatch with a dense input side:
+    ``x`` [T, B, I] (or [B, T, I] when ``batch_first``) -> ``(out, h_T)``.
+
+    Follows gru_layer.py:169-200 (time-major x, T/B checks, zero h0) and
+    :249-302: ``gi = input_projection(x, Wi_cat, bi_cat, x_quant=..., w_quant=...)``
+    (the reference's ``quant_x`` + ``quantize_input_weights`` + ``F.linear``),
+    then the scan of ``kind`` (``forward_fast_dispatch``). Differentiable in
+    x, h0 and every weight.
+    """
+    from .input_proj import input_projection
+
+    if x.dim() != 3:
+        raise ValueError(f"x must be [T, B, I] (or [B, T, I] with batch_first); got shape {tuple(x.shape)}")
+    if batch_first:
+        x = x.transpose(0, 1)
+    T, B, _ = x.shape
+    if T == 0:
+        raise ValueError(f"seq length T must be > 0; got T={T}")
+    if B == 0:
+        raise ValueError(f"batch size B must be > 0; got B={B}")
+    gi = input_projection(x, Wi_cat, bi_cat, x_quant=x_quant, w_quant=w_quant)
+    return forward_fast_dispatch(kind, gi, h0, hidden, bh_cat, h_in_quant=h_in_quant, h_out_quant=h_out_quant,
+                                 batch_first=batch_first, hidden2=hidden2)
+

@@ -13,6 +13,7 @@ from gru_qat_amd.gru_layer import (
     _extract_h_quant_params,
     fast_dispatch_eligible,
     forward_fast_dispatch,
+    layer_forward,
     resolve_use_triton,
 )
 
@@ -73,3 +74,41 @@ def test_forward_fast_dispatch_argument_errors():
     # CPU tensors reach the scan, which rejects them before any device work
     with pytest.raises(ValueError):
         forward_fast_dispatch("diagonal", torch.zeros(3, 2, 3 * H), None, w, bh)
+
+
+def test_frozen_scale_is_read_once_per_version(monkeypatch):
+    """The reference syncs on scale.item() every forward (gru_layer.py:48); a
+    frozen scale is read once, and an in-place update is seen."""
+    calls = {"n": 0}
+    orig = torch.Tensor.item
+
+    def counting_item(self):
+        calls["n"] += 1
+        return orig(self)
+
+    q = _quantizer(scale=0.02)
+    monkeypatch.setattr(torch.Tensor, "item", counting_item)
+    first = _extract_h_quant_params(q)
+    n1 = calls["n"]
+    for _ in range(5):
+        assert _extract_h_quant_params(q) == first
+    assert calls["n"] == n1 == 1
+    q.scale.fill_(0.5)
+    assert _extract_h_quant_params(q)[0] == 0.5
+    assert calls["n"] == 2
+    other = _quantizer(scale=0.02)  # a different tensor with the same value: its own entry
+    assert _extract_h_quant_params(other) == first
+
+
+def test_layer_forward_argument_errors():
+    W = torch.zeros(12, 3)
+    with pytest.raises(ValueError, match="x must be"):
+        layer_forward("dense", torch.zeros(2, 3), None, W, None, torch.zeros(12, 4), torch.zeros(12))
+    with pytest.raises(ValueError, match="seq length T"):
+        layer_forward("dense", torch.zeros(0, 2, 3), None, W, None, torch.zeros(12, 4), torch.zeros(12))
+    with pytest.raises(ValueError, match="batch size B"):
+        layer_forward("dense", torch.zeros(2, 0, 3), None, W, None, torch.zeros(12, 4), torch.zeros(12))
+    with pytest.raises(ValueError, match="batch size B"):
+        layer_forward("dense", torch.zeros(0, 2, 3), None, W, None, torch.zeros(12, 4), torch.zeros(12),
+                      batch_first=True)
+
