@@ -74,3 +74,28 @@ def test_backward_matches_oracle(dev, idx, shape, nb, two, q):
         err = (g.cpu() - r).abs().max().item()
         print(f"[bwd] {cfg['name']} {shape} q={q is not None} d{k}: max err {err:.3e} (|ref| {r.abs().max().item():.3e})")
         assert err <= 1e-4 * max(1.0, r.abs().max().item()), k
+
+
+@pytest.mark.parametrize("idx,shape,nb,two", [(1, (9, 6, 128), None, False), (3, (6, 5, 64), 4, True),
+                                              (4, (5, 3, 64), None, False), (0, (9, 6, 40), None, False)])
+def test_backward_is_deterministic_and_accepts_strided_inputs(dev, idx, shape, nb, two):
+    """Two backward calls give bitwise-equal gradients (no atomics anywhere), and
+    a gi that is a strided view (every other step of a longer sequence, batch
+    rows of a wider tensor) gives the same gradients as its contiguous copy."""
+    cfg = _cfg(idx, shape, nb=nb, two=two, q=COARSE)
+    keys = ["gi", "h0", "bh"] + list(O.hidden_params(cfg))
+    T, B, H = shape
+    big = torch.randn(2 * T, B + 3, 3 * H, generator=torch.Generator().manual_seed(5))
+    big[::2, :B] = cfg["gi"]
+    gi_view = big.to(dev)[::2, :B]
+    assert not gi_view.is_contiguous()
+    dout = torch.randn((T, B, H), generator=torch.Generator().manual_seed(13)).to(dev)
+    runs = []
+    for gi_src in (gi_view, gi_view.contiguous(), gi_view.contiguous()):
+        leaves = {k: cfg[k].to(dev).requires_grad_(True) for k in keys if k != "gi"}
+        leaves["gi"] = gi_src.detach().requires_grad_(True)
+        out = _run(cfg, dev, leaves)
+        runs.append(torch.autograd.grad(out, [leaves[k] for k in keys], dout))
+    for a, b, c in zip(*runs):
+        assert torch.equal(b, c)  # deterministic
+        assert torch.equal(a, b)  # strided input == contiguous input
