@@ -113,6 +113,7 @@ int64_t dense_workspace_bytes(const gs_args* a);
 int64_t monarch_workspace_bytes(const gs_args* a);
 int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a);
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
+int64_t butterfly_bwd_workspace_bytes(const gs_bwd_args* a);
 }  // namespace gs
 
 extern "C" {
@@ -140,8 +141,9 @@ int64_t gs_bwd_workspace_bytes(int kind, const gs_bwd_args* a) {
     case GS_KIND_DIAGONAL:
       return 0;
     case GS_KIND_MONARCH:
-    case GS_KIND_BUTTERFLY:
       return gs::struct_bwd_workspace_bytes(kind, a);
+    case GS_KIND_BUTTERFLY:
+      return gs::butterfly_bwd_workspace_bytes(a);
     default:
       return gs::set_error(GS_ERR_INVALID, "gs_bwd_workspace_bytes: unknown kind %d", kind);
   }

@@ -1,0 +1,481 @@
+// Butterfly GRU scan backward (gfx950), stage by stage.
+//
+// Reference: the butterfly backward kernel and launcher (LarocheC/gru-triton
+// src/gru_qat/triton_kernels/scan_butterfly.py:462-1075) and the PyTorch
+// backward it restates (scan.py:1460-1550 with the butterfly map). The map of
+// gate g is a chain of K = nchains L sparse stages S_1 .. S_K on vectors
+// zero-padded to N = 2^L (stage order, strides and twiddle selection as in the
+// forward, scan_butterfly.hip), so gh_g = [S_K ... S_1 q_in(h)]_{:H} + bh_g.
+//
+// As in the dense backward (scan_dense_bwd.hip), every gradient of step t is
+// D_t times a coefficient fixed by the forward, and the recurrence is
+//   D_{t-1} = dout[t-1] + Zm_t D_t + Mi_t sum_g S_1^T ... S_K^T (D_t Cg_t)
+// Batch rows never interact, so one workgroup owns one row for all T steps
+// and applies the transposed stages in reverse order in LDS, with no
+// exchange between workgroups. The launcher runs
+//   1. build_prev_state: hq = q_in([h0; out[0..T-2]]);
+//   2. bfly_apply_batch: gh of every (t, b) at once (the forward's stages on hq);
+//   3. the dense backward's coefficient pass;
+//   4. bfly_bwd_kernel: the recurrence, writing D_t and dh0;
+//   5. the dense backward's gradient pass: dgi, dgh_n, per-row dbh;
+//   6. bfly_twiddle_grad: for every (t, b) and gate, the stages run forward on
+//      hq (activations A_j kept in LDS) and dgh runs backward through them
+//      (G_j); stage j's twiddles collect the dots of G_{j+1} with A_j (own
+//      element for the diagonal twiddle, the partner for the other) in
+//      per-workgroup LDS accumulators, summed over workgroups by
+//      bfly_twiddle_sum.
+// Shapes whose LDS needs exceed the device limit fall back to the
+// materialized-map backward (scan_struct_bwd.hip).
+#include "gs_gemm.h"
+#include "gs_mfma.h"
+
+namespace gs {
+
+int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream);
+int grad_chunks(int64_t T);
+int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
+                float* chunks, hipStream_t stream, const char* who);
+int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
+int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* who);
+
+namespace {
+
+// Twiddles of element i in layer s of a single chain (stride 2^s): the
+// diagonal one (own element), the off-diagonal one (partner i ^ 2^s), and the
+// partner row's off-diagonal one (S[partner][i]), which the transposed stage
+// needs. tw_g is one gate's [L][N/2][2][2].
+struct ElemTw {
+  float t_ii, t_ip, t_pi;
+};
+
+__device__ __forceinline__ ElemTw elem_tw(const float* tw_g, int N, int s, int i) {
+  const int m = (i >> s) & 1;
+  const int pair = ((i >> (s + 1)) << s) | (i & ((1 << s) - 1));
+  const float* t = tw_g + ((int64_t)s * (N / 2) + pair) * 4;
+  ElemTw r;
+  r.t_ii = t[3 * m];          // [m][m]
+  r.t_ip = t[2 * m + 1 - m];  // [m][1 - m]
+  r.t_pi = t[2 - m];          // [1 - m][m]
+  return r;
+}
+
+// Lane layout of the forward's register kernel (scan_butterfly.hip): a gate
+// vector of N = 256 WPG elements spreads over WPG waves; lane l of the gate's
+// wave w holds elements i = l + 64 r + 256 w, r < 4. The partner of i in layer
+// s (i ^ 2^s) comes from a DPP move (strides 1-8), an LDS permute (16, 32),
+// another register of the same lane (64, 128) or an LDS exchange between the
+// gate's waves (>= 256, the only case that needs a workgroup barrier).
+template <int S>
+__device__ __forceinline__ void partner_of(const float (&x)[4], float (&y)[4], float* xch, const int (&idx)[4]) {
+  if constexpr (S <= 3) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = lane_xor_c<1 << S>(x[r]);
+  } else if constexpr (S < 6) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = lane_xor(x[r], 1 << S);
+  } else if constexpr (S < 8) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = x[r ^ (1 << (S - 6))];
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xch[idx[r]] = x[r];
+    lds_barrier();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = xch[idx[r] ^ (1 << S)];
+  }
+}
+
+template <int LOGN>
+struct Lay {
+  static constexpr int N = 1 << LOGN;
+  static constexpr int WPG = N / 256;  // waves per gate vector
+};
+
+// gh[v][g H + i] = [S_L ... S_1 hq[v]]_i + bh[g H + i] for every vector v:
+// 3 WPG waves, one gate per WPG of them.
+template <int LOGN>
+__global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_batch(const float* hq, const float* tw,
+                                                                        const float* bh, float* gh, int64_t nvec,
+                                                                        int H) {
+  constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
+  __shared__ float xch[2][3][N];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = wv / WPG, w = wv - g * WPG;
+  int idx[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) idx[r] = lane + 64 * r + 256 * w;
+  float tii[L][4], tip[L][4];
+  const float* tw_g = tw + (int64_t)g * L * (N / 2) * 4;
+#pragma unroll
+  for (int s = 0; s < L; ++s)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const ElemTw e = elem_tw(tw_g, N, s, idx[r]);
+      tii[s][r] = e.t_ii;
+      tip[s][r] = e.t_ip;
+    }
+  for (int64_t v = blockIdx.x; v < nvec; v += gridDim.x) {
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = idx[r] < H ? hq[v * H + idx[r]] : 0.0f;
+    static_for<0, L>([&](auto S) {
+      constexpr int s = S;
+      float y[4];
+      partner_of<s>(x, y, xch[s & 1][g], idx);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma clang fp contract(off)
+        x[r] = tii[s][r] * x[r] + tip[s][r] * y[r];
+      }
+    });
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (idx[r] < H) gh[v * 3 * H + g * H + idx[r]] = x[r] + bh[g * H + idx[r]];
+    lds_barrier();  // the next vector's exchanges reuse xch
+  }
+}
+
+struct RecParams {
+  const float* tw;
+  const float* dout;  // [T, B, H]
+  const float* cg;    // [T B, 3H] (Cr, Cz, Chn)
+  const float* zm;    // [T B, H]
+  const float* mi;    // [T B, H]
+  float* dsum;        // [T B, H] D_t
+  float* dh0;         // [B, H]
+  int T, B, H;
+};
+
+// One workgroup per batch row b for all T steps, the forward's wave layout.
+// Per step: each gate's waves form v_g = D_t Cg_t on their elements and run
+// the transposed layers from L-1 down to 0; gates z and n hand their results
+// to the gate-r waves through LDS, which form the carry and D_{t-1} and
+// broadcast it back.
+template <int LOGN>
+__global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams p) {
+  constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
+  __shared__ float xch[2][3][N];
+  __shared__ float ghs[3][N];
+  __shared__ float dv[N];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = wv / WPG, w = wv - g * WPG;
+  const int H = p.H, b = blockIdx.x;
+  int idx[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) idx[r] = lane + 64 * r + 256 * w;
+  float tii[L][4], tpi[L][4];
+  const float* tw_g = p.tw + (int64_t)g * L * (N / 2) * 4;
+#pragma unroll
+  for (int s = 0; s < L; ++s)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const ElemTw e = elem_tw(tw_g, N, s, idx[r]);
+      tii[s][r] = e.t_ii;
+      tpi[s][r] = e.t_pi;
+    }
+  const int64_t BH = (int64_t)p.B * H;
+  float d[4];  // D_t of this lane's elements
+#pragma unroll
+  for (int r = 0; r < 4; ++r) d[r] = idx[r] < H ? p.dout[(int64_t)(p.T - 1) * BH + (int64_t)b * H + idx[r]] : 0.0f;
+  // The step's inputs (Cg for every gate; Zm, Mi and dout[t-1] for gate r)
+  // are loaded one step ahead, so their memory latency overlaps the layers.
+  float cgv[4], zmv[4], miv[4], dprev[4];
+  auto load_step = [&](int t, float (&c)[4], float (&z)[4], float (&m)[4], float (&dp)[4]) {
+    const int64_t row = (int64_t)t * p.B + b;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = idx[r] < H;
+      c[r] = ok ? p.cg[row * 3 * H + g * H + idx[r]] : 0.0f;
+      if (g == 0) {
+        z[r] = ok ? p.zm[row * H + idx[r]] : 0.0f;
+        m[r] = ok ? p.mi[row * H + idx[r]] : 0.0f;
+        dp[r] = (ok && t > 0) ? p.dout[(row - p.B) * H + idx[r]] : 0.0f;
+      }
+    }
+  };
+  load_step(p.T - 1, cgv, zmv, miv, dprev);
+  for (int t = p.T - 1; t >= 0; --t) {
+    const int64_t row = (int64_t)t * p.B + b;
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = d[r] * cgv[r];
+      if (g == 0 && idx[r] < H) p.dsum[row * H + idx[r]] = d[r];
+    }
+    float ncg[4], nzm[4], nmi[4], ndp[4];
+    if (t > 0) load_step(t - 1, ncg, nzm, nmi, ndp);
+    static_for<0, L>([&](auto S) {
+      constexpr int s = L - 1 - S;
+      float y[4];
+      partner_of<s>(x, y, xch[S & 1][g], idx);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+#pragma clang fp contract(off)
+        x[r] = tii[s][r] * x[r] + tpi[s][r] * y[r];
+      }
+    });
+    if (g != 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ghs[g][idx[r]] = x[r];
+    }
+    lds_barrier();
+    if (g == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float via, carry;
+        {
+#pragma clang fp contract(off)
+          via = (x[r] + ghs[1][idx[r]]) + ghs[2][idx[r]];
+          carry = zmv[r] * d[r] + miv[r] * via;
+        }
+        if (idx[r] < H) {
+          if (t == 0)
+            p.dh0[(int64_t)b * H + idx[r]] = carry;
+          else
+            dv[idx[r]] = dprev[r] + carry;
+        }
+      }
+    }
+    lds_barrier();
+    if (t > 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        d[r] = idx[r] < H ? dv[idx[r]] : 0.0f;
+        cgv[r] = ncg[r];
+        zmv[r] = nzm[r];
+        miv[r] = nmi[r];
+        dprev[r] = ndp[r];
+      }
+    }
+  }
+}
+
+struct TwParams {
+  const float* tw;
+  const float* hq;    // [TB, H]
+  const float* dgi;   // [TB, 3H] (r, z parts are dgh's)
+  const float* dghn;  // [TB, H]
+  float* part;        // [3][nchunk][L][N][2]
+  int64_t nvec;
+  int nchunk, H;
+};
+
+// Workgroup (chunk, gate) of WPG waves, the forward's lane layout: for
+// vectors v = chunk, chunk + nchunk, ... the layers run forward on hq, each
+// lane keeping its elements' activations and their partners' (a, ap) in
+// registers, then dgh runs backward through the transposed layers; each lane
+// accumulates its elements' two twiddle gradients per layer in registers.
+template <int LOGN>
+__global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p) {
+  constexpr int N = Lay<LOGN>::N, L = LOGN;
+  __shared__ float xch[2][N];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int chunk = blockIdx.x, g = blockIdx.y, H = p.H;
+  int idx[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) idx[r] = lane + 64 * r + 256 * w;
+  float tii[L][4], tip[L][4], tpi[L][4], accd[L][4], acco[L][4];
+  const float* tw_g = p.tw + (int64_t)g * L * (N / 2) * 4;
+#pragma unroll
+  for (int s = 0; s < L; ++s)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const ElemTw e = elem_tw(tw_g, N, s, idx[r]);
+      tii[s][r] = e.t_ii;
+      tip[s][r] = e.t_ip;
+      tpi[s][r] = e.t_pi;
+      accd[s][r] = acco[s][r] = 0.0f;
+    }
+  for (int64_t v = chunk; v < p.nvec; v += p.nchunk) {
+    float a[L][4], ap[L][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) a[0][r] = idx[r] < H ? p.hq[v * H + idx[r]] : 0.0f;
+    static_for<0, L>([&](auto S) {
+      constexpr int s = S;
+      partner_of<s>(a[s], ap[s], xch[s & 1], idx);
+      if constexpr (s + 1 < L) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma clang fp contract(off)
+          a[s + 1][r] = tii[s][r] * a[s][r] + tip[s][r] * ap[s][r];
+        }
+      }
+    });
+    float gv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float d0 = 0.0f;
+      if (idx[r] < H) d0 = g < 2 ? p.dgi[v * 3 * H + g * H + idx[r]] : p.dghn[v * H + idx[r]];
+      gv[r] = d0;
+    }
+    static_for<0, L>([&](auto S) {
+      constexpr int s = L - 1 - S;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        accd[s][r] += gv[r] * a[s][r];
+        acco[s][r] += gv[r] * ap[s][r];
+      }
+      if constexpr (s > 0) {
+        float y[4];
+        partner_of<s>(gv, y, xch[S & 1], idx);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma clang fp contract(off)
+          gv[r] = tii[s][r] * gv[r] + tpi[s][r] * y[r];
+        }
+      }
+    });
+    lds_barrier();  // the next vector's exchanges reuse xch
+  }
+  float* out = p.part + ((int64_t)g * p.nchunk + chunk) * 2 * L * N;
+#pragma unroll
+  for (int s = 0; s < L; ++s)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      out[((int64_t)s * N + idx[r]) * 2] = accd[s][r];
+      out[((int64_t)s * N + idx[r]) * 2 + 1] = acco[s][r];
+    }
+}
+
+// dtw[g][0][s][pair][m][*] from the chunk sums of element i = the element
+// with that pair and m.
+__global__ void bfly_twiddle_sum(const float* part, float* dtw, int nchunk, int N, int L) {
+  const int64_t per_gate = (int64_t)L * N;
+  const int64_t n = 3 * per_gate;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int g = (int)(e / per_gate);
+    const int64_t r = e - g * per_gate;
+    const int s = (int)(r / N), i = (int)(r - (int64_t)s * N);
+    float sd = 0.0f, so = 0.0f;
+    const float* src = part + ((int64_t)g * nchunk * per_gate + r) * 2;
+    for (int c = 0; c < nchunk; ++c) {
+      sd += src[(int64_t)c * per_gate * 2];
+      so += src[(int64_t)c * per_gate * 2 + 1];
+    }
+    const int m = (i >> s) & 1;
+    const int pair = ((i >> (s + 1)) << s) | (i & ((1 << s) - 1));
+    float* d = dtw + (int64_t)g * L * (N / 2) * 4 + ((int64_t)s * (N / 2) + pair) * 4 + 2 * m;
+    d[m] = sd;
+    d[1 - m] = so;
+  }
+}
+
+struct NativePlan {
+  bool ok = false;
+  int nchunk = 0;
+  int64_t hq, cg, plane, chunks, part;
+  int64_t total() const { return kCtrlBytes + hq + cg + 5 * plane + chunks + part; }
+};
+
+NativePlan plan_native(const gs_bwd_args* a) {
+  NativePlan pl;
+  // The stage-wise kernels hold one chain's twiddles in registers: one chain,
+  // N = 2^log_n in {256, 512, 1024} (the forward's register-kernel shapes).
+  if (a->bfly_nblocks != 1 || a->log_n < 8 || a->log_n > 10) return pl;
+  const int N = 1 << a->log_n;
+  const int64_t H = a->H, TB = a->T * a->B;
+  if (N < H) return pl;
+  pl.nchunk = (int)std::max<int64_t>(1, std::min<int64_t>(TB, 256));
+  pl.hq = align256(TB * H * 4);
+  pl.cg = align256(TB * 3 * H * 4);
+  pl.plane = align256(TB * H * 4);
+  pl.chunks = align256((int64_t)grad_chunks(a->T) * a->B * 3 * H * 4);
+  pl.part = align256((int64_t)3 * pl.nchunk * 2 * a->log_n * N * 4);
+  pl.ok = true;
+  return pl;
+}
+
+template <int LOGN>
+int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* cg, float* cgn, float* zm, float* mi,
+                  float* dsum, float* dghn, float* chunks, float* part, hipStream_t stream, const char* who) {
+  constexpr int NT3 = 3 * (1 << LOGN) / 4;
+  const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
+  const int64_t TB = (int64_t)T * B;
+  hipLaunchKernelGGL(bfly_apply_batch<LOGN>, dim3((unsigned)std::min<int64_t>(TB, 2048)), dim3(NT3), 0, stream, hq,
+                     a->w, a->bh, cg, TB, H);
+  GS_CHECK_HIP(hipGetLastError());
+  int rc = launch_coef(a, cg, cgn, zm, mi, stream);
+  if (rc) return rc;
+  RecParams rp;
+  rp.tw = a->w;
+  rp.dout = a->dout;
+  rp.cg = cg;
+  rp.zm = zm;
+  rp.mi = mi;
+  rp.dsum = dsum;
+  rp.dh0 = a->dh0;
+  rp.T = T;
+  rp.B = B;
+  rp.H = H;
+  hipLaunchKernelGGL(bfly_bwd_kernel<LOGN>, dim3((unsigned)B), dim3(NT3), 0, stream, rp);
+  GS_CHECK_HIP(hipGetLastError());
+  rc = launch_grad(a, dsum, cg, cgn, dghn, chunks, stream, who);
+  if (rc) return rc;
+  TwParams tp;
+  tp.tw = a->w;
+  tp.hq = hq;
+  tp.dgi = a->dgi;
+  tp.dghn = dghn;
+  tp.part = part;
+  tp.nvec = TB;
+  tp.nchunk = pl.nchunk;
+  tp.H = H;
+  hipLaunchKernelGGL(bfly_twiddle_grad<LOGN>, dim3((unsigned)pl.nchunk, 3), dim3((1 << LOGN) / 4), 0, stream, tp);
+  GS_CHECK_HIP(hipGetLastError());
+  const int64_t nsum = (int64_t)3 * LOGN * (1 << LOGN);
+  hipLaunchKernelGGL(bfly_twiddle_sum, dim3((unsigned)((nsum + 255) / 256)), dim3(256), 0, stream, part, a->dw_part,
+                     pl.nchunk, 1 << LOGN, LOGN);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
+
+}  // namespace
+
+int64_t butterfly_bwd_workspace_bytes(const gs_bwd_args* a) {
+  const NativePlan pl = plan_native(a);
+  if (pl.ok) return pl.total();
+  return struct_bwd_workspace_bytes(GS_KIND_BUTTERFLY, a);
+}
+
+}  // namespace gs
+
+extern "C" int gs_butterfly_bwd(const gs_bwd_args* a, hipStream_t stream) {
+  using namespace gs;
+  const char* who = "gs_butterfly_bwd";
+  clear_error();
+  int rc = validate_bwd_common(a, who);
+  if (rc) return rc;
+  const NativePlan pl = plan_native(a);
+  if (!pl.ok) return run_struct(GS_KIND_BUTTERFLY, a, stream, who);
+  if (a->dw_part == nullptr) return set_error(GS_ERR_INVALID, "%s: dw_part must be a non-NULL device pointer", who);
+  if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the butterfly kind", who);
+  if (a->T > 1 && a->so_t != a->B * a->so_b)
+    return set_error(GS_ERR_INVALID, "%s: out must hold its steps back to back (so_t == B * so_b); got so_t=%lld, so_b=%lld",
+                     who, (long long)a->so_t, (long long)a->so_b);
+  const gs_args f = fwd_view(*a);
+  rc = check_workspace(&f, pl.total(), who);
+  if (rc) return rc;
+
+  const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
+  char* cur = static_cast<char*>(a->workspace) + kCtrlBytes;
+  auto take = [&](int64_t bytes) {
+    char* r = cur;
+    cur += bytes;
+    return reinterpret_cast<float*>(r);
+  };
+  float* hq = take(pl.hq);
+  float* cg = take(pl.cg);
+  float* cgn = take(pl.plane);
+  float* zm = take(pl.plane);
+  float* mi = take(pl.plane);
+  float* dsum = take(pl.plane);
+  float* dghn = take(pl.plane);
+  float* chunks = take(pl.chunks);
+  float* part = take(pl.part);
+
+  rc = build_prev_state(hq, a->h0, a->sh0_b, a->out, a->so_b, T, B, H, to_quant(a->q_in), stream, who);
+  if (rc) return rc;
+  switch (a->log_n) {
+    case 8: return launch_stages<8>(a, pl, hq, cg, cgn, zm, mi, dsum, dghn, chunks, part, stream, who);
+    case 9: return launch_stages<9>(a, pl, hq, cg, cgn, zm, mi, dsum, dghn, chunks, part, stream, who);
+    default: return launch_stages<10>(a, pl, hq, cg, cgn, zm, mi, dsum, dghn, chunks, part, stream, who);
+  }
+}

@@ -368,6 +368,28 @@ int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
 
 }  // namespace
 
+int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream) {
+  const int64_t n = a->T * a->B * a->H;
+  hipLaunchKernelGGL(coef_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0, stream,
+                     a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b, a->out, a->so_t, a->so_b, cg, cgn, zm, mi, (int)a->T,
+                     (int)a->B, (int)a->H, to_quant(a->q_in), to_quant(a->q_out));
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
+
+int grad_chunks(int64_t T) { return (int)((T + kGradSteps - 1) / kGradSteps); }
+
+int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
+                float* chunks, hipStream_t stream, const char* who) {
+  const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
+  const int nch = grad_chunks(T);
+  const int64_t n = (int64_t)nch * B * H;
+  hipLaunchKernelGGL(grad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, dsum, cg, cgn, a->dgi,
+                     dghn, chunks, T, B, H);
+  GS_CHECK_HIP(hipGetLastError());
+  return sum_partials(a->dbh_part, chunks, (int64_t)B * 3 * H, nch, (int64_t)B * 3 * H, stream, who);
+}
+
 int64_t dense_bwd_core_bytes(const gs_bwd_args* a, const char* who) {
   BPlan pl;
   const int rc = plan_bwd(a, &pl, who);

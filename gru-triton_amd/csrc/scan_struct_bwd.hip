@@ -280,6 +280,10 @@ int plan_struct(int kind, const gs_bwd_args* a, StructPlan* sp, const char* who)
   return GS_OK;
 }
 
+}  // namespace
+
+// The materialized-map backward of either kind (the butterfly entry point
+// also falls back here for shapes its stage kernels cannot hold in LDS).
 int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* who) {
   clear_error();
   int rc = validate_bwd_common(a, who);
@@ -351,8 +355,6 @@ int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* w
   return GS_OK;
 }
 
-}  // namespace
-
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a) {
   StructPlan sp;
   const int rc = plan_struct(kind, a, &sp, "gs_bwd_workspace_bytes");
@@ -366,6 +368,3 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   return gs::run_struct(GS_KIND_MONARCH, a, stream, "gs_monarch_bwd");
 }
 
-extern "C" int gs_butterfly_bwd(const gs_bwd_args* a, hipStream_t stream) {
-  return gs::run_struct(GS_KIND_BUTTERFLY, a, stream, "gs_butterfly_bwd");
-}

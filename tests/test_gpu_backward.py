@@ -99,3 +99,22 @@ def test_backward_is_deterministic_and_accepts_strided_inputs(dev, idx, shape, n
     for a, b, c in zip(*runs):
         assert torch.equal(b, c)  # deterministic
         assert torch.equal(a, b)  # strided input == contiguous input
+
+
+@pytest.mark.parametrize("q", [None, COARSE])
+def test_butterfly_backward_materialized_fallback(dev, q):
+    """Twiddles of H_PAD = 2048 for H = 600 exceed what the stage-wise kernels
+    hold in LDS, so gs_butterfly_bwd takes the materialized-map path."""
+    cfg = _cfg(4, (4, 3, 600), q=q)
+    cfg["w"] = torch.randn((3, 1, 11, 1024, 2, 2), generator=torch.Generator().manual_seed(8)) * 0.5 ** 0.5
+    keys = ["gi", "h0", "bh", "w"]
+    leaves = {k: cfg[k].to(dev).requires_grad_(True) for k in keys}
+    out = _run(cfg, dev, leaves)
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(13)).to(dev)
+    grads = torch.autograd.grad(out, [leaves[k] for k in keys], dout)
+    ref = O.scan_backward(cfg, out.detach().cpu(), dout.cpu())
+    for k, g in zip(keys, grads):
+        r = ref["d" + k]
+        err = (g.cpu() - r).abs().max().item()
+        print(f"[bwd] butterfly H_PAD=2048 d{k}: max err {err:.3e}")
+        assert err <= 1e-4 * max(1.0, r.abs().max().item()), k
