@@ -105,6 +105,16 @@ int check_workspace(const gs_args* a, int64_t need, const char* who) {
   return GS_OK;
 }
 
+int check_scratch(const gs_bwd_args* a, int64_t need, const char* who) {
+  if (need <= 0) return GS_OK;
+  if (a->scratch == nullptr || a->scratch_bytes < need)
+    return set_error(GS_ERR_INVALID, "%s: scratch of %lld bytes required; got %lld at %p", who, (long long)need,
+                     (long long)a->scratch_bytes, a->scratch);
+  if ((reinterpret_cast<uintptr_t>(a->scratch) & 255u) != 0)
+    return set_error(GS_ERR_INVALID, "%s: scratch must be 256-byte aligned", who);
+  return GS_OK;
+}
+
 }  // namespace gs
 
 // Defined in the kernel translation units.
@@ -112,8 +122,11 @@ namespace gs {
 int64_t dense_workspace_bytes(const gs_args* a);
 int64_t monarch_workspace_bytes(const gs_args* a);
 int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a);
+int64_t dense_bwd_scratch_bytes(const gs_bwd_args* a);
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
+int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
 int64_t butterfly_bwd_workspace_bytes(const gs_bwd_args* a);
+int64_t butterfly_bwd_scratch_bytes(const gs_bwd_args* a);
 }  // namespace gs
 
 extern "C" {
@@ -146,6 +159,22 @@ int64_t gs_bwd_workspace_bytes(int kind, const gs_bwd_args* a) {
       return gs::butterfly_bwd_workspace_bytes(a);
     default:
       return gs::set_error(GS_ERR_INVALID, "gs_bwd_workspace_bytes: unknown kind %d", kind);
+  }
+}
+
+int64_t gs_bwd_scratch_bytes(int kind, const gs_bwd_args* a) {
+  if (a == nullptr) return gs::set_error(GS_ERR_INVALID, "gs_bwd_scratch_bytes: args is NULL");
+  switch (kind) {
+    case GS_KIND_DENSE:
+      return gs::dense_bwd_scratch_bytes(a);
+    case GS_KIND_DIAGONAL:
+      return 0;
+    case GS_KIND_MONARCH:
+      return gs::struct_bwd_scratch_bytes(kind, a);
+    case GS_KIND_BUTTERFLY:
+      return gs::butterfly_bwd_scratch_bytes(a);
+    default:
+      return gs::set_error(GS_ERR_INVALID, "gs_bwd_scratch_bytes: unknown kind %d", kind);
   }
 }
 

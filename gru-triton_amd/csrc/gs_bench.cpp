@@ -252,11 +252,16 @@ int run_config(int idx, int launches, int warmup, bool backward) {
     b.q_in = a.q_in;
     b.q_out = a.q_out;
     const int64_t nb = gs_bwd_workspace_bytes(kind, &b);
-    if (nb < 0) {
-      fprintf(stderr, "gs_bench: gs_bwd_workspace_bytes: %s\n", gs_last_error());
+    const int64_t ns = gs_bwd_scratch_bytes(kind, &b);
+    if (nb < 0 || ns < 0) {
+      fprintf(stderr, "gs_bench: gs_bwd_workspace_bytes / gs_bwd_scratch_bytes: %s\n", gs_last_error());
       return 1;
     }
     need = std::max(need, nb);
+    if (ns > 0) {
+      CHECK(hipMalloc(&b.scratch, ns));
+      b.scratch_bytes = ns;
+    }
   }
   void* ws = nullptr;
   CHECK(hipMalloc(&ws, need));
@@ -308,6 +313,7 @@ int run_config(int idx, int launches, int warmup, bool backward) {
     report(kNames[idx], idx, ms, T, B, H);
   }
   CHECK(hipFree(ws));
+  if (b.scratch) CHECK(hipFree(b.scratch));
   for (float* p : owned) CHECK(hipFree(p));
   CHECK(hipStreamDestroy(st));
   return 0;

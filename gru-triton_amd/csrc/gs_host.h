@@ -63,5 +63,7 @@ gs_args fwd_view(const gs_bwd_args& a);
 int validate_bwd_common(const gs_bwd_args* a, const char* who);
 int validate_quant(const gs_quant& q, const char* name, const char* who);
 int check_workspace(const gs_args* a, int64_t need, const char* who);
+// The backward's plain scratch: non-NULL, large enough, 256-byte aligned.
+int check_scratch(const gs_bwd_args* a, int64_t need, const char* who);
 
 }  // namespace gs

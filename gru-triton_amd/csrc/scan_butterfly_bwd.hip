@@ -36,6 +36,7 @@ int grad_chunks(int64_t T);
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
                 float* chunks, hipStream_t stream, const char* who);
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
+int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
 int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* who);
 
 namespace {
@@ -362,7 +363,7 @@ struct NativePlan {
   bool ok = false;
   int nchunk = 0;
   int64_t hq, cg, plane, chunks, part;
-  int64_t total() const { return kCtrlBytes + hq + cg + 5 * plane + chunks + part; }
+  int64_t scratch() const { return hq + cg + 5 * plane + chunks + part; }  // no tagged words
 };
 
 NativePlan plan_native(const gs_bwd_args* a) {
@@ -431,8 +432,14 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
 
 int64_t butterfly_bwd_workspace_bytes(const gs_bwd_args* a) {
   const NativePlan pl = plan_native(a);
-  if (pl.ok) return pl.total();
+  if (pl.ok) return 0;
   return struct_bwd_workspace_bytes(GS_KIND_BUTTERFLY, a);
+}
+
+int64_t butterfly_bwd_scratch_bytes(const gs_bwd_args* a) {
+  const NativePlan pl = plan_native(a);
+  if (pl.ok) return pl.scratch();
+  return struct_bwd_scratch_bytes(GS_KIND_BUTTERFLY, a);
 }
 
 }  // namespace gs
@@ -450,12 +457,11 @@ extern "C" int gs_butterfly_bwd(const gs_bwd_args* a, hipStream_t stream) {
   if (a->T > 1 && a->so_t != a->B * a->so_b)
     return set_error(GS_ERR_INVALID, "%s: out must hold its steps back to back (so_t == B * so_b); got so_t=%lld, so_b=%lld",
                      who, (long long)a->so_t, (long long)a->so_b);
-  const gs_args f = fwd_view(*a);
-  rc = check_workspace(&f, pl.total(), who);
+  rc = check_scratch(a, pl.scratch(), who);
   if (rc) return rc;
 
   const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
-  char* cur = static_cast<char*>(a->workspace) + kCtrlBytes;
+  char* cur = static_cast<char*>(a->scratch);
   auto take = [&](int64_t bytes) {
     char* r = cur;
     cur += bytes;

@@ -327,15 +327,15 @@ BFn pick_bwd(int KC, int* nt) {
   }
 }
 
-// Workspace after the control words, each region 256-byte aligned:
-//   xh [2][Bp][H] tagged D | xw [nrb P] | cg [T B, 3H] | hq, cgn, zm, mi,
-//   dsum, dghn [T B, H] each | dbh chunks [nchunks][B][3H] | dWh split partials
+// Workspace (tagged words only): control words | xh [2][Bp][H] tagged D |
+// xw [nrb P]. Scratch (plain floats), each region 256-byte aligned:
+// cg [T B, 3H] | hq, cgn, zm, mi, dsum, dghn [T B, H] each |
+// dbh chunks [nchunks][B][3H] | dWh split partials.
 struct BPlan {
   int KC, nt, nwc, P, nrb, Bp, hsz, split, nchunks;
   int64_t xh_bytes, xw_bytes, cg_bytes, plane_bytes, chunk_bytes, part_bytes;
-  int64_t total() const {
-    return kCtrlBytes + xh_bytes + xw_bytes + cg_bytes + 6 * plane_bytes + chunk_bytes + part_bytes;
-  }
+  int64_t total() const { return kCtrlBytes + xh_bytes + xw_bytes; }
+  int64_t scratch() const { return cg_bytes + 6 * plane_bytes + chunk_bytes + part_bytes; }
 };
 
 int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
@@ -397,11 +397,20 @@ int64_t dense_bwd_core_bytes(const gs_bwd_args* a, const char* who) {
   return pl.total();
 }
 
+int64_t dense_bwd_core_scratch(const gs_bwd_args* a, const char* who) {
+  BPlan pl;
+  const int rc = plan_bwd(a, &pl, who);
+  if (rc) return rc;
+  return pl.scratch();
+}
+
 int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a) { return dense_bwd_core_bytes(a, "gs_bwd_workspace_bytes"); }
+int64_t dense_bwd_scratch_bytes(const gs_bwd_args* a) { return dense_bwd_core_scratch(a, "gs_bwd_scratch_bytes"); }
 
 // The dense backward of a hidden map given as the matrix w [3H, H] (rows r,
 // z, n); writes dgi, dh0 and dbh_part of `a` and the map's gradient dw
-// [3H, H]. Uses the first dense_bwd_core_bytes(a) bytes of a->workspace.
+// [3H, H]. Uses the first dense_bwd_core_bytes(a) bytes of a->workspace and
+// the first dense_bwd_core_scratch(a) bytes of a->scratch.
 int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t stream, const char* who) {
   if (a->T > 1 && a->so_t != a->B * a->so_b)
     return set_error(GS_ERR_INVALID, "%s: out must hold its steps back to back (so_t == B * so_b); got so_t=%lld, so_b=%lld",
@@ -412,17 +421,19 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   const gs_args f = fwd_view(*a);
   rc = check_workspace(&f, pl.total(), who);
   if (rc) return rc;
+  rc = check_scratch(a, pl.scratch(), who);
+  if (rc) return rc;
 
   const int T = (int)a->T, B = (int)a->B, H = (int)a->H, TB = T * B;
   char* ws = static_cast<char*>(a->workspace);
-  char* cur = ws + kCtrlBytes;
+  uint64_t* xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
+  uint64_t* xw = reinterpret_cast<uint64_t*>(ws + kCtrlBytes + pl.xh_bytes);
+  char* cur = static_cast<char*>(a->scratch);
   auto take = [&](int64_t bytes) {
     char* r = cur;
     cur += bytes;
     return r;
   };
-  uint64_t* xh = reinterpret_cast<uint64_t*>(take(pl.xh_bytes));
-  uint64_t* xw = reinterpret_cast<uint64_t*>(take(pl.xw_bytes));
   float* cg = reinterpret_cast<float*>(take(pl.cg_bytes));
   float* hq = reinterpret_cast<float*>(take(pl.plane_bytes));
   float* cgn = reinterpret_cast<float*>(take(pl.plane_bytes));

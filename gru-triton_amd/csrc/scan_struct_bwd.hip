@@ -8,7 +8,7 @@
 // the gradient through the map) and the map's dense gradient
 // dM_g = sum_t dgh_g,t^T q_in(h_{t-1}); both are what the dense backward
 // (scan_dense_bwd.hip) computes for a [3H, H] weight. So each entry point
-//   1. materializes M = [M_r; M_z; M_n] into the workspace,
+//   1. materializes M = [M_r; M_z; M_n] into the scratch,
 //   2. runs the dense backward core with it (dgi, dh0, dbh, dM), and
 //   3. carries dM onto the structured parameters:
 //      Monarch single factor   dW[g][n] = the n-th diagonal block of dM_g;
@@ -31,6 +31,7 @@
 namespace gs {
 
 int64_t dense_bwd_core_bytes(const gs_bwd_args* a, const char* who);
+int64_t dense_bwd_core_scratch(const gs_bwd_args* a, const char* who);
 int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t stream, const char* who);
 
 namespace {
@@ -249,15 +250,19 @@ __global__ __launch_bounds__(kRowThreads) void bfly_stage_bwd(const float* tw, i
 }
 
 struct StructPlan {
-  int64_t core, mat_bytes, act_bytes, g_bytes;
+  int64_t core, core_scratch, mat_bytes, act_bytes, g_bytes;
   int N = 0, L = 0, K = 0;
-  int64_t total() const { return core + 2 * mat_bytes + act_bytes + g_bytes; }
+  int64_t total() const { return core; }  // tagged workspace: the dense core's
+  int64_t scratch() const { return core_scratch + 2 * mat_bytes + act_bytes + g_bytes; }
 };
 
 int plan_struct(int kind, const gs_bwd_args* a, StructPlan* sp, const char* who) {
   const int64_t core = dense_bwd_core_bytes(a, who);
   if (core < 0) return (int)core;
+  const int64_t core_scratch = dense_bwd_core_scratch(a, who);
+  if (core_scratch < 0) return (int)core_scratch;
   sp->core = core;
+  sp->core_scratch = core_scratch;
   const int64_t H = a->H;
   sp->mat_bytes = align256(3 * H * H * 4);
   sp->act_bytes = sp->g_bytes = 0;
@@ -299,9 +304,11 @@ int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* w
   const gs_args f = fwd_view(*a);
   rc = check_workspace(&f, sp.total(), who);
   if (rc) return rc;
+  rc = check_scratch(a, sp.scratch(), who);
+  if (rc) return rc;
 
   const int H = (int)a->H;
-  char* base = static_cast<char*>(a->workspace) + sp.core;
+  char* base = static_cast<char*>(a->scratch) + sp.core_scratch;
   float* M = reinterpret_cast<float*>(base);
   float* dM = reinterpret_cast<float*>(base + sp.mat_bytes);
   const int64_t nmat = (int64_t)3 * H * H;
@@ -360,6 +367,13 @@ int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a) {
   const int rc = plan_struct(kind, a, &sp, "gs_bwd_workspace_bytes");
   if (rc) return rc;
   return sp.total();
+}
+
+int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a) {
+  StructPlan sp;
+  const int rc = plan_struct(kind, a, &sp, "gs_bwd_scratch_bytes");
+  if (rc) return rc;
+  return sp.scratch();
 }
 
 }  // namespace gs

@@ -42,6 +42,7 @@ EXPORTS = (
     "gs_input_proj_bwd_workspace_bytes",
     "gs_workspace_bytes",
     "gs_bwd_workspace_bytes",
+    "gs_bwd_scratch_bytes",
     "gs_workspace_status",
     "gs_last_error",
     "gs_abi_version",
@@ -104,6 +105,8 @@ class GsBwdArgs(ctypes.Structure):
         ("dbh_part", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_int64),
+        ("scratch", ctypes.c_void_p),
+        ("scratch_bytes", ctypes.c_int64),
         ("T", ctypes.c_int64),
         ("B", ctypes.c_int64),
         ("H", ctypes.c_int64),
@@ -198,6 +201,8 @@ def load() -> ctypes.CDLL:
         lib.gs_workspace_bytes.restype = ctypes.c_int64
         lib.gs_bwd_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsBwdArgs)]
         lib.gs_bwd_workspace_bytes.restype = ctypes.c_int64
+        lib.gs_bwd_scratch_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsBwdArgs)]
+        lib.gs_bwd_scratch_bytes.restype = ctypes.c_int64
         lib.gs_workspace_status.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
         lib.gs_workspace_status.restype = ctypes.c_int
         lib.gs_last_error.argtypes = []
@@ -353,11 +358,22 @@ def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w
     need = lib.gs_bwd_workspace_bytes(kind, ctypes.byref(a))
     if need < 0:
         raise_for(int(need), lib)
+    scratch_need = lib.gs_bwd_scratch_bytes(kind, ctypes.byref(a))
+    if scratch_need < 0:
+        raise_for(int(scratch_need), lib)
     with torch.cuda.device(gi.device):
         handle = torch.cuda.current_stream(gi.device).cuda_stream
         if need > 0:
             ws = workspace(gi.device, handle, int(need), steps=T)
             a.workspace = ws.data_ptr()
             a.workspace_bytes = ws.numel()
+        scratch = None
+        if scratch_need > 0:
+            # plain scratch from torch's stream-aware caching allocator
+            # (allocations are 512-byte aligned); kept alive until the launch is queued
+            scratch = torch.empty((int(scratch_need),), dtype=torch.uint8, device=gi.device)
+            a.scratch = scratch.data_ptr()
+            a.scratch_bytes = scratch.numel()
         rc = getattr(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
+        del scratch
     raise_for(rc, lib)

@@ -149,8 +149,13 @@ typedef struct gs_bwd_args {
                        * gradient of w; butterfly: gradient of the twiddles           */
   float* dw2_part;    /* two-factor Monarch: [3, nb, bs, bs] gradient of w2, else NULL */
   float* dbh_part;    /* [B, 3H] per-row partial gradient of bh                       */
-  void* workspace;
+  void* workspace;     /* tagged exchange words: as the forward's workspace (zeroed    *
+                        * once, may be shared with forward launches on one stream)   */
   int64_t workspace_bytes;
+  void* scratch;       /* plain scratch (no initial contents required), 256-byte    *
+                        * aligned; never shared with a workspace, whose tag words    *
+                        * must not see arbitrary float data                          */
+  int64_t scratch_bytes;
   int64_t T, B, H;
   int64_t sg_t, sg_b, sh0_b, so_t, so_b; /* strides of gi, h0, out (elements)      */
   int64_t nblocks, blksz, log_n, bfly_nblocks;
@@ -164,7 +169,8 @@ int gs_diagonal_bwd(const gs_bwd_args* args, hipStream_t stream);
  * its kernel, scan.py:296-643). `out` must hold its steps back to back
  * (so_t == B * so_b). Needs a workspace of gs_bwd_workspace_bytes(GS_KIND_DENSE,
  * args) bytes, 256-byte aligned, zeroed before its first use (like the
- * forward's, it may be shared with forward launches on the same stream). */
+ * forward's, it may be shared with forward launches on the same stream), and
+ * gs_bwd_scratch_bytes() bytes of scratch. */
 int gs_dense_bwd(const gs_bwd_args* args, hipStream_t stream);
 
 /* Monarch and butterfly backward (reference scan_monarch.py:409-884 and
@@ -175,9 +181,11 @@ int gs_dense_bwd(const gs_bwd_args* args, hipStream_t stream);
 int gs_monarch_bwd(const gs_bwd_args* args, hipStream_t stream);
 int gs_butterfly_bwd(const gs_bwd_args* args, hipStream_t stream);
 
-/* Scratch bytes a backward entry point needs (0 for the diagonal kind). Pure
- * host arithmetic. Negative on error. */
+/* Bytes of tagged workspace and of plain scratch a backward entry point needs
+ * (0 when it uses none: the diagonal kind needs neither, the butterfly kind's
+ * stage-wise path no workspace). Pure host arithmetic. Negative on error. */
 int64_t gs_bwd_workspace_bytes(int kind, const gs_bwd_args* args);
+int64_t gs_bwd_scratch_bytes(int kind, const gs_bwd_args* args);
 
 /* ---- input projection ----------------------------------------------------------
  * The producer of gi (reference GRULayer._forward_fast_dispatch,

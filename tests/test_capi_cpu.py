@@ -153,10 +153,11 @@ def test_dense_bwd_rejects_strided_out_and_missing_workspace():
 
 
 def test_bwd_workspace_sizes():
-    """Dense: control words, double-buffered tagged D rows (H words per padded
-    row) plus pad, one XCD word per workgroup, the coefficient block
-    [T B, 3H], six [T B, H] planes, per-chunk dbh sums and the K-split
-    partials of dWh; diagonal needs none."""
+    """Dense: the tagged workspace holds control words, double-buffered tagged
+    D rows (H words per padded row) plus pad and one XCD word per workgroup;
+    the plain scratch the coefficient block [T B, 3H], six [T B, H] planes,
+    per-chunk dbh sums and the K-split partials of dWh. Diagonal needs
+    neither, the stage-wise butterfly path no workspace."""
     lib = _lib.load()
     al = lambda x: (x + 255) // 256 * 256  # noqa: E731
     T, B, H = 64, 32, 512
@@ -166,13 +167,35 @@ def test_bwd_workspace_sizes():
     tiles = (3 * H // 64) * (H // 64)
     split = min(-(-512 // tiles), -(-(T * B) // 256))
     nchunks = -(-T // 8)
-    want = (256 + al(2 * B * H * 8 + 16 * kc * 8) + al((B // 4) * P * 8) + al(T * B * 3 * H * 4)
-            + 6 * al(T * B * H * 4) + al(nchunks * B * 3 * H * 4) + (al(split * 3 * H * H * 4) if split > 1 else 0))
-    assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == want
+    ws = 256 + al(2 * B * H * 8 + 16 * kc * 8) + al((B // 4) * P * 8)
+    scratch = (al(T * B * 3 * H * 4) + 6 * al(T * B * H * 4) + al(nchunks * B * 3 * H * 4)
+               + (al(split * 3 * H * H * 4) if split > 1 else 0))
+    assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == ws
+    assert lib.gs_bwd_scratch_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == scratch
     assert lib.gs_bwd_workspace_bytes(_lib.KIND_DIAGONAL, ctypes.byref(a)) == 0
+    assert lib.gs_bwd_scratch_bytes(_lib.KIND_DIAGONAL, ctypes.byref(a)) == 0
     assert lib.gs_bwd_workspace_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) == _lib.GS_ERR_INVALID
+    a.log_n, a.bfly_nblocks = 9, 1
+    assert lib.gs_bwd_workspace_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) == 0
+    assert lib.gs_bwd_scratch_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) > 0
+    a.log_n = 11  # stage-wise kernels cover N <= 1024: the materialized path needs the dense core
+    assert lib.gs_bwd_workspace_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) == ws
+    assert lib.gs_bwd_scratch_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) > scratch
     a = _bwd_args(T=2, B=3, H=2048)
     assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == _lib.GS_ERR_INVALID
+
+
+def test_dense_bwd_rejects_missing_scratch():
+    lib = _lib.load()
+    T, B, H = 4, 3, 8
+    a = _bwd_args(T=T, B=B, H=H, **{k: FAKE for k in BWD_PTRS})
+    need = lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a))
+    a.workspace, a.workspace_bytes = 0x10000, need  # validated before any device access
+    assert lib.gs_dense_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"scratch" in lib.gs_last_error()
+    a.scratch, a.scratch_bytes = 0x10010, 1 << 30  # misaligned
+    assert lib.gs_dense_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"aligned" in lib.gs_last_error()
 
 
 def test_workspace_sizes():
