@@ -146,13 +146,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   const int wy = wave >> 1, wx = wave & 1;
   const int i0 = blockIdx.x * BM, j0 = blockIdx.y * BN;
   const int kper = ((g.K + g.ksplit - 1) / g.ksplit + BK - 1) / BK * BK;
-  const int kbeg = blockIdx.z * kper;
+  const int z = blockIdx.z / g.ksplit, split = blockIdx.z - z * g.ksplit;
+  const int kbeg = split * kper;
   const int kend = min(g.K, kbeg + kper);
 
   TileLoader<A_KC, VEC_A, QA> la;
   TileLoader<B_KC, VEC_B, QB> lb;
-  la.init(g.a, g.lda, i0, g.M, kend);
-  lb.init(g.b, g.ldb, j0, g.N, kend);
+  la.init(g.a + (int64_t)(z % g.a_mod) * g.a_bs, g.lda, i0, g.M, kend);
+  lb.init(g.b + (int64_t)(z % g.b_mod) * g.b_bs, g.ldb, j0, g.N, kend);
   la.q = g.qa;
   lb.q = g.qb;
 
@@ -227,15 +228,16 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     buf ^= 1;
   }
 
-  float* c = g.c + (int64_t)blockIdx.z * g.split_stride;
-  const bool add_bias = g.bias != nullptr && blockIdx.z == 0;
+  float* c = g.c + (int64_t)z * g.c_bs + (int64_t)split * g.split_stride;
+  const float* biasp = g.bias ? g.bias + (int64_t)z * g.bias_bs : nullptr;
+  const bool add_bias = biasp != nullptr && split == 0;
 #pragma unroll
   for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
     for (int tj = 0; tj < 2; ++tj) {
       const int j = j0 + 32 * wx + 16 * tj + r16;
       if (j >= g.N) continue;
-      const float bias = add_bias ? g.bias[j] : 0.0f;
+      const float bias = add_bias ? biasp[j] : 0.0f;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int i = i0 + 32 * wy + 16 * ti + 4 * kq + v;
@@ -320,12 +322,16 @@ int gemm_f32(const GemmArgs& g, hipStream_t stream, const char* who) {
   if (g.M < 1 || g.N < 1 || g.K < 1 || g.ksplit < 1)
     return set_error(GS_ERR_INVALID, "%s: GEMM dims must be positive (M=%d, N=%d, K=%d, ksplit=%d)", who, g.M, g.N,
                      g.K, g.ksplit);
+  if (g.batch < 1 || g.a_mod < 1 || g.b_mod < 1 || (int64_t)g.batch * g.ksplit > 65535)
+    return set_error(GS_ERR_INVALID, "%s: bad GEMM batch (batch=%d, a_mod=%d, b_mod=%d, ksplit=%d)", who, g.batch,
+                     g.a_mod, g.b_mod, g.ksplit);
   if (g.layout != kGemmNT && g.layout != kGemmTN && g.layout != kGemmNN)
     return set_error(GS_ERR_INVALID, "%s: unknown GEMM layout %d", who, g.layout);
   // float4 loads need 16-byte aligned bases, leading dimensions that keep
   // rows aligned, and contiguous extents that are multiples of 4.
   const bool a_kc = g.layout != kGemmTN, b_kc = g.layout == kGemmNT;
-  const bool vec = aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 &&
+  const bool vec = aligned16(g.a) && aligned16(g.b) && g.lda % 4 == 0 && g.ldb % 4 == 0 && g.a_bs % 4 == 0 &&
+                   g.b_bs % 4 == 0 &&
                    (a_kc ? g.K % 4 == 0 : g.M % 4 == 0) && (b_kc ? g.K % 4 == 0 : g.N % 4 == 0);
 #define GS_GEMM_ROW(L, V) \
   {{gemm_kernel<L, V, false, false>, gemm_kernel<L, V, false, true>}, \
@@ -337,7 +343,8 @@ int gemm_f32(const GemmArgs& g, hipStream_t stream, const char* who) {
   };
 #undef GS_GEMM_ROW
   GemmFn fn = table[g.layout][vec ? 1 : 0][g.qa.on ? 1 : 0][g.qb.on ? 1 : 0];
-  const dim3 grid((unsigned)((g.M + BM - 1) / BM), (unsigned)((g.N + BN - 1) / BN), (unsigned)g.ksplit);
+  const dim3 grid((unsigned)((g.M + BM - 1) / BM), (unsigned)((g.N + BN - 1) / BN),
+                  (unsigned)(g.batch * g.ksplit));
   hipLaunchKernelGGL(fn, grid, dim3(kGemmThreads), 0, stream, g);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;

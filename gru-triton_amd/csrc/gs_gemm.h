@@ -27,6 +27,11 @@ struct GemmArgs {
   int layout = kGemmNT;                 // GemmLayout
   Quant qa{1.0f, 0.0f, 0.0f, 0};         // applied to A on load when qa.on
   Quant qb{1.0f, 0.0f, 0.0f, 0};         // applied to B on load when qb.on
+  // Batched products: product z < batch uses a + (z % a_mod) a_bs,
+  // b + (z % b_mod) b_bs, c + z c_bs and bias + z bias_bs (splits of
+  // product z still step by split_stride from there).
+  int batch = 1, a_mod = 1, b_mod = 1;
+  int64_t a_bs = 0, b_bs = 0, c_bs = 0, bias_bs = 0;
 };
 
 // Launches the product on `stream`. Every element of C (of every split) is written.
