@@ -6,7 +6,10 @@
 A step is one forward scan (the drop-in ``gru_scan_*`` call) over one batch
 of synthetic input already resident in HBM. A second table, "train_step_ms",
 times full training steps (input GEMM, scan, loss, backward) per hidden kind
-at the shape of the reference's published train-step table. The headline line is the dense
+at the shape of the reference's published train-step table; a third,
+"calibration_forward_ms", times one calibration forward per configuration
+(the scan with both hidden quantizers as min_max observers, gru_scan_observe).
+The headline line is the dense
 fp32 scan at T=64, B=32, H=512 (config 1, the configuration the metric is
 quoted on); the other four configurations are measured in the same run and
 reported under "kinds".
@@ -198,6 +201,40 @@ def train_steps(dev, iters: int, warmup: int) -> dict:
     return res
 
 
+def calibration_forwards(dev, kinds, iters: int, warmup: int) -> dict:
+    """One calibration forward per config: gru_scan_observe with quant_h_in and
+    quant_h_out as int8 symmetric min_max observers (the hidden-side work of a
+    GRULayer.calibrate batch, gru_layer.py:308-336, on the per-step path
+    gru_layer.py:205-223); median of HIP-event-timed calls on one stream."""
+    import torch
+
+    import gru_qat_amd as G
+    from gru_qat_amd.configs import make_config
+
+    res = {}
+    for idx in kinds:
+        d = make_config(idx, device=dev)
+        qs = [G.FakeQuantizePerTensor(G.QuantizerConfig(mode="min_max")).to(dev) for _ in range(2)]
+
+        def call():
+            G.gru_scan_observe(d["kind"], d["gi"], d["h0"], d["w"], d["bh"], quant_h_in=qs[0], quant_h_out=qs[1],
+                               hidden2=d.get("w2"))
+
+        with torch.no_grad():
+            for _ in range(warmup):
+                call()
+            samples = []
+            for _ in range(iters):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                call()
+                e1.record()
+                e1.synchronize()
+                samples.append(e0.elapsed_time(e1))
+        res[d["name"]] = {"ms": round(statistics.median(samples), 4), "T": d["T"], "B": d["B"], "H": d["H"]}
+    return res
+
+
 def cpu_baseline(idx: int, budget_s: float) -> dict:
     import torch
 
@@ -242,6 +279,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=4.0, help="seconds of CPU baseline per kind")
     ap.add_argument("--copy-mib", type=int, default=0, help="run a plain N MiB copy K times and exit")
     ap.add_argument("--no-train", action="store_true", help="skip the train-step table")
+    ap.add_argument("--no-calib", action="store_true", help="skip the calibration-forward table")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -281,6 +319,11 @@ def main() -> int:
         print("[bench] train steps ...", file=sys.stderr, flush=True)
         train = train_steps(dev, iters=30, warmup=10)
         print(f"[bench] train steps: {json.dumps(train)}", file=sys.stderr, flush=True)
+    calib = None
+    if not args.no_calib:
+        print("[bench] calibration forwards ...", file=sys.stderr, flush=True)
+        calib = calibration_forwards(dev, kinds, iters=10, warmup=2)
+        print(f"[bench] calibration forwards: {json.dumps(calib)}", file=sys.stderr, flush=True)
     faults = gru_qat_amd.workspace_faults(dev)
 
     cpu = {}
@@ -314,6 +357,7 @@ def main() -> int:
         "cpu_baseline": cpu.get(head),
         "kinds": {str(k): v for k, v in results.items()},
         "train_step_ms": train,
+        "calibration_forward_ms": calib,
         "device": {"name": props.name, "cus": props.multi_processor_count, "host_cpu": cpu_model(),
                    "host_cores": os.cpu_count()},
         "exchange_faults": faults,

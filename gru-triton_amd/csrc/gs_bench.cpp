@@ -13,7 +13,9 @@
 // prints one JSON line with the mean and median launch duration.
 //
 // Items b0..b4 time the backward entry point of a configuration instead
-// (gs_*_bwd on the forward's own output and a random upstream gradient), and
+// (gs_*_bwd on the forward's own output and a random upstream gradient),
+// items c0..c4 the calibration forward (gs_observe_scan with both hidden
+// quantizers as int8 symmetric min_max observers), and
 // "proj" times the input projection at the benchmark shape (x [2048, 512],
 // Wi_cat [1536, 512], int8 x and per-row weight fake-quant) forward and
 // backward.
@@ -153,7 +155,10 @@ int run_copy(int mib, int launches) {
   return 0;
 }
 
-int run_config(int idx, int launches, int warmup, bool backward) {
+enum Mode { kForward, kBackward, kCalibrate };
+
+int run_config(int idx, int launches, int warmup, Mode mode) {
+  const bool backward = mode == kBackward;
   const long long T = idx == 4 ? 512 : 64, B = idx == 4 ? 64 : 32, H = idx == 4 ? 1024 : 512;
   Rng g(idx + 1);
   const float k = 1.0f / std::sqrt((float)H);
@@ -263,6 +268,44 @@ int run_config(int idx, int launches, int warmup, bool backward) {
       b.scratch_bytes = ns;
     }
   }
+  gs_observe_args o;
+  memset(&o, 0, sizeof o);
+  float* stats = nullptr;
+  if (mode == kCalibrate) {
+    o.kind = kind;
+    o.gi = a.gi;
+    o.h0 = a.h0;
+    o.w = a.w;
+    o.w2 = a.w2;
+    o.bh = a.bh;
+    o.out = a.out;
+    o.T = T;
+    o.B = B;
+    o.H = H;
+    o.sg_t = a.sg_t;
+    o.sg_b = a.sg_b;
+    o.sh0_b = a.sh0_b;
+    o.so_t = a.so_t;
+    o.so_b = a.so_b;
+    o.nblocks = a.nblocks;
+    o.blksz = a.blksz;
+    o.log_n = a.log_n;
+    o.bfly_nblocks = a.bfly_nblocks;
+    CHECK(hipMalloc(&stats, 6 * sizeof(float)));
+    CHECK(hipMemset(stats, 0, 6 * sizeof(float)));  // not yet initialized
+    const gs_observer q = {GS_OBS_MIN_MAX, 1, -127, 127, 1.0f, 0.0f, nullptr};
+    o.q_in = q;
+    o.q_in.stats = stats;
+    o.q_out = q;
+    o.q_out.stats = stats + 3;
+    const int64_t ns = gs_observe_scan_scratch_bytes(&o);
+    if (ns < 0) {
+      fprintf(stderr, "gs_bench: gs_observe_scan_scratch_bytes: %s\n", gs_last_error());
+      return 1;
+    }
+    CHECK(hipMalloc(&o.scratch, ns));
+    o.scratch_bytes = ns;
+  }
   void* ws = nullptr;
   CHECK(hipMalloc(&ws, need));
   CHECK(hipMemset(ws, 0, need));
@@ -286,6 +329,14 @@ int run_config(int idx, int launches, int warmup, bool backward) {
     }
   };
   auto launch = [&] {
+    if (mode == kCalibrate) {
+      rc = gs_observe_scan(&o, st);
+      if (rc != GS_OK) {
+        fprintf(stderr, "gs_bench: gs_observe_scan failed (%d): %s\n", rc, gs_last_error());
+        exit(1);
+      }
+      return;
+    }
     if (!backward) return forward();
     switch (kind) {
       case GS_KIND_DIAGONAL: rc = gs_diagonal_bwd(&b, st); break;
@@ -305,15 +356,17 @@ int run_config(int idx, int launches, int warmup, bool backward) {
     fprintf(stderr, "gs_bench: a poll timed out (workspace fault word set)\n");
     return 1;
   }
-  if (backward) {
+  if (mode != kForward) {
     char name[64];
-    snprintf(name, sizeof name, "%s_backward", kNames[idx]);
+    snprintf(name, sizeof name, "%s_%s", kNames[idx], backward ? "backward" : "calibration");
     report(name, idx, ms, T, B, H);
   } else {
     report(kNames[idx], idx, ms, T, B, H);
   }
   CHECK(hipFree(ws));
   if (b.scratch) CHECK(hipFree(b.scratch));
+  if (o.scratch) CHECK(hipFree(o.scratch));
+  if (stats) CHECK(hipFree(stats));
   for (float* p : owned) CHECK(hipFree(p));
   CHECK(hipStreamDestroy(st));
   return 0;
@@ -408,7 +461,8 @@ int run_proj(int launches, int warmup) {
 
 int main(int argc, char** argv) {
   if (argc < 2) {
-    fprintf(stderr, "usage: gs_bench <items: configs 0..4, b0..b4 (backward), proj, copy; comma-separated> "
+    fprintf(stderr, "usage: gs_bench <items: configs 0..4, b0..b4 (backward), c0..c4 (calibration), proj, copy; "
+                    "comma-separated> "
                     "[launches] [warmup]\n");
     return 2;
   }
@@ -425,15 +479,15 @@ int main(int argc, char** argv) {
     } else if (!strcmp(tok, "proj")) {
       rc = run_proj(launches, warmup);
     } else {
-      const bool backward = tok[0] == 'b';
-      const char* num = backward ? tok + 1 : tok;
+      const Mode mode = tok[0] == 'b' ? kBackward : tok[0] == 'c' ? kCalibrate : kForward;
+      const char* num = mode == kForward ? tok : tok + 1;
       char* end = nullptr;
       const long idx = strtol(num, &end, 10);
       if (*num == 0 || *end != 0 || idx < 0 || idx > 4) {
         fprintf(stderr, "gs_bench: unknown item '%s'\n", tok);
         return 2;
       }
-      rc = run_config((int)idx, launches, warmup, backward);
+      rc = run_config((int)idx, launches, warmup, mode);
     }
     if (rc) return rc;
   }

@@ -159,17 +159,18 @@ __global__ void bfly_identity(float* acts, int64_t gate_stride, int N, int H) {
   }
 }
 
-// A_{j+1}[i][k] = tw_ii A_j[i][k] + tw_ip A_j[i ^ stride][k]; the last stage
-// also writes rows i < H into M (rows g H + i).
-__global__ void bfly_stage_fwd(const float* tw, int64_t tw_gate, float* acts, int64_t gate_stride, int j, int L,
-                               int N, int H, float* m_out) {
+// dst = A_{j+1} from src = A_j (each [N][H] per gate, gates gate_stride
+// apart): A_{j+1}[i][k] = tw_ii A_j[i][k] + tw_ip A_j[i ^ stride][k]; the
+// last stage also writes rows i < H into M (rows g H + i).
+__global__ void bfly_stage_fwd(const float* tw, int64_t tw_gate, const float* src, float* dst, int64_t gate_stride,
+                               int j, int L, int N, int H, float* m_out) {
   const int64_t n = (int64_t)3 * N * H;
   const Stage st = stage_of(j, L, N);
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
     const int g = (int)(e / ((int64_t)N * H));
     const int64_t r = e - (int64_t)g * N * H;
     const int i = (int)(r / H), k = (int)(r - (int64_t)i * H);
-    const float* a = acts + g * gate_stride + (int64_t)j * N * H;
+    const float* a = src + g * gate_stride;
     const float* t = tw + g * tw_gate + tw_index(st, i);
     const int m = (i >> st.ls) & 1;
     float y;
@@ -177,8 +178,18 @@ __global__ void bfly_stage_fwd(const float* tw, int64_t tw_gate, float* acts, in
 #pragma clang fp contract(off)
       y = t[m] * a[(int64_t)i * H + k] + t[1 - m] * a[(int64_t)(i ^ st.stride) * H + k];
     }
-    acts[g * gate_stride + (int64_t)(j + 1) * N * H + r] = y;
+    dst[g * gate_stride + r] = y;
     if (m_out != nullptr && i < H) m_out[((int64_t)g * H + i) * H + k] = y;
+  }
+}
+
+// Diagonal: M[g H + x][k] = (x == k) ? w[g][k] : 0.
+__global__ void diagonal_materialize(const float* w, float* m, int H) {
+  const int64_t n = (int64_t)3 * H * H;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int row = (int)(e / H), k = (int)(e - (int64_t)row * H);
+    const int g = row / H, x = row - g * H;
+    m[e] = x == k ? w[(int64_t)g * H + k] : 0.0f;
   }
 }
 
@@ -343,8 +354,9 @@ int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* w
   hipLaunchKernelGGL(bfly_identity, grid_for(nstage), dim3(256), 0, stream, acts, act_gate, N, H);
   GS_CHECK_HIP(hipGetLastError());
   for (int j = 0; j < K; ++j) {
-    hipLaunchKernelGGL(bfly_stage_fwd, grid_for(nstage), dim3(256), 0, stream, a->w, tw_gate, acts, act_gate, j, L, N,
-                       H, j == K - 1 ? M : nullptr);
+    hipLaunchKernelGGL(bfly_stage_fwd, grid_for(nstage), dim3(256), 0, stream, a->w, tw_gate,
+                       acts + (int64_t)j * N * H, acts + (int64_t)(j + 1) * N * H, act_gate, j, L, N, H,
+                       j == K - 1 ? M : nullptr);
     GS_CHECK_HIP(hipGetLastError());
   }
   rc = dense_bwd_core(a, M, dM, stream, who);
@@ -359,6 +371,80 @@ int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* w
     GS_CHECK_HIP(hipGetLastError());
     std::swap(g0, g1);
   }
+  return GS_OK;
+}
+
+int validate_map(const gs_map_args* a, const char* who) {
+  if (a == nullptr) return set_error(GS_ERR_INVALID, "%s: args is NULL", who);
+  const int64_t H = a->H;
+  if (H < 1 || H > 4096) return set_error(GS_ERR_INVALID, "%s: H must be in [1, 4096]; got %lld", who, (long long)H);
+  switch (a->kind) {
+    case GS_KIND_DENSE:
+    case GS_KIND_DIAGONAL:
+      if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for this kind", who);
+      return GS_OK;
+    case GS_KIND_MONARCH:
+      if (a->nblocks < 1 || a->blksz < 1 || a->nblocks * a->blksz != H)
+        return set_error(GS_ERR_INVALID, "%s: Wh_struct block dims must tile H: nblocks=%lld, blksz=%lld, H=%lld", who,
+                         (long long)a->nblocks, (long long)a->blksz, (long long)H);
+      return GS_OK;
+    case GS_KIND_BUTTERFLY:
+      if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the butterfly kind", who);
+      if (a->log_n < 1 || a->log_n > 12 || a->bfly_nblocks < 1 || a->bfly_nblocks > 64)
+        return set_error(GS_ERR_INVALID, "%s: butterfly needs 1 <= log_n <= 12 and 1 <= nblocks <= 64; got %lld, %lld",
+                         who, (long long)a->log_n, (long long)a->bfly_nblocks);
+      if ((int64_t(1) << a->log_n) < H)
+        return set_error(GS_ERR_INVALID, "%s: H_PAD = 2^log_n = %lld must be >= H = %lld", who,
+                         (long long)(int64_t(1) << a->log_n), (long long)H);
+      return GS_OK;
+    default:
+      return set_error(GS_ERR_INVALID, "%s: unknown kind %d", who, a->kind);
+  }
+}
+
+int64_t hidden_map_scratch(const gs_map_args* a) {
+  if (a->kind != GS_KIND_BUTTERFLY) return 0;
+  return 2 * align256((int64_t)3 * (int64_t(1) << a->log_n) * a->H * 4);
+}
+
+// Writes the hidden map of `a` as the dense [3H, H] matrix a->m
+// (gh = hq m^T + bh).
+int materialize_map(const gs_map_args* a, hipStream_t stream, const char* who) {
+  const int H = (int)a->H;
+  const int64_t nmat = (int64_t)3 * H * H;
+  switch (a->kind) {
+    case GS_KIND_DENSE:
+      GS_CHECK_HIP(hipMemcpyAsync(a->m, a->w, nmat * 4, hipMemcpyDeviceToDevice, stream));
+      return GS_OK;
+    case GS_KIND_DIAGONAL:
+      hipLaunchKernelGGL(diagonal_materialize, grid_for(nmat), dim3(256), 0, stream, a->w, a->m, H);
+      break;
+    case GS_KIND_MONARCH:
+      if (a->w2 == nullptr)
+        hipLaunchKernelGGL(monarch1_materialize, grid_for(nmat), dim3(256), 0, stream, a->w, a->m, H, (int)a->nblocks,
+                           (int)a->blksz);
+      else
+        hipLaunchKernelGGL(monarch2_materialize, grid_for(nmat), dim3(256), 0, stream, a->w, a->w2, a->m, H,
+                           (int)a->nblocks, (int)a->blksz);
+      break;
+    default: {  // butterfly: A_0 = [I; 0], then the K stages ping-ponging through the scratch
+      const int L = (int)a->log_n, N = 1 << L, K = (int)a->bfly_nblocks * L;
+      const int64_t half = hidden_map_scratch(a) / 2;
+      float* buf[2] = {static_cast<float*>(a->scratch),
+                       reinterpret_cast<float*>(static_cast<char*>(a->scratch) + half)};
+      const int64_t gate = (int64_t)N * H, nstage = 3 * gate;
+      const int64_t tw_gate = (int64_t)a->bfly_nblocks * L * (N / 2) * 4;
+      hipLaunchKernelGGL(bfly_identity, grid_for(nstage), dim3(256), 0, stream, buf[0], gate, N, H);
+      GS_CHECK_HIP(hipGetLastError());
+      for (int j = 0; j < K; ++j) {
+        hipLaunchKernelGGL(bfly_stage_fwd, grid_for(nstage), dim3(256), 0, stream, a->w, tw_gate, buf[j & 1],
+                           buf[(j + 1) & 1], gate, j, L, N, H, j == K - 1 ? a->m : nullptr);
+        GS_CHECK_HIP(hipGetLastError());
+      }
+      return GS_OK;
+    }
+  }
+  GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }
 
@@ -380,5 +466,26 @@ int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a) {
 
 extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   return gs::run_struct(GS_KIND_MONARCH, a, stream, "gs_monarch_bwd");
+}
+
+extern "C" int64_t gs_hidden_map_scratch_bytes(const gs_map_args* a) {
+  using namespace gs;
+  const int rc = validate_map(a, "gs_hidden_map_scratch_bytes");
+  if (rc) return rc;
+  return hidden_map_scratch(a);
+}
+
+extern "C" int gs_hidden_map_dense(const gs_map_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_hidden_map_dense";
+  int rc = validate_map(a, who);
+  if (rc) return rc;
+  if (!a->w || !a->m) return set_error(GS_ERR_INVALID, "%s: w and m must be non-NULL device pointers", who);
+  const int64_t need = hidden_map_scratch(a);
+  if (need > 0 && (a->scratch == nullptr || a->scratch_bytes < need))
+    return set_error(GS_ERR_INVALID, "%s: scratch of %lld bytes required; got %lld", who, (long long)need,
+                     (long long)a->scratch_bytes);
+  return materialize_map(a, stream, who);
 }
 

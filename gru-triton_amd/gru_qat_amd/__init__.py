@@ -23,16 +23,24 @@ from .scan_butterfly import (
 from .scan_diagonal import extract_diagonal_factors, gru_scan_diagonal, gru_scan_diagonal_forward
 from .scan_monarch import extract_monarch_factors, gru_scan_monarch, gru_scan_monarch_forward
 from ._lib import load as load_library, workspace_faults
-from .gru_layer import fast_dispatch_eligible, forward_fast_dispatch, layer_forward, resolve_use_triton
+from .gru_layer import ScanLayer, fast_dispatch_eligible, forward_fast_dispatch, layer_forward, resolve_use_triton
 from .input_proj import input_projection, quantize_input_weights
+from .quantizers import FakeQuantizePerTensor, QuantizerConfig
+from .observe import gru_scan_observe, hidden_map_dense
+from .calibration import calibrate, freeze_all
 
 __all__ = [
+    "FakeQuantizePerTensor",
     "GRUScanFunction",
     "GRUScanPersistentFunction",
+    "QuantizerConfig",
+    "ScanLayer",
+    "calibrate",
     "extract_butterfly_twiddles",
     "extract_diagonal_factors",
     "extract_monarch_factors",
     "fast_dispatch_eligible",
+    "freeze_all",
     "forward_fast_dispatch",
     "gru_scan",
     "gru_scan_butterfly_forward",
@@ -44,7 +52,9 @@ __all__ = [
     "gru_scan_forward_persistent",
     "gru_scan_monarch",
     "gru_scan_monarch_forward",
+    "gru_scan_observe",
     "gru_scan_persistent",
+    "hidden_map_dense",
     "input_projection",
     "layer_forward",
     "load_library",

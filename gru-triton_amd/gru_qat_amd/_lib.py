@@ -40,6 +40,12 @@ EXPORTS = (
     "gs_input_proj",
     "gs_input_proj_bwd",
     "gs_input_proj_bwd_workspace_bytes",
+    "gs_hidden_map_dense",
+    "gs_hidden_map_scratch_bytes",
+    "gs_observe_tensor",
+    "gs_observe_tensor_scratch_bytes",
+    "gs_observe_scan",
+    "gs_observe_scan_scratch_bytes",
     "gs_workspace_bytes",
     "gs_bwd_workspace_bytes",
     "gs_bwd_scratch_bytes",
@@ -164,6 +170,83 @@ class GsProjBwdArgs(ctypes.Structure):
     ]
 
 
+class GsMapArgs(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("w", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("m", ctypes.c_void_p),
+        ("scratch", ctypes.c_void_p),
+        ("scratch_bytes", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("nblocks", ctypes.c_int64),
+        ("blksz", ctypes.c_int64),
+        ("log_n", ctypes.c_int64),
+        ("bfly_nblocks", ctypes.c_int64),
+    ]
+
+
+OBS_OFF = 0
+OBS_FROZEN = 1
+OBS_DYNAMIC = 2
+OBS_MIN_MAX = 3
+
+
+class GsObserver(ctypes.Structure):
+    _fields_ = [
+        ("mode", ctypes.c_int32),
+        ("symmetric", ctypes.c_int32),
+        ("qmin", ctypes.c_int32),
+        ("qmax", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("zero_point", ctypes.c_float),
+        ("stats", ctypes.c_void_p),
+    ]
+
+
+class GsObserveTensorArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("used", ctypes.c_void_p),
+        ("scratch", ctypes.c_void_p),
+        ("scratch_bytes", ctypes.c_int64),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("ld", ctypes.c_int64),
+        ("q", GsObserver),
+    ]
+
+
+class GsObserveArgs(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("gi", ctypes.c_void_p),
+        ("h0", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("w2", ctypes.c_void_p),
+        ("bh", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("trace", ctypes.c_void_p),
+        ("scratch", ctypes.c_void_p),
+        ("scratch_bytes", ctypes.c_int64),
+        ("T", ctypes.c_int64),
+        ("B", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("sg_t", ctypes.c_int64),
+        ("sg_b", ctypes.c_int64),
+        ("sh0_b", ctypes.c_int64),
+        ("so_t", ctypes.c_int64),
+        ("so_b", ctypes.c_int64),
+        ("nblocks", ctypes.c_int64),
+        ("blksz", ctypes.c_int64),
+        ("log_n", ctypes.c_int64),
+        ("bfly_nblocks", ctypes.c_int64),
+        ("q_in", GsObserver),
+        ("q_out", GsObserver),
+    ]
+
+
 _lib = None
 _lib_lock = threading.Lock()
 
@@ -197,6 +280,14 @@ def load() -> ctypes.CDLL:
         lib.gs_input_proj_bwd.restype = ctypes.c_int
         lib.gs_input_proj_bwd_workspace_bytes.argtypes = [ctypes.POINTER(GsProjBwdArgs)]
         lib.gs_input_proj_bwd_workspace_bytes.restype = ctypes.c_int64
+        for name, argt in (("gs_hidden_map", GsMapArgs), ("gs_observe_tensor", GsObserveTensorArgs),
+                           ("gs_observe_scan", GsObserveArgs)):
+            run = getattr(lib, name if name != "gs_hidden_map" else "gs_hidden_map_dense")
+            run.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
+            run.restype = ctypes.c_int
+            size = getattr(lib, name + "_scratch_bytes")
+            size.argtypes = [ctypes.POINTER(argt)]
+            size.restype = ctypes.c_int64
         lib.gs_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsArgs)]
         lib.gs_workspace_bytes.restype = ctypes.c_int64
         lib.gs_bwd_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsBwdArgs)]

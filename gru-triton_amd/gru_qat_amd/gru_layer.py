@@ -17,9 +17,14 @@ This module keeps the parts of that path that decide and feed the scan:
   input side, through ``_forward_fast_dispatch`` (:234-302): x to time-major,
   the input projection (``input_projection``, :249-255), the scan.
 
-The cell and quantizer modules and calibration are not part of this build;
-callers pass the extracted weights (``extract_*`` helpers of the scan
-modules) and the frozen quant tuples.
+* ``ScanLayer`` -- GRULayer's forward, calibrate and freeze (gru_layer.py:52-65,
+  :153-302, :308-342) around these scans, with weights given as tensors and
+  per-tensor quantizers (``quantizers.FakeQuantizePerTensor``); its
+  calibration forwards run on the observer kernels (``observe``).
+
+The cell module is not part of this build; ``layer_forward`` callers pass the
+extracted weights (``extract_*`` helpers of the scan modules) and the frozen
+quant tuples.
 """
 
 from __future__ import annotations
@@ -195,3 +200,135 @@ def layer_forward(
     return forward_fast_dispatch(kind, gi, h0, hidden, bh_cat, h_in_quant=h_in_quant, h_out_quant=h_out_quant,
                                  batch_first=batch_first, hidden2=hidden2)
 
+
+
+class ScanLayer(torch.nn.Module):
+    """GRULayer's forward, calibrate and freeze around this build's scans, with
+    the weights given as tensors instead of a cell (the cell and its recipe
+    are not part of this build).
+
+    Follows gru_layer.py: the ``use_triton`` and ``batch_first`` arguments
+    (:52-65, resolved as :110-124, except that the dense kind is eligible
+    here), ``forward`` (:153-302), ``calibrate`` (:308-336) and ``freeze``
+    (:338-339).
+
+    * ``kind``: "dense", "diagonal", "monarch" or "butterfly"; ``Wi_cat``
+      [3H, I], ``bi_cat`` [3H] or None, ``hidden`` (and ``hidden2``) and
+      ``bh_cat`` as in ``forward_fast_dispatch``. They become parameters.
+    * ``x_quant`` and ``h_quant``: ``QuantizerConfig`` of the per-tensor
+      ``quant_x`` and of ``quant_h_in`` and ``quant_h_out`` (both built from
+      one config, as the reference builds both from recipe.hidden,
+      gru_cell.py:191-193), or None for no quantizer. ``w_bits``: the per-row
+      symmetric input-weight fake-quant (quantize_input_weights), or None.
+
+    With ``use_triton`` on, ``forward`` is the fast dispatch: quant_x is
+    applied to the whole sequence, and the hidden quantizers reach the scan
+    kernel only when frozen, per-tensor and symmetric (gru_layer.py:30-48);
+    otherwise the scan runs without them, as in the reference. With it off,
+    ``forward`` is the per-step path with every quantizer firing (the input
+    projected once over the sequence, as with the reference's pre_batch_input)
+    on the observer kernels (``gru_scan_observe``); that path has no autograd.
+    """
+
+    def __init__(self, kind: str, Wi_cat: torch.Tensor, bi_cat: Optional[torch.Tensor], hidden: torch.Tensor,
+                 bh_cat: torch.Tensor, *, hidden2: Optional[torch.Tensor] = None, x_quant: Any = None,
+                 h_quant: Any = None, w_bits: Optional[int] = None, use_triton: Any = "auto",
+                 batch_first: bool = False) -> None:
+        super().__init__()
+        from .quantizers import FakeQuantizePerTensor, QuantizerConfig
+
+        if kind not in ("dense",) + FAST_DISPATCH_KINDS:
+            raise ValueError(f"kind must be one of dense, diagonal, monarch, butterfly; got {kind!r}")
+        self.kind = kind
+        self.Wi_cat = torch.nn.Parameter(Wi_cat.detach().clone())
+        self.bi_cat = torch.nn.Parameter(bi_cat.detach().clone()) if bi_cat is not None else None
+        self.hidden = torch.nn.Parameter(hidden.detach().clone())
+        self.hidden2 = torch.nn.Parameter(hidden2.detach().clone()) if hidden2 is not None else None
+        self.bh_cat = torch.nn.Parameter(bh_cat.detach().clone())
+        self.hidden_size = bh_cat.shape[0] // 3
+
+        def make(cfg: Any) -> Optional[FakeQuantizePerTensor]:
+            if cfg is None:
+                return None
+            from copy import deepcopy
+
+            return FakeQuantizePerTensor(deepcopy(cfg) if isinstance(cfg, QuantizerConfig) else QuantizerConfig(**cfg))
+
+        self.quant_x = make(x_quant)
+        self.quant_h_in = make(h_quant)
+        self.quant_h_out = make(h_quant)
+        if w_bits is not None and not (2 <= int(w_bits) <= 16):
+            raise ValueError(f"w_bits must be in [2, 16] or None; got {w_bits}")
+        self.w_quant = None if w_bits is None else (-(2 ** (int(w_bits) - 1)) + 1, 2 ** (int(w_bits) - 1) - 1)
+        if use_triton == "auto":
+            self.use_triton = True
+        else:
+            self.use_triton = bool(use_triton)
+        self.batch_first = batch_first
+
+    def _x_side(self, x: torch.Tensor) -> Tuple[torch.Tensor, QuantTuple]:
+        """quant_x on the fast dispatch: a frozen symmetric per-tensor quantizer
+        goes to the input projection as a tuple (differentiable, fused into
+        the GEMM's operand load); any other runs on the observer kernel."""
+        q = self.quant_x
+        if q is None:
+            return x, None
+        frozen = _extract_h_quant_params(q)
+        if frozen is not None:
+            return x, frozen
+        return q(x), None
+
+    def forward(self, x: torch.Tensor, h0: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+        if not self.use_triton:
+            return self._forward_observe(x, h0)
+        xin, x_tuple = self._x_side(x)
+        h_in = _extract_h_quant_params(self.quant_h_in) if self.quant_h_in is not None else None
+        h_out = _extract_h_quant_params(self.quant_h_out) if self.quant_h_out is not None else None
+        return layer_forward(self.kind, xin, h0, self.Wi_cat, self.bi_cat, self.hidden, self.bh_cat,
+                             x_quant=x_tuple, w_quant=self.w_quant, h_in_quant=h_in, h_out_quant=h_out,
+                             batch_first=self.batch_first, hidden2=self.hidden2)
+
+    def _forward_observe(self, x: torch.Tensor, h0: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+        from .input_proj import input_projection
+        from .observe import gru_scan_observe
+
+        if x.dim() != 3:
+            raise ValueError(f"x must be [T, B, I] (or [B, T, I] with batch_first); got shape {tuple(x.shape)}")
+        if self.batch_first:
+            x = x.transpose(0, 1)
+        T, B, _ = x.shape
+        if T == 0:
+            raise ValueError(f"seq length T must be > 0; got T={T}")
+        if B == 0:
+            raise ValueError(f"batch size B must be > 0; got B={B}")
+        with torch.no_grad():
+            if h0 is None:
+                h0 = x.new_zeros(B, self.hidden_size)
+            xin = self.quant_x(x) if self.quant_x is not None else x
+            gi = input_projection(xin, self.Wi_cat, self.bi_cat, x_quant=None, w_quant=self.w_quant)
+            out = gru_scan_observe(self.kind, gi, h0, self.hidden, self.bh_cat, quant_h_in=self.quant_h_in,
+                                   quant_h_out=self.quant_h_out, hidden2=self.hidden2)
+        h_T = out[-1]
+        if self.batch_first:
+            out = out.transpose(0, 1)
+        return out, h_T
+
+    @torch.no_grad()
+    def calibrate(self, loader: Any, n_batches: int = 64, *, only_activations: bool = True) -> dict:
+        """gru_layer.py:308-336: runs ``calibration.calibrate`` with use_triton
+        off, so that the hidden quantizers fire every step; does not freeze."""
+        from .calibration import calibrate as _calibrate
+
+        saved = self.use_triton
+        self.use_triton = False
+        try:
+            return _calibrate(self, loader, n_batches=n_batches, only_activations=only_activations)
+        finally:
+            self.use_triton = saved
+
+    def freeze(self) -> None:
+        """gru_layer.py:338-339 (cell.freeze_quantizers, gru_cell.py:538-549):
+        every quantizer of the layer goes to frozen mode."""
+        from .calibration import freeze_all
+
+        freeze_all(self)

@@ -241,6 +241,100 @@ typedef struct gs_proj_bwd_args {
 int64_t gs_input_proj_bwd_workspace_bytes(const gs_proj_bwd_args* args);
 int gs_input_proj_bwd(const gs_proj_bwd_args* args, hipStream_t stream);
 
+/* ---- dense form of a hidden map --------------------------------------------------
+ * Writes the hidden map of any kind as the dense matrix m [3H, H] (rows r, z,
+ * n) with gh = hq m^T + bh: the diagonal kind's diag(w_g) blocks, the Monarch
+ * block-diagonal factor(s) composed, the butterfly's stages applied to the
+ * identity and cut to H x H. The reference materializes these maps only in
+ * its tests (e.g. tests/test_triton_monarch.py:81-101 against torch.block_diag);
+ * here the materialized map feeds gs_observe_scan and the backward's
+ * structured paths. */
+typedef struct gs_map_args {
+  int32_t kind;      /* GS_KIND_*                                                  */
+  const float* w;    /* as gs_args.w                                               */
+  const float* w2;   /* as gs_args.w2 (Monarch two-factor), else NULL              */
+  float* m;          /* [3H, H] contiguous output                                  */
+  void* scratch;     /* gs_hidden_map_scratch_bytes() bytes (butterfly), 256-byte aligned */
+  int64_t scratch_bytes;
+  int64_t H, nblocks, blksz, log_n, bfly_nblocks;
+} gs_map_args;
+
+int64_t gs_hidden_map_scratch_bytes(const gs_map_args* args);
+int gs_hidden_map_dense(const gs_map_args* args, hipStream_t stream);
+
+/* ---- observers (calibration) ----------------------------------------------------
+ * The reference's per-step path with its quantizers firing: GRULayer.forward
+ * with use_triton off (src/gru_qat/gru_layer.py:205-223) over the step
+ * step_with_gi (gru_cell.py:437-464), which GRULayer.calibrate runs to gather
+ * activation statistics (gru_layer.py:308-336, calibration.py:31-126). Every
+ * quantizer call is a per-tensor FakeQuantize (quantizers.py:84-96) in one of
+ * four modes:
+ *   GS_OBS_OFF      no quantizer (identity)
+ *   GS_OBS_FROZEN   the given scale and zero point (the fast-dispatch case)
+ *   GS_OBS_DYNAMIC  scale and zero point from this tensor's min and max
+ *                   (_scale_zp_from_min_max, quantizers.py:124-134)
+ *   GS_OBS_MIN_MAX  as DYNAMIC, and the running statistics take the tensor's
+ *                   min and max (_update_observer, quantizers.py:136-156: the
+ *                   first call sets them, later ones mix with momentum 0.99)
+ * The fake-quant is ste.py:65-95: q = clamp(rint(x / scale + zp), qmin, qmax),
+ * y = (q - zp) * scale. Scales stay on the device; nothing synchronises. */
+#define GS_OBS_OFF 0
+#define GS_OBS_FROZEN 1
+#define GS_OBS_DYNAMIC 2
+#define GS_OBS_MIN_MAX 3
+
+typedef struct gs_observer {
+  int32_t mode;       /* GS_OBS_*                                                    */
+  int32_t symmetric;  /* 1: scale = max(|min|, |max|, 1e-8) / qmax, zp = 0;          *
+                       * 0: scale = max(max - min, 1e-8) / (qmax - qmin),           *
+                       *    zp = rint(qmin - min / scale)                           */
+  int32_t qmin, qmax;
+  float scale, zero_point;  /* GS_OBS_FROZEN                                         */
+  float* stats;       /* GS_OBS_MIN_MAX: device float[3] = running_min, running_max, *
+                       * initialized (0 or 1); read and updated in place            */
+} gs_observer;
+
+/* One quantizer call on a [rows, cols] tensor (quant_x on the whole sequence,
+ * gru_layer.py:249-250): observes x and writes y = fq(x). */
+typedef struct gs_observe_tensor_args {
+  const float* x;   /* [rows, cols], row stride ld                                  */
+  float* y;         /* [rows, cols] contiguous output                               */
+  float* used;      /* device float[2]: the scale and zero point applied, or NULL  */
+  void* scratch;    /* gs_observe_tensor_scratch_bytes() bytes, 256-byte aligned     */
+  int64_t scratch_bytes;
+  int64_t rows, cols, ld;
+  gs_observer q;
+} gs_observe_tensor_args;
+
+int64_t gs_observe_tensor_scratch_bytes(const gs_observe_tensor_args* args);
+int gs_observe_tensor(const gs_observe_tensor_args* args, hipStream_t stream);
+
+/* The T-step scan with quant_h_in and quant_h_out as observers: at step t,
+ * q_in sees h_{t-1} (h0, then out[t-1]; T calls), q_out sees the pre-quant h_t
+ * (T calls). Same tensors, strides and hidden-map fields as gs_args; the map
+ * is materialized (gs_hidden_map_dense) into the scratch, the steps run as
+ * short launches. Forward only. */
+typedef struct gs_observe_args {
+  int32_t kind;     /* GS_KIND_*                                                    */
+  const float* gi;
+  const float* h0;
+  const float* w;
+  const float* w2;
+  const float* bh;
+  float* out;
+  float* trace;     /* device [T, 4]: (scale, zp) of q_in and of q_out used at step t, or NULL */
+  void* scratch;    /* gs_observe_scan_scratch_bytes() bytes, 256-byte aligned       */
+  int64_t scratch_bytes;
+  int64_t T, B, H;
+  int64_t sg_t, sg_b, sh0_b, so_t, so_b;
+  int64_t nblocks, blksz, log_n, bfly_nblocks;
+  gs_observer q_in;
+  gs_observer q_out;
+} gs_observe_args;
+
+int64_t gs_observe_scan_scratch_bytes(const gs_observe_args* args);
+int gs_observe_scan(const gs_observe_args* args, hipStream_t stream);
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* gs_last_error(void);
 

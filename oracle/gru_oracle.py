@@ -31,6 +31,13 @@ Functions and what they follow (reference file:line):
   input_projection gru_layer.py:249-255 (xq = quant_x(x); Wi_cat = quantize_input_weights();
                    gi = F.linear(xq, Wi_cat, bi_cat)); with ste=True the straight-through
                    gradients (clipped STE on x, scales held constant)
+  ObserverState, observer_forward, scale_zp_from_min_max, update_observer, freeze_observer
+                   quantizers.py:63-156 and :176-181 (per-tensor FakeQuantize: modes frozen,
+                   dynamic, min_max; scale and zero point from a min and max, symmetric or
+                   affine; the running-statistics update with momentum 0.99; freeze)
+  observe_scan     the per-step path with quant_h_in/quant_h_out firing (gru_layer.py:212-223
+                   over step_with_gi, gru_cell.py:437-464), as GRULayer.calibrate
+                   (gru_layer.py:308-336) runs it
 
 Pins (tests/test_oracle.py; the backward in tests/test_oracle_backward.py
 against torch.autograd through scan_ste, in float64): round-half-even and clipping known answers
@@ -41,7 +48,12 @@ hidden map), an independent permutation-matrix construction of the
 two-factor Monarch map and its reduction to the single-factor map, identity
 and single-stage closed forms of the butterfly, float64 brute force, and
 golden vectors produced from the reference's own butterfly kernel
-(tests/golden/).
+(tests/golden/). The observers (tests/test_oracle_observe.py): frozen and off
+modes reduce observe_scan to scan; known answers of the symmetric and affine
+scale rules; the code-range invariants of a dynamic quantizer (a symmetric
+one puts its largest |x| on code +-qmax, an affine one spans [qmin, qmax]);
+the running statistics against their float64 recursion; freeze against the
+scale rule applied by hand.
 """
 
 from __future__ import annotations
@@ -393,3 +405,96 @@ def input_projection(x: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]
         W = W + (wq - W).detach() if ste else wq
     return F.linear(xq, W, b)
 
+
+
+# ---- observers (calibration) -----------------------------------------------------------
+
+class ObserverState:
+    """A per-tensor FakeQuantize's state (quantizers.py:63-96): mode
+    ("off", "frozen", "dynamic", "min_max"), the range of _qrange
+    (quantizers.py:119-122), the frozen scale and zero point and the running
+    statistics."""
+
+    def __init__(self, mode: str, bits: int = 8, symmetric: bool = True, scale: float = 1.0,
+                 zero_point: float = 0.0) -> None:
+        self.mode = mode
+        self.symmetric = symmetric
+        if symmetric:
+            self.qmin, self.qmax = -(2 ** (bits - 1)) + 1, 2 ** (bits - 1) - 1
+        else:
+            self.qmin, self.qmax = 0.0, 2.0**bits - 1.0
+        self.scale = torch.tensor(scale, dtype=torch.float32)
+        self.zero_point = torch.tensor(zero_point, dtype=torch.float32)
+        self.running_min = torch.tensor(float("inf"))
+        self.running_max = torch.tensor(float("-inf"))
+        self.initialized = False
+
+
+def scale_zp_from_min_max(st: ObserverState, x_min: torch.Tensor,
+                          x_max: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """quantizers.py:124-134."""
+    if st.symmetric:
+        absmax = torch.maximum(x_max.abs(), x_min.abs()).clamp(min=1e-8)
+        scale = absmax / st.qmax
+        zp = torch.zeros_like(scale)
+    else:
+        scale = (x_max - x_min).clamp(min=1e-8) / (st.qmax - st.qmin)
+        zp = torch.round(st.qmin - x_min / scale)
+    return scale, zp
+
+
+def update_observer(st: ObserverState, x: torch.Tensor) -> None:
+    """The per-tensor branch of _update_observer (quantizers.py:136-156)."""
+    cur_min = x.detach().min()
+    cur_max = x.detach().max()
+    if not st.initialized:
+        st.running_min = cur_min
+        st.running_max = cur_max
+        st.initialized = True
+    else:
+        momentum = 0.99
+        st.running_min = momentum * st.running_min + (1 - momentum) * cur_min
+        st.running_max = momentum * st.running_max + (1 - momentum) * cur_max
+
+
+def observer_forward(st: ObserverState, x: torch.Tensor) -> Tuple[torch.Tensor, Tuple[float, float]]:
+    """FakeQuantize.forward (quantizers.py:84-96) with FakeQuantizePerTensor's
+    scale rule (:176-181) and fake_quant_ste's forward (ste.py:65-95); returns
+    the output and the (scale, zero point) applied."""
+    if st.mode == "off":
+        return x, (1.0, 0.0)
+    if st.mode == "frozen":
+        scale, zp = st.scale, st.zero_point
+    else:
+        scale, zp = scale_zp_from_min_max(st, x.min(), x.max())
+        if st.mode == "min_max":
+            update_observer(st, x)
+    q = torch.round(x / scale + zp)
+    q = torch.clamp(q, st.qmin, st.qmax)
+    return (q - zp) * scale, (float(scale), float(zp))
+
+
+def freeze_observer(st: ObserverState) -> None:
+    """FakeQuantize.freeze (quantizers.py:98-107)."""
+    if st.mode == "min_max":
+        st.scale, st.zero_point = scale_zp_from_min_max(st, st.running_min, st.running_max)
+    st.mode = "frozen"
+
+
+def observe_scan(gi: torch.Tensor, h0: torch.Tensor, gh_fn: GhFn, q_in: ObserverState,
+                 q_out: ObserverState) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The per-step path with quant_h_in / quant_h_out firing
+    (gru_layer.py:212-223 over step_with_gi, gru_cell.py:437-464); returns out
+    [T, B, H] and the (scale, zp) of q_in and q_out used per step [T, 4]."""
+    T = gi.shape[0]
+    out = torch.empty(T, *h0.shape, dtype=gi.dtype)
+    trace = torch.empty(T, 4, dtype=torch.float32)
+    h = h0
+    for t in range(T):
+        hq, (si, zi) = observer_forward(q_in, h)
+        h_new = gru_step(gi[t], h, gh_fn(hq))
+        h_new, (so, zo) = observer_forward(q_out, h_new)
+        out[t] = h_new
+        trace[t] = torch.tensor([si, zi, so, zo])
+        h = h_new
+    return out, trace
