@@ -27,9 +27,10 @@ namespace {
 
 constexpr int kRowThreads = 256;
 
-// One workgroup per row of w [rows, cols].
+// One workgroup per row of w [rows, cols]: the row's scale, then wq = the
+// fake-quantized row (when wq != null) and its integer codes (when codes != null).
 __global__ __launch_bounds__(kRowThreads) void weight_quant_rows(const float* w, int cols, float qmin, float qmax,
-                                                                 float* wq, float* scale_out) {
+                                                                 float* wq, float* scale_out, int8_t* codes) {
   __shared__ float red[kRowThreads / 64];
   const int64_t row = blockIdx.x;
   const float* src = w + row * cols;
@@ -42,8 +43,11 @@ __global__ __launch_bounds__(kRowThreads) void weight_quant_rows(const float* w,
   float absmax = red[0];
   for (int i = 1; i < kRowThreads / 64; ++i) absmax = fmaxf(absmax, red[i]);
   const float scale = fmaxf(absmax, 1e-8f) / qmax;
-  const Quant q{scale, qmin, qmax, 1};
-  for (int k = threadIdx.x; k < cols; k += kRowThreads) wq[row * cols + k] = fake_quant(src[k], q);
+  for (int k = threadIdx.x; k < cols; k += kRowThreads) {
+    const float c = __builtin_fminf(__builtin_fmaxf(__builtin_rintf(src[k] / scale), qmin), qmax);
+    if (wq != nullptr) wq[row * cols + k] = c * scale;  // fake_quant of src[k] at this scale
+    if (codes != nullptr) codes[row * cols + k] = (int8_t)c;
+  }
   if (threadIdx.x == 0) scale_out[row] = scale;
 }
 
@@ -98,7 +102,7 @@ extern "C" int gs_input_proj(const gs_proj_args* a, hipStream_t stream) {
       return set_error(GS_ERR_INVALID, "%s: weight quant needs qmax > 0 and qmin <= qmax; got [%d, %d]", who,
                        a->q_w.qmin, a->q_w.qmax);
     hipLaunchKernelGGL(weight_quant_rows, dim3((unsigned)a->N), dim3(kRowThreads), 0, stream, a->w, (int)a->I,
-                       (float)a->q_w.qmin, (float)a->q_w.qmax, a->w_q, a->w_scale);
+                       (float)a->q_w.qmin, (float)a->q_w.qmax, a->w_q, a->w_scale, nullptr);
     GS_CHECK_HIP(hipGetLastError());
     w = a->w_q;
   }
@@ -200,5 +204,26 @@ extern "C" int gs_input_proj_bwd(const gs_proj_bwd_args* a, hipStream_t stream) 
     if (rc) return rc;
   }
   if (a->dbias) return colsum(a->dbias, a->dgi, a->sdgi, M, N, colp, stream, who);
+  return GS_OK;
+}
+
+extern "C" int gs_quantize_rows(const gs_rows_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_quantize_rows";
+  if (a == nullptr) return set_error(GS_ERR_INVALID, "%s: args is NULL", who);
+  if (a->rows < 1 || a->cols < 1 || a->rows > INT32_MAX || a->cols > (1 << 24))
+    return set_error(GS_ERR_INVALID, "%s: rows and cols must be in [1, 2^31) and [1, 2^24]; got %lld, %lld", who,
+                     (long long)a->rows, (long long)a->cols);
+  if (!a->w || !a->scale || (!a->w_q && !a->codes))
+    return set_error(GS_ERR_INVALID, "%s: w, scale and at least one of w_q and codes must be non-NULL", who);
+  if (!(a->qmax > 0) || a->qmin > a->qmax)
+    return set_error(GS_ERR_INVALID, "%s: needs qmax > 0 and qmin <= qmax; got [%d, %d]", who, a->qmin, a->qmax);
+  if (a->codes && (a->qmin < -128 || a->qmax > 127))
+    return set_error(GS_ERR_INVALID, "%s: int8 codes need qmin >= -128 and qmax <= 127; got [%d, %d]", who, a->qmin,
+                     a->qmax);
+  hipLaunchKernelGGL(weight_quant_rows, dim3((unsigned)a->rows), dim3(kRowThreads), 0, stream, a->w, (int)a->cols,
+                     (float)a->qmin, (float)a->qmax, a->w_q, a->scale, a->codes);
+  GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }

@@ -28,6 +28,7 @@ from .input_proj import input_projection, quantize_input_weights
 from .quantizers import FakeQuantizePerTensor, QuantizerConfig
 from .observe import gru_scan_observe, hidden_map_dense
 from .calibration import calibrate, freeze_all
+from .export import dequantize_int_weights, export_int_weights, quantize_rows
 
 __all__ = [
     "FakeQuantizePerTensor",
@@ -36,6 +37,8 @@ __all__ = [
     "QuantizerConfig",
     "ScanLayer",
     "calibrate",
+    "dequantize_int_weights",
+    "export_int_weights",
     "extract_butterfly_twiddles",
     "extract_diagonal_factors",
     "extract_monarch_factors",
@@ -59,6 +62,7 @@ __all__ = [
     "layer_forward",
     "load_library",
     "quantize_input_weights",
+    "quantize_rows",
     "resolve_use_triton",
     "workspace_faults",
 ]

@@ -40,6 +40,7 @@ EXPORTS = (
     "gs_input_proj",
     "gs_input_proj_bwd",
     "gs_input_proj_bwd_workspace_bytes",
+    "gs_quantize_rows",
     "gs_hidden_map_dense",
     "gs_hidden_map_scratch_bytes",
     "gs_observe_tensor",
@@ -170,6 +171,19 @@ class GsProjBwdArgs(ctypes.Structure):
     ]
 
 
+class GsRowsArgs(ctypes.Structure):
+    _fields_ = [
+        ("w", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("codes", ctypes.c_void_p),
+        ("w_q", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("qmin", ctypes.c_int32),
+        ("qmax", ctypes.c_int32),
+    ]
+
+
 class GsMapArgs(ctypes.Structure):
     _fields_ = [
         ("kind", ctypes.c_int32),
@@ -288,6 +302,8 @@ def load() -> ctypes.CDLL:
             size = getattr(lib, name + "_scratch_bytes")
             size.argtypes = [ctypes.POINTER(argt)]
             size.restype = ctypes.c_int64
+        lib.gs_quantize_rows.argtypes = [ctypes.POINTER(GsRowsArgs), ctypes.c_void_p]
+        lib.gs_quantize_rows.restype = ctypes.c_int
         lib.gs_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsArgs)]
         lib.gs_workspace_bytes.restype = ctypes.c_int64
         lib.gs_bwd_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsBwdArgs)]

@@ -332,3 +332,11 @@ class ScanLayer(torch.nn.Module):
         from .calibration import freeze_all
 
         freeze_all(self)
+
+    def export_int_weights(self, bits: int = 8) -> dict:
+        """int8 weight codes, scales and zero points plus the frozen activation
+        scales (the export gru_cell.py:551-553 leaves as a TODO); see
+        ``export.export_int_weights``."""
+        from .export import export_int_weights
+
+        return export_int_weights(self, bits)

@@ -241,6 +241,26 @@ typedef struct gs_proj_bwd_args {
 int64_t gs_input_proj_bwd_workspace_bytes(const gs_proj_bwd_args* args);
 int gs_input_proj_bwd(const gs_proj_bwd_args* args, hipStream_t stream);
 
+/* ---- per-row weight codes (int8 export) -------------------------------------------
+ * Per-row symmetric quantization of a weight w [rows, cols] with the rule of
+ * FakeQuantizePerChannel (quantizers.py:188-199, 124-134): scale[r] =
+ * max(max_c |w[r][c]|, 1e-8) / qmax, codes[r][c] = clamp(rint(w[r][c] / scale[r]),
+ * qmin, qmax). Writes the scales, the int8 codes (codes != NULL, qmin >= -128,
+ * qmax <= 127) and/or the fake-quantized weight w_q = codes * scale (bit-exact
+ * with the input projection's weight fake-quant). This is the export the
+ * reference leaves as a TODO (gru_cell.py:551-553: "export_int_weights()
+ * returning a dict of int tensors, scales, and zero points"). */
+typedef struct gs_rows_args {
+  const float* w;   /* [rows, cols] contiguous                                   */
+  float* scale;     /* [rows]                                                    */
+  int8_t* codes;    /* [rows, cols] contiguous, or NULL                          */
+  float* w_q;       /* [rows, cols] contiguous, or NULL                          */
+  int64_t rows, cols;
+  int32_t qmin, qmax;
+} gs_rows_args;
+
+int gs_quantize_rows(const gs_rows_args* args, hipStream_t stream);
+
 /* ---- dense form of a hidden map --------------------------------------------------
  * Writes the hidden map of any kind as the dense matrix m [3H, H] (rows r, z,
  * n) with gh = hq m^T + bh: the diagonal kind's diag(w_g) blocks, the Monarch

@@ -209,3 +209,30 @@ def test_scan_layer_construction():
         G.ScanLayer("circulant", torch.zeros(3 * H, I), None, torch.zeros(3 * H, H), torch.zeros(3 * H))
     with pytest.raises(ValueError):
         G.ScanLayer("dense", torch.zeros(3 * H, I), None, torch.zeros(3 * H, H), torch.zeros(3 * H), w_bits=1)
+
+
+# ---- int8 export ----------------------------------------------------------------------
+
+def test_quantize_rows_rejects():
+    lib = _lib.load()
+    a = _lib.GsRowsArgs()
+    a.w, a.scale, a.codes = FAKE, FAKE, FAKE
+    a.rows, a.cols, a.qmin, a.qmax = 4, 8, -127, 127
+    a.rows = 0
+    assert lib.gs_quantize_rows(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    a.rows = 4
+    a.qmin, a.qmax = -200, 200
+    assert lib.gs_quantize_rows(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"int8 codes" in lib.gs_last_error()
+    a.qmin, a.qmax = -127, 127
+    a.codes = None
+    assert lib.gs_quantize_rows(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"at least one" in lib.gs_last_error()
+
+
+def test_export_requires_frozen_quantizers():
+    H, I = 8, 5
+    layer = G.ScanLayer("dense", torch.zeros(3 * H, I), None, torch.zeros(3 * H, H), torch.zeros(3 * H),
+                        h_quant=G.QuantizerConfig(mode="min_max"))
+    with pytest.raises(ValueError, match="freeze"):
+        G.export._frozen(layer.quant_h_in)
