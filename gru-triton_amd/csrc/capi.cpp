@@ -126,6 +126,8 @@ int64_t dense_bwd_scratch_bytes(const gs_bwd_args* a);
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
 int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
 int64_t butterfly_bwd_workspace_bytes(const gs_bwd_args* a);
+int64_t monarch_bwd_workspace_bytes(const gs_bwd_args* a);
+int64_t monarch_bwd_scratch_bytes(const gs_bwd_args* a);
 int64_t butterfly_bwd_scratch_bytes(const gs_bwd_args* a);
 }  // namespace gs
 
@@ -154,7 +156,7 @@ int64_t gs_bwd_workspace_bytes(int kind, const gs_bwd_args* a) {
     case GS_KIND_DIAGONAL:
       return 0;
     case GS_KIND_MONARCH:
-      return gs::struct_bwd_workspace_bytes(kind, a);
+      return gs::monarch_bwd_workspace_bytes(a);
     case GS_KIND_BUTTERFLY:
       return gs::butterfly_bwd_workspace_bytes(a);
     default:
@@ -170,7 +172,7 @@ int64_t gs_bwd_scratch_bytes(int kind, const gs_bwd_args* a) {
     case GS_KIND_DIAGONAL:
       return 0;
     case GS_KIND_MONARCH:
-      return gs::struct_bwd_scratch_bytes(kind, a);
+      return gs::monarch_bwd_scratch_bytes(a);
     case GS_KIND_BUTTERFLY:
       return gs::butterfly_bwd_scratch_bytes(a);
     default:

@@ -464,10 +464,6 @@ int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a) {
 
 }  // namespace gs
 
-extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
-  return gs::run_struct(GS_KIND_MONARCH, a, stream, "gs_monarch_bwd");
-}
-
 extern "C" int64_t gs_hidden_map_scratch_bytes(const gs_map_args* a) {
   using namespace gs;
   const int rc = validate_map(a, "gs_hidden_map_scratch_bytes");

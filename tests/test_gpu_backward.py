@@ -56,6 +56,10 @@ CASES = [
     (1, (1, 3, 16), None, False), (1, (7, 6, 128), None, False),
     (3, (16, 8, 512), 8, True), (3, (8, 6, 128), 8, False), (3, (5, 9, 96), 3, True),
     (4, (8, 6, 512), None, False), (4, (3, 2, 1000), None, False),
+    # single-factor Monarch on the block-local path: blksz 16, 32, 64, 128, B not a multiple of the
+    # rows per workgroup; blksz 48 takes the materialized path
+    (3, (64, 32, 512), 8, False), (3, (9, 5, 512), 4, False), (3, (7, 3, 256), 8, False),
+    (3, (11, 7, 64), 4, False), (3, (5, 3, 96), 2, False), (3, (1, 2, 64), 2, False),
 ]
 
 
@@ -77,6 +81,7 @@ def test_backward_matches_oracle(dev, idx, shape, nb, two, q):
 
 
 @pytest.mark.parametrize("idx,shape,nb,two", [(1, (9, 6, 128), None, False), (3, (6, 5, 64), 4, True),
+                                              (3, (6, 5, 128), 2, False),
                                               (4, (5, 3, 64), None, False), (0, (9, 6, 40), None, False)])
 def test_backward_is_deterministic_and_accepts_strided_inputs(dev, idx, shape, nb, two):
     """Two backward calls give bitwise-equal gradients (no atomics anywhere), and
