@@ -36,8 +36,14 @@ int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const 
 
 namespace {
 
-constexpr int kSplitK = 4;  // lanes sharing one unit's 3 bs-term dot product
-constexpr int kDepth = 8;   // steps of per-unit inputs loaded ahead
+constexpr int kDepth = 8;  // steps of per-unit inputs loaded ahead
+
+// Lanes (adjacent) sharing one unit's dot product over 3 bs terms (8 for
+// blksz 128 measured 4x slower: 1024-thread workgroups leave 128 VGPRs a lane).
+template <int BS>
+constexpr int split_k() {
+  return 4;
+}
 
 struct M1Params {
   const float* w;     // [3, nb, bs, bs] (out, in)
@@ -52,25 +58,31 @@ struct M1Params {
 
 template <int BS>
 constexpr int rows_per_wg() {
-  return 4 * BS >= 256 ? 1 : 256 / (4 * BS);
+  return split_k<BS>() * BS >= 256 ? 1 : 256 / (split_k<BS>() * BS);
 }
 
-// Thread (row slot rs, unit u, quarter kq) of workgroup (block n, row group):
-// holds W[g][n][j][u] for its quarter of the 3 bs terms kk = g bs + j in
-// registers, sums dgh_t[kk] W over them, and the quad of lanes of unit u
-// combines the quarters. Every lane of the quad then has D_{t-1}[u]; lane
+template <int BS>
+constexpr int m1_threads() {
+  return split_k<BS>() * BS * rows_per_wg<BS>();
+}
+
+// Thread (row slot rs, unit u, part kq) of workgroup (block n, row group):
+// holds W[g][n][j][u] for its part of the 3 bs terms kk = g bs + j in
+// registers, sums dgh_t[kk] W over them, and the SK adjacent lanes of unit u
+// combine the parts (DPP). Every one of them then has D_{t-1}[u]; lane
 // kq < 3 writes dgh_{t-1}[kq][u] = D_{t-1} C_kq for the next step.
 template <int BS>
-__global__ __launch_bounds__(4 * BS * rows_per_wg<BS>()) void monarch1_bwd_kernel(M1Params p) {
-  constexpr int TPR = 4 * BS;  // threads per batch row
+__global__ __launch_bounds__(m1_threads<BS>()) void monarch1_bwd_kernel(M1Params p) {
+  constexpr int SK = split_k<BS>();
+  constexpr int TPR = SK * BS;  // threads per batch row
   constexpr int R = rows_per_wg<BS>();
-  constexpr int KT = 3 * BS / kSplitK;  // terms per thread
+  constexpr int KT = 3 * BS / SK;  // terms per thread
   static_assert(KT % 4 == 0, "terms per thread must be whole float4s");
   __shared__ __attribute__((aligned(16))) float dgh[2][R][3 * BS];
 
   const int n = blockIdx.x;
   const int rs = threadIdx.x / TPR, lt = threadIdx.x - rs * TPR;
-  const int u = lt >> 2, kq = lt & 3;
+  const int u = lt / SK, kq = lt % SK;
   const int b = blockIdx.y * R + rs;
   const bool live = b < p.B;
   const int H = p.H, T = p.T;
@@ -118,18 +130,16 @@ __global__ __launch_bounds__(4 * BS * rows_per_wg<BS>()) void monarch1_bwd_kerne
       const int t = t0 - i;
       if (t >= 0) {
         const float* src = &dgh[buf][rs][kq * KT];
-        float acc0 = 0.0f, acc1 = 0.0f;
+        f4 a4 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int q = 0; q < KT; q += 4) {
           const f4 v = *reinterpret_cast<const f4*>(src + q);
-          acc0 += v[0] * wt[q];
-          acc1 += v[1] * wt[q + 1];
-          acc0 += v[2] * wt[q + 2];
-          acc1 += v[3] * wt[q + 3];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) a4[c] += v[c] * wt[q + c];
         }
-        float acc = acc0 + acc1;
-        acc += __shfl_xor(acc, 1);
-        acc += __shfl_xor(acc, 2);
+        float acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+        acc += lane_xor_c<1>(acc);
+        acc += lane_xor_c<2>(acc);
         float carry;
         {
 #pragma clang fp contract(off)
@@ -142,7 +152,8 @@ __global__ __launch_bounds__(4 * BS * rows_per_wg<BS>()) void monarch1_bwd_kerne
           if (live && kq == 0) p.dsum[(int64_t)(t - 1) * BH + e0] = D;
           if (kq < 3) dgh[buf ^ 1][rs][kq * BS + u] = D * ccc[i];
         }
-        __syncthreads();
+        // LDS-only barrier: the step's global stores need not complete here
+        lds_barrier();
         buf ^= 1;
       }
     }
@@ -160,10 +171,10 @@ typedef void (*M1Fn)(M1Params);
 
 M1Fn pick_m1(int bs, int* threads, int* rows) {
   switch (bs) {
-    case 16: *rows = rows_per_wg<16>(); *threads = 64 * *rows; return monarch1_bwd_kernel<16>;
-    case 32: *rows = rows_per_wg<32>(); *threads = 128 * *rows; return monarch1_bwd_kernel<32>;
-    case 64: *rows = rows_per_wg<64>(); *threads = 256 * *rows; return monarch1_bwd_kernel<64>;
-    case 128: *rows = rows_per_wg<128>(); *threads = 512 * *rows; return monarch1_bwd_kernel<128>;
+    case 16: *rows = rows_per_wg<16>(); *threads = m1_threads<16>(); return monarch1_bwd_kernel<16>;
+    case 32: *rows = rows_per_wg<32>(); *threads = m1_threads<32>(); return monarch1_bwd_kernel<32>;
+    case 64: *rows = rows_per_wg<64>(); *threads = m1_threads<64>(); return monarch1_bwd_kernel<64>;
+    case 128: *rows = rows_per_wg<128>(); *threads = m1_threads<128>(); return monarch1_bwd_kernel<128>;
     default: return nullptr;
   }
 }
