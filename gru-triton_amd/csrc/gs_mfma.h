@@ -247,5 +247,9 @@ inline int resident_groups(const void* fn, int threads, size_t lds, int per_grou
 
 int64_t monarch2_workspace_bytes(const gs_args* a);
 int run_monarch2(const gs_args* a, hipStream_t stream, const char* who);
+// Single-factor Monarch forward with one workgroup per block and batch rows
+// (scan_monarch1.hip): the shapes it takes, and its launch.
+bool monarch1_local_ok(const gs_args* a);
+int run_monarch1_local(const gs_args* a, hipStream_t stream);
 
 }  // namespace gs

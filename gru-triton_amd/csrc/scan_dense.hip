@@ -387,7 +387,8 @@ int64_t ws_bytes(int kind, const gs_args* a) {
 int64_t dense_workspace_bytes(const gs_args* a) { return ws_bytes(kDense, a); }
 
 int64_t monarch_workspace_bytes(const gs_args* a) {
-  return a->w2 ? monarch2_workspace_bytes(a) : ws_bytes(kMonarch1, a);
+  if (a->w2) return monarch2_workspace_bytes(a);
+  return monarch1_local_ok(a) ? kCtrlBytes : ws_bytes(kMonarch1, a);
 }
 
 }  // namespace gs
@@ -407,5 +408,6 @@ extern "C" int gs_monarch_fwd(const gs_args* a, hipStream_t stream) {
   int rc = gs::validate_common(a, who);
   if (rc) return rc;
   if (a->w2) return gs::run_monarch2(a, stream, who);
+  if (gs::monarch1_local_ok(a)) return gs::run_monarch1_local(a, stream);
   return gs::run(gs::kMonarch1, a, stream, who);
 }

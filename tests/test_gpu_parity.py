@@ -92,8 +92,11 @@ def _monarch(shape, nb, two=False, seed=0, **over):
     return cfg
 
 
+# blksz 16, 32, 64 and 128 run the block-local kernel (scan_monarch1.hip; (7, 5, 64) and (9, 3, 128)
+# leave the last workgroup's rows partly empty), other block sizes the MFMA kernel of scan_dense.hip
 MONARCH_CASES = [((8, 4, 32), 4), ((16, 8, 64), 4), ((8, 32, 64), 4), ((16, 32, 256), 4), ((6, 3, 30), 5),
-                 ((5, 4, 256), 2), ((4, 5, 8), 8), ((1, 4, 8), 2)]
+                 ((5, 4, 256), 2), ((4, 5, 8), 8), ((1, 4, 8), 2), ((7, 5, 64), 4), ((9, 3, 128), 4),
+                 ((3, 2, 1024), 16), ((4, 3, 192), 3)]
 
 
 @pytest.mark.parametrize("shape,nb", MONARCH_CASES)
@@ -112,15 +115,24 @@ def test_monarch_two_factor_fp32(dev, shape, nb):
     assert_fp32_parity(_monarch(shape, nb, two=True), dev)
 
 
-def test_monarch_two_factor_identity_equals_single(dev):
-    cfg = _monarch((6, 8, 64), 4)
-    eye = torch.eye(16).expand(3, 4, 16, 16).contiguous()
-    from parity_util import run_both, to_dev
+@pytest.mark.parametrize("shape,nb", [((6, 8, 64), 4), ((6, 8, 192), 4)])
+def test_monarch_two_factor_identity_equals_single(dev, shape, nb):
+    """Identity second factor gives the single-factor map. At blksz 48 both
+    forms run the same MFMA arithmetic (bit-exact); at blksz 16 the single
+    factor runs the block-local VALU kernel, whose sums run in another order
+    (within 1e-6)."""
+    cfg = _monarch(shape, nb)
+    bs = shape[2] // nb
+    eye = torch.eye(bs).expand(3, nb, bs, bs).contiguous()
+    from parity_util import to_dev
     from gru_qat_amd.configs import run_config
 
-    one = run_config(to_dev(cfg, dev))
-    two = run_config(to_dev(dict(cfg, w2=eye), dev))
-    assert torch.equal(one.cpu(), two.cpu())
+    one = run_config(to_dev(cfg, dev)).cpu()
+    two = run_config(to_dev(dict(cfg, w2=eye), dev)).cpu()
+    if bs in (16, 32, 64, 128):
+        assert (one - two).abs().max().item() <= 1e-6
+    else:
+        assert torch.equal(one, two)
 
 
 @pytest.mark.parametrize("two", [False, True])
