@@ -201,8 +201,9 @@ def test_dense_bwd_rejects_missing_scratch():
 def test_workspace_sizes():
     """Control words plus double-buffered tagged exchange words (8 bytes per
     unit and row) when a batch row's step spans workgroups; two-factor Monarch
-    adds 3 gates of first-factor words. A Monarch block of <= 64 units is
-    produced by one workgroup, which exchanges through LDS only."""
+    adds 3 gates of first-factor words. A single-factor Monarch block of 16,
+    32, 64 or 128 units is produced by one workgroup per batch row, which keeps
+    its state in LDS; other block sizes use the dense kernel's exchange."""
     lib = _lib.load()
     a = _args(T=64, B=32, H=512)
     n = lib.gs_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a))
@@ -217,8 +218,10 @@ def test_workspace_sizes():
     a_m1 = _args(T=64, B=32, H=512, nblocks=8, blksz=64)
     assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m1)) == 256
     a_m1 = _args(T=64, B=32, H=512, nblocks=4, blksz=128)
-    # 4 blocks x 4 workgroups of 8 compute waves per row-block
-    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m1)) == 256 + xh + 16 * 8 * 8 + 8 * 16 * 8
+    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m1)) == 256
+    a_m1 = _args(T=64, B=32, H=512, nblocks=2, blksz=256)
+    # 2 blocks x 16 workgroups of 4 compute waves per row-block; pollers read 16 * KC (KC = 16) words per row
+    assert lib.gs_workspace_bytes(_lib.KIND_MONARCH, ctypes.byref(a_m1)) == 256 + xh + 16 * 16 * 8 + 8 * 2 * 16 * 8
     a_m2 = _args(T=64, B=32, H=512, nblocks=8, blksz=64, w2=FAKE)
     # fused two-factor kernel (bs = 64, nb = 8): one exchange of q_in(h) padded
     # by 512 words, plus one XCD-id word per workgroup (8 row-blocks x 8 blocks)
