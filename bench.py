@@ -57,6 +57,9 @@ WORK = {
     2: {"bytes": 19_994_624, "flops": 3_221_225_472, "bound": "mfma"},
     3: {"bytes": 17_635_328, "flops": 805_306_368, "bound": "mfma"},
     4: {"bytes": 537_391_104, "flops": 3_019_898_880, "bound": "hbm"},
+    # single-factor Monarch (not a BASELINE.json configuration): 2 T B 3H blksz flops;
+    # fp32 FMA, on the VALU in this build (fp32 vector peak = fp32 MFMA peak on MI355X)
+    5: {"bytes": 17_242_112, "flops": 402_653_184, "bound": "mfma"},
 }
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -274,7 +277,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--kinds", default="0,1,2,3,4")
+    ap.add_argument("--kinds", default="0,1,2,3,4,5")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=4.0, help="seconds of CPU baseline per kind")
     ap.add_argument("--copy-mib", type=int, default=0, help="run a plain N MiB copy K times and exit")

@@ -2,7 +2,8 @@
 //
 //   gs_bench <items> [launches=30] [warmup=10]
 //
-// <items> is a comma-separated list of configs 0..4 and "copy", run in that
+// <items> is a comma-separated list of configs 0..5 (5: the single-factor
+// Monarch form of config 3, not a BASELINE configuration) and "copy", run in that
 // order in one process (one JSON line each). A config run builds the
 // synthetic inputs of one of the five benchmark configurations (shapes,
 // kinds and hidden quant of gru_qat_amd/configs.py;
@@ -83,8 +84,8 @@ __global__ void copy_kernel(const float4* __restrict__ src, float4* __restrict__
     dst[i] = src[i];
 }
 
-const char* kNames[5] = {"diagonal_fp32", "dense_fp32", "dense_int8_qat", "monarch_nb8_two_factor_int8",
-                         "butterfly_fp32"};
+const char* kNames[6] = {"diagonal_fp32", "dense_fp32", "dense_int8_qat", "monarch_nb8_two_factor_int8",
+                         "butterfly_fp32", "monarch_nb8_single_int8"};
 
 void report(const char* what, int idx, const std::vector<float>& ms, long long T, long long B, long long H) {
   std::vector<float> s = ms;
@@ -174,14 +175,16 @@ int run_config(int idx, int launches, int warmup, Mode mode) {
     kind = GS_KIND_DENSE;
     owned.push_back(upload(filled(3 * H * H, g, k)));
     a.w = owned.back();
-  } else if (idx == 3) {
+  } else if (idx == 3 || idx == 5) {
     kind = GS_KIND_MONARCH;
     a.nblocks = 8;
     a.blksz = H / 8;
     owned.push_back(upload(filled(3 * H * a.blksz, g, 0.125f)));
     a.w = owned.back();
-    owned.push_back(upload(filled(3 * H * a.blksz, g, 0.125f)));
-    a.w2 = owned.back();
+    if (idx == 3) {
+      owned.push_back(upload(filled(3 * H * a.blksz, g, 0.125f)));
+      a.w2 = owned.back();
+    }
   } else {
     kind = GS_KIND_BUTTERFLY;
     a.log_n = 10;
@@ -205,7 +208,7 @@ int run_config(int idx, int launches, int warmup, Mode mode) {
   a.sh0_b = H;
   a.so_t = B * H;
   a.so_b = H;
-  if (idx == 2 || idx == 3) {
+  if (idx == 2 || idx == 3 || idx == 5) {
     const gs_quant q = {1, 1.0f / 127.0f, -127, 127};
     a.q_in = q;
     a.q_out = q;
@@ -461,7 +464,7 @@ int run_proj(int launches, int warmup) {
 
 int main(int argc, char** argv) {
   if (argc < 2) {
-    fprintf(stderr, "usage: gs_bench <items: configs 0..4, b0..b4 (backward), c0..c4 (calibration), proj, copy; "
+    fprintf(stderr, "usage: gs_bench <items: configs 0..5, b0..b5 (backward), c0..c5 (calibration), proj, copy; "
                     "comma-separated> "
                     "[launches] [warmup]\n");
     return 2;
@@ -483,7 +486,7 @@ int main(int argc, char** argv) {
       const char* num = mode == kForward ? tok : tok + 1;
       char* end = nullptr;
       const long idx = strtol(num, &end, 10);
-      if (*num == 0 || *end != 0 || idx < 0 || idx > 4) {
+      if (*num == 0 || *end != 0 || idx < 0 || idx > 5) {
         fprintf(stderr, "gs_bench: unknown item '%s'\n", tok);
         return 2;
       }

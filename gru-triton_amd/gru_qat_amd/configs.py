@@ -18,6 +18,10 @@ weights, hidden bias, gi, h0.
   hidden quant as cfg2.
 * cfg4 butterfly: T=512 B=64 H=1024; twiddles [3, 1, 10, 512, 2, 2] ~
   N(0, 1/2); bh ~ U(+-1/sqrt(H)); gi ~ N(0, 1); h0 = 0.
+* cfg5 Monarch single factor (the reference's own Monarch form,
+  scan_monarch.py:74-127), nblocks=8, blksz=64: one factor [3, 8, 64, 64] ~
+  U(-1/8, 1/8), bh ~ U(+-1/sqrt(H)), gi ~ N(0, 1), h0 = 0, hidden quant as
+  cfg2. Not one of BASELINE.json's configurations; measured beside them.
 """
 
 from __future__ import annotations
@@ -35,9 +39,11 @@ NAMES = {
     2: "dense_int8_qat",
     3: "monarch_nb8_two_factor_int8",
     4: "butterfly_fp32",
+    5: "monarch_nb8_single_int8",
 }
 
-SHAPES = {0: (64, 32, 512), 1: (64, 32, 512), 2: (64, 32, 512), 3: (64, 32, 512), 4: (512, 64, 1024)}
+SHAPES = {0: (64, 32, 512), 1: (64, 32, 512), 2: (64, 32, 512), 3: (64, 32, 512), 4: (512, 64, 1024),
+          5: (64, 32, 512)}
 
 
 def _uniform(gen: torch.Generator, shape, bound: float) -> torch.Tensor:
@@ -83,12 +89,12 @@ def make_config(idx: int, device: Optional[torch.device] = None, seed: int = 0,
             d["h_in_quant"] = Q_INT8_HIDDEN
             d["h_out_quant"] = Q_INT8_HIDDEN
         d["w"] = Wh_cat
-    elif idx == 3:
+    elif idx in (3, 5):
         d["kind"] = "monarch"
         nb = 8 if H % 8 == 0 else 1
         bs = H // nb
         d["w"] = _uniform(gen, (3, nb, bs, bs), 1.0 / 8.0)
-        d["w2"] = _uniform(gen, (3, nb, bs, bs), 1.0 / 8.0)
+        d["w2"] = _uniform(gen, (3, nb, bs, bs), 1.0 / 8.0) if idx == 3 else None
         d["bh"] = _uniform(gen, (3 * H,), k)
         d["gi"] = torch.randn((T, B, 3 * H), generator=gen, dtype=torch.float32)
         d["h0"] = torch.zeros((B, H), dtype=torch.float32)
@@ -106,7 +112,7 @@ def make_config(idx: int, device: Optional[torch.device] = None, seed: int = 0,
         raise ValueError(f"unknown config {idx}")
     if device is not None:
         for key in ("w", "w2", "bh", "gi", "h0"):
-            if key in d:
+            if d.get(key) is not None:
                 d[key] = d[key].to(device)  # type: ignore[union-attr]
     return d
 

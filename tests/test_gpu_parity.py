@@ -151,6 +151,12 @@ def test_monarch_cfg3(dev):
     assert_quant_parity(make_config(3), dev)
 
 
+def test_monarch_single_factor_cfg5(dev):
+    """Config 5: the reference's single-factor Monarch (nb = 8, blksz 64) with
+    int8 hidden quant, on the block-local kernel."""
+    assert_quant_parity(make_config(5), dev)
+
+
 # ---- butterfly ----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("shape", [(8, 4, 256), (8, 5, 512), (8, 3, 1024), (6, 4, 1000), (5, 3, 12),
