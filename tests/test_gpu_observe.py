@@ -266,3 +266,64 @@ def test_layer_calibrate_freeze_and_fast_forward(dev):
 
 def F_linear(x, W, b):
     return torch.nn.functional.linear(x, W, b)
+
+
+@pytest.mark.parametrize("modes", [("min_max", None), (None, "min_max"), ("frozen", "dynamic"), ("dynamic", "frozen")])
+def test_observe_mixed_modes(dev, modes):
+    """Each hidden quantizer in its own mode (or absent): the scales each step
+    used and the statistics follow the oracle on the kernel's own trajectory."""
+    cfg = _cfg(1)
+    qs, sts = [], []
+    for m in modes:
+        if m is None:
+            qs.append(None)
+            sts.append(O.ObserverState("off"))
+        elif m == "frozen":
+            q = _quant("frozen", True)
+            q.scale = torch.tensor(0.004)
+            qs.append(q.to(dev))
+            sts.append(O.ObserverState("frozen", scale=0.004))
+        else:
+            qs.append(_quant(m, True).to(dev))
+            sts.append(O.ObserverState(m))
+    out, trace = _run(cfg, dev, qs[0], qs[1])
+    out, trace = out.cpu(), trace.cpu()
+    pre, sc = _teacher_forced(cfg, out, sts[0], sts[1])
+    assert torch.equal(trace[:, 0], sc[:, 0]) and torch.equal(trace[:, 1], sc[:, 1])
+    assert torch.allclose(trace[:, 2], sc[:, 2], rtol=1e-5, atol=0)
+    for t in range(out.shape[0]):
+        if modes[1] is None:
+            assert (out[t] - pre[t]).abs().max().item() <= 1e-5
+        else:
+            _codes_match(out[t], pre[t], float(trace[t, 2]), float(trace[t, 3]), -127, 127)
+    for q, st in zip(qs, sts):
+        if q is not None and q.config.mode == "min_max":
+            got = q.observer_stats.cpu()[:2]
+            want = torch.stack([st.running_min, st.running_max])
+            assert torch.allclose(got, want, rtol=1e-5, atol=1e-7)
+
+
+def test_observe_tensor_reports_the_applied_scale(dev):
+    """gs_observe_tensor's `used` output holds the (scale, zero point) it applied."""
+    import ctypes
+
+    from gru_qat_amd import _lib
+
+    x = (torch.randn(9, 17, generator=torch.Generator().manual_seed(4)) * 0.3 - 0.1).to(dev)
+    q = _quant("dynamic", False).to(dev)
+    y = torch.empty_like(x)
+    used = torch.zeros(2, device=dev)
+    a = _lib.GsObserveTensorArgs()
+    a.x, a.y, a.used = x.data_ptr(), y.data_ptr(), used.data_ptr()
+    a.rows, a.cols, a.ld = 9, 17, 17
+    a.q = q.observer()
+    lib = _lib.load()
+    need = lib.gs_observe_tensor_scratch_bytes(ctypes.byref(a))
+    scratch = torch.empty(int(need), dtype=torch.uint8, device=dev)
+    a.scratch, a.scratch_bytes = scratch.data_ptr(), scratch.numel()
+    assert lib.gs_observe_tensor(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)) == 0
+    torch.cuda.synchronize(dev)
+    st = O.ObserverState("dynamic", symmetric=False)
+    ref, (s, zp) = O.observer_forward(st, x.cpu())
+    assert torch.equal(y.cpu(), ref)
+    assert used.cpu().tolist() == [s, zp]
