@@ -141,6 +141,18 @@ def test_monarch_quant(dev, two):
     assert_quant_parity(cfg, dev)
 
 
+# single factor: blksz 64 (block-local kernel) and 24 (MFMA kernel), each quantizer alone and both
+# with different scales (q_in then re-quantizes the carried h every step)
+@pytest.mark.parametrize("shape,nb", [((12, 6, 256), 4), ((12, 6, 96), 4)])
+@pytest.mark.parametrize("qin,qout", [(None, Q), (Q, None), (Q2, Q)])
+def test_monarch_single_quant_modes(dev, shape, nb, qin, qout):
+    cfg = _monarch(shape, nb, h_in_quant=qin, h_out_quant=qout)
+    if qout is None:
+        assert_fp32_parity(cfg, dev)
+    else:
+        assert_quant_parity(cfg, dev)
+
+
 def test_monarch_cfg3_single_factor_fp32(dev):
     cfg = make_config(3)
     cfg.update(w2=None, h_in_quant=None, h_out_quant=None)
