@@ -160,6 +160,22 @@ def test_observe_dynamic_teacher_forced(dev, idx, mode, symmetric):
         f"stats_in={stats_in.tolist()} stats_out={stats_out.tolist()}")
 
 
+@pytest.mark.parametrize("idx,shape", [(1, (1, 1, 8)), (3, (1, 2, 64)), (0, (2, 1, 5)), (4, (1, 1, 16))])
+def test_observe_tiny(dev, idx, shape):
+    """T = 1 (q_in sees only h0, no next-step q_in pass) and B = 1."""
+    cfg = _cfg(idx, shape)
+    q_in, q_out = _quant("min_max", True).to(dev), _quant("min_max", True).to(dev)
+    out, trace = _run(cfg, dev, q_in, q_out)
+    out, trace = out.cpu(), trace.cpu()
+    st_in, st_out = O.ObserverState("min_max"), O.ObserverState("min_max")
+    pre, sc = _teacher_forced(cfg, out, st_in, st_out)
+    assert torch.equal(trace[:, 0], sc[:, 0])
+    assert torch.allclose(trace[:, 2], sc[:, 2], rtol=1e-5)
+    for t in range(out.shape[0]):
+        _codes_match(out[t], pre[t], float(trace[t, 2]), 0.0, -127, 127)
+    assert torch.equal(q_in.observer_stats.cpu()[:2], torch.stack([st_in.running_min, st_in.running_max]))
+
+
 @pytest.mark.parametrize("idx", sorted(BIG))
 def test_observe_large_batch(dev, idx):
     """B H up to 64K elements (256 reduction partials, K-split GEMM)."""

@@ -96,7 +96,7 @@ def _monarch(shape, nb, two=False, seed=0, **over):
 # leave the last workgroup's rows partly empty), other block sizes the MFMA kernel of scan_dense.hip
 MONARCH_CASES = [((8, 4, 32), 4), ((16, 8, 64), 4), ((8, 32, 64), 4), ((16, 32, 256), 4), ((6, 3, 30), 5),
                  ((5, 4, 256), 2), ((4, 5, 8), 8), ((1, 4, 8), 2), ((7, 5, 64), 4), ((9, 3, 128), 4),
-                 ((3, 2, 1024), 16), ((4, 3, 192), 3)]
+                 ((3, 2, 1024), 16), ((4, 3, 192), 3), ((1, 1, 64), 4), ((2, 1, 512), 4)]
 
 
 @pytest.mark.parametrize("shape,nb", MONARCH_CASES)
