@@ -51,50 +51,48 @@ __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
   const float* gib = p.gi + (int64_t)b * p.sg_b + j;
   float* outb = p.out + (int64_t)b * p.so_b + j;
 
-  float cr[kDepth], cz[kDepth], cn[kDepth];
-#pragma unroll
-  for (int i = 0; i < kDepth; ++i) {
-    if (i < p.T) {
-      const float* g = gib + (int64_t)i * p.sg_t;
-      cr[i] = g[0];
-      cz[i] = g[H];
-      cn[i] = g[2 * H];
-    }
-  }
-
-  for (int t0 = 0; t0 < p.T; t0 += kDepth) {
-    float nr[kDepth], nz[kDepth], nn[kDepth];
+  // Two register sets of gi take turns: while one set's kDepth steps compute,
+  // the other set's loads are in flight. Loads past T are clamped to T - 1 and
+  // never branched around, so the compiler's wait before step i counts only
+  // the loads issued before that step's own (a conditional or copied prefetch
+  // made it wait for the whole next chunk at the first step of each chunk).
+  const int tl = p.T - 1;
+  auto load = [&](int t0, float* r, float* z, float* c) {
 #pragma unroll
     for (int i = 0; i < kDepth; ++i) {
-      const int t = t0 + kDepth + i;
-      if (t < p.T) {
-        const float* g = gib + (int64_t)t * p.sg_t;
-        nr[i] = g[0];
-        nz[i] = g[H];
-        nn[i] = g[2 * H];
-      }
+      const float* g = gib + (int64_t)min(t0 + i, tl) * p.sg_t;
+      r[i] = g[0];
+      z[i] = g[H];
+      c[i] = g[2 * H];
     }
+  };
+  // Runs steps t0 .. t0 + kDepth - 1; true once step T - 1 is done.
+  auto run = [&](int t0, const float* r, const float* z, const float* c) -> bool {
 #pragma unroll
     for (int i = 0; i < kDepth; ++i) {
       const int t = t0 + i;
-      if (t < p.T) {
-        float hq = h;
-        if (p.qin.on && (t == 0 || p.qin_after_first)) hq = fake_quant(h, p.qin);
-        const float ghr = mul_add_nofma(wr, hq, br);
-        const float ghz = mul_add_nofma(wz, hq, bz);
-        const float ghn = mul_add_nofma(wn, hq, bn);
-        float hn = gru_update(cr[i], cz[i], cn[i], ghr, ghz, ghn, h);
-        if (p.qout.on) hn = fake_quant(hn, p.qout);
-        outb[(int64_t)t * p.so_t] = hn;
-        h = hn;
-      }
+      if (t >= p.T) return true;
+      float hq = h;
+      if (p.qin.on && (t == 0 || p.qin_after_first)) hq = fake_quant(h, p.qin);
+      const float ghr = mul_add_nofma(wr, hq, br);
+      const float ghz = mul_add_nofma(wz, hq, bz);
+      const float ghn = mul_add_nofma(wn, hq, bn);
+      float hn = gru_update(r[i], z[i], c[i], ghr, ghz, ghn, h);
+      if (p.qout.on) hn = fake_quant(hn, p.qout);
+      outb[(int64_t)t * p.so_t] = hn;
+      h = hn;
     }
-#pragma unroll
-    for (int i = 0; i < kDepth; ++i) {
-      cr[i] = nr[i];
-      cz[i] = nz[i];
-      cn[i] = nn[i];
-    }
+    return t0 + kDepth >= p.T;
+  };
+
+  float ar[kDepth], az[kDepth], an[kDepth];
+  float xr[kDepth], xz[kDepth], xn[kDepth];
+  load(0, ar, az, an);
+  for (int t0 = 0;; t0 += 2 * kDepth) {
+    load(t0 + kDepth, xr, xz, xn);
+    if (run(t0, ar, az, an)) return;
+    load(t0 + 2 * kDepth, ar, az, an);
+    if (run(t0 + kDepth, xr, xz, xn)) return;
   }
 }
 
@@ -140,70 +138,72 @@ __global__ __launch_bounds__(kBwdThreads) void diagonal_bwd_kernel(DiagBwdParams
   float* dgib = p.dgi + ((int64_t)b * 3 * H + j);
   const int64_t sd_t = (int64_t)p.B * H, sdg_t = (int64_t)p.B * 3 * H;
 
-  // step s of a chunk is t = t0 - s; loads of step t: gi[t], out[t-1] (h0 at 0), dout[t]
-  float cr[kBwdDepth], cz[kBwdDepth], cn[kBwdDepth], ch[kBwdDepth], cd[kBwdDepth];
-  auto load = [&](int t, float& gr, float& gz, float& gn, float& hp, float& dd) {
-    const float* g = gib + (int64_t)t * p.sg_t;
-    gr = g[0];
-    gz = g[H];
-    gn = g[2 * H];
-    hp = t > 0 ? outb[(int64_t)(t - 1) * p.so_t] : h0;
-    dd = doutb[(int64_t)t * sd_t];
-  };
+  // Step i of a chunk is t = t0 - i; its loads are gi[t], out[t-1] and
+  // dout[t], with t clamped to 0 (out[-1] is h0, selected at compute time). As
+  // in the forward, two register sets take turns and no load is branched
+  // around, so the wait before a step counts only the loads issued before its
+  // own.
+  auto load = [&](int t0, float* gr, float* gz, float* gn, float* hp, float* dd) {
 #pragma unroll
-  for (int i = 0; i < kBwdDepth; ++i)
-    if (p.T - 1 - i >= 0) load(p.T - 1 - i, cr[i], cz[i], cn[i], ch[i], cd[i]);
+    for (int i = 0; i < kBwdDepth; ++i) {
+      const int t = max(t0 - i, 0);
+      const float* g = gib + (int64_t)t * p.sg_t;
+      gr[i] = g[0];
+      gz[i] = g[H];
+      gn[i] = g[2 * H];
+      hp[i] = outb[(int64_t)max(t - 1, 0) * p.so_t];
+      dd[i] = doutb[(int64_t)t * sd_t];
+    }
+  };
 
   float dh = 0.0f;
   float dwr = 0.f, dwz = 0.f, dwn = 0.f, dbr = 0.f, dbz = 0.f, dbn = 0.f;
-  for (int t0 = p.T - 1; t0 >= 0; t0 -= kBwdDepth) {
-    float nr[kBwdDepth], nz[kBwdDepth], nn[kBwdDepth], nh[kBwdDepth], nd[kBwdDepth];
-#pragma unroll
-    for (int i = 0; i < kBwdDepth; ++i) {
-      const int t = t0 - kBwdDepth - i;
-      if (t >= 0) load(t, nr[i], nz[i], nn[i], nh[i], nd[i]);
-    }
+  // Runs steps t0 down to t0 - kBwdDepth + 1; true once step 0 is done.
+  auto run = [&](int t0, const float* cr, const float* cz, const float* cn, const float* ch,
+                 const float* cd) -> bool {
 #pragma unroll
     for (int i = 0; i < kBwdDepth; ++i) {
       const int t = t0 - i;
-      if (t >= 0) {
-        const float h_prev = ch[i];
-        float hq = h_prev;
-        bool keep_in = true;
-        if (p.qin.on) {
-          keep_in = quant_keeps(h_prev, p.qin);
-          hq = fake_quant(h_prev, p.qin);
-        }
-        const float ghr = mul_add_nofma(wr, hq, br);
-        const float ghz = mul_add_nofma(wz, hq, bz);
-        const float ghn = mul_add_nofma(wn, hq, bn);
-        const GateGrad gg = gru_backward(cr[i], cz[i], cn[i], ghr, ghz, ghn, h_prev, cd[i] + dh, p.qout);
-        float* dg = dgib + (int64_t)t * sdg_t;
-        dg[0] = gg.dgr;
-        dg[H] = gg.dgz;
-        dg[2 * H] = gg.dgn;
-        {
+      if (t < 0) return true;
+      const float h_prev = t > 0 ? ch[i] : h0;
+      float hq = h_prev;
+      bool keep_in = true;
+      if (p.qin.on) {
+        keep_in = quant_keeps(h_prev, p.qin);
+        hq = fake_quant(h_prev, p.qin);
+      }
+      const float ghr = mul_add_nofma(wr, hq, br);
+      const float ghz = mul_add_nofma(wz, hq, bz);
+      const float ghn = mul_add_nofma(wn, hq, bn);
+      const GateGrad gg = gru_backward(cr[i], cz[i], cn[i], ghr, ghz, ghn, h_prev, cd[i] + dh, p.qout);
+      float* dg = dgib + (int64_t)t * sdg_t;
+      dg[0] = gg.dgr;
+      dg[H] = gg.dgz;
+      dg[2 * H] = gg.dgn;
+      {
 #pragma clang fp contract(off)
-          float via = gg.dgr * wr + gg.dgz * wz + gg.dghn * wn;
-          if (!keep_in) via = 0.0f;
-          dh = gg.dh_direct + via;
-          dwr += gg.dgr * hq;
-          dwz += gg.dgz * hq;
-          dwn += gg.dghn * hq;
-          dbr += gg.dgr;
-          dbz += gg.dgz;
-          dbn += gg.dghn;
-        }
+        float via = gg.dgr * wr + gg.dgz * wz + gg.dghn * wn;
+        if (!keep_in) via = 0.0f;
+        dh = gg.dh_direct + via;
+        dwr += gg.dgr * hq;
+        dwz += gg.dgz * hq;
+        dwn += gg.dghn * hq;
+        dbr += gg.dgr;
+        dbz += gg.dgz;
+        dbn += gg.dghn;
       }
     }
-#pragma unroll
-    for (int i = 0; i < kBwdDepth; ++i) {
-      cr[i] = nr[i];
-      cz[i] = nz[i];
-      cn[i] = nn[i];
-      ch[i] = nh[i];
-      cd[i] = nd[i];
-    }
+    return t0 - kBwdDepth < 0;
+  };
+
+  float ar[kBwdDepth], az[kBwdDepth], an[kBwdDepth], ah[kBwdDepth], ad[kBwdDepth];
+  float xr[kBwdDepth], xz[kBwdDepth], xn[kBwdDepth], xh[kBwdDepth], xd[kBwdDepth];
+  load(p.T - 1, ar, az, an, ah, ad);
+  for (int t0 = p.T - 1;; t0 -= 2 * kBwdDepth) {
+    load(t0 - kBwdDepth, xr, xz, xn, xh, xd);
+    if (run(t0, ar, az, an, ah, ad)) break;
+    load(t0 - 2 * kBwdDepth, ar, az, an, ah, ad);
+    if (run(t0 - kBwdDepth, xr, xz, xn, xh, xd)) break;
   }
   p.dh0[(int64_t)b * H + j] = dh;
   float* dwp = p.dw_part + (int64_t)b * 3 * H + j;

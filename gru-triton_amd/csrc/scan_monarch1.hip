@@ -75,67 +75,69 @@ __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FPara
   float h = live ? p.h0[(int64_t)b * p.sh0_b + col] : 0.0f;
   if (kq == 0) hs[0][rs][u] = p.qin.on ? fake_quant(h, p.qin) : h;
 
+  // Rows past B read row 0 and never store; loads past T are clamped to
+  // T - 1. Two register sets of gi take turns (one set's kDepth steps compute
+  // while the other's loads are in flight) and no load is branched around, so
+  // the wait before step i counts only the loads issued before its own.
   const float* gib = p.gi + (int64_t)(live ? b : 0) * p.sg_b + col;
   float* outb = p.out + (int64_t)(live ? b : 0) * p.so_b + col;
-  auto load = [&](int t, float& r, float& z, float& c) {
-    if (live && t < T) {
-      const float* g = gib + (int64_t)t * p.sg_t;
-      r = g[0];
-      z = g[H];
-      c = g[2 * H];
-    } else {
-      r = z = c = 0.0f;
+  const int tl = T - 1;
+  auto load = [&](int t0, float* r, float* z, float* c) {
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      const float* g = gib + (int64_t)min(t0 + i, tl) * p.sg_t;
+      r[i] = g[0];
+      z[i] = g[H];
+      c[i] = g[2 * H];
     }
   };
-  float cr[kDepth], cz[kDepth], cn[kDepth];
-#pragma unroll
-  for (int i = 0; i < kDepth; ++i) load(i, cr[i], cz[i], cn[i]);
-  __syncthreads();
-
   int buf = 0;
-  for (int t0 = 0; t0 < T; t0 += kDepth) {
-    float nr[kDepth], nz[kDepth], nn[kDepth];
-#pragma unroll
-    for (int i = 0; i < kDepth; ++i) load(t0 + kDepth + i, nr[i], nz[i], nn[i]);
+  // Runs steps t0 .. t0 + kDepth - 1; true once step T - 1 is done.
+  auto run = [&](int t0, const float* cr, const float* cz, const float* cn) -> bool {
 #pragma unroll
     for (int i = 0; i < kDepth; ++i) {
       const int t = t0 + i;
-      if (t < T) {
-        const float* src = &hs[buf][rs][kq * KT];
-        f4 a[3];
+      if (t >= T) return true;
+      const float* src = &hs[buf][rs][kq * KT];
+      f4 a[3];
 #pragma unroll
-        for (int g = 0; g < 3; ++g) a[g] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int g = 0; g < 3; ++g) a[g] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < KT; q += 4) {
-          const f4 v = *reinterpret_cast<const f4*>(src + q);
+      for (int q = 0; q < KT; q += 4) {
+        const f4 v = *reinterpret_cast<const f4*>(src + q);
 #pragma unroll
-          for (int g = 0; g < 3; ++g)
+        for (int g = 0; g < 3; ++g)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) a[g][c] += v[c] * wr[g][q + c];
-        }
-        float gh[3];
-#pragma unroll
-        for (int g = 0; g < 3; ++g) {
-          float s = (a[g][0] + a[g][1]) + (a[g][2] + a[g][3]);
-          s += lane_xor_c<1>(s);
-          s += lane_xor_c<2>(s);
-          gh[g] = s;
-        }
-        float hn = gru_update(cr[i], cz[i], cn[i], gh[0] + br, gh[1] + bz, gh[2] + bn, h);
-        if (p.qout.on) hn = fake_quant(hn, p.qout);
-        if (live && kq == 0) outb[(int64_t)t * p.so_t] = hn;
-        if (kq == 0) hs[buf ^ 1][rs][u] = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
-        h = hn;
-        lds_barrier();  // LDS only: the out stores need not complete here
-        buf ^= 1;
+          for (int c = 0; c < 4; ++c) a[g][c] += v[c] * wr[g][q + c];
       }
-    }
+      float gh[3];
 #pragma unroll
-    for (int i = 0; i < kDepth; ++i) {
-      cr[i] = nr[i];
-      cz[i] = nz[i];
-      cn[i] = nn[i];
+      for (int g = 0; g < 3; ++g) {
+        float s = (a[g][0] + a[g][1]) + (a[g][2] + a[g][3]);
+        s += lane_xor_c<1>(s);
+        s += lane_xor_c<2>(s);
+        gh[g] = s;
+      }
+      float hn = gru_update(cr[i], cz[i], cn[i], gh[0] + br, gh[1] + bz, gh[2] + bn, h);
+      if (p.qout.on) hn = fake_quant(hn, p.qout);
+      if (live && kq == 0) outb[(int64_t)t * p.so_t] = hn;
+      if (kq == 0) hs[buf ^ 1][rs][u] = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
+      h = hn;
+      lds_barrier();  // LDS only: the out stores need not complete here
+      buf ^= 1;
     }
+    return t0 + kDepth >= T;
+  };
+
+  float ar[kDepth], az[kDepth], an[kDepth];
+  float xr[kDepth], xz[kDepth], xn[kDepth];
+  load(0, ar, az, an);
+  __syncthreads();
+  for (int t0 = 0;; t0 += 2 * kDepth) {
+    load(t0 + kDepth, xr, xz, xn);
+    if (run(t0, ar, az, an)) return;
+    load(t0 + 2 * kDepth, ar, az, an);
+    if (run(t0 + kDepth, xr, xz, xn)) return;
   }
 }
 

@@ -98,15 +98,20 @@ __global__ __launch_bounds__(m1_threads<BS>()) void monarch1_bwd_kernel(M1Params
     wt[i] = p.w[(((int64_t)g * p.nb + n) * BS + j) * BS + u];
   }
 
-  // Per-step inputs of the iteration that consumes D_t: Zm_t, Mi_t, dout[t-1], C_kq[t-1].
-  auto load = [&](int t, float& zm, float& mi, float& dn, float& cc) {
-    if (live && t >= 0) {
-      zm = p.zm[(int64_t)t * BH + e0];
-      mi = p.mi[(int64_t)t * BH + e0];
-      dn = t > 0 ? p.dout[(int64_t)(t - 1) * BH + e0] : 0.0f;
-      cc = (t > 0 && kq < 3) ? p.cg[(int64_t)(t - 1) * 3 * BH + c0] : 0.0f;
-    } else {
-      zm = mi = dn = cc = 0.0f;
+  // Per-step inputs of the iteration that consumes D_t: Zm_t, Mi_t, dout[t-1],
+  // C_kq[t-1]. Rows past B read row 0 and t is clamped to 0, so no load is
+  // branched around; the values a step must not use (dead rows, t = 0, parts
+  // kq = 3) are zeroed when the step reads them. Two register sets take turns
+  // (one set's kDepth steps compute while the other's loads are in flight), so
+  // the wait before a step counts only the loads issued before its own.
+  auto load = [&](int t0, float* zm, float* mi, float* dn, float* cc) {
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      const int t = max(t0 - i, 0), tp = max(t0 - i - 1, 0);
+      zm[i] = p.zm[(int64_t)t * BH + e0];
+      mi[i] = p.mi[(int64_t)t * BH + e0];
+      dn[i] = p.dout[(int64_t)tp * BH + e0];
+      cc[i] = p.cg[(int64_t)tp * 3 * BH + c0];
     }
   };
 
@@ -115,55 +120,53 @@ __global__ __launch_bounds__(m1_threads<BS>()) void monarch1_bwd_kernel(M1Params
   if (live && kq == 0) p.dsum[(int64_t)(T - 1) * BH + e0] = D;
   if (kq < 3) dgh[0][rs][kq * BS + u] = live ? D * p.cg[(int64_t)(T - 1) * 3 * BH + c0] : 0.0f;
 
-  float czm[kDepth], cmi[kDepth], cdn[kDepth], ccc[kDepth];
-#pragma unroll
-  for (int i = 0; i < kDepth; ++i) load(T - 1 - i, czm[i], cmi[i], cdn[i], ccc[i]);
-  __syncthreads();
-
   int buf = 0;
-  for (int t0 = T - 1; t0 >= 0; t0 -= kDepth) {
-    float nzm[kDepth], nmi[kDepth], ndn[kDepth], ncc[kDepth];
-#pragma unroll
-    for (int i = 0; i < kDepth; ++i) load(t0 - kDepth - i, nzm[i], nmi[i], ndn[i], ncc[i]);
+  // Runs steps t0 down to t0 - kDepth + 1; true once step 0 is done.
+  auto run = [&](int t0, const float* czm, const float* cmi, const float* cdn, const float* ccc) -> bool {
 #pragma unroll
     for (int i = 0; i < kDepth; ++i) {
       const int t = t0 - i;
-      if (t >= 0) {
-        const float* src = &dgh[buf][rs][kq * KT];
-        f4 a4 = f4{0.f, 0.f, 0.f, 0.f};
+      if (t < 0) return true;
+      const float* src = &dgh[buf][rs][kq * KT];
+      f4 a4 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < KT; q += 4) {
-          const f4 v = *reinterpret_cast<const f4*>(src + q);
+      for (int q = 0; q < KT; q += 4) {
+        const f4 v = *reinterpret_cast<const f4*>(src + q);
 #pragma unroll
-          for (int c = 0; c < 4; ++c) a4[c] += v[c] * wt[q + c];
-        }
-        float acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
-        acc += lane_xor_c<1>(acc);
-        acc += lane_xor_c<2>(acc);
-        float carry;
-        {
-#pragma clang fp contract(off)
-          carry = czm[i] * D + cmi[i] * acc;
-        }
-        if (t == 0) {
-          if (live && kq == 0) p.dh0[e0] = carry;
-        } else {
-          D = cdn[i] + carry;
-          if (live && kq == 0) p.dsum[(int64_t)(t - 1) * BH + e0] = D;
-          if (kq < 3) dgh[buf ^ 1][rs][kq * BS + u] = D * ccc[i];
-        }
-        // LDS-only barrier: the step's global stores need not complete here
-        lds_barrier();
-        buf ^= 1;
+        for (int c = 0; c < 4; ++c) a4[c] += v[c] * wt[q + c];
       }
+      float acc = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+      acc += lane_xor_c<1>(acc);
+      acc += lane_xor_c<2>(acc);
+      const float zm = live ? czm[i] : 0.0f, mi = live ? cmi[i] : 0.0f;
+      float carry;
+      {
+#pragma clang fp contract(off)
+        carry = zm * D + mi * acc;
+      }
+      if (t == 0) {
+        if (live && kq == 0) p.dh0[e0] = carry;
+      } else {
+        D = (live ? cdn[i] : 0.0f) + carry;
+        if (live && kq == 0) p.dsum[(int64_t)(t - 1) * BH + e0] = D;
+        if (kq < 3) dgh[buf ^ 1][rs][kq * BS + u] = D * (live ? ccc[i] : 0.0f);
+      }
+      // LDS-only barrier: the step's global stores need not complete here
+      lds_barrier();
+      buf ^= 1;
     }
-#pragma unroll
-    for (int i = 0; i < kDepth; ++i) {
-      czm[i] = nzm[i];
-      cmi[i] = nmi[i];
-      cdn[i] = ndn[i];
-      ccc[i] = ncc[i];
-    }
+    return t0 - kDepth < 0;
+  };
+
+  float azm[kDepth], ami[kDepth], adn[kDepth], acc_[kDepth];
+  float xzm[kDepth], xmi[kDepth], xdn[kDepth], xcc[kDepth];
+  load(T - 1, azm, ami, adn, acc_);
+  __syncthreads();
+  for (int t0 = T - 1;; t0 -= 2 * kDepth) {
+    load(t0 - kDepth, xzm, xmi, xdn, xcc);
+    if (run(t0, azm, ami, adn, acc_)) return;
+    load(t0 - 2 * kDepth, azm, ami, adn, acc_);
+    if (run(t0 - kDepth, xzm, xmi, xdn, xcc)) return;
   }
 }
 
