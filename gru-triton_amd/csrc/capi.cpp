@@ -24,8 +24,10 @@ void clear_error() { g_error.clear(); }
 
 int validate_quant(const gs_quant& q, const char* name, const char* who) {
   if (!q.enabled) return GS_OK;
-  if (!(std::isfinite(q.scale) && q.scale > 0.0f))
-    return set_error(GS_ERR_INVALID, "%s: %s scale must be finite and > 0; got %g", who, name,
+  // [2^-126, 2^64]: the kernels' division-free quotient needs 1 / scale normal
+  // and code * scale finite (gs_device.h quant_code)
+  if (!(std::isfinite(q.scale) && q.scale >= 0x1p-126f && q.scale <= 0x1p64f))
+    return set_error(GS_ERR_INVALID, "%s: %s scale must be in [2^-126, 2^64]; got %g", who, name,
                      (double)q.scale);
   if (q.qmin > q.qmax)
     return set_error(GS_ERR_INVALID, "%s: %s qmin (%d) must be <= qmax (%d)", who, name, q.qmin,

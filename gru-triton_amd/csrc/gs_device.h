@@ -7,8 +7,8 @@
 // contraction is off in the gate epilogue). sigmoid and tanh use the hardware
 // base-2 exponential and reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each);
 // their deviation from torch's CPU functions is a few 1e-8 absolute, far inside
-// the 1e-5 parity bar, and the fake-quant division stays IEEE so integer codes
-// depend only on the pre-quant value.
+// the 1e-5 parity bar, and the fake-quant code is that of the IEEE quotient so
+// integer codes depend only on the pre-quant value.
 #pragma once
 
 #include <type_traits>
@@ -20,19 +20,37 @@ namespace gs {
 
 // Frozen per-tensor symmetric fake-quant (reference src/gru_qat/ste.py:65-95 with
 // zero_point 0, and the in-kernel form at triton_kernels/scan.py:136-139):
-// q = clamp(rint(x / s), qmin, qmax) * s. The division is IEEE (HIP's default
-// fp32 '/' is correctly rounded) and rint rounds half to even, so for a given
-// fp32 x the integer code equals torch.round(x / s) exactly.
+// q = clamp(rint(x / s), qmin, qmax) * s, where x / s is the IEEE quotient and
+// rint rounds half to even, so for a given fp32 x the integer code equals
+// torch.round(x / s) exactly. `inv` is the fp32 rounding of 1 / s.
 struct Quant {
   float scale;
   float qmin;
   float qmax;
   int on;
+  float inv;
 };
 
+// rint(x / s) of the IEEE quotient, without the division sequence. With
+// inv = fl(1 / s) (within half an ulp of 1 / s) and q0 = fl(x inv) (within one
+// ulp of x / s), the residual r = x - q0 s is exact under an fma and
+// fl(q0 + r inv) is the correctly rounded quotient (Markstein's final
+// correction step, P. Markstein, IBM J. Res. Dev. 34(1), 1990). q0 is first
+// clamped to [-2^24, 2^24], beyond which every code clamps to qmin or qmax
+// anyway, so that infinite quotients leave no inf - inf. The host keeps s in
+// [2^-126, 2^64] (inv stays normal and q0 s finite). The fake-quant result is
+// then bit for bit that of clamp(rint(x / s)) s, NaN and infinities included;
+// tests/test_quant_quotient.py checks the steps against the IEEE division on
+// the CPU over sampled fp32 inputs, scales and code ranges.
+__device__ __forceinline__ float quant_code(float x, const Quant& q) {
+  float q0 = x * q.inv;
+  q0 = __builtin_fminf(__builtin_fmaxf(q0, -0x1p24f), 0x1p24f);
+  const float r = __builtin_fmaf(-q0, q.scale, x);
+  return __builtin_rintf(__builtin_fmaf(r, q.inv, q0));
+}
+
 __device__ __forceinline__ float fake_quant(float x, const Quant& q) {
-  float v = __builtin_rintf(x / q.scale);
-  v = __builtin_fminf(__builtin_fmaxf(v, q.qmin), q.qmax);
+  const float v = __builtin_fminf(__builtin_fmaxf(quant_code(x, q), q.qmin), q.qmax);
   return v * q.scale;
 }
 
@@ -74,7 +92,7 @@ struct GateGrad {
 };
 
 __device__ __forceinline__ bool quant_keeps(float x, const Quant& q) {
-  const float v = __builtin_rintf(x / q.scale);
+  const float v = quant_code(x, q);
   return v >= q.qmin && v <= q.qmax;
 }
 

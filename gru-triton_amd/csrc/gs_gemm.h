@@ -25,8 +25,8 @@ struct GemmArgs {
   const float* bias = nullptr;  // [N] added once (by split 0), or null
   int M = 0, N = 0, K = 0, ksplit = 1;
   int layout = kGemmNT;                 // GemmLayout
-  Quant qa{1.0f, 0.0f, 0.0f, 0};         // applied to A on load when qa.on
-  Quant qb{1.0f, 0.0f, 0.0f, 0};         // applied to B on load when qb.on
+  Quant qa{1.0f, 0.0f, 0.0f, 0, 1.0f};   // applied to A on load when qa.on
+  Quant qb{1.0f, 0.0f, 0.0f, 0, 1.0f};   // applied to B on load when qb.on
   // Batched products: product z < batch uses a + (z % a_mod) a_bs,
   // b + (z % b_mod) b_bs, c + z c_bs and bias + z bias_bs (splits of
   // product z still step by split_stride from there).

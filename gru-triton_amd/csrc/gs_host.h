@@ -44,7 +44,7 @@ inline Ctrl ctrl_of(void* ws) {
 }
 
 inline Quant to_quant(const gs_quant& q) {
-  return Quant{q.scale, (float)q.qmin, (float)q.qmax, q.enabled != 0};
+  return Quant{q.scale, (float)q.qmin, (float)q.qmax, q.enabled != 0, 1.0f / q.scale};
 }
 
 // The two quantizers are the same map when both are on with equal parameters.

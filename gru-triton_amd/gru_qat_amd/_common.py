@@ -63,8 +63,9 @@ def check_quant(q: QuantTuple, name: str) -> QuantTuple:
     except (TypeError, ValueError):
         raise ValueError(f"{name} must be None or a (scale, qmin, qmax) tuple; got {q!r}") from None
     scale = float(scale)
-    if not (scale > 0.0 and scale != float("inf")):
-        raise ValueError(f"{name} scale must be finite and > 0; got {scale}")
+    # the kernels' division-free quotient needs 1 / scale normal and code * scale finite
+    if not (2.0 ** -126 <= scale <= 2.0 ** 64):
+        raise ValueError(f"{name} scale must be in [2^-126, 2^64]; got {scale}")
     if int(qmin) > int(qmax):
         raise ValueError(f"{name} qmin must be <= qmax; got {qmin} > {qmax}")
     return (scale, int(qmin), int(qmax))

@@ -69,7 +69,8 @@ extern "C" {
 #define GS_KIND_BUTTERFLY 3
 
 /* Frozen per-tensor symmetric fake-quant: q = clamp(rint(x / scale), qmin, qmax) * scale,
- * with IEEE division and round-half-to-even. enabled == 0 turns it off. */
+ * with the IEEE quotient and round-half-to-even. enabled == 0 turns it off. When
+ * enabled, scale must lie in [2^-126, 2^64] (GS_ERR_INVALID otherwise). */
 typedef struct gs_quant {
   int32_t enabled;
   float scale;

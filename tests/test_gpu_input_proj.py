@@ -54,3 +54,45 @@ def test_input_projection_forward_and_backward(dev, lead, I, N, xq, wq, bias):
         e = (a.cpu() - r).abs().max().item()
         print(f"[proj]   {name}: max err {e:.3e} (|ref| {r.abs().max().item():.3e})")
         assert e <= 1e-4 * max(1.0, r.abs().max().item()), name
+
+
+QUOTIENT_SCALES = [1.0 / 127.0, 1.0 / 255.0, 0.02, 3.0, 1e-8, 2.0 ** -126, 2.0 ** 64, 0.0123456]
+
+
+@pytest.mark.parametrize("s", QUOTIENT_SCALES)
+def test_fake_quant_codes_at_rounding_boundaries(dev, s):
+    """q_x(x) from the kernel's division-free quotient equals torch's
+    clamp(round(x / s)) * s bit for bit, on values within a few ulps of every
+    rounding boundary (k + 1/2) s and of every k s, random values over many
+    binades, zeros, subnormals, infinities and NaN. The CPU restatement of the
+    same steps is pinned in test_quant_quotient.py."""
+    from gru_qat_amd.input_proj import _project
+
+    f32 = torch.float32
+    s32 = torch.tensor(s, dtype=f32)
+    k = torch.arange(-130, 131, dtype=torch.float64)
+    base = torch.cat([((k + 0.5) * float(s32)).to(f32), (k * float(s32)).to(f32)])
+    vals = [base]
+    up, dn = base, base
+    for _ in range(3):
+        up = torch.nextafter(up, torch.full_like(up, float("inf")))
+        dn = torch.nextafter(dn, torch.full_like(dn, float("-inf")))
+        vals += [up, dn]
+    g = torch.Generator().manual_seed(5)
+    vals.append((torch.randn(2000, generator=g, dtype=torch.float64) * float(s32)
+                 * 10.0 ** (torch.rand(2000, generator=g, dtype=torch.float64) * 9 - 3)).to(f32))
+    vals.append(torch.tensor([0.0, -0.0, 2.0 ** -149, -(2.0 ** -149), float("inf"), float("-inf"),
+                              float("nan"), 3.4e38, -3.4e38], dtype=f32))
+    x = torch.cat(vals)
+    x = torch.cat([x, torch.zeros((-x.numel()) % 64, dtype=f32)]).view(-1, 64)
+    W = torch.zeros(8, 64)
+    for qmin, qmax in ((-127, 127), (-8, 7)):
+        _, _, _, xq = _project(x.to(dev), W.to(dev), None, (s, qmin, qmax), None)
+        ref = torch.clamp(torch.round(x / s32), qmin, qmax) * s32
+        # NaN: fmaxf/fminf return the other operand, so NaN clamps to qmin, as in the
+        # reference kernel's tl.minimum(tl.maximum(q, qmin), qmax) (scan.py:136-139)
+        ref = torch.where(torch.isnan(x), torch.tensor(qmin * float(s32), dtype=f32), ref)
+        got = xq.cpu()
+        bad = ~((got == ref) | (torch.isnan(got) & torch.isnan(ref)))
+        print(f"[proj] quotient s={s:.3g} range=({qmin},{qmax}): {x.numel()} values, {int(bad.sum())} differ")
+        assert not bad.any(), (x[bad][:4], got[bad][:4], ref[bad][:4])
