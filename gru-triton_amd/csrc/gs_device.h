@@ -2,9 +2,11 @@
 //
 // Numerics follow the reference PyTorch cell (LarocheC/gru-triton
 // src/gru_qat/gru_cell.py:437-464): r = sigmoid(gi_r + gh_r),
-// z = sigmoid(gi_z + gh_z), n = tanh(gi_n + r * gh_n), h' = (1 - z) * n + z * h,
-// evaluated in that order as separately rounded fp32 operations (FMA
-// contraction is off in the gate epilogue). sigmoid and tanh use the hardware
+// z = sigmoid(gi_z + gh_z), n = tanh(gi_n + r * gh_n), h' = (1 - z) * n + z * h.
+// gru_update and gru_backward evaluate it in that order as separately rounded
+// fp32 operations (FMA contraction off); the forward scans use gru_update_l2,
+// the same math with the exp2 arguments fused into single fmas to shorten the
+// step's dependent chain. sigmoid and tanh use the hardware
 // base-2 exponential and reciprocal (v_exp_f32, v_rcp_f32, about 1 ulp each);
 // their deviation from torch's CPU functions is a few 1e-8 absolute, far inside
 // the 1e-5 parity bar, and the fake-quant code is that of the IEEE quotient so
@@ -79,6 +81,39 @@ __device__ __forceinline__ float gru_update(float gir, float giz, float gin, flo
   const float z = sigmoid(giz + ghz);
   const float n = tanh_fast(gin + r * ghn);
   return (1.0f - z) * n + z * h;
+}
+
+// The same gate epilogue with every exp2 argument formed by one fma on the
+// recurrence chain (11 dependent ops from h instead of 17). The caller passes
+// the pre-activations already scaled by the base-2 exponent factors:
+//   ar = -log2e (gi_r + gh_r),  az = -log2e (gi_z + gh_z),
+//   gn2 = 2 log2e gh_n,  an2 = 2 log2e gi_n,
+// and gets h' = n + z (h - n) with r = 1 / (1 + 2^ar), z = 1 / (1 + 2^az),
+// n = 1 - 2 / (1 + 2^(r gn2 + an2)). The scalings and the fused products round
+// differently from gru_update (a few 1e-8 absolute on r, z and n); both
+// saturate the same way.
+__device__ __forceinline__ float gru_update_l2(float ar, float az, float gn2, float an2, float h) {
+  const float r = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(ar));
+  const float z = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(az));
+  const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(r, gn2, an2));
+  const float n = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f);
+  return __builtin_fmaf(z, h - n, n);
+}
+
+// Scale factors of gru_update_l2's arguments: -log2e for the r and z gates,
+// 2 log2e for the n gate.
+constexpr float kScaleRZ = -kLog2e;
+constexpr float kScaleN = 2.0f * kLog2e;
+__device__ __forceinline__ float gate_scale(int g) { return g == 2 ? kScaleN : kScaleRZ; }
+
+// gru_update_l2 on the unscaled gate inputs gi*, hidden products gh* (bias not
+// added) and the biases pre-scaled by gate_scale (bs*). The gi terms do not
+// depend on the state, so only the three outer fmas sit on the step's chain.
+__device__ __forceinline__ float gru_update_gb(float gir, float giz, float gin, float ghr, float ghz, float ghn,
+                                               float bsr, float bsz, float bsn, float h) {
+  return gru_update_l2(__builtin_fmaf(kScaleRZ, ghr, __builtin_fmaf(kScaleRZ, gir, bsr)),
+                       __builtin_fmaf(kScaleRZ, ghz, __builtin_fmaf(kScaleRZ, giz, bsz)),
+                       __builtin_fmaf(kScaleN, ghn, bsn), kScaleN * gin, h);
 }
 
 // Backward of one GRU step (reference src/gru_qat/triton_kernels/scan.py:1498-1540):

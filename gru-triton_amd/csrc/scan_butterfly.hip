@@ -93,10 +93,8 @@ __global__ __launch_bounds__(kGenericThreads) void butterfly_generic_kernel(BPar
       float hq = 0.0f;
       if (i < H) {
         const float* g = p.gi + (int64_t)t * p.sg_t + (int64_t)b * p.sg_b + i;
-        const float ghr = cur[i] + p.bh[i];
-        const float ghz = cur[N + i] + p.bh[H + i];
-        const float ghn = cur[2 * N + i] + p.bh[2 * H + i];
-        float hn = gru_update(g[0], g[H], g[2 * H], ghr, ghz, ghn, hraw[i]);
+        float hn = gru_update_gb(g[0], g[H], g[2 * H], cur[i], cur[N + i], cur[2 * N + i], kScaleRZ * p.bh[i],
+                                 kScaleRZ * p.bh[H + i], kScaleN * p.bh[2 * H + i], hraw[i]);
         if (p.qout.on) hn = fake_quant(hn, p.qout);
         p.out[(int64_t)t * p.so_t + (int64_t)b * p.so_b + i] = hn;
         hraw[i] = hn;
@@ -168,7 +166,7 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
     hraw[r] = h;
     x[r] = (i < H && p.qin.on) ? fake_quant(h, p.qin) : h;
 #pragma unroll
-    for (int q = 0; q < 3; ++q) bias[q][r] = (i < H) ? p.bh[q * H + i] : 0.0f;
+    for (int q = 0; q < 3; ++q) bias[q][r] = (i < H) ? gate_scale(q) * p.bh[q * H + i] : 0.0f;  // for gru_update_gb
   }
 
   for (int t = 0; t < p.T; ++t) {
@@ -223,10 +221,8 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = idx[r];
-        const float ghr = x[r] + bias[0][r];
-        const float ghz = ghs[1][i] + bias[1][r];
-        const float ghn = ghs[2][i] + bias[2][r];
-        float hn = gru_update(gir[r], giz[r], gin[r], ghr, ghz, ghn, hraw[r]);
+        float hn = gru_update_gb(gir[r], giz[r], gin[r], x[r], ghs[1][i], ghs[2][i], bias[0][r], bias[1][r],
+                                 bias[2][r], hraw[r]);
         if (p.qout.on) hn = fake_quant(hn, p.qout);
         float hq = 0.0f;
         if (i < H) {

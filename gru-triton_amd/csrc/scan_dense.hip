@@ -132,9 +132,11 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   if (!poller) {
     float wr[3][KC];
     load_w<KC>(p.w, p.nb, p.bs, blk_g, o0, j, kb4, quad_ok, wr);
+    // biases pre-scaled for gru_update_l2 (-log2e for r and z, 2 log2e for n)
+    constexpr float kR = -kLog2e, kN = 2.0f * kLog2e;
     float bias[3];
 #pragma unroll
-    for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? p.bh[g * p.H + unit] : 0.0f;
+    for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? (g == 2 ? kN : kR) * p.bh[g * p.H + unit] : 0.0f;
     // lane parts of the out / exchange-word offsets (row = 4 rb + s)
     const int64_t lane_out = (int64_t)s * p.so_b + unit;
     const int64_t lane_xh = (int64_t)s * p.H + unit;
@@ -157,6 +159,8 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
         giz = g[p.H];
         gin = g[2 * p.H];
       }
+      // gate-input parts of the exp2 arguments, off the step's dependent chain
+      const float cr = __builtin_fmaf(kR, gir, bias[0]), cz = __builtin_fmaf(kR, giz, bias[1]), an2 = kN * gin;
       float* hkp = hk + (rbl * 4 + s) * U + 4 * wave + j;
       const float hprev = *hkp;
       float a[3][KC];
@@ -166,7 +170,8 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       float gh[3];
 #pragma unroll
       for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
-      float hn = gru_update(gir, giz, gin, gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
+      float hn = gru_update_l2(__builtin_fmaf(kR, gh[0], cr), __builtin_fmaf(kR, gh[1], cz),
+                               __builtin_fmaf(kN, gh[2], bias[2]), an2, hprev);
       if (p.qout.on) hn = fake_quant(hn, p.qout);
       if (mine) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = hn;
       const bool xcd_local = REMOTE && t >= 1 && __builtin_amdgcn_readfirstlane(flags[1]) != 0;

@@ -34,9 +34,12 @@ struct DiagParams {
   int64_t sg_t, sg_b, sh0_b, so_t, so_b;
   int T, B, H;
   Quant qin, qout;
-  int qin_after_first;  // 0: q_in is the identity on carried h for t >= 1
 };
 
+// QIN: 0 no q_in, 1 q_in on h0 only (q_in == q_out, so the carried state is
+// already on q_in's grid), 2 q_in every step. QOUT: q_out on. The modes are
+// template arguments so that the step holds no branch and no per-step test.
+template <int QIN, bool QOUT>
 __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
   const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (e >= (int64_t)p.B * p.H) return;
@@ -44,9 +47,13 @@ __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
   const int j = (int)(e - (int64_t)b * p.H);
   const int H = p.H;
 
-  const float wr = p.w[j], wz = p.w[H + j], wn = p.w[2 * H + j];
-  const float br = p.bh[j], bz = p.bh[H + j], bn = p.bh[2 * H + j];
+  // Weights and biases pre-scaled for gru_update_l2: the r and z arguments are
+  // fma(-log2e w, hq, -log2e (gi + b)), gh_n's is fma(2 log2e w_n, hq, 2 log2e b_n).
+  constexpr float kR = -kLog2e, kN = 2.0f * kLog2e;
+  const float wr = kR * p.w[j], wz = kR * p.w[H + j], wn = kN * p.w[2 * H + j];
+  const float br = kR * p.bh[j], bz = kR * p.bh[H + j], bn = kN * p.bh[2 * H + j];
   float h = p.h0[(int64_t)b * p.sh0_b + j];
+  float hq = QIN ? fake_quant(h, p.qin) : h;  // the matmul-side state of the next step
 
   const float* gib = p.gi + (int64_t)b * p.sg_b + j;
   float* outb = p.out + (int64_t)b * p.so_b + j;
@@ -72,15 +79,14 @@ __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
     for (int i = 0; i < kDepth; ++i) {
       const int t = t0 + i;
       if (t >= p.T) return true;
-      float hq = h;
-      if (p.qin.on && (t == 0 || p.qin_after_first)) hq = fake_quant(h, p.qin);
-      const float ghr = mul_add_nofma(wr, hq, br);
-      const float ghz = mul_add_nofma(wz, hq, bz);
-      const float ghn = mul_add_nofma(wn, hq, bn);
-      float hn = gru_update(r[i], z[i], c[i], ghr, ghz, ghn, h);
-      if (p.qout.on) hn = fake_quant(hn, p.qout);
+      const float ar = __builtin_fmaf(wr, hq, __builtin_fmaf(kR, r[i], br));
+      const float az = __builtin_fmaf(wz, hq, __builtin_fmaf(kR, z[i], bz));
+      const float gn2 = __builtin_fmaf(wn, hq, bn);
+      float hn = gru_update_l2(ar, az, gn2, kN * c[i], h);
+      if constexpr (QOUT) hn = fake_quant(hn, p.qout);
       outb[(int64_t)t * p.so_t] = hn;
       h = hn;
+      hq = QIN == 2 ? fake_quant(hn, p.qin) : hn;
     }
     return t0 + kDepth >= p.T;
   };
@@ -281,11 +287,16 @@ extern "C" int gs_diagonal_fwd(const gs_args* a, hipStream_t stream) {
   p.H = (int)a->H;
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
-  p.qin_after_first = !(same_quant(a->q_in, a->q_out));
 
   const int64_t n = a->B * a->H;
   const dim3 grid((unsigned)((n + kThreads - 1) / kThreads));
-  hipLaunchKernelGGL(diagonal_fwd_kernel, grid, dim3(kThreads), 0, stream, p);
+  const int qin = !a->q_in.enabled ? 0 : same_quant(a->q_in, a->q_out) ? 1 : 2;
+  void (*fn)(DiagParams) = nullptr;
+  if (a->q_out.enabled)
+    fn = qin == 0 ? diagonal_fwd_kernel<0, true> : qin == 1 ? diagonal_fwd_kernel<1, true> : diagonal_fwd_kernel<2, true>;
+  else
+    fn = qin == 0 ? diagonal_fwd_kernel<0, false> : diagonal_fwd_kernel<2, false>;
+  hipLaunchKernelGGL(fn, grid, dim3(kThreads), 0, stream, p);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }

@@ -45,10 +45,12 @@ struct M1FParams {
   int64_t sg_t, sg_b, sh0_b, so_t, so_b;
   int T, B, H, nb;
   Quant qin, qout;
-  int qin_after_first;  // 0: q_in is the identity on carried h for t >= 1
 };
 
-template <int BS>
+// QIN: 0 no q_in, 1 q_in on h0 only (q_in == q_out, so the carried state is
+// already on q_in's grid), 2 q_in every step. QOUT: q_out on. Template
+// arguments, so that the step holds no branch on them.
+template <int BS, int QIN, bool QOUT>
 __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FParams p) {
   constexpr int TPR = kSK * BS;
   constexpr int R = rows_per_wg<BS>();
@@ -71,9 +73,11 @@ __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FPara
 #pragma unroll
     for (int i = 0; i < KT; ++i) wr[g][i] = row[i];
   }
-  const float br = p.bh[col], bz = p.bh[H + col], bn = p.bh[2 * H + col];
+  // Biases pre-scaled for gru_update_l2 (-log2e for r and z, 2 log2e for n).
+  constexpr float kR = -kLog2e, kN = 2.0f * kLog2e;
+  const float br = kR * p.bh[col], bz = kR * p.bh[H + col], bn = kN * p.bh[2 * H + col];
   float h = live ? p.h0[(int64_t)b * p.sh0_b + col] : 0.0f;
-  if (kq == 0) hs[0][rs][u] = p.qin.on ? fake_quant(h, p.qin) : h;
+  if (kq == 0) hs[0][rs][u] = QIN ? fake_quant(h, p.qin) : h;
 
   // Rows past B read row 0 and never store; loads past T are clamped to
   // T - 1. Two register sets of gi take turns (one set's kDepth steps compute
@@ -118,10 +122,13 @@ __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FPara
         s += lane_xor_c<2>(s);
         gh[g] = s;
       }
-      float hn = gru_update(cr[i], cz[i], cn[i], gh[0] + br, gh[1] + bz, gh[2] + bn, h);
-      if (p.qout.on) hn = fake_quant(hn, p.qout);
+      const float ar = __builtin_fmaf(kR, gh[0], __builtin_fmaf(kR, cr[i], br));
+      const float az = __builtin_fmaf(kR, gh[1], __builtin_fmaf(kR, cz[i], bz));
+      const float gn2 = __builtin_fmaf(kN, gh[2], bn);
+      float hn = gru_update_l2(ar, az, gn2, kN * cn[i], h);
+      if constexpr (QOUT) hn = fake_quant(hn, p.qout);
       if (live && kq == 0) outb[(int64_t)t * p.so_t] = hn;
-      if (kq == 0) hs[buf ^ 1][rs][u] = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
+      if (kq == 0) hs[buf ^ 1][rs][u] = QIN == 2 ? fake_quant(hn, p.qin) : hn;
       h = hn;
       lds_barrier();  // LDS only: the out stores need not complete here
       buf ^= 1;
@@ -143,12 +150,21 @@ __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FPara
 
 typedef void (*M1FFn)(M1FParams);
 
-M1FFn pick(int bs, int* threads, int* rows) {
+template <int BS>
+M1FFn pick_modes(int qin, bool qout) {
+  if (qout)
+    return qin == 0 ? monarch1_fwd_kernel<BS, 0, true>
+                    : qin == 1 ? monarch1_fwd_kernel<BS, 1, true> : monarch1_fwd_kernel<BS, 2, true>;
+  return qin == 0 ? monarch1_fwd_kernel<BS, 0, false> : monarch1_fwd_kernel<BS, 2, false>;
+}
+
+// qin: 0 off, 1 on h0 only, 2 every step (see monarch1_fwd_kernel)
+M1FFn pick(int bs, int qin, bool qout, int* threads, int* rows) {
   switch (bs) {
-    case 16: *rows = rows_per_wg<16>(); *threads = m1f_threads<16>(); return monarch1_fwd_kernel<16>;
-    case 32: *rows = rows_per_wg<32>(); *threads = m1f_threads<32>(); return monarch1_fwd_kernel<32>;
-    case 64: *rows = rows_per_wg<64>(); *threads = m1f_threads<64>(); return monarch1_fwd_kernel<64>;
-    case 128: *rows = rows_per_wg<128>(); *threads = m1f_threads<128>(); return monarch1_fwd_kernel<128>;
+    case 16: *rows = rows_per_wg<16>(); *threads = m1f_threads<16>(); return pick_modes<16>(qin, qout);
+    case 32: *rows = rows_per_wg<32>(); *threads = m1f_threads<32>(); return pick_modes<32>(qin, qout);
+    case 64: *rows = rows_per_wg<64>(); *threads = m1f_threads<64>(); return pick_modes<64>(qin, qout);
+    case 128: *rows = rows_per_wg<128>(); *threads = m1f_threads<128>(); return pick_modes<128>(qin, qout);
     default: return nullptr;
   }
 }
@@ -160,12 +176,14 @@ M1FFn pick(int bs, int* threads, int* rows) {
 bool monarch1_local_ok(const gs_args* a) {
   int th = 0, rows = 0;
   return a->w2 == nullptr && a->nblocks >= 1 && a->blksz >= 1 && a->nblocks * a->blksz == a->H &&
-         pick((int)a->blksz, &th, &rows) != nullptr && a->nblocks <= 65535 && (a->B + rows - 1) / rows <= 65535;
+         pick((int)a->blksz, 0, false, &th, &rows) != nullptr && a->nblocks <= 65535 &&
+         (a->B + rows - 1) / rows <= 65535;
 }
 
 int run_monarch1_local(const gs_args* a, hipStream_t stream) {
   int threads = 0, rows = 0;
-  M1FFn fn = pick((int)a->blksz, &threads, &rows);
+  const int qin = !a->q_in.enabled ? 0 : same_quant(a->q_in, a->q_out) ? 1 : 2;
+  M1FFn fn = pick((int)a->blksz, qin, a->q_out.enabled != 0, &threads, &rows);
   M1FParams p;
   p.gi = a->gi;
   p.h0 = a->h0;
@@ -183,7 +201,6 @@ int run_monarch1_local(const gs_args* a, hipStream_t stream) {
   p.nb = (int)a->nblocks;
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
-  p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
   hipLaunchKernelGGL(fn, dim3((unsigned)p.nb, (unsigned)((p.B + rows - 1) / rows)), dim3(threads), 0, stream, p);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;

@@ -136,7 +136,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
     const int unit = m2_unit(b * bs + ie, nb, bs);
     float bias[3];
 #pragma unroll
-    for (int g = 0; g < 3; ++g) bias[g] = lead ? p.bh[g * H + unit] : 0.0f;
+    for (int g = 0; g < 3; ++g) bias[g] = lead ? gate_scale(g) * p.bh[g * H + unit] : 0.0f;  // for gru_update_gb
     const int64_t lane_out = (int64_t)s * p.so_b + unit;  // row = 4 rb + s
     const int64_t lane_xh = (int64_t)s * H + unit;
 
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       float* hkp = hk + (rbl * 4 + s) * U + ie;
       if (lead) {
         const float hprev = *hkp;
-        float hn = gru_update(gs_[0], gs_[U], gs_[2 * U], gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
+        float hn = gru_update_gb(gs_[0], gs_[U], gs_[2 * U], gh[0], gh[1], gh[2], bias[0], bias[1], bias[2], hprev);
         if (p.qout.on) hn = fake_quant(hn, p.qout);
         if (row < p.B) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = hn;
         *hkp = hn;
@@ -327,7 +327,7 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
   const int unit = (vi % p.nb) * p.bs + vi / p.nb;
   float bias[3];
 #pragma unroll
-  for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? p.bh[g * p.H + unit] : 0.0f;
+  for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? gate_scale(g) * p.bh[g * p.H + unit] : 0.0f;  // for gru_update_gb
 
   const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int rb_begin = gid * p.RB;
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
 #pragma unroll
       for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
 
-      float hn = gru_update(gir, giz, gin, gh[0] + bias[0], gh[1] + bias[1], gh[2] + bias[2], hprev);
+      float hn = gru_update_gb(gir, giz, gin, gh[0], gh[1], gh[2], bias[0], bias[1], bias[2], hprev);
       if (p.qout.on) hn = fake_quant(hn, p.qout);
       if (mine) p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
       if (pub && t + 1 < p.T) {
