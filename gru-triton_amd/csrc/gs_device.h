@@ -210,6 +210,29 @@ __device__ __forceinline__ float lane_xor_c(float x) {
 // across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// ---- raw buffer access --------------------------------------------------------------
+// A buffer resource over the 4 GiB above `base`, addressed by a per-lane 32-bit
+// byte offset (VGPR) plus a uniform 32-bit byte offset (SGPR). Against a
+// global access this drops the per-access 64-bit address add from the VALU:
+// the step loops of the latency-bound scans keep their per-lane offsets fixed
+// and advance only the scalar offset (diagonal forward measured 133 -> 114 ns
+// per step). Callers keep every offset sum below 2^32; the host checks the
+// tensor extents and otherwise launches the global-address variant. dword3:
+// DATA_FORMAT (bits 18:15) = 4, a 32-bit element; no other field set.
+constexpr int kBufDword3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, kBufDword3);
+}
+
+__device__ __forceinline__ float buf_ld(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+
+__device__ __forceinline__ void buf_st(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)voff, (int)soff, 0);
+}
+
 // x[l] + x[l ^ 16] + x[l ^ 32] + x[l ^ 48] in every lane, with gfx950's VALU
 // row swaps: permlane16_swap(x, x) returns (x with odd rows replaced by the
 // even rows below them, x with even rows replaced by the odd rows above

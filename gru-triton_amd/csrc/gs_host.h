@@ -56,6 +56,13 @@ inline bool same_quant(const gs_quant& a, const gs_quant& b) {
          std::fabs((double)a.qmin) <= 4194304.0 && std::fabs((double)a.qmax) <= 4194304.0;
 }
 
+// True when every byte offset of a [n2, n1, n0] view with element strides
+// (s2, s1, 1) fits the 32-bit offsets of raw buffer access (gs_device.h).
+inline bool fits_buf32(int64_t n2, int64_t s2, int64_t n1, int64_t s1, int64_t n0) {
+  const int64_t last = (n2 - 1) * s2 + (n1 - 1) * s1 + n0;
+  return n2 >= 1 && n1 >= 1 && s2 >= 0 && s1 >= 0 && last * 4 < (int64_t(1) << 32);
+}
+
 int validate_common(const gs_args* a, const char* who);
 // gs_args view of the forward fields of a backward call.
 gs_args fwd_view(const gs_bwd_args& a);

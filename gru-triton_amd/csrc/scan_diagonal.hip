@@ -39,7 +39,8 @@ struct DiagParams {
 // QIN: 0 no q_in, 1 q_in on h0 only (q_in == q_out, so the carried state is
 // already on q_in's grid), 2 q_in every step. QOUT: q_out on. The modes are
 // template arguments so that the step holds no branch and no per-step test.
-template <int QIN, bool QOUT>
+// BUF: gi and out through raw buffer offsets (their extents fit 32 bits).
+template <int QIN, bool QOUT, bool BUF>
 __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
   const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (e >= (int64_t)p.B * p.H) return;
@@ -57,6 +58,9 @@ __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
 
   const float* gib = p.gi + (int64_t)b * p.sg_b + j;
   float* outb = p.out + (int64_t)b * p.so_b + j;
+  const auto grs = raw_rsrc(p.gi), ors = raw_rsrc(p.out);
+  const uint32_t gl = (uint32_t)(((int64_t)b * p.sg_b + j) * 4), ol = (uint32_t)(((int64_t)b * p.so_b + j) * 4);
+  const uint32_t gt4 = (uint32_t)(p.sg_t * 4), ot4 = (uint32_t)(p.so_t * 4);
 
   // Two register sets of gi take turns: while one set's kDepth steps compute,
   // the other set's loads are in flight. Loads past T are clamped to T - 1 and
@@ -67,10 +71,17 @@ __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
   auto load = [&](int t0, float* r, float* z, float* c) {
 #pragma unroll
     for (int i = 0; i < kDepth; ++i) {
-      const float* g = gib + (int64_t)min(t0 + i, tl) * p.sg_t;
-      r[i] = g[0];
-      z[i] = g[H];
-      c[i] = g[2 * H];
+      if constexpr (BUF) {
+        const uint32_t so = (uint32_t)min(t0 + i, tl) * gt4;
+        r[i] = buf_ld(grs, gl, so);
+        z[i] = buf_ld(grs, gl + 4u * H, so);
+        c[i] = buf_ld(grs, gl + 8u * H, so);
+      } else {
+        const float* g = gib + (int64_t)min(t0 + i, tl) * p.sg_t;
+        r[i] = g[0];
+        z[i] = g[H];
+        c[i] = g[2 * H];
+      }
     }
   };
   // Runs steps t0 .. t0 + kDepth - 1; true once step T - 1 is done.
@@ -84,7 +95,10 @@ __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
       const float gn2 = __builtin_fmaf(wn, hq, bn);
       float hn = gru_update_l2(ar, az, gn2, kN * c[i], h);
       if constexpr (QOUT) hn = fake_quant(hn, p.qout);
-      outb[(int64_t)t * p.so_t] = hn;
+      if constexpr (BUF)
+        buf_st(ors, ol, (uint32_t)t * ot4, hn);
+      else
+        outb[(int64_t)t * p.so_t] = hn;
       h = hn;
       hq = QIN == 2 ? fake_quant(hn, p.qin) : hn;
     }
@@ -100,6 +114,14 @@ __global__ __launch_bounds__(kThreads) void diagonal_fwd_kernel(DiagParams p) {
     load(t0 + 2 * kDepth, ar, az, an);
     if (run(t0 + kDepth, xr, xz, xn)) return;
   }
+}
+
+template <bool BUF>
+void (*pick_fwd(int qin, bool qout))(DiagParams) {
+  if (qout)
+    return qin == 0 ? diagonal_fwd_kernel<0, true, BUF>
+                    : qin == 1 ? diagonal_fwd_kernel<1, true, BUF> : diagonal_fwd_kernel<2, true, BUF>;
+  return qin == 0 ? diagonal_fwd_kernel<0, false, BUF> : diagonal_fwd_kernel<2, false, BUF>;
 }
 
 // ---- backward ---------------------------------------------------------------------
@@ -127,6 +149,9 @@ struct DiagBwdParams {
   Quant qin, qout;
 };
 
+// QIN / QOUT: the quantizers are on (template arguments, so the step holds no
+// branch on them). BUF: the per-step tensors through raw buffer offsets.
+template <bool QIN, bool QOUT, bool BUF>
 __global__ __launch_bounds__(kBwdThreads) void diagonal_bwd_kernel(DiagBwdParams p) {
   const int64_t e = (int64_t)blockIdx.x * kBwdThreads + threadIdx.x;
   if (e >= (int64_t)p.B * p.H) return;
@@ -143,6 +168,14 @@ __global__ __launch_bounds__(kBwdThreads) void diagonal_bwd_kernel(DiagBwdParams
   const float* doutb = p.dout + ((int64_t)b * H + j);
   float* dgib = p.dgi + ((int64_t)b * 3 * H + j);
   const int64_t sd_t = (int64_t)p.B * H, sdg_t = (int64_t)p.B * 3 * H;
+  const auto grs = raw_rsrc(p.gi), ors = raw_rsrc(p.out), drs = raw_rsrc(p.dout), dgrs = raw_rsrc(p.dgi);
+  const uint32_t gl = (uint32_t)(((int64_t)b * p.sg_b + j) * 4), ol = (uint32_t)(((int64_t)b * p.so_b + j) * 4);
+  const uint32_t dl = (uint32_t)(((int64_t)b * H + j) * 4), dgl = (uint32_t)(((int64_t)b * 3 * H + j) * 4);
+  const uint32_t gt4 = (uint32_t)(p.sg_t * 4), ot4 = (uint32_t)(p.so_t * 4), dt4 = (uint32_t)(sd_t * 4),
+                 dgt4 = (uint32_t)(sdg_t * 4);
+  Quant qin = p.qin, qout = p.qout;
+  qin.on = QIN;
+  qout.on = QOUT;
 
   // Step i of a chunk is t = t0 - i; its loads are gi[t], out[t-1] and
   // dout[t], with t clamped to 0 (out[-1] is h0, selected at compute time). As
@@ -153,12 +186,21 @@ __global__ __launch_bounds__(kBwdThreads) void diagonal_bwd_kernel(DiagBwdParams
 #pragma unroll
     for (int i = 0; i < kBwdDepth; ++i) {
       const int t = max(t0 - i, 0);
-      const float* g = gib + (int64_t)t * p.sg_t;
-      gr[i] = g[0];
-      gz[i] = g[H];
-      gn[i] = g[2 * H];
-      hp[i] = outb[(int64_t)max(t - 1, 0) * p.so_t];
-      dd[i] = doutb[(int64_t)t * sd_t];
+      if constexpr (BUF) {
+        const uint32_t so = (uint32_t)t * gt4;
+        gr[i] = buf_ld(grs, gl, so);
+        gz[i] = buf_ld(grs, gl + 4u * H, so);
+        gn[i] = buf_ld(grs, gl + 8u * H, so);
+        hp[i] = buf_ld(ors, ol, (uint32_t)max(t - 1, 0) * ot4);
+        dd[i] = buf_ld(drs, dl, (uint32_t)t * dt4);
+      } else {
+        const float* g = gib + (int64_t)t * p.sg_t;
+        gr[i] = g[0];
+        gz[i] = g[H];
+        gn[i] = g[2 * H];
+        hp[i] = outb[(int64_t)max(t - 1, 0) * p.so_t];
+        dd[i] = doutb[(int64_t)t * sd_t];
+      }
     }
   };
 
@@ -174,18 +216,25 @@ __global__ __launch_bounds__(kBwdThreads) void diagonal_bwd_kernel(DiagBwdParams
       const float h_prev = t > 0 ? ch[i] : h0;
       float hq = h_prev;
       bool keep_in = true;
-      if (p.qin.on) {
-        keep_in = quant_keeps(h_prev, p.qin);
-        hq = fake_quant(h_prev, p.qin);
+      if constexpr (QIN) {
+        keep_in = quant_keeps(h_prev, qin);
+        hq = fake_quant(h_prev, qin);
       }
       const float ghr = mul_add_nofma(wr, hq, br);
       const float ghz = mul_add_nofma(wz, hq, bz);
       const float ghn = mul_add_nofma(wn, hq, bn);
-      const GateGrad gg = gru_backward(cr[i], cz[i], cn[i], ghr, ghz, ghn, h_prev, cd[i] + dh, p.qout);
-      float* dg = dgib + (int64_t)t * sdg_t;
-      dg[0] = gg.dgr;
-      dg[H] = gg.dgz;
-      dg[2 * H] = gg.dgn;
+      const GateGrad gg = gru_backward(cr[i], cz[i], cn[i], ghr, ghz, ghn, h_prev, cd[i] + dh, qout);
+      if constexpr (BUF) {
+        const uint32_t so = (uint32_t)t * dgt4;
+        buf_st(dgrs, dgl, so, gg.dgr);
+        buf_st(dgrs, dgl + 4u * H, so, gg.dgz);
+        buf_st(dgrs, dgl + 8u * H, so, gg.dgn);
+      } else {
+        float* dg = dgib + (int64_t)t * sdg_t;
+        dg[0] = gg.dgr;
+        dg[H] = gg.dgz;
+        dg[2 * H] = gg.dgn;
+      }
       {
 #pragma clang fp contract(off)
         float via = gg.dgr * wr + gg.dgz * wz + gg.dghn * wn;
@@ -220,6 +269,18 @@ __global__ __launch_bounds__(kBwdThreads) void diagonal_bwd_kernel(DiagBwdParams
   dbp[0] = dbr;
   dbp[H] = dbz;
   dbp[2 * H] = dbn;
+}
+
+typedef void (*DiagBwdFn)(DiagBwdParams);
+
+template <bool BUF>
+DiagBwdFn pick_bwd_buf(bool qin, bool qout) {
+  return qin ? (qout ? diagonal_bwd_kernel<true, true, BUF> : diagonal_bwd_kernel<true, false, BUF>)
+             : (qout ? diagonal_bwd_kernel<false, true, BUF> : diagonal_bwd_kernel<false, false, BUF>);
+}
+
+DiagBwdFn pick_bwd(bool qin, bool qout, bool buf) {
+  return buf ? pick_bwd_buf<true>(qin, qout) : pick_bwd_buf<false>(qin, qout);
 }
 
 }  // namespace
@@ -258,7 +319,11 @@ extern "C" int gs_diagonal_bwd(const gs_bwd_args* a, hipStream_t stream) {
 
   const int64_t n = a->B * a->H;
   const dim3 grid((unsigned)((n + kBwdThreads - 1) / kBwdThreads));
-  hipLaunchKernelGGL(diagonal_bwd_kernel, grid, dim3(kBwdThreads), 0, stream, p);
+  // dout and dgi are dense [T, B, H] and [T, B, 3H]
+  const bool buf = fits_buf32(a->T, a->sg_t, a->B, a->sg_b, 3 * a->H) &&
+                   fits_buf32(a->T, a->so_t, a->B, a->so_b, a->H) && fits_buf32(a->T, a->B * a->H, a->B, a->H, a->H) &&
+                   fits_buf32(a->T, a->B * 3 * a->H, a->B, 3 * a->H, 3 * a->H);
+  hipLaunchKernelGGL(pick_bwd(a->q_in.enabled != 0, a->q_out.enabled != 0, buf), grid, dim3(kBwdThreads), 0, stream, p);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }
@@ -291,11 +356,8 @@ extern "C" int gs_diagonal_fwd(const gs_args* a, hipStream_t stream) {
   const int64_t n = a->B * a->H;
   const dim3 grid((unsigned)((n + kThreads - 1) / kThreads));
   const int qin = !a->q_in.enabled ? 0 : same_quant(a->q_in, a->q_out) ? 1 : 2;
-  void (*fn)(DiagParams) = nullptr;
-  if (a->q_out.enabled)
-    fn = qin == 0 ? diagonal_fwd_kernel<0, true> : qin == 1 ? diagonal_fwd_kernel<1, true> : diagonal_fwd_kernel<2, true>;
-  else
-    fn = qin == 0 ? diagonal_fwd_kernel<0, false> : diagonal_fwd_kernel<2, false>;
+  const bool buf = fits_buf32(a->T, a->sg_t, a->B, a->sg_b, 3 * a->H) && fits_buf32(a->T, a->so_t, a->B, a->so_b, a->H);
+  void (*fn)(DiagParams) = buf ? pick_fwd<true>(qin, a->q_out.enabled != 0) : pick_fwd<false>(qin, a->q_out.enabled != 0);
   hipLaunchKernelGGL(fn, grid, dim3(kThreads), 0, stream, p);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
