@@ -145,16 +145,36 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
 #pragma unroll
   for (int r = 0; r < 4; ++r) idx[r] = lane + 64 * r + 256 * w;
 
+  auto twiddles = [&](int i, int s, float& self, float& partner) {
+    const int m = (i >> s) & 1;
+    const int64_t base = (((int64_t)g * L + s) * (N / 2) + pair_index(i, s)) * 4 + 2 * m;
+    self = p.tw[base + m];
+    partner = p.tw[base + 1 - m];
+  };
   float tss[L][4], tsp[L][4];
 #pragma unroll
   for (int s = 0; s < L; ++s) {
 #pragma unroll
+    for (int r = 0; r < 4; ++r) twiddles(idx[r], s, tss[s][r], tsp[s][r]);
+  }
+  // N = 1024: strides 256 and 512 (stages 8 and 9) both cross waves. They run
+  // as one exchange: with x8[i] = a8(i) x[i] + b8(i) x[i^256],
+  //   x9[i] = a9(i) x8[i] + b9(i) x8[i^512]
+  //         = a9 a8(i) x[i] + a9 b8(i) x[i^256] + b9 a8(i^512) x[i^512] + b9 b8(i^512) x[i^768],
+  // so each element needs its three cross-wave partners once, after one
+  // barrier, instead of two write/barrier/read rounds. The four products are
+  // formed once here (they round once where the two-stage form rounds twice).
+  // c8[k][r] takes the place of tss/tsp of stages 8 and 9 in registers.
+  float c8[4][4];
+  if constexpr (L == 10) {
+#pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = idx[r];
-      const int m = (i >> s) & 1;
-      const int64_t base = (((int64_t)g * L + s) * (N / 2) + pair_index(i, s)) * 4 + 2 * m;
-      tss[s][r] = p.tw[base + m];
-      tsp[s][r] = p.tw[base + 1 - m];
+      float a8p, b8p;
+      twiddles(idx[r] ^ 512, 8, a8p, b8p);
+      c8[0][r] = tss[9][r] * tss[8][r];
+      c8[1][r] = tss[9][r] * tsp[8][r];
+      c8[2][r] = tsp[9][r] * a8p;
+      c8[3][r] = tsp[9][r] * b8p;
     }
   }
 
@@ -201,6 +221,19 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
       } else if constexpr (s < 8) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = x[r ^ (1 << (s - 6))];
+      } else if constexpr (L == 10) {
+        if constexpr (s == 8) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xch[0][g][idx[r]] = x[r];
+          lds_barrier();
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float* xs = xch[0][g];
+            const int i = idx[r];
+            x[r] = c8[0][r] * x[r] + c8[1][r] * xs[i ^ 256] + c8[2][r] * xs[i ^ 512] + c8[3][r] * xs[i ^ 768];
+          }
+        }
+        return;  // stage 9 is folded into stage 8
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) xch[xsel][g][idx[r]] = x[r];
