@@ -122,8 +122,9 @@ __global__ __launch_bounds__(kGenericThreads) void butterfly_generic_kernel(BPar
 // inside a lane, strides >= 256 go through LDS between the gate's waves.
 // Each lane keeps the two twiddles of each of its 4 elements for all L stages
 // in registers (8L values), loaded
-// once. The gate epilogue for element i runs on the gate-r wave that holds i,
-// which reads gh_z and gh_n from LDS and broadcasts the next q_in(h) back.
+// once. The gate epilogue for element i runs on one of the three gate waves
+// that hold i (see owns() below), which reads the other gates' gh from LDS and
+// broadcasts the next q_in(h) back.
 // ---------------------------------------------------------------------------------
 template <int LOGN>
 __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BParams p) {
@@ -189,20 +190,22 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
     for (int q = 0; q < 3; ++q) bias[q][r] = (i < H) ? gate_scale(q) * p.bh[q * H + i] : 0.0f;  // for gru_update_gb
   }
 
+  // The gate epilogue of element r of a lane runs on one of the three gate
+  // waves that hold it (they share a SIMD): r = 0, 1 on the r-gate wave, r = 2
+  // on the z-gate wave, r = 3 on the n-gate wave, so the three waves' epilogue
+  // chains interleave instead of one wave running all four.
+  auto owns = [&](int r) { return r < 2 ? g == 0 : g == r - 1; };
   for (int t = 0; t < p.T; ++t) {
+    // gate inputs of the owned elements (padding elements read element H-1's
+    // and discard their result)
     float gir[4], giz[4], gin[4];
-    if (g == 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = idx[r];
-        if (i < H) {
-          const float* gp = p.gi + (int64_t)t * p.sg_t + (int64_t)b * p.sg_b + i;
-          gir[r] = gp[0];
-          giz[r] = gp[H];
-          gin[r] = gp[2 * H];
-        } else {
-          gir[r] = giz[r] = gin[r] = 0.0f;
-        }
+    for (int r = 0; r < 4; ++r) {
+      if (owns(r)) {
+        const float* gp = p.gi + (int64_t)t * p.sg_t + (int64_t)b * p.sg_b + min(idx[r], H - 1);
+        gir[r] = gp[0];
+        giz[r] = gp[H];
+        gin[r] = gp[2 * H];
       }
     }
     int xsel = 0;
@@ -245,26 +248,26 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
 #pragma unroll
       for (int r = 0; r < 4; ++r) x[r] = tss[s][r] * x[r] + tsp[s][r] * y[r];
     });
-    if (g != 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ghs[g][idx[r]] = x[r];
-    }
+    for (int r = 0; r < 4; ++r)
+      if (!owns(r)) ghs[g][idx[r]] = x[r];  // what the owner of r reads
     lds_barrier();
-    if (g == 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = idx[r];
-        float hn = gru_update_gb(gir[r], giz[r], gin[r], x[r], ghs[1][i], ghs[2][i], bias[0][r], bias[1][r],
-                                 bias[2][r], hraw[r]);
-        if (p.qout.on) hn = fake_quant(hn, p.qout);
-        float hq = 0.0f;
-        if (i < H) {
-          p.out[(int64_t)t * p.so_t + (int64_t)b * p.so_b + i] = hn;
-          hraw[r] = hn;
-          hq = (p.qin.on && p.qin_after_first) ? fake_quant(hn, p.qin) : hn;
-        }
-        hqs[i] = hq;
+    for (int r = 0; r < 4; ++r) {
+      if (!owns(r)) continue;
+      const int i = idx[r];
+      const float ghr = g == 0 ? x[r] : ghs[0][i];
+      const float ghz = g == 1 ? x[r] : ghs[1][i];
+      const float ghn = g == 2 ? x[r] : ghs[2][i];
+      float hn = gru_update_gb(gir[r], giz[r], gin[r], ghr, ghz, ghn, bias[0][r], bias[1][r], bias[2][r], hraw[r]);
+      if (p.qout.on) hn = fake_quant(hn, p.qout);
+      float hq = 0.0f;
+      if (i < H) {
+        p.out[(int64_t)t * p.so_t + (int64_t)b * p.so_b + i] = hn;
+        hraw[r] = hn;
+        hq = (p.qin.on && p.qin_after_first) ? fake_quant(hn, p.qin) : hn;
       }
+      hqs[i] = hq;
     }
     lds_barrier();
 #pragma unroll
