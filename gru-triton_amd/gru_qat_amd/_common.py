@@ -15,6 +15,16 @@ QuantTuple = Optional[Tuple[float, int, int]]
 
 
 def require_cuda(who: str, **tensors: torch.Tensor) -> None:
+    dev = None
+    for v in tensors.values():  # fast path: every tensor on one CUDA device
+        if not (isinstance(v, torch.Tensor) and v.is_cuda):
+            break
+        if dev is None:
+            dev = v.device
+        elif v.device != dev:
+            break
+    else:
+        return
     bad = {k: v.device for k, v in tensors.items() if not (isinstance(v, torch.Tensor) and v.is_cuda)}
     if bad:
         devs = ", ".join(f"{k}={v.device if isinstance(v, torch.Tensor) else type(v).__name__}"

@@ -396,42 +396,56 @@ def workspace_faults(device: Optional[torch.device] = None) -> int:
     return total
 
 
+_FN_CACHE: dict = {}
+
+
+def _entry(lib: ctypes.CDLL, fn_name: str):
+    fn = _FN_CACHE.get(fn_name)
+    if fn is None:
+        fn = _FN_CACHE[fn_name] = getattr(lib, fn_name)
+    return fn
+
+
 def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,
            w2: Optional[torch.Tensor], bh: torch.Tensor, out: torch.Tensor,
            h_in_quant: QuantTuple, h_out_quant: QuantTuple, nblocks: int = 0, blksz: int = 0,
            log_n: int = 0, bfly_nblocks: int = 0) -> None:
-    """Fill gs_args from contiguous fp32 device tensors and call the entry point
-    on the current torch stream of gi's device."""
-    lib = load()
-    T, B, threeH = gi.shape
-    H = threeH // 3
-    a = GsArgs()
-    a.gi = gi.data_ptr()
-    a.h0 = h0.data_ptr()
-    a.w = w.data_ptr()
-    a.w2 = w2.data_ptr() if w2 is not None else None
-    a.bh = bh.data_ptr()
-    a.out = out.data_ptr()
-    a.T, a.B, a.H = T, B, H
-    a.sg_t, a.sg_b = gi.stride(0), gi.stride(1)
-    a.sh0_b = h0.stride(0)
-    a.so_t, a.so_b = out.stride(0), out.stride(1)
-    a.nblocks, a.blksz = nblocks, blksz
-    a.log_n, a.bfly_nblocks = log_n, bfly_nblocks
-    a.q_in = make_quant(h_in_quant, "h_in_quant")
-    a.q_out = make_quant(h_out_quant, "h_out_quant")
+    """Fill gs_args from fp32 device tensors and call the entry point on the
+    current torch stream of gi's device.
 
-    need = lib.gs_workspace_bytes(kind, ctypes.byref(a))
-    if need < 0:
-        raise_for(int(need), lib)
-    with torch.cuda.device(gi.device):
-        handle = torch.cuda.current_stream(gi.device).cuda_stream
-        tagged = kind in (KIND_DENSE, KIND_MONARCH)
-        ws = workspace(gi.device, handle, int(need), steps=T if tagged else 0)
-        a.workspace = ws.data_ptr()
-        a.workspace_bytes = ws.numel()
-        rc = getattr(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
+    Kept short on the host: one positional struct construction, the workspace
+    size query only for the kinds whose workspace depends on the shape (dense
+    and Monarch), and the device switch only when gi's device is not current.
+    The short scans (diagonal, single-factor Monarch) take about as long on the
+    GPU as a launch does on the host."""
+    lib = _lib if _lib is not None else load()
+    T, B, threeH = gi.shape
+    a = GsArgs(gi.data_ptr(), h0.data_ptr(), w.data_ptr(), w2.data_ptr() if w2 is not None else None,
+               bh.data_ptr(), out.data_ptr(), None, 0, T, B, threeH // 3, gi.stride(0), gi.stride(1),
+               h0.stride(0), out.stride(0), out.stride(1), nblocks, blksz, log_n, bfly_nblocks,
+               make_quant(h_in_quant, "h_in_quant"), make_quant(h_out_quant, "h_out_quant"))
+    tagged = kind in (KIND_DENSE, KIND_MONARCH)
+    if tagged:
+        need = lib.gs_workspace_bytes(kind, ctypes.byref(a))
+        if need < 0:
+            raise_for(int(need), lib)
+    else:
+        need = 0  # the diagonal and butterfly forwards use no workspace beyond the cached minimum
+    dev = gi.device
+    if dev.index == torch.cuda.current_device():
+        rc = _launch_current(lib, fn_name, a, dev, need, T if tagged else 0)
+    else:
+        with torch.cuda.device(dev):
+            rc = _launch_current(lib, fn_name, a, dev, need, T if tagged else 0)
     raise_for(rc, lib)
+
+
+def _launch_current(lib: ctypes.CDLL, fn_name: str, a: "GsArgs", dev: torch.device, need: int, steps: int) -> int:
+    handle = torch.cuda.current_stream().cuda_stream
+    ws = workspace(dev, handle, int(need), steps=steps)
+    a.workspace = ws.data_ptr()
+    a.workspace_bytes = ws.numel()
+    return _entry(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
 
 
 def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,
