@@ -172,6 +172,22 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
       tii[s][r] = e.t_ii;
       tpi[s][r] = e.t_pi;
     }
+  // N = 1024: the transposed layers 9 and 8 (strides 512, 256) both cross
+  // waves; they run as one exchange. With x9[j] = tii9(j) x[j] + tpi9(j) x[j^512],
+  //   x8[i] = tii8 tii9(i) x[i] + tii8 tpi9(i) x[i^512] + tpi8 tii9(i^256) x[i^256]
+  //         + tpi8 tpi9(i^256) x[i^768],
+  // the four products formed here once (as in the forward's register kernel).
+  float c89[4][4];
+  if constexpr (L == 10) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const ElemTw q = elem_tw(tw_g, N, 9, idx[r] ^ 256);
+      c89[0][r] = tii[8][r] * tii[9][r];
+      c89[1][r] = tii[8][r] * tpi[9][r];
+      c89[2][r] = tpi[8][r] * q.t_ii;
+      c89[3][r] = tpi[8][r] * q.t_pi;
+    }
+  }
   const int64_t BH = (int64_t)p.B * H;
   float d[4];  // D_t of this lane's elements
 #pragma unroll
@@ -205,6 +221,21 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
     if (t > 0) load_step(t - 1, ncg, nzm, nmi, ndp);
     static_for<0, L>([&](auto S) {
       constexpr int s = L - 1 - S;
+      if constexpr (L == 10 && s >= 8) {
+        if constexpr (s == 9) {
+          float* xs = xch[0][g];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xs[idx[r]] = x[r];
+          lds_barrier();
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+#pragma clang fp contract(off)
+            const int i = idx[r];
+            x[r] = ((c89[0][r] * x[r] + c89[1][r] * xs[i ^ 512]) + c89[2][r] * xs[i ^ 256]) + c89[3][r] * xs[i ^ 768];
+          }
+        }
+        return;  // layer 8 is folded into layer 9's exchange
+      }
       float y[4];
       partner_of<s>(x, y, xch[S & 1][g], idx);
 #pragma unroll
