@@ -124,7 +124,6 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_batch(const fl
       partner_of<s>(x, y, xch[s & 1][g], idx);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-#pragma clang fp contract(off)
         x[r] = tii[s][r] * x[r] + tip[s][r] * y[r];
       }
     });
@@ -229,7 +228,6 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
           lds_barrier();
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-#pragma clang fp contract(off)
             const int i = idx[r];
             x[r] = ((c89[0][r] * x[r] + c89[1][r] * xs[i ^ 512]) + c89[2][r] * xs[i ^ 256]) + c89[3][r] * xs[i ^ 768];
           }
@@ -240,7 +238,6 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
       partner_of<s>(x, y, xch[S & 1][g], idx);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-#pragma clang fp contract(off)
         x[r] = tii[s][r] * x[r] + tpi[s][r] * y[r];
       }
     });
@@ -326,7 +323,6 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
       if constexpr (s + 1 < L) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-#pragma clang fp contract(off)
           a[s + 1][r] = tii[s][r] * a[s][r] + tip[s][r] * ap[s][r];
         }
       }
@@ -350,7 +346,6 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
         partner_of<s>(gv, y, xch[S & 1], idx);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-#pragma clang fp contract(off)
           gv[r] = tii[s][r] * gv[r] + tpi[s][r] * y[r];
         }
       }
