@@ -32,9 +32,10 @@ def test_diagonal_fp32(dev, shape):
     assert_fp32_parity(small_cfg(0, shape), dev)
 
 
-@pytest.mark.parametrize("qin,qout", [(Q, Q), (None, Q), (Q, None), (Q2, Q)])
-def test_diagonal_quant(dev, qin, qout):
-    cfg = small_cfg(0, (16, 8, 64), h_in_quant=qin, h_out_quant=qout)
+@pytest.mark.parametrize("shape", [(16, 8, 64), (1, 1, 8), (37, 3, 100)])
+@pytest.mark.parametrize("qin,qout", [(Q, Q), (None, Q), (Q, None), (Q2, Q), (Q2, None)])
+def test_diagonal_quant(dev, shape, qin, qout):
+    cfg = small_cfg(0, shape, h_in_quant=qin, h_out_quant=qout)
     if qout is None:
         assert_fp32_parity(cfg, dev)
     else:
@@ -143,8 +144,9 @@ def test_monarch_quant(dev, two):
 
 # single factor: blksz 64 (block-local kernel) and 24 (MFMA kernel), each quantizer alone and both
 # with different scales (q_in then re-quantizes the carried h every step)
-@pytest.mark.parametrize("shape,nb", [((12, 6, 256), 4), ((12, 6, 96), 4)])
-@pytest.mark.parametrize("qin,qout", [(None, Q), (Q, None), (Q2, Q)])
+# blksz 64, 16, 128 (block-local kernel, every quantizer-mode instantiation) and 24 (MFMA kernel)
+@pytest.mark.parametrize("shape,nb", [((12, 6, 256), 4), ((12, 6, 96), 4), ((9, 5, 128), 8), ((7, 3, 512), 4)])
+@pytest.mark.parametrize("qin,qout", [(None, Q), (Q, None), (Q2, Q), (Q, Q), (Q2, None)])
 def test_monarch_single_quant_modes(dev, shape, nb, qin, qout):
     cfg = _monarch(shape, nb, h_in_quant=qin, h_out_quant=qout)
     if qout is None:
