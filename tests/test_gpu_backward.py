@@ -125,3 +125,25 @@ def test_butterfly_backward_materialized_fallback(dev, q):
         err = (g.cpu() - r).abs().max().item()
         print(f"[bwd] butterfly H_PAD=2048 d{k}: max err {err:.3e}")
         assert err <= 1e-4 * max(1.0, r.abs().max().item()), k
+
+
+@pytest.mark.parametrize("idx,shape,nb", [(0, (13, 5, 96), None), (0, (4, 3, 1024), None), (3, (9, 5, 128), 8),
+                                           (1, (6, 4, 64), None)])
+@pytest.mark.parametrize("qin,qout", [(COARSE, None), (None, COARSE), (Q_INT8_HIDDEN, COARSE)])
+def test_backward_one_sided_quantizers(dev, idx, shape, nb, qin, qout):
+    """Only one of the hidden quantizers on, or two different ones: the
+    gradients follow q_in's and q_out's clipped straight-through masks
+    separately (each kernel variant of the quantizer modes)."""
+    cfg = _cfg(idx, shape, nb=nb)
+    cfg["h_in_quant"], cfg["h_out_quant"] = qin, qout
+    keys = ["gi", "h0", "bh"] + list(O.hidden_params(cfg))
+    leaves = {k: cfg[k].to(dev).requires_grad_(True) for k in keys}
+    out = _run(cfg, dev, leaves)
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(17)).to(dev)
+    grads = torch.autograd.grad(out, [leaves[k] for k in keys], dout)
+    ref = O.scan_backward(cfg, out.detach(), dout)
+    for k, g in zip(keys, grads):
+        r = ref["d" + k]
+        err = (g.cpu() - r).abs().max().item()
+        print(f"[bwd] {cfg['name']} {shape} qin={qin is not None} qout={qout is not None} d{k}: max err {err:.3e}")
+        assert err <= 1e-4 * max(1.0, r.abs().max().item()), k
