@@ -70,6 +70,7 @@ gs_args fwd_view(const gs_bwd_args& a) {
   f.out = const_cast<float*>(a.out);
   f.workspace = a.workspace;
   f.workspace_bytes = a.workspace_bytes;
+  f.fault_mirror = a.fault_mirror;
   f.T = a.T;
   f.B = a.B;
   f.H = a.H;
@@ -192,7 +193,7 @@ int gs_workspace_status(void* ws, int64_t bytes, hipStream_t stream) {
     const uint32_t zero = 0;
     GS_CHECK_HIP(hipMemcpy(ws, &zero, sizeof(zero), hipMemcpyHostToDevice));
   }
-  return (int)word;
+  return word != 0 ? 1 : 0;
 }
 
 const char* gs_last_error(void) { return gs::last_error(); }

@@ -264,13 +264,48 @@ __device__ __forceinline__ float sum_across_rows(float x) {
 // steps on one workspace. Polls are bounded: after kSpinLimit polls the
 // waiter raises the fault word and every waiter gives up, so a broken launch
 // drains instead of hanging the device.
+//
+// The fault word is scoped to one launch: a waiter that gives up stores
+// fval = tag_base + 1 of its launch, and waiters treat the word as raised only
+// when it holds their own launch's fval. A fault left over from an earlier
+// launch (a different tag_base) therefore never cuts a later launch's waits
+// short. A workgroup whose wait gave up is dead for the rest of the launch:
+// it stops publishing (so no other workgroup accepts words computed from
+// stale inputs) and writes NaN into every output it would have written from
+// then on. The last workgroup to leave copies a raised fault word into the
+// optional host-visible `mirror` (hipHostMalloc memory), where the host can
+// read it without synchronising.
 constexpr uint32_t kSpinLimit = 1u << 22;
 
 struct Ctrl {
-  uint32_t* fault;       // nonzero after a poll time-out
+  uint32_t* fault;       // fval of the launch whose wait gave up (0: none yet)
   uint32_t* exit_count;  // workgroups that have finished this launch
   uint32_t* tag_base;    // tags of this launch are tag_base + t + 1
+  uint32_t* spin;        // poll bound override: 0 (a zeroed workspace) means kSpinLimit
+  uint32_t* mirror;      // host-visible copy of a raised fault word, or NULL
+  uint32_t fval;         // this launch's fault value, tag_base + 1 (set in the kernel)
+  uint32_t limit;        // this launch's poll bound (set in the kernel)
 };
+
+// The kernel-side control block: the host's pointers plus this launch's fault
+// value and poll bound. The bound is kSpinLimit unless the host wrote an
+// override into the workspace (tests use a tiny one to make waits run out
+// while every kernel still exits normally).
+__device__ __forceinline__ Ctrl launch_ctrl(const Ctrl& host, uint32_t base) {
+  Ctrl c = host;
+  c.fval = base + 1u;
+  const uint32_t o = __hip_atomic_load(host.spin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  c.limit = o != 0u ? o : kSpinLimit;
+  return c;
+}
+
+__device__ __forceinline__ void raise_fault(const Ctrl& c) {
+  __hip_atomic_store(c.fault, c.fval, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool fault_raised(const Ctrl& c) {
+  return __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c.fval;
+}
 
 __device__ __forceinline__ uint64_t ld_tagged(const uint64_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -302,26 +337,31 @@ __device__ __forceinline__ float value_of(uint64_t w) { return __uint_as_float((
 // Polls MW words base[src[i]] (those with bit i of `valid`) until each
 // carries `tag`, then stores their values to dst_lds[dst[i]]. Offsets are
 // precomputed by the caller, so the loop is loads, compares and a sleep.
+// Returns false when the wait gave up (the staged values are then stale).
 template <int MW>
-__device__ __forceinline__ void poll_to_lds(const Ctrl& c, const uint64_t* base, const int (&src)[MW],
+__device__ __forceinline__ bool poll_to_lds(const Ctrl& c, const uint64_t* base, const int (&src)[MW],
                                             const int (&dst)[MW], uint32_t valid, uint32_t tag,
                                             float* dst_lds) {
   uint64_t v[MW];
 #pragma unroll
   for (int i = 0; i < MW; ++i) v[i] = ld_tagged(base + src[i]);
   uint32_t polls = 0;
+  bool ok = true;
   while (true) {
     uint32_t pending = 0;
 #pragma unroll
     for (int i = 0; i < MW; ++i) pending |= (tag_of(v[i]) != tag ? 1u : 0u) << i;
     pending &= valid;
     if (pending == 0u) break;
-    if (++polls > kSpinLimit) {
-      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (++polls > c.limit) {
+      raise_fault(c);
+      ok = false;
       break;
     }
-    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+    if ((polls & 255u) == 0u && fault_raised(c)) {
+      ok = false;
       break;
+    }
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int i = 0; i < MW; ++i)
@@ -330,6 +370,7 @@ __device__ __forceinline__ void poll_to_lds(const Ctrl& c, const uint64_t* base,
 #pragma unroll
   for (int i = 0; i < MW; ++i)
     if ((valid >> i) & 1u) dst_lds[dst[i]] = value_of(v[i]);
+  return ok;
 }
 
 // Calls f(integral_constant<int, I>) for I = 0 .. N-1 as straight-line code.
@@ -341,36 +382,41 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Waits (bounded) until the LDS counter reaches target.
-__device__ __forceinline__ void wait_lds_count(const Ctrl& c, const int* cnt, int target) {
+// Waits (bounded) until the LDS counter reaches target; false if it gave up.
+__device__ __forceinline__ bool wait_lds_count(const Ctrl& c, const int* cnt, int target) {
   uint32_t polls = 0;
   while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
-    if (++polls > kSpinLimit) {
-      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
+    if (++polls > c.limit) {
+      raise_fault(c);
+      return false;
     }
     __builtin_amdgcn_s_sleep(1);
   }
+  return true;
 }
 
 // Whether the n workgroups whose XCD words sit at words[0], words[stride], ...
 // all run on one XCD. Every workgroup stores its word (st_tagged of its
 // xcc_id with `tag`) at launch; one wave of each workgroup calls this and all
-// of them reach the same answer. n <= 64.
+// of them reach the same answer. n <= 64. `ok` turns false when the wait gave
+// up (the answer is then false).
 __device__ __forceinline__ bool group_on_one_xcd(const Ctrl& c, const uint64_t* words, int stride, int n,
-                                                 uint32_t tag) {
+                                                 uint32_t tag, bool& ok) {
   const int lane = threadIdx.x & 63;
   const bool mine = lane < n;
   const uint64_t* src = words + (int64_t)(mine ? lane : 0) * stride;
   uint64_t v = ld_tagged(src);
   uint32_t polls = 0;
   while (__ballot(mine && tag_of(v) != tag)) {
-    if (++polls > kSpinLimit) {
-      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (++polls > c.limit) {
+      raise_fault(c);
+      ok = false;
       return false;
     }
-    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+    if ((polls & 255u) == 0u && fault_raised(c)) {
+      ok = false;
       return false;
+    }
     __builtin_amdgcn_s_sleep(1);
     if (mine && tag_of(v) != tag) v = ld_tagged(src);
   }
@@ -379,14 +425,25 @@ __device__ __forceinline__ bool group_on_one_xcd(const Ctrl& c, const uint64_t* 
   return __ballot(mine && x != x0) == 0;
 }
 
-// Called once by every workgroup after its last exchange. The last one to
-// leave advances tag_base by the launch's step count (every workgroup read
-// tag_base before it incremented exit_count) and rearms exit_count.
-__device__ __forceinline__ void leave_grid(const Ctrl& c, uint32_t nwg, uint32_t base, uint32_t steps) {
+// Called by every thread of every workgroup after its last exchange, with
+// the LDS word (and bit mask) that records whether a wait of this workgroup
+// gave up, read after the workgroup barrier below. The workgroup's first thread raises the
+// fault word itself for a dead workgroup, so that its own release increment of
+// exit_count orders the fault word before it. The last workgroup to leave
+// (its acquire increment sees every earlier workgroup's writes) copies a fault
+// word holding this launch's value into the host mirror, advances tag_base by
+// the launch's step count (every workgroup read tag_base before it incremented
+// exit_count) and rearms exit_count.
+__device__ __forceinline__ void leave_grid(const Ctrl& c, uint32_t nwg, uint32_t base, uint32_t steps,
+                                           const int* dead_flag, int dead_mask) {
+  __syncthreads();
   if (threadIdx.x == 0) {
+    if (*dead_flag & dead_mask) raise_fault(c);
     const uint32_t prev =
         __hip_atomic_fetch_add(c.exit_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == nwg - 1u) {
+      if (c.mirror != nullptr && fault_raised(c))
+        __hip_atomic_store(c.mirror, c.fval, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       __hip_atomic_store(c.tag_base, base + steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(c.exit_count, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }

@@ -28,8 +28,10 @@ void clear_error();
   } while (0)
 
 // Workspace layout (bytes from the start):
-//   [0, 256)        control words: fault flag (word 0), exit count (word 32),
-//                   tag base (word 48); zero on first use
+//   [0, 256)        control words: fault word (word 0; the fault value
+//                   tag_base + 1 of the last launch whose wait gave up),
+//                   poll bound override (word 16; 0 = the default bound),
+//                   exit count (word 32), tag base (word 48); zero on first use
 //   [256, ...)      tagged exchange words (uint64), 256-byte aligned regions
 // Every launch leaves the exit count at zero and the tag base advanced, and
 // only ever compares exchange words against tags newer than any word an
@@ -38,9 +40,10 @@ constexpr int64_t kCtrlBytes = 256;
 
 inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-inline Ctrl ctrl_of(void* ws) {
+// Host half of the control block; the kernel adds its launch's fault value.
+inline Ctrl ctrl_of(void* ws, uint32_t* mirror) {
   uint32_t* w = static_cast<uint32_t*>(ws);
-  return Ctrl{w, w + 32, w + 48};
+  return Ctrl{w, w + 32, w + 48, w + 16, mirror, 0u, 0u};
 }
 
 inline Quant to_quant(const gs_quant& q) {

@@ -80,10 +80,10 @@ __device__ __forceinline__ void lds_a_il(const float* blk, int lane, float (&a)[
 // instruction instead measured 25 % slower exchanges). Loads address up to
 // src[64 MPR - 1], so the buffer must extend that far (words past klen are
 // loaded but not waited for). Only stale words are loaded again. Returns the
-// mask of valid m.
+// mask of valid m; `ok` turns false when the wait gave up.
 template <int MPR>
 __device__ __forceinline__ uint32_t poll_row_words(const Ctrl& c, const uint64_t* src, int klen, uint32_t tag,
-                                                   uint64_t (&v)[MPR]) {
+                                                   uint64_t (&v)[MPR], bool& ok) {
   static_assert(MPR <= 32, "poll mask is 32 bits");
   const int lane = threadIdx.x & 63;
   const uint64_t* s0 = src + lane;
@@ -97,12 +97,15 @@ __device__ __forceinline__ uint32_t poll_row_words(const Ctrl& c, const uint64_t
     static_for<0, MPR>([&](auto I) { pending |= (tag_of(v[I]) != tag ? 1u : 0u) << I; });
     pending &= valid;
     if (pending == 0u) break;
-    if (++polls > kSpinLimit) {
-      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (++polls > c.limit) {
+      raise_fault(c);
+      ok = false;
       break;
     }
-    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+    if ((polls & 255u) == 0u && fault_raised(c)) {
+      ok = false;
       break;
+    }
     __builtin_amdgcn_s_sleep(1);
     static_for<0, MPR>([&](auto I) {
       if ((pending >> I) & 1u) v[I] = ld_tagged(s0 + 64 * I);
@@ -116,9 +119,10 @@ __device__ __forceinline__ uint32_t poll_row_words(const Ctrl& c, const uint64_t
 // k < klen, with the loads, waits and bounds of poll_row_words. (The wait loop
 // is written out here rather than shared: the forward kernels' code around
 // this inlined loop is tuned, and the shared form schedules differently.)
+// `ok` turns false when the wait gave up.
 template <int MPR>
 __device__ __forceinline__ void poll_row_il(const Ctrl& c, const uint64_t* src, float* dst, int r, int klen,
-                                            uint32_t tag) {
+                                            uint32_t tag, bool& ok) {
   static_assert(MPR <= 32, "poll mask is 32 bits");
   const int lane = threadIdx.x & 63;
   const uint64_t* s0 = src + lane;
@@ -133,12 +137,15 @@ __device__ __forceinline__ void poll_row_il(const Ctrl& c, const uint64_t* src, 
     static_for<0, MPR>([&](auto I) { pending |= (tag_of(v[I]) != tag ? 1u : 0u) << I; });
     pending &= valid;
     if (pending == 0u) break;
-    if (++polls > kSpinLimit) {
-      __hip_atomic_store(c.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (++polls > c.limit) {
+      raise_fault(c);
+      ok = false;
       break;
     }
-    if ((polls & 255u) == 0u && __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+    if ((polls & 255u) == 0u && fault_raised(c)) {
+      ok = false;
       break;
+    }
     __builtin_amdgcn_s_sleep(1);
     static_for<0, MPR>([&](auto I) {
       if ((pending >> I) & 1u) v[I] = ld_tagged(s0 + 64 * I);

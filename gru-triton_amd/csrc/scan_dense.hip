@@ -87,11 +87,13 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   float* hk = hst + 2 * p.hsz;       // [RB][4][U]   raw h of this workgroup's units
   float* gst = hk + p.RB * 4 * U;    // [2][4][3][U] staged gi (remote mode)
   int* flags = reinterpret_cast<int*>(gst + 24 * U);  // remote mode: [0] compute-wave iterations
-                                                      // published, [1] group on one XCD
+                                                      // published, [1] bit 0: group on one XCD,
+                                                      // bit 1: a wait of this workgroup gave up
   const int lds_floats = 2 * p.hsz + p.RB * 4 * U + (REMOTE ? 24 * U + 4 : 0);
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
   const uint32_t base = REMOTE ? __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+  const Ctrl ctrl = launch_ctrl(p.ctrl, base);
   if (REMOTE && threadIdx.x == 0) st_tagged(p.xw + blockIdx.x, __uint_as_float(xcc_id()), base + 1u);
   const int niter = p.T * nrbm;
 
@@ -173,11 +175,15 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       float hn = gru_update_l2(__builtin_fmaf(kR, gh[0], cr), __builtin_fmaf(kR, gh[1], cz),
                                __builtin_fmaf(kN, gh[2], bias[2]), an2, hprev);
       if (p.qout.on) hn = fake_quant(hn, p.qout);
-      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = hn;
-      const bool xcd_local = REMOTE && t >= 1 && __builtin_amdgcn_readfirstlane(flags[1]) != 0;
+      // flags[1] as staged for this iteration: after a give-up the workgroup's
+      // outputs are NaN and it publishes nothing more
+      const int fl = REMOTE ? __builtin_amdgcn_readfirstlane(flags[1]) : 0;
+      const bool xcd_local = t >= 1 && (fl & 1) != 0;
+      const bool dead = (fl & 2) != 0;
+      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = dead ? __builtin_nanf("") : hn;
       if (lead && unit_ok) {
         *hkp = hn;
-        if (t + 1 < p.T) {
+        if (t + 1 < p.T && !dead) {
           const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
           if (REMOTE) {
             uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * p.H + lane_xh;
@@ -202,6 +208,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
     // loads the memory system that carries their stores.
     const int pr = wave - nwc;
     constexpr int NGI = NT / 64 > kPollers ? (3 * 4 * (NT / 64 - kPollers) + 63) / 64 : 1;  // gi words per lane
+    bool alive = true;  // no wait of this wave has given up
     for (int it = 0; it < niter; ++it) {
       const int nx = it + 1;
       if (nx < niter) {
@@ -227,12 +234,16 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
             hs[il_index(pr, k)] = v;
           }
         } else {
-          if (pr == 0 && nx == nrbm)  // first exchange of the launch
-            flags[1] = (p.P <= 64 && group_on_one_xcd(p.ctrl, p.xw + gid, p.ngroups, p.P, base + 1u)) ? 1 : 0;
-          wait_lds_count(p.ctrl, &flags[0], nwc * (it + 1));
-          // bs words of row pr, k < 16 KC
-          const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * p.H + klo;
-          poll_row_il<KC / 4>(p.ctrl, hb, hs, pr, p.bs, base + (uint32_t)t2);
+          if (alive) {
+            if (pr == 0 && nx == nrbm &&  // first exchange of the launch
+                p.P <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, p.P, base + 1u, alive))
+              __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
+            // bs words of row pr, k < 16 KC
+            const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * p.H + klo;
+            if (alive) poll_row_il<KC / 4>(ctrl, hb, hs, pr, p.bs, base + (uint32_t)t2, alive);
+            if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
         }
         float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
 #pragma unroll
@@ -244,7 +255,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       lds_barrier();
     }
   }
-  if (REMOTE) leave_grid(p.ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T);
+  if (REMOTE) leave_grid(ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T, &flags[1], 2);
 }
 
 typedef void (*DFn)(DParams);
@@ -349,7 +360,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.bh = a->bh;
   p.out = a->out;
   char* ws = static_cast<char*>(a->workspace);
-  p.ctrl = ctrl_of(ws);
+  p.ctrl = ctrl_of(ws, a->fault_mirror);
   p.xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
   p.xw = reinterpret_cast<uint64_t*>(ws + kCtrlBytes + pl.xh_bytes);
   p.sg_t = a->sg_t;

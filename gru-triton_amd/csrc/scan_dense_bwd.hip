@@ -160,11 +160,13 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
   float* sti = hst + 6 * p.hsz;       // [2][4][kNV][U] staged per-unit values
   float* dd = sti + 2 * 4 * kNV * U;  // [RB][4][U] D_t of this workgroup's units
   int* flags = reinterpret_cast<int*>(dd + p.RB * 4 * U);  // [0] compute-wave iterations published,
-                                                          // [1] group on one XCD
+                                                          // [1] bit 0: group on one XCD, bit 1: a
+                                                          // wait of this workgroup gave up
   const int lds_floats = 6 * p.hsz + 8 * kNV * U + p.RB * 4 * U + 4;
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
   const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const Ctrl ctrl = launch_ctrl(p.ctrl, base);
   if (threadIdx.x == 0) st_tagged(p.xw + blockIdx.x, __uint_as_float(xcc_id()), base + 1u);
   const int niter = T * nrbm;
   const int64_t BH = (int64_t)p.B * H;
@@ -225,7 +227,10 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
         }
       });
       const float via_w = reduce16(acc0 + acc1, s);
-      const bool xcd_local = st >= 1 && __builtin_amdgcn_readfirstlane(flags[1]) != 0;
+      // after a give-up the workgroup's D_t and dh0 are NaN and it publishes nothing more
+      const int fl = __builtin_amdgcn_readfirstlane(flags[1]);
+      const bool xcd_local = st >= 1 && (fl & 1) != 0;
+      const bool dead = (fl & 2) != 0;
       if (lead && unit_ok && row < p.B) {
         const float* sv = sti + (buf * 4 + s) * kNV * U + uo;
         float* ddp = dd + (rbl * 4 + s) * U + uo;
@@ -235,15 +240,17 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
           carry = sv[0] * *ddp + sv[U] * via_w;
         }
         if (t == 0) {
-          p.dh0[(int64_t)row * H + unit] = carry;
+          p.dh0[(int64_t)row * H + unit] = dead ? __builtin_nanf("") : carry;
         } else {
           const float dn = sv[2 * U] + carry;  // D_{t-1}
           uint64_t* dst = p.xh + ((int64_t)(st & 1) * p.Bp + row) * H + unit;
-          if (xcd_local)
-            st_tagged_xcd(dst, dn, base + (uint32_t)st + 1u);
-          else
-            st_tagged(dst, dn, base + (uint32_t)st + 1u);
-          p.dsum[(int64_t)(t - 1) * BH + (int64_t)row * H + unit] = dn;
+          if (!dead) {
+            if (xcd_local)
+              st_tagged_xcd(dst, dn, base + (uint32_t)st + 1u);
+            else
+              st_tagged(dst, dn, base + (uint32_t)st + 1u);
+          }
+          p.dsum[(int64_t)(t - 1) * BH + (int64_t)row * H + unit] = dead ? __builtin_nanf("") : dn;
           *ddp = dn;
         }
       }
@@ -259,6 +266,7 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
     const int pr = wave - nwc;
     constexpr int NWC_MAX = NT / 64 - kPollers;
     constexpr int NSV = (kNV * 4 * NWC_MAX + 63) / 64;  // staged values per lane
+    bool alive = true;  // no wait of this wave has given up
     for (int it = 0; it < niter; ++it) {
       const int nx = it + 1;
       if (nx < niter) {
@@ -284,12 +292,16 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
 #pragma unroll
             for (int g = 0; g < 3; ++g) cf[g][m] = ok ? crow[g * H + 64 * m] : 0.0f;
           }
-          if (pr == 0 && nx == nrbm)  // first exchange of the launch
-            flags[1] = (p.P <= 64 && group_on_one_xcd(p.ctrl, p.xw + gid, p.ngroups, p.P, base + 1u)) ? 1 : 0;
-          wait_lds_count(p.ctrl, &flags[0], nwc * (it + 1));
+          if (alive && pr == 0 && nx == nrbm &&  // first exchange of the launch
+              p.P <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, p.P, base + 1u, alive))
+            __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
           uint64_t v[MPR];
-          const uint32_t valid =
-              poll_row_words<MPR>(p.ctrl, p.xh + ((int64_t)((st2 - 1) & 1) * p.Bp + row) * H, H, base + (uint32_t)st2, v);
+          uint32_t valid = 0;
+          if (alive)
+            valid = poll_row_words<MPR>(ctrl, p.xh + ((int64_t)((st2 - 1) & 1) * p.Bp + row) * H, H,
+                                        base + (uint32_t)st2, v, alive);
+          if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           float* hs = hst + (nx & 1) * 3 * p.hsz;
           static_for<0, MPR>([&](auto I) {
             if ((valid >> I) & 1u) {
@@ -311,7 +323,7 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
       lds_barrier();
     }
   }
-  leave_grid(p.ctrl, (uint32_t)p.nwg, base, (uint32_t)T);
+  leave_grid(ctrl, (uint32_t)p.nwg, base, (uint32_t)T, &flags[1], 2);
 }
 
 typedef void (*BFn)(BParams);
@@ -503,7 +515,7 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   p.dh0 = a->dh0;
   p.xh = xh;
   p.xw = xw;
-  p.ctrl = ctrl_of(ws);
+  p.ctrl = ctrl_of(ws, a->fault_mirror);
   p.T = T;
   p.B = B;
   p.H = H;

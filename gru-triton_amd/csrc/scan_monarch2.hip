@@ -74,11 +74,13 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
   float* hk = zst + 3 * 256;            // [RB][4][U]   raw h of this workgroup's units
   float* gst = hk + p.RB * 4 * U;       // [2][4][3][U] staged gi
   int* flags = reinterpret_cast<int*>(gst + 24 * U);  // [0] compute-wave iterations published,
-                                                      // [1] group on one XCD
+                                                      // [1] bit 0: group on one XCD, bit 1: a
+                                                      // wait of this workgroup gave up
   const int lds_floats = 2 * p.hsz + 3 * 256 + p.RB * 4 * U + 24 * U + 4;
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
   const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const Ctrl ctrl = launch_ctrl(p.ctrl, base);
   if (threadIdx.x == 0) st_tagged(p.xw + blockIdx.x, __uint_as_float(xcc_id()), base + 1u);
   const int niter = p.T * nrbm;
   lds_barrier();
@@ -178,16 +180,19 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       const int row = 4 * rb + s;
       const float* gs_ = gst + buf * 12 * U + s * 3 * U + ie;
       float* hkp = hk + (rbl * 4 + s) * U + ie;
+      // after a give-up the workgroup's outputs are NaN and it publishes nothing more
+      const int fl = __builtin_amdgcn_readfirstlane(flags[1]);
+      const bool dead = (fl & 2) != 0;
       if (lead) {
         const float hprev = *hkp;
         float hn = gru_update_gb(gs_[0], gs_[U], gs_[2 * U], gh[0], gh[1], gh[2], bias[0], bias[1], bias[2], hprev);
         if (p.qout.on) hn = fake_quant(hn, p.qout);
-        if (row < p.B) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = hn;
+        if (row < p.B) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = dead ? __builtin_nanf("") : hn;
         *hkp = hn;
-        if (t + 1 < p.T) {
+        if (t + 1 < p.T && !dead) {
           const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
           uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * H + lane_xh;
-          if (t >= 1 && flags[1] != 0)
+          if (t >= 1 && (fl & 1) != 0)
             st_tagged_xcd(dst, hq, base + (uint32_t)t + 1u);
           else
             st_tagged(dst, hq, base + (uint32_t)t + 1u);
@@ -200,6 +205,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
     // Poller wave pr stages row pr of iteration it + 1 (see the dense kernel).
     const int pr = wave - nwc;
     constexpr int NGI = (3 * 64 + 63) / 64;  // 3 U <= 192 gate inputs per row
+    bool alive = true;  // no wait of this wave has given up
     for (int it = 0; it < niter; ++it) {
       const int nx = it + 1;
       const bool more = nx < niter;
@@ -227,19 +233,22 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
             hs[il_index(pr, k)] = v;
           }
         } else {
-          if (pr == 0 && nx == nrbm)  // first exchange of the launch
-            flags[1] = (nb <= 64 && group_on_one_xcd(p.ctrl, p.xw + gid, p.ngroups, nb, base + 1u)) ? 1 : 0;
-          wait_lds_count(p.ctrl, &flags[0], nwc * (it + 1));
+          if (alive && pr == 0 && nx == nrbm &&  // first exchange of the launch
+              nb <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, nb, base + 1u, alive))
+            __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
           const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * H;
           const uint32_t tag = base + (uint32_t)t2;
           // H words of row pr in chunks of 512 (a chunk starting at k0 fills
           // the interleaved block from il_index(0, k0) = 4 k0)
-          if (H <= 256) {
-            poll_row_il<4>(p.ctrl, hb, hs, pr, H, tag);
+          if (!alive) {
+          } else if (H <= 256) {
+            poll_row_il<4>(ctrl, hb, hs, pr, H, tag, alive);
           } else {
-            for (int k0 = 0; k0 < H; k0 += 512)
-              poll_row_il<8>(p.ctrl, hb + k0, hs + 4 * k0, pr, min(512, H - k0), tag);
+            for (int k0 = 0; k0 < H && alive; k0 += 512)
+              poll_row_il<8>(ctrl, hb + k0, hs + 4 * k0, pr, min(512, H - k0), tag, alive);
           }
+          if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
 #pragma unroll
@@ -251,7 +260,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       lds_barrier();
     }
   }
-  leave_grid(p.ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T);
+  leave_grid(ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T, &flags[1], 2);
 }
 
 struct M2Params {
@@ -274,12 +283,14 @@ struct M2Params {
 };
 
 // Polls `words` tagged words of one exchange slice into LDS, MW per thread and pass.
-// Word w maps to (src offset, LDS offset) through addr(w, &src, &dst).
+// Word w maps to (src offset, LDS offset) through addr(w, &src, &dst). `ok`
+// turns false when a wait gave up; a thread whose `ok` is already false polls
+// nothing.
 template <int MW, typename Map>
 __device__ __forceinline__ void stage_words(const Ctrl& c, const uint64_t* base, int words, uint32_t tag, float* lds,
-                                            Map map) {
+                                            Map map, bool& ok) {
   const int tid = threadIdx.x, nth = blockDim.x;
-  for (int c0 = 0; c0 < words; c0 += MW * nth) {
+  for (int c0 = 0; c0 < words && ok; c0 += MW * nth) {
     int src[MW], dst[MW];
     uint32_t valid = 0;
 #pragma unroll
@@ -289,7 +300,7 @@ __device__ __forceinline__ void stage_words(const Ctrl& c, const uint64_t* base,
       map(ok ? w : 0, src[i], dst[i]);
       valid |= (ok ? 1u : 0u) << i;
     }
-    poll_to_lds<MW>(c, base, src, dst, valid, tag, lds);
+    ok = poll_to_lds<MW>(c, base, src, dst, valid, tag, lds);
   }
 }
 
@@ -315,7 +326,8 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
 
   float* hst = lds;             // [2][4][rs]
   float* zst = lds + 8 * p.rs;  // [2][12][rs]
-  for (int i = threadIdx.x; i < 32 * p.rs; i += blockDim.x) lds[i] = 0.0f;
+  int* dead = reinterpret_cast<int*>(lds + 32 * p.rs);  // a wait of this workgroup gave up
+  for (int i = threadIdx.x; i < 32 * p.rs + 1; i += blockDim.x) lds[i] = 0.0f;
   lds_barrier();
 
   float wr[3][KC], wl[3][KC];
@@ -330,6 +342,8 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
   for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? gate_scale(g) * p.bh[g * p.H + unit] : 0.0f;  // for gru_update_gb
 
   const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const Ctrl ctrl = launch_ctrl(p.ctrl, base);
+  bool alive = true;  // no wait of this thread has given up
   const int rb_begin = gid * p.RB;
   const int rb_end = min(rb_begin + p.RB, p.nrb);
   int hbuf = 0, zbuf = 0;
@@ -366,13 +380,16 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
         }
       } else {
         const uint64_t* hb = p.xh + ((int64_t)((t - 1) & 1) * Bp + 4 * rb) * H;
-        stage_words<MWH>(p.ctrl, hb, 4 * bs, tag - 1u, hs, [&](int w, int& src, int& dst) {
+        stage_words<MWH>(ctrl, hb, 4 * bs, tag - 1u, hs, [&](int w, int& src, int& dst) {
           const int r = w / bs, k = w - r * bs;
           src = r * H + klo + k;
           dst = r * rs + k;
-        });
+        }, alive);
+        if (!alive) *dead = 1;
       }
       lds_barrier();
+      // after a give-up the workgroup's outputs are NaN and it publishes nothing more
+      const bool wg_dead = __builtin_amdgcn_readfirstlane(*dead) != 0;
       float a[3][KC];
       lds_a<KC>(hs + j * rs, kb4, a[0]);
       f4 acc[3];
@@ -380,7 +397,7 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
       float gh[3];
 #pragma unroll
       for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
-      if (pub) {
+      if (pub && !wg_dead) {
 #pragma unroll
         for (int g = 0; g < 3; ++g) st_tagged(p.xz + ((int64_t)((t & 1) * 3 + g) * Bp + row) * H + vi, gh[g], tag);
       }
@@ -388,14 +405,16 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
       float* zs = zst + zbuf * 12 * rs;
       zbuf ^= 1;
       const uint64_t* zb = p.xz + (int64_t)(t & 1) * 3 * Bp * H + (int64_t)4 * rb * H;
-      stage_words<MWZ>(p.ctrl, zb, 12 * bs, tag, zs, [&](int w, int& src, int& dst) {
+      stage_words<MWZ>(ctrl, zb, 12 * bs, tag, zs, [&](int w, int& src, int& dst) {
         const int gr = w / bs, k = w - gr * bs;
         const int idx = wg_blk * bs + k;
         const int zpos = (idx % nb) * bs + idx / nb;
         src = ((gr >> 2) * Bp + (gr & 3)) * H + zpos;
         dst = gr * rs + k;
-      });
+      }, alive);
+      if (!alive) *dead = 1;
       lds_barrier();
+      const bool wg_dead2 = __builtin_amdgcn_readfirstlane(*dead) != 0;
 #pragma unroll
       for (int g = 0; g < 3; ++g) lds_a<KC>(zs + (g * 4 + j) * rs, kb4, a[g]);
       mfma3<KC, false>(a, wl, acc);
@@ -404,14 +423,14 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
 
       float hn = gru_update_gb(gir, giz, gin, gh[0], gh[1], gh[2], bias[0], bias[1], bias[2], hprev);
       if (p.qout.on) hn = fake_quant(hn, p.qout);
-      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = hn;
-      if (pub && t + 1 < p.T) {
+      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + unit] = wg_dead2 ? __builtin_nanf("") : hn;
+      if (pub && t + 1 < p.T && !wg_dead2) {
         const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
         st_tagged(p.xh + ((int64_t)(t & 1) * Bp + row) * H + unit, hq, tag);
       }
     }
   }
-  leave_grid(p.ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T);
+  leave_grid(ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T, dead, 1);
 }
 
 typedef void (*M2Fn)(M2Params);
@@ -449,7 +468,7 @@ int plan_m2(const gs_args* a, M2Plan* pl, const char* who) {
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
   pl->rs = 16 * pl->KC + 4;
-  pl->lds = (size_t)32 * pl->rs * sizeof(float);
+  pl->lds = (size_t)(32 * pl->rs + 1) * sizeof(float);
   pl->xh_bytes = align256(2 * (int64_t)pl->Bp * a->H * 8);
   pl->xz_bytes = align256(6 * (int64_t)pl->Bp * a->H * 8);
   return GS_OK;
@@ -516,7 +535,7 @@ int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const cha
   p.bh = a->bh;
   p.out = a->out;
   char* ws = static_cast<char*>(a->workspace);
-  p.ctrl = ctrl_of(ws);
+  p.ctrl = ctrl_of(ws, a->fault_mirror);
   p.xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
   p.xw = reinterpret_cast<uint64_t*>(ws + kCtrlBytes + pl.xh_bytes);
   p.sg_t = a->sg_t;
@@ -588,7 +607,7 @@ int run_monarch2(const gs_args* a, hipStream_t stream, const char* who) {
   p.bh = a->bh;
   p.out = a->out;
   char* ws = static_cast<char*>(a->workspace);
-  p.ctrl = ctrl_of(ws);
+  p.ctrl = ctrl_of(ws, a->fault_mirror);
   p.xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
   p.xz = reinterpret_cast<uint64_t*>(ws + kCtrlBytes + pl.xh_bytes);
   p.sg_t = a->sg_t;

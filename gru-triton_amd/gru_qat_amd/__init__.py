@@ -22,7 +22,7 @@ from .scan_butterfly import (
 )
 from .scan_diagonal import extract_diagonal_factors, gru_scan_diagonal, gru_scan_diagonal_forward
 from .scan_monarch import extract_monarch_factors, gru_scan_monarch, gru_scan_monarch_forward
-from ._lib import load as load_library, workspace_faults
+from ._lib import PersistentScanFault, check_faults, load as load_library, workspace_faults
 from .gru_layer import ScanLayer, fast_dispatch_eligible, forward_fast_dispatch, layer_forward, resolve_use_triton
 from .input_proj import input_projection, quantize_input_weights
 from .quantizers import FakeQuantizePerTensor, QuantizerConfig
@@ -65,4 +65,6 @@ __all__ = [
     "quantize_rows",
     "resolve_use_triton",
     "workspace_faults",
+    "check_faults",
+    "PersistentScanFault",
 ]

@@ -55,7 +55,7 @@ EXPORTS = (
     "gs_abi_version",
 )
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 QuantTuple = Optional[Tuple[float, int, int]]
 
@@ -79,6 +79,7 @@ class GsArgs(ctypes.Structure):
         ("out", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_int64),
+        ("fault_mirror", ctypes.c_void_p),
         ("T", ctypes.c_int64),
         ("B", ctypes.c_int64),
         ("H", ctypes.c_int64),
@@ -112,6 +113,7 @@ class GsBwdArgs(ctypes.Structure):
         ("dbh_part", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_int64),
+        ("fault_mirror", ctypes.c_void_p),
         ("scratch", ctypes.c_void_p),
         ("scratch_bytes", ctypes.c_int64),
         ("T", ctypes.c_int64),
@@ -355,6 +357,66 @@ _ws_steps: dict = {}
 _ws_lock = threading.Lock()
 _TAG_LIMIT = (1 << 32) - (1 << 24)
 
+# ---- fault mirrors and cross-stream order of persistent launches -------------------
+# Each (device, stream) has one pinned host word (torch's pinned allocator is
+# hipHostMalloc) that the persistent kernels' last workgroup writes when a
+# bounded wait of the launch gave up. The next persistent launch on that
+# stream reads it (a host memory read, no synchronisation) and raises
+# RuntimeError, so a launch that ran out of its wait cannot pass unnoticed;
+# its output is NaN from the failed step on in any case.
+_mirrors: dict = {}
+
+
+class PersistentScanFault(RuntimeError):
+    """A persistent scan launched earlier on this stream gave up a bounded
+    wait: its workgroups were not all resident at once (another kernel held
+    the device's CUs), and its output is NaN from the failed step on."""
+
+
+def _mirror(dev: torch.device, stream_handle: int):
+    key = (dev.index, stream_handle)
+    m = _mirrors.get(key)
+    if m is None:
+        t = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        m = _mirrors[key] = (t, t.numpy())
+    return m
+
+
+def _raise_if_faulted(m, what: str) -> None:
+    if m[1][0] != 0:
+        value = int(m[1][0])
+        m[1][0] = 0
+        raise PersistentScanFault(
+            f"{what}: a persistent scan launched earlier on this stream ran out of its bounded wait "
+            f"(fault value {value}); its output is invalid (NaN from the failed step on). Another kernel "
+            "holding the device's compute units while the scan ran is the usual cause.")
+
+
+def check_faults(device: Optional[torch.device] = None) -> None:
+    """Raises PersistentScanFault if a completed persistent launch on any
+    stream of ``device`` (all devices when None) gave up a wait. Reads the
+    host mirrors only: launches still running are not covered (use
+    ``workspace_faults``, which synchronises, for those)."""
+    for (dev, _), m in list(_mirrors.items()):
+        if device is None or device.index == dev:
+            _raise_if_faulted(m, "check_faults")
+
+
+# Persistent scans on one device run one at a time: their grids fill the
+# device, and two of them running at once would each wait for workgroups the
+# other holds until their bounded waits give up. Launches on one stream are
+# ordered already; when a persistent launch goes on a stream other than the
+# device's previous one, that stream first waits for everything queued on the
+# previous stream (torch's wait_stream: one event, recorded only on a switch).
+_last_stream: dict = {}
+
+
+def _order_after_previous(dev: torch.device, stream: "torch.cuda.Stream") -> None:
+    prev = _last_stream.get(dev.index)
+    if prev is not None and prev.cuda_stream != stream.cuda_stream:
+        stream.wait_stream(prev)
+    _last_stream[dev.index] = stream
+
 
 def workspace(device: torch.device, stream_handle: int, nbytes: int, steps: int = 0) -> torch.Tensor:
     key = (device.index, stream_handle)
@@ -376,7 +438,8 @@ def workspace(device: torch.device, stream_handle: int, nbytes: int, steps: int 
 
 
 def workspace_faults(device: Optional[torch.device] = None) -> int:
-    """Read and clear the fault word of every cached workspace (synchronises).
+    """Read and clear the fault word of every cached workspace and its host
+    mirror (synchronises each stream); returns how many were set.
 
     Nonzero means a persistent kernel ran out of its bounded wait and the output
     of that launch is invalid.
@@ -393,6 +456,9 @@ def workspace_faults(device: Optional[torch.device] = None) -> int:
         if rc < 0:
             raise_for(rc, lib)
         total += rc
+        m = _mirrors.get((dev, stream_handle))
+        if m is not None:
+            m[1][0] = 0
     return total
 
 
@@ -421,7 +487,7 @@ def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: to
     lib = _lib if _lib is not None else load()
     T, B, threeH = gi.shape
     a = GsArgs(gi.data_ptr(), h0.data_ptr(), w.data_ptr(), w2.data_ptr() if w2 is not None else None,
-               bh.data_ptr(), out.data_ptr(), None, 0, T, B, threeH // 3, gi.stride(0), gi.stride(1),
+               bh.data_ptr(), out.data_ptr(), None, 0, None, T, B, threeH // 3, gi.stride(0), gi.stride(1),
                h0.stride(0), out.stride(0), out.stride(1), nblocks, blksz, log_n, bfly_nblocks,
                make_quant(h_in_quant, "h_in_quant"), make_quant(h_out_quant, "h_out_quant"))
     tagged = kind in (KIND_DENSE, KIND_MONARCH)
@@ -441,10 +507,16 @@ def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: to
 
 
 def _launch_current(lib: ctypes.CDLL, fn_name: str, a: "GsArgs", dev: torch.device, need: int, steps: int) -> int:
-    handle = torch.cuda.current_stream().cuda_stream
+    stream = torch.cuda.current_stream()
+    handle = stream.cuda_stream
     ws = workspace(dev, handle, int(need), steps=steps)
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws.numel()
+    if steps:  # a persistent kernel: fault mirror and cross-stream order
+        m = _mirror(dev, handle)
+        _raise_if_faulted(m, fn_name)
+        _order_after_previous(dev, stream)
+        a.fault_mirror = m[0].data_ptr()
     return _entry(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
 
 
@@ -483,11 +555,16 @@ def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w
     if scratch_need < 0:
         raise_for(int(scratch_need), lib)
     with torch.cuda.device(gi.device):
-        handle = torch.cuda.current_stream(gi.device).cuda_stream
+        stream = torch.cuda.current_stream(gi.device)
+        handle = stream.cuda_stream
         if need > 0:
             ws = workspace(gi.device, handle, int(need), steps=T)
             a.workspace = ws.data_ptr()
             a.workspace_bytes = ws.numel()
+            m = _mirror(gi.device, handle)
+            _raise_if_faulted(m, fn_name)
+            _order_after_previous(gi.device, stream)
+            a.fault_mirror = m[0].data_ptr()
         scratch = None
         if scratch_need > 0:
             # plain scratch from torch's stream-aware caching allocator

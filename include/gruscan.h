@@ -28,7 +28,12 @@
  * once (occupancy x CUs) and launched as an ordinary kernel. A kernel on
  * another stream that holds CUs delays part of the grid; every wait is
  * bounded, and a wait that runs out sets the workspace fault word (see
- * gs_workspace_status) instead of hanging.
+ * gs_workspace_status) instead of hanging. The fault is scoped to the launch
+ * (a later launch's waits are not cut short by it) and never silent: every
+ * output element the launch wrote after the failed wait is NaN, and, when
+ * the caller passes fault_mirror, the launch's last workgroup stores the
+ * nonzero fault value into that host-visible word as the launch ends, so the
+ * host can check it without synchronising.
  *
  * Return codes: GS_OK, or a negative GS_ERR_* value; gs_last_error() then
  * returns a message for the calling thread.
@@ -56,7 +61,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 1
+#define GS_ABI_VERSION 2
 
 #define GS_OK 0
 #define GS_ERR_INVALID (-1)  /* bad pointer, shape, stride or quant parameter (Python: ValueError) */
@@ -94,6 +99,9 @@ typedef struct gs_args {
   float* out;       /* [T, B, H];  strides so_t, so_b, 1                                    */
   void* workspace;  /* gs_workspace_bytes() bytes, 256-byte aligned, zero on first use     */
   int64_t workspace_bytes;
+  uint32_t* fault_mirror; /* optional host-visible word (hipHostMalloc memory) or NULL: a
+                             persistent launch whose wait gave up stores its nonzero fault
+                             value there when it ends; the caller clears it                 */
   int64_t T, B, H;
   int64_t sg_t, sg_b, sh0_b, so_t, so_b;
   int64_t nblocks, blksz;      /* Monarch: nblocks * blksz == H                             */
@@ -118,8 +126,9 @@ int gs_butterfly_fwd_generic(const gs_args* args, hipStream_t stream);
 int64_t gs_workspace_bytes(int kind, const gs_args* args);
 
 /* Reads and clears the device-side fault word of a workspace (nonzero means a
- * persistent kernel ran out of its bounded wait and its output is invalid).
- * Synchronises the stream. Returns the word, or a negative GS_ERR_* value. */
+ * persistent kernel ran out of its bounded wait and its output is invalid; the
+ * value is that launch's tag base + 1). Synchronises the stream. Returns 1 if
+ * the word was set, 0 if not, or a negative GS_ERR_* value. */
 int gs_workspace_status(void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /* ---- backward ------------------------------------------------------------------
@@ -153,6 +162,7 @@ typedef struct gs_bwd_args {
   void* workspace;     /* tagged exchange words: as the forward's workspace (zeroed    *
                         * once, may be shared with forward launches on one stream)   */
   int64_t workspace_bytes;
+  uint32_t* fault_mirror; /* as gs_args.fault_mirror                                */
   void* scratch;       /* plain scratch (no initial contents required), 256-byte    *
                         * aligned; never shared with a workspace, whose tag words    *
                         * must not see arbitrary float data                          */

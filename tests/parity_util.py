@@ -44,7 +44,8 @@ def assert_fp32_parity(cfg: Dict[str, object], dev: torch.device, tol: float = F
 
 
 def assert_quant_parity(cfg: Dict[str, object], dev: torch.device, prequant_tol: float = 2e-6,
-                        max_flip_frac: float = 1e-3) -> Dict[str, float]:
+                        max_flip_frac: float = 1e-3, free_bound: Optional[float] = None,
+                        min_clipped: int = 0) -> Dict[str, float]:
     """Bit-exact codes wherever the pre-quant fp32 values agree.
 
     Step by step (teacher forcing): the oracle recomputes the pre-q_out state of
@@ -53,6 +54,14 @@ def assert_quant_parity(cfg: Dict[str, object], dev: torch.device, prequant_tol:
     equal the oracle's code exactly; within that band a one-code difference is
     allowed (the two fp32 pre-quant values may straddle the boundary). The
     kernel's output must also be exactly code * scale.
+
+    Free running (kernel and oracle each on their own trajectory): a flip near
+    a boundary moves the next step's pre-quant values of every unit the map
+    mixes it into, so later codes may differ too. ``free_bound`` bounds that
+    divergence, max |out - oracle|, in quantization steps (scale units); with
+    no flip the two trajectories must be identical. ``min_clipped`` asserts
+    that the in-scan clamp fired at least that many times (codes past qmin or
+    qmax before the clamp).
     """
     q = cfg["h_out_quant"]
     assert q is not None
@@ -76,10 +85,20 @@ def assert_quant_parity(cfg: Dict[str, object], dev: torch.device, prequant_tol:
     flips = int(mism.sum())
     frac = flips / mism.numel()
     free_diff = int((out != ref_free).sum())
+    free_steps = (out - ref_free).abs().max().item() / q[0]
+    n_clipped = int(clipped.sum())
     log(f"[parity]   teacher-forced code flips={flips} ({frac:.2e}), all within {prequant_tol:.0e} of a "
-        f"boundary; clipped={int(clipped.sum())}; free-running elements differing={free_diff}")
+        f"boundary; clipped={n_clipped}; free-running: {free_diff} elements differ "
+        f"({free_diff / out.numel():.2e}), max {free_steps:.2f} steps")
     assert frac <= max_flip_frac
-    return {"flips": flips, "free_diff": free_diff}
+    assert n_clipped >= min_clipped, f"the in-scan clamp fired {n_clipped} times, expected >= {min_clipped}"
+    if free_bound is not None:
+        assert free_steps <= free_bound, f"free-running divergence {free_steps:.2f} steps > {free_bound}"
+    if flips == 0:
+        # every step's code equals the oracle's given the same h_{t-1}, so by
+        # induction from h0 the free-running trajectories are identical
+        assert free_diff == 0, f"no teacher-forced flip, yet {free_diff} free-running elements differ"
+    return {"flips": flips, "free_diff": free_diff, "free_steps": free_steps, "clipped": n_clipped}
 
 
 def small_cfg(idx: int, shape, seed: int = 0, **over) -> Dict[str, object]:
