@@ -427,3 +427,89 @@ extern "C" int gs_monarch_fwd(const gs_args* a, hipStream_t stream) {
   if (gs::monarch1_local_ok(a)) return gs::run_monarch1_local(a, stream);
   return gs::run(gs::kMonarch1, a, stream, who);
 }
+
+// ---- dense forward without a caller workspace ----------------------------------------
+// For callers that cannot allocate device memory (code under HIP graph capture,
+// tight serving loops, harnesses that forbid hipMalloc): the dense forward's
+// exchange workspace comes from this file-scope device array instead of the
+// caller. Each GPU the library runs on holds its own copy until the process
+// ends. Host code never uses the array's name as an address: its device
+// address is looked up once per device with hipGetSymbolAddress.
+namespace gs {
+namespace {
+constexpr int64_t kStaticScratchBytes = int64_t(4) << 20;
+}  // namespace
+}  // namespace gs
+
+static __device__ __align__(256) unsigned char scratch[gs::kStaticScratchBytes];
+
+namespace gs {
+namespace {
+
+__global__ void zero_scratch(uint4* p, int64_t n16) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+struct StaticScratch {
+  void* ptr = nullptr;  // device address of `scratch` on this device
+  uint64_t steps = 0;   // scan steps issued since the array was last cleared
+  bool cleared = false;
+};
+
+std::mutex g_static_mu;
+StaticScratch g_static[64];
+
+// The device address of this device's array (looked up on its first use, with
+// the device current), cleared on first use and again before the 32-bit step
+// tags could wrap; the clear is a fill kernel queued on `stream`.
+int static_scratch(hipStream_t stream, int64_t steps, void** out, const char* who) {
+  int dev = 0;
+  GS_CHECK_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) return set_error(GS_ERR_HIP, "%s: device ordinal %d out of range", who, dev);
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  StaticScratch& s = g_static[dev];
+  if (s.ptr == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(GS_ERR_HIP, "%s: hipGetSymbolAddress(scratch) failed: %s", who, hipGetErrorString(e));
+    s.ptr = p;
+  }
+  constexpr uint64_t kTagLimit = (uint64_t(1) << 32) - (uint64_t(1) << 24);
+  if (!s.cleared || s.steps + (uint64_t)steps + 1 >= kTagLimit) {
+    hipLaunchKernelGGL(zero_scratch, dim3(256), dim3(256), 0, stream, static_cast<uint4*>(s.ptr),
+                       kStaticScratchBytes / 16);
+    GS_CHECK_HIP(hipGetLastError());
+    s.cleared = true;
+    s.steps = 0;
+  }
+  s.steps += (uint64_t)steps;
+  *out = s.ptr;
+  return GS_OK;
+}
+
+}  // namespace
+}  // namespace gs
+
+extern "C" int gs_dense_fwd_noalloc(const gs_args* a, hipStream_t stream) {
+  gs::clear_error();
+  const char* who = "gs_dense_fwd_noalloc";
+  int rc = gs::validate_common(a, who);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
+  gs::DPlan pl;
+  rc = gs::plan_dense(gs::kDense, a, &pl, who);
+  if (rc) return rc;
+  const int64_t need = gs::kCtrlBytes + pl.xh_bytes + pl.xw_bytes;
+  if (need > gs::kStaticScratchBytes)
+    return gs::set_error(GS_ERR_INVALID,
+                         "%s: this shape needs %lld bytes of exchange scratch; the static scratch holds %lld "
+                         "(use gs_dense_fwd with a caller workspace)",
+                         who, (long long)need, (long long)gs::kStaticScratchBytes);
+  gs_args b = *a;
+  rc = gs::static_scratch(stream, a->T, &b.workspace, who);
+  if (rc) return rc;
+  b.workspace_bytes = gs::kStaticScratchBytes;
+  return gs::run(gs::kDense, &b, stream, who);
+}

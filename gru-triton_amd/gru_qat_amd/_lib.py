@@ -29,6 +29,7 @@ KIND_BUTTERFLY = 3
 # Every symbol include/gruscan.h declares.
 EXPORTS = (
     "gs_dense_fwd",
+    "gs_dense_fwd_noalloc",
     "gs_diagonal_fwd",
     "gs_monarch_fwd",
     "gs_butterfly_fwd",
@@ -281,8 +282,8 @@ def load() -> ctypes.CDLL:
                 "`make -C gru-triton_amd/csrc` or __graft_entry__.build()"
             )
         lib = ctypes.CDLL(LIB_PATH)
-        for name in ("gs_dense_fwd", "gs_diagonal_fwd", "gs_monarch_fwd", "gs_butterfly_fwd",
-                     "gs_butterfly_fwd_generic"):
+        for name in ("gs_dense_fwd", "gs_dense_fwd_noalloc", "gs_diagonal_fwd", "gs_monarch_fwd",
+                     "gs_butterfly_fwd", "gs_butterfly_fwd_generic"):
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(GsArgs), ctypes.c_void_p]
             fn.restype = ctypes.c_int

@@ -115,6 +115,21 @@ int gs_diagonal_fwd(const gs_args* args, hipStream_t stream);
 int gs_monarch_fwd(const gs_args* args, hipStream_t stream);
 int gs_butterfly_fwd(const gs_args* args, hipStream_t stream);
 
+/* Dense forward that allocates nothing and takes no workspace. No counterpart
+ * in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same contract and kernels as gs_dense_fwd, except that
+ * args->workspace and args->workspace_bytes are ignored: the exchange words
+ * and control words live in a static 4 MiB device array inside the library
+ * (one per GPU, held until the process ends), which serves shapes whose
+ * gs_workspace_bytes(GS_KIND_DENSE, args) is at most 4 MiB (B * H up to about
+ * 260,000); larger shapes return GS_ERR_INVALID. The array is cleared by a
+ * fill kernel on the first call on each GPU and again before its step tags
+ * could wrap. Every call on one GPU shares that GPU's array, so calls that
+ * overlap in time on one GPU (two streams, two threads) race; issue them in
+ * order on one stream. */
+int gs_dense_fwd_noalloc(const gs_args* args, hipStream_t stream);
+
 /* Same contract as gs_butterfly_fwd, but always runs the general LDS kernel
  * (any 2^log_n <= 4096, any bfly_nblocks) instead of the register kernel that
  * gs_butterfly_fwd picks for one chain at 2^log_n in {256, 512, 1024}. No
