@@ -81,16 +81,23 @@ def _extract_h_quant_params(quantizer: Any) -> QuantTuple:
     return (value, int(quantizer.qmin), int(quantizer.qmax))
 
 
-def fast_dispatch_eligible(kind: Optional[str], gate_layout: str) -> bool:
+def fast_dispatch_eligible(kind: Optional[str], gate_layout: str, *, dense_eligible: bool = False) -> bool:
     """gru_layer.py:110-113: the hidden structure kind is diagonal, monarch or
-    butterfly and the gate layout is fused (gi is one [T, B, 3H] tensor)."""
-    return kind in FAST_DISPATCH_KINDS and gate_layout == "fused"
+    butterfly and the gate layout is fused (gi is one [T, B, 3H] tensor).
+
+    ``dense_eligible=True`` adds the dense hidden kind, which this build scans
+    with a persistent kernel of its own (the reference sends dense hidden
+    weights to its per-step loop); the default is the reference's rule."""
+    kinds = FAST_DISPATCH_KINDS + (("dense",) if dense_eligible else ())
+    return kind in kinds and gate_layout == "fused"
 
 
-def resolve_use_triton(use_triton: Any, kind: Optional[str], gate_layout: str) -> bool:
+def resolve_use_triton(use_triton: Any, kind: Optional[str], gate_layout: str, *,
+                       dense_eligible: bool = False) -> bool:
     """gru_layer.py:115-124: "auto" follows eligibility; a truthy value on an
-    ineligible configuration raises ValueError; falsy disables dispatch."""
-    eligible = fast_dispatch_eligible(kind, gate_layout)
+    ineligible configuration raises ValueError; falsy disables dispatch.
+    ``dense_eligible`` as in ``fast_dispatch_eligible``."""
+    eligible = fast_dispatch_eligible(kind, gate_layout, dense_eligible=dense_eligible)
     if use_triton == "auto":
         return eligible
     use = bool(use_triton)
@@ -208,8 +215,10 @@ class ScanLayer(torch.nn.Module):
     are not part of this build).
 
     Follows gru_layer.py: the ``use_triton`` and ``batch_first`` arguments
-    (:52-65, resolved as :110-124, except that the dense kind is eligible
-    here), ``forward`` (:153-302), ``calibrate`` (:308-336) and ``freeze``
+    (:52-65, resolved by ``resolve_use_triton`` as :110-124 with
+    ``dense_eligible=True``: the dense kind has a fast scan here, so "auto"
+    dispatches it too; a reference ``GRULayer`` keeps the reference rule),
+    ``forward`` (:153-302), ``calibrate`` (:308-336) and ``freeze``
     (:338-339).
 
     * ``kind``: "dense", "diagonal", "monarch" or "butterfly"; ``Wi_cat``
@@ -260,10 +269,7 @@ class ScanLayer(torch.nn.Module):
         if w_bits is not None and not (2 <= int(w_bits) <= 16):
             raise ValueError(f"w_bits must be in [2, 16] or None; got {w_bits}")
         self.w_quant = None if w_bits is None else (-(2 ** (int(w_bits) - 1)) + 1, 2 ** (int(w_bits) - 1) - 1)
-        if use_triton == "auto":
-            self.use_triton = True
-        else:
-            self.use_triton = bool(use_triton)
+        self.use_triton = resolve_use_triton(use_triton, kind, "fused", dense_eligible=True)
         self.batch_first = batch_first
 
     def _x_side(self, x: torch.Tensor) -> Tuple[torch.Tensor, QuantTuple]:

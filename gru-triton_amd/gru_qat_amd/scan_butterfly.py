@@ -82,7 +82,8 @@ def gru_scan_butterfly_forward_generic(gi, h0, twiddles, bh_cat, *, h_in_quant: 
                     bh_cat, h_in_quant, h_out_quant)
 
 
-def gru_scan_butterfly_backward(gi, h0, twiddles, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None):
+def gru_scan_butterfly_backward(gi, h0, twiddles, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None,
+                                **_ignored_tiling: Any):
     """Gradients (dgi, dh0, dtwiddles, dbh_cat) of the butterfly scan
     (reference backward: scan_butterfly.py:462-1075).
 
@@ -108,6 +109,10 @@ def gru_scan_butterfly_backward(gi, h0, twiddles, bh_cat, out, dout, *, h_in_qua
                     h_in_quant=check_quant(h_in_quant, "h_in_quant"),
                     h_out_quant=check_quant(h_out_quant, "h_out_quant"), log_n=log_n, bfly_nblocks=nblocks)
     return dgi, dh0, dtw, dbh_part.sum(0)
+
+
+# The reference's name for the backward launcher.
+gru_scan_butterfly_backward_triton = gru_scan_butterfly_backward
 
 
 class GRUScanButterflyTritonFunction(torch.autograd.Function):

@@ -59,7 +59,8 @@ def gru_scan_diagonal_forward(
 gru_scan_diagonal_forward_triton = gru_scan_diagonal_forward
 
 
-def gru_scan_diagonal_backward(gi, h0, Wh_diag, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None):
+def gru_scan_diagonal_backward(gi, h0, Wh_diag, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None,
+                               **_ignored_tiling: Any):
     """Gradients (dgi, dh0, dWh_diag, dbh_cat) of the diagonal scan.
 
     Mirrors the reference's backward launcher (scan_diagonal.py:285-561):
@@ -86,6 +87,10 @@ def gru_scan_diagonal_backward(gi, h0, Wh_diag, bh_cat, out, dout, *, h_in_quant
                     h_in_quant=check_quant(h_in_quant, "h_in_quant"),
                     h_out_quant=check_quant(h_out_quant, "h_out_quant"))
     return dgi, dh0, dw_part.sum(0), dbh_part.sum(0)
+
+
+# The reference's name for the backward launcher.
+gru_scan_diagonal_backward_triton = gru_scan_diagonal_backward
 
 
 class GRUScanDiagonalFunction(torch.autograd.Function):

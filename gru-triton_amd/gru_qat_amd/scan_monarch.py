@@ -89,7 +89,7 @@ gru_scan_monarch_forward_triton = gru_scan_monarch_forward
 
 
 def gru_scan_monarch_backward(gi, h0, Wh_struct, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None,
-                              Wh_struct2=None):
+                              Wh_struct2=None, **_ignored_tiling: Any):
     """Gradients (dgi, dh0, [dWh_struct(, dWh_struct2)], dbh_cat) of the
     Monarch scan (reference backward: scan_monarch.py:409-884 and :955-1053).
 
@@ -124,6 +124,10 @@ def gru_scan_monarch_backward(gi, h0, Wh_struct, bh_cat, out, dout, *, h_in_quan
                     h_out_quant=check_quant(h_out_quant, "h_out_quant"), nblocks=nblocks, blksz=blksz)
     dps = [dW] if dW2 is None else [dW, dW2]
     return dgi, dh0, dps, dbh_part.sum(0)
+
+
+# The reference's name for the backward launcher.
+gru_scan_monarch_backward_triton = gru_scan_monarch_backward
 
 
 class GRUScanMonarchFunction(torch.autograd.Function):

@@ -112,3 +112,24 @@ def test_layer_forward_argument_errors():
         layer_forward("dense", torch.zeros(0, 2, 3), None, W, None, torch.zeros(12, 4), torch.zeros(12),
                       batch_first=True)
 
+
+
+def test_dense_kind_eligible_only_when_named():
+    """One rule: the reference's (dense not eligible) unless the caller names
+    the dense extension, as ScanLayer does."""
+    assert resolve_use_triton("auto", "dense", "fused") is False
+    assert resolve_use_triton("auto", "dense", "fused", dense_eligible=True) is True
+    assert resolve_use_triton("auto", "dense", "split", dense_eligible=True) is False
+    with pytest.raises(ValueError, match="use_triton=True requires"):
+        resolve_use_triton(True, "dense", "fused")
+    assert resolve_use_triton(True, "dense", "fused", dense_eligible=True) is True
+
+
+def test_scan_layer_resolves_auto_with_the_shared_rule():
+    from gru_qat_amd.gru_layer import ScanLayer
+
+    H = 8
+    Wi = torch.zeros(3 * H, 4)
+    for kind, hidden in (("dense", torch.zeros(3 * H, H)), ("diagonal", torch.zeros(3, H))):
+        assert ScanLayer(kind, Wi, None, hidden, torch.zeros(3 * H)).use_triton is True
+        assert ScanLayer(kind, Wi, None, hidden, torch.zeros(3 * H), use_triton=False).use_triton is False

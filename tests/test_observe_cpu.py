@@ -190,7 +190,7 @@ def test_calibrate_loop_contract():
                                       "initialized": True}}
     summary = G.calibrate(m, [], only_activations=False)
     assert set(summary) == {"quant_h_in", "quant_w"} and not summary["quant_w"]["initialized"]
-    with pytest.raises(TypeError, match="unsupported type"):
+    with pytest.raises(TypeError, match="cannot feed"):
         G.calibrate(m, [3])
     G.freeze_all(m)
     assert m.quant_h_in.config.mode == "frozen" and m.quant_w.config.mode == "frozen"
