@@ -60,4 +60,12 @@ int quant_copy(float* dst, const float* src, int64_t ld, int rows, int cols, con
 int build_prev_state(float* hq, const float* h0, int64_t sh0_b, const float* out, int64_t so_b, int T, int B, int H,
                      const Quant& q, hipStream_t stream, const char* who);
 
+// Backward of a per-row dynamic symmetric fake-quant (scale = max(max |row|,
+// 1e-8) / qmax) on rows x cols, with the scale's own gradient path, as
+// torch's autograd gives it for a scale computed from the tensor: d = g plus
+// the scale terms on each row's max and min elements (struct_proj.hip).
+// y and g/d have row strides ldy and ldg/ldd, s[row] the row scales; d may alias g.
+int launch_rows_dynamic_bwd(const float* y, int64_t ldy, const float* s, const float* g, int64_t ldg, float* d,
+                            int64_t ldd, int rows, int cols, int qmin, int qmax, hipStream_t stream);
+
 }  // namespace gs

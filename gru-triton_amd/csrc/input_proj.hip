@@ -17,8 +17,10 @@
 // the row's absmax, then the codes), which also returns the per-row scales.
 // The backward follows the straight-through estimator: dx = mask_x (dgi W_q) with q_x's clipped-STE
 // mask, dW = dgi^T q_x(x) (the gradient reaching W_q; the per-row clamp never
-// clips, since every |W / scale| <= qmax), dbi = column sums of dgi. The
-// scales are treated as constants, as in the reference's frozen mode.
+// clips, since every |W / scale| <= qmax) plus, as the reference's autograd
+// has it for a scale computed from the weight itself, each row scale's
+// gradient carried to the row's max and min elements (launch_rows_dynamic_bwd,
+// struct_proj.hip); dbi = column sums of dgi. x's frozen scale is a constant.
 #include "gs_gemm.h"
 #include "gs_mfma.h"
 
@@ -201,6 +203,16 @@ extern "C" int gs_input_proj_bwd(const gs_proj_bwd_args* a, hipStream_t stream) 
   if (rc) return rc;
   if (split > 1) {
     rc = sum_partials(a->dw, part, (int64_t)N * I, split, (int64_t)N * I, stream, who);
+    if (rc) return rc;
+  }
+  if (a->q_w.enabled) {
+    // the per-row weight scales depend on the weight: add their gradient path
+    if (!a->w_raw || !a->w_scale)
+      return set_error(GS_ERR_INVALID, "%s: w_raw and w_scale must be non-NULL when the weight quant is on", who);
+    if (!(a->q_w.qmax > 0) || a->q_w.qmin > a->q_w.qmax)
+      return set_error(GS_ERR_INVALID, "%s: weight quant needs qmax > 0 and qmin <= qmax; got [%d, %d]", who,
+                       a->q_w.qmin, a->q_w.qmax);
+    rc = launch_rows_dynamic_bwd(a->w_raw, I, a->w_scale, a->dw, I, a->dw, I, N, I, a->q_w.qmin, a->q_w.qmax, stream);
     if (rc) return rc;
   }
   if (a->dbias) return colsum(a->dbias, a->dgi, a->sdgi, M, N, colp, stream, who);

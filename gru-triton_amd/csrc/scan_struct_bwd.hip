@@ -448,6 +448,44 @@ int materialize_map(const gs_map_args* a, hipStream_t stream, const char* who) {
   return GS_OK;
 }
 
+// The butterfly map of all three gates as the dense M [3H, H], keeping every
+// stage's activations A_j in acts ([3][K + 1][N][H] floats, K = nch L).
+int bfly_materialize_keep(const float* tw, int nch, int L, int H, float* acts, float* M, hipStream_t stream) {
+  const int N = 1 << L, K = nch * L;
+  const int64_t act_gate = (int64_t)(K + 1) * N * H, nstage = (int64_t)3 * N * H;
+  const int64_t tw_gate = (int64_t)nch * L * (N / 2) * 4;
+  hipLaunchKernelGGL(bfly_identity, grid_for(nstage), dim3(256), 0, stream, acts, act_gate, N, H);
+  GS_CHECK_HIP(hipGetLastError());
+  for (int j = 0; j < K; ++j) {
+    hipLaunchKernelGGL(bfly_stage_fwd, grid_for(nstage), dim3(256), 0, stream, tw, tw_gate,
+                       acts + (int64_t)j * N * H, acts + (int64_t)(j + 1) * N * H, act_gate, j, L, N, H,
+                       j == K - 1 ? M : nullptr);
+    GS_CHECK_HIP(hipGetLastError());
+  }
+  return GS_OK;
+}
+
+// Carries a dense gradient dM [3H, H] of that map onto the twiddles dtw (the
+// shape of tw), with the activations bfly_materialize_keep left in acts;
+// gbuf holds 2 * 3 N H floats.
+int bfly_project_grad(const float* tw, int nch, int L, int H, const float* acts, const float* dM, float* gbuf,
+                      float* dtw, hipStream_t stream) {
+  const int N = 1 << L, K = nch * L;
+  const int64_t act_gate = (int64_t)(K + 1) * N * H, g_gate = (int64_t)N * H, nstage = 3 * g_gate;
+  const int64_t tw_gate = (int64_t)nch * L * (N / 2) * 4;
+  float* g0 = gbuf;
+  float* g1 = gbuf + 3 * g_gate;
+  hipLaunchKernelGGL(bfly_grad_init, grid_for(nstage), dim3(256), 0, stream, dM, g0, g_gate, N, H);
+  GS_CHECK_HIP(hipGetLastError());
+  for (int j = K - 1; j >= 0; --j) {
+    hipLaunchKernelGGL(bfly_stage_bwd, dim3((unsigned)N, 3), dim3(kRowThreads), 0, stream, tw, tw_gate, acts, act_gate,
+                       g0, g1, g_gate, dtw, j, L, N, H);
+    GS_CHECK_HIP(hipGetLastError());
+    std::swap(g0, g1);
+  }
+  return GS_OK;
+}
+
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a) {
   StructPlan sp;
   const int rc = plan_struct(kind, a, &sp, "gs_bwd_workspace_bytes");

@@ -25,6 +25,7 @@ from .scan_monarch import extract_monarch_factors, gru_scan_monarch, gru_scan_mo
 from ._lib import PersistentScanFault, check_faults, load as load_library, workspace_faults
 from .gru_layer import ScanLayer, fast_dispatch_eligible, forward_fast_dispatch, layer_forward, resolve_use_triton
 from .input_proj import input_projection, quantize_input_weights
+from .struct_proj import structured_input_projection
 from .quantizers import FakeQuantizePerTensor, QuantizerConfig
 from .observe import gru_scan_observe, hidden_map_dense
 from .calibration import calibrate, freeze_all
@@ -65,6 +66,7 @@ __all__ = [
     "quantize_rows",
     "resolve_use_triton",
     "workspace_faults",
+    "structured_input_projection",
     "check_faults",
     "PersistentScanFault",
 ]

@@ -41,6 +41,10 @@ EXPORTS = (
     "gs_input_proj",
     "gs_input_proj_bwd",
     "gs_input_proj_bwd_workspace_bytes",
+    "gs_struct_input_proj",
+    "gs_struct_input_proj_scratch_bytes",
+    "gs_struct_input_proj_bwd",
+    "gs_struct_input_proj_bwd_scratch_bytes",
     "gs_quantize_rows",
     "gs_hidden_map_dense",
     "gs_hidden_map_scratch_bytes",
@@ -171,6 +175,71 @@ class GsProjBwdArgs(ctypes.Structure):
         ("sdgi", ctypes.c_int64),
         ("sdx", ctypes.c_int64),
         ("q_x", GsQuant),
+        ("w_raw", ctypes.c_void_p),
+        ("w_scale", ctypes.c_void_p),
+        ("q_w", GsQuant),
+    ]
+
+
+class GsOQuant(ctypes.Structure):
+    _fields_ = [
+        ("mode", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("qmin", ctypes.c_int32),
+        ("qmax", ctypes.c_int32),
+    ]
+
+
+class GsSProjArgs(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("gi", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("y_scale", ctypes.c_void_p),
+        ("x_q", ctypes.c_void_p),
+        ("scratch", ctypes.c_void_p),
+        ("scratch_bytes", ctypes.c_int64),
+        ("M", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("sx", ctypes.c_int64),
+        ("sgi", ctypes.c_int64),
+        ("nblocks", ctypes.c_int64),
+        ("blksz", ctypes.c_int64),
+        ("log_n", ctypes.c_int64),
+        ("bfly_nblocks", ctypes.c_int64),
+        ("q_x", GsQuant),
+        ("q_out", GsOQuant * 3),
+    ]
+
+
+class GsSProjBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("kind", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("x_q", ctypes.c_void_p),
+        ("w", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("y_scale", ctypes.c_void_p),
+        ("dgi", ctypes.c_void_p),
+        ("dx", ctypes.c_void_p),
+        ("dw", ctypes.c_void_p),
+        ("dbias", ctypes.c_void_p),
+        ("scratch", ctypes.c_void_p),
+        ("scratch_bytes", ctypes.c_int64),
+        ("M", ctypes.c_int64),
+        ("H", ctypes.c_int64),
+        ("sx", ctypes.c_int64),
+        ("sdgi", ctypes.c_int64),
+        ("sdx", ctypes.c_int64),
+        ("nblocks", ctypes.c_int64),
+        ("blksz", ctypes.c_int64),
+        ("log_n", ctypes.c_int64),
+        ("bfly_nblocks", ctypes.c_int64),
+        ("q_x", GsQuant),
+        ("q_out", GsOQuant * 3),
     ]
 
 
@@ -297,6 +366,13 @@ def load() -> ctypes.CDLL:
         lib.gs_input_proj_bwd.restype = ctypes.c_int
         lib.gs_input_proj_bwd_workspace_bytes.argtypes = [ctypes.POINTER(GsProjBwdArgs)]
         lib.gs_input_proj_bwd_workspace_bytes.restype = ctypes.c_int64
+        for name, argt in (("gs_struct_input_proj", GsSProjArgs), ("gs_struct_input_proj_bwd", GsSProjBwdArgs)):
+            run = getattr(lib, name)
+            run.argtypes = [ctypes.POINTER(argt), ctypes.c_void_p]
+            run.restype = ctypes.c_int
+            size = getattr(lib, name + "_scratch_bytes")
+            size.argtypes = [ctypes.POINTER(argt)]
+            size.restype = ctypes.c_int64
         for name, argt in (("gs_hidden_map", GsMapArgs), ("gs_observe_tensor", GsObserveTensorArgs),
                            ("gs_observe_scan", GsObserveArgs)):
             run = getattr(lib, name if name != "gs_hidden_map" else "gs_hidden_map_dense")

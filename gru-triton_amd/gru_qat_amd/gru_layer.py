@@ -182,17 +182,25 @@ def layer_forward(
     h_out_quant: QuantTuple = None,
     batch_first: bool = False,
     hidden2: Optional[torch.Tensor] = None,
+    input_kind: Optional[str] = None,
+    wi_out_quant: Any = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """GRULayer's forward on the fast dispatch with a dense input side:
+    """GRULayer's forward on the fast dispatch:
     ``x`` [T, B, I] (or [B, T, I] when ``batch_first``) -> ``(out, h_T)``.
 
     Follows gru_layer.py:169-200 (time-major x, T/B checks, zero h0) and
-    :249-302: ``gi = input_projection(x, Wi_cat, bi_cat, x_quant=..., w_quant=...)``
-    (the reference's ``quant_x`` + ``quantize_input_weights`` + ``F.linear``),
-    then the scan of ``kind`` (``forward_fast_dispatch``). Differentiable in
-    x, h0 and every weight.
+    :249-302. A dense input side (``input_kind`` None) gives
+    ``gi = input_projection(x, Wi_cat, bi_cat, x_quant=..., w_quant=...)``
+    (the reference's ``quant_x`` + ``quantize_input_weights`` + ``F.linear``,
+    :249-255); a structured one (``input_kind`` "diagonal", "monarch" or
+    "butterfly", ``Wi_cat`` then holding the stacked per-gate weights and
+    ``wi_out_quant`` the output-side quantizers) gives
+    ``gi = structured_input_projection(...)`` (``cell.structured_input_projection``,
+    :256). Then the scan of ``kind`` (``forward_fast_dispatch``).
+    Differentiable in x, h0 and every weight.
     """
     from .input_proj import input_projection
+    from .struct_proj import structured_input_projection
 
     if x.dim() != 3:
         raise ValueError(f"x must be [T, B, I] (or [B, T, I] with batch_first); got shape {tuple(x.shape)}")
@@ -203,7 +211,13 @@ def layer_forward(
         raise ValueError(f"seq length T must be > 0; got T={T}")
     if B == 0:
         raise ValueError(f"batch size B must be > 0; got B={B}")
-    gi = input_projection(x, Wi_cat, bi_cat, x_quant=x_quant, w_quant=w_quant)
+    if input_kind is None:
+        gi = input_projection(x, Wi_cat, bi_cat, x_quant=x_quant, w_quant=w_quant)
+    else:
+        if w_quant is not None:
+            raise ValueError("w_quant is the dense input side's weight quantizer; a structured input side "
+                             "quantizes its outputs (wi_out_quant)")
+        gi = structured_input_projection(x, input_kind, Wi_cat, bi_cat, x_quant=x_quant, out_quant=wi_out_quant)
     return forward_fast_dispatch(kind, gi, h0, hidden, bh_cat, h_in_quant=h_in_quant, h_out_quant=h_out_quant,
                                  batch_first=batch_first, hidden2=hidden2)
 
@@ -222,7 +236,10 @@ class ScanLayer(torch.nn.Module):
     (:338-339).
 
     * ``kind``: "dense", "diagonal", "monarch" or "butterfly"; ``Wi_cat``
-      [3H, I], ``bi_cat`` [3H] or None, ``hidden`` (and ``hidden2``) and
+      [3H, I] (or, with ``input_kind`` set, the stacked structured input
+      weights of that kind, input size H, and ``wi_out_quant`` the per-gate
+      output quantizers of ``structured_input_projection``), ``bi_cat`` [3H]
+      or None, ``hidden`` (and ``hidden2``) and
       ``bh_cat`` as in ``forward_fast_dispatch``. They become parameters.
     * ``x_quant`` and ``h_quant``: ``QuantizerConfig`` of the per-tensor
       ``quant_x`` and of ``quant_h_in`` and ``quant_h_out`` (both built from
@@ -242,13 +259,21 @@ class ScanLayer(torch.nn.Module):
     def __init__(self, kind: str, Wi_cat: torch.Tensor, bi_cat: Optional[torch.Tensor], hidden: torch.Tensor,
                  bh_cat: torch.Tensor, *, hidden2: Optional[torch.Tensor] = None, x_quant: Any = None,
                  h_quant: Any = None, w_bits: Optional[int] = None, use_triton: Any = "auto",
-                 batch_first: bool = False) -> None:
+                 batch_first: bool = False, input_kind: Optional[str] = None, wi_out_quant: Any = None) -> None:
         super().__init__()
         from .quantizers import FakeQuantizePerTensor, QuantizerConfig
 
         if kind not in ("dense",) + FAST_DISPATCH_KINDS:
             raise ValueError(f"kind must be one of dense, diagonal, monarch, butterfly; got {kind!r}")
+        if input_kind is not None and input_kind not in FAST_DISPATCH_KINDS:
+            raise ValueError(f"input_kind must be None (dense) or one of diagonal, monarch, butterfly; "
+                             f"got {input_kind!r}")
+        if input_kind is not None and w_bits is not None:
+            raise ValueError("w_bits quantizes a dense input weight; a structured input side quantizes its "
+                             "outputs (wi_out_quant)")
         self.kind = kind
+        self.input_kind = input_kind
+        self.wi_out_quant = wi_out_quant
         self.Wi_cat = torch.nn.Parameter(Wi_cat.detach().clone())
         self.bi_cat = torch.nn.Parameter(bi_cat.detach().clone()) if bi_cat is not None else None
         self.hidden = torch.nn.Parameter(hidden.detach().clone())
@@ -292,7 +317,8 @@ class ScanLayer(torch.nn.Module):
         h_out = _extract_h_quant_params(self.quant_h_out) if self.quant_h_out is not None else None
         return layer_forward(self.kind, xin, h0, self.Wi_cat, self.bi_cat, self.hidden, self.bh_cat,
                              x_quant=x_tuple, w_quant=self.w_quant, h_in_quant=h_in, h_out_quant=h_out,
-                             batch_first=self.batch_first, hidden2=self.hidden2)
+                             batch_first=self.batch_first, hidden2=self.hidden2, input_kind=self.input_kind,
+                             wi_out_quant=self.wi_out_quant)
 
     def _forward_observe(self, x: torch.Tensor, h0: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
         from .input_proj import input_projection
@@ -311,7 +337,13 @@ class ScanLayer(torch.nn.Module):
             if h0 is None:
                 h0 = x.new_zeros(B, self.hidden_size)
             xin = self.quant_x(x) if self.quant_x is not None else x
-            gi = input_projection(xin, self.Wi_cat, self.bi_cat, x_quant=None, w_quant=self.w_quant)
+            if self.input_kind is None:
+                gi = input_projection(xin, self.Wi_cat, self.bi_cat, x_quant=None, w_quant=self.w_quant)
+            else:
+                from .struct_proj import structured_input_projection
+
+                gi = structured_input_projection(xin, self.input_kind, self.Wi_cat, self.bi_cat,
+                                                 out_quant=self.wi_out_quant)
             out = gru_scan_observe(self.kind, gi, h0, self.hidden, self.bh_cat, quant_h_in=self.quant_h_in,
                                    quant_h_out=self.quant_h_out, hidden2=self.hidden2)
         h_T = out[-1]

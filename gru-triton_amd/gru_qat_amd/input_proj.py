@@ -8,9 +8,11 @@ gate weight through its per-channel quantizer, quantizers.py:188-199) and
 ``gi = F.linear(xq, Wi_cat, bi_cat)``. Here the three steps are one call of
 ``gs_input_proj`` (libgruscan.so): the per-row weight fake-quant, then one
 fp32 MFMA GEMM that fake-quantizes x as it loads it and adds the bias in its
-epilogue. The backward (``gs_input_proj_bwd``) follows the straight-through
-estimator of fake_quant_ste (ste.py:65-95) with the quantizer scales held
-constant.
+epilogue. The backward (``gs_input_proj_bwd``) follows torch's autograd of
+fake_quant_ste (ste.py:65-95): straight through the rounding, clipped at the
+clamp, x's frozen scale constant, and the per-row weight scales (computed from
+the weight, not detached, in the reference's dynamic weight quantizer)
+passing gradient to each row's max and min elements.
 """
 
 from __future__ import annotations
@@ -101,16 +103,17 @@ class InputProjectionFunction(torch.autograd.Function):
         x2 = x.reshape(-1, x.shape[-1])
         if x2.stride(-1) != 1:
             x2 = x2.contiguous()
-        gi, w_used, _, xq = _project(x2, Wi_cat, bi_cat, x_quant, w_quant)
-        ctx.save_for_backward(x2, w_used, xq)
+        gi, w_used, scales, xq = _project(x2, Wi_cat, bi_cat, x_quant, w_quant)
+        ctx.save_for_backward(x2, w_used, xq, Wi_cat if w_quant is not None else None, scales)
         ctx.x_quant = x_quant
+        ctx.w_quant = w_quant
         ctx.has_bias = bi_cat is not None
         ctx.x_shape = x.shape
         return gi.view(*x.shape[:-1], Wi_cat.shape[0])
 
     @staticmethod
     def backward(ctx: Any, dgi: torch.Tensor):  # type: ignore[override]
-        x2, w_used, xq = ctx.saved_tensors
+        x2, w_used, xq, w_raw, scales = ctx.saved_tensors
         lib = _lib.load()
         M, I = x2.shape
         N = w_used.shape[0]
@@ -127,6 +130,9 @@ class InputProjectionFunction(torch.autograd.Function):
         a.M, a.N, a.I = M, N, I
         a.sx, a.sdgi, a.sdx = x2.stride(0), dgi2.stride(0), dx.stride(0)
         a.q_x = _lib.make_quant(ctx.x_quant, "x_quant")
+        if ctx.w_quant is not None:
+            a.w_raw, a.w_scale = w_raw.data_ptr(), scales.data_ptr()
+            a.q_w = _lib.GsQuant(1, 1.0, int(ctx.w_quant[0]), int(ctx.w_quant[1]))
         need = lib.gs_input_proj_bwd_workspace_bytes(ctypes.byref(a))
         if need < 0:
             _lib.raise_for(int(need), lib)

@@ -241,13 +241,17 @@ typedef struct gs_proj_args {
 
 int gs_input_proj(const gs_proj_args* args, hipStream_t stream);
 
-/* Backward of gs_input_proj with the straight-through estimator (scales held
- * constant, as in the reference's frozen mode): dx = mask_x (dgi w), with q_x's
- * clipped-STE mask; dw = dgi^T q_x(x), the gradient reaching the weight that
- * was used (w_q when q_w was on; the per-row clamp never clips); dbias = the
- * column sums of dgi (skipped when NULL). No reference counterpart as one call:
- * the reference gets these from autograd through F.linear and
- * fake_quant_ste. */
+/* Backward of gs_input_proj with the straight-through estimator of
+ * fake_quant_ste (ste.py:65-95): dx = mask_x (dgi w), with q_x's clipped-STE
+ * mask (its frozen scale is a constant); dw = dgi^T q_x(x), the gradient
+ * reaching the weight that was used, and, when the per-row weight quant was on
+ * (q_w.enabled, with w_raw and w_scale), also the path through each row's
+ * scale, which the reference's dynamic per-channel weight quantizer computes
+ * from the weight without detaching it (quantizers.py:188-199): the row's
+ * dL/ds = sum_i dw_q[n][i] (q[n][i] - w[n][i] / s[n]) carried to its max and
+ * min elements (the per-row clamp never clips); dbias = the column sums of
+ * dgi (skipped when NULL). No reference counterpart as one call: the
+ * reference gets these from autograd through F.linear and fake_quant_ste. */
 typedef struct gs_proj_bwd_args {
   const float* x;     /* [M, I], row stride sx                                       */
   const float* w;     /* [N, I] contiguous: the weight the forward used              */
@@ -262,10 +266,90 @@ typedef struct gs_proj_bwd_args {
   int64_t M, N, I;
   int64_t sx, sdgi, sdx;
   gs_quant q_x;
+  const float* w_raw;   /* [N, I] contiguous: the weight before its fake-quant (q_w on)  */
+  const float* w_scale; /* [N] the forward's per-row scales (q_w on)                     */
+  gs_quant q_w;         /* per-row weight fake-quant of the forward: enabled, qmin, qmax */
 } gs_proj_bwd_args;
 
 int64_t gs_input_proj_bwd_workspace_bytes(const gs_proj_bwd_args* args);
 int gs_input_proj_bwd(const gs_proj_bwd_args* args, hipStream_t stream);
+
+/* ---- structured input projection -------------------------------------------------
+ * The producer of gi when the cell's input side is structured (reference
+ * GRUCellQuant.structured_input_projection, src/gru_qat/gru_cell.py:466-503,
+ * taken by GRULayer._forward_fast_dispatch at gru_layer.py:256): for gates
+ * g = r, z, n,
+ *   gi[m][g H + j] = oq_g(map_g(q_x(x[m])))[j] + bias[g H + j]
+ * with map_g the gate's structured input weight (struct_Wi_g; input size ==
+ * hidden size H), oq_g its output-side fake-quant (quant_struct_Wi_g, applied
+ * to the map's output before the bias) and q_x a frozen per-tensor fake-quant.
+ * Kinds: diagonal (w [3, H], y = w_g * x), Monarch single factor (w [3,
+ * nblocks, blksz, blksz] as (out, in), one block-diagonal product) and
+ * butterfly (twiddles [3, bfly_nblocks, log_n, 2^log_n / 2, 2, 2], the
+ * stages of the hidden-side kind). Output quantizer modes: */
+#define GS_OQ_OFF 0          /* identity                                                     */
+#define GS_OQ_FROZEN 1       /* per tensor, the given scale (a frozen FakeQuantizePerTensor)  */
+#define GS_OQ_DYNAMIC_ROWS 2 /* symmetric, one scale per row m of the gate's output:
+                                max(max_j |y[m][j]|, 1e-8) / qmax -- FakeQuantizePerChannel on
+                                axis 0 in dynamic mode (quantizers.py:124-134, 188-199), the
+                                reference's default weight recipe (quantizers.py:292)         */
+
+typedef struct gs_oquant {
+  int32_t mode;  /* GS_OQ_*                                                              */
+  float scale;   /* GS_OQ_FROZEN                                                         */
+  int32_t qmin, qmax;
+} gs_oquant;
+
+typedef struct gs_sproj_args {
+  int32_t kind;       /* GS_KIND_DIAGONAL, GS_KIND_MONARCH or GS_KIND_BUTTERFLY           */
+  const float* x;     /* [M, H], row stride sx                                            */
+  const float* w;     /* the three gates' input-side weights, layout of gs_args.w         */
+  const float* bias;  /* [3H] (b_ir, b_iz, b_in) or NULL                                  */
+  float* gi;          /* [M, 3H] output, row stride sgi                                   */
+  float* y;           /* [M, 3H] contiguous: map outputs before the output fake-quant;
+                         required when any gate's quantizer is on (the backward reads it) */
+  float* y_scale;     /* [3, M]: per-row scales of GS_OQ_DYNAMIC_ROWS gates, else NULL    */
+  float* x_q;         /* [M, H] contiguous q_x(x), required when q_x is on                */
+  void* scratch;      /* gs_struct_input_proj_scratch_bytes() bytes, 256-byte aligned     */
+  int64_t scratch_bytes;
+  int64_t M, H, sx, sgi;
+  int64_t nblocks, blksz, log_n, bfly_nblocks;
+  gs_quant q_x;
+  gs_oquant q_out[3];
+} gs_sproj_args;
+
+int64_t gs_struct_input_proj_scratch_bytes(const gs_sproj_args* args);
+int gs_struct_input_proj(const gs_sproj_args* args, hipStream_t stream);
+
+/* Backward with the straight-through estimator of fake_quant_ste (ste.py:65-95):
+ * q_x and frozen output quantizers pass the gradient where they did not clip;
+ * a dynamic per-row output quantizer also passes it through its scale, as the
+ * reference's autograd does (the scale is computed from the tensor, not
+ * detached): dL/ds = sum_j g_j (q_j - y_j / s), carried to the row's max and
+ * min elements through max(|max|, |min|) / qmax (ties shared as torch's amax,
+ * amin and maximum share them). dbias = column sums of dgi. No reference
+ * counterpart as one call: the reference gets these from autograd. */
+typedef struct gs_sproj_bwd_args {
+  int32_t kind;
+  const float* x;     /* [M, H], row stride sx                                            */
+  const float* x_q;   /* the forward's x_q when q_x is on                                 */
+  const float* w;
+  const float* y;     /* the forward's y when any output quantizer is on                  */
+  const float* y_scale; /* the forward's y_scale when a gate is GS_OQ_DYNAMIC_ROWS        */
+  const float* dgi;   /* [M, 3H], row stride sdgi                                         */
+  float* dx;          /* [M, H], row stride sdx                                           */
+  float* dw;          /* gradient of w (same shape)                                       */
+  float* dbias;       /* [3H] or NULL                                                     */
+  void* scratch;      /* gs_struct_input_proj_bwd_scratch_bytes() bytes, 256-byte aligned */
+  int64_t scratch_bytes;
+  int64_t M, H, sx, sdgi, sdx;
+  int64_t nblocks, blksz, log_n, bfly_nblocks;
+  gs_quant q_x;
+  gs_oquant q_out[3];
+} gs_sproj_bwd_args;
+
+int64_t gs_struct_input_proj_bwd_scratch_bytes(const gs_sproj_bwd_args* args);
+int gs_struct_input_proj_bwd(const gs_sproj_bwd_args* args, hipStream_t stream);
 
 /* ---- per-row weight codes (int8 export) -------------------------------------------
  * Per-row symmetric quantization of a weight w [rows, cols] with the rule of

@@ -29,8 +29,17 @@ Functions and what they follow (reference file:line):
                    and :124-134 (symmetric: scale = max(|max|, |min|).clamp(1e-8) / qmax,
                    zp = 0), then ste.py:65-95
   input_projection gru_layer.py:249-255 (xq = quant_x(x); Wi_cat = quantize_input_weights();
-                   gi = F.linear(xq, Wi_cat, bi_cat)); with ste=True the straight-through
-                   gradients (clipped STE on x, scales held constant)
+                   gi = F.linear(xq, Wi_cat, bi_cat)); with ste=True torch's autograd of the
+                   reference quantizers: clipped STE on x (frozen scale), and the dynamic
+                   per-row weight quantizer through fake_quant_rows_dynamic
+  fake_quant_rows_dynamic
+                   FakeQuantizePerChannel on axis 0 in dynamic mode (quantizers.py:188-199,
+                   :124-134) into fake_quant_ste (ste.py:17-95, STERound / STEClamp): the scale
+                   is computed from the tensor and not detached, so autograd carries gradient
+                   through it to each row's max and min
+  structured_input_projection
+                   gru_cell.py:466-503: per gate quant_struct_Wi_g(struct_Wi_g(quant_x(x))) + b_ig,
+                   concatenated r, z, n; the per-gate maps are the hidden-side kinds
   ObserverState, observer_forward, scale_zp_from_min_max, update_observer, freeze_observer
                    quantizers.py:63-156 and :176-181 (per-tensor FakeQuantize: modes frozen,
                    dynamic, min_max; scale and zero point from a min and max, symmetric or
@@ -270,6 +279,51 @@ def fake_quant_ste(x: torch.Tensor, q: QuantTuple) -> torch.Tensor:
     return x if q is None else _FakeQuantSTE.apply(x, *q)
 
 
+class _STERound(torch.autograd.Function):
+    """ste.py:17-37: round half to even forward, identity backward."""
+
+    @staticmethod
+    def forward(ctx, x):  # type: ignore[override]
+        return torch.round(x)
+
+    @staticmethod
+    def backward(ctx, g):  # type: ignore[override]
+        return g
+
+
+class _STEClamp(torch.autograd.Function):
+    """ste.py:40-62: clamp forward, gradient only inside [qmin, qmax]."""
+
+    @staticmethod
+    def forward(ctx, x, qmin, qmax):  # type: ignore[override]
+        ctx.save_for_backward(x)
+        ctx.qmin, ctx.qmax = qmin, qmax
+        return torch.clamp(x, qmin, qmax)
+
+    @staticmethod
+    def backward(ctx, g):  # type: ignore[override]
+        (x,) = ctx.saved_tensors
+        return g * ((x >= ctx.qmin) & (x <= ctx.qmax)), None, None
+
+
+def fake_quant_rows_dynamic(W: torch.Tensor, qmin: int, qmax: int) -> torch.Tensor:
+    """Per-row (axis 0) symmetric fake-quant with the scale computed from W
+    itself, differentiable as the reference's autograd differentiates it:
+    FakeQuantizePerChannel._compute_scale_zp (quantizers.py:188-199: amin and
+    amax over every dim but 0, keepdim), the symmetric rule (:124-134: scale =
+    max(|max|, |min|).clamp(1e-8) / qmax, zp = zeros_like(scale)) and
+    fake_quant_ste (ste.py:65-95: (STEClamp(STERound(W / scale + zp)) - zp) *
+    scale). Nothing is detached, so the gradient also flows through the scale."""
+    x_min = W.amin(dim=1, keepdim=True)
+    x_max = W.amax(dim=1, keepdim=True)
+    absmax = torch.maximum(x_max.abs(), x_min.abs()).clamp(min=1e-8)
+    scale = absmax / qmax
+    zp = torch.zeros_like(scale)
+    q = _STERound.apply(W / scale + zp)
+    q = _STEClamp.apply(q, qmin, qmax)
+    return (q - zp) * scale
+
+
 def hidden_params(cfg: dict) -> Tuple[str, ...]:
     """Keys of the hidden-map parameters of a config (w, and w2 for two-factor Monarch)."""
     return ("w", "w2") if cfg.get("w2") is not None else ("w",)
@@ -401,9 +455,42 @@ def input_projection(x: torch.Tensor, W: torch.Tensor, b: Optional[torch.Tensor]
     else:
         xq = x
     if w_quant is not None:
-        wq, _ = weight_fake_quant_rows(W.detach(), w_quant[0], w_quant[1])
-        W = W + (wq - W).detach() if ste else wq
+        W = fake_quant_rows_dynamic(W, w_quant[0], w_quant[1]) if ste else \
+            weight_fake_quant_rows(W, w_quant[0], w_quant[1])[0]
     return F.linear(xq, W, b)
+
+
+def _out_quant(y: torch.Tensor, oq, ste: bool) -> torch.Tensor:
+    """One gate's output quantizer: None, a frozen per-tensor (scale, qmin,
+    qmax) or ("rows", qmin, qmax), the dynamic per-row quantizer."""
+    if oq is None:
+        return y
+    if oq[0] == "rows":
+        return fake_quant_rows_dynamic(y, oq[1], oq[2]) if ste else \
+            fake_quant_rows_dynamic(y.detach(), oq[1], oq[2]).detach()
+    return fake_quant_ste(y, oq) if ste else fake_quant(y, oq)
+
+
+def structured_input_projection(x: torch.Tensor, kind: str, w: torch.Tensor, b: Optional[torch.Tensor],
+                                x_quant: QuantTuple = None, out_quant=(None, None, None),
+                                ste: bool = False) -> torch.Tensor:
+    """gi [..., 3H] of a structured input side (gru_cell.py:466-503): q_x over
+    the whole sequence, each gate's map (the hidden-side map of ``kind`` with
+    weights w, input size = H), the gate's output quantizer (_out_quant), its
+    bias, concatenation r, z, n."""
+    H = x.shape[-1]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, H)
+    xq = (fake_quant_ste(x2, x_quant) if ste else fake_quant(x2, x_quant)) if x_quant is not None else x2
+    cfg = {"kind": kind, "w": w, "h0": torch.zeros(1, H, dtype=x.dtype), "gi": torch.zeros(1, 1, 3 * H, dtype=x.dtype)}
+    y = gh_map_nobias(cfg)(xq, w)
+    parts = []
+    for g in range(3):
+        o = _out_quant(y[:, g * H:(g + 1) * H], out_quant[g], ste)
+        if b is not None:
+            o = o + b[g * H:(g + 1) * H]
+        parts.append(o)
+    return torch.cat(parts, dim=-1).reshape(*lead, 3 * H)
 
 
 

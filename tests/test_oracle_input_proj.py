@@ -86,6 +86,31 @@ def test_planted_mistakes_fail_the_pins(mistake):
         assert bad[0] == 0.0 and O.weight_fake_quant_rows(W, -127, 127)[1][0].item() > 0.0
 
 
+def _rows_dynamic_grad_closed_form(W: np.ndarray, G: np.ndarray, qmax: float) -> np.ndarray:
+    """d/dW of sum(G * fq(W)) for the per-row dynamic symmetric fake-quant, by
+    hand in float64: STE (G itself) plus dL/ds = sum_i G_i (q_i - W_i / s) per
+    row, times ds/dW = (1 / qmax) d max(|max|, |min|) / dW, where the max (min)
+    element gets sign(max) (sign(min)), halved when |max| == |min| and shared
+    by equal maxima (minima)."""
+    W = W.astype(np.float64)
+    out = G.astype(np.float64).copy()
+    for n in range(W.shape[0]):
+        row = W[n]
+        mx, mn = row.max(), row.min()
+        absmax = max(abs(mx), abs(mn))
+        s = max(absmax, 1e-8) / qmax
+        q = np.clip(np.round(row / s), -qmax, qmax)
+        dLds = float(np.sum(G[n] * (q - row / s)))
+        if absmax < 1e-8:
+            continue
+        w_mx = 1.0 if abs(mx) > abs(mn) else (0.5 if abs(mx) == abs(mn) else 0.0)
+        w_mn = 1.0 if abs(mn) > abs(mx) else (0.5 if abs(mx) == abs(mn) else 0.0)
+        at_mx, at_mn = row == mx, row == mn
+        out[n, at_mx] += dLds / qmax * w_mx * np.sign(mx) / at_mx.sum()
+        out[n, at_mn] += dLds / qmax * w_mn * np.sign(mn) / at_mn.sum()
+    return out
+
+
 def test_ste_gradients_match_the_straight_through_formulas():
     g = torch.Generator().manual_seed(9)
     x = (torch.randn(5, 8, generator=g) * 2.0).requires_grad_(True)
@@ -98,6 +123,29 @@ def test_ste_gradients_match_the_straight_through_formulas():
     wq, _ = O.weight_fake_quant_rows(W.detach(), -127, 127)
     mask = (torch.round(x.detach() / 0.02).abs() <= 127).float()
     assert torch.allclose(dx, (dgi @ wq) * mask, atol=1e-6)
-    assert torch.allclose(dW, dgi.t() @ O.fake_quant(x.detach(), q), atol=1e-5)
+    gw = (dgi.t() @ O.fake_quant(x.detach(), q)).numpy()  # gradient reaching W_q
+    want = _rows_dynamic_grad_closed_form(W.detach().numpy(), gw, 127.0)
+    assert np.allclose(dW.numpy(), want, atol=1e-4, rtol=1e-5)
+    # the scale path is not negligible: dropping it (a detached scale) misses the closed form
+    assert not np.allclose(gw, want, atol=1e-3)
     assert torch.allclose(db, dgi.sum(0), atol=1e-6)
     assert mask.min().item() == 0.0  # some x clip at |x| > 2.55
+
+
+@pytest.mark.parametrize("row", [[1.0, -1.0, 0.5, 0.25],      # |max| == |min|: halved
+                                 [2.0, 2.0, -1.0, 0.5],       # two equal maxima: shared
+                                 [-3.0, 0.5, -3.0, 1.0],      # two equal minima carry the scale
+                                 [0.0, 0.0, 0.0, 0.0]])       # the 1e-8 floor: no scale path
+def test_dynamic_rows_gradient_ties_and_floor(row):
+    W = torch.tensor([row], dtype=torch.float64, requires_grad=True)
+    G = torch.tensor([[0.3, -0.7, 1.1, 0.2]], dtype=torch.float64)
+    (O.fake_quant_rows_dynamic(W, -127, 127) * G).sum().backward()
+    want = _rows_dynamic_grad_closed_form(W.detach().numpy(), G.numpy(), 127.0)
+    assert np.allclose(W.grad.numpy(), want, atol=1e-12)
+
+
+def test_fake_quant_rows_dynamic_forward_is_the_pinned_rule():
+    g = torch.Generator().manual_seed(4)
+    W = torch.randn(7, 33, generator=g)
+    W[3] = 0.0
+    assert torch.equal(O.fake_quant_rows_dynamic(W, -127, 127), O.weight_fake_quant_rows(W, -127, 127)[0])
