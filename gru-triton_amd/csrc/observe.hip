@@ -351,7 +351,7 @@ int plan_observe(const gs_observe_args* a, OPlan* p, const char* who) {
   if (B * 3 * H > INT32_MAX / 4)
     return set_error(GS_ERR_INVALID, "%s: B * 3H = %lld is too large", who, (long long)(B * 3 * H));
   p->gemm = a->kind != GS_KIND_DIAGONAL;
-  p->own_map = a->kind == GS_KIND_MONARCH || a->kind == GS_KIND_BUTTERFLY;
+  p->own_map = a->kind == GS_KIND_MONARCH || a->kind == GS_KIND_BUTTERFLY || a->kind == GS_KIND_CIRCULANT;
   // gh has only B rows: split K in up to 8 parts of >= 64 terms so that the
   // product spreads over a few hundred workgroups (the gates kernel sums them).
   p->split = p->gemm ? (int)std::max<int64_t>(1, std::min<int64_t>(kMaxSplit, H / 64)) : 1;

@@ -193,6 +193,41 @@ __global__ void diagonal_materialize(const float* w, float* m, int H) {
   }
 }
 
+// Circulant: M[g H + i][k] = col[g][(i - k) mod H].
+__global__ void circulant_materialize(const float* col, float* m, int H) {
+  const int64_t n = (int64_t)3 * H * H;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int row = (int)(e / H), k = (int)(e - (int64_t)row * H);
+    const int g = row / H, i = row - g * H;
+    int d = i - k;
+    if (d < 0) d += H;
+    m[e] = col[(int64_t)g * H + d];
+  }
+}
+
+// dcol[g][d] = sum_i dM[g H + i][(i - d) mod H], one thread per (g, d), i ascending.
+__global__ void circulant_project(const float* dm, float* dcol, int H) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= 3 * H) return;
+  const int g = e / H, d = e - g * H;
+  const float* base = dm + (int64_t)g * H * H;
+  float acc = 0.0f;
+  for (int i = 0; i < H; ++i) {
+    int k = i - d;
+    if (k < 0) k += H;
+    acc += base[(int64_t)i * H + k];
+  }
+  dcol[e] = acc;
+}
+
+// dw[g][k] = dM[g H + k][k].
+__global__ void diagonal_project(const float* dm, float* dw, int H) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= 3 * H) return;
+  const int g = e / H, k = e - g * H;
+  dw[e] = dm[((int64_t)g * H + k) * H + k];
+}
+
 // G_K = [dM_g; 0].
 __global__ void bfly_grad_init(const float* dm, float* gbuf, int64_t gate_stride, int N, int H) {
   const int64_t n = (int64_t)3 * N * H;
@@ -381,6 +416,7 @@ int validate_map(const gs_map_args* a, const char* who) {
   switch (a->kind) {
     case GS_KIND_DENSE:
     case GS_KIND_DIAGONAL:
+    case GS_KIND_CIRCULANT:
       if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for this kind", who);
       return GS_OK;
     case GS_KIND_MONARCH:
@@ -418,6 +454,9 @@ int materialize_map(const gs_map_args* a, hipStream_t stream, const char* who) {
       return GS_OK;
     case GS_KIND_DIAGONAL:
       hipLaunchKernelGGL(diagonal_materialize, grid_for(nmat), dim3(256), 0, stream, a->w, a->m, H);
+      break;
+    case GS_KIND_CIRCULANT:
+      hipLaunchKernelGGL(circulant_materialize, grid_for(nmat), dim3(256), 0, stream, a->w, a->m, H);
       break;
     case GS_KIND_MONARCH:
       if (a->w2 == nullptr)
@@ -507,6 +546,36 @@ extern "C" int64_t gs_hidden_map_scratch_bytes(const gs_map_args* a) {
   const int rc = validate_map(a, "gs_hidden_map_scratch_bytes");
   if (rc) return rc;
   return hidden_map_scratch(a);
+}
+
+extern "C" int gs_hidden_map_grad(const gs_map_args* a, const float* dm, float* dw, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_hidden_map_grad";
+  int rc = validate_map(a, who);
+  if (rc) return rc;
+  if (!dm || !dw) return set_error(GS_ERR_INVALID, "%s: dm and dw must be non-NULL device pointers", who);
+  const int H = (int)a->H;
+  const unsigned blocks = (unsigned)((3 * H + 255) / 256);
+  switch (a->kind) {
+    case GS_KIND_DIAGONAL:
+      hipLaunchKernelGGL(diagonal_project, dim3(blocks), dim3(256), 0, stream, dm, dw, H);
+      break;
+    case GS_KIND_CIRCULANT:
+      hipLaunchKernelGGL(circulant_project, dim3(blocks), dim3(256), 0, stream, dm, dw, H);
+      break;
+    case GS_KIND_MONARCH:
+      if (a->w2 != nullptr)
+        return set_error(GS_ERR_INVALID, "%s: a two-factor Monarch gets its gradients from gs_monarch_bwd", who);
+      hipLaunchKernelGGL(monarch1_project, grid_for((int64_t)3 * H * a->blksz), dim3(256), 0, stream, dm, dw, H,
+                         (int)a->nblocks, (int)a->blksz);
+      break;
+    default:
+      return set_error(GS_ERR_INVALID, "%s: kind %d has no dense-gradient fold here (use its backward entry point)",
+                       who, a->kind);
+  }
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
 }
 
 extern "C" int gs_hidden_map_dense(const gs_map_args* a, hipStream_t stream) {

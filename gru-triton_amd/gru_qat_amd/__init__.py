@@ -22,6 +22,7 @@ from .scan_butterfly import (
 )
 from .scan_diagonal import extract_diagonal_factors, gru_scan_diagonal, gru_scan_diagonal_forward
 from .scan_monarch import extract_monarch_factors, gru_scan_monarch, gru_scan_monarch_forward
+from .scan_circulant import extract_circulant_factors, gru_scan_circulant, gru_scan_circulant_forward
 from ._lib import PersistentScanFault, check_faults, load as load_library, workspace_faults
 from .gru_layer import ScanLayer, fast_dispatch_eligible, forward_fast_dispatch, layer_forward, resolve_use_triton
 from .input_proj import input_projection, quantize_input_weights
@@ -67,6 +68,9 @@ __all__ = [
     "resolve_use_triton",
     "workspace_faults",
     "structured_input_projection",
+    "gru_scan_circulant",
+    "gru_scan_circulant_forward",
+    "extract_circulant_factors",
     "check_faults",
     "PersistentScanFault",
 ]

@@ -25,6 +25,7 @@ KIND_DENSE = 0
 KIND_DIAGONAL = 1
 KIND_MONARCH = 2
 KIND_BUTTERFLY = 3
+KIND_CIRCULANT = 4
 
 # Every symbol include/gruscan.h declares.
 EXPORTS = (
@@ -48,6 +49,7 @@ EXPORTS = (
     "gs_quantize_rows",
     "gs_hidden_map_dense",
     "gs_hidden_map_scratch_bytes",
+    "gs_hidden_map_grad",
     "gs_observe_tensor",
     "gs_observe_tensor_scratch_bytes",
     "gs_observe_scan",
@@ -381,6 +383,9 @@ def load() -> ctypes.CDLL:
             size = getattr(lib, name + "_scratch_bytes")
             size.argtypes = [ctypes.POINTER(argt)]
             size.restype = ctypes.c_int64
+        lib.gs_hidden_map_grad.argtypes = [ctypes.POINTER(GsMapArgs), ctypes.c_void_p, ctypes.c_void_p,
+                                           ctypes.c_void_p]
+        lib.gs_hidden_map_grad.restype = ctypes.c_int
         lib.gs_quantize_rows.argtypes = [ctypes.POINTER(GsRowsArgs), ctypes.c_void_p]
         lib.gs_quantize_rows.restype = ctypes.c_int
         lib.gs_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsArgs)]

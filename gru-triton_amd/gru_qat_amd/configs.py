@@ -18,6 +18,11 @@ weights, hidden bias, gi, h0.
   hidden quant as cfg2.
 * cfg4 butterfly: T=512 B=64 H=1024; twiddles [3, 1, 10, 512, 2, 2] ~
   N(0, 1/2); bh ~ U(+-1/sqrt(H)); gi ~ N(0, 1); h0 = 0.
+* cfg6 circulant fp32 (the reference's _CirculantLinear, structure.py:220-240, which it
+  runs on its per-step loop): T=64 B=32 H=512; Wh_circ [3, H] ~ N(0, 1/H) (the
+  reference init randn(n) / sqrt(n)); bh ~ U(+-1/sqrt(H)); gi ~ N(0, 1);
+  h0 ~ N(0, 0.1^2). Not one of BASELINE.json's configurations; measured beside
+  the dense kernel it runs on.
 * cfg5 Monarch single factor (the reference's own Monarch form,
   scan_monarch.py:74-127), nblocks=8, blksz=64: one factor [3, 8, 64, 64] ~
   U(-1/8, 1/8), bh ~ U(+-1/sqrt(H)), gi ~ N(0, 1), h0 = 0, hidden quant as
@@ -40,10 +45,11 @@ NAMES = {
     3: "monarch_nb8_two_factor_int8",
     4: "butterfly_fp32",
     5: "monarch_nb8_single_int8",
+    6: "circulant_fp32",
 }
 
 SHAPES = {0: (64, 32, 512), 1: (64, 32, 512), 2: (64, 32, 512), 3: (64, 32, 512), 4: (512, 64, 1024),
-          5: (64, 32, 512)}
+          5: (64, 32, 512), 6: (64, 32, 512)}
 
 
 def _uniform(gen: torch.Generator, shape, bound: float) -> torch.Tensor:
@@ -108,6 +114,12 @@ def make_config(idx: int, device: Optional[torch.device] = None, seed: int = 0,
         d["bh"] = _uniform(gen, (3 * H,), k)
         d["gi"] = torch.randn((T, B, 3 * H), generator=gen, dtype=torch.float32)
         d["h0"] = torch.zeros((B, H), dtype=torch.float32)
+    elif idx == 6:
+        d["kind"] = "circulant"
+        d["w"] = torch.randn((3, H), generator=gen, dtype=torch.float32) / math.sqrt(H)
+        d["bh"] = _uniform(gen, (3 * H,), k)
+        d["gi"] = torch.randn((T, B, 3 * H), generator=gen, dtype=torch.float32)
+        d["h0"] = torch.randn((B, H), generator=gen, dtype=torch.float32) * 0.1
     else:
         raise ValueError(f"unknown config {idx}")
     if device is not None:
@@ -121,6 +133,7 @@ def run_config(d: Dict[str, object]) -> torch.Tensor:
     """Runs the HIP scan of a config dict (tensors on a GPU); returns out."""
     from .scan import gru_scan_forward_persistent
     from .scan_butterfly import gru_scan_butterfly_forward
+    from .scan_circulant import gru_scan_circulant_forward
     from .scan_diagonal import gru_scan_diagonal_forward
     from .scan_monarch import gru_scan_monarch_forward
 
@@ -134,4 +147,6 @@ def run_config(d: Dict[str, object]) -> torch.Tensor:
         return gru_scan_monarch_forward(d["gi"], d["h0"], d["w"], d["bh"], Wh_struct2=d.get("w2"), **kw)
     if kind == "butterfly":
         return gru_scan_butterfly_forward(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    if kind == "circulant":
+        return gru_scan_circulant_forward(d["gi"], d["h0"], d["w"], d["bh"], **kw)
     raise ValueError(kind)

@@ -37,6 +37,9 @@ import torch
 from ._common import QuantTuple
 
 FAST_DISPATCH_KINDS = ("diagonal", "monarch", "butterfly")
+# Hidden kinds this build also scans on the GPU, which the reference sends to
+# its per-step loop (gru_layer.py:109-113).
+EXTENDED_KINDS = ("dense", "circulant")
 
 
 _SCALE_CACHE: "weakref.WeakKeyDictionary[Any, Tuple[int, int, float]]" = weakref.WeakKeyDictionary()
@@ -81,23 +84,23 @@ def _extract_h_quant_params(quantizer: Any) -> QuantTuple:
     return (value, int(quantizer.qmin), int(quantizer.qmax))
 
 
-def fast_dispatch_eligible(kind: Optional[str], gate_layout: str, *, dense_eligible: bool = False) -> bool:
+def fast_dispatch_eligible(kind: Optional[str], gate_layout: str, *, extended: bool = False) -> bool:
     """gru_layer.py:110-113: the hidden structure kind is diagonal, monarch or
     butterfly and the gate layout is fused (gi is one [T, B, 3H] tensor).
 
-    ``dense_eligible=True`` adds the dense hidden kind, which this build scans
-    with a persistent kernel of its own (the reference sends dense hidden
-    weights to its per-step loop); the default is the reference's rule."""
-    kinds = FAST_DISPATCH_KINDS + (("dense",) if dense_eligible else ())
+    ``extended=True`` adds EXTENDED_KINDS, the dense and circulant hidden
+    kinds, which this build scans on the GPU too (the reference sends them to
+    its per-step loop); the default is the reference's rule."""
+    kinds = FAST_DISPATCH_KINDS + (EXTENDED_KINDS if extended else ())
     return kind in kinds and gate_layout == "fused"
 
 
 def resolve_use_triton(use_triton: Any, kind: Optional[str], gate_layout: str, *,
-                       dense_eligible: bool = False) -> bool:
+                       extended: bool = False) -> bool:
     """gru_layer.py:115-124: "auto" follows eligibility; a truthy value on an
     ineligible configuration raises ValueError; falsy disables dispatch.
-    ``dense_eligible`` as in ``fast_dispatch_eligible``."""
-    eligible = fast_dispatch_eligible(kind, gate_layout, dense_eligible=dense_eligible)
+    ``extended`` as in ``fast_dispatch_eligible``."""
+    eligible = fast_dispatch_eligible(kind, gate_layout, extended=extended)
     if use_triton == "auto":
         return eligible
     use = bool(use_triton)
@@ -128,8 +131,8 @@ def forward_fast_dispatch(
 
     ``hidden`` is Wh_diag [3, H] (diagonal), Wh_struct [3, nb, bs, bs]
     (monarch; ``hidden2`` the optional second factor), twiddles (butterfly),
-    or Wh_cat [3H, H] for kind "dense", which this build adds (the reference
-    routes dense hidden weights to its per-step loop). ``h0`` None means
+    or, for the kinds this build adds (the reference routes them to its
+    per-step loop), Wh_cat [3H, H] (dense) or Wh_circ [3, H] (circulant). ``h0`` None means
     zeros, as in gru_layer.py:191-192. An unknown kind raises RuntimeError
     (gru_layer.py:294-297).
     """
@@ -159,6 +162,10 @@ def forward_fast_dispatch(
         from .scan import gru_scan_persistent
 
         out = gru_scan_persistent(gi, h0, hidden, bh_cat, **kw)
+    elif kind == "circulant":
+        from .scan_circulant import gru_scan_circulant
+
+        out = gru_scan_circulant(gi, h0, hidden, bh_cat, **kw)
     else:
         raise RuntimeError(f"unexpected dispatch kind {kind!r}")
     h_T = out[-1]
@@ -230,8 +237,9 @@ class ScanLayer(torch.nn.Module):
 
     Follows gru_layer.py: the ``use_triton`` and ``batch_first`` arguments
     (:52-65, resolved by ``resolve_use_triton`` as :110-124 with
-    ``dense_eligible=True``: the dense kind has a fast scan here, so "auto"
-    dispatches it too; a reference ``GRULayer`` keeps the reference rule),
+    ``extended=True``: the dense and circulant kinds have fast scans here, so
+    "auto" dispatches them too; a reference ``GRULayer`` keeps the reference
+    rule),
     ``forward`` (:153-302), ``calibrate`` (:308-336) and ``freeze``
     (:338-339).
 
@@ -263,8 +271,8 @@ class ScanLayer(torch.nn.Module):
         super().__init__()
         from .quantizers import FakeQuantizePerTensor, QuantizerConfig
 
-        if kind not in ("dense",) + FAST_DISPATCH_KINDS:
-            raise ValueError(f"kind must be one of dense, diagonal, monarch, butterfly; got {kind!r}")
+        if kind not in EXTENDED_KINDS + FAST_DISPATCH_KINDS:
+            raise ValueError(f"kind must be one of dense, diagonal, monarch, butterfly, circulant; got {kind!r}")
         if input_kind is not None and input_kind not in FAST_DISPATCH_KINDS:
             raise ValueError(f"input_kind must be None (dense) or one of diagonal, monarch, butterfly; "
                              f"got {input_kind!r}")
@@ -294,7 +302,7 @@ class ScanLayer(torch.nn.Module):
         if w_bits is not None and not (2 <= int(w_bits) <= 16):
             raise ValueError(f"w_bits must be in [2, 16] or None; got {w_bits}")
         self.w_quant = None if w_bits is None else (-(2 ** (int(w_bits) - 1)) + 1, 2 ** (int(w_bits) - 1) - 1)
-        self.use_triton = resolve_use_triton(use_triton, kind, "fused", dense_eligible=True)
+        self.use_triton = resolve_use_triton(use_triton, kind, "fused", extended=True)
         self.batch_first = batch_first
 
     def _x_side(self, x: torch.Tensor) -> Tuple[torch.Tensor, QuantTuple]:

@@ -23,7 +23,7 @@ from ._common import check_common, require_cuda, require_f32
 from .quantizers import FakeQuantizePerTensor
 
 KINDS = {"dense": _lib.KIND_DENSE, "diagonal": _lib.KIND_DIAGONAL, "monarch": _lib.KIND_MONARCH,
-         "butterfly": _lib.KIND_BUTTERFLY}
+         "butterfly": _lib.KIND_BUTTERFLY, "circulant": _lib.KIND_CIRCULANT}
 
 
 def _map_dims(kind: str, hidden: torch.Tensor, hidden2: Optional[torch.Tensor], H: int) -> Tuple[int, int, int, int]:
@@ -33,9 +33,10 @@ def _map_dims(kind: str, hidden: torch.Tensor, hidden2: Optional[torch.Tensor], 
         if tuple(hidden.shape) != (3 * H, H):
             raise ValueError(f"Wh_cat shape must be (3H, H)=({3 * H}, {H}); got {tuple(hidden.shape)}")
         return 0, 0, 0, 0
-    if kind == "diagonal":
+    if kind in ("diagonal", "circulant"):
+        name = "Wh_diag" if kind == "diagonal" else "Wh_circ"
         if tuple(hidden.shape) != (3, H):
-            raise ValueError(f"Wh_diag shape must be (3, H)=(3, {H}); got {tuple(hidden.shape)}")
+            raise ValueError(f"{name} shape must be (3, H)=(3, {H}); got {tuple(hidden.shape)}")
         return 0, 0, 0, 0
     if kind == "monarch":
         from .scan_monarch import _check_struct
@@ -81,6 +82,28 @@ def hidden_map_dense(kind: str, hidden: torch.Tensor, H: int, hidden2: Optional[
         del scratch
     _lib.raise_for(rc, lib)
     return m
+
+
+def hidden_map_grad(kind: str, dm: torch.Tensor, hidden: torch.Tensor, H: int) -> torch.Tensor:
+    """Folds a gradient ``dm`` [3H, H] of the dense form onto the parameters
+    of a diagonal, single-factor Monarch or circulant hidden weight (the shape
+    of ``hidden``), with ``gs_hidden_map_grad``."""
+    nb, bs, log_n, bfly_nb = _map_dims(kind, hidden, None, H)
+    if tuple(dm.shape) != (3 * H, H):
+        raise ValueError(f"dm must be [3H, H]=[{3 * H}, {H}]; got {tuple(dm.shape)}")
+    lib = _lib.load()
+    dm = dm.contiguous()
+    dw = torch.empty(hidden.shape, device=hidden.device, dtype=torch.float32)
+    a = _lib.GsMapArgs()
+    a.kind = KINDS[kind]
+    a.w, a.w2, a.m = hidden.data_ptr(), None, None
+    a.H, a.nblocks, a.blksz, a.log_n, a.bfly_nblocks = H, nb, bs, log_n, bfly_nb
+    with torch.cuda.device(hidden.device):
+        handle = torch.cuda.current_stream(hidden.device).cuda_stream
+        rc = lib.gs_hidden_map_grad(ctypes.byref(a), ctypes.c_void_p(dm.data_ptr()), ctypes.c_void_p(dw.data_ptr()),
+                                    ctypes.c_void_p(handle))
+    _lib.raise_for(rc, lib)
+    return dw
 
 
 def _off() -> _lib.GsObserver:

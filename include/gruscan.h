@@ -72,6 +72,13 @@ extern "C" {
 #define GS_KIND_DIAGONAL 1
 #define GS_KIND_MONARCH 2
 #define GS_KIND_BUTTERFLY 3
+/* Circulant hidden weights (reference _CirculantLinear, src/gru_qat/structure.py:220-240:
+ * y = irfft(rfft(col) * rfft(x)), i.e. y[i] = sum_j col[(i - j) mod H] x[j]): w is Wh_circ
+ * [3, H], each gate's first column col. The reference runs this kind on its per-step loop
+ * (gru_layer.py:109-113); here it is the dense scan on the circulant matrices:
+ * gs_hidden_map_dense(GS_KIND_CIRCULANT) writes them, gs_dense_fwd / gs_dense_bwd run the
+ * scan, and gs_hidden_map_grad folds the dense weight gradient back onto col. */
+#define GS_KIND_CIRCULANT 4
 
 /* Frozen per-tensor symmetric fake-quant: q = clamp(rint(x / scale), qmin, qmax) * scale,
  * with the IEEE quotient and round-half-to-even. enabled == 0 turns it off. When
@@ -391,6 +398,16 @@ typedef struct gs_map_args {
 
 int64_t gs_hidden_map_scratch_bytes(const gs_map_args* args);
 int gs_hidden_map_dense(const gs_map_args* args, hipStream_t stream);
+
+/* The reverse: carries a gradient dm [3H, H] of the dense form onto the map's
+ * parameters, dw (the shape of args->w): diagonal dw[g][k] = dm[g H + k][k];
+ * single-factor Monarch the diagonal blocks of each gate; circulant
+ * dw[g][d] = sum_i dm[g H + i][(i - d) mod H]. Each entry is one thread's
+ * fixed-order sum, so results are deterministic. Butterfly and two-factor
+ * Monarch parameters get their gradients from gs_butterfly_bwd /
+ * gs_monarch_bwd instead (GS_ERR_INVALID here). No reference counterpart:
+ * the reference gets these from autograd. */
+int gs_hidden_map_grad(const gs_map_args* args, const float* dm, float* dw, hipStream_t stream);
 
 /* ---- observers (calibration) ----------------------------------------------------
  * The reference's per-step path with its quantizers firing: GRULayer.forward

@@ -15,6 +15,8 @@ Functions and what they follow (reference file:line):
   gh_diagonal      triton_kernels/scan_diagonal.py:110-115, structure.py:213-217
   gh_monarch       triton_kernels/scan_monarch.py:107-113
   gh_monarch2      build-defined two-factor form P^T L P R (no reference counterpart)
+  gh_circulant     structure.py:220-240 (_CirculantLinear: y = irfft(rfft(col) * rfft(x))),
+                   restated as the circular convolution y[i] = sum_j col[(i - j) mod H] x[j]
   butterfly_apply  triton_kernels/scan_butterfly.py:276-317 (stage order, stride
                    direction per chain, pair index and twiddle element selection)
   scan             the T-step loops of scan_diagonal.py:79-124 / scan_monarch.py:74-127 /
@@ -144,6 +146,20 @@ def gh_monarch2(hq: torch.Tensor, R: torch.Tensor, L: torch.Tensor, bh: torch.Te
     return (y + bh.view(3, H)).reshape(B, 3 * H)
 
 
+def circulant_matrix(col: torch.Tensor) -> torch.Tensor:
+    """C [H, H] with C[i][j] = col[(i - j) mod H]: y = C x is the circular
+    convolution of col and x."""
+    H = col.shape[-1]
+    idx = (torch.arange(H).unsqueeze(1) - torch.arange(H).unsqueeze(0)) % H
+    return col[idx]
+
+
+def gh_circulant(hq: torch.Tensor, Wh_circ: torch.Tensor, bh: torch.Tensor) -> torch.Tensor:
+    """structure.py:220-240 for the three gates: [C(col_r) hq; C(col_z) hq; C(col_n) hq] + bh."""
+    parts = [hq @ circulant_matrix(Wh_circ[g]).t() for g in range(3)]
+    return torch.cat(parts, dim=-1) + bh
+
+
 def butterfly_apply(x: torch.Tensor, tw_g: torch.Tensor) -> torch.Tensor:
     """One gate's butterfly on rows of x [B, N]; tw_g is [nchains, L, N/2, 2, 2]."""
     nchains, L, n2 = tw_g.shape[0], tw_g.shape[1], tw_g.shape[2]
@@ -202,6 +218,8 @@ def gh_fn_for(cfg: dict) -> GhFn:
         return lambda hq: gh_monarch(hq, w, bh)
     if kind == "butterfly":
         return lambda hq: gh_butterfly(hq, w, bh)
+    if kind == "circulant":
+        return lambda hq: gh_circulant(hq, w, bh)
     raise ValueError(kind)
 
 
@@ -345,6 +363,9 @@ def gh_map_nobias(cfg: dict) -> Callable[..., torch.Tensor]:
     if kind == "butterfly":
         zero = torch.zeros(3 * cfg["h0"].shape[-1], dtype=cfg["gi"].dtype)
         return lambda hq, w: gh_butterfly(hq, w, zero)
+    if kind == "circulant":
+        zero = torch.zeros(3 * cfg["h0"].shape[-1], dtype=cfg["gi"].dtype)
+        return lambda hq, w: gh_circulant(hq, w, zero)
     raise ValueError(kind)
 
 

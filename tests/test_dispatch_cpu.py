@@ -69,8 +69,8 @@ def test_forward_fast_dispatch_argument_errors():
         forward_fast_dispatch("diagonal", torch.zeros(3, 0, 3 * H), None, w, bh)
     with pytest.raises(ValueError, match=r"gi must be \[T, B, 3H\]"):
         forward_fast_dispatch("diagonal", torch.zeros(3, 3 * H), None, w, bh)
-    with pytest.raises(RuntimeError, match="unexpected dispatch kind 'circulant'"):
-        forward_fast_dispatch("circulant", torch.zeros(3, 2, 3 * H), None, w, bh)
+    with pytest.raises(RuntimeError, match="unexpected dispatch kind 'ldr'"):
+        forward_fast_dispatch("ldr", torch.zeros(3, 2, 3 * H), None, w, bh)
     # CPU tensors reach the scan, which rejects them before any device work
     with pytest.raises(ValueError):
         forward_fast_dispatch("diagonal", torch.zeros(3, 2, 3 * H), None, w, bh)
@@ -114,15 +114,17 @@ def test_layer_forward_argument_errors():
 
 
 
-def test_dense_kind_eligible_only_when_named():
-    """One rule: the reference's (dense not eligible) unless the caller names
-    the dense extension, as ScanLayer does."""
-    assert resolve_use_triton("auto", "dense", "fused") is False
-    assert resolve_use_triton("auto", "dense", "fused", dense_eligible=True) is True
-    assert resolve_use_triton("auto", "dense", "split", dense_eligible=True) is False
+@pytest.mark.parametrize("kind", ["dense", "circulant"])
+def test_extended_kinds_eligible_only_when_named(kind):
+    """One rule: the reference's (dense and circulant not eligible) unless the
+    caller names the extension, as ScanLayer does."""
+    assert resolve_use_triton("auto", kind, "fused") is False
+    assert resolve_use_triton("auto", kind, "fused", extended=True) is True
+    assert resolve_use_triton("auto", kind, "split", extended=True) is False
     with pytest.raises(ValueError, match="use_triton=True requires"):
-        resolve_use_triton(True, "dense", "fused")
-    assert resolve_use_triton(True, "dense", "fused", dense_eligible=True) is True
+        resolve_use_triton(True, kind, "fused")
+    assert resolve_use_triton(True, kind, "fused", extended=True) is True
+    assert resolve_use_triton("auto", "ldr", "fused", extended=True) is False
 
 
 def test_scan_layer_resolves_auto_with_the_shared_rule():

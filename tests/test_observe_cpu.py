@@ -206,7 +206,7 @@ def test_scan_layer_construction():
     names = {n for n, m in layer.named_modules() if isinstance(m, G.FakeQuantizePerTensor)}
     assert names == {"quant_x", "quant_h_in", "quant_h_out"}
     with pytest.raises(ValueError):
-        G.ScanLayer("circulant", torch.zeros(3 * H, I), None, torch.zeros(3 * H, H), torch.zeros(3 * H))
+        G.ScanLayer("ldr", torch.zeros(3 * H, I), None, torch.zeros(3 * H, H), torch.zeros(3 * H))
     with pytest.raises(ValueError):
         G.ScanLayer("dense", torch.zeros(3 * H, I), None, torch.zeros(3 * H, H), torch.zeros(3 * H), w_bits=1)
 

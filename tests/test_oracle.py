@@ -227,9 +227,56 @@ def test_butterfly_scan_matches_gru_cell_on_materialized_map():
     assert (O.scan_config(cfg) - ref).abs().max().item() < 5e-6
 
 
+# ---- circulant -------------------------------------------------------------------------------
+
+def _reference_circulant_fft(col: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """The reference's _CirculantLinear.forward (structure.py:236-240), for the pin."""
+    n = col.shape[-1]
+    return torch.fft.irfft(torch.fft.rfft(col) * torch.fft.rfft(x, dim=-1), n=n, dim=-1)
+
+
+def test_circulant_matrix_known_answer():
+    a, b, c = 2.0, 3.0, 5.0
+    C = O.circulant_matrix(torch.tensor([a, b, c]))
+    assert torch.equal(C, torch.tensor([[a, c, b], [b, a, c], [c, b, a]]))
+
+
+@pytest.mark.parametrize("H", [1, 2, 7, 16, 100, 512])
+def test_circulant_map_matches_the_reference_fft(H):
+    g = torch.Generator().manual_seed(H)
+    col = torch.randn(3, H, generator=g, dtype=torch.float64) / H ** 0.5
+    x = torch.randn(5, H, generator=g, dtype=torch.float64)
+    got = O.gh_circulant(x, col, torch.zeros(3 * H, dtype=torch.float64))
+    want = torch.cat([_reference_circulant_fft(col[k], x) for k in range(3)], dim=-1)
+    assert (got - want).abs().max().item() < 1e-12
+    # fp32, as the reference runs it: the direct sum stays within the scan tolerance of the FFT
+    got32 = O.gh_circulant(x.float(), col.float(), torch.zeros(3 * H))
+    assert (got32.double() - want).abs().max().item() < 1e-5
+
+
+def test_circulant_brute_force_and_transposed_mistake():
+    H = 6
+    g = torch.Generator().manual_seed(2)
+    col = torch.randn(H, generator=g, dtype=torch.float64)
+    x = torch.randn(H, generator=g, dtype=torch.float64)
+    y = [sum(col[(i - j) % H] * x[j] for j in range(H)) for i in range(H)]
+    assert torch.allclose(O.circulant_matrix(col) @ x, torch.stack(y), atol=1e-12)
+    transposed = O.circulant_matrix(col).t()  # col[(j - i) mod H]: a plausible index slip
+    assert (transposed @ x - _reference_circulant_fft(col, x)).abs().max().item() > 1e-3
+
+
+def test_circulant_scan_matches_gru_cell():
+    cfg = make_config(6, shape=(6, 4, 20))
+    w = cfg["w"]
+    M = torch.cat([O.circulant_matrix(w[k]) for k in range(3)], dim=0)
+    ref = _gru_cell_scan(cfg["gi"], cfg["h0"], M, cfg["bh"])
+    assert (O.scan_config(cfg) - ref).abs().max().item() < 2e-6
+    assert torch.equal(O.materialize_hidden(cfg), M)
+
+
 # ---- float64 brute force, invariants ------------------------------------------------------
 
-@pytest.mark.parametrize("idx", [0, 1, 3, 4])
+@pytest.mark.parametrize("idx", [0, 1, 3, 4, 6])
 def test_fp32_oracle_close_to_float64(idx):
     shape = (6, 3, 16) if idx != 4 else (6, 3, 16)
     cfg = make_config(idx, shape=shape)

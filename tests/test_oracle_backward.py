@@ -35,6 +35,7 @@ def _cfg64(idx, shape, seed=0, nb=None, two=False, q=None):
 CASES = [
     (1, (4, 3, 6), None, False), (0, (5, 3, 5), None, False), (3, (4, 2, 8), 2, False),
     (3, (4, 2, 8), 2, True), (4, (3, 2, 8), None, False), (4, (3, 2, 6), None, False),
+    (6, (4, 3, 7), None, False),
 ]
 
 
