@@ -60,6 +60,10 @@ WORK = {
     # single-factor Monarch (not a BASELINE.json configuration): 2 T B 3H blksz flops;
     # fp32 FMA, on the VALU in this build (fp32 vector peak = fp32 MFMA peak on MI355X)
     5: {"bytes": 17_242_112, "flops": 402_653_184, "bound": "mfma"},
+    # circulant (not a BASELINE.json configuration): bytes as config 0 (Wh_circ is [3, H]);
+    # flops of the circulant products done directly, 2 T B 3H H, which is how the dense
+    # kernel it runs on computes them
+    6: {"bytes": 16_855_040, "flops": 3_221_225_472, "bound": "mfma"},
 }
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -277,7 +281,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--kinds", default="0,1,2,3,4,5")
+    ap.add_argument("--kinds", default="0,1,2,3,4,5,6")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=4.0, help="seconds of CPU baseline per kind")
     ap.add_argument("--copy-mib", type=int, default=0, help="run a plain N MiB copy K times and exit")

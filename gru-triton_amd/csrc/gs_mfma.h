@@ -55,18 +55,37 @@ __device__ __forceinline__ void load_w(const float* w, int nb, int bs, int blk, 
   }
 }
 
-// Interleaved staging layout of a 4-row operand block: element (row r, k) sits
-// at il_index(r, k) = (k / 4) * 16 + 4 r + k % 4. The A operand of lane l for
-// K-chunk q (k = 64 q + 4 (l / 4) + e, row l % 4) is then the float4 at
-// 256 q + 4 l: a wave's operand reads cover contiguous LDS, free of bank
-// conflicts. A block holding K values per row takes 4 K floats.
-__device__ __forceinline__ int il_index(int r, int k) { return ((k >> 2) << 4) + (r << 2) + (k & 3); }
+// Interleaved staging layout of a 4-row operand block. K is cut into chunks
+// of 4 (c = k / 4); chunk c holds the four rows' 4-float slices back to back,
+// 16 floats, with row r in slot il_slot(r, c). The A operand of lane l for
+// K-chunk q (k = 64 q + 4 (l / 4) + e, row l % 4) is then one float4 of chunk
+// 16 q + l / 4, and a wave's 64 operand reads cover 1 KiB of contiguous LDS
+// (each chunk's four slots read by its four lanes in some order), free of
+// bank conflicts. The slot rotation makes the pollers' stores conflict-free
+// too: a poller stores one row, lane l word k = l + 64 i at il_index(r, k);
+// without rotation (slot = r) the 64 lanes would land on 16 banks, with
+// slot = (r + c / 2 + c / 8) mod 4 they land on 64 distinct banks (and each
+// half-wave on 32, so the layout is conflict-free with 32 or 64 banks). A
+// block holding K values per row takes 4 K floats.
+__device__ __forceinline__ int il_slot(int r, int c) { return (r + (c >> 1) + (c >> 3)) & 3; }
+__device__ __forceinline__ int il_index(int r, int k) {
+  const int c = k >> 2;
+  return (c << 4) + (il_slot(r, c) << 2) + (k & 3);
+}
 
+// A operand of lane l from an interleaved block: a[m] = row (l % 4), k =
+// kofs + kmap(m, l / 4). blk points at the block's chunk kofs / 4 (kofs a
+// multiple of 4). Adding 16 to a chunk index adds 2 (mod 4) to its slot, so
+// the reads alternate between two per-lane bases by the parity of q.
 template <int KC>
-__device__ __forceinline__ void lds_a_il(const float* blk, int lane, float (&a)[KC]) {
+__device__ __forceinline__ void lds_a_il(const float* blk, int lane, float (&a)[KC], int kofs = 0) {
+  const int m = lane >> 2, x = (kofs >> 2) + m;
+  const int s0 = ((lane & 3) + (x >> 1) + (x >> 3)) & 3;
+  const float* p0 = blk + 16 * m + 4 * s0;
+  const float* p1 = blk + 16 * m + 4 * (s0 ^ 2);
 #pragma unroll
   for (int q = 0; q < KC / 4; ++q) {
-    const f4 v = *reinterpret_cast<const f4*>(blk + 256 * q + 4 * lane);
+    const f4 v = *reinterpret_cast<const f4*>(((q & 1) ? p1 : p0) + 256 * q);
     a[4 * q + 0] = v[0];
     a[4 * q + 1] = v[1];
     a[4 * q + 2] = v[2];
@@ -79,8 +98,13 @@ __device__ __forceinline__ void lds_a_il(const float* blk, int lane, float (&a)[
 // instruction reads 64 consecutive words (polling 4 rows x 16 words per
 // instruction instead measured 25 % slower exchanges). Loads address up to
 // src[64 MPR - 1], so the buffer must extend that far (words past klen are
-// loaded but not waited for). Only stale words are loaded again. Returns the
-// mask of valid m; `ok` turns false when the wait gave up.
+// loaded but not waited for). Every round reloads all MPR words: a word that
+// already carries the tag keeps it until this workgroup publishes its next
+// step (the producer's next write to the same buffer half needs that step),
+// and unconditional loads measured faster than reloading only the stale words
+// under per-lane exec masks (one-way exchange latency of 512 words by one
+// wave: 575 ns against 693 ns). Returns the mask of valid m; `ok` turns false
+// when the wait gave up.
 template <int MPR>
 __device__ __forceinline__ uint32_t poll_row_words(const Ctrl& c, const uint64_t* src, int klen, uint32_t tag,
                                                    uint64_t (&v)[MPR], bool& ok) {
@@ -107,20 +131,20 @@ __device__ __forceinline__ uint32_t poll_row_words(const Ctrl& c, const uint64_t
       break;
     }
     __builtin_amdgcn_s_sleep(1);
-    static_for<0, MPR>([&](auto I) {
-      if ((pending >> I) & 1u) v[I] = ld_tagged(s0 + 64 * I);
-    });
+    static_for<0, MPR>([&](auto I) { v[I] = ld_tagged(s0 + 64 * I); });
   }
   return valid;
 }
 
-// Polls one row of tagged words into an interleaved LDS block: lane l takes
-// k = 64 m + l (m < MPR) from src[k] and stores dst[il_index(r, k)] for
-// k < klen, with the loads, waits and bounds of poll_row_words. (The wait loop
-// is written out here rather than shared: the forward kernels' code around
-// this inlined loop is tuned, and the shared form schedules differently.)
-// `ok` turns false when the wait gave up.
-template <int MPR>
+// Polls one row of tagged words into LDS: lane l takes k = 64 m + l (m < MPR)
+// from src[k] and stores it for k < klen at dst[il_index(r, k)] (IL: the
+// interleaved layout; a dst that starts k0 into a larger block keeps that
+// block's slots when k0 is a multiple of 128) or at dst[k] (row-major), with
+// the loads, waits and bounds of poll_row_words. (The wait loop is written out
+// here rather than shared: the forward kernels' code around this inlined loop
+// is tuned, and the shared form schedules differently.) `ok` turns false when
+// the wait gave up.
+template <int MPR, bool IL = true>
 __device__ __forceinline__ void poll_row_il(const Ctrl& c, const uint64_t* src, float* dst, int r, int klen,
                                             uint32_t tag, bool& ok) {
   static_assert(MPR <= 32, "poll mask is 32 bits");
@@ -147,12 +171,10 @@ __device__ __forceinline__ void poll_row_il(const Ctrl& c, const uint64_t* src, 
       break;
     }
     __builtin_amdgcn_s_sleep(1);
-    static_for<0, MPR>([&](auto I) {
-      if ((pending >> I) & 1u) v[I] = ld_tagged(s0 + 64 * I);
-    });
+    static_for<0, MPR>([&](auto I) { v[I] = ld_tagged(s0 + 64 * I); });
   }
   static_for<0, MPR>([&](auto I) {
-    if ((valid >> I) & 1u) dst[il_index(r, lane + 64 * I)] = value_of(v[I]);
+    if ((valid >> I) & 1u) dst[IL ? il_index(r, lane + 64 * I) : lane + 64 * I] = value_of(v[I]);
   });
 }
 

@@ -21,9 +21,9 @@
 // straight into the LDS staging buffer of the next step.
 // Remote mode (a group spans workgroups): compute waves publish q_in(h_t) as
 // tagged 64-bit words (gs_device.h) and never load from global memory inside
-// the loop. Four poller waves per workgroup, one per batch row of the
-// row-block, poll the words the next iteration needs and stage them, with the
-// next gate inputs, into LDS while the compute waves work. The two roles meet
+// the loop. Poller waves (one or two per batch row of the row-block) poll
+// the words the next iteration needs and stage them, with the next gate
+// inputs, into LDS while the compute waves work. The two roles meet
 // at one LDS-only barrier per iteration, so no wave ever waits for its own
 // stores to be acknowledged. During the first exchange the pollers check that
 // their group runs on one XCD; if so, later steps publish with non-temporal
@@ -35,7 +35,12 @@ namespace gs {
 namespace {
 
 enum : int { kDense = 0, kMonarch1 = 1 };
-constexpr int kPollers = 4;  // remote mode: poller waves per workgroup, one per row
+// Remote mode: poller waves per batch row. Two for KC = 16 and 32, each
+// polling half of the row (measured 2 % faster than one at config 1: fewer
+// words per lane shorten a poll round); one for KC <= 8, whose workgroups
+// already hold up to 12 compute waves, and for KC = 64, whose 192 weight VGPRs
+// need the register budget of two waves per SIMD.
+constexpr int pollers_per_row(int KC) { return KC == 16 || KC == 32 ? 2 : 1; }
 
 struct DParams {
   const float* gi;
@@ -200,14 +205,18 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       lds_barrier();
     }
   } else if (REMOTE) {
-    // Poller wave pr stages row pr of iteration it + 1's inputs while the
-    // compute waves run iteration it. The gate-input loads are issued first so
-    // that their latency overlaps the polls, which start once this
-    // workgroup's compute waves have published iteration it: the other
-    // workgroups publish at about the same time, and polling earlier only
-    // loads the memory system that carries their stores.
-    const int pr = wave - nwc;
-    constexpr int NGI = NT / 64 > kPollers ? (3 * 4 * (NT / 64 - kPollers) + 63) / 64 : 1;  // gi words per lane
+    // NPR poller waves per batch row stage row pr of iteration it + 1's inputs
+    // while the compute waves run iteration it, each polling its share of the
+    // row's words. The gate-input loads (by part 0) are issued first so that
+    // their latency overlaps the polls, which start once this workgroup's
+    // compute waves have published iteration it: the other workgroups publish
+    // at about the same time, and polling earlier only loads the memory system
+    // that carries their stores.
+    constexpr int NPR = pollers_per_row(KC);
+    static_assert(!REMOTE || NT / 64 >= 4 * NPR + 1, "launch bounds hold the poller waves");
+    const int pq = wave - nwc;
+    const int pr = pq / NPR, part = pq - pr * NPR;
+    constexpr int NGI = NT / 64 > 4 * NPR ? (3 * 4 * (NT / 64 - 4 * NPR) + 63) / 64 : 1;  // gi words per lane
     bool alive = true;  // no wait of this wave has given up
     for (int it = 0; it < niter; ++it) {
       const int nx = it + 1;
@@ -220,12 +229,12 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
         for (int i = 0; i < NGI; ++i) {
           const int w = lane + 64 * i;
           const int g = w / U, u = w - g * U;
-          const bool ok = w < 3 * U && row < p.B && (ulo + u - klo) < p.bs;
+          const bool ok = part == 0 && w < 3 * U && row < p.B && (ulo + u - klo) < p.bs;
           gv[i] = ok ? p.gi[(int64_t)t2 * p.sg_t + (int64_t)row * p.sg_b + g * p.H + ulo + u] : 0.0f;
         }
         float* hs = hst + (nx & 1) * p.hsz;
         if (t2 == 0) {
-          for (int k = lane; k < p.bs; k += 64) {
+          for (int k = lane + 64 * part; k < p.bs; k += 64 * NPR) {
             float v = 0.0f;
             if (row < p.B) {
               v = p.h0[(int64_t)row * p.sh0_b + klo + k];
@@ -235,21 +244,27 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
           }
         } else {
           if (alive) {
-            if (pr == 0 && nx == nrbm &&  // first exchange of the launch
+            if (pq == 0 && nx == nrbm &&  // first exchange of the launch
                 p.P <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, p.P, base + 1u, alive))
               __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
-            // bs words of row pr, k < 16 KC
+            // this wave's share of row pr's bs words: k in [part KW, part KW + KW)
+            // (part KW is a multiple of 128, so the staged slots are those of il_index)
             const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * p.H + klo;
-            if (alive) poll_row_il<KC / 4>(ctrl, hb, hs, pr, p.bs, base + (uint32_t)t2, alive);
+            constexpr int KW = 16 * KC / NPR;
+            if (alive && part * KW < p.bs)
+              poll_row_il<KC / 4 / NPR>(ctrl, hb + part * KW, hs + 4 * part * KW, pr, min(KW, p.bs - part * KW),
+                                        base + (uint32_t)t2, alive);
             if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           }
         }
         float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
+        if (part == 0) {
 #pragma unroll
-        for (int i = 0; i < NGI; ++i) {
-          const int w = lane + 64 * i;
-          if (w < 3 * U) gs_[w] = gv[i];
+          for (int i = 0; i < NGI; ++i) {
+            const int w = lane + 64 * i;
+            if (w < 3 * U) gs_[w] = gv[i];
+          }
         }
       }
       lds_barrier();
@@ -262,13 +277,14 @@ typedef void (*DFn)(DParams);
 
 template <int KIND, bool REMOTE>
 DFn pick_kernel(int KC, int* nt) {
-  // Remote instances add 4 poller waves to 4 compute waves (KC >= 16) or up
-  // to 12 (KC <= 8); local instances hold up to 16 compute waves.
+  // Remote instances add 4 pollers_per_row(KC) poller waves to 4 compute
+  // waves (KC >= 16) or to up to 12 (KC <= 8); local instances hold up to 16
+  // compute waves.
   switch (KC) {
     case 4: *nt = 1024; return scan_kernel<KIND, 4, 1024, REMOTE>;
     case 8: *nt = 1024; return scan_kernel<KIND, 8, 1024, REMOTE>;
-    case 16: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 16, REMOTE ? 512 : 256, REMOTE>;
-    case 32: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 32, REMOTE ? 512 : 256, REMOTE>;
+    case 16: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 16, REMOTE ? 768 : 256, REMOTE>;
+    case 32: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 32, REMOTE ? 768 : 256, REMOTE>;
     case 64: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 64, REMOTE ? 512 : 256, REMOTE>;
     default: return nullptr;
   }
@@ -331,7 +347,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   rc = check_workspace(a, kCtrlBytes + pl.xh_bytes + pl.xw_bytes, who);
   if (rc) return rc;
   DFn fn = pick(kind, pl.remote, pl.KC, &pl.nt);
-  const int threads = 64 * (pl.nwc + (pl.remote ? kPollers : 0));
+  const int threads = 64 * (pl.nwc + (pl.remote ? 4 * pollers_per_row(pl.KC) : 0));
   const int per_set = pl.P * (kind == kMonarch1 ? pl.nb : 1);
 
   int G = pl.nrb, RB = 1;

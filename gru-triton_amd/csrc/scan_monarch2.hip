@@ -42,8 +42,8 @@ struct M2FParams {
   int T, B, H;
   int nb, bs, cpb, nq;  // nq = bs / 4 quads per phase
   int ngroups, RB, nrb, Bp, nwg;
-  int nwc;       // compute waves per workgroup
-  int hsz;       // floats per staged q_in(h) block (4 rows x H interleaved, plus read-over pad)
+  int nwc;       // compute waves per workgroup (quad groups, ceil(nq / 4))
+  int hs, zs;    // LDS row strides of the staged q_in(h) and z (floats)
   Quant qin, qout;
   int qin_after_first;
 };
@@ -51,15 +51,38 @@ struct M2FParams {
 // Unit of H that output i of L-block b lands on: y = P^T v, v index m = b bs + i.
 __device__ __forceinline__ int m2_unit(int m, int nb, int bs) { return (m % nb) * bs + m / nb; }
 
-template <int QW, int NT>
+// Sum of a quad-group MFMA's four K slices, picked for the lane's row: the
+// chain's D holds, in lane 16 qs + 4 sl + j, VGPR v = slice sl's partial for
+// row v, unit j of quad qs. Two row rotations sum the slices (every lane of a
+// quad column then holds all four rows), and the lane keeps row sl.
+__device__ __forceinline__ float slice_sum(f4 acc, int sl) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    acc[c] += row_ror<8>(acc[c]);
+    acc[c] += row_ror<4>(acc[c]);
+  }
+  const float lo = (sl & 1) ? acc[1] : acc[0];
+  const float hi = (sl & 1) ? acc[3] : acc[2];
+  return (sl & 2) ? hi : lo;
+}
+
+// Fused kernel. Quad-group MFMA layout: lane l = 16 qs + 4 sl + j supplies
+// A[row j] and B[unit j] of K slice sl for quad qs, so one
+// v_mfma_f32_4x4x1_16b_f32 covers 4 quads (16 outputs) x 4 rows x 4 K slices
+// and a chain of SP instructions covers K = 4 SP (slice sl takes k in
+// [sl SP, sl SP + SP)). The slice sum is two row rotations per accumulator
+// row (slice_sum), and every lane ends with one (row, output): phase 2's
+// gate epilogue runs on all 64 lanes. Compute wave w owns quads 4 w .. 4 w + 3
+// of both phases; three gate chains, two accumulators each.
+// EXACT: bs == 4 SP; otherwise phase-1 operands past the block are zeroed.
+template <int SP, bool EXACT, int NT>
 __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
-  constexpr int KC = 4;  // bs <= 64
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nwc = p.nwc;
   const bool poller = wave >= nwc;
-  const int j = lane & 3, kb4 = lane >> 2, s = (lane >> 2) & 3;
+  const int j = lane & 3, sl = (lane >> 2) & 3, qs = lane >> 4;
   const int bs = p.bs, H = p.H, nb = p.nb;
 
   const int gid = blockIdx.x % p.ngroups;
@@ -67,16 +90,17 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
   const int rb_begin = gid * p.RB;
   const int rb_end = min(rb_begin + p.RB, p.nrb);
   const int nrbm = rb_end - rb_begin;
-  const int U = bs;  // units per workgroup, in y order i = 0 .. bs-1
+  const int U = bs;  // outputs per workgroup, in y order i = 0 .. bs-1
+  const int HS = p.hs, ZS = p.zs;
 
-  float* hst = lds;                     // [2][hsz]     staged q_in(h), all H (il_index)
-  float* zst = hst + 2 * p.hsz;         // [3][256]     z_g in y order of block b (il_index)
-  float* hk = zst + 3 * 256;            // [RB][4][U]   raw h of this workgroup's units
+  float* hst = lds;                     // [2][4][HS]   staged q_in(h), row-major
+  float* zst = hst + 8 * HS;            // [3][4][ZS]   z_g in y order of block b, row-major
+  float* hk = zst + 12 * ZS;            // [RB][4][U]   raw h of this workgroup's units
   float* gst = hk + p.RB * 4 * U;       // [2][4][3][U] staged gi
   int* flags = reinterpret_cast<int*>(gst + 24 * U);  // [0] compute-wave iterations published,
                                                       // [1] bit 0: group on one XCD, bit 1: a
                                                       // wait of this workgroup gave up
-  const int lds_floats = 2 * p.hsz + 3 * 256 + p.RB * 4 * U + 24 * U + 4;
+  const int lds_floats = 8 * HS + 12 * ZS + p.RB * 4 * U + 24 * U + 4;
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
   const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -96,7 +120,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
         v = p.h0[(int64_t)row * p.sh0_b + k];
         if (p.qin.on) v = fake_quant(v, p.qin);
       }
-      hst[il_index(r, k)] = v;
+      hst[r * HS + k] = v;
     }
     for (int w = threadIdx.x; w < nrbm * 4 * U; w += blockDim.x) {
       const int rbl = w / (4 * U), rem = w - rbl * 4 * U, r = rem / U, i = rem - r * U;
@@ -112,78 +136,89 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
   lds_barrier();
 
   if (!poller) {
-    // Phase-1 quad q of this wave: qd = wave + nwc q -> first-factor block
-    // a = qd / (cpb / 4), rows c0 .. c0 + 3 of R_g[a]. Phase-2 quad: rows
-    // 4 qd .. 4 qd + 3 of L_g[b].
+    // Quad qd = 4 wave + qs. Phase 1: entries z[a bs + c0 + j] of first-factor
+    // block a = qd / (cpb / 4), c0 = b cpb + 4 (qd - a cpb / 4). Phase 2: rows
+    // 4 qd + j of L_g[b].
     const int qpa = p.cpb / 4;
-    float wr[QW][3][KC], wl[QW][3][KC];
-    int ablk[QW], zpos[QW];
-    bool ok[QW];
+    const int qd = 4 * wave + qs;
+    const bool qok = qd < p.nq;
+    const int a = qok ? qd / qpa : 0;
+    const int c0 = b * p.cpb + 4 * (qd - a * qpa);
+    const int zpos = (c0 + j) * nb + a - b * bs;  // this lane's z entry in y order (row sl)
+    float wr[3][SP], wl[3][SP];
 #pragma unroll
-    for (int q = 0; q < QW; ++q) {
-      const int qd = wave + nwc * q;
-      ok[q] = qd < p.nq;
-      const int a = ok[q] ? qd / qpa : 0;
-      const int c0 = b * p.cpb + 4 * (qd - a * qpa);
-      ablk[q] = a;
-      zpos[q] = (c0 + j) * nb + a - b * bs;  // this lane's z entry in y order (lane < 16)
-      load_w<KC>(p.w, nb, bs, a, c0, j, kb4, ok[q], wr[q]);
-      load_w<KC>(p.w2, nb, bs, b, 4 * qd, j, kb4, ok[q], wl[q]);
+    for (int g = 0; g < 3; ++g) {
+      const float* r1 = p.w + ((int64_t)(g * nb + a) * bs + c0 + j) * bs;
+      const float* r2 = p.w2 + ((int64_t)(g * nb + b) * bs + 4 * qd + j) * bs;
+#pragma unroll
+      for (int m = 0; m < SP; ++m) {
+        const int k = sl * SP + m;
+        const bool okk = qok && (EXACT || k < bs);
+        wr[g][m] = okk ? r1[k] : 0.0f;
+        wl[g][m] = okk ? r2[k] : 0.0f;
+      }
     }
-    // Epilogue lanes: lanes 16 q .. 16 q + 15 take phase-2 quad q.
-    const int qe = lane >> 4;
-    const int qde = wave + nwc * (qe < QW ? qe : 0);
-    const bool lead = lane < 16 * QW && qde < p.nq;
-    const int ie = 4 * qde + j;  // this lane's output in y order
+    const int ie = 4 * qd + j;  // this lane's output in y order (row sl)
     const int unit = m2_unit(b * bs + ie, nb, bs);
     float bias[3];
 #pragma unroll
-    for (int g = 0; g < 3; ++g) bias[g] = lead ? gate_scale(g) * p.bh[g * H + unit] : 0.0f;  // for gru_update_gb
-    const int64_t lane_out = (int64_t)s * p.so_b + unit;  // row = 4 rb + s
-    const int64_t lane_xh = (int64_t)s * H + unit;
+    for (int g = 0; g < 3; ++g) bias[g] = qok ? gate_scale(g) * p.bh[g * H + unit] : 0.0f;  // for gru_update_gb
+    const int64_t lane_out = (int64_t)sl * p.so_b + unit;  // row = 4 rb + sl
+    const int64_t lane_xh = (int64_t)sl * H + unit;
+    const int a1off = j * HS + a * bs + sl * SP;  // phase-1 A: row j of q_in(h), block a, slice sl
+    const int a2off = j * ZS + sl * SP;           // phase-2 A: row j of z_g, slice sl
+    float* zw = zst + sl * ZS + zpos;             // phase-1 result of this lane (gate g at + 4 g ZS)
 
     for (int it = 0; it < niter; ++it) {
       const int t = it / nrbm;
       const int rbl = it - t * nrbm;
       const int rb = rb_begin + rbl;
       const int buf = it & 1;
-      const float* hs = hst + buf * p.hsz;
       // phase 1: z_g entries of this wave's quads -> zst (y order)
+      {
+        float a1[3][SP];
+        const float* src = hst + buf * 4 * HS + a1off;
 #pragma unroll
-      for (int q = 0; q < QW; ++q) {
-        float a1[3][KC];
-        lds_a_il<KC>(hs + 4 * ablk[q] * bs, lane, a1[0]);  // block a starts at k = a bs, bs % 4 == 0
+        for (int q = 0; q < SP / 4; ++q) {
+          const f4 v = *reinterpret_cast<const f4*>(src + 4 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a1[0][4 * q + e] = (EXACT || sl * SP + 4 * q + e < bs) ? v[e] : 0.0f;
+        }
         f4 acc[3];
-        mfma3<KC, true>(a1, wr[q], acc);
+        mfma3<SP, true>(a1, wr, acc);
 #pragma unroll
         for (int g = 0; g < 3; ++g) {
-          const float z = reduce16(acc[g], s);
-          if (lane < 16 && ok[q]) zst[g * 256 + il_index(s, zpos[q])] = z;
+          const float z = slice_sum(acc[g], sl);
+          if (qok) zw[4 * g * ZS] = z;
         }
       }
       lds_barrier();
       // phase 2: L_g[b] times the staged z_g
-      float a2[3][KC];
-#pragma unroll
-      for (int g = 0; g < 3; ++g) lds_a_il<KC>(zst + g * 256, lane, a2[g]);
-      float gh[3] = {0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < QW; ++q) {
-        f4 acc[3];
-        mfma3<KC, false>(a2, wl[q], acc);
+      float gh[3];
+      {
+        float a2[3][SP];
 #pragma unroll
         for (int g = 0; g < 3; ++g) {
-          const float v = reduce16(acc[g], s);
-          gh[g] = (qe == q) ? v : gh[g];
+          const float* src = zst + 4 * g * ZS + a2off;
+#pragma unroll
+          for (int q = 0; q < SP / 4; ++q) {
+            const f4 v = *reinterpret_cast<const f4*>(src + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a2[g][4 * q + e] = v[e];
+          }
         }
+        f4 acc[3];
+        mfma3<SP, false>(a2, wl, acc);
+#pragma unroll
+        for (int g = 0; g < 3; ++g) gh[g] = slice_sum(acc[g], sl);
       }
-      const int row = 4 * rb + s;
-      const float* gs_ = gst + buf * 12 * U + s * 3 * U + ie;
-      float* hkp = hk + (rbl * 4 + s) * U + ie;
+      const int row = 4 * rb + sl;
+      const float* gs_ = gst + buf * 12 * U + sl * 3 * U + ie;
+      float* hkp = hk + (rbl * 4 + sl) * U + ie;
       // after a give-up the workgroup's outputs are NaN and it publishes nothing more
       const int fl = __builtin_amdgcn_readfirstlane(flags[1]);
       const bool dead = (fl & 2) != 0;
-      if (lead) {
+      if (qok) {
         const float hprev = *hkp;
         float hn = gru_update_gb(gs_[0], gs_[U], gs_[2 * U], gh[0], gh[1], gh[2], bias[0], bias[1], bias[2], hprev);
         if (p.qout.on) hn = fake_quant(hn, p.qout);
@@ -222,7 +257,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       }
       lds_barrier();  // the compute waves' phase-1/phase-2 barrier
       if (more) {
-        float* hs = hst + (nx & 1) * p.hsz;
+        float* hs = hst + (nx & 1) * 4 * HS + pr * HS;
         if (t2 == 0) {
           for (int k = lane; k < H; k += 64) {
             float v = 0.0f;
@@ -230,7 +265,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
               v = p.h0[(int64_t)row * p.sh0_b + k];
               if (p.qin.on) v = fake_quant(v, p.qin);
             }
-            hs[il_index(pr, k)] = v;
+            hs[k] = v;
           }
         } else {
           if (alive && pr == 0 && nx == nrbm &&  // first exchange of the launch
@@ -239,14 +274,13 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
           if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
           const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * H;
           const uint32_t tag = base + (uint32_t)t2;
-          // H words of row pr in chunks of 512 (a chunk starting at k0 fills
-          // the interleaved block from il_index(0, k0) = 4 k0)
+          // H words of row pr, in chunks of 512
           if (!alive) {
           } else if (H <= 256) {
-            poll_row_il<4>(ctrl, hb, hs, pr, H, tag, alive);
+            poll_row_il<4, false>(ctrl, hb, hs, pr, H, tag, alive);
           } else {
             for (int k0 = 0; k0 < H && alive; k0 += 512)
-              poll_row_il<8>(ctrl, hb + k0, hs + 4 * k0, pr, min(512, H - k0), tag, alive);
+              poll_row_il<8, false>(ctrl, hb + k0, hs + k0, pr, min(512, H - k0), tag, alive);
           }
           if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
@@ -479,30 +513,32 @@ int plan_m2(const gs_args* a, M2Plan* pl, const char* who) {
 typedef void (*M2FFn)(M2FParams);
 
 struct M2FPlan {
-  int QW, nt, nwc, nrb, Bp, hsz;
+  int nwc, nrb, Bp, hs, zs;
   int64_t xh_bytes, xw_bytes;
   M2FFn fn;
 };
 
 // The fused kernel covers bs <= 64 with nb | bs and bs / nb a multiple of 4,
-// for H <= 2048.
+// for H <= 2048. A chain covers K = 4 SP with SP in {4, 8, 16}, the smallest
+// with 4 SP >= bs.
 bool plan_fused(const gs_args* a, M2FPlan* pl) {
   const int nb = (int)a->nblocks, bs = (int)a->blksz, H = (int)a->H;
   if (bs > 64 || bs % nb != 0 || (bs / nb) % 4 != 0 || H > 2048) return false;
   const int nq = bs / 4;
-  pl->QW = nq <= 12 ? 1 : 2;
-  pl->nwc = (nq + pl->QW - 1) / pl->QW;
-  if (pl->QW == 1) {
-    pl->nt = 1024;
-    pl->fn = monarch2_fused_kernel<1, 1024>;
-  } else {
-    pl->nt = 768;
-    pl->fn = monarch2_fused_kernel<2, 768>;
-  }
+  pl->nwc = (nq + 3) / 4;
+  const int SP = bs <= 16 ? 4 : bs <= 32 ? 8 : 16;
+  const bool exact = bs == 4 * SP;
+  if (SP == 4) pl->fn = exact ? monarch2_fused_kernel<4, true, 512> : monarch2_fused_kernel<4, false, 512>;
+  else if (SP == 8) pl->fn = exact ? monarch2_fused_kernel<8, true, 512> : monarch2_fused_kernel<8, false, 512>;
+  else pl->fn = exact ? monarch2_fused_kernel<16, true, 512> : monarch2_fused_kernel<16, false, 512>;
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
-  // phase-1 operand reads cover 64 k from a block start: up to 64 - bs past H
-  pl->hsz = 4 * H + 256;
+  // Row strides = 4 mod 64 floats: phase-1 and phase-2 operand reads of a
+  // quad's 16 lanes (row j, slice sl) then hit distinct banks at SP = 16.
+  // Phase-1 reads of the last block run up to 4 SP - bs past H (masked when
+  // bs < 4 SP) and stay inside the LDS allocation.
+  pl->hs = (H + 63) / 64 * 64 + 4;
+  pl->zs = 4 * SP + 4;
   // pollers load up to 511 words past the last chunk start of a row
   pl->xh_bytes = align256(2 * (int64_t)pl->Bp * H * 8 + 512 * 8);
   pl->xw_bytes = align256((int64_t)pl->nrb * nb * 8);
@@ -518,7 +554,7 @@ int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const cha
   for (int pass = 0; pass < 2; ++pass) {
     RB = (pl.nrb + G - 1) / G;
     G = (pl.nrb + RB - 1) / RB;
-    lds = sizeof(float) * (size_t)(2 * pl.hsz + 3 * 256 + RB * 4 * U + 24 * U + 4);
+    lds = sizeof(float) * (size_t)(8 * pl.hs + 12 * pl.zs + RB * 4 * U + 24 * U + 4);
     if (lds > 65536)
       GS_CHECK_HIP(hipFuncSetAttribute((const void*)pl.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     int gfit = 0;
@@ -556,7 +592,8 @@ int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const cha
   p.Bp = pl.Bp;
   p.nwg = G * nb;
   p.nwc = pl.nwc;
-  p.hsz = pl.hsz;
+  p.hs = pl.hs;
+  p.zs = pl.zs;
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
   p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
