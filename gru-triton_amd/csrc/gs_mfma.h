@@ -191,27 +191,31 @@ __device__ __forceinline__ void lds_a(const float* row, int kb4, float (&a)[KC])
   }
 }
 
-// Three MFMA chains (one per gate), two accumulators each for issue overlap.
-// SHARED_A: every gate multiplies a[0].
-template <int KC, bool SHARED_A>
+// Three MFMA chains (one per gate), NA accumulators each for issue overlap
+// (instruction m feeds accumulator m % NA; NA divides KC). SHARED_A: every
+// gate multiplies a[0].
+template <int KC, bool SHARED_A, int NA = 2>
 __device__ __forceinline__ void mfma3(const float (&a)[3][KC], const float (&wr)[3][KC], f4 (&acc)[3]) {
-  f4 acc0[3], acc1[3];
+  static_assert(NA == 2 || NA == 4, "accumulators per gate");
+  static_assert(KC % NA == 0, "NA divides KC");
+  f4 part[NA][3];
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+#pragma unroll
+    for (int g = 0; g < 3; ++g) part[i][g] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < KC; m += NA) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+#pragma unroll
+      for (int g = 0; g < 3; ++g)
+        part[i][g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[SHARED_A ? 0 : g][m + i], wr[g][m + i], part[i][g], 0, 0, 0);
+  }
 #pragma unroll
   for (int g = 0; g < 3; ++g) {
-    acc0[g] = f4{0.f, 0.f, 0.f, 0.f};
-    acc1[g] = f4{0.f, 0.f, 0.f, 0.f};
+    acc[g] = part[0][g] + part[1][g];
+    if constexpr (NA == 4) acc[g] += part[2][g] + part[3][g];
   }
-#pragma unroll
-  for (int m = 0; m < KC; m += 2) {
-#pragma unroll
-    for (int g = 0; g < 3; ++g)
-      acc0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[SHARED_A ? 0 : g][m], wr[g][m], acc0[g], 0, 0, 0);
-#pragma unroll
-    for (int g = 0; g < 3; ++g)
-      acc1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[SHARED_A ? 0 : g][m + 1], wr[g][m + 1], acc1[g], 0, 0, 0);
-  }
-#pragma unroll
-  for (int g = 0; g < 3; ++g) acc[g] = acc0[g] + acc1[g];
 }
 
 

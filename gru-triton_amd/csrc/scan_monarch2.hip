@@ -13,7 +13,7 @@
 // in y order, multiplies by L_g[b] (phase 2) and runs the gate epilogue for
 // the units y = P^T v places its outputs on. One exchange per step, of
 // q_in(h_t), exactly as in the dense kernel: compute waves publish tagged
-// words and four poller waves, one per batch row, stage the next step's
+// words and eight poller waves, two per batch row, stage the next step's
 // q_in(h) and gate inputs into LDS.
 //
 // monarch2_split_kernel (any nb, bs). A group covers all H units for its
@@ -26,7 +26,7 @@
 namespace gs {
 namespace {
 
-constexpr int kPollers = 4;  // fused kernel: poller waves per workgroup, one per row
+constexpr int kPollers = 8;  // fused kernel: poller waves per workgroup, two per row
 
 struct M2FParams {
   const float* gi;
@@ -193,6 +193,15 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
         }
       }
       lds_barrier();
+      // Epilogue inputs, read now so that their LDS latency overlaps phase 2
+      // (lanes of quads past nq read a clamped address and discard it).
+      const int iec = min(ie, U - 1);
+      const float* gs_ = gst + buf * 12 * U + sl * 3 * U + iec;
+      const float gir = gs_[0], giz = gs_[U], gin = gs_[2 * U];
+      float* hkp = hk + (rbl * 4 + sl) * U + iec;
+      const float hprev = *hkp;
+      // after a give-up the workgroup's outputs are NaN and it publishes nothing more
+      const int fl = __builtin_amdgcn_readfirstlane(flags[1]);
       // phase 2: L_g[b] times the staged z_g
       float gh[3];
       {
@@ -213,14 +222,9 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
         for (int g = 0; g < 3; ++g) gh[g] = slice_sum(acc[g], sl);
       }
       const int row = 4 * rb + sl;
-      const float* gs_ = gst + buf * 12 * U + sl * 3 * U + ie;
-      float* hkp = hk + (rbl * 4 + sl) * U + ie;
-      // after a give-up the workgroup's outputs are NaN and it publishes nothing more
-      const int fl = __builtin_amdgcn_readfirstlane(flags[1]);
       const bool dead = (fl & 2) != 0;
       if (qok) {
-        const float hprev = *hkp;
-        float hn = gru_update_gb(gs_[0], gs_[U], gs_[2 * U], gh[0], gh[1], gh[2], bias[0], bias[1], bias[2], hprev);
+        float hn = gru_update_gb(gir, giz, gin, gh[0], gh[1], gh[2], bias[0], bias[1], bias[2], hprev);
         if (p.qout.on) hn = fake_quant(hn, p.qout);
         if (row < p.B) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = dead ? __builtin_nanf("") : hn;
         *hkp = hn;
@@ -237,8 +241,11 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       lds_barrier();
     }
   } else {
-    // Poller wave pr stages row pr of iteration it + 1 (see the dense kernel).
-    const int pr = wave - nwc;
+    // Poller waves 2 pr + part stage row pr of iteration it + 1 (see the dense
+    // kernel), each half of the row's words.
+    const int pq = wave - nwc;
+    const int pr = pq >> 1, part = pq & 1;
+    const int kh = (H + 127) / 128 * 64;  // first k of part 1
     constexpr int NGI = (3 * 64 + 63) / 64;  // 3 U <= 192 gate inputs per row
     bool alive = true;  // no wait of this wave has given up
     for (int it = 0; it < niter; ++it) {
@@ -252,14 +259,14 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       for (int i = 0; i < NGI; ++i) {
         const int w = lane + 64 * i;
         const int g = w / U, ii = w - g * U;
-        const bool okw = more && w < 3 * U && row < p.B;
+        const bool okw = more && part == 0 && w < 3 * U && row < p.B;
         gv[i] = okw ? p.gi[(int64_t)t2 * p.sg_t + (int64_t)row * p.sg_b + g * H + m2_unit(b * bs + ii, nb, bs)] : 0.0f;
       }
       lds_barrier();  // the compute waves' phase-1/phase-2 barrier
       if (more) {
         float* hs = hst + (nx & 1) * 4 * HS + pr * HS;
         if (t2 == 0) {
-          for (int k = lane; k < H; k += 64) {
+          for (int k = lane + part * kh; k < (part ? H : min(H, kh)); k += 64) {
             float v = 0.0f;
             if (row < p.B) {
               v = p.h0[(int64_t)row * p.sh0_b + k];
@@ -268,27 +275,25 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
             hs[k] = v;
           }
         } else {
-          if (alive && pr == 0 && nx == nrbm &&  // first exchange of the launch
+          if (alive && pq == 0 && nx == nrbm &&  // first exchange of the launch
               nb <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, nb, base + 1u, alive))
             __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
           const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * H;
           const uint32_t tag = base + (uint32_t)t2;
-          // H words of row pr, in chunks of 512
-          if (!alive) {
-          } else if (H <= 256) {
-            poll_row_il<4, false>(ctrl, hb, hs, pr, H, tag, alive);
-          } else {
-            for (int k0 = 0; k0 < H && alive; k0 += 512)
-              poll_row_il<8, false>(ctrl, hb + k0, hs + k0, pr, min(512, H - k0), tag, alive);
-          }
+          // this wave's half of row pr's H words, in chunks of 256
+          const int kend = part ? H : min(H, kh);
+          for (int k0 = part * kh; k0 < kend && alive; k0 += 256)
+            poll_row_il<4, false>(ctrl, hb + k0, hs + k0, pr, min(256, kend - k0), tag, alive);
           if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
+        if (part == 0) {
 #pragma unroll
-        for (int i = 0; i < NGI; ++i) {
-          const int w = lane + 64 * i;
-          if (w < 3 * U) gs_[w] = gv[i];
+          for (int i = 0; i < NGI; ++i) {
+            const int w = lane + 64 * i;
+            if (w < 3 * U) gs_[w] = gv[i];
+          }
         }
       }
       lds_barrier();
@@ -528,9 +533,9 @@ bool plan_fused(const gs_args* a, M2FPlan* pl) {
   pl->nwc = (nq + 3) / 4;
   const int SP = bs <= 16 ? 4 : bs <= 32 ? 8 : 16;
   const bool exact = bs == 4 * SP;
-  if (SP == 4) pl->fn = exact ? monarch2_fused_kernel<4, true, 512> : monarch2_fused_kernel<4, false, 512>;
-  else if (SP == 8) pl->fn = exact ? monarch2_fused_kernel<8, true, 512> : monarch2_fused_kernel<8, false, 512>;
-  else pl->fn = exact ? monarch2_fused_kernel<16, true, 512> : monarch2_fused_kernel<16, false, 512>;
+  if (SP == 4) pl->fn = exact ? monarch2_fused_kernel<4, true, 768> : monarch2_fused_kernel<4, false, 768>;
+  else if (SP == 8) pl->fn = exact ? monarch2_fused_kernel<8, true, 768> : monarch2_fused_kernel<8, false, 768>;
+  else pl->fn = exact ? monarch2_fused_kernel<16, true, 768> : monarch2_fused_kernel<16, false, 768>;
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
   // Row strides = 4 mod 64 floats: phase-1 and phase-2 operand reads of a
