@@ -51,10 +51,12 @@ __device__ __forceinline__ float quant_code(float x, const Quant& q) {
   return __builtin_rintf(__builtin_fmaf(r, q.inv, q0));
 }
 
-__device__ __forceinline__ float fake_quant(float x, const Quant& q) {
-  const float v = __builtin_fminf(__builtin_fmaxf(quant_code(x, q), q.qmin), q.qmax);
-  return v * q.scale;
+// The clamped integer level of fake_quant: fake_quant(x, q) == quant_level(x, q) * q.scale.
+__device__ __forceinline__ float quant_level(float x, const Quant& q) {
+  return __builtin_fminf(__builtin_fmaxf(quant_code(x, q), q.qmin), q.qmax);
 }
+
+__device__ __forceinline__ float fake_quant(float x, const Quant& q) { return quant_level(x, q) * q.scale; }
 
 constexpr float kLog2e = 1.4426950408889634f;
 

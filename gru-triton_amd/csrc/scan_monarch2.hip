@@ -46,6 +46,8 @@ struct M2FParams {
   int hs, zs;    // LDS row strides of the staged q_in(h) and z (floats)
   Quant qin, qout;
   int qin_after_first;
+  float pscale;  // packed exchange: the scale of the published levels
+  float pbias;   // -128 pscale (exact)
 };
 
 // Unit of H that output i of L-block b lands on: y = P^T v, v index m = b bs + i.
@@ -75,7 +77,18 @@ __device__ __forceinline__ float slice_sum(f4 acc, int sl) {
 // gate epilogue runs on all 64 lanes. Compute wave w owns quads 4 w .. 4 w + 3
 // of both phases; three gate chains, two accumulators each.
 // EXACT: bs == 4 SP; otherwise phase-1 operands past the block are zeroed.
-template <int SP, bool EXACT, int NT>
+//
+// PM > 0: packed exchange, for a published q_in(h) that is a fake-quant level
+// in [-128, 127] times pscale (int8 hidden quant). A quad's four lanes of one
+// row put their four levels, one byte each (level + 128 of output 4 qd + e in
+// byte e), into one tagged word at row position b nq + qd, so a row has H / 4
+// words instead of H, and each poller wave polls PM words per lane. The
+// consumer's value fma(byte, pscale, -128 pscale) rounds (byte - 128) pscale
+// once (-128 pscale is exact), so it is bit for bit the producer's fake_quant
+// result. (Bytes are stored biased because this compiler folded a signed byte
+// extract and an int-to-float conversion into an unsigned conversion of the
+// sign-extended byte, which decodes negative levels wrongly.)
+template <int SP, bool EXACT, int PM, int NT>
 __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
@@ -225,16 +238,43 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       const bool dead = (fl & 2) != 0;
       if (qok) {
         float hn = gru_update_gb(gir, giz, gin, gh[0], gh[1], gh[2], bias[0], bias[1], bias[2], hprev);
-        if (p.qout.on) hn = fake_quant(hn, p.qout);
+        float lv = 0.0f;  // level of the published value (packed exchange)
+        if (p.qout.on) {
+          lv = quant_level(hn, p.qout);
+          hn = lv * p.qout.scale;
+        }
         if (row < p.B) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = dead ? __builtin_nanf("") : hn;
         *hkp = hn;
         if (t + 1 < p.T && !dead) {
-          const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
-          uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * H + lane_xh;
-          if (t >= 1 && (fl & 1) != 0)
-            st_tagged_xcd(dst, hq, base + (uint32_t)t + 1u);
-          else
-            st_tagged(dst, hq, base + (uint32_t)t + 1u);
+          float hq = hn;
+          if (p.qin_after_first) {
+            lv = quant_level(hn, p.qin);
+            hq = lv * p.qin.scale;
+          }
+          const uint32_t tag = base + (uint32_t)t + 1u;
+          const bool xl = t >= 1 && (fl & 1) != 0;
+          if constexpr (PM > 0) {
+            // the quad's four levels, byte e from lane j = e (a quad is all active or all idle)
+            const int c = ((int)lv + 128) & 0xff;
+            const int c0 = __builtin_amdgcn_mov_dpp(c, 0x00, 0xF, 0xF, true);
+            const int c1 = __builtin_amdgcn_mov_dpp(c, 0x55, 0xF, 0xF, true);
+            const int c2 = __builtin_amdgcn_mov_dpp(c, 0xAA, 0xF, 0xF, true);
+            const int c3 = __builtin_amdgcn_mov_dpp(c, 0xFF, 0xF, 0xF, true);
+            const uint32_t word = (uint32_t)c0 | ((uint32_t)c1 << 8) | ((uint32_t)c2 << 16) | ((uint32_t)c3 << 24);
+            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb + sl) * (H / 4) + b * p.nq + qd;
+            if (j == 0) {
+              if (xl)
+                st_tagged_xcd(dst, __uint_as_float(word), tag);
+              else
+                st_tagged(dst, __uint_as_float(word), tag);
+            }
+          } else {
+            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * H + lane_xh;
+            if (xl)
+              st_tagged_xcd(dst, hq, tag);
+            else
+              st_tagged(dst, hq, tag);
+          }
         }
       }
       if (lane == 0) __hip_atomic_fetch_add(&flags[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -246,6 +286,19 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
     const int pq = wave - nwc;
     const int pr = pq >> 1, part = pq & 1;
     const int kh = (H + 127) / 128 * 64;  // first k of part 1
+    // Packed exchange: this wave polls words part 64 PM + lane + 64 m (m < PM)
+    // of a row, word w carrying outputs 4 qd + e (e < 4) of workgroup b' =
+    // w / nq, qd = w % nq, which land on units un[m][e].
+    constexpr int PMX = PM > 0 ? PM : 1;
+    int un[PMX][4];
+    const int nwrow = H / 4;  // packed words per row
+#pragma unroll
+    for (int m = 0; m < PMX; ++m) {
+      const int w = part * 64 * PM + lane + 64 * m;
+      const int bw = w / p.nq, qw = w - bw * p.nq;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) un[m][e] = PM > 0 && w < nwrow ? m2_unit(bw * bs + 4 * qw + e, nb, bs) : 0;
+    }
     constexpr int NGI = (3 * 64 + 63) / 64;  // 3 U <= 192 gate inputs per row
     bool alive = true;  // no wait of this wave has given up
     for (int it = 0; it < niter; ++it) {
@@ -279,12 +332,30 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
               nb <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, nb, base + 1u, alive))
             __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
-          const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * H;
           const uint32_t tag = base + (uint32_t)t2;
-          // this wave's half of row pr's H words, in chunks of 256
-          const int kend = part ? H : min(H, kh);
-          for (int k0 = part * kh; k0 < kend && alive; k0 += 256)
-            poll_row_il<4, false>(ctrl, hb + k0, hs + k0, pr, min(256, kend - k0), tag, alive);
+          if constexpr (PM > 0) {
+            // this wave's PM words per lane of row pr's H / 4 packed words
+            const int w0 = part * 64 * PM;
+            const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * nwrow + w0;
+            uint64_t v[PMX];
+            uint32_t valid = 0;
+            if (alive && w0 < nwrow) valid = poll_row_words<PMX>(ctrl, hb, nwrow - w0, tag, v, alive);
+#pragma unroll
+            for (int m = 0; m < PMX; ++m) {
+              if ((valid >> m) & 1u) {
+                const uint32_t x = (uint32_t)v[m];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  hs[un[m][e]] = __builtin_fmaf((float)((x >> (8 * e)) & 0xffu), p.pscale, p.pbias);
+              }
+            }
+          } else {
+            const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * H;
+            // this wave's half of row pr's H words, in chunks of 256
+            const int kend = part ? H : min(H, kh);
+            for (int k0 = part * kh; k0 < kend && alive; k0 += 256)
+              poll_row_il<4, false>(ctrl, hb + k0, hs + k0, pr, min(256, kend - k0), tag, alive);
+          }
           if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
@@ -518,7 +589,8 @@ int plan_m2(const gs_args* a, M2Plan* pl, const char* who) {
 typedef void (*M2FFn)(M2FParams);
 
 struct M2FPlan {
-  int nwc, nrb, Bp, hs, zs;
+  int nwc, nrb, Bp, hs, zs, pm;
+  float pscale;
   int64_t xh_bytes, xw_bytes;
   M2FFn fn;
 };
@@ -533,9 +605,26 @@ bool plan_fused(const gs_args* a, M2FPlan* pl) {
   pl->nwc = (nq + 3) / 4;
   const int SP = bs <= 16 ? 4 : bs <= 32 ? 8 : 16;
   const bool exact = bs == 4 * SP;
-  if (SP == 4) pl->fn = exact ? monarch2_fused_kernel<4, true, 768> : monarch2_fused_kernel<4, false, 768>;
-  else if (SP == 8) pl->fn = exact ? monarch2_fused_kernel<8, true, 768> : monarch2_fused_kernel<8, false, 768>;
-  else pl->fn = exact ? monarch2_fused_kernel<16, true, 768> : monarch2_fused_kernel<16, false, 768>;
+  // Packed exchange when the published value is a fake-quant level in
+  // [-128, 127] (q_in after q_out, or q_out when q_in repeats it or is off):
+  // PM words per lane for each of a row's two poller waves (H <= 16 * 64 for
+  // this kernel, so at most 128 words per wave).
+  const gs_quant& qp = (a->q_in.enabled && !same_quant(a->q_in, a->q_out)) ? a->q_in : a->q_out;
+  const bool pack = qp.enabled && qp.qmin >= -128 && qp.qmax <= 127;
+  const int half_words = (H / 4 + 1) / 2;
+  if (pack && half_words > 128) return false;
+  pl->pm = !pack ? 0 : half_words <= 64 ? 1 : 2;
+  pl->pscale = pack ? qp.scale : 1.0f;
+  switch (pl->pm * 8 + (SP == 4 ? 0 : SP == 8 ? 1 : 2) * 2 + (exact ? 1 : 0)) {
+#define GS_M2F(PMV, SPI, SPV)                                                          \
+  case PMV * 8 + SPI * 2 + 1: pl->fn = monarch2_fused_kernel<SPV, true, PMV, 768>; break; \
+  case PMV * 8 + SPI * 2 + 0: pl->fn = monarch2_fused_kernel<SPV, false, PMV, 768>; break;
+    GS_M2F(0, 0, 4) GS_M2F(0, 1, 8) GS_M2F(0, 2, 16)
+    GS_M2F(1, 0, 4) GS_M2F(1, 1, 8) GS_M2F(1, 2, 16)
+    GS_M2F(2, 0, 4) GS_M2F(2, 1, 8) GS_M2F(2, 2, 16)
+#undef GS_M2F
+    default: return false;
+  }
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
   // Row strides = 4 mod 64 floats: phase-1 and phase-2 operand reads of a
@@ -602,6 +691,8 @@ int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const cha
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
   p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
+  p.pscale = pl.pscale;
+  p.pbias = -128.0f * pl.pscale;
   hipLaunchKernelGGL(pl.fn, dim3(p.nwg), dim3(threads), lds, stream, p);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;

@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from gru_qat_amd.configs import Q_INT8_HIDDEN, make_config
-from parity_util import assert_fp32_parity, assert_quant_parity, small_cfg
+from parity_util import assert_fp32_parity, assert_fp32_teacher_forced, assert_quant_parity, small_cfg
 
 pytestmark = pytest.mark.gpu
 
@@ -114,6 +114,23 @@ def test_monarch_single_fp32(dev, shape, nb):
                                       ((4, 33, 512), 8)])
 def test_monarch_two_factor_fp32(dev, shape, nb):
     assert_fp32_parity(_monarch(shape, nb, two=True), dev)
+
+
+# Fused two-factor kernel with hidden quantizers. A published q_in(h) that is
+# an int8 fake-quant level goes through the packed exchange (four levels per
+# tagged word): H = 64 and 512 poll one word per lane, H = 1024 two. WIDE's
+# levels do not fit a byte and keep the fp32 exchange words.
+WIDE = (0.004, -1000, 1000)
+
+
+@pytest.mark.parametrize("shape,nb", [((6, 4, 64), 4), ((6, 5, 512), 8), ((5, 3, 1024), 16)])
+@pytest.mark.parametrize("qin,qout", [(Q, Q), (Q2, Q), (None, Q), (Q, None), (Q2, None), (WIDE, WIDE)])
+def test_monarch_two_factor_quant_modes(dev, shape, nb, qin, qout):
+    cfg = _monarch(shape, nb, two=True, h_in_quant=qin, h_out_quant=qout)
+    if qout is None:
+        assert_fp32_teacher_forced(cfg, dev)
+    else:
+        assert_quant_parity(cfg, dev)
 
 
 @pytest.mark.parametrize("shape,nb", [((6, 8, 64), 4), ((6, 8, 192), 4)])
