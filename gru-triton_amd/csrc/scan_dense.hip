@@ -59,9 +59,17 @@ struct DParams {
   int hsz;  // floats per LDS staging block (4 rows x 16 KC, interleaved)
   Quant qin, qout;
   int qin_after_first;
+  float pscale, pbias;  // packed exchange: scale of the published levels, -128 pscale
 };
 
-template <int KIND, int KC, int NT, bool REMOTE>
+// Packed exchange (PACK, dense remote mode, int8 hidden quant): a published
+// q_in(h) that is a fake-quant level in [-128, 127] times pscale travels as
+// one tagged word per quad of units and row (the four levels + 128, byte e
+// for unit 4 w + e of word w = unit / 4), H / 4 words per row instead of H.
+// A poller decodes a word into the four consecutive staged slots of its units
+// with fma(byte, pscale, -128 pscale), bit for bit the producer's value (see
+// the two-factor Monarch kernel, which packs the same way).
+template <int KIND, int KC, int NT, bool REMOTE, bool PACK = false>
 __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
@@ -179,7 +187,11 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
       float hn = gru_update_l2(__builtin_fmaf(kR, gh[0], cr), __builtin_fmaf(kR, gh[1], cz),
                                __builtin_fmaf(kN, gh[2], bias[2]), an2, hprev);
-      if (p.qout.on) hn = fake_quant(hn, p.qout);
+      float lv = 0.0f;  // level of the published value (packed exchange)
+      if (p.qout.on) {
+        lv = quant_level(hn, p.qout);
+        hn = lv * p.qout.scale;
+      }
       // flags[1] as staged for this iteration: after a give-up the workgroup's
       // outputs are NaN and it publishes nothing more
       const int fl = REMOTE ? __builtin_amdgcn_readfirstlane(flags[1]) : 0;
@@ -189,8 +201,27 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       if (lead && unit_ok) {
         *hkp = hn;
         if (t + 1 < p.T && !dead) {
-          const float hq = p.qin_after_first ? fake_quant(hn, p.qin) : hn;
-          if (REMOTE) {
+          float hq = hn;
+          if (p.qin_after_first) {
+            lv = quant_level(hn, p.qin);
+            hq = lv * p.qin.scale;
+          }
+          if constexpr (PACK) {
+            // lanes 4 s + j of one row hold the quad's four units (all valid or none)
+            const int c = ((int)lv + 128) & 0xff;
+            const int c0 = __builtin_amdgcn_mov_dpp(c, 0x00, 0xF, 0xF, true);
+            const int c1 = __builtin_amdgcn_mov_dpp(c, 0x55, 0xF, 0xF, true);
+            const int c2 = __builtin_amdgcn_mov_dpp(c, 0xAA, 0xF, 0xF, true);
+            const int c3 = __builtin_amdgcn_mov_dpp(c, 0xFF, 0xF, 0xF, true);
+            const uint32_t word = (uint32_t)c0 | ((uint32_t)c1 << 8) | ((uint32_t)c2 << 16) | ((uint32_t)c3 << 24);
+            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb + s) * (p.H / 4) + (unit >> 2);
+            if (j == 0) {
+              if (xcd_local)
+                st_tagged_xcd(dst, __uint_as_float(word), base + (uint32_t)t + 1u);
+              else
+                st_tagged(dst, __uint_as_float(word), base + (uint32_t)t + 1u);
+            }
+          } else if (REMOTE) {
             uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * p.H + lane_xh;
             if (xcd_local)
               st_tagged_xcd(dst, hq, base + (uint32_t)t + 1u);
@@ -250,11 +281,31 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
             if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
             // this wave's share of row pr's bs words: k in [part KW, part KW + KW)
             // (part KW is a multiple of 128, so the staged slots are those of il_index)
-            const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * p.H + klo;
             constexpr int KW = 16 * KC / NPR;
-            if (alive && part * KW < p.bs)
-              poll_row_il<KC / 4 / NPR>(ctrl, hb + part * KW, hs + 4 * part * KW, pr, min(KW, p.bs - part * KW),
-                                        base + (uint32_t)t2, alive);
+            if constexpr (PACK) {
+              // packed words w in [part KW / 4, part KW / 4 + KW / 4), PMW per lane
+              constexpr int PMW = KW / 4 >= 64 ? KW / 4 / 64 : 1;
+              const int nw = p.H / 4, w0 = part * (KW / 4);
+              const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * nw + w0;
+              uint64_t v[PMW];
+              uint32_t valid = 0;
+              if (alive && w0 < nw) valid = poll_row_words<PMW>(ctrl, hb, min(KW / 4, nw - w0), base + (uint32_t)t2, v, alive);
+#pragma unroll
+              for (int m = 0; m < PMW; ++m) {
+                if ((valid >> m) & 1u) {
+                  const uint32_t x = (uint32_t)v[m];
+                  f4 q;
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) q[e] = __builtin_fmaf((float)((x >> (8 * e)) & 0xffu), p.pscale, p.pbias);
+                  *reinterpret_cast<f4*>(hs + il_index(pr, 4 * (w0 + lane + 64 * m))) = q;
+                }
+              }
+            } else {
+              const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * p.H + klo;
+              if (alive && part * KW < p.bs)
+                poll_row_il<KC / 4 / NPR>(ctrl, hb + part * KW, hs + 4 * part * KW, pr, min(KW, p.bs - part * KW),
+                                          base + (uint32_t)t2, alive);
+            }
             if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           }
         }
@@ -275,22 +326,23 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
 
 typedef void (*DFn)(DParams);
 
-template <int KIND, bool REMOTE>
+template <int KIND, bool REMOTE, bool PACK = false>
 DFn pick_kernel(int KC, int* nt) {
   // Remote instances add 4 pollers_per_row(KC) poller waves to 4 compute
   // waves (KC >= 16) or to up to 12 (KC <= 8); local instances hold up to 16
   // compute waves.
   switch (KC) {
-    case 4: *nt = 1024; return scan_kernel<KIND, 4, 1024, REMOTE>;
-    case 8: *nt = 1024; return scan_kernel<KIND, 8, 1024, REMOTE>;
-    case 16: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 16, REMOTE ? 768 : 256, REMOTE>;
-    case 32: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 32, REMOTE ? 768 : 256, REMOTE>;
-    case 64: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 64, REMOTE ? 512 : 256, REMOTE>;
+    case 4: *nt = 1024; return scan_kernel<KIND, 4, 1024, REMOTE, PACK>;
+    case 8: *nt = 1024; return scan_kernel<KIND, 8, 1024, REMOTE, PACK>;
+    case 16: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 16, REMOTE ? 768 : 256, REMOTE, PACK>;
+    case 32: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 32, REMOTE ? 768 : 256, REMOTE, PACK>;
+    case 64: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 64, REMOTE ? 512 : 256, REMOTE, PACK>;
     default: return nullptr;
   }
 }
 
-DFn pick(int kind, bool remote, int KC, int* nt) {
+DFn pick(int kind, bool remote, int KC, int* nt, bool pack = false) {
+  if (kind == kDense && remote && pack) return pick_kernel<kDense, true, true>(KC, nt);
   if (kind == kDense) return remote ? pick_kernel<kDense, true>(KC, nt) : pick_kernel<kDense, false>(KC, nt);
   return remote ? pick_kernel<kMonarch1, true>(KC, nt) : pick_kernel<kMonarch1, false>(KC, nt);
 }
@@ -298,6 +350,8 @@ DFn pick(int kind, bool remote, int KC, int* nt) {
 struct DPlan {
   int KC, nt, nwc, P, nrb, Bp, hsz, nb, bs, qpb;
   bool remote;
+  bool pack;     // packed int8 exchange (dense remote mode)
+  float pscale;  // its level scale
   int64_t xh_bytes, xw_bytes;
 };
 
@@ -328,7 +382,12 @@ int plan_dense(int kind, const gs_args* a, DPlan* pl, const char* who) {
     pl->nwc = nwc;
     pl->P = (pl->qpb + nwc - 1) / nwc;
   }
-  pick(kind, pl->remote, pl->KC, &pl->nt);
+  // Packed exchange when the published value is a fake-quant level in
+  // [-128, 127] (q_in after q_out, or q_out when q_in repeats it or is off).
+  const gs_quant& qp = (a->q_in.enabled && !same_quant(a->q_in, a->q_out)) ? a->q_in : a->q_out;
+  pl->pack = kind == kDense && pl->remote && a->H % 4 == 0 && qp.enabled && qp.qmin >= -128 && qp.qmax <= 127;
+  pl->pscale = pl->pack ? qp.scale : 1.0f;
+  pick(kind, pl->remote, pl->KC, &pl->nt, pl->pack);
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
   pl->hsz = 64 * pl->KC;
@@ -346,7 +405,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   if (rc) return rc;
   rc = check_workspace(a, kCtrlBytes + pl.xh_bytes + pl.xw_bytes, who);
   if (rc) return rc;
-  DFn fn = pick(kind, pl.remote, pl.KC, &pl.nt);
+  DFn fn = pick(kind, pl.remote, pl.KC, &pl.nt, pl.pack);
   const int threads = 64 * (pl.nwc + (pl.remote ? 4 * pollers_per_row(pl.KC) : 0));
   const int per_set = pl.P * (kind == kMonarch1 ? pl.nb : 1);
 
@@ -402,6 +461,8 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
   p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
+  p.pscale = pl.pscale;
+  p.pbias = -128.0f * pl.pscale;
   hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), lds, stream, p);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;

@@ -20,6 +20,7 @@ pytestmark = pytest.mark.gpu
 
 Q = Q_INT8_HIDDEN
 Q2 = (0.02, -100, 100)
+WIDE = (0.004, -1000, 1000)  # levels beyond a byte
 
 # ---- diagonal -----------------------------------------------------------------------------
 
@@ -62,6 +63,21 @@ def test_dense_quant(dev, qin, qout):
     cfg = small_cfg(1, (8, 4, 64), h_in_quant=qin, h_out_quant=qout)
     if qout is None:
         assert_fp32_parity(cfg, dev)
+    else:
+        assert_quant_parity(cfg, dev)
+
+
+# Remote mode (the group spans workgroups) with hidden quantizers: an int8 level
+# published through the packed exchange, four levels per tagged word, at KC =
+# 8 (H 100), 16 (H 256), 32 (H 300 and 512; 300 leaves the second poller wave
+# 11 words) and 64 (H 1024, four words per lane). H 302 is not a multiple of 4
+# and WIDE's levels do not fit a byte: both keep the fp32 exchange words.
+@pytest.mark.parametrize("shape", [(5, 4, 100), (5, 3, 256), (5, 4, 300), (6, 5, 512), (4, 3, 1024), (4, 3, 302)])
+@pytest.mark.parametrize("qin,qout", [(Q, Q), (Q2, Q), (None, Q), (Q, None), (WIDE, WIDE)])
+def test_dense_remote_quant_modes(dev, shape, qin, qout):
+    cfg = small_cfg(1, shape, h_in_quant=qin, h_out_quant=qout)
+    if qout is None:
+        assert_fp32_teacher_forced(cfg, dev)
     else:
         assert_quant_parity(cfg, dev)
 
@@ -120,7 +136,6 @@ def test_monarch_two_factor_fp32(dev, shape, nb):
 # an int8 fake-quant level goes through the packed exchange (four levels per
 # tagged word): H = 64 and 512 poll one word per lane, H = 1024 two. WIDE's
 # levels do not fit a byte and keep the fp32 exchange words.
-WIDE = (0.004, -1000, 1000)
 
 
 @pytest.mark.parametrize("shape,nb", [((6, 4, 64), 4), ((6, 5, 512), 8), ((5, 3, 1024), 16)])
