@@ -10,7 +10,7 @@
 // z[a * bs + c] for every first-factor block a and c in [b cpb, (b + 1) cpb),
 // cpb = bs / nb, so the workgroup computes exactly those bs entries of z_g
 // itself (phase 1, quads of 4 consecutive c under one a), stages them in LDS
-// in y order, multiplies by L_g[b] (phase 2) and runs the gate epilogue for
+// (quad order, below), multiplies by L_g[b] (phase 2) and runs the gate epilogue for
 // the units y = P^T v places its outputs on. One exchange per step, of
 // q_in(h_t), exactly as in the dense kernel: compute waves publish tagged
 // words and eight poller waves, two per batch row, stage the next step's
@@ -44,6 +44,8 @@ struct M2FParams {
   int ngroups, RB, nrb, Bp, nwg;
   int nwc;       // compute waves per workgroup (quad groups, ceil(nq / 4))
   int hs, zs;    // LDS row strides of the staged q_in(h) and z (floats)
+  int hpad;      // pad floats after every 256 units of a staged q_in(h) row (0 unless 256 % bs == 0)
+  int ks, gs;    // LDS row strides of the raw h and of the staged gate inputs (floats)
   Quant qin, qout;
   int qin_after_first;
   float pscale;  // packed exchange: the scale of the published levels
@@ -52,6 +54,12 @@ struct M2FParams {
 
 // Unit of H that output i of L-block b lands on: y = P^T v, v index m = b bs + i.
 __device__ __forceinline__ int m2_unit(int m, int nb, int bs) { return (m % nb) * bs + m / nb; }
+
+// LDS chunk of z quad qd: qd with bits 0 and 2 swapped when `swap` (an
+// involution, so also the inverse map).
+__device__ __forceinline__ int m2_zchunk(int qd, int swap) {
+  return swap ? (qd & ~5) | ((qd & 1) << 2) | ((qd >> 2) & 1) : qd;
+}
 
 // Sum of a quad-group MFMA's four K slices, picked for the lane's row: the
 // chain's D holds, in lane 16 qs + 4 sl + j, VGPR v = slice sl's partial for
@@ -77,6 +85,18 @@ __device__ __forceinline__ float slice_sum(f4 acc, int sl) {
 // gate epilogue runs on all 64 lanes. Compute wave w owns quads 4 w .. 4 w + 3
 // of both phases; three gate chains, two accumulators each.
 // EXACT: bs == 4 SP; otherwise phase-1 operands past the block are zeroed.
+//
+// LDS layout, for gfx950's banks as measured (4-byte accesses: 32 banks, 32
+// lanes a pass; 16-byte reads: 64 banks, 16 lanes a pass, lane groups
+// 8 i .. 8 i + 7 paired {0, 3}, {1, 2}, {4, 7}, {5, 6}). z sits in quad order:
+// entry j of phase-1 quad qd at 4 m2_zchunk(qd) + j of each batch row, and
+// phase 2's weights are gathered to match. A 32-lane pass of the z stores
+// then covers two quads whose chunks lie 4 apart, times four rows 4 floats
+// apart: 32 banks. Row strides of 4 mod 64 keep the 16-byte operand reads of
+// both phases on 64 banks; the raw h and gate-input rows are 8 mod 32 apart,
+// so the epilogue's 32-lane accesses (4 rows x 8 consecutive outputs) hit 32
+// banks; and the pad after every 256 units of a staged q_in(h) row spreads the
+// packed decode's stores (units 256 apart) across banks.
 //
 // PM > 0: packed exchange, for a published q_in(h) that is a fake-quant level
 // in [-128, 127] times pscale (int8 hidden quant). A quad's four lanes of one
@@ -104,16 +124,20 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
   const int rb_end = min(rb_begin + p.RB, p.nrb);
   const int nrbm = rb_end - rb_begin;
   const int U = bs;  // outputs per workgroup, in y order i = 0 .. bs-1
-  const int HS = p.hs, ZS = p.zs;
+  const int HS = p.hs, ZS = p.zs, KS = p.ks, GS = p.gs;
+  // LDS position of unit k in a staged q_in(h) row (hpad floats after every
+  // 256; a block of bs units then never straddles a pad)
+  const int hpad = p.hpad;
+  auto hx = [hpad](int k) { return k + (k >> 8) * hpad; };
 
-  float* hst = lds;                     // [2][4][HS]   staged q_in(h), row-major
-  float* zst = hst + 8 * HS;            // [3][4][ZS]   z_g in y order of block b, row-major
-  float* hk = zst + 12 * ZS;            // [RB][4][U]   raw h of this workgroup's units
-  float* gst = hk + p.RB * 4 * U;       // [2][4][3][U] staged gi
-  int* flags = reinterpret_cast<int*>(gst + 24 * U);  // [0] compute-wave iterations published,
+  float* hst = lds;                     // [2][4][HS]   staged q_in(h), row-major (hx)
+  float* zst = hst + 8 * HS;            // [3][4][ZS]   z_g of block b in quad order, row-major
+  float* hk = zst + 12 * ZS;            // [RB][4][KS]  raw h of this workgroup's units
+  float* gst = hk + p.RB * 4 * KS;      // [2][4][GS]   staged gi, [3][U] per row
+  int* flags = reinterpret_cast<int*>(gst + 8 * GS);  // [0] compute-wave iterations published,
                                                       // [1] bit 0: group on one XCD, bit 1: a
                                                       // wait of this workgroup gave up
-  const int lds_floats = 8 * HS + 12 * ZS + p.RB * 4 * U + 24 * U + 4;
+  const int lds_floats = 8 * HS + 12 * ZS + p.RB * 4 * KS + 8 * GS + 4;
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
   const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -133,17 +157,17 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
         v = p.h0[(int64_t)row * p.sh0_b + k];
         if (p.qin.on) v = fake_quant(v, p.qin);
       }
-      hst[r * HS + k] = v;
+      hst[r * HS + hx(k)] = v;
     }
     for (int w = threadIdx.x; w < nrbm * 4 * U; w += blockDim.x) {
       const int rbl = w / (4 * U), rem = w - rbl * 4 * U, r = rem / U, i = rem - r * U;
       const int row = 4 * (rb_begin + rbl) + r;
-      hk[w] = row < p.B ? p.h0[(int64_t)row * p.sh0_b + m2_unit(b * bs + i, nb, bs)] : 0.0f;
+      hk[(rbl * 4 + r) * KS + i] = row < p.B ? p.h0[(int64_t)row * p.sh0_b + m2_unit(b * bs + i, nb, bs)] : 0.0f;
     }
     for (int w = threadIdx.x; w < 12 * U; w += blockDim.x) {
       const int r = w / (3 * U), rem = w - r * 3 * U, g = rem / U, i = rem - g * U;
       const int row = 4 * rb + r;
-      gst[w] = row < p.B ? p.gi[(int64_t)row * p.sg_b + g * H + m2_unit(b * bs + i, nb, bs)] : 0.0f;
+      gst[r * GS + rem] = row < p.B ? p.gi[(int64_t)row * p.sg_b + g * H + m2_unit(b * bs + i, nb, bs)] : 0.0f;
     }
   }
   lds_barrier();
@@ -157,7 +181,18 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
     const bool qok = qd < p.nq;
     const int a = qok ? qd / qpa : 0;
     const int c0 = b * p.cpb + 4 * (qd - a * qpa);
-    const int zpos = (c0 + j) * nb + a - b * bs;  // this lane's z entry in y order (row sl)
+    // z quads are staged at swapped chunks exactly when nq = SP >= 8
+    constexpr int QSW = EXACT && SP >= 8 ? 1 : 0;
+    const int zpos = 4 * m2_zchunk(qd, QSW) + j;  // this lane's z entry (row sl)
+    // Phase-2 K position k = 4 i + e holds entry e of quad m2_zchunk(i), whose
+    // z index (a', c') is column c' nb + a' of L_g[b] (y order).
+    int ycol[SP / 4];
+#pragma unroll
+    for (int i = 0; i < SP / 4; ++i) {
+      const int qk = m2_zchunk(sl * (SP / 4) + i, QSW);
+      const int ak = qk / qpa;
+      ycol[i] = 4 * (qk - ak * qpa) * nb + ak;
+    }
     float wr[3][SP], wl[3][SP];
 #pragma unroll
     for (int g = 0; g < 3; ++g) {
@@ -168,7 +203,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
         const int k = sl * SP + m;
         const bool okk = qok && (EXACT || k < bs);
         wr[g][m] = okk ? r1[k] : 0.0f;
-        wl[g][m] = okk ? r2[k] : 0.0f;
+        wl[g][m] = okk ? r2[ycol[m >> 2] + (m & 3) * nb] : 0.0f;
       }
     }
     const int ie = 4 * qd + j;  // this lane's output in y order (row sl)
@@ -178,7 +213,9 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
     for (int g = 0; g < 3; ++g) bias[g] = qok ? gate_scale(g) * p.bh[g * H + unit] : 0.0f;  // for gru_update_gb
     const int64_t lane_out = (int64_t)sl * p.so_b + unit;  // row = 4 rb + sl
     const int64_t lane_xh = (int64_t)sl * H + unit;
-    const int a1off = j * HS + a * bs + sl * SP;  // phase-1 A: row j of q_in(h), block a, slice sl
+    // phase-1 A: row j of q_in(h), block a, slice sl (a block lies inside one
+    // 256-run when hpad is on, so its reads stay contiguous)
+    const int a1off = j * HS + hx(a * bs) + sl * SP;
     const int a2off = j * ZS + sl * SP;           // phase-2 A: row j of z_g, slice sl
     float* zw = zst + sl * ZS + zpos;             // phase-1 result of this lane (gate g at + 4 g ZS)
 
@@ -209,9 +246,9 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       // Epilogue inputs, read now so that their LDS latency overlaps phase 2
       // (lanes of quads past nq read a clamped address and discard it).
       const int iec = min(ie, U - 1);
-      const float* gs_ = gst + buf * 12 * U + sl * 3 * U + iec;
+      const float* gs_ = gst + buf * 4 * GS + sl * GS + iec;
       const float gir = gs_[0], giz = gs_[U], gin = gs_[2 * U];
-      float* hkp = hk + (rbl * 4 + sl) * U + iec;
+      float* hkp = hk + (rbl * 4 + sl) * KS + iec;
       const float hprev = *hkp;
       // after a give-up the workgroup's outputs are NaN and it publishes nothing more
       const int fl = __builtin_amdgcn_readfirstlane(flags[1]);
@@ -285,7 +322,9 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
     // kernel), each half of the row's words.
     const int pq = wave - nwc;
     const int pr = pq >> 1, part = pq & 1;
-    const int kh = (H + 127) / 128 * 64;  // first k of part 1
+    // first k of part 1: a multiple of 256 when q_in(h) rows are padded, so
+    // that the 256-word poll chunks below stay contiguous in LDS
+    const int kh = hpad ? (H / 2 + 255) / 256 * 256 : (H + 127) / 128 * 64;
     // Packed exchange: this wave polls words part 64 PM + lane + 64 m (m < PM)
     // of a row, word w carrying outputs 4 qd + e (e < 4) of workgroup b' =
     // w / nq, qd = w % nq, which land on units un[m][e].
@@ -297,7 +336,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       const int w = part * 64 * PM + lane + 64 * m;
       const int bw = w / p.nq, qw = w - bw * p.nq;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) un[m][e] = PM > 0 && w < nwrow ? m2_unit(bw * bs + 4 * qw + e, nb, bs) : 0;
+      for (int e = 0; e < 4; ++e) un[m][e] = PM > 0 && w < nwrow ? hx(m2_unit(bw * bs + 4 * qw + e, nb, bs)) : 0;
     }
     constexpr int NGI = (3 * 64 + 63) / 64;  // 3 U <= 192 gate inputs per row
     bool alive = true;  // no wait of this wave has given up
@@ -325,7 +364,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
               v = p.h0[(int64_t)row * p.sh0_b + k];
               if (p.qin.on) v = fake_quant(v, p.qin);
             }
-            hs[k] = v;
+            hs[hx(k)] = v;
           }
         } else {
           if (alive && pq == 0 && nx == nrbm &&  // first exchange of the launch
@@ -354,11 +393,11 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
             // this wave's half of row pr's H words, in chunks of 256
             const int kend = part ? H : min(H, kh);
             for (int k0 = part * kh; k0 < kend && alive; k0 += 256)
-              poll_row_il<4, false>(ctrl, hb + k0, hs + k0, pr, min(256, kend - k0), tag, alive);
+              poll_row_il<4, false>(ctrl, hb + k0, hs + hx(k0), pr, min(256, kend - k0), tag, alive);
           }
           if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
-        float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
+        float* gs_ = gst + (nx & 1) * 4 * GS + pr * GS;
         if (part == 0) {
 #pragma unroll
           for (int i = 0; i < NGI; ++i) {
@@ -589,7 +628,7 @@ int plan_m2(const gs_args* a, M2Plan* pl, const char* who) {
 typedef void (*M2FFn)(M2FParams);
 
 struct M2FPlan {
-  int nwc, nrb, Bp, hs, zs, pm;
+  int nwc, nrb, Bp, hs, zs, pm, hpad, ks, gs;
   float pscale;
   int64_t xh_bytes, xw_bytes;
   M2FFn fn;
@@ -627,12 +666,17 @@ bool plan_fused(const gs_args* a, M2FPlan* pl) {
   }
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
-  // Row strides = 4 mod 64 floats: phase-1 and phase-2 operand reads of a
-  // quad's 16 lanes (row j, slice sl) then hit distinct banks at SP = 16.
-  // Phase-1 reads of the last block run up to 4 SP - bs past H (masked when
-  // bs < 4 SP) and stay inside the LDS allocation.
-  pl->hs = (H + 63) / 64 * 64 + 4;
+  // LDS layout (the kernel's comment gives the bank reasoning). Phase-1 reads
+  // of the last block run up to 4 SP - bs past H (masked when bs < 4 SP) and
+  // stay inside the LDS allocation. The packed decode's 32-lane stores reach
+  // H / 256 runs of 256 units (H = 512: 2, 1024: 4), so the pad is 32 / runs
+  // banks.
+  pl->hpad = 256 % bs != 0 ? 0 : H > 512 ? 8 : 16;
+  const int hlen = H + ((H - 1) >> 8) * pl->hpad;  // padded row length
+  pl->hs = (hlen + 63) / 64 * 64 + 4;
   pl->zs = 4 * SP + 4;
+  pl->ks = (bs + 63) / 64 * 64 + 8;
+  pl->gs = (3 * bs + 63) / 64 * 64 + 8;
   // pollers load up to 511 words past the last chunk start of a row
   pl->xh_bytes = align256(2 * (int64_t)pl->Bp * H * 8 + 512 * 8);
   pl->xw_bytes = align256((int64_t)pl->nrb * nb * 8);
@@ -642,13 +686,12 @@ bool plan_fused(const gs_args* a, M2FPlan* pl) {
 int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const char* who) {
   const int nb = (int)a->nblocks, bs = (int)a->blksz;
   const int threads = 64 * (pl.nwc + kPollers);
-  const int U = bs;
   int G = pl.nrb, RB = 1;
   size_t lds = 0;
   for (int pass = 0; pass < 2; ++pass) {
     RB = (pl.nrb + G - 1) / G;
     G = (pl.nrb + RB - 1) / RB;
-    lds = sizeof(float) * (size_t)(8 * pl.hs + 12 * pl.zs + RB * 4 * U + 24 * U + 4);
+    lds = sizeof(float) * (size_t)(8 * pl.hs + 12 * pl.zs + RB * 4 * pl.ks + 8 * pl.gs + 4);
     if (lds > 65536)
       GS_CHECK_HIP(hipFuncSetAttribute((const void*)pl.fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     int gfit = 0;
@@ -687,6 +730,9 @@ int run_fused(const gs_args* a, const M2FPlan& pl, hipStream_t stream, const cha
   p.nwg = G * nb;
   p.nwc = pl.nwc;
   p.hs = pl.hs;
+  p.hpad = pl.hpad;
+  p.ks = pl.ks;
+  p.gs = pl.gs;
   p.zs = pl.zs;
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
