@@ -57,6 +57,7 @@ struct DParams {
   int ngroups, G, RB, nrb, Bp, nwg, P;
   int nwc;  // compute waves per workgroup
   int hsz;  // floats per LDS staging block (4 rows x 16 KC, interleaved)
+  int kr, gr;  // LDS row strides of the raw h (U units) and the staged gi (3 U), floats
   Quant qin, qout;
   int qin_after_first;
   float pscale, pbias;  // packed exchange: scale of the published levels, -128 pscale
@@ -69,6 +70,11 @@ struct DParams {
 // A poller decodes a word into the four consecutive staged slots of its units
 // with fma(byte, pscale, -128 pscale), bit for bit the producer's value (see
 // the two-factor Monarch kernel, which packs the same way).
+// Units per workgroup in dense remote mode (compute waves x 4).
+__host__ __device__ constexpr int dense_remote_units(int KC) { return 4 * (KC >= 16 ? 4 : 12); }
+// LDS row stride of a row of n floats that a wave reads as 4 rows x 4 units.
+__host__ __device__ constexpr int row_stride_pad(int n) { return n % 16 == 0 ? n + 4 : n; }
+
 template <int KIND, int KC, int NT, bool REMOTE, bool PACK = false>
 __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   extern __shared__ float lds[];
@@ -97,12 +103,18 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   const int nrbm = rb_end - rb_begin;
 
   float* hst = lds;                  // [2][hsz]     staged q_in(h) of the K range (il_index)
-  float* hk = hst + 2 * p.hsz;       // [RB][4][U]   raw h of this workgroup's units
-  float* gst = hk + p.RB * 4 * U;    // [2][4][3][U] staged gi (remote mode)
-  int* flags = reinterpret_cast<int*>(gst + 24 * U);  // remote mode: [0] compute-wave iterations
+  // The raw h and gi rows are read (and h written) by a wave as 4 rows x 4
+  // consecutive units: row strides that are not multiples of 16 floats put
+  // the four rows on different banks of each 32-lane pass. Dense remote mode
+  // has U = 4 nwc fixed by KC (16 or 48), so its strides are constants.
+  constexpr int UD = (KIND == kDense && REMOTE) ? dense_remote_units(KC) : 0;
+  const int KR = UD ? row_stride_pad(UD) : p.kr, GR = UD ? row_stride_pad(3 * UD) : p.gr;
+  float* hk = hst + 2 * p.hsz;       // [RB][4][KR]  raw h of this workgroup's units
+  float* gst = hk + p.RB * 4 * KR;   // [2][4][GR]   staged gi, [3][U] per row (remote mode)
+  int* flags = reinterpret_cast<int*>(gst + 8 * GR);  // remote mode: [0] compute-wave iterations
                                                       // published, [1] bit 0: group on one XCD,
                                                       // bit 1: a wait of this workgroup gave up
-  const int lds_floats = 2 * p.hsz + p.RB * 4 * U + (REMOTE ? 24 * U + 4 : 0);
+  const int lds_floats = 2 * p.hsz + p.RB * 4 * KR + (REMOTE ? 8 * GR + 4 : 0);
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
   const uint32_t base = REMOTE ? __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
@@ -128,14 +140,14 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       const int rbl = w / (4 * U), rem = w - rbl * 4 * U, r = rem / U, u = rem - r * U;
       const int row = 4 * (rb_begin + rbl) + r;
       const bool ok = row < p.B && (ulo + u - klo) < p.bs;
-      hk[w] = ok ? p.h0[(int64_t)row * p.sh0_b + ulo + u] : 0.0f;
+      hk[(rbl * 4 + r) * KR + u] = ok ? p.h0[(int64_t)row * p.sh0_b + ulo + u] : 0.0f;
     }
     if (REMOTE) {
       for (int w = threadIdx.x; w < 12 * U; w += blockDim.x) {
         const int r = w / (3 * U), rem = w - r * 3 * U, g = rem / U, u = rem - g * U;
         const int row = 4 * rb + r;
         const bool ok = row < p.B && (ulo + u - klo) < p.bs;
-        gst[w] = ok ? p.gi[(int64_t)row * p.sg_b + g * p.H + ulo + u] : 0.0f;
+        gst[r * GR + rem] = ok ? p.gi[(int64_t)row * p.sg_b + g * p.H + ulo + u] : 0.0f;
       }
     }
   }
@@ -164,7 +176,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       const bool mine = lead && row < p.B && unit_ok;
       float gir = 0.f, giz = 0.f, gin = 0.f;
       if (REMOTE) {
-        const float* gs_ = gst + buf * 12 * U + s * 3 * U + 4 * wave + j;
+        const float* gs_ = gst + buf * 4 * GR + s * GR + 4 * wave + j;
         gir = gs_[0];
         giz = gs_[U];
         gin = gs_[2 * U];
@@ -176,7 +188,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       }
       // gate-input parts of the exp2 arguments, off the step's dependent chain
       const float cr = __builtin_fmaf(kR, gir, bias[0]), cz = __builtin_fmaf(kR, giz, bias[1]), an2 = kN * gin;
-      float* hkp = hk + (rbl * 4 + s) * U + 4 * wave + j;
+      float* hkp = hk + (rbl * 4 + s) * KR + 4 * wave + j;
       const float hprev = *hkp;
       float a[3][KC];
       lds_a_il<KC>(hst + buf * p.hsz, lane, a[0]);
@@ -309,7 +321,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
             if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           }
         }
-        float* gs_ = gst + (nx & 1) * 12 * U + pr * 3 * U;
+        float* gs_ = gst + (nx & 1) * 4 * GR + pr * GR;
         if (part == 0) {
 #pragma unroll
           for (int i = 0; i < NGI; ++i) {
@@ -348,7 +360,7 @@ DFn pick(int kind, bool remote, int KC, int* nt, bool pack = false) {
 }
 
 struct DPlan {
-  int KC, nt, nwc, P, nrb, Bp, hsz, nb, bs, qpb;
+  int KC, nt, nwc, P, nrb, Bp, hsz, nb, bs, qpb, kr, gr;
   bool remote;
   bool pack;     // packed int8 exchange (dense remote mode)
   float pscale;  // its level scale
@@ -375,7 +387,7 @@ int plan_dense(int kind, const gs_args* a, DPlan* pl, const char* who) {
     pl->nwc = pl->qpb;
     pl->P = 1;
   } else {
-    const int nwmax = pl->KC >= 16 ? 4 : 12;
+    const int nwmax = dense_remote_units(pl->KC) / 4;
     int nwc = pl->qpb < nwmax ? pl->qpb : nwmax;
     if (kind == kMonarch1)
       while (pl->qpb % nwc != 0) --nwc;
@@ -391,6 +403,12 @@ int plan_dense(int kind, const gs_args* a, DPlan* pl, const char* who) {
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
   pl->hsz = 64 * pl->KC;
+  const int U = 4 * pl->nwc;
+  if (kind == kDense && pl->remote && U != dense_remote_units(pl->KC))
+    return set_error(GS_ERR_INVALID, "%s: dense remote plan has %d units per workgroup, kernel assumes %d", who, U,
+                     dense_remote_units(pl->KC));
+  pl->kr = row_stride_pad(U);
+  pl->gr = row_stride_pad(3 * U);
   // The pollers load 16 KC words per row from the row's first unit; the pad
   // keeps the reads past the last row inside the workspace.
   pl->xh_bytes = pl->remote ? align256(2 * (int64_t)pl->Bp * a->H * 8 + 16 * pl->KC * 8) : 0;
@@ -416,8 +434,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   for (int pass = 0; pass < 2; ++pass) {
     RB = (pl.nrb + G - 1) / G;
     G = (pl.nrb + RB - 1) / RB;
-    const int U = 4 * pl.nwc;
-    lds = sizeof(float) * (size_t)(2 * pl.hsz + RB * 4 * U + (pl.remote ? 24 * U + 4 : 0));
+    lds = sizeof(float) * (size_t)(2 * pl.hsz + RB * 4 * pl.kr + (pl.remote ? 8 * pl.gr + 4 : 0));
     if (lds > 65536)
       GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     if (!pl.remote) break;
@@ -458,6 +475,8 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.P = pl.P;
   p.nwc = pl.nwc;
   p.hsz = pl.hsz;
+  p.kr = pl.kr;
+  p.gr = pl.gr;
   p.qin = to_quant(a->q_in);
   p.qout = to_quant(a->q_out);
   p.qin_after_first = a->q_in.enabled && !same_quant(a->q_in, a->q_out);
