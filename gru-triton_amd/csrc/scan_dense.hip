@@ -167,9 +167,8 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
     // lane parts of the out / exchange-word offsets (row = 4 rb + s)
     const int64_t lane_out = (int64_t)s * p.so_b + unit;
     const int64_t lane_xh = (int64_t)s * p.H + unit;
-    for (int it = 0; it < niter; ++it) {
-      const int t = it / nrbm;
-      const int rbl = it - t * nrbm;
+    // (t, rbl) = divmod(it, nrbm), stepped rather than divided
+    for (int it = 0, t = 0, rbl = 0; it < niter; ++it, rbl = rbl + 1 == nrbm ? 0 : rbl + 1, t += rbl == 0) {
       const int rb = rb_begin + rbl;
       const int buf = it & 1;
       const int row = 4 * rb + s;

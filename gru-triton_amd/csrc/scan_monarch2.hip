@@ -219,9 +219,8 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
     const int a2off = j * ZS + sl * SP;           // phase-2 A: row j of z_g, slice sl
     float* zw = zst + sl * ZS + zpos;             // phase-1 result of this lane (gate g at + 4 g ZS)
 
-    for (int it = 0; it < niter; ++it) {
-      const int t = it / nrbm;
-      const int rbl = it - t * nrbm;
+    // (t, rbl) = divmod(it, nrbm), stepped rather than divided
+    for (int it = 0, t = 0, rbl = 0; it < niter; ++it, rbl = rbl + 1 == nrbm ? 0 : rbl + 1, t += rbl == 0) {
       const int rb = rb_begin + rbl;
       const int buf = it & 1;
       // phase 1: z_g entries of this wave's quads -> zst (y order)
@@ -250,6 +249,8 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       const float gir = gs_[0], giz = gs_[U], gin = gs_[2 * U];
       float* hkp = hk + (rbl * 4 + sl) * KS + iec;
       const float hprev = *hkp;
+      // keep these reads ahead of phase 2 (the scheduler would sink them below its MFMAs)
+      __builtin_amdgcn_sched_barrier(0);
       // after a give-up the workgroup's outputs are NaN and it publishes nothing more
       const int fl = __builtin_amdgcn_readfirstlane(flags[1]);
       // phase 2: L_g[b] times the staged z_g
