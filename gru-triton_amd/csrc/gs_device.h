@@ -279,15 +279,25 @@ __device__ __forceinline__ float sum_across_rows(float x) {
 // read it without synchronising.
 constexpr uint32_t kSpinLimit = 1u << 22;
 
+// One pointer addresses the workspace's control words (each on its own
+// 64-byte line), so a kernel holds two scalar registers for them rather than
+// eight: the persistent kernels run at the scalar-register limit, where every
+// register held across the step loop can push a spill into it.
 struct Ctrl {
-  uint32_t* fault;       // fval of the launch whose wait gave up (0: none yet)
-  uint32_t* exit_count;  // workgroups that have finished this launch
-  uint32_t* tag_base;    // tags of this launch are tag_base + t + 1
-  uint32_t* spin;        // poll bound override: 0 (a zeroed workspace) means kSpinLimit
-  uint32_t* mirror;      // host-visible copy of a raised fault word, or NULL
-  uint32_t fval;         // this launch's fault value, tag_base + 1 (set in the kernel)
-  uint32_t limit;        // this launch's poll bound (set in the kernel)
+  uint32_t* w;       // control words: ctrl_fault, ctrl_spin, ctrl_exit_count, ctrl_tag_base
+  uint32_t* mirror;  // host-visible copy of a raised fault word, or NULL
+  uint32_t fval;     // this launch's fault value, tag_base + 1 (set in the kernel)
+  uint32_t limit;    // this launch's poll bound (set in the kernel)
 };
+
+// fval of the launch whose wait gave up (0: none yet)
+__host__ __device__ __forceinline__ uint32_t* ctrl_fault(const Ctrl& c) { return c.w; }
+// poll bound override: 0 (a zeroed workspace) means kSpinLimit
+__host__ __device__ __forceinline__ uint32_t* ctrl_spin(const Ctrl& c) { return c.w + 16; }
+// workgroups that have finished this launch
+__host__ __device__ __forceinline__ uint32_t* ctrl_exit_count(const Ctrl& c) { return c.w + 32; }
+// tags of this launch are tag_base + t + 1
+__host__ __device__ __forceinline__ uint32_t* ctrl_tag_base(const Ctrl& c) { return c.w + 48; }
 
 // The kernel-side control block: the host's pointers plus this launch's fault
 // value and poll bound. The bound is kSpinLimit unless the host wrote an
@@ -296,17 +306,17 @@ struct Ctrl {
 __device__ __forceinline__ Ctrl launch_ctrl(const Ctrl& host, uint32_t base) {
   Ctrl c = host;
   c.fval = base + 1u;
-  const uint32_t o = __hip_atomic_load(host.spin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t o = __hip_atomic_load(ctrl_spin(host), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   c.limit = o != 0u ? o : kSpinLimit;
   return c;
 }
 
 __device__ __forceinline__ void raise_fault(const Ctrl& c) {
-  __hip_atomic_store(c.fault, c.fval, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(ctrl_fault(c), c.fval, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ bool fault_raised(const Ctrl& c) {
-  return __hip_atomic_load(c.fault, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c.fval;
+  return __hip_atomic_load(ctrl_fault(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == c.fval;
 }
 
 __device__ __forceinline__ uint64_t ld_tagged(const uint64_t* p) {
@@ -384,26 +394,39 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Waits (bounded) until the LDS counter reaches target; false if it gave up.
-__device__ __forceinline__ bool wait_lds_count(const Ctrl& c, const int* cnt, int target) {
+// A wait of this wave gave up: its workgroup is dead for the rest of the
+// launch. `dead` is the workgroup's LDS flag word (bit 1), which the compute
+// waves read every step and leave_grid reads at the end. Waits record this
+// themselves rather than returning a status, so a poller loop carries no
+// give-up state in registers: a loop-carried flag and the branches around
+// each wait cost the dense forward 5.5 us and its backward 20 us per launch.
+// A dead workgroup's later waits still run; with the fault word raised each
+// ends within 256 polls.
+__device__ __forceinline__ void mark_dead(int* dead) {
+  __hip_atomic_fetch_or(dead, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Waits (bounded) until the LDS counter reaches target; marks the workgroup
+// dead if it gave up.
+__device__ __forceinline__ void wait_lds_count(const Ctrl& c, const int* cnt, int target, int* dead) {
   uint32_t polls = 0;
   while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
     if (++polls > c.limit) {
       raise_fault(c);
-      return false;
+      mark_dead(dead);
+      return;
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  return true;
 }
 
 // Whether the n workgroups whose XCD words sit at words[0], words[stride], ...
 // all run on one XCD. Every workgroup stores its word (st_tagged of its
 // xcc_id with `tag`) at launch; one wave of each workgroup calls this and all
-// of them reach the same answer. n <= 64. `ok` turns false when the wait gave
-// up (the answer is then false).
+// of them reach the same answer. n <= 64. A wait that gives up marks the
+// workgroup dead (the answer is then false).
 __device__ __forceinline__ bool group_on_one_xcd(const Ctrl& c, const uint64_t* words, int stride, int n,
-                                                 uint32_t tag, bool& ok) {
+                                                 uint32_t tag, int* dead) {
   const int lane = threadIdx.x & 63;
   const bool mine = lane < n;
   const uint64_t* src = words + (int64_t)(mine ? lane : 0) * stride;
@@ -412,11 +435,11 @@ __device__ __forceinline__ bool group_on_one_xcd(const Ctrl& c, const uint64_t* 
   while (__ballot(mine && tag_of(v) != tag)) {
     if (++polls > c.limit) {
       raise_fault(c);
-      ok = false;
+      mark_dead(dead);
       return false;
     }
     if ((polls & 255u) == 0u && fault_raised(c)) {
-      ok = false;
+      mark_dead(dead);
       return false;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -442,12 +465,12 @@ __device__ __forceinline__ void leave_grid(const Ctrl& c, uint32_t nwg, uint32_t
   if (threadIdx.x == 0) {
     if (*dead_flag & dead_mask) raise_fault(c);
     const uint32_t prev =
-        __hip_atomic_fetch_add(c.exit_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(ctrl_exit_count(c), 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == nwg - 1u) {
       if (c.mirror != nullptr && fault_raised(c))
         __hip_atomic_store(c.mirror, c.fval, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-      __hip_atomic_store(c.tag_base, base + steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(c.exit_count, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctrl_tag_base(c), base + steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctrl_exit_count(c), 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }

@@ -42,8 +42,7 @@ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
 // Host half of the control block; the kernel adds its launch's fault value.
 inline Ctrl ctrl_of(void* ws, uint32_t* mirror) {
-  uint32_t* w = static_cast<uint32_t*>(ws);
-  return Ctrl{w, w + 32, w + 48, w + 16, mirror, 0u, 0u};
+  return Ctrl{static_cast<uint32_t*>(ws), mirror, 0u, 0u};
 }
 
 inline Quant to_quant(const gs_quant& q) {

@@ -103,11 +103,11 @@ __device__ __forceinline__ void lds_a_il(const float* blk, int lane, float (&a)[
 // step (the producer's next write to the same buffer half needs that step),
 // and unconditional loads measured faster than reloading only the stale words
 // under per-lane exec masks (one-way exchange latency of 512 words by one
-// wave: 575 ns against 693 ns). Returns the mask of valid m; `ok` turns false
-// when the wait gave up.
+// wave: 575 ns against 693 ns). Returns the mask of valid m; a wait that
+// gives up marks the workgroup dead (mark_dead).
 template <int MPR>
 __device__ __forceinline__ uint32_t poll_row_words(const Ctrl& c, const uint64_t* src, int klen, uint32_t tag,
-                                                   uint64_t (&v)[MPR], bool& ok) {
+                                                   uint64_t (&v)[MPR], int* dead) {
   static_assert(MPR <= 32, "poll mask is 32 bits");
   const int lane = threadIdx.x & 63;
   const uint64_t* s0 = src + lane;
@@ -123,11 +123,11 @@ __device__ __forceinline__ uint32_t poll_row_words(const Ctrl& c, const uint64_t
     if (pending == 0u) break;
     if (++polls > c.limit) {
       raise_fault(c);
-      ok = false;
+      mark_dead(dead);
       break;
     }
     if ((polls & 255u) == 0u && fault_raised(c)) {
-      ok = false;
+      mark_dead(dead);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -142,11 +142,11 @@ __device__ __forceinline__ uint32_t poll_row_words(const Ctrl& c, const uint64_t
 // block's slots when k0 is a multiple of 128) or at dst[k] (row-major), with
 // the loads, waits and bounds of poll_row_words. (The wait loop is written out
 // here rather than shared: the forward kernels' code around this inlined loop
-// is tuned, and the shared form schedules differently.) `ok` turns false when
-// the wait gave up.
+// is tuned, and the shared form schedules differently.) A wait that gives up
+// marks the workgroup dead (mark_dead).
 template <int MPR, bool IL = true>
 __device__ __forceinline__ void poll_row_il(const Ctrl& c, const uint64_t* src, float* dst, int r, int klen,
-                                            uint32_t tag, bool& ok) {
+                                            uint32_t tag, int* dead) {
   static_assert(MPR <= 32, "poll mask is 32 bits");
   const int lane = threadIdx.x & 63;
   const uint64_t* s0 = src + lane;
@@ -163,11 +163,11 @@ __device__ __forceinline__ void poll_row_il(const Ctrl& c, const uint64_t* src, 
     if (pending == 0u) break;
     if (++polls > c.limit) {
       raise_fault(c);
-      ok = false;
+      mark_dead(dead);
       break;
     }
     if ((polls & 255u) == 0u && fault_raised(c)) {
-      ok = false;
+      mark_dead(dead);
       break;
     }
     __builtin_amdgcn_s_sleep(1);

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   const int lds_floats = 2 * p.hsz + p.RB * 4 * KR + (REMOTE ? 8 * GR + 4 : 0);
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
-  const uint32_t base = REMOTE ? __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
+  const uint32_t base = REMOTE ? __hip_atomic_load(ctrl_tag_base(p.ctrl), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0u;
   const Ctrl ctrl = launch_ctrl(p.ctrl, base);
   if (REMOTE && threadIdx.x == 0) st_tagged(p.xw + blockIdx.x, __uint_as_float(xcc_id()), base + 1u);
   const int niter = p.T * nrbm;
@@ -259,7 +259,6 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
     const int pq = wave - nwc;
     const int pr = pq / NPR, part = pq - pr * NPR;
     constexpr int NGI = NT / 64 > 4 * NPR ? (3 * 4 * (NT / 64 - 4 * NPR) + 63) / 64 : 1;  // gi words per lane
-    bool alive = true;  // no wait of this wave has given up
     for (int it = 0; it < niter; ++it) {
       const int nx = it + 1;
       if (nx < niter) {
@@ -285,11 +284,11 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
             hs[il_index(pr, k)] = v;
           }
         } else {
-          if (alive) {
+          {
             if (pq == 0 && nx == nrbm &&  // first exchange of the launch
-                p.P <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, p.P, base + 1u, alive))
+                p.P <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, p.P, base + 1u, &flags[1]))
               __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
+            wait_lds_count(ctrl, &flags[0], nwc * (it + 1), &flags[1]);
             // this wave's share of row pr's bs words: k in [part KW, part KW + KW)
             // (part KW is a multiple of 128, so the staged slots are those of il_index)
             constexpr int KW = 16 * KC / NPR;
@@ -300,7 +299,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
               const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * nw + w0;
               uint64_t v[PMW];
               uint32_t valid = 0;
-              if (alive && w0 < nw) valid = poll_row_words<PMW>(ctrl, hb, min(KW / 4, nw - w0), base + (uint32_t)t2, v, alive);
+              if (w0 < nw) valid = poll_row_words<PMW>(ctrl, hb, min(KW / 4, nw - w0), base + (uint32_t)t2, v, &flags[1]);
 #pragma unroll
               for (int m = 0; m < PMW; ++m) {
                 if ((valid >> m) & 1u) {
@@ -313,11 +312,10 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
               }
             } else {
               const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * p.H + klo;
-              if (alive && part * KW < p.bs)
+              if (part * KW < p.bs)
                 poll_row_il<KC / 4 / NPR>(ctrl, hb + part * KW, hs + 4 * part * KW, pr, min(KW, p.bs - part * KW),
-                                          base + (uint32_t)t2, alive);
+                                          base + (uint32_t)t2, &flags[1]);
             }
-            if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           }
         }
         float* gs_ = gst + (nx & 1) * 4 * GR + pr * GR;

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
   const int lds_floats = 6 * p.hsz + 8 * kNV * U + p.RB * 4 * U + 4;
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
-  const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t base = __hip_atomic_load(ctrl_tag_base(p.ctrl), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const Ctrl ctrl = launch_ctrl(p.ctrl, base);
   if (threadIdx.x == 0) st_tagged(p.xw + blockIdx.x, __uint_as_float(xcc_id()), base + 1u);
   const int niter = T * nrbm;
@@ -266,7 +266,6 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
     const int pr = wave - nwc;
     constexpr int NWC_MAX = NT / 64 - kPollers;
     constexpr int NSV = (kNV * 4 * NWC_MAX + 63) / 64;  // staged values per lane
-    bool alive = true;  // no wait of this wave has given up
     for (int it = 0; it < niter; ++it) {
       const int nx = it + 1;
       if (nx < niter) {
@@ -292,16 +291,13 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
 #pragma unroll
             for (int g = 0; g < 3; ++g) cf[g][m] = ok ? crow[g * H + 64 * m] : 0.0f;
           }
-          if (alive && pr == 0 && nx == nrbm &&  // first exchange of the launch
-              p.P <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, p.P, base + 1u, alive))
+          if (pr == 0 && nx == nrbm &&  // first exchange of the launch
+              p.P <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, p.P, base + 1u, &flags[1]))
             __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
+          wait_lds_count(ctrl, &flags[0], nwc * (it + 1), &flags[1]);
           uint64_t v[MPR];
-          uint32_t valid = 0;
-          if (alive)
-            valid = poll_row_words<MPR>(ctrl, p.xh + ((int64_t)((st2 - 1) & 1) * p.Bp + row) * H, H,
-                                        base + (uint32_t)st2, v, alive);
-          if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          const uint32_t valid = poll_row_words<MPR>(ctrl, p.xh + ((int64_t)((st2 - 1) & 1) * p.Bp + row) * H, H,
+                                                     base + (uint32_t)st2, v, &flags[1]);
           float* hs = hst + (nx & 1) * 3 * p.hsz;
           static_for<0, MPR>([&](auto I) {
             if ((valid >> I) & 1u) {

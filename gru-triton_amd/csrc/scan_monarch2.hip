@@ -140,7 +140,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
   const int lds_floats = 8 * HS + 12 * ZS + p.RB * 4 * KS + 8 * GS + 4;
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
-  const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t base = __hip_atomic_load(ctrl_tag_base(p.ctrl), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const Ctrl ctrl = launch_ctrl(p.ctrl, base);
   if (threadIdx.x == 0) st_tagged(p.xw + blockIdx.x, __uint_as_float(xcc_id()), base + 1u);
   const int niter = p.T * nrbm;
@@ -340,7 +340,6 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       for (int e = 0; e < 4; ++e) un[m][e] = PM > 0 && w < nwrow ? hx(m2_unit(bw * bs + 4 * qw + e, nb, bs)) : 0;
     }
     constexpr int NGI = (3 * 64 + 63) / 64;  // 3 U <= 192 gate inputs per row
-    bool alive = true;  // no wait of this wave has given up
     for (int it = 0; it < niter; ++it) {
       const int nx = it + 1;
       const bool more = nx < niter;
@@ -368,10 +367,10 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
             hs[hx(k)] = v;
           }
         } else {
-          if (alive && pq == 0 && nx == nrbm &&  // first exchange of the launch
-              nb <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, nb, base + 1u, alive))
+          if (pq == 0 && nx == nrbm &&  // first exchange of the launch
+              nb <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, nb, base + 1u, &flags[1]))
             __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          if (alive) alive = wait_lds_count(ctrl, &flags[0], nwc * (it + 1));
+          wait_lds_count(ctrl, &flags[0], nwc * (it + 1), &flags[1]);
           const uint32_t tag = base + (uint32_t)t2;
           if constexpr (PM > 0) {
             // this wave's PM words per lane of row pr's H / 4 packed words
@@ -379,7 +378,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
             const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * nwrow + w0;
             uint64_t v[PMX];
             uint32_t valid = 0;
-            if (alive && w0 < nwrow) valid = poll_row_words<PMX>(ctrl, hb, nwrow - w0, tag, v, alive);
+            if (w0 < nwrow) valid = poll_row_words<PMX>(ctrl, hb, nwrow - w0, tag, v, &flags[1]);
 #pragma unroll
             for (int m = 0; m < PMX; ++m) {
               if ((valid >> m) & 1u) {
@@ -393,10 +392,9 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
             const uint64_t* hb = p.xh + ((int64_t)((t2 - 1) & 1) * p.Bp + row) * H;
             // this wave's half of row pr's H words, in chunks of 256
             const int kend = part ? H : min(H, kh);
-            for (int k0 = part * kh; k0 < kend && alive; k0 += 256)
-              poll_row_il<4, false>(ctrl, hb + k0, hs + hx(k0), pr, min(256, kend - k0), tag, alive);
+            for (int k0 = part * kh; k0 < kend; k0 += 256)
+              poll_row_il<4, false>(ctrl, hb + k0, hs + hx(k0), pr, min(256, kend - k0), tag, &flags[1]);
           }
-          if (!alive) __hip_atomic_fetch_or(&flags[1], 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
         float* gs_ = gst + (nx & 1) * 4 * GS + pr * GS;
         if (part == 0) {
@@ -491,7 +489,7 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
 #pragma unroll
   for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? gate_scale(g) * p.bh[g * p.H + unit] : 0.0f;  // for gru_update_gb
 
-  const uint32_t base = __hip_atomic_load(p.ctrl.tag_base, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t base = __hip_atomic_load(ctrl_tag_base(p.ctrl), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const Ctrl ctrl = launch_ctrl(p.ctrl, base);
   bool alive = true;  // no wait of this thread has given up
   const int rb_begin = gid * p.RB;
