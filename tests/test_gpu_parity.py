@@ -124,10 +124,12 @@ def test_monarch_single_fp32(dev, shape, nb):
 # Fused kernel (bs <= 64, nb | bs, bs / nb a multiple of 4): (6, 5, 64) nb 4,
 # (7, 9, 128) nb 4, (3, 2, 96) nb 2 (12 compute waves), (5, 6, 256) nb 4 (two
 # quads per wave), (3, 5, 1024) nb 16 (rows polled in two chunks), (4, 33, 512)
-# nb 8 (ragged batch). Split kernel: the rest.
+# nb 8 (ragged batch), (4, 3, 48) nb 2 (bs 24: K chain of 32 with the last 8
+# masked). bs 32 and 64 stage z with swapped quad chunks (qpa 1, 2 and 4 here).
+# Split kernel: the rest.
 @pytest.mark.parametrize("shape,nb", [((5, 3, 32), 8), ((6, 5, 64), 4), ((4, 4, 256), 2), ((6, 3, 30), 5),
                                       ((7, 9, 128), 4), ((3, 2, 96), 2), ((5, 6, 256), 4), ((3, 5, 1024), 16),
-                                      ((4, 33, 512), 8)])
+                                      ((4, 33, 512), 8), ((4, 3, 48), 2)])
 def test_monarch_two_factor_fp32(dev, shape, nb):
     assert_fp32_parity(_monarch(shape, nb, two=True), dev)
 
