@@ -37,7 +37,9 @@
 namespace gs {
 namespace {
 
-constexpr int kPollers = 4;
+// Poller waves per batch row of the recurrence: two at KC 16 and 32 (each
+// polls half of the row's D words), one otherwise.
+__host__ __device__ constexpr int bwd_pollers_per_row(int KC) { return KC == 16 || KC == 32 ? 2 : 1; }
 // Per-unit values staged for the iteration that consumes D_t: 0 Zm_t, 1 Mi_t, 2 dout[t-1]
 constexpr int kNV = 3;
 
@@ -141,7 +143,6 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
   const int j = lane & 3, kb4 = lane >> 2, s = (lane >> 2) & 3;
   const bool lead = lane < 16;
   const int H = p.H, T = p.T;
-  constexpr int MPR = KC / 4;  // polled words per lane per row
 
   const int gid = blockIdx.x % p.ngroups;
   const int pw = blockIdx.x / p.ngroups;
@@ -263,9 +264,15 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
     // loaded first (their latency overlaps the poll), then D_t is polled once
     // this workgroup's compute waves have published iteration it, and dgh_t
     // = D_t (Cr, Cz, Chn) goes to LDS.
-    const int pr = wave - nwc;
-    constexpr int NWC_MAX = NT / 64 - kPollers;
-    constexpr int NSV = (kNV * 4 * NWC_MAX + 63) / 64;  // staged values per lane
+    constexpr int NPR = bwd_pollers_per_row(KC);
+    static_assert(NT / 64 >= 4 * NPR + 1, "launch bounds hold the poller waves");
+    const int pq = wave - nwc;
+    const int pr = pq / NPR, part = pq - pr * NPR;
+    constexpr int KW = 16 * KC / NPR;  // this wave's share of a row's words: k in [part KW, part KW + KW)
+    constexpr int MPW = KW / 64;       // polled words per lane
+    const int k0 = part * KW;
+    constexpr int NWC_MAX = NT / 64 - 4 * NPR;
+    constexpr int NSV = (kNV * 4 * NWC_MAX + 63) / 64;  // staged values per lane (part 0)
     for (int it = 0; it < niter; ++it) {
       const int nx = it + 1;
       if (nx < niter) {
@@ -278,31 +285,33 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
         for (int i = 0; i < NSV; ++i) {
           const int w = lane + 64 * i;
           const int v = w / U, u = w - v * U;
-          sv[i] = (w < kNV * U && row < p.B && ulo + u < H) ? step_value(t2, row, ulo + u, v) : 0.0f;
+          sv[i] = (part == 0 && w < kNV * U && row < p.B && ulo + u < H) ? step_value(t2, row, ulo + u, v) : 0.0f;
         }
         if (st2 == 0) {
-          for (int k = lane; k < H; k += 64) stage_first(nx, pr, k);
+          for (int k = k0 + lane; k < min(H, k0 + KW); k += 64) stage_first(nx, pr, k);
         } else if (row < p.B) {
-          const float* crow = p.cg + ((int64_t)t2 * p.B + row) * 3 * H + lane;
-          float cf[3][MPR];
+          const float* crow = p.cg + ((int64_t)t2 * p.B + row) * 3 * H + k0 + lane;
+          float cf[3][MPW];
 #pragma unroll
-          for (int m = 0; m < MPR; ++m) {
-            const bool ok = lane + 64 * m < H;
+          for (int m = 0; m < MPW; ++m) {
+            const bool ok = k0 + lane + 64 * m < H;
 #pragma unroll
             for (int g = 0; g < 3; ++g) cf[g][m] = ok ? crow[g * H + 64 * m] : 0.0f;
           }
-          if (pr == 0 && nx == nrbm &&  // first exchange of the launch
+          if (pq == 0 && nx == nrbm &&  // first exchange of the launch
               p.P <= 64 && group_on_one_xcd(ctrl, p.xw + gid, p.ngroups, p.P, base + 1u, &flags[1]))
             __hip_atomic_fetch_or(&flags[1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
           wait_lds_count(ctrl, &flags[0], nwc * (it + 1), &flags[1]);
-          uint64_t v[MPR];
-          const uint32_t valid = poll_row_words<MPR>(ctrl, p.xh + ((int64_t)((st2 - 1) & 1) * p.Bp + row) * H, H,
-                                                     base + (uint32_t)st2, v, &flags[1]);
+          uint64_t v[MPW];
+          uint32_t valid = 0;
+          if (k0 < H)
+            valid = poll_row_words<MPW>(ctrl, p.xh + ((int64_t)((st2 - 1) & 1) * p.Bp + row) * H + k0, H - k0,
+                                        base + (uint32_t)st2, v, &flags[1]);
           float* hs = hst + (nx & 1) * 3 * p.hsz;
-          static_for<0, MPR>([&](auto I) {
+          static_for<0, MPW>([&](auto I) {
             if ((valid >> I) & 1u) {
               const float D = value_of(v[I]);
-              const int li = il_index(pr, lane + 64 * I);
+              const int li = il_index(pr, k0 + lane + 64 * I);
               hs[li] = D * cf[0][I];
               hs[p.hsz + li] = D * cf[1][I];
               hs[2 * p.hsz + li] = D * cf[2][I];
@@ -310,10 +319,12 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
           });
         }
         float* sd = sti + ((nx & 1) * 4 + pr) * kNV * U;
+        if (part == 0) {
 #pragma unroll
-        for (int i = 0; i < NSV; ++i) {
-          const int w = lane + 64 * i;
-          if (w < kNV * U) sd[w] = sv[i];
+          for (int i = 0; i < NSV; ++i) {
+            const int w = lane + 64 * i;
+            if (w < kNV * U) sd[w] = sv[i];
+          }
         }
       }
       lds_barrier();
@@ -328,8 +339,8 @@ BFn pick_bwd(int KC, int* nt) {
   switch (KC) {
     case 4: *nt = 1024; return dense_bwd_kernel<4, 1024>;
     case 8: *nt = 1024; return dense_bwd_kernel<8, 1024>;
-    case 16: *nt = 512; return dense_bwd_kernel<16, 512>;
-    case 32: *nt = 512; return dense_bwd_kernel<32, 512>;
+    case 16: *nt = 768; return dense_bwd_kernel<16, 768>;
+    case 32: *nt = 768; return dense_bwd_kernel<32, 768>;
     case 64: *nt = 512; return dense_bwd_kernel<64, 512>;
     default: return nullptr;
   }
@@ -485,7 +496,7 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   // 3. the recurrence
   int nt = 0;
   BFn fn = pick_bwd(pl.KC, &nt);
-  const int threads = 64 * (pl.nwc + kPollers);
+  const int threads = 64 * (pl.nwc + 4 * bwd_pollers_per_row(pl.KC));
   int G = pl.nrb, RB = 1;
   size_t lds = 0;
   for (int pass = 0; pass < 2; ++pass) {
