@@ -12,16 +12,20 @@
 // loads are in flight while the current one feeds the MFMAs. Global loads are
 // float4 along each operand's contiguous dimension when the shapes allow it
 // (scalar otherwise), and land in LDS without transposition:
-//   k-contiguous operand: S[row][k], row stride 36;
-//   row-contiguous operand: S[k][row], row stride 80.
-// When both operands are k-contiguous (NT), the 16 lanes of k-group q read
-// k = 8 q + s (s < 8) of their row as two float4 (36 = 4 mod 64 x 9 puts the
-// 16 rows x 4 words in distinct banks). Otherwise MFMA s reads k = q + 4 s
-// as single words: from S[k][row] the four k-groups sit 80 = 16 mod 64 words
-// apart, and from S[row][k] the 16 rows x 4 k-groups land on 36 r + q, all
-// distinct mod 64; either way the 64 lanes hit 64 banks. Any bijection
-// between (MFMA step, k-group) and k is valid as long as A and B use the same
-// one.
+//   k-contiguous operand: S[row][k], row stride 40;
+//   row-contiguous operand: S[k][row], row stride 68 (NN) or 80 (TN).
+// A k-contiguous operand is read as float4s: lane (row r, k-group q) reads
+// k = 4 q and 4 q + 16, and MFMA s takes k = 4 q + 16 (s / 4) + s % 4.
+// gfx950 serves a 16-byte LDS read in 16-lane passes that pair 8-lane groups
+// {0, 3}, {1, 2}, {4, 7}, {5, 6}, i.e. rows r < 8 of one k-group with rows
+// r >= 8 of the next; with stride 40 (10 four-bank groups) every row starts on
+// an even group and the two k-groups of a pass sit one group apart, so a pass
+// covers all 64 banks (the earlier k = 8 q + s with stride 36 put two lanes of
+// every pass on one bank). A row-contiguous operand is read as single words
+// (32 banks, 32-lane passes covering k-groups q and q + 1): under the NN
+// mapping those rows are 4 k apart, 4 x 68 = 16 mod 32 words; under TN's
+// k = q + 4 s they are 1 k apart, 80 = 16 mod 32. Any bijection between (MFMA
+// step, k-group) and k is valid as long as A and B use the same one.
 //
 // MFMA operand layout (16x16x4 f32): lane l supplies A[i = l % 16][k-group
 // l / 16] and B[k-group l / 16][j = l % 16]; D VGPR v of lane l is
@@ -33,15 +37,16 @@ namespace gs {
 namespace {
 
 constexpr int BM = 64, BN = 64, BK = 32, kGemmThreads = 256;
-constexpr int kNTStride = BK + 4;  // NT: floats per LDS row (one row of the tile, 32 k)
-constexpr int kTNStride = 64 + 16; // TN: floats per LDS row (one k, 64 rows of the tile)
-constexpr int kStageFloats = (BM * kNTStride > BK * kTNStride) ? BM * kNTStride : BK * kTNStride;
+constexpr int kKStride = BK + 8;  // floats per LDS row of a k-contiguous operand (one row of the tile, 32 k)
+// floats per LDS row of a row-contiguous operand (one k, 64 rows of the tile)
+constexpr int kRStrideNN = 64 + 4, kRStrideTN = 64 + 16;
+constexpr int kStageFloats = (BM * kKStride > BK * kRStrideTN) ? BM * kKStride : BK * kRStrideTN;
 
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 // Loads of one operand tile (64 rows of the output dimension x 32 k) into
 // registers, then into LDS. KC: the operand is contiguous along k.
-template <bool KC, bool VEC, bool QUANT>
+template <bool KC, bool VEC, bool QUANT, int RS>
 struct TileLoader {
   // VEC: 2 float4 per thread; scalar: 8 floats per thread.
   static constexpr int N = VEC ? 2 : 8;
@@ -118,9 +123,9 @@ struct TileLoader {
         const int idx = tid + kGemmThreads * e;
         float* d;
         if constexpr (KC)
-          d = s + (idx >> 3) * kNTStride + (idx & 7) * 4;
+          d = s + (idx >> 3) * kKStride + (idx & 7) * 4;
         else
-          d = s + (idx >> 4) * kTNStride + (idx & 15) * 4;
+          d = s + (idx >> 4) * RS + (idx & 15) * 4;
         *reinterpret_cast<f4v*>(d) = f4v{r[4 * e], r[4 * e + 1], r[4 * e + 2], r[4 * e + 3]};
       }
     } else {
@@ -128,9 +133,9 @@ struct TileLoader {
       for (int e = 0; e < 8; ++e) {
         const int idx = tid + kGemmThreads * e;
         if constexpr (KC)
-          s[(idx >> 5) * kNTStride + (idx & 31)] = r[e];
+          s[(idx >> 5) * kKStride + (idx & 31)] = r[e];
         else
-          s[(idx >> 6) * kTNStride + (idx & 63)] = r[e];
+          s[(idx >> 6) * RS + (idx & 63)] = r[e];
       }
     }
   }
@@ -150,8 +155,9 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
   const int kbeg = split * kper;
   const int kend = min(g.K, kbeg + kper);
 
-  TileLoader<A_KC, VEC_A, QA> la;
-  TileLoader<B_KC, VEC_B, QB> lb;
+  constexpr int RS = LAYOUT == kGemmNN ? kRStrideNN : kRStrideTN;
+  TileLoader<A_KC, VEC_A, QA, RS> la;
+  TileLoader<B_KC, VEC_B, QB, RS> lb;
   la.init(g.a + (int64_t)(z % g.a_mod) * g.a_bs, g.lda, i0, g.M, kend);
   lb.init(g.b + (int64_t)(z % g.b_mod) * g.b_bs, g.ldb, j0, g.N, kend);
   la.q = g.qa;
@@ -181,14 +187,14 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     const float* as = As[buf];
     const float* bs = Bs[buf];
     if constexpr (A_KC && B_KC) {
-      // lane: rows 32 wy + 16 ti + r16 (A) and 32 wx + 16 tj + r16 (B), k = 8 kq + s
+      // lane: rows 32 wy + 16 ti + r16 (A) and 32 wx + 16 tj + r16 (B), k = 4 kq + 16 h + e
       f4v a[2][2], b[2][2];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          a[t][h] = *reinterpret_cast<const f4v*>(as + (32 * wy + 16 * t + r16) * kNTStride + 8 * kq + 4 * h);
-          b[t][h] = *reinterpret_cast<const f4v*>(bs + (32 * wx + 16 * t + r16) * kNTStride + 8 * kq + 4 * h);
+          a[t][h] = *reinterpret_cast<const f4v*>(as + (32 * wy + 16 * t + r16) * kKStride + 4 * kq + 16 * h);
+          b[t][h] = *reinterpret_cast<const f4v*>(bs + (32 * wx + 16 * t + r16) * kKStride + 4 * kq + 16 * h);
         }
 #pragma unroll
       for (int s = 0; s < 8; ++s)
@@ -198,21 +204,31 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
           for (int tj = 0; tj < 2; ++tj)
             acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti][s >> 2][s & 3], b[tj][s >> 2][s & 3],
                                                                acc[ti][tj], 0, 0, 0);
-    } else {
-      // k = kq + 4 s
+    } else if constexpr (A_KC) {
+      // NN: A as float4s (as NT), B single words of row k = 4 kq + 16 (s / 4) + s % 4
+      f4v a[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          a[t][h] = *reinterpret_cast<const f4v*>(as + (32 * wy + 16 * t + r16) * kKStride + 4 * kq + 16 * h);
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        float a0, a1;
-        if constexpr (A_KC) {
-          const float* ar = as + (32 * wy + r16) * kNTStride + kq + 4 * s;
-          a0 = ar[0];
-          a1 = ar[16 * kNTStride];
-        } else {
-          const float* ar = as + (kq + 4 * s) * kTNStride + 32 * wy + r16;
-          a0 = ar[0];
-          a1 = ar[16];
+        const float* br = bs + (4 * kq + 16 * (s >> 2) + (s & 3)) * RS + 32 * wx + r16;
+        const float b0 = br[0], b1 = br[16];
+#pragma unroll
+        for (int ti = 0; ti < 2; ++ti) {
+          acc[ti][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti][s >> 2][s & 3], b0, acc[ti][0], 0, 0, 0);
+          acc[ti][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti][s >> 2][s & 3], b1, acc[ti][1], 0, 0, 0);
         }
-        const float* br = bs + (kq + 4 * s) * kTNStride + 32 * wx + r16;
+      }
+    } else {
+      // TN: k = kq + 4 s
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float* ar = as + (kq + 4 * s) * RS + 32 * wy + r16;
+        const float a0 = ar[0], a1 = ar[16];
+        const float* br = bs + (kq + 4 * s) * RS + 32 * wx + r16;
         const float b0 = br[0], b1 = br[16];
         acc[0][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b0, acc[0][0], 0, 0, 0);
         acc[0][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b1, acc[0][1], 0, 0, 0);

@@ -494,17 +494,25 @@ def _out_quant(y: torch.Tensor, oq, ste: bool) -> torch.Tensor:
 
 def structured_input_projection(x: torch.Tensor, kind: str, w: torch.Tensor, b: Optional[torch.Tensor],
                                 x_quant: QuantTuple = None, out_quant=(None, None, None),
-                                ste: bool = False) -> torch.Tensor:
+                                ste: bool = False, y_value: Optional[torch.Tensor] = None) -> torch.Tensor:
     """gi [..., 3H] of a structured input side (gru_cell.py:466-503): q_x over
     the whole sequence, each gate's map (the hidden-side map of ``kind`` with
     weights w, input size = H), the gate's output quantizer (_out_quant), its
-    bias, concatenation r, z, n."""
+    bias, concatenation r, z, n.
+
+    ``y_value`` (optional, [N, 3H]) replaces the maps' output values while
+    keeping their gradient: the output quantizers then see exactly the values
+    a kernel under test produced (teacher forcing), so a backward can be
+    checked without the rounding-boundary flips that a different summation
+    order causes in the forward."""
     H = x.shape[-1]
     lead = x.shape[:-1]
     x2 = x.reshape(-1, H)
     xq = (fake_quant_ste(x2, x_quant) if ste else fake_quant(x2, x_quant)) if x_quant is not None else x2
     cfg = {"kind": kind, "w": w, "h0": torch.zeros(1, H, dtype=x.dtype), "gi": torch.zeros(1, 1, 3 * H, dtype=x.dtype)}
     y = gh_map_nobias(cfg)(xq, w)
+    if y_value is not None:
+        y = y + (y_value.reshape(y.shape).to(y.dtype) - y).detach()
     parts = []
     for g in range(3):
         o = _out_quant(y[:, g * H:(g + 1) * H], out_quant[g], ste)

@@ -5,8 +5,11 @@ where an output quantizer's pre-quant value lies within 1e-4 of a rounding
 boundary (in code units) a one-step difference is allowed. Backward: dx,
 dWi_struct and dbi within 1e-4 * max(1, max|oracle|) of torch's autograd
 through the oracle's restatement of the reference quantizers (STE, clipped STE,
-and the dynamic per-row scale's own gradient path). End to end: layer_forward
-with a structured input side against the oracle's projection and scan.
+and the dynamic per-row scale's own gradient path), teacher-forced: the oracle's
+output quantizers see the kernel's own pre-quant values (the same call with the
+output quantizers off), so a forward boundary flip (allowed above) does not
+move the gradient it is compared with. End to end: layer_forward with a
+structured input side against the oracle's projection and scan.
 """
 
 from __future__ import annotations
@@ -106,8 +109,12 @@ def test_struct_input_projection_forward_and_gradients(dev, kind, H, kw, qname, 
     _check_forward(kind, x, W, b, x_quant, out_quant, gi.detach().cpu())
     dgi = torch.randn(gi.shape, generator=gen)
     (gi * dgi.to(dev)).sum().backward()
+    with torch.no_grad():
+        y_kernel = G.structured_input_projection(x.to(dev), kind, W.to(dev), None, x_quant=x_quant,
+                                                 out_quant=(None, None, None)).cpu()
     xr, Wr, br = (t.clone().requires_grad_(True) for t in (x, W, b))
-    ref = O.structured_input_projection(xr, kind, Wr, br, x_quant=x_quant, out_quant=out_quant, ste=True)
+    ref = O.structured_input_projection(xr, kind, Wr, br, x_quant=x_quant, out_quant=out_quant, ste=True,
+                                        y_value=y_kernel.reshape(-1, 3 * H))
     (ref * dgi).sum().backward()
     for name, got, want in (("dx", xd.grad, xr.grad), ("dW", Wd.grad, Wr.grad), ("db", bd.grad, br.grad)):
         err = (got.cpu() - want).abs().max().item()
