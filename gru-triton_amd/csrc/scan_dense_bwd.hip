@@ -69,10 +69,13 @@ __global__ void coef_kernel(const float* gi, int64_t sg_t, int64_t sg_b, const f
 }
 
 // dgi, dgh_n and per-row partial dbh sums over chunks of kGradSteps steps:
-// thread (chunk, b, k) walks the chunk's steps t.
+// thread (chunk, b, k) walks the chunk's steps t. Optional outputs (NULL: not
+// written): dghn [T B, H], and dgh [T B, 3H] = (dg_r, dg_z, dgh_n), the A
+// operand of the one dWh product; dgh may be cg itself, since each thread
+// reads its three coefficients before it writes the same three positions.
 constexpr int kGradSteps = 8;
 __global__ void grad_kernel(const float* dsum, const float* cg, const float* cgn, float* dgi, float* dghn,
-                            float* dbh_chunks, int T, int B, int H) {
+                            float* dgh, float* dbh_chunks, int T, int B, int H) {
   const int64_t per_chunk = (int64_t)B * H;
   const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int nchunks = (T + kGradSteps - 1) / kGradSteps;
@@ -91,7 +94,13 @@ __global__ void grad_kernel(const float* dsum, const float* cg, const float* cgn
     d[0] = gr;
     d[H] = gz;
     d[2 * H] = D * cgn[m * H + k];
-    dghn[m * H + k] = ghn;
+    if (dghn != nullptr) dghn[m * H + k] = ghn;
+    if (dgh != nullptr) {
+      float* o = dgh + m * 3 * H + k;
+      o[0] = gr;
+      o[H] = gz;
+      o[2 * H] = ghn;
+    }
     sr += gr;
     sz += gz;
     sn += ghn;
@@ -348,13 +357,13 @@ BFn pick_bwd(int KC, int* nt) {
 
 // Workspace (tagged words only): control words | xh [2][Bp][H] tagged D |
 // xw [nrb P]. Scratch (plain floats), each region 256-byte aligned:
-// cg [T B, 3H] | hq, cgn, zm, mi, dsum, dghn [T B, H] each |
+// cg [T B, 3H] | hq, cgn, zm, mi, dsum [T B, H] each |
 // dbh chunks [nchunks][B][3H] | dWh split partials.
 struct BPlan {
   int KC, nt, nwc, P, nrb, Bp, hsz, split, nchunks;
   int64_t xh_bytes, xw_bytes, cg_bytes, plane_bytes, chunk_bytes, part_bytes;
   int64_t total() const { return kCtrlBytes + xh_bytes + xw_bytes; }
-  int64_t scratch() const { return cg_bytes + 6 * plane_bytes + chunk_bytes + part_bytes; }
+  int64_t scratch() const { return cg_bytes + 5 * plane_bytes + chunk_bytes + part_bytes; }
 };
 
 int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
@@ -404,7 +413,7 @@ int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const 
   const int nch = grad_chunks(T);
   const int64_t n = (int64_t)nch * B * H;
   hipLaunchKernelGGL(grad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, dsum, cg, cgn, a->dgi,
-                     dghn, chunks, T, B, H);
+                     dghn, nullptr, chunks, T, B, H);
   GS_CHECK_HIP(hipGetLastError());
   return sum_partials(a->dbh_part, chunks, (int64_t)B * 3 * H, nch, (int64_t)B * 3 * H, stream, who);
 }
@@ -459,7 +468,6 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   float* zm = reinterpret_cast<float*>(take(pl.plane_bytes));
   float* mi = reinterpret_cast<float*>(take(pl.plane_bytes));
   float* dsum = reinterpret_cast<float*>(take(pl.plane_bytes));
-  float* dghn = reinterpret_cast<float*>(take(pl.plane_bytes));
   float* chunks = reinterpret_cast<float*>(take(pl.chunk_bytes));
   float* part = reinterpret_cast<float*>(take(pl.part_bytes));
   const Quant qin = to_quant(a->q_in), qout = to_quant(a->q_out);
@@ -537,20 +545,19 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), lds, stream, p);
   GS_CHECK_HIP(hipGetLastError());
 
-  // 4. dgi, dgh_n, per-row dbh
+  // 4. dgi, per-row dbh, and dgh = (dg_r, dg_z, dgh_n) over the coefficients in cg
   const int64_t n_grad = (int64_t)pl.nchunks * B * H;
   hipLaunchKernelGGL(grad_kernel, dim3((unsigned)((n_grad + 255) / 256)), dim3(256), 0, stream, dsum, cg, cgn, a->dgi,
-                     dghn, chunks, T, B, H);
+                     nullptr, cg, chunks, T, B, H);
   GS_CHECK_HIP(hipGetLastError());
   rc = sum_partials(a->dbh_part, chunks, (int64_t)B * 3 * H, pl.nchunks, (int64_t)B * 3 * H, stream, who);
   if (rc) return rc;
 
-  // 5. dWh[n][k] = sum_m dgh[m][n] hq[m][k]: rows [0, 2H) from dgi's r and z
-  //    parts, rows [2H, 3H) from dgh_n.
+  // 5. dWh[n][k] = sum_m dgh[m][n] hq[m][k], one product over the 3H rows
   float* dst = pl.split > 1 ? part : dw;
   const int64_t split_stride = (int64_t)3 * H * H;
   GemmArgs g3;
-  g3.a = a->dgi;  // A(n, m) = dgi[m][n]
+  g3.a = cg;  // A(n, m) = dgh[m][n]
   g3.lda = 3 * H;
   g3.b = hq;  // B(m, k) = hq[m][k]
   g3.ldb = H;
@@ -558,17 +565,11 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   g3.ldc = H;
   g3.split_stride = split_stride;
   g3.bias = nullptr;
-  g3.M = 2 * H;
+  g3.M = 3 * H;
   g3.N = H;
   g3.K = TB;
   g3.ksplit = pl.split;
   g3.layout = kGemmTN;
-  rc = gemm_f32(g3, stream, who);
-  if (rc) return rc;
-  g3.a = dghn;
-  g3.lda = H;
-  g3.c = dst + (int64_t)2 * H * H;
-  g3.M = H;
   rc = gemm_f32(g3, stream, who);
   if (rc) return rc;
   if (pl.split > 1) return sum_partials(dw, part, split_stride, pl.split, split_stride, stream, who);
