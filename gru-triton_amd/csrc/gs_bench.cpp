@@ -16,7 +16,10 @@
 // Items b0..b4 time the backward entry point of a configuration instead
 // (gs_*_bwd on the forward's own output and a random upstream gradient),
 // items c0..c4 the calibration forward (gs_observe_scan with both hidden
-// quantizers as int8 symmetric min_max observers), and
+// quantizers as int8 symmetric min_max observers), items t1, t2 the dense
+// training forward (gs_dense_fwd also storing gh through gs_args.gh_save),
+// items s1, s2 the dense backward given that saved gh (gs_bwd_args.gh_saved),
+// and
 // "proj" times the input projection at the benchmark shape (x [2048, 512],
 // Wi_cat [1536, 512], int8 x and per-row weight fake-quant) forward and
 // backward.
@@ -156,10 +159,11 @@ int run_copy(int mib, int launches) {
   return 0;
 }
 
-enum Mode { kForward, kBackward, kCalibrate };
+enum Mode { kForward, kBackward, kCalibrate, kTrainForward, kSavedBackward };
 
 int run_config(int idx, int launches, int warmup, Mode mode) {
-  const bool backward = mode == kBackward;
+  const bool backward = mode == kBackward || mode == kSavedBackward;
+  const bool save = mode == kTrainForward || mode == kSavedBackward;
   const long long T = idx == 4 ? 512 : 64, B = idx == 4 ? 64 : 32, H = idx == 4 ? 1024 : 512;
   Rng g(idx + 1);
   const float k = 1.0f / std::sqrt((float)H);
@@ -309,6 +313,16 @@ int run_config(int idx, int launches, int warmup, Mode mode) {
     CHECK(hipMalloc(&o.scratch, ns));
     o.scratch_bytes = ns;
   }
+  float* gh = nullptr;
+  if (save) {
+    if (kind != GS_KIND_DENSE) {
+      fprintf(stderr, "gs_bench: saved gh is a dense-only option (config %d is not dense)\n", idx);
+      return 2;
+    }
+    CHECK(hipMalloc(&gh, (size_t)T * B * 3 * H * sizeof(float)));
+    a.gh_save = gh;
+    if (backward) b.gh_saved = gh;
+  }
   void* ws = nullptr;
   CHECK(hipMalloc(&ws, need));
   CHECK(hipMemset(ws, 0, need));
@@ -361,12 +375,17 @@ int run_config(int idx, int launches, int warmup, Mode mode) {
   }
   if (mode != kForward) {
     char name[64];
-    snprintf(name, sizeof name, "%s_%s", kNames[idx], backward ? "backward" : "calibration");
+    snprintf(name, sizeof name, "%s_%s", kNames[idx],
+             mode == kBackward        ? "backward"
+             : mode == kSavedBackward ? "backward_saved_gh"
+             : mode == kTrainForward  ? "train_forward"
+                                      : "calibration");
     report(name, idx, ms, T, B, H);
   } else {
     report(kNames[idx], idx, ms, T, B, H);
   }
   CHECK(hipFree(ws));
+  if (gh) CHECK(hipFree(gh));
   if (b.scratch) CHECK(hipFree(b.scratch));
   if (o.scratch) CHECK(hipFree(o.scratch));
   if (stats) CHECK(hipFree(stats));
@@ -464,7 +483,8 @@ int run_proj(int launches, int warmup) {
 
 int main(int argc, char** argv) {
   if (argc < 2) {
-    fprintf(stderr, "usage: gs_bench <items: configs 0..5, b0..b5 (backward), c0..c5 (calibration), proj, copy; "
+    fprintf(stderr, "usage: gs_bench <items: configs 0..5, b0..b5 (backward), c0..c5 (calibration), "
+                    "t1, t2 (dense training forward), s1, s2 (dense backward on the saved gh), proj, copy; "
                     "comma-separated> "
                     "[launches] [warmup]\n");
     return 2;
@@ -482,7 +502,11 @@ int main(int argc, char** argv) {
     } else if (!strcmp(tok, "proj")) {
       rc = run_proj(launches, warmup);
     } else {
-      const Mode mode = tok[0] == 'b' ? kBackward : tok[0] == 'c' ? kCalibrate : kForward;
+      const Mode mode = tok[0] == 'b'   ? kBackward
+                        : tok[0] == 'c' ? kCalibrate
+                        : tok[0] == 't' ? kTrainForward
+                        : tok[0] == 's' ? kSavedBackward
+                                        : kForward;
       const char* num = mode == kForward ? tok : tok + 1;
       char* end = nullptr;
       const long idx = strtol(num, &end, 10);

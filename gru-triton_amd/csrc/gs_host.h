@@ -65,11 +65,13 @@ inline bool fits_buf32(int64_t n2, int64_t s2, int64_t n1, int64_t s1, int64_t n
   return n2 >= 1 && n1 >= 1 && s2 >= 0 && s1 >= 0 && last * 4 < (int64_t(1) << 32);
 }
 
-int validate_common(const gs_args* a, const char* who);
+// gh_ok / gh_saved_ok: the entry point takes gs_args.gh_save / gs_bwd_args.gh_saved
+// (dense only); elsewhere a non-NULL one is rejected.
+int validate_common(const gs_args* a, const char* who, bool gh_ok = false);
 // gs_args view of the forward fields of a backward call.
 gs_args fwd_view(const gs_bwd_args& a);
 // validate_common on the forward fields plus the gradient pointers.
-int validate_bwd_common(const gs_bwd_args* a, const char* who);
+int validate_bwd_common(const gs_bwd_args* a, const char* who, bool gh_saved_ok = false);
 int validate_quant(const gs_quant& q, const char* name, const char* who);
 int check_workspace(const gs_args* a, int64_t need, const char* who);
 // The backward's plain scratch: non-NULL, large enough, 256-byte aligned.

@@ -48,6 +48,7 @@ struct DParams {
   const float* w;
   const float* bh;
   float* out;
+  float* gh_save;  // SAVE instances: [T, B, 3H] q_in(h_{t-1}) Wh^T as the step computed it (no bias)
   uint64_t* xh;  // remote mode: [2][Bp][H] tagged q_in(h_t)
   uint64_t* xw;  // remote mode: [nwg] tagged XCD ids
   Ctrl ctrl;
@@ -75,7 +76,7 @@ __host__ __device__ constexpr int dense_remote_units(int KC) { return 4 * (KC >=
 // LDS row stride of a row of n floats that a wave reads as 4 rows x 4 units.
 __host__ __device__ constexpr int row_stride_pad(int n) { return n % 16 == 0 ? n + 4 : n; }
 
-template <int KIND, int KC, int NT, bool REMOTE, bool PACK = false>
+template <int KIND, int KC, int NT, bool REMOTE, bool PACK = false, bool SAVE = false>
 __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
@@ -196,6 +197,13 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       float gh[3];
 #pragma unroll
       for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
+      if constexpr (SAVE) {
+        if (mine) {
+          float* o = p.gh_save + ((int64_t)t * p.B + row) * 3 * p.H + unit;
+#pragma unroll
+          for (int g = 0; g < 3; ++g) o[g * p.H] = gh[g];
+        }
+      }
       float hn = gru_update_l2(__builtin_fmaf(kR, gh[0], cr), __builtin_fmaf(kR, gh[1], cz),
                                __builtin_fmaf(kN, gh[2], bias[2]), an2, hprev);
       float lv = 0.0f;  // level of the published value (packed exchange)
@@ -335,22 +343,27 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
 
 typedef void (*DFn)(DParams);
 
-template <int KIND, bool REMOTE, bool PACK = false>
+template <int KIND, bool REMOTE, bool PACK = false, bool SAVE = false>
 DFn pick_kernel(int KC, int* nt) {
   // Remote instances add 4 pollers_per_row(KC) poller waves to 4 compute
   // waves (KC >= 16) or to up to 12 (KC <= 8); local instances hold up to 16
   // compute waves.
   switch (KC) {
-    case 4: *nt = 1024; return scan_kernel<KIND, 4, 1024, REMOTE, PACK>;
-    case 8: *nt = 1024; return scan_kernel<KIND, 8, 1024, REMOTE, PACK>;
-    case 16: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 16, REMOTE ? 768 : 256, REMOTE, PACK>;
-    case 32: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 32, REMOTE ? 768 : 256, REMOTE, PACK>;
-    case 64: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 64, REMOTE ? 512 : 256, REMOTE, PACK>;
+    case 4: *nt = 1024; return scan_kernel<KIND, 4, 1024, REMOTE, PACK, SAVE>;
+    case 8: *nt = 1024; return scan_kernel<KIND, 8, 1024, REMOTE, PACK, SAVE>;
+    case 16: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 16, REMOTE ? 768 : 256, REMOTE, PACK, SAVE>;
+    case 32: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 32, REMOTE ? 768 : 256, REMOTE, PACK, SAVE>;
+    case 64: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 64, REMOTE ? 512 : 256, REMOTE, PACK, SAVE>;
     default: return nullptr;
   }
 }
 
-DFn pick(int kind, bool remote, int KC, int* nt, bool pack = false) {
+// save: the dense instances that also write gh_t (the training forward)
+DFn pick(int kind, bool remote, int KC, int* nt, bool pack = false, bool save = false) {
+  if (kind == kDense && save) {
+    if (remote && pack) return pick_kernel<kDense, true, true, true>(KC, nt);
+    return remote ? pick_kernel<kDense, true, false, true>(KC, nt) : pick_kernel<kDense, false, false, true>(KC, nt);
+  }
   if (kind == kDense && remote && pack) return pick_kernel<kDense, true, true>(KC, nt);
   if (kind == kDense) return remote ? pick_kernel<kDense, true>(KC, nt) : pick_kernel<kDense, false>(KC, nt);
   return remote ? pick_kernel<kMonarch1, true>(KC, nt) : pick_kernel<kMonarch1, false>(KC, nt);
@@ -420,7 +433,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   if (rc) return rc;
   rc = check_workspace(a, kCtrlBytes + pl.xh_bytes + pl.xw_bytes, who);
   if (rc) return rc;
-  DFn fn = pick(kind, pl.remote, pl.KC, &pl.nt, pl.pack);
+  DFn fn = pick(kind, pl.remote, pl.KC, &pl.nt, pl.pack, a->gh_save != nullptr);
   const int threads = 64 * (pl.nwc + (pl.remote ? 4 * pollers_per_row(pl.KC) : 0));
   const int per_set = pl.P * (kind == kMonarch1 ? pl.nb : 1);
 
@@ -448,6 +461,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.w = a->w;
   p.bh = a->bh;
   p.out = a->out;
+  p.gh_save = a->gh_save;
   char* ws = static_cast<char*>(a->workspace);
   p.ctrl = ctrl_of(ws, a->fault_mirror);
   p.xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
@@ -505,7 +519,7 @@ int64_t monarch_workspace_bytes(const gs_args* a) {
 extern "C" int gs_dense_fwd(const gs_args* a, hipStream_t stream) {
   gs::clear_error();
   const char* who = "gs_dense_fwd";
-  int rc = gs::validate_common(a, who);
+  int rc = gs::validate_common(a, who, true);
   if (rc) return rc;
   if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
   return gs::run(gs::kDense, a, stream, who);
@@ -588,7 +602,7 @@ int static_scratch(hipStream_t stream, int64_t steps, void** out, const char* wh
 extern "C" int gs_dense_fwd_noalloc(const gs_args* a, hipStream_t stream) {
   gs::clear_error();
   const char* who = "gs_dense_fwd_noalloc";
-  int rc = gs::validate_common(a, who);
+  int rc = gs::validate_common(a, who, true);
   if (rc) return rc;
   if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
   gs::DPlan pl;

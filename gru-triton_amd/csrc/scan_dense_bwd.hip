@@ -46,19 +46,30 @@ constexpr int kNV = 3;
 // ---- parallel passes ---------------------------------------------------------------
 
 // For every (t, b, k): gradients of step t per unit D_t (gru_backward with
-// dh = 1). cg [T B, 3H] holds gh on entry and (Cr, Cz, Chn) on exit.
+// dh = 1) from gh [T B, 3H] (plus bh [3H] when bh is non-NULL: gh then holds
+// the bias-free product the forward saved); writes (Cr, Cz, Chn) to cg
+// [T B, 3H], which may be gh itself (each thread reads its three gh values
+// before it writes the same three positions).
 __global__ void coef_kernel(const float* gi, int64_t sg_t, int64_t sg_b, const float* h0, int64_t sh0_b,
-                            const float* out, int64_t so_t, int64_t so_b, float* cg, float* cgn, float* zm, float* mi,
-                            int T, int B, int H, Quant qin, Quant qout) {
+                            const float* out, int64_t so_t, int64_t so_b, const float* gh, const float* bh,
+                            float* cg, float* cgn, float* zm, float* mi, int T, int B, int H, Quant qin,
+                            Quant qout) {
   const int64_t n = (int64_t)T * B * H;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = e / H;
     const int k = (int)(e - m * H);
     const int t = (int)(m / B), b = (int)(m - (int64_t)t * B);
     const float* g = gi + (int64_t)t * sg_t + (int64_t)b * sg_b + k;
+    const float* h = gh + m * 3 * H + k;
     float* c = cg + m * 3 * H + k;
     const float hp = t > 0 ? out[(int64_t)(t - 1) * so_t + (int64_t)b * so_b + k] : h0[(int64_t)b * sh0_b + k];
-    const GateGrad gg = gru_backward(g[0], g[H], g[2 * H], c[0], c[H], c[2 * H], hp, 1.0f, qout);
+    float ghr = h[0], ghz = h[H], ghn = h[2 * H];
+    if (bh != nullptr) {
+      ghr += bh[k];
+      ghz += bh[H + k];
+      ghn += bh[2 * H + k];
+    }
+    const GateGrad gg = gru_backward(g[0], g[H], g[2 * H], ghr, ghz, ghn, hp, 1.0f, qout);
     c[0] = gg.dgr;
     c[H] = gg.dgz;
     c[2 * H] = gg.dghn;
@@ -399,7 +410,7 @@ int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
 int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream) {
   const int64_t n = a->T * a->B * a->H;
   hipLaunchKernelGGL(coef_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0, stream,
-                     a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b, a->out, a->so_t, a->so_b, cg, cgn, zm, mi, (int)a->T,
+                     a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b, a->out, a->so_t, a->so_b, cg, nullptr, cg, cgn, zm, mi, (int)a->T,
                      (int)a->B, (int)a->H, to_quant(a->q_in), to_quant(a->q_out));
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
@@ -478,27 +489,31 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   rc = build_prev_state(hq, a->h0, a->sh0_b, a->out, a->so_b, T, B, H, qin, stream, who);
   if (rc) return rc;
 
-  // 1. gh = hq Wh^T + bh  -> cg [T B, 3H]
-  GemmArgs g1;
-  g1.a = hq;
-  g1.lda = H;
-  g1.b = w;  // B(k, n) = Wh[n][k]
-  g1.ldb = H;
-  g1.c = cg;
-  g1.ldc = 3 * H;
-  g1.split_stride = 0;
-  g1.bias = a->bh;
-  g1.M = TB;
-  g1.N = 3 * H;
-  g1.K = H;
-  g1.ksplit = 1;
-  g1.layout = kGemmNT;
-  rc = gemm_f32(g1, stream, who);
-  if (rc) return rc;
+  // 1. gh = hq Wh^T + bh  -> cg [T B, 3H], unless the forward saved it
+  const float* gh = a->gh_saved != nullptr ? a->gh_saved : cg;
+  if (a->gh_saved == nullptr) {
+    GemmArgs g1;
+    g1.a = hq;
+    g1.lda = H;
+    g1.b = w;  // B(k, n) = Wh[n][k]
+    g1.ldb = H;
+    g1.c = cg;
+    g1.ldc = 3 * H;
+    g1.split_stride = 0;
+    g1.bias = a->bh;
+    g1.M = TB;
+    g1.N = 3 * H;
+    g1.K = H;
+    g1.ksplit = 1;
+    g1.layout = kGemmNT;
+    rc = gemm_f32(g1, stream, who);
+    if (rc) return rc;
+  }
 
   // 2. coefficient planes
   hipLaunchKernelGGL(coef_kernel, grid1d(n_plane), dim3(256), 0, stream, a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b,
-                     a->out, a->so_t, a->so_b, cg, cgn, zm, mi, T, B, H, qin, qout);
+                     a->out, a->so_t, a->so_b, gh, a->gh_saved != nullptr ? a->bh : nullptr, cg, cgn, zm, mi, T,
+                     B, H, qin, qout);
   GS_CHECK_HIP(hipGetLastError());
 
   // 3. the recurrence
@@ -582,7 +597,7 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
   using namespace gs;
   clear_error();
   const char* who = "gs_dense_bwd";
-  int rc = validate_bwd_common(a, who);
+  int rc = validate_bwd_common(a, who, true);
   if (rc) return rc;
   if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
   if (a->dw_part == nullptr) return set_error(GS_ERR_INVALID, "%s: dw_part must be a non-NULL device pointer", who);

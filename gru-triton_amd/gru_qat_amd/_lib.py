@@ -62,7 +62,7 @@ EXPORTS = (
     "gs_abi_version",
 )
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 QuantTuple = Optional[Tuple[float, int, int]]
 
@@ -101,6 +101,7 @@ class GsArgs(ctypes.Structure):
         ("bfly_nblocks", ctypes.c_int64),
         ("q_in", GsQuant),
         ("q_out", GsQuant),
+        ("gh_save", ctypes.c_void_p),
     ]
 
 
@@ -137,6 +138,7 @@ class GsBwdArgs(ctypes.Structure):
         ("bfly_nblocks", ctypes.c_int64),
         ("q_in", GsQuant),
         ("q_out", GsQuant),
+        ("gh_saved", ctypes.c_void_p),
     ]
 
 
@@ -554,10 +556,17 @@ def _entry(lib: ctypes.CDLL, fn_name: str):
     return fn
 
 
+def _check_gh(name: str, gh: torch.Tensor, gi: torch.Tensor) -> None:
+    """gh_save / gh_saved must be a contiguous fp32 [T, B, 3H] tensor on gi's device."""
+    if gh.shape != gi.shape or gh.dtype != torch.float32 or not gh.is_contiguous() or gh.device != gi.device:
+        raise ValueError(f"{name} must be a contiguous float32 tensor of shape {tuple(gi.shape)} on {gi.device}; "
+                         f"got {tuple(gh.shape)} {gh.dtype} on {gh.device}")
+
+
 def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,
            w2: Optional[torch.Tensor], bh: torch.Tensor, out: torch.Tensor,
            h_in_quant: QuantTuple, h_out_quant: QuantTuple, nblocks: int = 0, blksz: int = 0,
-           log_n: int = 0, bfly_nblocks: int = 0) -> None:
+           log_n: int = 0, bfly_nblocks: int = 0, gh_save: Optional[torch.Tensor] = None) -> None:
     """Fill gs_args from fp32 device tensors and call the entry point on the
     current torch stream of gi's device.
 
@@ -568,10 +577,13 @@ def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: to
     GPU as a launch does on the host."""
     lib = _lib if _lib is not None else load()
     T, B, threeH = gi.shape
+    if gh_save is not None:
+        _check_gh("gh_save", gh_save, gi)
     a = GsArgs(gi.data_ptr(), h0.data_ptr(), w.data_ptr(), w2.data_ptr() if w2 is not None else None,
                bh.data_ptr(), out.data_ptr(), None, 0, None, T, B, threeH // 3, gi.stride(0), gi.stride(1),
                h0.stride(0), out.stride(0), out.stride(1), nblocks, blksz, log_n, bfly_nblocks,
-               make_quant(h_in_quant, "h_in_quant"), make_quant(h_out_quant, "h_out_quant"))
+               make_quant(h_in_quant, "h_in_quant"), make_quant(h_out_quant, "h_out_quant"),
+               gh_save.data_ptr() if gh_save is not None else None)
     tagged = kind in (KIND_DENSE, KIND_MONARCH)
     if tagged:
         need = lib.gs_workspace_bytes(kind, ctypes.byref(a))
@@ -607,7 +619,8 @@ def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w
                dgi: torch.Tensor, dh0: torch.Tensor, dw_part: Optional[torch.Tensor],
                dbh_part: torch.Tensor, h_in_quant: QuantTuple, h_out_quant: QuantTuple,
                dw2_part: Optional[torch.Tensor] = None,
-               nblocks: int = 0, blksz: int = 0, log_n: int = 0, bfly_nblocks: int = 0) -> None:
+               nblocks: int = 0, blksz: int = 0, log_n: int = 0, bfly_nblocks: int = 0,
+               gh_saved: Optional[torch.Tensor] = None) -> None:
     """Fill gs_bwd_args from fp32 device tensors (dout, dgi, dh0 and the
     partials contiguous) and call a backward entry point on the current torch
     stream of gi's device, with the stream's cached workspace when the kind
@@ -630,6 +643,9 @@ def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w
     a.log_n, a.bfly_nblocks = log_n, bfly_nblocks
     a.q_in = make_quant(h_in_quant, "h_in_quant")
     a.q_out = make_quant(h_out_quant, "h_out_quant")
+    if gh_saved is not None:
+        _check_gh("gh_saved", gh_saved, gi)
+    a.gh_saved = gh_saved.data_ptr() if gh_saved is not None else None
     need = lib.gs_bwd_workspace_bytes(kind, ctypes.byref(a))
     if need < 0:
         raise_for(int(need), lib)

@@ -19,7 +19,7 @@ there and are accepted only as keywords that are ignored.
 
 from __future__ import annotations
 
-from typing import Any, cast
+from typing import Any, Optional, cast
 
 import torch
 
@@ -28,7 +28,10 @@ from ._common import QuantTuple, check_common, check_quant, require_cuda, requir
 
 
 def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.Tensor,
-                   bh_cat: torch.Tensor, h_in_quant: QuantTuple, h_out_quant: QuantTuple) -> torch.Tensor:
+                   bh_cat: torch.Tensor, h_in_quant: QuantTuple, h_out_quant: QuantTuple,
+                   gh_save: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Runs gs_dense_fwd; with gh_save ([T, B, 3H] contiguous fp32) the kernel also
+    stores every step's q_in(h_{t-1}) Wh^T (gh_t without bh) there for the backward."""
     require_cuda(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
     require_f32(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
     T, B, H = check_common(who, gi, h0, bh_cat)
@@ -42,7 +45,7 @@ def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.T
     bh_cat = bh_cat.contiguous()
     out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
     _lib.launch(_lib.KIND_DENSE, "gs_dense_fwd", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat, out=out,
-                h_in_quant=h_in_quant, h_out_quant=h_out_quant)
+                h_in_quant=h_in_quant, h_out_quant=h_out_quant, gh_save=gh_save)
     return out
 
 
@@ -82,7 +85,14 @@ def gru_scan_backward_persistent(gi, h0, Wh_cat, bh_cat, out, dout, *, h_in_quan
     GEMM, runs the reverse recurrence as one persistent launch and forms dWh
     with a second GEMM; dbh comes back as per-row partials summed here.
     """
-    who = "gru_scan_backward_persistent"
+    return _dense_backward("gru_scan_backward_persistent", gi, h0, Wh_cat, bh_cat, out, dout, h_in_quant,
+                           h_out_quant)
+
+
+def _dense_backward(who: str, gi, h0, Wh_cat, bh_cat, out, dout, h_in_quant, h_out_quant,
+                    gh_saved: Optional[torch.Tensor] = None):
+    """Runs gs_dense_bwd; gh_saved is the gh the forward stored through gh_save
+    (then the backward skips its recompute GEMM)."""
     require_cuda(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat, out=out, dout=dout)
     require_f32(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat, out=out, dout=dout)
     T, B, H = check_common(who, gi, h0, bh_cat)
@@ -99,7 +109,7 @@ def gru_scan_backward_persistent(gi, h0, Wh_cat, bh_cat, out, dout, *, h_in_quan
     _lib.launch_bwd(_lib.KIND_DENSE, "gs_dense_bwd", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat, out=out,
                     dout=dout, dgi=dgi, dh0=dh0, dw_part=dW, dbh_part=dbh_part,
                     h_in_quant=check_quant(h_in_quant, "h_in_quant"),
-                    h_out_quant=check_quant(h_out_quant, "h_out_quant"))
+                    h_out_quant=check_quant(h_out_quant, "h_out_quant"), gh_saved=gh_saved)
     return dgi, dh0, dW, dbh_part.sum(0)
 
 
@@ -109,22 +119,30 @@ gru_scan_backward = gru_scan_backward_persistent
 
 
 class GRUScanPersistentFunction(torch.autograd.Function):
-    """autograd wrapper; saves (gi, h0, Wh_cat, bh_cat, out) like scan.py:1650."""
+    """autograd wrapper; saves (gi, h0, Wh_cat, bh_cat, out) like scan.py:1650.
+
+    When a gradient is needed the forward also has the kernel store every
+    step's q_in(h_{t-1}) Wh^T ([T, B, 3H], saved with the rest), so
+    the backward skips the reference's recompute of gh (scan.py:388-421)."""
 
     @staticmethod
     def forward(ctx: Any, gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant):  # type: ignore[override]
-        out = gru_scan_forward_persistent(gi, h0, Wh_cat, bh_cat, h_in_quant=h_in_quant,
-                                          h_out_quant=h_out_quant)
-        ctx.save_for_backward(gi, h0, Wh_cat, bh_cat, out)
+        gh = None
+        if any(ctx.needs_input_grad[:4]) and gi.dim() == 3:
+            T, B, G3 = gi.shape
+            gh = torch.empty((T, B, G3), device=gi.device, dtype=torch.float32)
+        out = _dense_forward("gru_scan_forward_persistent", gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant,
+                             gh_save=gh)
+        ctx.save_for_backward(gi, h0, Wh_cat, bh_cat, out, gh)
         ctx.h_in_quant = check_quant(h_in_quant, "h_in_quant")
         ctx.h_out_quant = check_quant(h_out_quant, "h_out_quant")
         return out
 
     @staticmethod
     def backward(ctx: Any, dout: torch.Tensor):  # type: ignore[override]
-        gi, h0, Wh_cat, bh_cat, out = ctx.saved_tensors
-        grads = gru_scan_backward(gi, h0, Wh_cat, bh_cat, out, dout, h_in_quant=ctx.h_in_quant,
-                                  h_out_quant=ctx.h_out_quant)
+        gi, h0, Wh_cat, bh_cat, out, gh = ctx.saved_tensors
+        grads = _dense_backward("gru_scan_backward_persistent", gi, h0, Wh_cat, bh_cat, out, dout,
+                                ctx.h_in_quant, ctx.h_out_quant, gh_saved=gh)
         return (*grads, None, None)
 
 

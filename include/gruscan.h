@@ -61,7 +61,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 2
+#define GS_ABI_VERSION 3
 
 #define GS_OK 0
 #define GS_ERR_INVALID (-1)  /* bad pointer, shape, stride or quant parameter (Python: ValueError) */
@@ -115,6 +115,11 @@ typedef struct gs_args {
   int64_t log_n, bfly_nblocks; /* butterfly: 2^log_n >= H                                   */
   gs_quant q_in;  /* applied to the matmul-side h only                                      */
   gs_quant q_out; /* applied to h_t before it is stored and carried                         */
+  float* gh_save; /* dense kind only, optional (NULL: not written; other kinds must pass NULL):
+                     [T, B, 3H] contiguous, where the forward also stores q_in(h_{t-1}) Wh^T
+                     (gh_t without the bias bh) of every step, so that a backward can take it as
+                     gs_bwd_args.gh_saved instead of recomputing it. No counterpart in the
+                     reference, whose backward recomputes gh (scan.py:388-421).                */
 } gs_args;
 
 int gs_dense_fwd(const gs_args* args, hipStream_t stream);
@@ -194,6 +199,9 @@ typedef struct gs_bwd_args {
   int64_t nblocks, blksz, log_n, bfly_nblocks;
   gs_quant q_in;
   gs_quant q_out;
+  const float* gh_saved; /* gs_dense_bwd only, optional (NULL: gh is recomputed; the other
+                            backward entry points must pass NULL): [T, B, 3H] contiguous, the
+                            gh the forward wrote through gs_args.gh_save with the same inputs */
 } gs_bwd_args;
 
 int gs_diagonal_bwd(const gs_bwd_args* args, hipStream_t stream);

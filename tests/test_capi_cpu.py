@@ -155,7 +155,7 @@ def test_dense_bwd_rejects_strided_out_and_missing_workspace():
 def test_bwd_workspace_sizes():
     """Dense: the tagged workspace holds control words, double-buffered tagged
     D rows (H words per padded row) plus pad and one XCD word per workgroup;
-    the plain scratch the coefficient block [T B, 3H], six [T B, H] planes,
+    the plain scratch the coefficient block [T B, 3H], five [T B, H] planes,
     per-chunk dbh sums and the K-split partials of dWh. Diagonal needs
     neither, the stage-wise butterfly path no workspace."""
     lib = _lib.load()
@@ -168,7 +168,7 @@ def test_bwd_workspace_sizes():
     split = min(-(-512 // tiles), -(-(T * B) // 256))
     nchunks = -(-T // 8)
     ws = 256 + al(2 * B * H * 8 + 16 * kc * 8) + al((B // 4) * P * 8)
-    scratch = (al(T * B * 3 * H * 4) + 6 * al(T * B * H * 4) + al(nchunks * B * 3 * H * 4)
+    scratch = (al(T * B * 3 * H * 4) + 5 * al(T * B * H * 4) + al(nchunks * B * 3 * H * 4)
                + (al(split * 3 * H * H * 4) if split > 1 else 0))
     assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == ws
     assert lib.gs_bwd_scratch_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == scratch
@@ -326,3 +326,24 @@ def test_input_projection_rejects_cpu_tensors():
         G.input_projection(torch.zeros(2, 3), torch.zeros(4, 3))
     with pytest.raises(ValueError):
         G.quantize_input_weights(torch.zeros(4, 3), (-127, 127))
+
+
+@pytest.mark.parametrize("fn", ["gs_diagonal_fwd", "gs_monarch_fwd", "gs_butterfly_fwd", "gs_butterfly_fwd_generic"])
+def test_gh_save_only_on_the_dense_forward(fn):
+    lib = _lib.load()
+    a = _args(gi=FAKE, h0=FAKE, w=FAKE, bh=FAKE, out=FAKE, gh_save=FAKE)
+    assert getattr(lib, fn)(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"gh_save" in lib.gs_last_error()
+    # the dense forward accepts it and fails later, on the missing workspace
+    assert lib.gs_dense_fwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"workspace" in lib.gs_last_error()
+
+
+@pytest.mark.parametrize("fn", ["gs_diagonal_bwd", "gs_monarch_bwd", "gs_butterfly_bwd"])
+def test_gh_saved_only_on_the_dense_backward(fn):
+    lib = _lib.load()
+    a = _bwd_args(gh_saved=FAKE, **{k: FAKE for k in BWD_PTRS})
+    assert getattr(lib, fn)(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"gh_saved" in lib.gs_last_error()
+    assert lib.gs_dense_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"gh_saved" not in lib.gs_last_error()

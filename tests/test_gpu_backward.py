@@ -147,3 +147,37 @@ def test_backward_one_sided_quantizers(dev, idx, shape, nb, qin, qout):
         err = (g.cpu() - r).abs().max().item()
         print(f"[bwd] {cfg['name']} {shape} qin={qin is not None} qout={qout is not None} d{k}: max err {err:.3e}")
         assert err <= 1e-4 * max(1.0, r.abs().max().item()), k
+
+
+@pytest.mark.parametrize("shape", [(8, 5, 64), (6, 4, 300), (64, 32, 512), (5, 37, 1000), (3, 2, 8), (9, 6, 1024)])
+@pytest.mark.parametrize("q", [None, COARSE, Q_INT8_HIDDEN])
+def test_dense_saved_gh_matches_recompute(dev, shape, q):
+    """The training forward also stores q_in(h_{t-1}) Wh^T of every step
+    (gh_save) and the dense backward then skips its recompute GEMM (gh_saved).
+    The forward's out is bit-identical with and without gh_save; the saved
+    product matches q_in(h_{t-1}) Wh^T in float64 to 1e-5 x the row scale; the
+    gradients of both backward paths agree to 1e-5 x max(1, max |grad|)."""
+    from gru_qat_amd import scan as S
+
+    T, B, H = shape
+    cfg = _cfg(1, shape, q=q)
+    x = {k: cfg[k].to(dev) for k in ("gi", "h0", "w", "bh")}
+    out_plain = S.gru_scan_forward_persistent(x["gi"], x["h0"], x["w"], x["bh"], h_in_quant=q, h_out_quant=q)
+    gh = torch.full((T, B, 3 * H), float("nan"), device=dev)
+    out = S._dense_forward("test", x["gi"], x["h0"], x["w"], x["bh"], q, q, gh_save=gh)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(out, out_plain)
+    hprev = torch.cat([x["h0"][None], out[:-1]]).cpu().double()
+    hq = O.fake_quant(hprev, q)
+    want = hq @ cfg["w"].double().T
+    scale = (hq.abs() @ cfg["w"].double().abs().T).clamp_min(1.0)
+    err = ((gh.cpu().double() - want).abs() / scale).max().item()
+    assert err <= 1e-5, f"saved gh off by {err:.3e} (relative to the row scale)"
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(13)).to(dev)
+    args = (x["gi"], x["h0"], x["w"], x["bh"], out, dout, q, q)
+    g_saved = S._dense_backward("test", *args, gh_saved=gh)
+    g_recomp = S._dense_backward("test", *args)
+    for name, a, b in zip(("dgi", "dh0", "dW", "dbh"), g_saved, g_recomp):
+        tol = 1e-5 * max(1.0, b.abs().max().item())
+        err = (a - b).abs().max().item()
+        assert err <= tol, f"{name}: saved-gh path differs from the recompute by {err:.3e} (tol {tol:.3e})"
