@@ -450,27 +450,38 @@ __device__ __forceinline__ bool group_on_one_xcd(const Ctrl& c, const uint64_t* 
   return __ballot(mine && x != x0) == 0;
 }
 
+// exit_count word: bits 0-15 count the workgroups that have left, bits 16-31
+// those of them that were dead (a grid holds at most CUs x occupancy < 2^16
+// workgroups, so neither field overflows).
+constexpr uint32_t kExitDead = 1u << 16;
+
 // Called by every thread of every workgroup after its last exchange, with
 // the LDS word (and bit mask) that records whether a wait of this workgroup
-// gave up, read after the workgroup barrier below. The workgroup's first thread raises the
-// fault word itself for a dead workgroup, so that its own release increment of
-// exit_count orders the fault word before it. The last workgroup to leave
-// (its acquire increment sees every earlier workgroup's writes) copies a fault
-// word holding this launch's value into the host mirror, advances tag_base by
-// the launch's step count (every workgroup read tag_base before it incremented
-// exit_count) and rearms exit_count.
+// gave up, read after the workgroup barrier below. The workgroup's first
+// thread raises the fault word itself for a dead workgroup and adds 1 (plus
+// kExitDead if dead) to exit_count. Every wait that raises the fault word, or
+// gives up because it was raised, marks its workgroup dead, so the last
+// workgroup to leave learns from the value its own increment returns whether
+// this launch faulted: then it stores the fault value into the host mirror.
+// It advances tag_base by the launch's step count (every workgroup read
+// tag_base before it incremented exit_count) and rearms exit_count. All of
+// this is one chain of read-modify-writes on one word, so relaxed atomics
+// suffice; acquire / release ones would write back and invalidate the XCD's
+// L2 once per workgroup (3.4 us per launch of the dense scan at 256
+// workgroups). The next launch reads the words after the kernel boundary.
 __device__ __forceinline__ void leave_grid(const Ctrl& c, uint32_t nwg, uint32_t base, uint32_t steps,
                                            const int* dead_flag, int dead_mask) {
   __syncthreads();
   if (threadIdx.x == 0) {
-    if (*dead_flag & dead_mask) raise_fault(c);
-    const uint32_t prev =
-        __hip_atomic_fetch_add(ctrl_exit_count(c), 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev == nwg - 1u) {
-      if (c.mirror != nullptr && fault_raised(c))
+    const bool dead = (*dead_flag & dead_mask) != 0;
+    if (dead) raise_fault(c);
+    const uint32_t prev = __hip_atomic_fetch_add(ctrl_exit_count(c), dead ? 1u + kExitDead : 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+    if ((prev & (kExitDead - 1u)) == nwg - 1u) {
+      if (c.mirror != nullptr && (dead || prev >= kExitDead))
         __hip_atomic_store(c.mirror, c.fval, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       __hip_atomic_store(ctrl_tag_base(c), base + steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctrl_exit_count(c), 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctrl_exit_count(c), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
