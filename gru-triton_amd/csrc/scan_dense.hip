@@ -115,6 +115,10 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   int* flags = reinterpret_cast<int*>(gst + 8 * GR);  // remote mode: [0] compute-wave iterations
                                                       // published, [1] bit 0: group on one XCD,
                                                       // bit 1: a wait of this workgroup gave up
+  // The compute waves' Wh slice is loaded first, so that its latency overlaps
+  // the LDS clear and the prologue (T = 1 and 64: 0.6 and 1.8 us less).
+  float wr[3][KC];
+  if (!poller) load_w<KC>(p.w, p.nb, p.bs, blk_g, o0, j, kb4, quad_ok, wr);
   const int lds_floats = 2 * p.hsz + p.RB * 4 * KR + (REMOTE ? 8 * GR + 4 : 0);
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
@@ -158,8 +162,6 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   // number of iterations and one barrier each, so each role's registers are
   // allocated only for its own live values.
   if (!poller) {
-    float wr[3][KC];
-    load_w<KC>(p.w, p.nb, p.bs, blk_g, o0, j, kb4, quad_ok, wr);
     // biases pre-scaled for gru_update_l2 (-log2e for r and z, 2 log2e for n)
     constexpr float kR = -kLog2e, kN = 2.0f * kLog2e;
     float bias[3];
