@@ -149,7 +149,8 @@ def test_backward_one_sided_quantizers(dev, idx, shape, nb, qin, qout):
         assert err <= 1e-4 * max(1.0, r.abs().max().item()), k
 
 
-@pytest.mark.parametrize("shape", [(8, 5, 64), (6, 4, 300), (64, 32, 512), (5, 37, 1000), (3, 2, 8), (9, 6, 1024)])
+@pytest.mark.parametrize("shape", [(8, 5, 64), (6, 4, 300), (64, 32, 512), (5, 37, 1000), (3, 2, 8), (9, 6, 1024),
+                                   (1, 3, 16), (1, 7, 512)])
 @pytest.mark.parametrize("q", [None, COARSE, Q_INT8_HIDDEN])
 def test_dense_saved_gh_matches_recompute(dev, shape, q):
     """The training forward also stores q_in(h_{t-1}) Wh^T of every step
