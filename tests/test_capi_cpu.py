@@ -152,6 +152,28 @@ def test_dense_bwd_rejects_strided_out_and_missing_workspace():
     assert b"workspace" in lib.gs_last_error()
 
 
+def _pick_split(tiles, K, cus=256):
+    """The K split of gemm_pick_split: at least 2 workgroups per CU where K
+    allows (>= 256 terms per split, <= 16 splits), best-filled last round."""
+    smax = max(1, min(16, -(-K // 256)))
+    best, best_fill = 1, -1.0
+    for s in range(1, smax + 1):
+        n = tiles * s
+        if n < 2 * cus and s < smax:
+            continue
+        fill = n / (cus * -(-n // cus))
+        if fill > best_fill:
+            best, best_fill = s, fill
+    return best
+
+
+def test_gemm_split_choice():
+    assert _pick_split(192, 2048) == 4  # dense backward dWh at T=64, B=32, H=512: 768 workgroups
+    assert _pick_split(256, 2048) == 2
+    assert _pick_split(192, 300) == 2   # K caps it
+    assert _pick_split(1, 100) == 1
+
+
 def test_bwd_workspace_sizes():
     """Dense: the tagged workspace holds control words, double-buffered tagged
     D rows (H words per padded row) plus pad and one XCD word per workgroup;
@@ -165,7 +187,7 @@ def test_bwd_workspace_sizes():
     kc = 32
     P = 128 // 4
     tiles = (3 * H // 64) * (H // 64)
-    split = min(-(-512 // tiles), -(-(T * B) // 256))
+    split = _pick_split(tiles, T * B)
     nchunks = -(-T // 8)
     ws = 256 + al(2 * B * H * 8 + 16 * kc * 8) + al((B // 4) * P * 8)
     scratch = (al(T * B * 3 * H * 4) + 5 * al(T * B * H * 4) + al(nchunks * B * 3 * H * 4)
@@ -308,7 +330,7 @@ def test_input_proj_bwd_workspace_and_validation():
     a.sx, a.sdgi, a.sdx = 512, 1536, 512
     al = lambda x: (x + 255) // 256 * 256  # noqa: E731
     tiles = (1536 // 64) * (512 // 64)
-    split = min(-(-512 // tiles), -(-2048 // 256))
+    split = _pick_split(tiles, 2048)
     want = al(-(-2048 // 256) * 1536 * 4) + (al(split * 1536 * 512 * 4) if split > 1 else 0)
     assert lib.gs_input_proj_bwd_workspace_bytes(ctypes.byref(a)) == want
     a.x, a.w, a.dgi, a.dx, a.dw = FAKE, FAKE, FAKE, FAKE, FAKE
