@@ -118,17 +118,25 @@ gru_scan_backward_triton = gru_scan_backward_persistent
 gru_scan_backward = gru_scan_backward_persistent
 
 
+def _wants_grad(*tensors: torch.Tensor) -> bool:
+    return torch.is_grad_enabled() and any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
+
+
 class GRUScanPersistentFunction(torch.autograd.Function):
     """autograd wrapper; saves (gi, h0, Wh_cat, bh_cat, out) like scan.py:1650.
 
     When a gradient is needed the forward also has the kernel store every
     step's q_in(h_{t-1}) Wh^T ([T, B, 3H], saved with the rest), so
-    the backward skips the reference's recompute of gh (scan.py:388-421)."""
+    the backward skips the reference's recompute of gh (scan.py:388-421).
+    ``save_gh`` (not in the reference signature; default: whether any input
+    needs a gradient) overrides that choice: ``needs_input_grad`` does not see
+    ``torch.no_grad()``, so the wrappers pass the grad mode in."""
 
     @staticmethod
-    def forward(ctx: Any, gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant):  # type: ignore[override]
+    def forward(ctx: Any, gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant, save_gh=None):  # type: ignore[override]
         gh = None
-        if any(ctx.needs_input_grad[:4]) and gi.dim() == 3:
+        save = any(ctx.needs_input_grad[:4]) if save_gh is None else bool(save_gh)
+        if save and gi.dim() == 3:
             T, B, G3 = gi.shape
             gh = torch.empty((T, B, G3), device=gi.device, dtype=torch.float32)
         out = _dense_forward("gru_scan_forward_persistent", gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant,
@@ -143,7 +151,7 @@ class GRUScanPersistentFunction(torch.autograd.Function):
         gi, h0, Wh_cat, bh_cat, out, gh = ctx.saved_tensors
         grads = _dense_backward("gru_scan_backward_persistent", gi, h0, Wh_cat, bh_cat, out, dout,
                                 ctx.h_in_quant, ctx.h_out_quant, gh_saved=gh)
-        return (*grads, None, None)
+        return (*grads, None, None, None)
 
 
 GRUScanFunction = GRUScanPersistentFunction
@@ -159,7 +167,8 @@ def gru_scan_persistent(
     h_out_quant: QuantTuple = None,
 ) -> torch.Tensor:
     """Differentiable dense persistent GRU scan; returns out [T, B, H]."""
-    return cast(torch.Tensor, GRUScanPersistentFunction.apply(gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant))
+    return cast(torch.Tensor, GRUScanPersistentFunction.apply(gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant,
+                                                              _wants_grad(gi, h0, Wh_cat, bh_cat)))
 
 
 def gru_scan(
@@ -173,4 +182,5 @@ def gru_scan(
 ) -> torch.Tensor:
     """Differentiable dense GRU scan (reference scan.py:1607-1627); same kernel
     as ``gru_scan_persistent`` on MI355X."""
-    return cast(torch.Tensor, GRUScanPersistentFunction.apply(gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant))
+    return cast(torch.Tensor, GRUScanPersistentFunction.apply(gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant,
+                                                              _wants_grad(gi, h0, Wh_cat, bh_cat)))

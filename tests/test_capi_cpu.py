@@ -369,3 +369,16 @@ def test_gh_saved_only_on_the_dense_backward(fn):
     assert b"gh_saved" in lib.gs_last_error()
     assert lib.gs_dense_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
     assert b"gh_saved" not in lib.gs_last_error()
+
+
+def test_dense_function_saves_gh_only_under_grad_mode():
+    """gru_scan_persistent asks its Function to store gh only when a gradient
+    will be taken: under torch.no_grad() needs_input_grad still reads True for
+    leaves that require grad, so the wrapper passes the grad mode in."""
+    from gru_qat_amd import scan as S
+
+    x = torch.ones(2, requires_grad=True)
+    assert S._wants_grad(x, torch.ones(2))
+    with torch.no_grad():
+        assert not S._wants_grad(x)
+    assert not S._wants_grad(torch.ones(2), torch.ones(3))
