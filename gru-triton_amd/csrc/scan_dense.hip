@@ -216,7 +216,9 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       // flags[1] as staged for this iteration: after a give-up the workgroup's
       // outputs are NaN and it publishes nothing more
       const int fl = REMOTE ? __builtin_amdgcn_readfirstlane(flags[1]) : 0;
-      const bool xcd_local = t >= 1 && (fl & 1) != 0;
+      // bit 0: a poller of this workgroup has seen every workgroup of the group
+      // on this XCD (first exchange), so a publish may stay in the XCD's L2
+      const bool xcd_local = (fl & 1) != 0;
       const bool dead = (fl & 2) != 0;
       if (mine) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = dead ? __builtin_nanf("") : hn;
       if (lead && unit_ok) {

@@ -253,7 +253,7 @@ __global__ __launch_bounds__(NT) void dense_bwd_kernel(BParams p) {
       const float via_w = reduce16(acc0 + acc1, s);
       // after a give-up the workgroup's D_t and dh0 are NaN and it publishes nothing more
       const int fl = __builtin_amdgcn_readfirstlane(flags[1]);
-      const bool xcd_local = st >= 1 && (fl & 1) != 0;
+      const bool xcd_local = (fl & 1) != 0;
       const bool dead = (fl & 2) != 0;
       if (lead && unit_ok && row < p.B) {
         const float* sv = sti + (buf * 4 + s) * kNV * U + uo;

@@ -290,7 +290,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
             hq = lv * p.qin.scale;
           }
           const uint32_t tag = base + (uint32_t)t + 1u;
-          const bool xl = t >= 1 && (fl & 1) != 0;
+          const bool xl = (fl & 1) != 0;
           if constexpr (PM > 0) {
             // the quad's four levels, byte e from lane j = e (a quad is all active or all idle)
             const int c = ((int)lv + 128) & 0xff;
