@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
-from typing import Optional, Tuple
+from typing import Callable, Optional, Tuple
 
 import torch
 
@@ -410,9 +410,12 @@ def load() -> ctypes.CDLL:
         return lib
 
 
+_QUANT_OFF = GsQuant(0, 1.0, -(2**31), 2**31 - 1)
+
+
 def make_quant(q: QuantTuple, name: str) -> GsQuant:
     if q is None:
-        return GsQuant(0, 1.0, -(2**31), 2**31 - 1)
+        return _QUANT_OFF  # copied into the args struct on assignment
     try:
         scale, qmin, qmax = q
     except (TypeError, ValueError):
@@ -492,14 +495,30 @@ def check_faults(device: Optional[torch.device] = None) -> None:
 # ordered already; when a persistent launch goes on a stream other than the
 # device's previous one, that stream first waits for everything queued on the
 # previous stream (torch's wait_stream: one event, recorded only on a switch).
+# Entries are (raw stream handle, torch stream object); the object is built
+# only when the device's persistent launches change streams.
 _last_stream: dict = {}
 
 
-def _order_after_previous(dev: torch.device, stream: "torch.cuda.Stream") -> None:
+def _order_after_previous(dev: torch.device, handle: int, current: Callable[[], "torch.cuda.Stream"]) -> None:
     prev = _last_stream.get(dev.index)
-    if prev is not None and prev.cuda_stream != stream.cuda_stream:
-        stream.wait_stream(prev)
-    _last_stream[dev.index] = stream
+    if prev is not None and prev[0] == handle:
+        return
+    stream = current()
+    if prev is not None:
+        stream.wait_stream(prev[1])
+    _last_stream[dev.index] = (handle, stream)
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream_handle(dev: torch.device) -> int:
+    """The raw handle of the current stream of `dev` (without building a
+    torch Stream object, which costs the host about 2.5 us per call)."""
+    if _raw_stream is not None:
+        return int(_raw_stream(dev.index if dev.index is not None else torch.cuda.current_device()))
+    return torch.cuda.current_stream(dev).cuda_stream
 
 
 def workspace(device: torch.device, stream_handle: int, nbytes: int, steps: int = 0) -> torch.Tensor:
@@ -601,15 +620,14 @@ def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: to
 
 
 def _launch_current(lib: ctypes.CDLL, fn_name: str, a: "GsArgs", dev: torch.device, need: int, steps: int) -> int:
-    stream = torch.cuda.current_stream()
-    handle = stream.cuda_stream
+    handle = current_stream_handle(dev)
     ws = workspace(dev, handle, int(need), steps=steps)
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws.numel()
     if steps:  # a persistent kernel: fault mirror and cross-stream order
         m = _mirror(dev, handle)
         _raise_if_faulted(m, fn_name)
-        _order_after_previous(dev, stream)
+        _order_after_previous(dev, handle, lambda: torch.cuda.current_stream(dev))
         a.fault_mirror = m[0].data_ptr()
     return _entry(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
 
@@ -653,15 +671,14 @@ def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w
     if scratch_need < 0:
         raise_for(int(scratch_need), lib)
     with torch.cuda.device(gi.device):
-        stream = torch.cuda.current_stream(gi.device)
-        handle = stream.cuda_stream
+        handle = current_stream_handle(gi.device)
         if need > 0:
             ws = workspace(gi.device, handle, int(need), steps=T)
             a.workspace = ws.data_ptr()
             a.workspace_bytes = ws.numel()
             m = _mirror(gi.device, handle)
             _raise_if_faulted(m, fn_name)
-            _order_after_previous(gi.device, stream)
+            _order_after_previous(gi.device, handle, lambda: torch.cuda.current_stream(gi.device))
             a.fault_mirror = m[0].data_ptr()
         scratch = None
         if scratch_need > 0:

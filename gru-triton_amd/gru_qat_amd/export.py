@@ -49,7 +49,7 @@ def quantize_rows(w: torch.Tensor, rows: int, bits: int = 8) -> Tuple[torch.Tens
     a.qmin, a.qmax = -qmax, qmax
     lib = _lib.load()
     with torch.cuda.device(w.device):
-        rc = lib.gs_quantize_rows(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(w.device).cuda_stream))
+        rc = lib.gs_quantize_rows(ctypes.byref(a), ctypes.c_void_p(_lib.current_stream_handle(w.device)))
     _lib.raise_for(rc, lib)
     return codes, scale
 

@@ -66,7 +66,7 @@ def _project(x2: torch.Tensor, Wi_cat: torch.Tensor, bi_cat: Optional[torch.Tens
     else:
         a.q_w = _lib.make_quant(None, "w_quant")
     with torch.cuda.device(x2.device):
-        rc = lib.gs_input_proj(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(x2.device).cuda_stream))
+        rc = lib.gs_input_proj(ctypes.byref(a), ctypes.c_void_p(_lib.current_stream_handle(x2.device)))
     _lib.raise_for(rc, lib)
     return gi, w_used, scales, xq
 
@@ -140,7 +140,7 @@ class InputProjectionFunction(torch.autograd.Function):
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
         with torch.cuda.device(x2.device):
             rc = lib.gs_input_proj_bwd(ctypes.byref(a),
-                                       ctypes.c_void_p(torch.cuda.current_stream(x2.device).cuda_stream))
+                                       ctypes.c_void_p(_lib.current_stream_handle(x2.device)))
         _lib.raise_for(rc, lib)
         return dx.view(ctx.x_shape), dw, dbias, None, None
 

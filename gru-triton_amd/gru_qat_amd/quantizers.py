@@ -191,7 +191,7 @@ def observe_tensor(x: torch.Tensor, q: FakeQuantizePerTensor) -> torch.Tensor:
     if need < 0:
         _lib.raise_for(int(need), lib)
     with torch.cuda.device(x.device):
-        handle = torch.cuda.current_stream(x.device).cuda_stream
+        handle = _lib.current_stream_handle(x.device)
         scratch = torch.empty((int(need),), dtype=torch.uint8, device=x.device)
         a.scratch, a.scratch_bytes = scratch.data_ptr(), scratch.numel()
         rc = lib.gs_observe_tensor(ctypes.byref(a), ctypes.c_void_p(handle))

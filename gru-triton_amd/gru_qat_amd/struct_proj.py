@@ -84,7 +84,7 @@ def struct_dims(kind: str, W: torch.Tensor, H: int) -> Tuple[int, int, int, int]
 
 
 def _stream(dev: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    return ctypes.c_void_p(_lib.current_stream_handle(dev))
 
 
 class StructInputProjFunction(torch.autograd.Function):

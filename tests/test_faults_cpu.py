@@ -42,15 +42,16 @@ def test_persistent_launches_wait_for_the_previous_stream():
     try:
         a, b = _FakeStream(11), _FakeStream(22)
         dev = _Dev(7)
-        _lib._order_after_previous(dev, a)
-        _lib._order_after_previous(dev, a)
+        order = lambda d, s: _lib._order_after_previous(d, s.cuda_stream, lambda: s)  # noqa: E731
+        order(dev, a)
+        order(dev, a)
         assert a.waited == []  # same stream: ordered already
-        _lib._order_after_previous(dev, b)
+        order(dev, b)
         assert b.waited == [11]
-        _lib._order_after_previous(dev, a)
+        order(dev, a)
         assert a.waited == [22]
         other = _FakeStream(33)
-        _lib._order_after_previous(_Dev(8), other)  # another device: independent
+        order(_Dev(8), other)  # another device: independent
         assert other.waited == []
     finally:
         _lib._last_stream.clear()
