@@ -7,6 +7,7 @@ or cannot be loaded, every scan entry point raises ``RuntimeError``.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -513,6 +514,18 @@ def _order_after_previous(dev: torch.device, handle: int, current: Callable[[], 
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
+_NO_SWITCH = contextlib.nullcontext()
+
+
+def on_device(dev: torch.device):
+    """torch.cuda.device(dev), or a no-op context when dev is already the
+    current device (the common case; entering and leaving torch's context
+    costs the host a few microseconds)."""
+    if dev.index is None or dev.index == torch.cuda.current_device():
+        return _NO_SWITCH
+    return torch.cuda.device(dev)
+
+
 def current_stream_handle(dev: torch.device) -> int:
     """The raw handle of the current stream of `dev` (without building a
     torch Stream object, which costs the host about 2.5 us per call)."""
@@ -670,7 +683,7 @@ def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w
     scratch_need = lib.gs_bwd_scratch_bytes(kind, ctypes.byref(a))
     if scratch_need < 0:
         raise_for(int(scratch_need), lib)
-    with torch.cuda.device(gi.device):
+    with on_device(gi.device):
         handle = current_stream_handle(gi.device)
         if need > 0:
             ws = workspace(gi.device, handle, int(need), steps=T)

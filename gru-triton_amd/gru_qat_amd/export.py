@@ -48,7 +48,7 @@ def quantize_rows(w: torch.Tensor, rows: int, bits: int = 8) -> Tuple[torch.Tens
     a.rows, a.cols = rows, wc.numel() // rows
     a.qmin, a.qmax = -qmax, qmax
     lib = _lib.load()
-    with torch.cuda.device(w.device):
+    with _lib.on_device(w.device):
         rc = lib.gs_quantize_rows(ctypes.byref(a), ctypes.c_void_p(_lib.current_stream_handle(w.device)))
     _lib.raise_for(rc, lib)
     return codes, scale

@@ -65,7 +65,7 @@ def _project(x2: torch.Tensor, Wi_cat: torch.Tensor, bi_cat: Optional[torch.Tens
         a.q_w = _lib.GsQuant(1, 1.0, int(w_quant[0]), int(w_quant[1]))
     else:
         a.q_w = _lib.make_quant(None, "w_quant")
-    with torch.cuda.device(x2.device):
+    with _lib.on_device(x2.device):
         rc = lib.gs_input_proj(ctypes.byref(a), ctypes.c_void_p(_lib.current_stream_handle(x2.device)))
     _lib.raise_for(rc, lib)
     return gi, w_used, scales, xq
@@ -138,7 +138,7 @@ class InputProjectionFunction(torch.autograd.Function):
             _lib.raise_for(int(need), lib)
         ws = torch.empty((max(int(need), 256),), device=x2.device, dtype=torch.uint8)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
-        with torch.cuda.device(x2.device):
+        with _lib.on_device(x2.device):
             rc = lib.gs_input_proj_bwd(ctypes.byref(a),
                                        ctypes.c_void_p(_lib.current_stream_handle(x2.device)))
         _lib.raise_for(rc, lib)

@@ -73,7 +73,7 @@ def hidden_map_dense(kind: str, hidden: torch.Tensor, H: int, hidden2: Optional[
     need = lib.gs_hidden_map_scratch_bytes(ctypes.byref(a))
     if need < 0:
         _lib.raise_for(int(need), lib)
-    with torch.cuda.device(hidden.device):
+    with _lib.on_device(hidden.device):
         handle = _lib.current_stream_handle(hidden.device)
         scratch = torch.empty((int(need),), dtype=torch.uint8, device=hidden.device) if need > 0 else None
         if scratch is not None:
@@ -98,7 +98,7 @@ def hidden_map_grad(kind: str, dm: torch.Tensor, hidden: torch.Tensor, H: int) -
     a.kind = KINDS[kind]
     a.w, a.w2, a.m = hidden.data_ptr(), None, None
     a.H, a.nblocks, a.blksz, a.log_n, a.bfly_nblocks = H, nb, bs, log_n, bfly_nb
-    with torch.cuda.device(hidden.device):
+    with _lib.on_device(hidden.device):
         handle = _lib.current_stream_handle(hidden.device)
         rc = lib.gs_hidden_map_grad(ctypes.byref(a), ctypes.c_void_p(dm.data_ptr()), ctypes.c_void_p(dw.data_ptr()),
                                     ctypes.c_void_p(handle))
@@ -166,7 +166,7 @@ def gru_scan_observe(
     need = lib.gs_observe_scan_scratch_bytes(ctypes.byref(a))
     if need < 0:
         _lib.raise_for(int(need), lib)
-    with torch.cuda.device(gi.device):
+    with _lib.on_device(gi.device):
         handle = _lib.current_stream_handle(gi.device)
         scratch = torch.empty((int(need),), dtype=torch.uint8, device=gi.device)
         a.scratch, a.scratch_bytes = scratch.data_ptr(), scratch.numel()

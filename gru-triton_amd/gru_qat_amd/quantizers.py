@@ -190,7 +190,7 @@ def observe_tensor(x: torch.Tensor, q: FakeQuantizePerTensor) -> torch.Tensor:
     need = lib.gs_observe_tensor_scratch_bytes(ctypes.byref(a))
     if need < 0:
         _lib.raise_for(int(need), lib)
-    with torch.cuda.device(x.device):
+    with _lib.on_device(x.device):
         handle = _lib.current_stream_handle(x.device)
         scratch = torch.empty((int(need),), dtype=torch.uint8, device=x.device)
         a.scratch, a.scratch_bytes = scratch.data_ptr(), scratch.numel()

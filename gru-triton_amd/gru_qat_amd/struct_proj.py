@@ -122,7 +122,7 @@ class StructInputProjFunction(torch.autograd.Function):
             _lib.raise_for(int(need), lib)
         scratch = torch.empty((max(int(need), 256),), device=dev, dtype=torch.uint8)
         a.scratch, a.scratch_bytes = scratch.data_ptr(), scratch.numel()
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = lib.gs_struct_input_proj(ctypes.byref(a), _stream(dev))
         _lib.raise_for(rc, lib)
         ctx.save_for_backward(x2, W, xq, y, y_scale)
@@ -161,7 +161,7 @@ class StructInputProjFunction(torch.autograd.Function):
             _lib.raise_for(int(need), lib)
         scratch = torch.empty((max(int(need), 256),), device=dev, dtype=torch.uint8)
         a.scratch, a.scratch_bytes = scratch.data_ptr(), scratch.numel()
-        with torch.cuda.device(dev):
+        with _lib.on_device(dev):
             rc = lib.gs_struct_input_proj_bwd(ctypes.byref(a), _stream(dev))
         _lib.raise_for(rc, lib)
         return dx.view(ctx.x_shape), dW, dbias, None, None, None
