@@ -455,10 +455,10 @@ __device__ __forceinline__ bool group_on_one_xcd(const Ctrl& c, const uint64_t* 
 // workgroups, so neither field overflows).
 constexpr uint32_t kExitDead = 1u << 16;
 
-// Called by every thread of every workgroup after its last exchange, with
-// the LDS word (and bit mask) that records whether a wait of this workgroup
-// gave up, read after the workgroup barrier below. The workgroup's first
-// thread raises the fault word itself for a dead workgroup and adds 1 (plus
+// Counts a workgroup out of the launch; called by one lane once every wait of
+// the launch in this workgroup is over, so that its dead flag (the LDS word
+// and bit mask that record whether a wait of this workgroup gave up) is
+// final. A dead workgroup raises the fault word itself and adds 1 (plus
 // kExitDead if dead) to exit_count. Every wait that raises the fault word, or
 // gives up because it was raised, marks its workgroup dead, so the last
 // workgroup to leave learns from the value its own increment returns whether
@@ -469,21 +469,26 @@ constexpr uint32_t kExitDead = 1u << 16;
 // suffice; acquire / release ones would write back and invalidate the XCD's
 // L2 once per workgroup (3.4 us per launch of the dense scan at 256
 // workgroups). The next launch reads the words after the kernel boundary.
+__device__ __forceinline__ void leave_grid_lane(const Ctrl& c, uint32_t nwg, uint32_t base, uint32_t steps,
+                                                const int* dead_flag, int dead_mask) {
+  const bool dead = (*dead_flag & dead_mask) != 0;
+  if (dead) raise_fault(c);
+  const uint32_t prev = __hip_atomic_fetch_add(ctrl_exit_count(c), dead ? 1u + kExitDead : 1u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+  if ((prev & (kExitDead - 1u)) == nwg - 1u) {
+    if (c.mirror != nullptr && (dead || prev >= kExitDead))
+      __hip_atomic_store(c.mirror, c.fval, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(ctrl_tag_base(c), base + steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ctrl_exit_count(c), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// leave_grid_lane at the end of the kernel: called by every thread of every
+// workgroup after its last exchange; the barrier makes the dead flag final.
 __device__ __forceinline__ void leave_grid(const Ctrl& c, uint32_t nwg, uint32_t base, uint32_t steps,
                                            const int* dead_flag, int dead_mask) {
   __syncthreads();
-  if (threadIdx.x == 0) {
-    const bool dead = (*dead_flag & dead_mask) != 0;
-    if (dead) raise_fault(c);
-    const uint32_t prev = __hip_atomic_fetch_add(ctrl_exit_count(c), dead ? 1u + kExitDead : 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    if ((prev & (kExitDead - 1u)) == nwg - 1u) {
-      if (c.mirror != nullptr && (dead || prev >= kExitDead))
-        __hip_atomic_store(c.mirror, c.fval, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-      __hip_atomic_store(ctrl_tag_base(c), base + steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctrl_exit_count(c), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  if (threadIdx.x == 0) leave_grid_lane(c, nwg, base, steps, dead_flag, dead_mask);
 }
 
 }  // namespace gs

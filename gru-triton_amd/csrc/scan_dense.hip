@@ -273,6 +273,11 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
     constexpr int NGI = NT / 64 > 4 * NPR ? (3 * 4 * (NT / 64 - 4 * NPR) + 63) / 64 : 1;  // gi words per lane
     for (int it = 0; it < niter; ++it) {
       const int nx = it + 1;
+      // every wait of the launch is behind the barrier that ended iteration
+      // niter - 2: the last poller wave counts the workgroup out while the
+      // compute waves run the final step
+      if (it == niter - 1 && wave == (int)(blockDim.x >> 6) - 1 && lane == 0)
+        leave_grid_lane(ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T, &flags[1], 2);
       if (nx < niter) {
         const int t2 = nx / nrbm;
         const int rb2 = rb_begin + (nx - t2 * nrbm);
@@ -342,7 +347,6 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       lds_barrier();
     }
   }
-  if (REMOTE) leave_grid(ctrl, (uint32_t)p.nwg, base, (uint32_t)p.T, &flags[1], 2);
 }
 
 typedef void (*DFn)(DParams);
