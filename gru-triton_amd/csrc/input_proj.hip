@@ -73,10 +73,20 @@ int validate_proj(int64_t M, int64_t N, int64_t I, const char* who) {
   return GS_OK;
 }
 
+// K split of the dx product (dx contiguous only: the split sums run over
+// whole planes). At the benchmark shape its 256 tiles fill the CUs once per
+// split: 2 splits, 512 workgroups, instead of one workgroup per CU.
+int dx_split(const gs_proj_bwd_args* a) {
+  return a->sdx == a->I ? gemm_pick_split((int)a->M, (int)a->I, (int)a->N) : 1;
+}
+
+// workspace: colsum partials | dW split partials | dx split partials
 int64_t proj_bwd_bytes(const gs_proj_bwd_args* a) {
   const int split = gemm_pick_split((int)a->N, (int)a->I, (int)a->M);
+  const int dxs = dx_split(a);
   return align256(colsum_partial_floats((int)a->M, (int)a->N) * 4) +
-         (split > 1 ? align256((int64_t)split * a->N * a->I * 4) : 0);
+         (split > 1 ? align256((int64_t)split * a->N * a->I * 4) : 0) +
+         (dxs > 1 ? align256((int64_t)dxs * a->M * a->I * 4) : 0);
 }
 
 }  // namespace
@@ -161,6 +171,10 @@ extern "C" int gs_input_proj_bwd(const gs_proj_bwd_args* a, hipStream_t stream) 
   const Quant qx = to_quant(a->q_x);
   float* colp = static_cast<float*>(a->workspace);
   float* part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + align256(colsum_partial_floats(M, N) * 4));
+  const int split = gemm_pick_split(N, I, M);
+  const int dxs = dx_split(a);
+  float* part_dx = reinterpret_cast<float*>(reinterpret_cast<char*>(part) +
+                                            (split > 1 ? align256((int64_t)split * N * I * 4) : 0));
 
   // dx = dgi W  (NN: A(m, n) = dgi[m][n], B(n, i) = W[n][i]), then q_x's mask
   GemmArgs g;
@@ -168,14 +182,20 @@ extern "C" int gs_input_proj_bwd(const gs_proj_bwd_args* a, hipStream_t stream) 
   g.lda = a->sdgi;
   g.b = a->w;
   g.ldb = I;
-  g.c = a->dx;
-  g.ldc = a->sdx;
+  g.c = dxs > 1 ? part_dx : a->dx;
+  g.ldc = dxs > 1 ? I : a->sdx;
+  g.split_stride = (int64_t)M * I;
   g.M = M;
   g.N = I;
   g.K = N;
+  g.ksplit = dxs;
   g.layout = kGemmNN;
   rc = gemm_f32(g, stream, who);
   if (rc) return rc;
+  if (dxs > 1) {
+    rc = sum_partials(a->dx, part_dx, (int64_t)M * I, dxs, (int64_t)M * I, stream, who);
+    if (rc) return rc;
+  }
   if (qx.on) {
     const int64_t n = (int64_t)M * I;
     hipLaunchKernelGGL(mask_clipped, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0, stream,
@@ -184,7 +204,6 @@ extern "C" int gs_input_proj_bwd(const gs_proj_bwd_args* a, hipStream_t stream) 
   }
 
   // dW = dgi^T q_x(x)  (TN: A(n, m) = dgi[m][n], B(m, i) = q_x(x[m][i]))
-  const int split = gemm_pick_split(N, I, M);
   GemmArgs h;
   h.a = a->dgi;
   h.lda = a->sdgi;

@@ -331,8 +331,14 @@ def test_input_proj_bwd_workspace_and_validation():
     al = lambda x: (x + 255) // 256 * 256  # noqa: E731
     tiles = (1536 // 64) * (512 // 64)
     split = _pick_split(tiles, 2048)
-    want = al(-(-2048 // 256) * 1536 * 4) + (al(split * 1536 * 512 * 4) if split > 1 else 0)
+    dxs = _pick_split((2048 // 64) * (512 // 64), 1536)  # dx = dgi W, K split (dx contiguous)
+    want = (al(-(-2048 // 256) * 1536 * 4) + (al(split * 1536 * 512 * 4) if split > 1 else 0)
+            + (al(dxs * 2048 * 512 * 4) if dxs > 1 else 0))
     assert lib.gs_input_proj_bwd_workspace_bytes(ctypes.byref(a)) == want
+    a.sdx = 520  # a strided dx is written by one unsplit product
+    want_strided = al(-(-2048 // 256) * 1536 * 4) + (al(split * 1536 * 512 * 4) if split > 1 else 0)
+    assert lib.gs_input_proj_bwd_workspace_bytes(ctypes.byref(a)) == want_strided
+    a.sdx = 512
     a.x, a.w, a.dgi, a.dx, a.dw = FAKE, FAKE, FAKE, FAKE, FAKE
     assert lib.gs_input_proj_bwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
     assert b"workspace" in lib.gs_last_error()
