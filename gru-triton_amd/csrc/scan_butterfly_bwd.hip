@@ -34,7 +34,7 @@ namespace gs {
 int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream);
 int grad_chunks(int64_t T);
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
-                float* chunks, hipStream_t stream, const char* who);
+                float* dgh, float* chunks, hipStream_t stream, const char* who);
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
 int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
 int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* who);
@@ -434,7 +434,7 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   rp.H = H;
   hipLaunchKernelGGL(bfly_bwd_kernel<LOGN>, dim3((unsigned)B), dim3(NT3), 0, stream, rp);
   GS_CHECK_HIP(hipGetLastError());
-  rc = launch_grad(a, dsum, cg, cgn, dghn, chunks, stream, who);
+  rc = launch_grad(a, dsum, cg, cgn, dghn, nullptr, chunks, stream, who);
   if (rc) return rc;
   TwParams tp;
   tp.tw = a->w;

@@ -421,13 +421,15 @@ int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* m
 
 int grad_chunks(int64_t T) { return (int)((T + kGradSteps - 1) / kGradSteps); }
 
+// grad_kernel over every step, then the dbh row sums; dghn and dgh as in
+// grad_kernel (either may be NULL; dgh may be cg).
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
-                float* chunks, hipStream_t stream, const char* who) {
+                float* dgh, float* chunks, hipStream_t stream, const char* who) {
   const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
   const int nch = grad_chunks(T);
   const int64_t n = (int64_t)nch * B * H;
   hipLaunchKernelGGL(grad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, dsum, cg, cgn, a->dgi,
-                     dghn, nullptr, chunks, T, B, H);
+                     dghn, dgh, chunks, T, B, H);
   GS_CHECK_HIP(hipGetLastError());
   return sum_partials(a->dbh_part, chunks, (int64_t)B * 3 * H, nch, (int64_t)B * 3 * H, stream, who);
 }

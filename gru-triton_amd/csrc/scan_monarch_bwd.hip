@@ -14,9 +14,9 @@
 //   3. monarch1_bwd_kernel: one workgroup per (block, batch rows) walks t
 //      from T-1 to 0 with D in registers and dgh_t in LDS; no exchange
 //      between workgroups
-//   4. grad_kernel (dgi, dgh_n, dbh)
-//   5. dW[g][n] = sum_m dgh[m, g, n, :]^T hq[m, n, :]: batched TN GEMMs with
-//      the T B terms split, then one sum.
+//   4. grad_kernel (dgi, dbh, and dgh = (dg_r, dg_z, dgh_n) over cg)
+//   5. dW[g][n] = sum_m dgh[m, g, n, :]^T hq[m, n, :]: one batched TN GEMM
+//      of 3 nb products with the T B terms split, then one sum.
 // The dense path would spend 3H H per row-step on the map; this one spends
 // 3 bs^2 per block (1/nb of it) and never leaves the workgroup per step.
 // Shapes outside blksz in {16, 32, 64, 128}, and the two-factor form, take
@@ -32,7 +32,7 @@ int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
 int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream);
 int grad_chunks(int64_t T);
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
-                float* chunks, hipStream_t stream, const char* who);
+                float* dgh, float* chunks, hipStream_t stream, const char* who);
 
 namespace {
 
@@ -182,13 +182,13 @@ M1Fn pick_m1(int bs, int* threads, int* rows) {
   }
 }
 
-// Scratch (plain floats), each region 256-byte aligned: hq, cgn, zm, mi, dsum,
-// dghn [T B, H] | cg [T B, 3H] | dbh chunks | dW split partials.
+// Scratch (plain floats), each region 256-byte aligned: hq, cgn, zm, mi, dsum
+// [T B, H] | cg [T B, 3H] | dbh chunks | dW split partials.
 struct M1Plan {
   bool ok = false;
   int bs = 0, nb = 0, split = 1;
   int64_t plane = 0, cg = 0, chunks = 0, part = 0;
-  int64_t scratch() const { return 6 * plane + cg + chunks + part; }
+  int64_t scratch() const { return 5 * plane + cg + chunks + part; }
 };
 
 M1Plan plan_m1(const gs_bwd_args* a) {
@@ -252,7 +252,6 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   float* zm = take(pl.plane);
   float* mi = take(pl.plane);
   float* dsum = take(pl.plane);
-  float* dghn = take(pl.plane);
   float* cg = take(pl.cg);
   float* chunks = take(pl.chunks);
   float* part = take(pl.part);
@@ -306,19 +305,20 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   hipLaunchKernelGGL(fn, dim3((unsigned)nb, (unsigned)((B + rows - 1) / rows)), dim3(threads), 0, stream, p);
   GS_CHECK_HIP(hipGetLastError());
 
-  // 4. dgi, dgh_n, dbh
-  rc = launch_grad(a, dsum, cg, cgn, dghn, chunks, stream, who);
+  // 4. dgi, dbh, and dgh = (dg_r, dg_z, dgh_n) written over the coefficients in cg
+  rc = launch_grad(a, dsum, cg, cgn, nullptr, cg, chunks, stream, who);
   if (rc) return rc;
 
-  // 5. dW[z][j][k] = sum_m dgh[m][z bs + j] hq[m][n bs + k]: the r and z gates
-  //    from dgi (products z < 2 nb), the n gate from dgh_n.
+  // 5. dW[z][j][k] = sum_m dgh[m][z bs + j] hq[m][n bs + k], z = g nb + n: one
+  //    batched product over the three gates (H = nb bs, so gate g block n sits
+  //    at column z bs of dgh)
   const int64_t wsize = (int64_t)3 * nb * bs * bs;
   float* dst = pl.split > 1 ? part : a->dw_part;
   GemmArgs g3;
-  g3.a = a->dgi;  // A(j, m) = dgi[m][z bs + j]
+  g3.a = cg;  // A(j, m) = dgh[m][z bs + j]
   g3.lda = 3 * H;
   g3.a_bs = bs;
-  g3.a_mod = 2 * nb;
+  g3.a_mod = 3 * nb;
   g3.b = hq;  // B(m, k) = hq[m][n bs + k]
   g3.ldb = H;
   g3.b_bs = bs;
@@ -331,15 +331,8 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   g3.N = bs;
   g3.K = TB;
   g3.ksplit = pl.split;
-  g3.batch = 2 * nb;
+  g3.batch = 3 * nb;
   g3.layout = kGemmTN;
-  rc = gemm_f32(g3, stream, who);
-  if (rc) return rc;
-  g3.a = dghn;
-  g3.lda = H;
-  g3.a_mod = nb;
-  g3.c = dst + (int64_t)2 * nb * bs * bs;
-  g3.batch = nb;
   rc = gemm_f32(g3, stream, who);
   if (rc) return rc;
   if (pl.split > 1) return sum_partials(a->dw_part, part, wsize, pl.split, wsize, stream, who);
