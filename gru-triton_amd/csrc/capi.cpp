@@ -38,7 +38,10 @@ int validate_quant(const gs_quant& q, const char* name, const char* who) {
 int validate_common(const gs_args* a, const char* who, bool gh_ok) {
   if (a == nullptr) return set_error(GS_ERR_INVALID, "%s: args is NULL", who);
   if (a->gh_save != nullptr && !gh_ok)
-    return set_error(GS_ERR_INVALID, "%s: gh_save is only supported by the dense forward; pass NULL", who);
+    return set_error(GS_ERR_INVALID,
+                     "%s: gh_save is only supported by the dense forward and the single-factor Monarch forward "
+                     "with blksz 16, 32, 64 or 128; pass NULL",
+                     who);
   if (a->T < 1) return set_error(GS_ERR_INVALID, "%s: seq length T must be > 0; got T=%lld", who, (long long)a->T);
   if (a->B < 1) return set_error(GS_ERR_INVALID, "%s: batch size B must be > 0; got B=%lld", who, (long long)a->B);
   if (a->H < 1) return set_error(GS_ERR_INVALID, "%s: hidden size H must be > 0; got H=%lld", who, (long long)a->H);
@@ -93,7 +96,10 @@ gs_args fwd_view(const gs_bwd_args& a) {
 int validate_bwd_common(const gs_bwd_args* a, const char* who, bool gh_saved_ok) {
   if (a == nullptr) return set_error(GS_ERR_INVALID, "%s: args is NULL", who);
   if (a->gh_saved != nullptr && !gh_saved_ok)
-    return set_error(GS_ERR_INVALID, "%s: gh_saved is only supported by the dense backward; pass NULL", who);
+    return set_error(GS_ERR_INVALID,
+                     "%s: gh_saved is only supported by the dense backward and the single-factor Monarch backward "
+                     "with blksz 16, 32, 64 or 128; pass NULL",
+                     who);
   const gs_args f = fwd_view(*a);
   const int rc = validate_common(&f, who);
   if (rc) return rc;

@@ -19,7 +19,7 @@
 // quantizers as int8 symmetric min_max observers), items t1, t2 the dense
 // training forward (gs_dense_fwd also storing gh through gs_args.gh_save),
 // items s1, s2 the dense backward given that saved gh (gs_bwd_args.gh_saved),
-// and
+// t5 and s5 the same for the single-factor Monarch configuration, and
 // "proj" times the input projection at the benchmark shape (x [2048, 512],
 // Wi_cat [1536, 512], int8 x and per-row weight fake-quant) forward and
 // backward.
@@ -315,8 +315,9 @@ int run_config(int idx, int launches, int warmup, Mode mode) {
   }
   float* gh = nullptr;
   if (save) {
-    if (kind != GS_KIND_DENSE) {
-      fprintf(stderr, "gs_bench: saved gh is a dense-only option (config %d is not dense)\n", idx);
+    if (kind != GS_KIND_DENSE && !(kind == GS_KIND_MONARCH && a.w2 == nullptr)) {
+      fprintf(stderr, "gs_bench: saved gh is an option of the dense and single-factor Monarch configurations "
+                      "(1, 2, 5), not of %d\n", idx);
       return 2;
     }
     CHECK(hipMalloc(&gh, (size_t)T * B * 3 * H * sizeof(float)));
@@ -484,7 +485,7 @@ int run_proj(int launches, int warmup) {
 int main(int argc, char** argv) {
   if (argc < 2) {
     fprintf(stderr, "usage: gs_bench <items: configs 0..5, b0..b5 (backward), c0..c5 (calibration), "
-                    "t1, t2 (dense training forward), s1, s2 (dense backward on the saved gh), proj, copy; "
+                    "t1, t2, t5 (training forward), s1, s2, s5 (backward on the saved gh), proj, copy; "
                     "comma-separated> "
                     "[launches] [warmup]\n");
     return 2;

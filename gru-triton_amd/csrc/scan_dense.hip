@@ -536,7 +536,8 @@ extern "C" int gs_dense_fwd(const gs_args* a, hipStream_t stream) {
 extern "C" int gs_monarch_fwd(const gs_args* a, hipStream_t stream) {
   gs::clear_error();
   const char* who = "gs_monarch_fwd";
-  int rc = gs::validate_common(a, who);
+  // gh_save: the single-factor forward on its block-local path only
+  int rc = gs::validate_common(a, who, a != nullptr && a->w2 == nullptr && gs::monarch1_local_ok(a));
   if (rc) return rc;
   if (a->w2) return gs::run_monarch2(a, stream, who);
   if (gs::monarch1_local_ok(a)) return gs::run_monarch1_local(a, stream);

@@ -410,10 +410,13 @@ int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
 
 }  // namespace
 
+// coef_kernel from gh in cg, or from the forward's saved gh (a->gh_saved, bias added) when set.
 int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream) {
   const int64_t n = a->T * a->B * a->H;
+  const float* gh = a->gh_saved != nullptr ? a->gh_saved : cg;
+  const float* bh = a->gh_saved != nullptr ? a->bh : nullptr;
   hipLaunchKernelGGL(coef_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0, stream,
-                     a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b, a->out, a->so_t, a->so_b, cg, nullptr, cg, cgn, zm, mi, (int)a->T,
+                     a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b, a->out, a->so_t, a->so_b, gh, bh, cg, cgn, zm, mi, (int)a->T,
                      (int)a->B, (int)a->H, to_quant(a->q_in), to_quant(a->q_out));
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;

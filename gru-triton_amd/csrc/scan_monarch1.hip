@@ -42,6 +42,7 @@ struct M1FParams {
   const float* w;   // [3, nb, bs, bs] (out, in)
   const float* bh;  // [3H]
   float* out;
+  float* gh_save;  // SAVE instances: [T, B, 3H] q_in(h_{t-1}) W^T per block (no bias)
   int64_t sg_t, sg_b, sh0_b, so_t, so_b;
   int T, B, H, nb;
   Quant qin, qout;
@@ -49,8 +50,8 @@ struct M1FParams {
 
 // QIN: 0 no q_in, 1 q_in on h0 only (q_in == q_out, so the carried state is
 // already on q_in's grid), 2 q_in every step. QOUT: q_out on. Template
-// arguments, so that the step holds no branch on them.
-template <int BS, int QIN, bool QOUT>
+// arguments, so that the step holds no branch on them. SAVE: also store gh.
+template <int BS, int QIN, bool QOUT, bool SAVE = false>
 __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FParams p) {
   constexpr int TPR = kSK * BS;
   constexpr int R = rows_per_wg<BS>();
@@ -122,6 +123,11 @@ __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FPara
         s += lane_xor_c<2>(s);
         gh[g] = s;
       }
+      if constexpr (SAVE) {
+        // the unit's four lanes hold the same sums: lane kq < 3 stores gate kq
+        if (live && kq < 3)
+          p.gh_save[((int64_t)t * p.B + b) * 3 * H + kq * H + col] = kq == 0 ? gh[0] : kq == 1 ? gh[1] : gh[2];
+      }
       const float ar = __builtin_fmaf(kR, gh[0], __builtin_fmaf(kR, cr[i], br));
       const float az = __builtin_fmaf(kR, gh[1], __builtin_fmaf(kR, cz[i], bz));
       const float gn2 = __builtin_fmaf(kN, gh[2], bn);
@@ -150,21 +156,28 @@ __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FPara
 
 typedef void (*M1FFn)(M1FParams);
 
-template <int BS>
+template <int BS, bool SAVE>
 M1FFn pick_modes(int qin, bool qout) {
   if (qout)
-    return qin == 0 ? monarch1_fwd_kernel<BS, 0, true>
-                    : qin == 1 ? monarch1_fwd_kernel<BS, 1, true> : monarch1_fwd_kernel<BS, 2, true>;
-  return qin == 0 ? monarch1_fwd_kernel<BS, 0, false> : monarch1_fwd_kernel<BS, 2, false>;
+    return qin == 0   ? monarch1_fwd_kernel<BS, 0, true, SAVE>
+           : qin == 1 ? monarch1_fwd_kernel<BS, 1, true, SAVE>
+                      : monarch1_fwd_kernel<BS, 2, true, SAVE>;
+  return qin == 0 ? monarch1_fwd_kernel<BS, 0, false, SAVE> : monarch1_fwd_kernel<BS, 2, false, SAVE>;
 }
 
-// qin: 0 off, 1 on h0 only, 2 every step (see monarch1_fwd_kernel)
-M1FFn pick(int bs, int qin, bool qout, int* threads, int* rows) {
+template <int BS>
+M1FFn pick_save(int qin, bool qout, bool save) {
+  return save ? pick_modes<BS, true>(qin, qout) : pick_modes<BS, false>(qin, qout);
+}
+
+// qin: 0 off, 1 on h0 only, 2 every step (see monarch1_fwd_kernel); save: the
+// training instance that also stores gh
+M1FFn pick(int bs, int qin, bool qout, int* threads, int* rows, bool save = false) {
   switch (bs) {
-    case 16: *rows = rows_per_wg<16>(); *threads = m1f_threads<16>(); return pick_modes<16>(qin, qout);
-    case 32: *rows = rows_per_wg<32>(); *threads = m1f_threads<32>(); return pick_modes<32>(qin, qout);
-    case 64: *rows = rows_per_wg<64>(); *threads = m1f_threads<64>(); return pick_modes<64>(qin, qout);
-    case 128: *rows = rows_per_wg<128>(); *threads = m1f_threads<128>(); return pick_modes<128>(qin, qout);
+    case 16: *rows = rows_per_wg<16>(); *threads = m1f_threads<16>(); return pick_save<16>(qin, qout, save);
+    case 32: *rows = rows_per_wg<32>(); *threads = m1f_threads<32>(); return pick_save<32>(qin, qout, save);
+    case 64: *rows = rows_per_wg<64>(); *threads = m1f_threads<64>(); return pick_save<64>(qin, qout, save);
+    case 128: *rows = rows_per_wg<128>(); *threads = m1f_threads<128>(); return pick_save<128>(qin, qout, save);
     default: return nullptr;
   }
 }
@@ -183,13 +196,14 @@ bool monarch1_local_ok(const gs_args* a) {
 int run_monarch1_local(const gs_args* a, hipStream_t stream) {
   int threads = 0, rows = 0;
   const int qin = !a->q_in.enabled ? 0 : same_quant(a->q_in, a->q_out) ? 1 : 2;
-  M1FFn fn = pick((int)a->blksz, qin, a->q_out.enabled != 0, &threads, &rows);
+  M1FFn fn = pick((int)a->blksz, qin, a->q_out.enabled != 0, &threads, &rows, a->gh_save != nullptr);
   M1FParams p;
   p.gi = a->gi;
   p.h0 = a->h0;
   p.w = a->w;
   p.bh = a->bh;
   p.out = a->out;
+  p.gh_save = a->gh_save;
   p.sg_t = a->sg_t;
   p.sg_b = a->sg_b;
   p.sh0_b = a->sh0_b;

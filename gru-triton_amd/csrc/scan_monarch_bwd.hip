@@ -228,7 +228,8 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   using namespace gs;
   const char* who = "gs_monarch_bwd";
   clear_error();
-  int rc = validate_bwd_common(a, who);
+  // gh_saved: the block-local single-factor backward only
+  int rc = validate_bwd_common(a, who, a != nullptr && plan_m1(a).ok);
   if (rc) return rc;
   const M1Plan pl = plan_m1(a);
   if (!pl.ok) return run_struct(GS_KIND_MONARCH, a, stream, who);
@@ -260,28 +261,31 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   rc = build_prev_state(hq, a->h0, a->sh0_b, a->out, a->so_b, T, B, H, to_quant(a->q_in), stream, who);
   if (rc) return rc;
 
-  // 1. gh: product z = g nb + n writes cg[:, z bs : (z + 1) bs] = hq[:, n bs : (n + 1) bs] W[g][n]^T + bh
-  GemmArgs g1;
-  g1.a = hq;
-  g1.lda = H;
-  g1.a_bs = bs;
-  g1.a_mod = nb;
-  g1.b = a->w;  // B(k, j) = W[z][j][k]
-  g1.ldb = bs;
-  g1.b_bs = (int64_t)bs * bs;
-  g1.b_mod = 3 * nb;
-  g1.c = cg;
-  g1.ldc = 3 * H;
-  g1.c_bs = bs;
-  g1.bias = a->bh;
-  g1.bias_bs = bs;
-  g1.M = TB;
-  g1.N = bs;
-  g1.K = bs;
-  g1.batch = 3 * nb;
-  g1.layout = kGemmNT;
-  rc = gemm_f32(g1, stream, who);
-  if (rc) return rc;
+  // 1. gh: product z = g nb + n writes cg[:, z bs : (z + 1) bs] = hq[:, n bs : (n + 1) bs] W[g][n]^T + bh,
+  //    unless the forward saved it (launch_coef then reads it and adds bh)
+  if (a->gh_saved == nullptr) {
+    GemmArgs g1;
+    g1.a = hq;
+    g1.lda = H;
+    g1.a_bs = bs;
+    g1.a_mod = nb;
+    g1.b = a->w;  // B(k, j) = W[z][j][k]
+    g1.ldb = bs;
+    g1.b_bs = (int64_t)bs * bs;
+    g1.b_mod = 3 * nb;
+    g1.c = cg;
+    g1.ldc = 3 * H;
+    g1.c_bs = bs;
+    g1.bias = a->bh;
+    g1.bias_bs = bs;
+    g1.M = TB;
+    g1.N = bs;
+    g1.K = bs;
+    g1.batch = 3 * nb;
+    g1.layout = kGemmNT;
+    rc = gemm_f32(g1, stream, who);
+    if (rc) return rc;
+  }
 
   // 2. coefficient planes
   rc = launch_coef(a, cg, cgn, zm, mi, stream);

@@ -11,6 +11,12 @@ R_g = Wh_struct[g], L_g = Wh_struct2[g] (both block-diagonal, blocks stored as
 ``(P z)[c * nblocks + a] = z[a * blksz + c]``, the hidden map is
 ``gh_g = P^T L_g P R_g q_in(h) + bh_g``. With identity blocks in Wh_struct2
 it is exactly the single-factor map.
+
+Saved gh (no reference counterpart): in training the single-factor forward
+with blksz 16, 32, 64 or 128 also stores each step's bias-free
+q_in(h_{t-1}) W^T ([T, B, 3H]), and the backward reads it instead of
+recomputing it with a batched product (the reference recomputes it,
+scan_monarch.py:409-884).
 """
 
 from __future__ import annotations
@@ -52,6 +58,17 @@ def _check_struct(name: str, W: torch.Tensor, H: int) -> Tuple[int, int]:
     return nblocks, out_blksz
 
 
+def monarch_saves_gh(T: int, B: int, nblocks: int, blksz: int, two_factor: bool) -> bool:
+    """Whether gs_monarch_fwd / gs_monarch_bwd take gh_save / gh_saved at this
+    shape: the single-factor block-local forward (blksz 16-128, launch grid
+    within 65535 in y and z) whose backward runs block-local too
+    (T * B <= INT32_MAX / 4)."""
+    if two_factor or blksz not in (16, 32, 64, 128):
+        return False
+    rows = max(1, 256 // (4 * blksz))
+    return nblocks <= 65535 and (B + rows - 1) // rows <= 65535 and T * B <= (2**31 - 1) // 4
+
+
 def gru_scan_monarch_forward(
     gi: torch.Tensor,
     h0: torch.Tensor,
@@ -61,8 +78,12 @@ def gru_scan_monarch_forward(
     h_in_quant: QuantTuple = None,
     h_out_quant: QuantTuple = None,
     Wh_struct2: Optional[torch.Tensor] = None,
+    gh_save: Optional[torch.Tensor] = None,
     **_ignored_tiling: Any,
 ) -> torch.Tensor:
+    """Runs gs_monarch_fwd. gh_save (keyword-only, no reference counterpart;
+    where ``monarch_saves_gh`` holds): a contiguous fp32 [T, B, 3H] tensor
+    the kernel fills with each step's bias-free q_in(h_{t-1}) W^T."""
     who = "gru_scan_monarch_forward"
     tensors = dict(gi=gi, h0=h0, Wh_struct=Wh_struct, bh_cat=bh_cat)
     if Wh_struct2 is not None:
@@ -81,7 +102,8 @@ def gru_scan_monarch_forward(
     gi, h0, Wh_struct, bh_cat = gi.contiguous(), h0.contiguous(), Wh_struct.contiguous(), bh_cat.contiguous()
     out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
     _lib.launch(_lib.KIND_MONARCH, "gs_monarch_fwd", gi=gi, h0=h0, w=Wh_struct, w2=Wh_struct2, bh=bh_cat,
-                out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, nblocks=nblocks, blksz=blksz)
+                out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, nblocks=nblocks, blksz=blksz,
+                gh_save=gh_save)
     return out
 
 
@@ -89,13 +111,15 @@ gru_scan_monarch_forward_triton = gru_scan_monarch_forward
 
 
 def gru_scan_monarch_backward(gi, h0, Wh_struct, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None,
-                              Wh_struct2=None, **_ignored_tiling: Any):
+                              Wh_struct2=None, gh_saved=None, **_ignored_tiling: Any):
     """Gradients (dgi, dh0, [dWh_struct(, dWh_struct2)], dbh_cat) of the
     Monarch scan (reference backward: scan_monarch.py:409-884 and :955-1053).
 
     ``gs_monarch_bwd`` materializes the (one- or two-factor) map as a [3H, H]
     matrix, runs the dense backward with it and carries the matrix gradient
-    onto the factors; dbh comes back as per-row partials summed here.
+    onto the factors; dbh comes back as per-row partials summed here. The
+    single-factor backward works on the blocks directly instead and, given
+    gh_saved (what the forward stored through gh_save), skips its gh product.
     """
     who = "gru_scan_monarch_backward"
     require_cuda(who, gi=gi, h0=h0, Wh_struct=Wh_struct, bh_cat=bh_cat, out=out, dout=dout)
@@ -121,7 +145,8 @@ def gru_scan_monarch_backward(gi, h0, Wh_struct, bh_cat, out, dout, *, h_in_quan
     _lib.launch_bwd(_lib.KIND_MONARCH, "gs_monarch_bwd", gi=gi, h0=h0, w=Wh_struct, w2=Wh_struct2, bh=bh_cat,
                     out=out, dout=dout, dgi=dgi, dh0=dh0, dw_part=dW, dw2_part=dW2, dbh_part=dbh_part,
                     h_in_quant=check_quant(h_in_quant, "h_in_quant"),
-                    h_out_quant=check_quant(h_out_quant, "h_out_quant"), nblocks=nblocks, blksz=blksz)
+                    h_out_quant=check_quant(h_out_quant, "h_out_quant"), nblocks=nblocks, blksz=blksz,
+                    gh_saved=gh_saved)
     dps = [dW] if dW2 is None else [dW, dW2]
     return dgi, dh0, dps, dbh_part.sum(0)
 
@@ -131,23 +156,34 @@ gru_scan_monarch_backward_triton = gru_scan_monarch_backward
 
 
 class GRUScanMonarchFunction(torch.autograd.Function):
+    """autograd wrapper; ``save_gh`` (no reference counterpart; default:
+    whether any input needs a gradient) asks the forward to store gh for the
+    backward where ``monarch_saves_gh`` allows it."""
+
     @staticmethod
-    def forward(ctx: Any, gi, h0, Wh_struct, bh_cat, h_in_quant, h_out_quant, Wh_struct2):  # type: ignore[override]
+    def forward(ctx: Any, gi, h0, Wh_struct, bh_cat, h_in_quant, h_out_quant, Wh_struct2,  # type: ignore[override]
+                save_gh=None):
+        gh = None
+        save = any(ctx.needs_input_grad[:4]) if save_gh is None else bool(save_gh)
+        if save and gi.dim() == 3 and Wh_struct.dim() == 4:
+            T, B, G3 = gi.shape
+            if monarch_saves_gh(T, B, Wh_struct.shape[1], Wh_struct.shape[3], Wh_struct2 is not None):
+                gh = torch.empty((T, B, G3), device=gi.device, dtype=torch.float32)
         out = gru_scan_monarch_forward(gi, h0, Wh_struct, bh_cat, h_in_quant=h_in_quant,
-                                       h_out_quant=h_out_quant, Wh_struct2=Wh_struct2)
-        ctx.save_for_backward(gi, h0, Wh_struct, bh_cat, out, Wh_struct2)
+                                       h_out_quant=h_out_quant, Wh_struct2=Wh_struct2, gh_save=gh)
+        ctx.save_for_backward(gi, h0, Wh_struct, bh_cat, out, Wh_struct2, gh)
         ctx.h_in_quant = check_quant(h_in_quant, "h_in_quant")
         ctx.h_out_quant = check_quant(h_out_quant, "h_out_quant")
         return out
 
     @staticmethod
     def backward(ctx: Any, dout: torch.Tensor):  # type: ignore[override]
-        gi, h0, Wh_struct, bh_cat, out, Wh_struct2 = ctx.saved_tensors
+        gi, h0, Wh_struct, bh_cat, out, Wh_struct2, gh = ctx.saved_tensors
         dgi, dh0, dps, dbh = gru_scan_monarch_backward(gi, h0, Wh_struct, bh_cat, out, dout,
                                                        h_in_quant=ctx.h_in_quant, h_out_quant=ctx.h_out_quant,
-                                                       Wh_struct2=Wh_struct2)
+                                                       Wh_struct2=Wh_struct2, gh_saved=gh)
         dW2 = dps[1] if Wh_struct2 is not None else None
-        return dgi, dh0, dps[0], dbh, None, None, dW2
+        return dgi, dh0, dps[0], dbh, None, None, dW2, None
 
 
 def gru_scan_monarch(
@@ -161,5 +197,7 @@ def gru_scan_monarch(
     Wh_struct2: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Differentiable Monarch-hidden GRU scan; returns out [T, B, H]."""
+    wants = torch.is_grad_enabled() and any(
+        isinstance(t, torch.Tensor) and t.requires_grad for t in (gi, h0, Wh_struct, bh_cat, Wh_struct2))
     return cast(torch.Tensor, GRUScanMonarchFunction.apply(gi, h0, Wh_struct, bh_cat, h_in_quant, h_out_quant,
-                                                           Wh_struct2))
+                                                           Wh_struct2, wants))

@@ -115,11 +115,14 @@ typedef struct gs_args {
   int64_t log_n, bfly_nblocks; /* butterfly: 2^log_n >= H                                   */
   gs_quant q_in;  /* applied to the matmul-side h only                                      */
   gs_quant q_out; /* applied to h_t before it is stored and carried                         */
-  float* gh_save; /* dense kind only, optional (NULL: not written; other kinds must pass NULL):
+  float* gh_save; /* gs_dense_fwd, and gs_monarch_fwd for a single factor (w2 NULL) with blksz
+                     16, 32, 64 or 128, nblocks <= 65535 and ceil(B / max(1, 64 / blksz))
+                     <= 65535; optional (NULL: not written; other calls must pass NULL):
                      [T, B, 3H] contiguous, where the forward also stores q_in(h_{t-1}) Wh^T
                      (gh_t without the bias bh) of every step, so that a backward can take it as
                      gs_bwd_args.gh_saved instead of recomputing it. No counterpart in the
-                     reference, whose backward recomputes gh (scan.py:388-421).                */
+                     reference, whose backwards recompute gh (scan.py:388-421,
+                     scan_monarch.py:409-884).                                                  */
 } gs_args;
 
 int gs_dense_fwd(const gs_args* args, hipStream_t stream);
@@ -199,8 +202,9 @@ typedef struct gs_bwd_args {
   int64_t nblocks, blksz, log_n, bfly_nblocks;
   gs_quant q_in;
   gs_quant q_out;
-  const float* gh_saved; /* gs_dense_bwd only, optional (NULL: gh is recomputed; the other
-                            backward entry points must pass NULL): [T, B, 3H] contiguous, the
+  const float* gh_saved; /* gs_dense_bwd, and gs_monarch_bwd for a single factor with blksz 16,
+                            32, 64 or 128 and T * B <= INT32_MAX / 4; optional (NULL: gh is
+                            recomputed; other calls must pass NULL): [T, B, 3H] contiguous, the
                             gh the forward wrote through gs_args.gh_save with the same inputs */
 } gs_bwd_args;
 

@@ -377,6 +377,35 @@ def test_gh_saved_only_on_the_dense_backward(fn):
     assert b"gh_saved" not in lib.gs_last_error()
 
 
+def test_monarch_gh_save_rules():
+    """gs_monarch_fwd takes gh_save only for the single-factor block-local
+    forward and gs_monarch_bwd takes gh_saved only for the block-local
+    single-factor backward; monarch_saves_gh states the same shapes."""
+    from gru_qat_amd.scan_monarch import monarch_saves_gh
+
+    lib = _lib.load()
+    # two factors: rejected before any launch
+    a = _args(H=32, nblocks=2, blksz=16, gi=FAKE, h0=FAKE, w=FAKE, w2=FAKE, bh=FAKE, out=FAKE, gh_save=FAKE)
+    assert lib.gs_monarch_fwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"gh_save" in lib.gs_last_error()
+    # blksz 8 has no block-local kernel
+    a = _args(H=32, nblocks=4, blksz=8, gi=FAKE, h0=FAKE, w=FAKE, bh=FAKE, out=FAKE, gh_save=FAKE)
+    assert lib.gs_monarch_fwd(ctypes.byref(a), None) == _lib.GS_ERR_INVALID
+    assert b"gh_save" in lib.gs_last_error()
+    # the block-local backward accepts gh_saved and fails later, on the missing scratch
+    b = _bwd_args(H=32, nblocks=2, blksz=16, gh_saved=FAKE, **{k: FAKE for k in BWD_PTRS})
+    assert lib.gs_monarch_bwd(ctypes.byref(b), None) == _lib.GS_ERR_INVALID
+    assert b"gh_saved" not in lib.gs_last_error() and b"scratch" in lib.gs_last_error()
+    b.w2 = FAKE
+    assert lib.gs_monarch_bwd(ctypes.byref(b), None) == _lib.GS_ERR_INVALID
+    assert b"gh_saved" in lib.gs_last_error()
+    assert monarch_saves_gh(64, 32, 8, 64, False)
+    assert not monarch_saves_gh(64, 32, 8, 64, True)
+    assert not monarch_saves_gh(64, 32, 4, 8, False) and not monarch_saves_gh(64, 32, 1, 256, False)
+    assert monarch_saves_gh(4, 4 * 65535, 2, 16, False) and not monarch_saves_gh(4, 4 * 65535 + 1, 2, 16, False)
+    assert not monarch_saves_gh(1 << 16, 1 << 14, 8, 64, False)
+
+
 def test_dense_function_saves_gh_only_under_grad_mode():
     """gru_scan_persistent asks its Function to store gh only when a gradient
     will be taken: under torch.no_grad() needs_input_grad still reads True for

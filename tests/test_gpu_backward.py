@@ -182,3 +182,76 @@ def test_dense_saved_gh_matches_recompute(dev, shape, q):
         tol = 1e-5 * max(1.0, b.abs().max().item())
         err = (a - b).abs().max().item()
         assert err <= tol, f"{name}: saved-gh path differs from the recompute by {err:.3e} (tol {tol:.3e})"
+
+
+@pytest.mark.parametrize("shape,nb", [((8, 5, 64), 4), ((6, 4, 256), 8), ((64, 32, 512), 8), ((5, 37, 1024), 8),
+                                      ((1, 3, 128), 2), ((7, 9, 128), 1)])
+@pytest.mark.parametrize("q", [None, COARSE, Q_INT8_HIDDEN])
+def test_monarch_saved_gh_matches_recompute(dev, shape, nb, q):
+    """Single-factor Monarch (blksz 16 to 128): the training forward stores
+    each step's bias-free q_in(h_{t-1}) W^T through gh_save; out is
+    bit-identical with and without it, the saved product matches the block
+    product in float64 to 1e-5 x the row scale, and the backward given
+    gh_saved agrees with the recomputing backward to 1e-5 x max(1, max |grad|)."""
+    from gru_qat_amd import scan_monarch as M
+
+    T, B, H = shape
+    bs = H // nb
+    assert M.monarch_saves_gh(T, B, nb, bs, False)
+    cfg = _cfg(3, shape, nb=nb, q=q)
+    x = {k: cfg[k].to(dev) for k in ("gi", "h0", "w", "bh")}
+    kw = dict(h_in_quant=q, h_out_quant=q)
+    out_plain = M.gru_scan_monarch_forward(x["gi"], x["h0"], x["w"], x["bh"], **kw)
+    gh = torch.full((T, B, 3 * H), float("nan"), device=dev)
+    out = M.gru_scan_monarch_forward(x["gi"], x["h0"], x["w"], x["bh"], gh_save=gh, **kw)
+    torch.cuda.synchronize(dev)
+    assert torch.equal(out, out_plain)
+    hprev = torch.cat([x["h0"][None], out[:-1]]).cpu().double()
+    hq = O.fake_quant(hprev, q).reshape(T, B, nb, bs)
+    W = cfg["w"].double()
+    want = torch.einsum("tbni,gnoi->tbgno", hq, W).reshape(T, B, 3 * H)
+    scale = torch.einsum("tbni,gnoi->tbgno", hq.abs(), W.abs()).reshape(T, B, 3 * H).clamp_min(1.0)
+    err = ((gh.cpu().double() - want).abs() / scale).max().item()
+    assert err <= 1e-5, f"saved gh off by {err:.3e} (relative to the row scale)"
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(13)).to(dev)
+    args = (x["gi"], x["h0"], x["w"], x["bh"], out, dout)
+    g_saved = M.gru_scan_monarch_backward(*args, gh_saved=gh, **kw)
+    g_recomp = M.gru_scan_monarch_backward(*args, **kw)
+    names = ("dgi", "dh0", "dW", "dbh")
+    for name, a, b in zip(names, g_saved, g_recomp):
+        a, b = (a[0], b[0]) if name == "dW" else (a, b)
+        tol = 1e-5 * max(1.0, b.abs().max().item())
+        err = (a - b).abs().max().item()
+        assert err <= tol, f"{name}: saved-gh path differs from the recompute by {err:.3e} (tol {tol:.3e})"
+
+
+def test_monarch_function_saves_gh_only_where_supported(dev):
+    """gru_scan_monarch saves gh for the single-factor scan under grad mode,
+    not for the two-factor scan or under no_grad; the gradients through the
+    autograd function match the recomputing backward either way."""
+    import gru_qat_amd as G
+    from gru_qat_amd import scan_monarch as M
+
+    for two in (False, True):
+        cfg = _cfg(3, (6, 4, 256), nb=8, two=two)
+        keys = ["gi", "h0", "w", "bh"] + (["w2"] if two else [])
+        leaves = {k: cfg[k].to(dev).requires_grad_(True) for k in keys}
+        out = G.gru_scan_monarch(leaves["gi"], leaves["h0"], leaves["w"], leaves["bh"],
+                                 Wh_struct2=leaves.get("w2"))
+        saved = out.grad_fn.saved_tensors
+        assert (saved[-1] is not None) == (not two)
+        dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(5)).to(dev)
+        grads = torch.autograd.grad(out, [leaves[k] for k in keys], dout)
+        plain = {k: v.detach() for k, v in leaves.items()}
+        dgi, dh0, dps, dbh = M.gru_scan_monarch_backward(plain["gi"], plain["h0"], plain["w"], plain["bh"],
+                                                         out.detach(), dout, Wh_struct2=plain.get("w2"))
+        want = [dgi, dh0, dps[0], dbh] + ([dps[1]] if two else [])
+        order = ["gi", "h0", "w", "bh"] + (["w2"] if two else [])
+        for k, g, w in zip(order, grads, want):
+            tol = 1e-5 * max(1.0, w.abs().max().item())
+            assert (g - w).abs().max().item() <= tol, k
+        with torch.no_grad():
+            out_ng = G.gru_scan_monarch(leaves["gi"], leaves["h0"], leaves["w"], leaves["bh"],
+                                        Wh_struct2=leaves.get("w2"))
+        assert out_ng.grad_fn is None
+        assert torch.equal(out_ng, out.detach())
