@@ -199,13 +199,6 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       float gh[3];
 #pragma unroll
       for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
-      if constexpr (SAVE) {
-        if (mine) {
-          float* o = p.gh_save + ((int64_t)t * p.B + row) * 3 * p.H + unit;
-#pragma unroll
-          for (int g = 0; g < 3; ++g) o[g * p.H] = gh[g];
-        }
-      }
       float hn = gru_update_l2(__builtin_fmaf(kR, gh[0], cr), __builtin_fmaf(kR, gh[1], cz),
                                __builtin_fmaf(kN, gh[2], bias[2]), an2, hprev);
       float lv = 0.0f;  // level of the published value (packed exchange)
@@ -253,6 +246,15 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
           } else {
             hst[(buf ^ 1) * p.hsz + il_index(s, unit - klo)] = hq;  // local mode: RB == 1
           }
+        }
+      }
+      if constexpr (SAVE) {
+        // after the publish, off the step's dependent chain; non-temporal (read once, by the
+        // backward)
+        if (mine) {
+          float* o = p.gh_save + ((int64_t)t * p.B + row) * 3 * p.H + unit;
+#pragma unroll
+          for (int g = 0; g < 3; ++g) __builtin_nontemporal_store(gh[g], o + g * p.H);
         }
       }
       if (REMOTE && lane == 0) __hip_atomic_fetch_add(&flags[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);

@@ -123,11 +123,6 @@ __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FPara
         s += lane_xor_c<2>(s);
         gh[g] = s;
       }
-      if constexpr (SAVE) {
-        // the unit's four lanes hold the same sums: lane kq < 3 stores gate kq
-        if (live && kq < 3)
-          p.gh_save[((int64_t)t * p.B + b) * 3 * H + kq * H + col] = kq == 0 ? gh[0] : kq == 1 ? gh[1] : gh[2];
-      }
       const float ar = __builtin_fmaf(kR, gh[0], __builtin_fmaf(kR, cr[i], br));
       const float az = __builtin_fmaf(kR, gh[1], __builtin_fmaf(kR, cz[i], bz));
       const float gn2 = __builtin_fmaf(kN, gh[2], bn);
@@ -135,6 +130,13 @@ __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FPara
       if constexpr (QOUT) hn = fake_quant(hn, p.qout);
       if (live && kq == 0) outb[(int64_t)t * p.so_t] = hn;
       if (kq == 0) hs[buf ^ 1][rs][u] = QIN == 2 ? fake_quant(hn, p.qin) : hn;
+      if constexpr (SAVE) {
+        // the unit's four lanes hold the same sums: lane kq < 3 stores gate kq; issued
+        // after the LDS write, off the gates' critical path, and non-temporal (read once, by
+        // the backward)
+        if (live && kq < 3)
+          __builtin_nontemporal_store(kq == 0 ? gh[0] : kq == 1 ? gh[1] : gh[2], &p.gh_save[((int64_t)t * p.B + b) * 3 * H + kq * H + col]);
+      }
       h = hn;
       lds_barrier();  // LDS only: the out stores need not complete here
       buf ^= 1;
