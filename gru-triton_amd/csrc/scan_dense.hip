@@ -213,7 +213,6 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       // on this XCD (first exchange), so a publish may stay in the XCD's L2
       const bool xcd_local = (fl & 1) != 0;
       const bool dead = (fl & 2) != 0;
-      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = dead ? __builtin_nanf("") : hn;
       if (lead && unit_ok) {
         *hkp = hn;
         if (t + 1 < p.T && !dead) {
@@ -248,6 +247,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
           }
         }
       }
+      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = dead ? __builtin_nanf("") : hn;
       if constexpr (SAVE) {
         // after the publish, off the step's dependent chain; non-temporal (read once, by the
         // backward)

@@ -128,8 +128,8 @@ __global__ __launch_bounds__(m1f_threads<BS>()) void monarch1_fwd_kernel(M1FPara
       const float gn2 = __builtin_fmaf(kN, gh[2], bn);
       float hn = gru_update_l2(ar, az, gn2, kN * cn[i], h);
       if constexpr (QOUT) hn = fake_quant(hn, p.qout);
-      if (live && kq == 0) outb[(int64_t)t * p.so_t] = hn;
       if (kq == 0) hs[buf ^ 1][rs][u] = QIN == 2 ? fake_quant(hn, p.qin) : hn;
+      if (live && kq == 0) outb[(int64_t)t * p.so_t] = hn;
       if constexpr (SAVE) {
         // the unit's four lanes hold the same sums: lane kq < 3 stores gate kq; issued
         // after the LDS write, off the gates' critical path, and non-temporal (read once, by
