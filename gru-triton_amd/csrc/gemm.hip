@@ -270,6 +270,20 @@ __global__ void sum_partials_kernel(float* dst, const float* src, int64_t n, int
   }
 }
 
+// Two independent sums of partials in one launch: element e < a.n of job a,
+// then the elements of job b.
+__global__ void sum_partials2_kernel(SumJob a, SumJob b) {
+  const int64_t n = a.n + b.n;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const bool first = e < a.n;
+    const SumJob& j = first ? a : b;
+    const int64_t i = first ? e : e - a.n;
+    float s = j.src[i];
+    for (int p = 1; p < j.parts; ++p) s += j.src[p * j.stride + i];
+    j.dst[i] = s;
+  }
+}
+
 // Column sums: a workgroup takes 64 columns x kColRows rows; its 256 threads
 // are 64 columns x 4 row lanes, each lane summing every 4th row (8 loads in
 // flight), and the 4 lanes are combined through LDS into partial[chunk][j].
@@ -389,6 +403,16 @@ int sum_partials(float* dst, const float* src, int64_t n, int parts, int64_t str
   const int64_t blocks = (n + 255) / 256;
   hipLaunchKernelGGL(sum_partials_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, stream, dst,
                      src, n, parts, stride);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
+
+int sum_partials2(const SumJob& a, const SumJob& b, hipStream_t stream, const char* who) {
+  (void)who;
+  const int64_t blocks = (a.n + b.n + 255) / 256;
+  if (blocks == 0) return GS_OK;
+  hipLaunchKernelGGL(sum_partials2_kernel, dim3((unsigned)(blocks < 2048 ? blocks : 2048)), dim3(256), 0, stream, a,
+                     b);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }

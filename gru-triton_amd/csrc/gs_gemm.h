@@ -41,6 +41,17 @@ int gemm_f32(const GemmArgs& g, hipStream_t stream, const char* who);
 int sum_partials(float* dst, const float* src, int64_t n, int parts, int64_t stride, hipStream_t stream,
                  const char* who);
 
+// One sum_partials job; sum_partials2 runs two of them in one launch (the
+// jobs' destinations must not overlap each other's sources).
+struct SumJob {
+  float* dst;
+  const float* src;
+  int64_t n;
+  int parts;
+  int64_t stride;
+};
+int sum_partials2(const SumJob& a, const SumJob& b, hipStream_t stream, const char* who);
+
 // dst[j] = sum_{i < rows} src[i * ld + j] for j < cols; `partials` holds
 // colsum_partial_floats(rows, cols) floats of scratch.
 int64_t colsum_partial_floats(int rows, int cols);

@@ -34,7 +34,7 @@ namespace gs {
 int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream);
 int grad_chunks(int64_t T);
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
-                float* dgh, float* chunks, hipStream_t stream, const char* who);
+                float* dgh, float* chunks, hipStream_t stream, const char* who, SumJob* dbh_sum = nullptr);
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
 int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
 int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* who);

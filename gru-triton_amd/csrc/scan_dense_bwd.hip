@@ -424,17 +424,24 @@ int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* m
 
 int grad_chunks(int64_t T) { return (int)((T + kGradSteps - 1) / kGradSteps); }
 
-// grad_kernel over every step, then the dbh row sums; dghn and dgh as in
-// grad_kernel (either may be NULL; dgh may be cg).
+// grad_kernel over every step, then the dbh row sums unless `dbh_sum` is given:
+// then the sum is left to the caller, as *dbh_sum (to be run after the last
+// reader of the chunks' producer has been launched, e.g. with sum_partials2).
+// dghn and dgh as in grad_kernel (either may be NULL; dgh may be cg).
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
-                float* dgh, float* chunks, hipStream_t stream, const char* who) {
+                float* dgh, float* chunks, hipStream_t stream, const char* who, SumJob* dbh_sum) {
   const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
   const int nch = grad_chunks(T);
   const int64_t n = (int64_t)nch * B * H;
   hipLaunchKernelGGL(grad_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, dsum, cg, cgn, a->dgi,
                      dghn, dgh, chunks, T, B, H);
   GS_CHECK_HIP(hipGetLastError());
-  return sum_partials(a->dbh_part, chunks, (int64_t)B * 3 * H, nch, (int64_t)B * 3 * H, stream, who);
+  const SumJob job{a->dbh_part, chunks, (int64_t)B * 3 * H, nch, (int64_t)B * 3 * H};
+  if (dbh_sum != nullptr) {
+    *dbh_sum = job;
+    return GS_OK;
+  }
+  return sum_partials(job.dst, job.src, job.n, job.parts, job.stride, stream, who);
 }
 
 int64_t dense_bwd_core_bytes(const gs_bwd_args* a, const char* who) {
@@ -573,8 +580,8 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   hipLaunchKernelGGL(grad_kernel, dim3((unsigned)((n_grad + 255) / 256)), dim3(256), 0, stream, dsum, cg, cgn, a->dgi,
                      nullptr, cg, chunks, T, B, H);
   GS_CHECK_HIP(hipGetLastError());
-  rc = sum_partials(a->dbh_part, chunks, (int64_t)B * 3 * H, pl.nchunks, (int64_t)B * 3 * H, stream, who);
-  if (rc) return rc;
+  // the dbh row sums run with the dWh split sums below, in one launch
+  const SumJob dbh_sum{a->dbh_part, chunks, (int64_t)B * 3 * H, pl.nchunks, (int64_t)B * 3 * H};
 
   // 5. dWh[n][k] = sum_m dgh[m][n] hq[m][k], one product over the 3H rows
   float* dst = pl.split > 1 ? part : dw;
@@ -595,8 +602,8 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   g3.layout = kGemmTN;
   rc = gemm_f32(g3, stream, who);
   if (rc) return rc;
-  if (pl.split > 1) return sum_partials(dw, part, split_stride, pl.split, split_stride, stream, who);
-  return GS_OK;
+  if (pl.split > 1) return sum_partials2(dbh_sum, SumJob{dw, part, split_stride, pl.split, split_stride}, stream, who);
+  return sum_partials(dbh_sum.dst, dbh_sum.src, dbh_sum.n, dbh_sum.parts, dbh_sum.stride, stream, who);
 }
 
 }  // namespace gs

@@ -32,7 +32,7 @@ int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
 int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream);
 int grad_chunks(int64_t T);
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
-                float* dgh, float* chunks, hipStream_t stream, const char* who);
+                float* dgh, float* chunks, hipStream_t stream, const char* who, SumJob* dbh_sum = nullptr);
 
 namespace {
 
@@ -310,7 +310,8 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   GS_CHECK_HIP(hipGetLastError());
 
   // 4. dgi, dbh, and dgh = (dg_r, dg_z, dgh_n) written over the coefficients in cg
-  rc = launch_grad(a, dsum, cg, cgn, nullptr, cg, chunks, stream, who);
+  SumJob dbh_sum;  // run with the dW split sums below, in one launch
+  rc = launch_grad(a, dsum, cg, cgn, nullptr, cg, chunks, stream, who, &dbh_sum);
   if (rc) return rc;
 
   // 5. dW[z][j][k] = sum_m dgh[m][z bs + j] hq[m][n bs + k], z = g nb + n: one
@@ -339,6 +340,6 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   g3.layout = kGemmTN;
   rc = gemm_f32(g3, stream, who);
   if (rc) return rc;
-  if (pl.split > 1) return sum_partials(a->dw_part, part, wsize, pl.split, wsize, stream, who);
-  return GS_OK;
+  if (pl.split > 1) return sum_partials2(dbh_sum, SumJob{a->dw_part, part, wsize, pl.split, wsize}, stream, who);
+  return sum_partials(dbh_sum.dst, dbh_sum.src, dbh_sum.n, dbh_sum.parts, dbh_sum.stride, stream, who);
 }
