@@ -31,7 +31,8 @@
 
 namespace gs {
 
-int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream);
+int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream,
+                float* hq = nullptr);
 int grad_chunks(int64_t T);
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
                 float* dgh, float* chunks, hipStream_t stream, const char* who, SumJob* dbh_sum = nullptr);

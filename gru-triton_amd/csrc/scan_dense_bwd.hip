@@ -49,11 +49,13 @@ constexpr int kNV = 3;
 // dh = 1) from gh [T B, 3H] (plus bh [3H] when bh is non-NULL: gh then holds
 // the bias-free product the forward saved); writes (Cr, Cz, Chn) to cg
 // [T B, 3H], which may be gh itself (each thread reads its three gh values
-// before it writes the same three positions).
+// before it writes the same three positions). hq (NULL: not written): also
+// writes q_in(h_{t-1}) [T B, H], as build_prev_state does, from the h_{t-1}
+// the thread reads anyway.
 __global__ void coef_kernel(const float* gi, int64_t sg_t, int64_t sg_b, const float* h0, int64_t sh0_b,
                             const float* out, int64_t so_t, int64_t so_b, const float* gh, const float* bh,
-                            float* cg, float* cgn, float* zm, float* mi, int T, int B, int H, Quant qin,
-                            Quant qout) {
+                            float* cg, float* cgn, float* zm, float* mi, float* hq, int T, int B, int H,
+                            Quant qin, Quant qout) {
   const int64_t n = (int64_t)T * B * H;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = e / H;
@@ -76,6 +78,7 @@ __global__ void coef_kernel(const float* gi, int64_t sg_t, int64_t sg_b, const f
     cgn[e] = gg.dgn;
     zm[e] = gg.dh_direct;
     mi[e] = (qin.on && !quant_keeps(hp, qin)) ? 0.0f : 1.0f;
+    if (hq != nullptr) hq[e] = qin.on ? fake_quant(hp, qin) : hp;
   }
 }
 
@@ -410,14 +413,15 @@ int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
 
 }  // namespace
 
-// coef_kernel from gh in cg, or from the forward's saved gh (a->gh_saved, bias added) when set.
-int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream) {
+// coef_kernel from gh in cg, or from the forward's saved gh (a->gh_saved, bias added) when set;
+// hq as in coef_kernel.
+int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream, float* hq) {
   const int64_t n = a->T * a->B * a->H;
   const float* gh = a->gh_saved != nullptr ? a->gh_saved : cg;
   const float* bh = a->gh_saved != nullptr ? a->bh : nullptr;
   hipLaunchKernelGGL(coef_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0, stream,
-                     a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b, a->out, a->so_t, a->so_b, gh, bh, cg, cgn, zm, mi, (int)a->T,
-                     (int)a->B, (int)a->H, to_quant(a->q_in), to_quant(a->q_out));
+                     a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b, a->out, a->so_t, a->so_b, gh, bh, cg, cgn, zm, mi, hq,
+                     (int)a->T, (int)a->B, (int)a->H, to_quant(a->q_in), to_quant(a->q_out));
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }
@@ -500,9 +504,12 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   const int64_t n_plane = (int64_t)TB * H;
   auto grid1d = [](int64_t n) { return dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)); };
 
-  // 0. hq = q_in([h0; out[0..T-2]]): rows m = t B + b of a [T B, H] matrix
-  rc = build_prev_state(hq, a->h0, a->sh0_b, a->out, a->so_b, T, B, H, qin, stream, who);
-  if (rc) return rc;
+  // 0. hq = q_in([h0; out[0..T-2]]): rows m = t B + b of a [T B, H] matrix; with the saved
+  //    gh nothing reads it before the coefficient pass, which writes it then
+  if (a->gh_saved == nullptr) {
+    rc = build_prev_state(hq, a->h0, a->sh0_b, a->out, a->so_b, T, B, H, qin, stream, who);
+    if (rc) return rc;
+  }
 
   // 1. gh = hq Wh^T + bh  -> cg [T B, 3H], unless the forward saved it
   const float* gh = a->gh_saved != nullptr ? a->gh_saved : cg;
@@ -527,7 +534,8 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
 
   // 2. coefficient planes
   hipLaunchKernelGGL(coef_kernel, grid1d(n_plane), dim3(256), 0, stream, a->gi, a->sg_t, a->sg_b, a->h0, a->sh0_b,
-                     a->out, a->so_t, a->so_b, gh, a->gh_saved != nullptr ? a->bh : nullptr, cg, cgn, zm, mi, T,
+                     a->out, a->so_t, a->so_b, gh, a->gh_saved != nullptr ? a->bh : nullptr, cg, cgn, zm, mi,
+                     a->gh_saved != nullptr ? hq : nullptr, T,
                      B, H, qin, qout);
   GS_CHECK_HIP(hipGetLastError());
 

@@ -29,7 +29,8 @@ namespace gs {
 int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* who);
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
 int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
-int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream);
+int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream,
+                float* hq = nullptr);
 int grad_chunks(int64_t T);
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
                 float* dgh, float* chunks, hipStream_t stream, const char* who, SumJob* dbh_sum = nullptr);
@@ -257,9 +258,11 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   float* chunks = take(pl.chunks);
   float* part = take(pl.part);
 
-  // 0. hq
-  rc = build_prev_state(hq, a->h0, a->sh0_b, a->out, a->so_b, T, B, H, to_quant(a->q_in), stream, who);
-  if (rc) return rc;
+  // 0. hq = q_in([h0; out[0..T-2]]); with the saved gh the coefficient pass writes it instead
+  if (a->gh_saved == nullptr) {
+    rc = build_prev_state(hq, a->h0, a->sh0_b, a->out, a->so_b, T, B, H, to_quant(a->q_in), stream, who);
+    if (rc) return rc;
+  }
 
   // 1. gh: product z = g nb + n writes cg[:, z bs : (z + 1) bs] = hq[:, n bs : (n + 1) bs] W[g][n]^T + bh,
   //    unless the forward saved it (launch_coef then reads it and adds bh)
@@ -288,7 +291,7 @@ extern "C" int gs_monarch_bwd(const gs_bwd_args* a, hipStream_t stream) {
   }
 
   // 2. coefficient planes
-  rc = launch_coef(a, cg, cgn, zm, mi, stream);
+  rc = launch_coef(a, cg, cgn, zm, mi, stream, a->gh_saved != nullptr ? hq : nullptr);
   if (rc) return rc;
 
   // 3. the block-local recurrence
