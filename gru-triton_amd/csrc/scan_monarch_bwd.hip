@@ -149,8 +149,8 @@ __global__ __launch_bounds__(m1_threads<BS>()) void monarch1_bwd_kernel(M1Params
         if (live && kq == 0) p.dh0[e0] = carry;
       } else {
         D = (live ? cdn[i] : 0.0f) + carry;
-        if (live && kq == 0) p.dsum[(int64_t)(t - 1) * BH + e0] = D;
         if (kq < 3) dgh[buf ^ 1][rs][kq * BS + u] = D * (live ? ccc[i] : 0.0f);
+        if (live && kq == 0) p.dsum[(int64_t)(t - 1) * BH + e0] = D;
       }
       // LDS-only barrier: the step's global stores need not complete here
       lds_barrier();
