@@ -134,8 +134,8 @@ int check_scratch(const gs_bwd_args* a, int64_t need, const char* who) {
 namespace gs {
 int64_t dense_workspace_bytes(const gs_args* a);
 int64_t monarch_workspace_bytes(const gs_args* a);
-int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a);
-int64_t dense_bwd_scratch_bytes(const gs_bwd_args* a);
+int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a, bool tiled);
+int64_t dense_bwd_scratch_bytes(const gs_bwd_args* a, bool tiled);
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
 int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
 int64_t butterfly_bwd_workspace_bytes(const gs_bwd_args* a);
@@ -151,6 +151,8 @@ int64_t gs_workspace_bytes(int kind, const gs_args* a) {
   switch (kind) {
     case GS_KIND_DENSE:
       return gs::dense_workspace_bytes(a);
+    case GS_KIND_DENSE_TILED:
+      return 0;
     case GS_KIND_MONARCH:
       return gs::monarch_workspace_bytes(a);
     case GS_KIND_DIAGONAL:
@@ -165,7 +167,9 @@ int64_t gs_bwd_workspace_bytes(int kind, const gs_bwd_args* a) {
   if (a == nullptr) return gs::set_error(GS_ERR_INVALID, "gs_bwd_workspace_bytes: args is NULL");
   switch (kind) {
     case GS_KIND_DENSE:
-      return gs::dense_bwd_workspace_bytes(a);
+      return gs::dense_bwd_workspace_bytes(a, false);
+    case GS_KIND_DENSE_TILED:
+      return gs::dense_bwd_workspace_bytes(a, true);
     case GS_KIND_DIAGONAL:
       return 0;
     case GS_KIND_MONARCH:
@@ -181,7 +185,9 @@ int64_t gs_bwd_scratch_bytes(int kind, const gs_bwd_args* a) {
   if (a == nullptr) return gs::set_error(GS_ERR_INVALID, "gs_bwd_scratch_bytes: args is NULL");
   switch (kind) {
     case GS_KIND_DENSE:
-      return gs::dense_bwd_scratch_bytes(a);
+      return gs::dense_bwd_scratch_bytes(a, false);
+    case GS_KIND_DENSE_TILED:
+      return gs::dense_bwd_scratch_bytes(a, true);
     case GS_KIND_DIAGONAL:
       return 0;
     case GS_KIND_MONARCH:

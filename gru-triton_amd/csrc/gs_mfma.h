@@ -278,6 +278,17 @@ inline int resident_groups(const void* fn, int threads, size_t lds, int per_grou
   return GS_OK;
 }
 
+// Dense hidden sizes above the persistent kernels' largest reduction (KC 64,
+// 1024 units) run on the batch-tiled kernels of scan_tiled.hip.
+constexpr int64_t kPersistentMaxH = 1024;
+inline bool dense_uses_tiled(const gs_args* a) { return a->H > kPersistentMaxH; }
+int64_t tiled_max_h();
+int run_tiled_fwd(const gs_args* a, hipStream_t stream, const char* who);
+int64_t tiled_bwd_wt_bytes(int64_t H);
+int run_tiled_bwd_recurrence(const float* w, float* wt, const float* dout, const float* cg, const float* zm,
+                             const float* mi, float* dsum, float* dh0, int64_t T, int64_t B, int64_t H,
+                             hipStream_t stream, const char* who);
+
 int64_t monarch2_workspace_bytes(const gs_args* a);
 int run_monarch2(const gs_args* a, hipStream_t stream, const char* who);
 // Single-factor Monarch forward with one workgroup per block and batch rows

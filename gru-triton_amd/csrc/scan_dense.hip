@@ -509,6 +509,7 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
 }
 
 int64_t ws_bytes(int kind, const gs_args* a) {
+  if (kind == kDense && dense_uses_tiled(a)) return 0;  // the batch-tiled kernel exchanges nothing
   DPlan pl;
   const int rc = plan_dense(kind, a, &pl, "gs_workspace_bytes");
   if (rc) return rc;
@@ -532,6 +533,7 @@ extern "C" int gs_dense_fwd(const gs_args* a, hipStream_t stream) {
   int rc = gs::validate_common(a, who, true);
   if (rc) return rc;
   if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
+  if (gs::dense_uses_tiled(a)) return gs::run_tiled_fwd(a, stream, who);
   return gs::run(gs::kDense, a, stream, who);
 }
 
@@ -616,6 +618,8 @@ extern "C" int gs_dense_fwd_noalloc(const gs_args* a, hipStream_t stream) {
   int rc = gs::validate_common(a, who, true);
   if (rc) return rc;
   if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
+  // the batch-tiled kernel of H > 1024 uses no scratch at all
+  if (gs::dense_uses_tiled(a)) return gs::run_tiled_fwd(a, stream, who);
   gs::DPlan pl;
   rc = gs::plan_dense(gs::kDense, a, &pl, who);
   if (rc) return rc;

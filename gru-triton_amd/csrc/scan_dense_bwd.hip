@@ -377,33 +377,46 @@ BFn pick_bwd(int KC, int* nt) {
 // cg [T B, 3H] | hq, cgn, zm, mi, dsum [T B, H] each |
 // dbh chunks [nchunks][B][3H] | dWh split partials.
 struct BPlan {
+  bool tiled;  // the recurrence runs on the batch-tiled kernel (scan_tiled.hip)
   int KC, nt, nwc, P, nrb, Bp, hsz, split, nchunks;
-  int64_t xh_bytes, xw_bytes, cg_bytes, plane_bytes, chunk_bytes, part_bytes;
-  int64_t total() const { return kCtrlBytes + xh_bytes + xw_bytes; }
-  int64_t scratch() const { return cg_bytes + 5 * plane_bytes + chunk_bytes + part_bytes; }
+  int64_t xh_bytes, xw_bytes, cg_bytes, plane_bytes, chunk_bytes, part_bytes, wt_bytes;
+  int64_t total() const { return tiled ? 0 : kCtrlBytes + xh_bytes + xw_bytes; }
+  int64_t scratch() const { return cg_bytes + 5 * plane_bytes + chunk_bytes + part_bytes + wt_bytes; }
 };
 
-int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who) {
+// tiled: run the recurrence on the batch-tiled kernel (it also does for H > 1024,
+// beyond the persistent kernel's largest reduction).
+int plan_bwd(const gs_bwd_args* a, BPlan* pl, const char* who, bool tiled) {
   const int H = (int)a->H;
-  pl->KC = choose_kc(H);
-  if (pl->KC < 0)
-    return set_error(GS_ERR_INVALID, "%s: hidden size %d exceeds the supported maximum of 1024", who, H);
-  const int qpb = (H + 3) / 4;
-  const int nwmax = pl->KC >= 16 ? 4 : 12;
-  pl->nwc = qpb < nwmax ? qpb : nwmax;
-  pl->P = (qpb + pl->nwc - 1) / pl->nwc;
-  pick_bwd(pl->KC, &pl->nt);
+  pl->tiled = tiled || a->H > kPersistentMaxH;
+  pl->KC = pl->nt = pl->nwc = pl->P = pl->hsz = 0;
+  pl->xh_bytes = pl->xw_bytes = pl->wt_bytes = 0;
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
-  pl->hsz = 64 * pl->KC;
+  if (pl->tiled) {
+    if (a->H > tiled_max_h())
+      return set_error(GS_ERR_INVALID, "%s: hidden size %d exceeds the supported maximum of %lld", who, H,
+                       (long long)tiled_max_h());
+    pl->wt_bytes = tiled_bwd_wt_bytes(H);
+  } else {
+    pl->KC = choose_kc(H);
+    if (pl->KC < 0)
+      return set_error(GS_ERR_INVALID, "%s: hidden size %d exceeds the supported maximum of 1024", who, H);
+    const int qpb = (H + 3) / 4;
+    const int nwmax = pl->KC >= 16 ? 4 : 12;
+    pl->nwc = qpb < nwmax ? qpb : nwmax;
+    pl->P = (qpb + pl->nwc - 1) / pl->nwc;
+    pick_bwd(pl->KC, &pl->nt);
+    pl->hsz = 64 * pl->KC;
+    // The pollers load 16 KC words per row from the row's start; the pad keeps
+    // the reads past the last row inside the workspace.
+    pl->xh_bytes = align256(2 * (int64_t)pl->Bp * H * 8 + 16 * pl->KC * 8);
+    pl->xw_bytes = align256((int64_t)pl->nrb * pl->P * 8);
+  }
   const int64_t TB = a->T * a->B;
   if (TB > INT32_MAX / 4) return set_error(GS_ERR_INVALID, "%s: T*B = %lld is too large", who, (long long)TB);
   pl->split = gemm_pick_split(3 * H, H, (int)TB);
   pl->nchunks = (int)((a->T + kGradSteps - 1) / kGradSteps);
-  // The pollers load 16 KC words per row from the row's start; the pad keeps
-  // the reads past the last row inside the workspace.
-  pl->xh_bytes = align256(2 * (int64_t)pl->Bp * H * 8 + 16 * pl->KC * 8);
-  pl->xw_bytes = align256((int64_t)pl->nrb * pl->P * 8);
   pl->cg_bytes = align256(TB * 3 * H * 4);
   pl->plane_bytes = align256(TB * H * 4);
   pl->chunk_bytes = align256((int64_t)pl->nchunks * a->B * 3 * H * 4);
@@ -448,33 +461,44 @@ int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const 
   return sum_partials(job.dst, job.src, job.n, job.parts, job.stride, stream, who);
 }
 
-int64_t dense_bwd_core_bytes(const gs_bwd_args* a, const char* who) {
+int64_t dense_bwd_core_bytes(const gs_bwd_args* a, const char* who, bool tiled) {
   BPlan pl;
-  const int rc = plan_bwd(a, &pl, who);
+  const int rc = plan_bwd(a, &pl, who, tiled);
   if (rc) return rc;
   return pl.total();
 }
 
-int64_t dense_bwd_core_scratch(const gs_bwd_args* a, const char* who) {
+int64_t dense_bwd_core_scratch(const gs_bwd_args* a, const char* who, bool tiled) {
   BPlan pl;
-  const int rc = plan_bwd(a, &pl, who);
+  const int rc = plan_bwd(a, &pl, who, tiled);
   if (rc) return rc;
   return pl.scratch();
 }
 
-int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a) { return dense_bwd_core_bytes(a, "gs_bwd_workspace_bytes"); }
-int64_t dense_bwd_scratch_bytes(const gs_bwd_args* a) { return dense_bwd_core_scratch(a, "gs_bwd_scratch_bytes"); }
+int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a, bool tiled) {
+  return dense_bwd_core_bytes(a, "gs_bwd_workspace_bytes", tiled);
+}
+int64_t dense_bwd_scratch_bytes(const gs_bwd_args* a, bool tiled) {
+  return dense_bwd_core_scratch(a, "gs_bwd_scratch_bytes", tiled);
+}
+
+namespace {
+int launch_recurrence(const BPlan& pl, const float* w, const gs_bwd_args* a, const float* cg, const float* zm,
+                      const float* mi, float* dsum, uint64_t* xh, uint64_t* xw, char* ws, hipStream_t stream,
+                      const char* who);
+}  // namespace
 
 // The dense backward of a hidden map given as the matrix w [3H, H] (rows r,
 // z, n); writes dgi, dh0 and dbh_part of `a` and the map's gradient dw
 // [3H, H]. Uses the first dense_bwd_core_bytes(a) bytes of a->workspace and
-// the first dense_bwd_core_scratch(a) bytes of a->scratch.
-int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t stream, const char* who) {
+// the first dense_bwd_core_scratch(a) bytes of a->scratch. tiled: the
+// recurrence runs on the batch-tiled kernel, as it does anyway for H > 1024.
+int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t stream, const char* who, bool tiled) {
   if (a->T > 1 && a->so_t != a->B * a->so_b)
     return set_error(GS_ERR_INVALID, "%s: out must hold its steps back to back (so_t == B * so_b); got so_t=%lld, so_b=%lld",
                      who, (long long)a->so_t, (long long)a->so_b);
   BPlan pl;
-  int rc = plan_bwd(a, &pl, who);
+  int rc = plan_bwd(a, &pl, who, tiled);
   if (rc) return rc;
   const gs_args f = fwd_view(*a);
   rc = check_workspace(&f, pl.total(), who);
@@ -540,6 +564,54 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   GS_CHECK_HIP(hipGetLastError());
 
   // 3. the recurrence
+  if (pl.tiled) {
+    float* wt = reinterpret_cast<float*>(take(pl.wt_bytes));
+    rc = run_tiled_bwd_recurrence(w, wt, a->dout, cg, zm, mi, dsum, a->dh0, T, B, H, stream, who);
+    if (rc) return rc;
+  } else {
+    rc = launch_recurrence(pl, w, a, cg, zm, mi, dsum, xh, xw, ws, stream, who);
+    if (rc) return rc;
+  }
+
+  // 4. dgi, per-row dbh, and dgh = (dg_r, dg_z, dgh_n) over the coefficients in cg
+  const int64_t n_grad = (int64_t)pl.nchunks * B * H;
+  hipLaunchKernelGGL(grad_kernel, dim3((unsigned)((n_grad + 255) / 256)), dim3(256), 0, stream, dsum, cg, cgn, a->dgi,
+                     nullptr, cg, chunks, T, B, H);
+  GS_CHECK_HIP(hipGetLastError());
+  // the dbh row sums run with the dWh split sums below, in one launch
+  const SumJob dbh_sum{a->dbh_part, chunks, (int64_t)B * 3 * H, pl.nchunks, (int64_t)B * 3 * H};
+
+  // 5. dWh[n][k] = sum_m dgh[m][n] hq[m][k], one product over the 3H rows
+  float* dst = pl.split > 1 ? part : dw;
+  const int64_t split_stride = (int64_t)3 * H * H;
+  GemmArgs g3;
+  g3.a = cg;  // A(n, m) = dgh[m][n]
+  g3.lda = 3 * H;
+  g3.b = hq;  // B(m, k) = hq[m][k]
+  g3.ldb = H;
+  g3.c = dst;
+  g3.ldc = H;
+  g3.split_stride = split_stride;
+  g3.bias = nullptr;
+  g3.M = 3 * H;
+  g3.N = H;
+  g3.K = TB;
+  g3.ksplit = pl.split;
+  g3.layout = kGemmTN;
+  rc = gemm_f32(g3, stream, who);
+  if (rc) return rc;
+  if (pl.split > 1) return sum_partials2(dbh_sum, SumJob{dw, part, split_stride, pl.split, split_stride}, stream, who);
+  return sum_partials(dbh_sum.dst, dbh_sum.src, dbh_sum.n, dbh_sum.parts, dbh_sum.stride, stream, who);
+}
+
+namespace {
+
+// Step 3 of dense_bwd_core on the persistent kernel (H <= 1024).
+int launch_recurrence(const BPlan& pl, const float* w, const gs_bwd_args* a, const float* cg, const float* zm,
+                      const float* mi, float* dsum, uint64_t* xh, uint64_t* xw, char* ws, hipStream_t stream,
+                      const char* who) {
+  const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
+  int rc = GS_OK;
   int nt = 0;
   BFn fn = pick_bwd(pl.KC, &nt);
   const int threads = 64 * (pl.nwc + 4 * bwd_pollers_per_row(pl.KC));
@@ -582,37 +654,10 @@ int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t 
   p.hsz = pl.hsz;
   hipLaunchKernelGGL(fn, dim3(p.nwg), dim3(threads), lds, stream, p);
   GS_CHECK_HIP(hipGetLastError());
-
-  // 4. dgi, per-row dbh, and dgh = (dg_r, dg_z, dgh_n) over the coefficients in cg
-  const int64_t n_grad = (int64_t)pl.nchunks * B * H;
-  hipLaunchKernelGGL(grad_kernel, dim3((unsigned)((n_grad + 255) / 256)), dim3(256), 0, stream, dsum, cg, cgn, a->dgi,
-                     nullptr, cg, chunks, T, B, H);
-  GS_CHECK_HIP(hipGetLastError());
-  // the dbh row sums run with the dWh split sums below, in one launch
-  const SumJob dbh_sum{a->dbh_part, chunks, (int64_t)B * 3 * H, pl.nchunks, (int64_t)B * 3 * H};
-
-  // 5. dWh[n][k] = sum_m dgh[m][n] hq[m][k], one product over the 3H rows
-  float* dst = pl.split > 1 ? part : dw;
-  const int64_t split_stride = (int64_t)3 * H * H;
-  GemmArgs g3;
-  g3.a = cg;  // A(n, m) = dgh[m][n]
-  g3.lda = 3 * H;
-  g3.b = hq;  // B(m, k) = hq[m][k]
-  g3.ldb = H;
-  g3.c = dst;
-  g3.ldc = H;
-  g3.split_stride = split_stride;
-  g3.bias = nullptr;
-  g3.M = 3 * H;
-  g3.N = H;
-  g3.K = TB;
-  g3.ksplit = pl.split;
-  g3.layout = kGemmTN;
-  rc = gemm_f32(g3, stream, who);
-  if (rc) return rc;
-  if (pl.split > 1) return sum_partials2(dbh_sum, SumJob{dw, part, split_stride, pl.split, split_stride}, stream, who);
-  return sum_partials(dbh_sum.dst, dbh_sum.src, dbh_sum.n, dbh_sum.parts, dbh_sum.stride, stream, who);
+  return GS_OK;
 }
+
+}  // namespace
 
 }  // namespace gs
 
@@ -624,5 +669,19 @@ extern "C" int gs_dense_bwd(const gs_bwd_args* a, hipStream_t stream) {
   if (rc) return rc;
   if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
   if (a->dw_part == nullptr) return set_error(GS_ERR_INVALID, "%s: dw_part must be a non-NULL device pointer", who);
-  return dense_bwd_core(a, a->w, a->dw_part, stream, who);
+  return dense_bwd_core(a, a->w, a->dw_part, stream, who, false);
+}
+
+// The barrier-free dense backward (reference gru_scan_backward_triton,
+// scan.py:1355-1447, kernel gru_scan_bwd_kernel :916-1352): dense_bwd_core with
+// the recurrence on the batch-tiled kernel at every H.
+extern "C" int gs_dense_bwd_tiled(const gs_bwd_args* a, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_dense_bwd_tiled";
+  int rc = validate_bwd_common(a, who, true);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
+  if (a->dw_part == nullptr) return set_error(GS_ERR_INVALID, "%s: dw_part must be a non-NULL device pointer", who);
+  return dense_bwd_core(a, a->w, a->dw_part, stream, who, true);
 }

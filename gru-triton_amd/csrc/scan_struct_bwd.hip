@@ -30,9 +30,10 @@
 
 namespace gs {
 
-int64_t dense_bwd_core_bytes(const gs_bwd_args* a, const char* who);
-int64_t dense_bwd_core_scratch(const gs_bwd_args* a, const char* who);
-int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t stream, const char* who);
+int64_t dense_bwd_core_bytes(const gs_bwd_args* a, const char* who, bool tiled = false);
+int64_t dense_bwd_core_scratch(const gs_bwd_args* a, const char* who, bool tiled = false);
+int dense_bwd_core(const gs_bwd_args* a, const float* w, float* dw, hipStream_t stream, const char* who,
+                   bool tiled = false);
 
 namespace {
 

@@ -23,6 +23,7 @@ from .scan_butterfly import (
 from .scan_diagonal import extract_diagonal_factors, gru_scan_diagonal, gru_scan_diagonal_forward
 from .scan_monarch import extract_monarch_factors, gru_scan_monarch, gru_scan_monarch_forward
 from .scan_circulant import extract_circulant_factors, gru_scan_circulant, gru_scan_circulant_forward
+from ._common import set_save_gh
 from ._lib import PersistentScanFault, check_faults, load as load_library, workspace_faults
 from .gru_layer import ScanLayer, fast_dispatch_eligible, forward_fast_dispatch, layer_forward, resolve_use_triton
 from .input_proj import input_projection, quantize_input_weights
@@ -73,4 +74,5 @@ __all__ = [
     "extract_circulant_factors",
     "check_faults",
     "PersistentScanFault",
+    "set_save_gh",
 ]

@@ -79,3 +79,23 @@ def check_quant(q: QuantTuple, name: str) -> QuantTuple:
     if int(qmin) > int(qmax):
         raise ValueError(f"{name} qmin must be <= qmax; got {qmin} > {qmax}")
     return (scale, int(qmin), int(qmax))
+
+
+# Training forwards of the dense and single-factor Monarch scans store gh
+# ([T, B, 3H] fp32, 75 % more saved activations than the reference) so that
+# their backward skips the recompute GEMM. set_save_gh(False) turns that off:
+# the backward then recomputes gh, as the reference does (scan.py:388-421).
+_SAVE_GH = True
+
+
+def set_save_gh(enabled: bool) -> None:
+    """Whether training forwards store gh for the backward (default True)."""
+    global _SAVE_GH
+    _SAVE_GH = bool(enabled)
+
+
+def save_gh_default(*tensors: Optional[torch.Tensor]) -> bool:
+    """The forward stores gh when the switch is on, grad mode is on and any
+    tensor input requires a gradient."""
+    return _SAVE_GH and torch.is_grad_enabled() and any(
+        isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)

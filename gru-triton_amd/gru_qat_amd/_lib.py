@@ -27,10 +27,12 @@ KIND_DIAGONAL = 1
 KIND_MONARCH = 2
 KIND_BUTTERFLY = 3
 KIND_CIRCULANT = 4
+KIND_DENSE_TILED = 5  # size queries of the batch-tiled dense entry points
 
 # Every symbol include/gruscan.h declares.
 EXPORTS = (
     "gs_dense_fwd",
+    "gs_dense_fwd_tiled",
     "gs_dense_fwd_noalloc",
     "gs_diagonal_fwd",
     "gs_monarch_fwd",
@@ -38,6 +40,7 @@ EXPORTS = (
     "gs_butterfly_fwd_generic",
     "gs_diagonal_bwd",
     "gs_dense_bwd",
+    "gs_dense_bwd_tiled",
     "gs_monarch_bwd",
     "gs_butterfly_bwd",
     "gs_input_proj",
@@ -63,7 +66,7 @@ EXPORTS = (
     "gs_abi_version",
 )
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 QuantTuple = Optional[Tuple[float, int, int]]
 
@@ -356,12 +359,12 @@ def load() -> ctypes.CDLL:
                 "`make -C gru-triton_amd/csrc` or __graft_entry__.build()"
             )
         lib = ctypes.CDLL(LIB_PATH)
-        for name in ("gs_dense_fwd", "gs_dense_fwd_noalloc", "gs_diagonal_fwd", "gs_monarch_fwd",
+        for name in ("gs_dense_fwd", "gs_dense_fwd_tiled", "gs_dense_fwd_noalloc", "gs_diagonal_fwd", "gs_monarch_fwd",
                      "gs_butterfly_fwd", "gs_butterfly_fwd_generic"):
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(GsArgs), ctypes.c_void_p]
             fn.restype = ctypes.c_int
-        for name in ("gs_diagonal_bwd", "gs_dense_bwd", "gs_monarch_bwd", "gs_butterfly_bwd"):
+        for name in ("gs_diagonal_bwd", "gs_dense_bwd", "gs_dense_bwd_tiled", "gs_monarch_bwd", "gs_butterfly_bwd"):
             fn = getattr(lib, name)
             fn.argtypes = [ctypes.POINTER(GsBwdArgs), ctypes.c_void_p]
             fn.restype = ctypes.c_int

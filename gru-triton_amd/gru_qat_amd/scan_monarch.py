@@ -26,7 +26,7 @@ from typing import Any, Optional, Tuple, cast
 import torch
 
 from . import _lib
-from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
+from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32, save_gh_default
 
 
 def extract_monarch_factors(cell: Any) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -156,9 +156,16 @@ gru_scan_monarch_backward_triton = gru_scan_monarch_backward
 
 
 class GRUScanMonarchFunction(torch.autograd.Function):
-    """autograd wrapper; ``save_gh`` (no reference counterpart; default:
-    whether any input needs a gradient) asks the forward to store gh for the
-    backward where ``monarch_saves_gh`` allows it."""
+    """autograd wrapper; ``save_gh`` (no reference counterpart) asks the
+    forward to store gh for the backward where ``monarch_saves_gh`` allows it;
+    it is decided when ``apply`` is called, where the grad mode is still
+    visible (by default ``save_gh_default``)."""
+
+    @classmethod
+    def apply(cls, *args, **kwargs):  # type: ignore[override]
+        if len(args) == 7:  # without save_gh
+            args = (*args, save_gh_default(*args[:4], args[6]))
+        return super().apply(*args, **kwargs)
 
     @staticmethod
     def forward(ctx: Any, gi, h0, Wh_struct, bh_cat, h_in_quant, h_out_quant, Wh_struct2,  # type: ignore[override]
@@ -197,7 +204,6 @@ def gru_scan_monarch(
     Wh_struct2: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Differentiable Monarch-hidden GRU scan; returns out [T, B, H]."""
-    wants = torch.is_grad_enabled() and any(
-        isinstance(t, torch.Tensor) and t.requires_grad for t in (gi, h0, Wh_struct, bh_cat, Wh_struct2))
+    wants = save_gh_default(gi, h0, Wh_struct, bh_cat, Wh_struct2)
     return cast(torch.Tensor, GRUScanMonarchFunction.apply(gi, h0, Wh_struct, bh_cat, h_in_quant, h_out_quant,
                                                            Wh_struct2, wants))

@@ -40,8 +40,9 @@
  *
  * Reference interfaces replaced (LarocheC/gru-triton, src/gru_qat/triton_kernels/):
  *   gs_dense_fwd     <- scan.py:76-210 (gru_scan_fwd_persistent_kernel), launched by
- *                       gru_scan_forward_persistent scan.py:213-293 and, with the same
- *                       contract, gru_scan_forward scan.py:1688-1765
+ *                       gru_scan_forward_persistent scan.py:213-293
+ *   gs_dense_fwd_tiled <- scan.py:755-913 (gru_scan_fwd_kernel, barrier-free), launched by
+ *                       gru_scan_forward scan.py:1688-1765
  *   gs_diagonal_fwd  <- scan_diagonal.py:127-223, launched by scan_diagonal.py:226-282
  *   gs_monarch_fwd   <- scan_monarch.py:130-291, launched by scan_monarch.py:320-406
  *                       (w2 != NULL selects the two-factor form, which has no
@@ -61,7 +62,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 3
+#define GS_ABI_VERSION 4
 
 #define GS_OK 0
 #define GS_ERR_INVALID (-1)  /* bad pointer, shape, stride or quant parameter (Python: ValueError) */
@@ -79,6 +80,9 @@ extern "C" {
  * gs_hidden_map_dense(GS_KIND_CIRCULANT) writes them, gs_dense_fwd / gs_dense_bwd run the
  * scan, and gs_hidden_map_grad folds the dense weight gradient back onto col. */
 #define GS_KIND_CIRCULANT 4
+/* Size queries only (gs_workspace_bytes, gs_bwd_workspace_bytes, gs_bwd_scratch_bytes): the
+ * batch-tiled dense entry points gs_dense_fwd_tiled / gs_dense_bwd_tiled. */
+#define GS_KIND_DENSE_TILED 5
 
 /* Frozen per-tensor symmetric fake-quant: q = clamp(rint(x / scale), qmin, qmax) * scale,
  * with the IEEE quotient and round-half-to-even. enabled == 0 turns it off. When
@@ -125,7 +129,22 @@ typedef struct gs_args {
                      scan_monarch.py:409-884).                                                  */
 } gs_args;
 
+/* Dense forward. H <= 1024: the persistent kernel (Wh resident in registers, the state
+ * exchanged between workgroups every step, a workspace of gs_workspace_bytes() bytes).
+ * 1024 < H <= 8192: the batch-tiled kernel of gs_dense_fwd_tiled (same results,
+ * no workspace: gs_workspace_bytes() returns 0). */
 int gs_dense_fwd(const gs_args* args, hipStream_t stream);
+
+/* Barrier-free dense forward (reference gru_scan_fwd_kernel, scan.py:755-913, launched
+ * by gru_scan_forward, scan.py:1688-1765): a 1-D grid over tiles of up to 4 batch rows,
+ * each workgroup running every step of its rows and reading Wh from memory each step,
+ * so no workgroup waits for another: no co-residency requirement, no workspace
+ * (workspace and fault_mirror are ignored), no poll bound. 1 <= H <= 8192.
+ * Same products and gate arithmetic as gs_dense_fwd, so at H <= 1024 the two return
+ * bit-identical outputs; gs_dense_fwd is the faster of the two there (each step here
+ * streams all 3 H^2 weights through one CU). gh_save as for gs_dense_fwd. */
+int gs_dense_fwd_tiled(const gs_args* args, hipStream_t stream);
+
 int gs_diagonal_fwd(const gs_args* args, hipStream_t stream);
 int gs_monarch_fwd(const gs_args* args, hipStream_t stream);
 int gs_butterfly_fwd(const gs_args* args, hipStream_t stream);
@@ -215,14 +234,28 @@ int gs_diagonal_bwd(const gs_bwd_args* args, hipStream_t stream);
  * (so_t == B * so_b). Needs a workspace of gs_bwd_workspace_bytes(GS_KIND_DENSE,
  * args) bytes, 256-byte aligned, zeroed before its first use (like the
  * forward's, it may be shared with forward launches on the same stream), and
- * gs_bwd_scratch_bytes() bytes of scratch. */
+ * gs_bwd_scratch_bytes() bytes of scratch. H <= 1024: the reverse recurrence
+ * runs on the persistent kernel; 1024 < H <= 8192: on the batch-tiled kernel of
+ * gs_dense_bwd_tiled (no workspace; gs_bwd_workspace_bytes() returns 0). */
 int gs_dense_bwd(const gs_bwd_args* args, hipStream_t stream);
 
+/* Barrier-free dense backward (reference gru_scan_backward_triton, scan.py:1355-1447,
+ * kernel gru_scan_bwd_kernel, scan.py:916-1352): the passes and products of
+ * gs_dense_bwd with the reverse recurrence on a 1-D grid over tiles of batch rows
+ * that never wait for each other (Wh transposed once into the scratch, then read
+ * from memory every step). No workspace (gs_bwd_workspace_bytes(GS_KIND_DENSE_TILED)
+ * is 0), gs_bwd_scratch_bytes(GS_KIND_DENSE_TILED, args) bytes of scratch,
+ * 1 <= H <= 8192. Gradients bit-identical to gs_dense_bwd's at H <= 1024. */
+int gs_dense_bwd_tiled(const gs_bwd_args* args, hipStream_t stream);
+
 /* Monarch and butterfly backward (reference scan_monarch.py:409-884 and
- * scan_butterfly.py:462-1075). Both hidden maps are linear in q_in(h), so the
- * map is materialized as a [3H, H] matrix and run through the dense backward;
- * its [3H, H] gradient is then carried onto the structured parameters
- * (dw_part, and dw2_part for a two-factor Monarch). H <= 1024. */
+ * scan_butterfly.py:462-1075). A single-factor Monarch with blksz 16, 32, 64 or
+ * 128 and a butterfly with one chain at 2^log_n in {256, 512, 1024} run
+ * block-local / stage-wise kernels. Otherwise the hidden map, linear in q_in(h),
+ * is materialized as a [3H, H] matrix and run through the dense backward (its
+ * recurrence persistent up to H = 1024, batch-tiled beyond), and its [3H, H]
+ * gradient is carried onto the structured parameters (dw_part, and dw2_part for
+ * a two-factor Monarch): H <= 8192 for Monarch, 2^log_n <= 4096 for butterfly. */
 int gs_monarch_bwd(const gs_bwd_args* args, hipStream_t stream);
 int gs_butterfly_bwd(const gs_bwd_args* args, hipStream_t stream);
 

@@ -203,8 +203,21 @@ def test_bwd_workspace_sizes():
     a.log_n = 11  # stage-wise kernels cover N <= 1024: the materialized path needs the dense core
     assert lib.gs_bwd_workspace_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) == ws
     assert lib.gs_bwd_scratch_bytes(_lib.KIND_BUTTERFLY, ctypes.byref(a)) > scratch
-    a = _bwd_args(T=2, B=3, H=2048)
+    # the batch-tiled recurrence: no workspace, the dense scratch plus Wh transposed
+    a = _bwd_args(T=T, B=B, H=H)
+    assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE_TILED, ctypes.byref(a)) == 0
+    assert lib.gs_bwd_scratch_bytes(_lib.KIND_DENSE_TILED, ctypes.byref(a)) == scratch + al(3 * H * H * 4)
+    # above H = 1024 the dense entry point takes the batch-tiled recurrence itself
+    T2, B2, H2 = 2, 3, 2048
+    a = _bwd_args(T=T2, B=B2, H=H2)
+    tiled = (al(T2 * B2 * 3 * H2 * 4) + 5 * al(T2 * B2 * H2 * 4) + al(1 * B2 * 3 * H2 * 4)
+             + al(3 * H2 * H2 * 4))  # K = T B = 6 allows no dWh split
+    assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == 0
+    assert lib.gs_bwd_scratch_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == tiled
+    assert lib.gs_bwd_scratch_bytes(_lib.KIND_DENSE_TILED, ctypes.byref(a)) == tiled
+    a = _bwd_args(T=2, B=3, H=8193)
     assert lib.gs_bwd_workspace_bytes(_lib.KIND_DENSE, ctypes.byref(a)) == _lib.GS_ERR_INVALID
+    assert b"8192" in lib.gs_last_error()
 
 
 def test_dense_bwd_rejects_missing_scratch():
@@ -406,14 +419,36 @@ def test_monarch_gh_save_rules():
     assert not monarch_saves_gh(1 << 16, 1 << 14, 8, 64, False)
 
 
-def test_dense_function_saves_gh_only_under_grad_mode():
-    """gru_scan_persistent asks its Function to store gh only when a gradient
-    will be taken: under torch.no_grad() needs_input_grad still reads True for
-    leaves that require grad, so the wrapper passes the grad mode in."""
+def test_dense_function_saves_gh_only_under_grad_mode(monkeypatch):
+    """The scan Functions store gh only when a gradient will be taken and the
+    switch is on: under torch.no_grad() needs_input_grad still reads True for
+    leaves that require grad, so the choice is made where apply is called,
+    also for the reference's six-argument form."""
+    from gru_qat_amd import _common as C
     from gru_qat_amd import scan as S
 
     x = torch.ones(2, requires_grad=True)
-    assert S._wants_grad(x, torch.ones(2))
+    assert C.save_gh_default(x, torch.ones(2))
     with torch.no_grad():
-        assert not S._wants_grad(x)
-    assert not S._wants_grad(torch.ones(2), torch.ones(3))
+        assert not C.save_gh_default(x)
+    assert not C.save_gh_default(torch.ones(2), torch.ones(3))
+    C.set_save_gh(False)
+    try:
+        assert not C.save_gh_default(x)
+    finally:
+        C.set_save_gh(True)
+
+    seen = []
+
+    def fake_forward(ctx, tiled, gi, h0, Wh_cat, bh_cat, hin, hout, save_gh):
+        seen.append((tiled, save_gh))
+        return gi.detach().clone()
+
+    monkeypatch.setattr(S, "_function_forward", fake_forward)
+    gi = torch.ones(1, 1, 3, requires_grad=True)
+    args = (gi, torch.zeros(1, 1), torch.zeros(3, 1), torch.zeros(3), None, None)
+    S.GRUScanPersistentFunction.apply(*args)
+    with torch.no_grad():
+        S.GRUScanFunction.apply(*args)
+    S.GRUScanFunction.apply(*args, False)
+    assert seen == [(False, True), (True, False), (True, False)]
