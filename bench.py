@@ -20,6 +20,8 @@ Per kind:
   kernel_ms    average device duration of one launch, from HIP events around
                each launch while the queue is kept ahead of the GPU, so host
                overhead is not counted (this feeds the roofline);
+  host_us_per_call  host time of one call with the queue kept ahead of the
+               GPU (wrapper, C entry point and HIP launch; best of 3 x 50);
   roofline     algorithmic bytes or FLOPs per launch / kernel_ms against the
                MI355X peak (HBM 8 TB/s; fp32 MFMA 157.3 TFLOP/s);
   cpu_baseline the oracle (the reference's per-step PyTorch CPU path) timed on
@@ -120,6 +122,18 @@ def time_kind(idx: int, steps: int, warmup: int, dev) -> dict:
         durs += [a.elapsed_time(b) for a, b in ev]
         done += n
     kernel_ms = statistics.mean(durs)
+
+    # Host time per call: the same calls with the queue kept ahead of the GPU,
+    # timed on the host only (what the wrapper, the C entry point and the HIP
+    # launch cost the caller's thread).
+    host = []
+    for _ in range(3):
+        torch.cuda._sleep(int(2e7))
+        t0 = time.perf_counter()
+        for _ in range(50):
+            run_config(cfg)
+        host.append((time.perf_counter() - t0) * 1e6 / 50)
+        torch.cuda.synchronize(dev)
     T, B, H = SHAPES[idx]
     return {
         "name": NAMES[idx],
@@ -127,6 +141,7 @@ def time_kind(idx: int, steps: int, warmup: int, dev) -> dict:
         "ms_per_step": round(wall_ms, 5),
         "kernel_ms": round(kernel_ms, 5),
         "kernel_ms_median": round(statistics.median(durs), 5),
+        "host_us_per_call": round(min(host), 2),
         "tokens_per_s": round(T * B / (wall_ms * 1e-3), 1),
         "kernel_tokens_per_s": round(T * B / (kernel_ms * 1e-3), 1),
         "roofline": roofline(idx, kernel_ms),
@@ -360,6 +375,7 @@ def main() -> int:
                                f"H={r['shape']['H']}", "kind": r["name"], **r["shape"]},
         "tokens_per_s": r["tokens_per_s"],
         "kernel_ms": r["kernel_ms"],
+        "host_us_per_call": r["host_us_per_call"],
         "roofline": r["roofline"],
         "cpu_baseline": cpu.get(head),
         "kinds": {str(k): v for k, v in results.items()},

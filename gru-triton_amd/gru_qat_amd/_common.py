@@ -37,6 +37,26 @@ def require_cuda(who: str, **tensors: torch.Tensor) -> None:
         raise ValueError(f"{who}: all tensors must be on {dev}; got {other}")
 
 
+_F32 = torch.float32
+
+
+def cuda_f32(*tensors) -> bool:
+    """Whether every argument is an fp32 tensor on one CUDA device: the common
+    case, checked with integer device ordinals (building torch.device objects
+    and keyword dicts costs the host a few microseconds a call). Callers run
+    require_cuda and require_f32 when it is False, for their exact errors."""
+    try:
+        d = tensors[0].get_device()
+        if d < 0:
+            return False
+        for t in tensors:
+            if t.dtype is not _F32 or t.get_device() != d:
+                return False
+    except AttributeError:
+        return False
+    return True
+
+
 def require_f32(who: str, **tensors: torch.Tensor) -> None:
     for k, v in tensors.items():
         if v.dtype != torch.float32:
@@ -57,6 +77,11 @@ def split_gi(who: str, gi: torch.Tensor) -> Tuple[int, int, int]:
 
 
 def check_common(who: str, gi: torch.Tensor, h0: torch.Tensor, bh_cat: torch.Tensor) -> Tuple[int, int, int]:
+    s = gi.shape
+    if len(s) == 3:  # fast path: every check passes
+        T, B, G3 = s
+        if T > 0 and B > 0 and G3 > 0 and G3 % 3 == 0 and h0.shape == (B, G3 // 3) and bh_cat.shape == (G3,):
+            return T, B, G3 // 3
     T, B, H = split_gi(who, gi)
     if tuple(h0.shape) != (B, H):
         raise ValueError(f"h0 shape must be (B, H)=({B}, {H}); got {tuple(h0.shape)}")

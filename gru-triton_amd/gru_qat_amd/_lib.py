@@ -10,6 +10,7 @@ from __future__ import annotations
 import contextlib
 import ctypes
 import os
+import struct
 import threading
 from typing import Callable, Optional, Tuple
 
@@ -598,54 +599,103 @@ def _check_gh(name: str, gh: torch.Tensor, gi: torch.Tensor) -> None:
                          f"got {tuple(gh.shape)} {gh.dtype} on {gh.device}")
 
 
+# gs_args packed by one call: 9 pointer / byte-count words, 12 int64 sizes and
+# strides, the two gs_quant (int32, float, int32, int32), gh_save. The layout
+# is that of the ctypes GsArgs above (checked bytewise by the CPU tests);
+# building a ctypes Structure field by field cost the host about 4 us a call.
+GS_ARGS = struct.Struct("<9Q12q" "ifii" "ifii" "Q")
+_QOFF = (0, 1.0, -(2**31), 2**31 - 1)
+_TAGGED = (KIND_DENSE, KIND_MONARCH)
+_RAW_FN: dict = {}
+_NEED: dict = {}  # workspace bytes per (kind, sizes, quant) of the tagged kinds
+
+
+def _raw_entry(lib: ctypes.CDLL, fn_name: str):
+    """The entry point as a function of (packed gs_args bytes, stream handle)."""
+    fn = _RAW_FN.get(fn_name)
+    if fn is None:
+        fn = lib[fn_name]  # an independent function object: its argtypes do not touch getattr(lib, ...)
+        fn.argtypes = [ctypes.c_char_p, ctypes.c_void_p]
+        fn.restype = ctypes.c_int
+        _RAW_FN[fn_name] = fn
+    return fn
+
+
+def _qfields(q: QuantTuple, name: str) -> tuple:
+    if q is None:
+        return _QOFF
+    try:
+        scale, qmin, qmax = q
+    except (TypeError, ValueError):
+        raise ValueError(f"{name} must be None or a (scale, qmin, qmax) tuple; got {q!r}") from None
+    return (1, float(scale), int(qmin), int(qmax))
+
+
 def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,
            w2: Optional[torch.Tensor], bh: torch.Tensor, out: torch.Tensor,
            h_in_quant: QuantTuple, h_out_quant: QuantTuple, nblocks: int = 0, blksz: int = 0,
-           log_n: int = 0, bfly_nblocks: int = 0, gh_save: Optional[torch.Tensor] = None) -> None:
+           log_n: int = 0, bfly_nblocks: int = 0, gh_save: Optional[torch.Tensor] = None,
+           contiguous: bool = False) -> None:
     """Fill gs_args from fp32 device tensors and call the entry point on the
-    current torch stream of gi's device.
+    current torch stream of gi's device. contiguous: the caller guarantees that
+    gi, h0 and out are contiguous (the wrappers make them so), which fixes their
+    strides without reading them.
 
-    Kept short on the host: one positional struct construction, the workspace
-    size query only for the kinds whose workspace depends on the shape (dense
-    and Monarch), and the device switch only when gi's device is not current.
-    The short scans (diagonal, single-factor Monarch) take about as long on the
-    GPU as a launch does on the host."""
+    Kept short on the host: the arguments packed by one struct call, the
+    workspace size query once per shape for the kinds whose workspace depends
+    on it (dense and Monarch), and the device switch only when gi's device is
+    not current. The short scans (diagonal, single-factor Monarch) take about
+    as long on the GPU as a launch does on the host."""
     lib = _lib if _lib is not None else load()
-    T, B, threeH = gi.shape
+    T, B, G3 = gi.shape
+    H = G3 // 3
     if gh_save is not None:
         _check_gh("gh_save", gh_save, gi)
-    a = GsArgs(gi.data_ptr(), h0.data_ptr(), w.data_ptr(), w2.data_ptr() if w2 is not None else None,
-               bh.data_ptr(), out.data_ptr(), None, 0, None, T, B, threeH // 3, gi.stride(0), gi.stride(1),
-               h0.stride(0), out.stride(0), out.stride(1), nblocks, blksz, log_n, bfly_nblocks,
-               make_quant(h_in_quant, "h_in_quant"), make_quant(h_out_quant, "h_out_quant"),
-               gh_save.data_ptr() if gh_save is not None else None)
-    tagged = kind in (KIND_DENSE, KIND_MONARCH)
-    if tagged:
-        need = lib.gs_workspace_bytes(kind, ctypes.byref(a))
-        if need < 0:
-            raise_for(int(need), lib)
+    qi = _qfields(h_in_quant, "h_in_quant")
+    qo = _qfields(h_out_quant, "h_out_quant")
+    ptrs = (gi.data_ptr(), h0.data_ptr(), w.data_ptr(), w2.data_ptr() if w2 is not None else 0, bh.data_ptr(),
+            out.data_ptr())
+    if contiguous:
+        sizes = (T, B, H, B * G3, G3, H, B * H, H, nblocks, blksz, log_n, bfly_nblocks)
     else:
-        need = 0  # the diagonal and butterfly forwards use no workspace beyond the cached minimum
+        sg, so = gi.stride(), out.stride()
+        sizes = (T, B, H, sg[0], sg[1], h0.stride(0), so[0], so[1], nblocks, blksz, log_n, bfly_nblocks)
+    gh_ptr = gh_save.data_ptr() if gh_save is not None else 0
+    tagged = kind in _TAGGED
+    need = 0  # the diagonal and butterfly forwards use no workspace beyond the cached minimum
+    if tagged:
+        key = (kind, sizes, w2 is None, qi, qo, gh_ptr == 0)
+        need = _NEED.get(key)
+        if need is None:
+            a = GS_ARGS.pack(*ptrs, 0, 0, 0, *sizes, *qi, *qo, gh_ptr)
+            fn = lib["gs_workspace_bytes"]
+            fn.argtypes = [ctypes.c_int, ctypes.c_char_p]
+            fn.restype = ctypes.c_int64
+            need = int(fn(kind, a))
+            if need < 0:
+                raise_for(need, lib)
+            _NEED[key] = need
     dev = gi.device
     if dev.index == torch.cuda.current_device():
-        rc = _launch_current(lib, fn_name, a, dev, need, T if tagged else 0)
+        rc = _launch_current(lib, fn_name, ptrs, sizes, qi, qo, gh_ptr, dev, need, T if tagged else 0)
     else:
         with torch.cuda.device(dev):
-            rc = _launch_current(lib, fn_name, a, dev, need, T if tagged else 0)
+            rc = _launch_current(lib, fn_name, ptrs, sizes, qi, qo, gh_ptr, dev, need, T if tagged else 0)
     raise_for(rc, lib)
 
 
-def _launch_current(lib: ctypes.CDLL, fn_name: str, a: "GsArgs", dev: torch.device, need: int, steps: int) -> int:
+def _launch_current(lib: ctypes.CDLL, fn_name: str, ptrs: tuple, sizes: tuple, qi: tuple, qo: tuple, gh_ptr: int,
+                    dev: torch.device, need: int, steps: int) -> int:
     handle = current_stream_handle(dev)
-    ws = workspace(dev, handle, int(need), steps=steps)
-    a.workspace = ws.data_ptr()
-    a.workspace_bytes = ws.numel()
+    ws = workspace(dev, handle, need, steps=steps)
+    mirror = 0
     if steps:  # a persistent kernel: fault mirror and cross-stream order
         m = _mirror(dev, handle)
         _raise_if_faulted(m, fn_name)
         _order_after_previous(dev, handle, lambda: torch.cuda.current_stream(dev))
-        a.fault_mirror = m[0].data_ptr()
-    return _entry(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
+        mirror = m[0].data_ptr()
+    a = GS_ARGS.pack(*ptrs, ws.data_ptr(), ws.numel(), mirror, *sizes, *qi, *qo, gh_ptr)
+    return _raw_entry(lib, fn_name)(a, handle)
 
 
 def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,

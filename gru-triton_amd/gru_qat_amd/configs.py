@@ -129,24 +129,32 @@ def make_config(idx: int, device: Optional[torch.device] = None, seed: int = 0,
     return d
 
 
+_FORWARDS: Dict[str, object] = {}
+
+
+def _forwards() -> Dict[str, object]:
+    # imported once, on first use (the scan modules load the library); an
+    # import statement per call cost the benchmark loop about 1 us each
+    if not _FORWARDS:
+        from .scan import gru_scan_forward_persistent
+        from .scan_butterfly import gru_scan_butterfly_forward
+        from .scan_circulant import gru_scan_circulant_forward
+        from .scan_diagonal import gru_scan_diagonal_forward
+        from .scan_monarch import gru_scan_monarch_forward
+
+        _FORWARDS.update(dense=gru_scan_forward_persistent, diagonal=gru_scan_diagonal_forward,
+                         monarch=gru_scan_monarch_forward, butterfly=gru_scan_butterfly_forward,
+                         circulant=gru_scan_circulant_forward)
+    return _FORWARDS
+
+
 def run_config(d: Dict[str, object]) -> torch.Tensor:
     """Runs the HIP scan of a config dict (tensors on a GPU); returns out."""
-    from .scan import gru_scan_forward_persistent
-    from .scan_butterfly import gru_scan_butterfly_forward
-    from .scan_circulant import gru_scan_circulant_forward
-    from .scan_diagonal import gru_scan_diagonal_forward
-    from .scan_monarch import gru_scan_monarch_forward
-
-    kw = dict(h_in_quant=d["h_in_quant"], h_out_quant=d["h_out_quant"])
     kind = d["kind"]
-    if kind == "dense":
-        return gru_scan_forward_persistent(d["gi"], d["h0"], d["w"], d["bh"], **kw)
-    if kind == "diagonal":
-        return gru_scan_diagonal_forward(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    fwd = _forwards().get(kind)  # type: ignore[attr-defined]
+    if fwd is None:
+        raise ValueError(kind)
     if kind == "monarch":
-        return gru_scan_monarch_forward(d["gi"], d["h0"], d["w"], d["bh"], Wh_struct2=d.get("w2"), **kw)
-    if kind == "butterfly":
-        return gru_scan_butterfly_forward(d["gi"], d["h0"], d["w"], d["bh"], **kw)
-    if kind == "circulant":
-        return gru_scan_circulant_forward(d["gi"], d["h0"], d["w"], d["bh"], **kw)
-    raise ValueError(kind)
+        return fwd(d["gi"], d["h0"], d["w"], d["bh"], Wh_struct2=d.get("w2"), h_in_quant=d["h_in_quant"],
+                   h_out_quant=d["h_out_quant"])
+    return fwd(d["gi"], d["h0"], d["w"], d["bh"], h_in_quant=d["h_in_quant"], h_out_quant=d["h_out_quant"])

@@ -38,7 +38,7 @@ from typing import Any, Optional, cast
 import torch
 
 from . import _lib
-from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32, save_gh_default
+from ._common import QuantTuple, check_common, check_quant, cuda_f32, require_cuda, require_f32, save_gh_default
 
 
 def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.Tensor,
@@ -47,10 +47,11 @@ def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.T
     """Runs gs_dense_fwd (tiled: gs_dense_fwd_tiled); with gh_save ([T, B, 3H]
     contiguous fp32) the kernel also stores every step's q_in(h_{t-1}) Wh^T (gh_t
     without bh) there for the backward."""
-    require_cuda(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
-    require_f32(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
+    if not cuda_f32(gi, h0, Wh_cat, bh_cat):
+        require_cuda(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
+        require_f32(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
     T, B, H = check_common(who, gi, h0, bh_cat)
-    if tuple(Wh_cat.shape) != (3 * H, H):
+    if Wh_cat.shape != (3 * H, H):
         raise ValueError(f"Wh_cat shape must be (3H, H)=({3 * H}, {H}); got {tuple(Wh_cat.shape)}")
     h_in_quant = check_quant(h_in_quant, "h_in_quant")
     h_out_quant = check_quant(h_out_quant, "h_out_quant")
@@ -61,10 +62,10 @@ def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.T
     out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
     if tiled:
         _lib.launch(_lib.KIND_DENSE_TILED, "gs_dense_fwd_tiled", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat,
-                    out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, gh_save=gh_save)
+                    out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, gh_save=gh_save, contiguous=True)
     else:
         _lib.launch(_lib.KIND_DENSE, "gs_dense_fwd", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat, out=out,
-                    h_in_quant=h_in_quant, h_out_quant=h_out_quant, gh_save=gh_save)
+                    h_in_quant=h_in_quant, h_out_quant=h_out_quant, gh_save=gh_save, contiguous=True)
     return out
 
 

@@ -18,7 +18,7 @@ from typing import Any, Tuple, cast
 import torch
 
 from . import _lib
-from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
+from ._common import QuantTuple, check_common, check_quant, cuda_f32, require_cuda, require_f32
 
 
 def extract_butterfly_twiddles(cell: Any) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -53,8 +53,9 @@ def check_twiddles(twiddles: torch.Tensor, H: int) -> Tuple[int, int]:
 
 
 def _forward(fn_name: str, who: str, gi, h0, twiddles, bh_cat, h_in_quant, h_out_quant) -> torch.Tensor:
-    require_cuda(who, gi=gi, h0=h0, twiddles=twiddles, bh_cat=bh_cat)
-    require_f32(who, gi=gi, h0=h0, twiddles=twiddles, bh_cat=bh_cat)
+    if not cuda_f32(gi, h0, twiddles, bh_cat):
+        require_cuda(who, gi=gi, h0=h0, twiddles=twiddles, bh_cat=bh_cat)
+        require_f32(who, gi=gi, h0=h0, twiddles=twiddles, bh_cat=bh_cat)
     T, B, H = check_common(who, gi, h0, bh_cat)
     nblocks, log_n = check_twiddles(twiddles, H)
     h_in_quant = check_quant(h_in_quant, "h_in_quant")
@@ -62,7 +63,7 @@ def _forward(fn_name: str, who: str, gi, h0, twiddles, bh_cat, h_in_quant, h_out
     gi, h0, twiddles, bh_cat = gi.contiguous(), h0.contiguous(), twiddles.contiguous(), bh_cat.contiguous()
     out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
     _lib.launch(_lib.KIND_BUTTERFLY, fn_name, gi=gi, h0=h0, w=twiddles, w2=None, bh=bh_cat, out=out,
-                h_in_quant=h_in_quant, h_out_quant=h_out_quant, log_n=log_n, bfly_nblocks=nblocks)
+                h_in_quant=h_in_quant, h_out_quant=h_out_quant, log_n=log_n, bfly_nblocks=nblocks, contiguous=True)
     return out
 
 

@@ -14,7 +14,7 @@ from typing import Any, Tuple, cast
 import torch
 
 from . import _lib
-from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
+from ._common import QuantTuple, check_common, check_quant, cuda_f32, require_cuda, require_f32
 
 
 def extract_diagonal_factors(cell: Any) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -41,17 +41,18 @@ def gru_scan_diagonal_forward(
     **_ignored_tiling: Any,
 ) -> torch.Tensor:
     who = "gru_scan_diagonal_forward"
-    require_cuda(who, gi=gi, h0=h0, Wh_diag=Wh_diag, bh_cat=bh_cat)
-    require_f32(who, gi=gi, h0=h0, Wh_diag=Wh_diag, bh_cat=bh_cat)
+    if not cuda_f32(gi, h0, Wh_diag, bh_cat):
+        require_cuda(who, gi=gi, h0=h0, Wh_diag=Wh_diag, bh_cat=bh_cat)
+        require_f32(who, gi=gi, h0=h0, Wh_diag=Wh_diag, bh_cat=bh_cat)
     T, B, H = check_common(who, gi, h0, bh_cat)
-    if tuple(Wh_diag.shape) != (3, H):
+    if Wh_diag.shape != (3, H):
         raise ValueError(f"Wh_diag shape must be (3, H)=(3, {H}); got {tuple(Wh_diag.shape)}")
     h_in_quant = check_quant(h_in_quant, "h_in_quant")
     h_out_quant = check_quant(h_out_quant, "h_out_quant")
     gi, h0, Wh_diag, bh_cat = gi.contiguous(), h0.contiguous(), Wh_diag.contiguous(), bh_cat.contiguous()
     out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
     _lib.launch(_lib.KIND_DIAGONAL, "gs_diagonal_fwd", gi=gi, h0=h0, w=Wh_diag, w2=None, bh=bh_cat,
-                out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant)
+                out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, contiguous=True)
     return out
 
 

@@ -26,7 +26,7 @@ from typing import Any, Optional, Tuple, cast
 import torch
 
 from . import _lib
-from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32, save_gh_default
+from ._common import QuantTuple, check_common, check_quant, cuda_f32, require_cuda, require_f32, save_gh_default
 
 
 def extract_monarch_factors(cell: Any) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -85,11 +85,13 @@ def gru_scan_monarch_forward(
     where ``monarch_saves_gh`` holds): a contiguous fp32 [T, B, 3H] tensor
     the kernel fills with each step's bias-free q_in(h_{t-1}) W^T."""
     who = "gru_scan_monarch_forward"
-    tensors = dict(gi=gi, h0=h0, Wh_struct=Wh_struct, bh_cat=bh_cat)
-    if Wh_struct2 is not None:
-        tensors["Wh_struct2"] = Wh_struct2
-    require_cuda(who, **tensors)
-    require_f32(who, **tensors)
+    if not (cuda_f32(gi, h0, Wh_struct, bh_cat) if Wh_struct2 is None
+            else cuda_f32(gi, h0, Wh_struct, bh_cat, Wh_struct2)):
+        tensors = dict(gi=gi, h0=h0, Wh_struct=Wh_struct, bh_cat=bh_cat)
+        if Wh_struct2 is not None:
+            tensors["Wh_struct2"] = Wh_struct2
+        require_cuda(who, **tensors)
+        require_f32(who, **tensors)
     T, B, H = check_common(who, gi, h0, bh_cat)
     nblocks, blksz = _check_struct("Wh_struct", Wh_struct, H)
     if Wh_struct2 is not None:
@@ -103,7 +105,7 @@ def gru_scan_monarch_forward(
     out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
     _lib.launch(_lib.KIND_MONARCH, "gs_monarch_fwd", gi=gi, h0=h0, w=Wh_struct, w2=Wh_struct2, bh=bh_cat,
                 out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, nblocks=nblocks, blksz=blksz,
-                gh_save=gh_save)
+                gh_save=gh_save, contiguous=True)
     return out
 
 

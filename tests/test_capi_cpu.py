@@ -452,3 +452,32 @@ def test_dense_function_saves_gh_only_under_grad_mode(monkeypatch):
         S.GRUScanFunction.apply(*args)
     S.GRUScanFunction.apply(*args, False)
     assert seen == [(False, True), (True, False), (True, False)]
+
+
+def test_packed_args_match_the_ctypes_layout():
+    """launch() packs gs_args with one struct call; the bytes must be those of
+    the ctypes GsArgs (the C layout) for the same field values."""
+    a = _lib.GsArgs(1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21,
+                    _lib.GsQuant(1, 0.25, -7, 9), _lib.GsQuant(0, 1.0, -(2**31), 2**31 - 1), 22)
+    b = _lib.GS_ARGS.pack(1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15, 16, 17, 18, 19, 20, 21,
+                          1, 0.25, -7, 9, *_lib._QOFF, 22)
+    assert _lib.GS_ARGS.size == ctypes.sizeof(_lib.GsArgs)
+    assert bytes(a) == b
+    assert _lib._qfields((0.25, -7, 9), "q") == (1, 0.25, -7, 9)
+    with pytest.raises(ValueError, match="tuple"):
+        _lib._qfields(0.5, "h_in_quant")
+
+
+def test_fast_checks_fall_back_to_the_exact_errors():
+    from gru_qat_amd._common import check_common, cuda_f32
+
+    assert not cuda_f32(torch.zeros(2), torch.zeros(2))  # CPU tensors
+    assert not cuda_f32(torch.zeros(2), None)
+    gi, h0, bh = torch.zeros(4, 3, 6), torch.zeros(3, 2), torch.zeros(6)
+    assert check_common("f", gi, h0, bh) == (4, 3, 2)
+    with pytest.raises(ValueError, match="h0 shape"):
+        check_common("f", gi, torch.zeros(3, 3), bh)
+    with pytest.raises(ValueError, match="bh_cat shape"):
+        check_common("f", gi, h0, torch.zeros(5))
+    with pytest.raises(ValueError, match="T must be > 0"):
+        check_common("f", torch.zeros(0, 3, 6), h0, bh)
