@@ -292,23 +292,40 @@ struct Ctrl {
 
 // fval of the launch whose wait gave up (0: none yet)
 __host__ __device__ __forceinline__ uint32_t* ctrl_fault(const Ctrl& c) { return c.w; }
-// poll bound override: 0 (a zeroed workspace) means kSpinLimit
+// poll bound override: bits 0-23 the bound (0, as in a zeroed workspace: kSpinLimit),
+// bits 24-31 a forced-late step (launch_ctrl)
 __host__ __device__ __forceinline__ uint32_t* ctrl_spin(const Ctrl& c) { return c.w + 16; }
 // workgroups that have finished this launch
 __host__ __device__ __forceinline__ uint32_t* ctrl_exit_count(const Ctrl& c) { return c.w + 32; }
 // tags of this launch are tag_base + t + 1
 __host__ __device__ __forceinline__ uint32_t* ctrl_tag_base(const Ctrl& c) { return c.w + 48; }
 
+// The poll-bound override word (ctrl_spin) holds the bound in bits 0-23 (0:
+// kSpinLimit) and, in bits 24-31, a step F (0: none) whose exchange is forced
+// late: the waits that check it (group_on_one_xcd, which every persistent
+// kernel with XCD-local publishes runs on its first exchange, tag tag_base + 1,
+// and the split two-factor kernel's waits, poll_to_lds) treat every word of
+// tag tag_base + F as not yet arrived, so they run out at the bound and give
+// up through the kernels' own fault path. Tests set it from the host to make a
+// chosen exchange give up deterministically while every kernel still exits
+// normally. The per-step word polls of the other kernels do not check it, so
+// that their step loops carry nothing for it.
+constexpr uint32_t kBoundMask = 0xffffffu;
+
 // The kernel-side control block: the host's pointers plus this launch's fault
-// value and poll bound. The bound is kSpinLimit unless the host wrote an
-// override into the workspace (tests use a tiny one to make waits run out
-// while every kernel still exits normally).
+// value and poll bound (kSpinLimit unless the host wrote an override into the
+// workspace).
 __device__ __forceinline__ Ctrl launch_ctrl(const Ctrl& host, uint32_t base) {
   Ctrl c = host;
   c.fval = base + 1u;
-  const uint32_t o = __hip_atomic_load(ctrl_spin(host), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t o = __hip_atomic_load(ctrl_spin(host), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kBoundMask;
   c.limit = o != 0u ? o : kSpinLimit;
   return c;
+}
+
+// The forced-late step F of this launch (0: none), read from the control word.
+__device__ __forceinline__ uint32_t forced_step(const Ctrl& c) {
+  return __hip_atomic_load(ctrl_spin(c), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> 24;
 }
 
 __device__ __forceinline__ void raise_fault(const Ctrl& c) {
@@ -353,7 +370,7 @@ __device__ __forceinline__ float value_of(uint64_t w) { return __uint_as_float((
 template <int MW>
 __device__ __forceinline__ bool poll_to_lds(const Ctrl& c, const uint64_t* base, const int (&src)[MW],
                                             const int (&dst)[MW], uint32_t valid, uint32_t tag,
-                                            float* dst_lds) {
+                                            float* dst_lds, bool forced = false) {
   uint64_t v[MW];
 #pragma unroll
   for (int i = 0; i < MW; ++i) v[i] = ld_tagged(base + src[i]);
@@ -364,6 +381,7 @@ __device__ __forceinline__ bool poll_to_lds(const Ctrl& c, const uint64_t* base,
 #pragma unroll
     for (int i = 0; i < MW; ++i) pending |= (tag_of(v[i]) != tag ? 1u : 0u) << i;
     pending &= valid;
+    if (forced) pending = valid;  // forced late (launch_ctrl)
     if (pending == 0u) break;
     if (++polls > c.limit) {
       raise_fault(c);
@@ -430,9 +448,11 @@ __device__ __forceinline__ bool group_on_one_xcd(const Ctrl& c, const uint64_t* 
   const int lane = threadIdx.x & 63;
   const bool mine = lane < n;
   const uint64_t* src = words + (int64_t)(mine ? lane : 0) * stride;
+  const uint32_t f = forced_step(c);
+  const bool forced = f != 0u && tag == c.fval - 1u + f;  // forced late (launch_ctrl)
   uint64_t v = ld_tagged(src);
   uint32_t polls = 0;
-  while (__ballot(mine && tag_of(v) != tag)) {
+  while (__ballot(mine && (forced || tag_of(v) != tag))) {
     if (++polls > c.limit) {
       raise_fault(c);
       mark_dead(dead);

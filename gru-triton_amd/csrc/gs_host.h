@@ -30,7 +30,8 @@ void clear_error();
 // Workspace layout (bytes from the start):
 //   [0, 256)        control words: fault word (word 0; the fault value
 //                   tag_base + 1 of the last launch whose wait gave up),
-//                   poll bound override (word 16; 0 = the default bound),
+//                   poll bound override (word 16; bits 0-23 the bound, 0 = the
+//                   default; bits 24-31 a forced-late step, gs_device.h),
 //                   exit count (word 32), tag base (word 48); zero on first use
 //   [256, ...)      tagged exchange words (uint64), 256-byte aligned regions
 // Every launch leaves the exit count at zero and the tag base advanced, and

@@ -436,7 +436,7 @@ struct M2Params {
 // nothing.
 template <int MW, typename Map>
 __device__ __forceinline__ void stage_words(const Ctrl& c, const uint64_t* base, int words, uint32_t tag, float* lds,
-                                            Map map, bool& ok) {
+                                            Map map, bool& ok, uint32_t forced_tag) {
   const int tid = threadIdx.x, nth = blockDim.x;
   for (int c0 = 0; c0 < words && ok; c0 += MW * nth) {
     int src[MW], dst[MW];
@@ -448,7 +448,7 @@ __device__ __forceinline__ void stage_words(const Ctrl& c, const uint64_t* base,
       map(ok ? w : 0, src[i], dst[i]);
       valid |= (ok ? 1u : 0u) << i;
     }
-    ok = poll_to_lds<MW>(c, base, src, dst, valid, tag, lds);
+    ok = poll_to_lds<MW>(c, base, src, dst, valid, tag, lds, tag == forced_tag);
   }
 }
 
@@ -491,6 +491,9 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
 
   const uint32_t base = __hip_atomic_load(ctrl_tag_base(p.ctrl), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const Ctrl ctrl = launch_ctrl(p.ctrl, base);
+  // tag of the exchange forced late (launch_ctrl; none: a tag no step uses)
+  const uint32_t fstep = forced_step(ctrl);
+  const uint32_t forced_tag = fstep != 0u ? base + fstep : base;
   bool alive = true;  // no wait of this thread has given up
   const int rb_begin = gid * p.RB;
   const int rb_end = min(rb_begin + p.RB, p.nrb);
@@ -532,7 +535,7 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
           const int r = w / bs, k = w - r * bs;
           src = r * H + klo + k;
           dst = r * rs + k;
-        }, alive);
+        }, alive, forced_tag);
         if (!alive) *dead = 1;
       }
       lds_barrier();
@@ -559,7 +562,7 @@ __global__ __launch_bounds__(NT) void monarch2_split_kernel(M2Params p) {
         const int zpos = (idx % nb) * bs + idx / nb;
         src = ((gr >> 2) * Bp + (gr & 3)) * H + zpos;
         dst = gr * rs + k;
-      }, alive);
+      }, alive, forced_tag);
       if (!alive) *dead = 1;
       lds_barrier();
       const bool wg_dead2 = __builtin_amdgcn_readfirstlane(*dead) != 0;

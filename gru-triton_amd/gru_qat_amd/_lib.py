@@ -698,6 +698,13 @@ def _launch_current(lib: ctypes.CDLL, fn_name: str, ptrs: tuple, sizes: tuple, q
     return _raw_entry(lib, fn_name)(a, handle)
 
 
+# gs_bwd_args packed by one call: 12 tensor pointers, the workspace (pointer,
+# bytes), the fault mirror, the scratch (pointer, bytes), 12 int64 sizes and
+# strides, the two gs_quant, gh_saved (layout of the ctypes GsBwdArgs).
+GS_BWD_ARGS = struct.Struct("<12QQqQQq12q" "ifii" "ifii" "Q")
+_BWD_NEED: dict = {}  # (workspace, scratch) bytes per (kind, sizes, quant, optional inputs)
+
+
 def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: torch.Tensor,
                w2: Optional[torch.Tensor], bh: torch.Tensor, out: torch.Tensor, dout: torch.Tensor,
                dgi: torch.Tensor, dh0: torch.Tensor, dw_part: Optional[torch.Tensor],
@@ -708,51 +715,54 @@ def launch_bwd(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w
     """Fill gs_bwd_args from fp32 device tensors (dout, dgi, dh0 and the
     partials contiguous) and call a backward entry point on the current torch
     stream of gi's device, with the stream's cached workspace when the kind
-    needs one."""
-    lib = load()
-    T, B, threeH = gi.shape
-    a = GsBwdArgs()
-    a.gi, a.h0, a.w = gi.data_ptr(), h0.data_ptr(), w.data_ptr()
-    a.w2 = w2.data_ptr() if w2 is not None else None
-    a.bh, a.out, a.dout = bh.data_ptr(), out.data_ptr(), dout.data_ptr()
-    a.dgi, a.dh0 = dgi.data_ptr(), dh0.data_ptr()
-    a.dw_part = dw_part.data_ptr() if dw_part is not None else None
-    a.dw2_part = dw2_part.data_ptr() if dw2_part is not None else None
-    a.dbh_part = dbh_part.data_ptr()
-    a.T, a.B, a.H = T, B, threeH // 3
-    a.sg_t, a.sg_b = gi.stride(0), gi.stride(1)
-    a.sh0_b = h0.stride(0)
-    a.so_t, a.so_b = out.stride(0), out.stride(1)
-    a.nblocks, a.blksz = nblocks, blksz
-    a.log_n, a.bfly_nblocks = log_n, bfly_nblocks
-    a.q_in = make_quant(h_in_quant, "h_in_quant")
-    a.q_out = make_quant(h_out_quant, "h_out_quant")
+    needs one. The workspace and scratch sizes are queried once per shape."""
+    lib = _lib if _lib is not None else load()
+    T, B, G3 = gi.shape
     if gh_saved is not None:
         _check_gh("gh_saved", gh_saved, gi)
-    a.gh_saved = gh_saved.data_ptr() if gh_saved is not None else None
-    need = lib.gs_bwd_workspace_bytes(kind, ctypes.byref(a))
-    if need < 0:
-        raise_for(int(need), lib)
-    scratch_need = lib.gs_bwd_scratch_bytes(kind, ctypes.byref(a))
-    if scratch_need < 0:
-        raise_for(int(scratch_need), lib)
-    with on_device(gi.device):
-        handle = current_stream_handle(gi.device)
+    ptrs = (gi.data_ptr(), h0.data_ptr(), w.data_ptr(), w2.data_ptr() if w2 is not None else 0, bh.data_ptr(),
+            out.data_ptr(), dout.data_ptr(), dgi.data_ptr(), dh0.data_ptr(),
+            dw_part.data_ptr() if dw_part is not None else 0, dw2_part.data_ptr() if dw2_part is not None else 0,
+            dbh_part.data_ptr())
+    sg, so = gi.stride(), out.stride()
+    sizes = (T, B, G3 // 3, sg[0], sg[1], h0.stride(0), so[0], so[1], nblocks, blksz, log_n, bfly_nblocks)
+    qi = _qfields(h_in_quant, "h_in_quant")
+    qo = _qfields(h_out_quant, "h_out_quant")
+    gh_ptr = gh_saved.data_ptr() if gh_saved is not None else 0
+    key = (kind, sizes, w2 is None, dw_part is None, dw2_part is None, qi, qo, gh_ptr == 0)
+    needs = _BWD_NEED.get(key)
+    if needs is None:
+        a = GS_BWD_ARGS.pack(*ptrs, 0, 0, 0, 0, 0, *sizes, *qi, *qo, gh_ptr)
+        sizes_fn = []
+        for name in ("gs_bwd_workspace_bytes", "gs_bwd_scratch_bytes"):
+            fn = lib[name]
+            fn.argtypes = [ctypes.c_int, ctypes.c_char_p]
+            fn.restype = ctypes.c_int64
+            n = int(fn(kind, a))
+            if n < 0:
+                raise_for(n, lib)
+            sizes_fn.append(n)
+        needs = _BWD_NEED[key] = tuple(sizes_fn)
+    need, scratch_need = needs
+    dev = gi.device
+    with on_device(dev):
+        handle = current_stream_handle(dev)
+        ws_ptr = ws_bytes = mirror = 0
         if need > 0:
-            ws = workspace(gi.device, handle, int(need), steps=T)
-            a.workspace = ws.data_ptr()
-            a.workspace_bytes = ws.numel()
-            m = _mirror(gi.device, handle)
+            ws = workspace(dev, handle, need, steps=T)
+            ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+            m = _mirror(dev, handle)
             _raise_if_faulted(m, fn_name)
-            _order_after_previous(gi.device, handle, lambda: torch.cuda.current_stream(gi.device))
-            a.fault_mirror = m[0].data_ptr()
+            _order_after_previous(dev, handle, lambda: torch.cuda.current_stream(dev))
+            mirror = m[0].data_ptr()
         scratch = None
+        sc_ptr = 0
         if scratch_need > 0:
             # plain scratch from torch's stream-aware caching allocator
             # (allocations are 512-byte aligned); kept alive until the launch is queued
-            scratch = torch.empty((int(scratch_need),), dtype=torch.uint8, device=gi.device)
-            a.scratch = scratch.data_ptr()
-            a.scratch_bytes = scratch.numel()
-        rc = getattr(lib, fn_name)(ctypes.byref(a), ctypes.c_void_p(handle))
+            scratch = torch.empty((scratch_need,), dtype=torch.uint8, device=dev)
+            sc_ptr = scratch.data_ptr()
+        a = GS_BWD_ARGS.pack(*ptrs, ws_ptr, ws_bytes, mirror, sc_ptr, scratch_need, *sizes, *qi, *qo, gh_ptr)
+        rc = _raw_entry(lib, fn_name)(a, handle)
         del scratch
     raise_for(rc, lib)

@@ -481,3 +481,11 @@ def test_fast_checks_fall_back_to_the_exact_errors():
         check_common("f", gi, h0, torch.zeros(5))
     with pytest.raises(ValueError, match="T must be > 0"):
         check_common("f", torch.zeros(0, 3, 6), h0, bh)
+
+
+def test_packed_bwd_args_match_the_ctypes_layout():
+    vals = list(range(1, 30))
+    a = _lib.GsBwdArgs(*vals[:29], _lib.GsQuant(1, 0.5, -3, 4), _lib.GsQuant(0, 1.0, -(2**31), 2**31 - 1), 99)
+    b = _lib.GS_BWD_ARGS.pack(*vals[:29], 1, 0.5, -3, 4, *_lib._QOFF, 99)
+    assert _lib.GS_BWD_ARGS.size == ctypes.sizeof(_lib.GsBwdArgs)
+    assert bytes(a) == b

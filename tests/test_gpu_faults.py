@@ -1,14 +1,17 @@
 """A persistent scan whose bounded wait gives up is never silent.
 
-The condition is forced from the host: the test writes a poll bound of 1 into
-the workspace's override word, so the kernels' own bounded waits run out almost
-at once while every kernel still exits normally (no fault, no hang); a wait
-whose words arrive by its second check still completes, so a launch is
-repeated until one gives up. Then:
+The condition is forced from the host, deterministically: the test writes
+into the workspace's poll-bound override word a small bound and a step F whose
+exchange the kernels treat as late (the waits that check it see every word of
+tag tag_base + F as not yet arrived: the XCD-id exchange, tag tag_base + 1,
+which the dense and fused two-factor kernels and the dense backward run with
+their first exchange, and every exchange of the split two-factor kernel), so
+exactly that exchange runs out through the kernels' own bounded waits while
+every kernel still exits normally (no fault, no hang). Then:
 
-* every output element written after the failed wait is NaN, and every
-  element that is not NaN equals the oracle (no value computed from stale
-  inputs passes as valid);
+* the outputs up to the forced exchange equal the oracle, and every output
+  element from it on is NaN (no value computed from stale inputs passes as
+  valid);
 * the next persistent launch on that stream raises ``PersistentScanFault`` (a
   ``RuntimeError``), read from the pinned host mirror without synchronising;
 * the launch after that is correct again: the fault word names the launch that
@@ -41,12 +44,16 @@ def _words(dev: torch.device) -> torch.Tensor:
     return _lib._ws_cache[(dev.index, handle)].view(torch.int32)
 
 
+BOUND = 4096   # polls before a wait gives up: far more than an on-time exchange takes
+
+
 @contextlib.contextmanager
-def poll_bound_of_one(dev: torch.device):
-    """Launches queued inside the block run with a poll bound of 1; the
-    override is cleared on the way out whatever happens inside."""
+def forced_late_exchange(dev: torch.device, step: int, bound: int = BOUND):
+    """Launches queued inside the block run with exchange `step` forced late
+    and a poll bound of `bound`; the override is cleared on the way out
+    whatever happens inside."""
     words = _words(dev)
-    words[SPIN_WORD] = 1  # queued on the stream before the next launch
+    words[SPIN_WORD] = (step << 24) | bound  # queued on the stream before the next launch
     try:
         yield
     finally:
@@ -72,14 +79,12 @@ def _cases():
 CASES = _cases()
 
 
-def _check_partial(out: torch.Tensor, ref: torch.Tensor) -> int:
-    nan = torch.isnan(out)
-    keep = ~nan
-    assert keep.any() or nan.all()
-    if keep.any():
-        err = (out[keep] - ref[keep]).abs().max().item()
-        assert err <= FP32_TOL, f"a value written before the give-up differs from the oracle by {err:.3e}"
-    return int(nan.sum())
+# The exchange forced late per kernel and the first step whose output is then
+# NaN. Dense and fused: F = 1, the XCD-id exchange that runs with the first
+# exchange of q_in(h_0), which step 1 needs. Split: F = 2, the z exchange of
+# step 1 (its second exchange of step t carries tag tag_base + t + 1).
+FORCED = {"dense": 1, "monarch2_fused": 1, "monarch2_split": 2}
+FIRST_NAN = {"dense": 1, "monarch2_fused": 1, "monarch2_split": 1}
 
 
 @pytest.mark.parametrize("name", list(CASES))
@@ -91,20 +96,15 @@ def test_forward_give_up_is_nan_then_raises(dev, name):
     out = run_config(d)
     torch.cuda.synchronize(dev)
     assert (out.cpu() - ref).abs().max().item() <= FP32_TOL
-    # A wait gives up only when its words are not there by the second check, so
-    # a small grid can get through a launch without one; repeat until one does.
-    # A launch that did not give up must be exact and leave the fault word clear.
-    n_nan = 0
-    for attempt in range(20):
-        log(f"[faults] {name}: launch with a poll bound of 1 (attempt {attempt})")
-        with poll_bound_of_one(dev):
-            out = run_config(d)
-        n_nan = _check_partial(out.cpu(), ref)
-        log(f"[faults] {name}: {n_nan} of {out.numel()} outputs NaN")
-        if n_nan:
-            break
-        assert gru_qat_amd.workspace_faults(dev) == 0, "a launch with no NaN output reported a give-up"
-    assert n_nan > 0, "20 launches with a poll bound of 1 never gave up a wait"
+    log(f"[faults] {name}: launch with exchange {FORCED[name]} forced late")
+    with forced_late_exchange(dev, FORCED[name]):
+        out = run_config(d)
+    out = out.cpu()
+    s = FIRST_NAN[name]
+    log(f"[faults] {name}: {int(torch.isnan(out).sum())} of {out.numel()} outputs NaN")
+    assert not torch.isnan(out[:s]).any(), "an output before the forced exchange is NaN"
+    assert (out[:s] - ref[:s]).abs().max().item() <= FP32_TOL
+    assert torch.isnan(out[s:]).all(), "an output from the forced exchange on is not NaN"
     with pytest.raises(gru_qat_amd.PersistentScanFault):
         run_config(d)
     assert issubclass(gru_qat_amd.PersistentScanFault, RuntimeError)
@@ -117,22 +117,41 @@ def test_forward_give_up_is_nan_then_raises(dev, name):
     assert gru_qat_amd.workspace_faults(dev) == 0
 
 
+@pytest.mark.parametrize("name", list(CASES))
+def test_bound_alone_gives_no_fault(dev, name):
+    """The bound the forced test uses, with no exchange forced: every wait is
+    met long before it, so the launch is exact and raises nothing."""
+    cfg = CASES[name]
+    d = to_dev(cfg, dev)
+    ref = O.scan_config(cfg)
+    with forced_late_exchange(dev, step=0):
+        out = run_config(d)
+    assert (out.cpu() - ref).abs().max().item() <= FP32_TOL
+    assert gru_qat_amd.workspace_faults(dev) == 0
+
+
 def test_backward_give_up_is_nan_then_raises(dev):
+    """The dense backward's recurrence walks t down from T - 1; its first
+    exchange (with the XCD-id words, tag tag_base + 1, forced late here)
+    carries D_{T-2}, which reverse step 1 needs, so the gradients of steps
+    T-2 and T-1 are exact and those of steps 0 .. T-3 (and dh0) NaN."""
+    FORCED = 1
     cfg = make_config(1, shape=(12, 8, 512))
+    T = cfg["T"]
     d = {k: cfg[k].to(dev) for k in ("gi", "h0", "w", "bh")}
     out = gru_qat_amd.gru_scan_forward_persistent(d["gi"], d["h0"], d["w"], d["bh"])
     dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(1)).to(dev)
     torch.cuda.synchronize(dev)
     ref = O.scan_backward(cfg, out.cpu(), dout.cpu())
-    for attempt in range(20):
-        log(f"[faults] dense backward with a poll bound of 1 (attempt {attempt})")
-        with poll_bound_of_one(dev):
-            grads = gru_scan_backward_persistent(d["gi"], d["h0"], d["w"], d["bh"], out, dout)
-        dgi = grads[0].cpu()
-        if torch.isnan(dgi).any():
-            break
-        assert gru_qat_amd.workspace_faults(dev) == 0, "a launch with no NaN gradient reported a give-up"
-    assert torch.isnan(dgi).any(), "20 launches with a poll bound of 1 never gave up a wait"
+    log(f"[faults] dense backward with exchange {FORCED} forced late")
+    with forced_late_exchange(dev, FORCED):
+        grads = gru_scan_backward_persistent(d["gi"], d["h0"], d["w"], d["bh"], out, dout)
+    dgi, dh0 = grads[0].cpu(), grads[1].cpu()
+    keep = T - 1 - FORCED
+    assert torch.isnan(dgi[:keep]).all() and torch.isnan(dh0).all()
+    assert not torch.isnan(dgi[keep:]).any()
+    bar = 1e-4 * max(1.0, ref["dgi"].abs().max().item())
+    assert (dgi[keep:] - ref["dgi"][keep:]).abs().max().item() <= bar
     with pytest.raises(gru_qat_amd.PersistentScanFault):
         gru_scan_backward_persistent(d["gi"], d["h0"], d["w"], d["bh"], out, dout)
     grads = gru_scan_backward_persistent(d["gi"], d["h0"], d["w"], d["bh"], out, dout)

@@ -149,3 +149,100 @@ def test_fake_quant_rows_dynamic_forward_is_the_pinned_rule():
     W = torch.randn(7, 33, generator=g)
     W[3] = 0.0
     assert torch.equal(O.fake_quant_rows_dynamic(W, -127, 127), O.weight_fake_quant_rows(W, -127, 127)[0])
+
+
+# ---- the structured input side ---------------------------------------------------------------
+# The oracle's structured_input_projection against a composition written out
+# here from gru_cell.py:466-503 with nothing shared but the pinned butterfly
+# product (tests/test_golden_butterfly.py): each gate's map materialized as a
+# matrix, q_x, the map, the gate's output quantizer and then its bias done by
+# hand in numpy (float64), concatenated r, z, n. Planted mistakes in the
+# by-hand composition (bias before the output quantizer, q_x skipped, one
+# scale for the whole tensor instead of one per row, r and z swapped) must
+# each move the result away from the oracle.
+
+def _np_fake_quant(y, s, qmin, qmax):
+    return np.clip(np.rint(y / s), qmin, qmax) * s
+
+
+def _np_rows(y, qmin, qmax):
+    s = np.maximum(np.abs(y).max(axis=1, keepdims=True), 1e-8) / qmax
+    return np.clip(np.rint(y / s), qmin, qmax) * s
+
+
+def _gate_matrices(kind, w, H):
+    """[3] matrices A_g with y_g = x @ A_g (x a row vector of length H)."""
+    mats = []
+    for g in range(3):
+        if kind == "diagonal":
+            mats.append(np.diag(w[g].numpy()))
+        elif kind == "monarch":
+            nb, bs = w.shape[1], w.shape[2]
+            M = np.zeros((H, H))
+            for n in range(nb):
+                M[n * bs:(n + 1) * bs, n * bs:(n + 1) * bs] = w[g, n].numpy()  # (out, in) block
+            mats.append(M.T)
+        else:
+            N = 2 * w.shape[3]
+            A = O.butterfly_apply(torch.eye(N, dtype=w.dtype), w[g]).numpy()
+            mats.append(A[:H, :H])
+    return mats
+
+
+def _by_hand(x, kind, w, b, xq_param, oq, mistake=""):
+    H = x.shape[-1]
+    xn = x.reshape(-1, H).numpy()
+    xq = xn if (xq_param is None or mistake == "no_qx") else _np_fake_quant(xn, *xq_param)
+    mats = _gate_matrices(kind, w, H)
+    order = (1, 0, 2) if mistake == "rz_swapped" else (0, 1, 2)
+    parts = []
+    for g in order:
+        y = xq @ mats[g]
+        bg = b[g * H:(g + 1) * H].numpy()
+        if mistake == "bias_first":
+            y = y + bg
+        q = oq[g]
+        if q is not None:
+            if q[0] == "rows":
+                y = _np_fake_quant(y, np.maximum(np.abs(y).max(), 1e-8) / q[2], q[1], q[2]) \
+                    if mistake == "tensor_scale" else _np_rows(y, q[1], q[2])
+            else:
+                y = _np_fake_quant(y, *q)
+        if mistake != "bias_first":
+            y = y + bg
+        parts.append(y)
+    return np.concatenate(parts, axis=-1).reshape(*x.shape[:-1], 3 * H)
+
+
+def _struct_weights(kind, H, gen):
+    if kind == "diagonal":
+        return torch.rand(3, H, generator=gen, dtype=torch.float64) * 2 - 1
+    if kind == "monarch":
+        nb = 4
+        return (torch.rand(3, nb, H // nb, H // nb, generator=gen, dtype=torch.float64) * 2 - 1) / (H // nb) ** 0.5
+    N = 1 << (H - 1).bit_length()
+    L = N.bit_length() - 1
+    return torch.randn(3, 1, L, N // 2, 2, 2, generator=gen, dtype=torch.float64) * 0.5 ** 0.5
+
+
+OUT_QUANTS = [(None, None, None), ((0.03, -20, 20), ("rows", -127, 127), None),
+              (("rows", -7, 7), (0.01, -127, 127), ("rows", -127, 127))]
+
+
+@pytest.mark.parametrize("kind,H", [("diagonal", 40), ("monarch", 64), ("butterfly", 64), ("butterfly", 48)])
+@pytest.mark.parametrize("oq", OUT_QUANTS)
+def test_structured_input_projection_matches_the_composition_by_hand(kind, H, oq):
+    gen = torch.Generator().manual_seed(17)
+    x = torch.randn(3, 5, H, generator=gen, dtype=torch.float64) * 0.7
+    w = _struct_weights(kind, H, gen)
+    b = torch.randn(3 * H, generator=gen, dtype=torch.float64) * 0.2
+    xq = (0.05, -127, 127)
+    got = O.structured_input_projection(x, kind, w, b, x_quant=xq, out_quant=oq).numpy()
+    want = _by_hand(x, kind, w, b, xq, oq)
+    assert np.abs(got - want).max() <= 1e-9
+    for mistake in ("bias_first", "no_qx", "rz_swapped") + (("tensor_scale",) if any(
+            q is not None and q[0] == "rows" for q in oq) else ()):
+        if mistake == "bias_first" and all(q is None for q in oq):
+            continue  # without an output quantizer the order of the bias does not matter
+        wrong = _by_hand(x, kind, w, b, xq, oq, mistake)
+        assert np.abs(got - wrong).max() > 1e-6, mistake
