@@ -580,13 +580,24 @@ struct StaticScratch {
 std::mutex g_static_mu;
 StaticScratch g_static[64];
 
-// The device address of this device's array (looked up on its first use, with
-// the device current), cleared on first use and again before the 32-bit step
-// tags could wrap; the clear is a fill kernel queued on `stream`.
-int static_scratch(hipStream_t stream, int64_t steps, void** out, const char* who) {
+// The device address of the stream's device's array (looked up on its first
+// use, with that device current: a stream of another device is refused),
+// cleared on first use and before a launch of `steps` steps could take the
+// 32-bit step tags past their limit; the clear is a fill kernel queued on
+// `stream`. The caller counts the launch's steps with count_static_steps once
+// it has been queued.
+int static_scratch(hipStream_t stream, int64_t steps, void** out, int* dev_out, const char* who) {
   int dev = 0;
   GS_CHECK_HIP(hipGetDevice(&dev));
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    GS_CHECK_HIP(hipStreamGetDevice(stream, &sdev));
+    if (sdev != dev)
+      return set_error(GS_ERR_INVALID, "%s: the stream belongs to device %d but device %d is current", who, (int)sdev,
+                       dev);
+  }
   if (dev < 0 || dev >= 64) return set_error(GS_ERR_HIP, "%s: device ordinal %d out of range", who, dev);
+  *dev_out = dev;
   std::lock_guard<std::mutex> lk(g_static_mu);
   StaticScratch& s = g_static[dev];
   if (s.ptr == nullptr) {
@@ -604,9 +615,13 @@ int static_scratch(hipStream_t stream, int64_t steps, void** out, const char* wh
     s.cleared = true;
     s.steps = 0;
   }
-  s.steps += (uint64_t)steps;
   *out = s.ptr;
   return GS_OK;
+}
+
+void count_static_steps(int dev, int64_t steps) {
+  std::lock_guard<std::mutex> lk(g_static_mu);
+  g_static[dev].steps += (uint64_t)steps;
 }
 
 }  // namespace
@@ -630,8 +645,11 @@ extern "C" int gs_dense_fwd_noalloc(const gs_args* a, hipStream_t stream) {
                          "(use gs_dense_fwd with a caller workspace)",
                          who, (long long)need, (long long)gs::kStaticScratchBytes);
   gs_args b = *a;
-  rc = gs::static_scratch(stream, a->T, &b.workspace, who);
+  int dev = 0;
+  rc = gs::static_scratch(stream, a->T, &b.workspace, &dev, who);
   if (rc) return rc;
   b.workspace_bytes = gs::kStaticScratchBytes;
-  return gs::run(gs::kDense, &b, stream, who);
+  rc = gs::run(gs::kDense, &b, stream, who);
+  if (rc == GS_OK) gs::count_static_steps(dev, a->T);
+  return rc;
 }

@@ -505,6 +505,23 @@ int bfly_materialize_keep(const float* tw, int nch, int L, int H, float* acts, f
   return GS_OK;
 }
 
+// The same map without keeping the activations: the stages ping-pong between
+// two planes of 3 N H floats in buf.
+int bfly_materialize(const float* tw, int nch, int L, int H, float* buf, float* M, hipStream_t stream) {
+  const int N = 1 << L, K = nch * L;
+  const int64_t gate = (int64_t)N * H, nstage = 3 * gate;
+  const int64_t tw_gate = (int64_t)nch * L * (N / 2) * 4;
+  float* pp[2] = {buf, buf + nstage};
+  hipLaunchKernelGGL(bfly_identity, grid_for(nstage), dim3(256), 0, stream, pp[0], gate, N, H);
+  GS_CHECK_HIP(hipGetLastError());
+  for (int j = 0; j < K; ++j) {
+    hipLaunchKernelGGL(bfly_stage_fwd, grid_for(nstage), dim3(256), 0, stream, tw, tw_gate, pp[j & 1],
+                       pp[(j + 1) & 1], gate, j, L, N, H, j == K - 1 ? M : nullptr);
+    GS_CHECK_HIP(hipGetLastError());
+  }
+  return GS_OK;
+}
+
 // Carries a dense gradient dM [3H, H] of that map onto the twiddles dtw (the
 // shape of tw), with the activations bfly_materialize_keep left in acts;
 // gbuf holds 2 * 3 N H floats.

@@ -13,47 +13,36 @@
 // name, and every dense recurrence with H > 1024 (gs_dense_fwd, gs_dense_bwd and
 // the materialized-map backwards of the structured kinds).
 //
-// Work split. A workgroup of 16 waves owns BT <= 4 batch rows. Per step each
-// wave takes quads of 4 hidden units (quad q, q + 16, ...) and forms their 3
+// Work split. A workgroup of 8 waves owns BT <= 4 batch rows. Per step each
+// wave takes quads of 4 hidden units (quad q, q + 8, ...) and forms their 3
 // gates' products with v_mfma_f32_4x4x1_16b_f32 chains exactly as the
-// persistent kernels do (A = the 4 staged rows from LDS, B = 4 weight rows
-// loaded as float4 from memory, the 16 MFMA blocks as 16 K slices, two
-// accumulators alternating by instruction, reduce16), so the products, and the
-// gate epilogue after them, are bit for bit those of the persistent kernels.
+// persistent kernels do (A = the 4 staged rows from LDS, B = 4 weight rows,
+// the 16 MFMA blocks as 16 K slices, two accumulators alternating by
+// instruction, reduce16), so the products, and the gate epilogue after them,
+// are bit for bit those of the persistent kernels. The weights reach the MFMA
+// through an LDS transpose (forward) or a copy in operand order (backward), so
+// that every load instruction reads contiguous memory.
 // Then an LDS barrier, a pass that stages the next step's operand rows from
 // the new state, and a second barrier.
 //
 // Bound: each workgroup streams the whole of Wh (3 H^2 floats) from L2 or
-// memory every step; a CU reads about 64 bytes per clock, so a step takes
-// about 3 H^2 4 / 64 clocks whatever BT is (BT only sets how many CUs work).
+// memory every step through one CU's texture addresser (about 64 bytes per
+// clock for contiguous 16-byte lanes), so a step takes at least 3 H^2 4 / 64
+// clocks whatever BT is (BT only sets how many CUs work).
 #include "gs_gemm.h"
 #include "gs_mfma.h"
 
 namespace gs {
 namespace {
 
-constexpr int kTileWaves = 16;
+constexpr int kTileWaves = 8;  // forward (its LDS weight staging takes 6.9 KiB per wave)
 constexpr int kTileThreads = 64 * kTileWaves;
+constexpr int kBwdWaves = 16;  // backward recurrence (measured 3.04 ms with 8 waves, 2.36 ms with 16)
+constexpr int kBwdThreads = 64 * kBwdWaves;
 // LDS a workgroup may take (gfx950: 160 KiB per CU).
 constexpr int64_t kTileLdsMax = 160 * 1024;
-// K chunks of 64 whose loads a wave issues together (forward: 3 gates each)
+// Backward: K chunks of 64 whose loads a wave issues together
 constexpr int kUnroll = 4;
-
-// A chunk of 4 consecutive weights of one row at k (from `row`, which already
-// points at this lane's k offset), zero past `klim` elements. VEC: the row
-// length is a multiple of 4, so a chunk is either whole or past the end and
-// loads as one float4.
-template <bool VEC>
-__device__ __forceinline__ f4 ld_chunk(const float* row, int k, int klim, bool ok) {
-  if constexpr (VEC) {
-    return (ok && k < klim) ? *reinterpret_cast<const f4*>(row + k) : f4{0.f, 0.f, 0.f, 0.f};
-  } else {
-    f4 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = (ok && k + e < klim) ? row[k + e] : 0.0f;
-    return v;
-  }
-}
 
 struct TFParams {
   const float* gi;
@@ -72,6 +61,24 @@ struct TFParams {
   int qin_after_first;
 };
 
+// Forward weight staging. The MFMA's B operand puts 4 different units (rows of
+// Wh) on every 4 adjacent lanes, and loading it in place spans 4 rows per group
+// of 4 lanes, which the texture addresser serves at about 14 bytes per clock.
+// So a wave loads an item (KI = 128 consecutive k of the 12 rows of its quad:
+// 3 gates x 4 units) with 32 lanes per row (512 contiguous bytes each half
+// wave), writes it to a wave-private LDS buffer and reads the operands back in
+// MFMA order; the next item's loads are in flight meanwhile. The buffer holds
+// 12 rows of kItemK floats with a stride of 16 mod 64 floats: the 16-byte
+// stores (8 lanes a pass, 128 contiguous bytes) and the operand reads (lanes
+// 4 b + j at row j, 4 b, rows 16 banks apart) are free of bank conflicts.
+constexpr int kItemK = 128;           // k per item: 2 chunks of 64
+constexpr int kItemRS = kItemK + 16;  // LDS row stride of the staging buffer (floats)
+constexpr int kItemFloats = 12 * kItemRS;
+constexpr int kItemLoads = 6;         // 12 rows, 2 per load instruction
+// items whose loads are in flight: 3 for 16-byte loads; the scalar path holds
+// 4 addresses per float4 and spills at 3
+template <bool VEC> constexpr int kFwdDepth = VEC ? 3 : 2;
+
 template <bool VEC, bool SAVE>
 __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
   extern __shared__ float lds[];
@@ -82,8 +89,9 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
   const int j = lane & 3, s = (lane >> 2) & 3;     // epilogue: unit of the quad, row (lanes < 16)
   const bool lead = lane < 16;
   const int row0 = blockIdx.x * BT;
-  float* hq = lds;              // [BT][rs] staged q_in(h_{t-1}), zero from H on
-  float* hraw = hq + BT * rs;   // [BT][hr] raw h_{t-1}
+  float* hq = lds;                   // [BT][rs] staged q_in(h_{t-1}), zero from H on
+  float* hraw = hq + BT * rs;        // [BT][hr] raw h_{t-1}
+  float* wbuf = hraw + BT * hr + wave * kItemFloats;  // this wave's weight staging buffer
 
   for (int i = threadIdx.x; i < BT * rs; i += kTileThreads) {
     const int rr = i / rs, k = i - rr * rs, row = row0 + rr;
@@ -104,61 +112,88 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
   const int nq = (H + 3) >> 2;
   const bool a_ok = r < BT;
   const float* arow = hq + (a_ok ? r : 0) * rs + 4 * kb;
-  const int klim = H - 4 * kb;
   const int64_t HH = (int64_t)H * H;
   const int row = row0 + s;
   const bool row_ok = lead && s < BT && row < p.B;
+  const int row_c = min(row0 + (s < BT ? s : 0), p.B - 1);  // gate-input row, clamped to a valid one
+  // staging: load instruction i of an item covers rows 2 i + lane / 32 (row = 4 g + unit), 4 floats
+  // of k at kl = 4 (lane mod 32); operand reads: row 4 g + j, k = 64 c + 4 kb
+  const int kl = 4 * (lane & 31), rh = lane >> 5;
+  float* wst = wbuf + rh * kItemRS + kl;        // + 2 i kItemRS for load instruction i
+  const float* wop = wbuf + j * kItemRS + 4 * kb;  // + 4 g kItemRS + 64 c for gate g, chunk c
+  const int myq = wave < nq ? (nq - 1 - wave) / kTileWaves + 1 : 0;
+  const int nbat = (H + kItemK - 1) / kItemK;   // items per quad
+  const int nit = myq * nbat;
   for (int t = 0; t < p.T; ++t) {
-    for (int q = wave; q < nq; q += kTileWaves) {
-      const int u = 4 * q + j;
-      const bool u_ok = u < H;
-      const bool mine = row_ok && u_ok;
-      // epilogue inputs first: their latency overlaps the K loop
-      float gir = 0.f, giz = 0.f, gin = 0.f, b0 = 0.f, b1 = 0.f, b2 = 0.f;
-      if (mine) {
-        const float* g = p.gi + (int64_t)t * p.sg_t + (int64_t)row * p.sg_b + u;
-        gir = g[0];
-        giz = g[H];
-        gin = g[2 * H];
-        b0 = kR * p.bh[u];
-        b1 = kR * p.bh[H + u];
-        b2 = kN * p.bh[2 * H + u];
-      }
-      const float* w0 = p.w + (int64_t)u * H + 4 * kb;  // row u of gate r; gate g adds g H^2
-      f4 p0[3], p1[3];
+    const float* git = p.gi + (int64_t)t * p.sg_t + (int64_t)row_c * p.sg_b;
+    // Item (q, b): k in [b kItemK, (b + 1) kItemK) of quad q's 12 rows, loaded
+    // coalesced into registers; also the quad's gate inputs and biases (raw).
+    struct Item {
+      f4 w[kItemLoads];
+      float g[3], bb[3];
+    };
+    auto load = [&](int q, int b, Item& it) {
 #pragma unroll
-      for (int g = 0; g < 3; ++g) p0[g] = p1[g] = f4{0.f, 0.f, 0.f, 0.f};
-      // kUnroll chunks per iteration: their 3 kUnroll weight loads are in flight together
-      for (int c0 = 0; c0 < p.nch; c0 += kUnroll) {
-        f4 a[kUnroll], wv[kUnroll][3];
+      for (int i = 0; i < kItemLoads; ++i) {
+        const int rr = 2 * i + rh, g = rr >> 2, u = 4 * q + (rr & 3);
+        const int k = b * kItemK + kl;
+        const bool ok = u < H && k < H;
+        const int64_t off = g * HH + (int64_t)(u < H ? u : H - 1) * H + k;
+        if constexpr (VEC) {
+          const f4 v = *reinterpret_cast<const f4*>(p.w + (ok ? off : 0));
+          it.w[i] = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
+        } else {
 #pragma unroll
-        for (int i = 0; i < kUnroll; ++i) {
-          const int c = c0 + i;
-          const bool in = c < p.nch;  // uniform
-          a[i] = (in && a_ok) ? *reinterpret_cast<const f4*>(arow + 64 * c) : f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int g = 0; g < 3; ++g) wv[i][g] = ld_chunk<VEC>(w0 + g * HH, 64 * c, klim, in && u_ok);
-        }
-#pragma unroll
-        for (int i = 0; i < kUnroll; ++i) {
-          if (c0 + i >= p.nch) break;  // uniform: no MFMA past the last chunk
-#pragma unroll
-          for (int g = 0; g < 3; ++g) {
-            p0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[i][0], wv[i][g][0], p0[g], 0, 0, 0);
-            p1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[i][1], wv[i][g][1], p1[g], 0, 0, 0);
-            p0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[i][2], wv[i][g][2], p0[g], 0, 0, 0);
-            p1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[i][3], wv[i][g][3], p1[g], 0, 0, 0);
+          for (int e = 0; e < 4; ++e) {
+            const bool in = u < H && k + e < H;
+            const float x = p.w[in ? off + e : 0];
+            it.w[i][e] = in ? x : 0.0f;
           }
         }
       }
+      const int uc = min(4 * q + j, H - 1);
+#pragma unroll
+      for (int g = 0; g < 3; ++g) {
+        it.g[g] = git[g * H + uc];
+        it.bb[g] = p.bh[g * H + uc];
+      }
+    };
+    f4 p0[3], p1[3];
+    // one item: stage its weights, its MFMAs, and after a quad's last item the
+    // reduction and the gate epilogue (the staging buffer is this wave's alone,
+    // and a wave's LDS accesses complete in order, so no barrier is needed)
+    auto run = [&](int q, int b, const Item& it) {
+#pragma unroll
+      for (int i = 0; i < kItemLoads; ++i) *reinterpret_cast<f4*>(wst + 2 * i * kItemRS) = it.w[i];
+      if (b == 0) {
+#pragma unroll
+        for (int g = 0; g < 3; ++g) p0[g] = p1[g] = f4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int ci = 0; ci < kItemK / 64; ++ci) {
+        const int c = b * (kItemK / 64) + ci;
+        if (c >= p.nch) break;  // uniform
+        const f4 a = a_ok ? *reinterpret_cast<const f4*>(arow + 64 * c) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < 3; ++g) {
+          const f4 wv = *reinterpret_cast<const f4*>(wop + 4 * g * kItemRS + 64 * ci);
+          p0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[0], wv[0], p0[g], 0, 0, 0);
+          p1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[1], wv[1], p1[g], 0, 0, 0);
+          p0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[2], wv[2], p0[g], 0, 0, 0);
+          p1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[3], wv[3], p1[g], 0, 0, 0);
+        }
+      }
+      if (b != nbat - 1) return;
       float gh[3];
 #pragma unroll
       for (int g = 0; g < 3; ++g) gh[g] = reduce16(p0[g] + p1[g], s);
-      if (mine) {
+      const int u = 4 * q + j;
+      if (row_ok && u < H) {
         float* hp = hraw + s * hr + u;
-        const float cr = __builtin_fmaf(kR, gir, b0), cz = __builtin_fmaf(kR, giz, b1), an2 = kN * gin;
+        const float cr = __builtin_fmaf(kR, it.g[0], kR * it.bb[0]);
+        const float cz = __builtin_fmaf(kR, it.g[1], kR * it.bb[1]), an2 = kN * it.g[2];
         float hn = gru_update_l2(__builtin_fmaf(kR, gh[0], cr), __builtin_fmaf(kR, gh[1], cz),
-                                 __builtin_fmaf(kN, gh[2], b2), an2, *hp);
+                                 __builtin_fmaf(kN, gh[2], kN * it.bb[2]), an2, *hp);
         if (p.qout.on) hn = fake_quant(hn, p.qout);
         *hp = hn;  // only this lane reads or writes this (row, unit) during the step
         p.out[(int64_t)t * p.so_t + (int64_t)row * p.so_b + u] = hn;
@@ -168,6 +203,24 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
           for (int g = 0; g < 3; ++g) __builtin_nontemporal_store(gh[g], o + g * H);
         }
       }
+    };
+    // item m is quad wave + kTileWaves (m / nbat), part m mod nbat; kD items
+    // are in flight, in register sets that rotate at compile time
+    auto quad_of = [&](int m) { return wave + kTileWaves * (m / nbat); };
+    constexpr int kD = kFwdDepth<VEC>;
+    Item buf[kD];
+    static_for<0, kD - 1>([&](auto I) {
+      if (I < nit) load(quad_of(I), I % nbat, buf[I]);
+    });
+    for (int n = 0; n < nit; n += kD) {
+      static_for<0, kD>([&](auto I) {
+        const int m = n + I;
+        if (m < nit) {
+          const int ml = m + kD - 1;
+          if (ml < nit) load(quad_of(ml), ml % nbat, buf[(I + kD - 1) % kD]);
+          run(quad_of(m), m % nbat, buf[I]);
+        }
+      });
     }
     lds_barrier();
     if (t + 1 < p.T) {
@@ -185,10 +238,16 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
 // Backward recurrence (the dense backward's step 3, scan_dense_bwd.hip):
 //   D_{t-1} = dout[t-1] + Zm_t D_t + Mi_t (dgh_t Wh),   dgh_t = D_t (Cr, Cz, Chn)_t,
 //   dh0 = Zm_0 D_0 + Mi_0 (dgh_0 Wh),
-// with Wh read transposed (wt [H, 3H], wt[u][n] = Wh[n][u]) so that a unit's
-// weights over the 3H reduction are one contiguous row.
+// with Wh read from a copy in the MFMA operand order (wl, written once per call
+// by lane_order_kernel): the float4 that lane l of a wave needs for quad q and
+// reduction chunk cc (over the 3H rows, 64 per chunk) sits at
+// wl[((q 3 nch + cc) 64 + l) 4], so every load instruction of a wave reads 1 KiB
+// of contiguous memory. (Read in place, lanes 4 b + j hold 4 different columns
+// of Wh: each group of 4 adjacent lanes spans 4 rows of the transposed matrix,
+// which the texture addresser serves at about 14 bytes per clock, the kernel's
+// bound when first measured: TA_TA_BUSY ~93 % of the kernel's cycles.)
 struct TBParams {
-  const float* wt;    // [H, 3H]
+  const float* wl;    // [nq][3 nch][64][4], zero past H
   const float* dout;  // [T, B, H] contiguous
   const float* cg;    // [T, B, 3H] (Cr, Cz, Chn)
   const float* zm;    // [T, B, H]
@@ -198,8 +257,7 @@ struct TBParams {
   int T, B, H, BT, nch, rs, hr;
 };
 
-template <bool VEC>
-__global__ __launch_bounds__(kTileThreads) void tiled_bwd_kernel(TBParams p) {
+__global__ __launch_bounds__(kBwdThreads) void tiled_bwd_kernel(TBParams p) {
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -213,8 +271,8 @@ __global__ __launch_bounds__(kTileThreads) void tiled_bwd_kernel(TBParams p) {
   float* dd = dg + 3 * BT * rs;     // [BT][hr] D_t
 
   // D_{T-1} = dout[T-1]
-  for (int i = threadIdx.x; i < 3 * BT * rs; i += kTileThreads) dg[i] = 0.0f;
-  for (int i = threadIdx.x; i < BT * hr; i += kTileThreads) {
+  for (int i = threadIdx.x; i < 3 * BT * rs; i += kBwdThreads) dg[i] = 0.0f;
+  for (int i = threadIdx.x; i < BT * hr; i += kBwdThreads) {
     const int rr = i / hr, k = i - rr * hr, row = row0 + rr;
     float D = 0.0f;
     if (k < H && row < p.B) {
@@ -228,14 +286,14 @@ __global__ __launch_bounds__(kTileThreads) void tiled_bwd_kernel(TBParams p) {
 
   const int nq = (H + 3) >> 2;
   const bool a_ok = r < BT;
-  const int klim = H - 4 * kb;
   const int row = row0 + s;
   const bool row_ok = lead && s < BT && row < p.B;
   const int H3 = 3 * H;
+  const int nk = 3 * p.nch;
   for (int st = 0; st < T; ++st) {
     const int t = T - 1 - st;
     // stage dgh_t = D_t (Cr, Cz, Chn)_t
-    for (int i = threadIdx.x; i < BT * H; i += kTileThreads) {
+    for (int i = threadIdx.x; i < BT * H; i += kBwdThreads) {
       const int rr = i / H, k = i - rr * H, rw = row0 + rr;
       if (rw < p.B) {
         const float D = dd[rr * hr + k];
@@ -247,7 +305,7 @@ __global__ __launch_bounds__(kTileThreads) void tiled_bwd_kernel(TBParams p) {
       }
     }
     lds_barrier();
-    for (int q = wave; q < nq; q += kTileWaves) {
+    for (int q = wave; q < nq; q += kBwdWaves) {
       const int u = 4 * q + j;
       const bool u_ok = u < H;
       const bool mine = row_ok && u_ok;
@@ -258,12 +316,12 @@ __global__ __launch_bounds__(kTileThreads) void tiled_bwd_kernel(TBParams p) {
         mi = p.mi[e];
         if (t > 0) dprev = p.dout[e - BH];
       }
-      const float* w0 = p.wt + (int64_t)u * H3 + 4 * kb;
+      const f4* wq = reinterpret_cast<const f4*>(p.wl) + (int64_t)q * nk * 64 + lane;  // chunk cc at + 64 cc
       f4 acc0 = f4{0.f, 0.f, 0.f, 0.f}, acc1 = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int g = 0; g < 3; ++g) {
         const float* arow = dg + (g * BT + (a_ok ? r : 0)) * rs + 4 * kb;
-        const float* wg = w0 + g * H;
+        const f4* wg = wq + (int64_t)g * p.nch * 64;
         for (int c0 = 0; c0 < p.nch; c0 += 2 * kUnroll) {
           f4 a[2 * kUnroll], wv[2 * kUnroll];
 #pragma unroll
@@ -271,7 +329,7 @@ __global__ __launch_bounds__(kTileThreads) void tiled_bwd_kernel(TBParams p) {
             const int c = c0 + i;
             const bool in = c < p.nch;  // uniform
             a[i] = (in && a_ok) ? *reinterpret_cast<const f4*>(arow + 64 * c) : f4{0.f, 0.f, 0.f, 0.f};
-            wv[i] = ld_chunk<VEC>(wg, 64 * c, klim, in && u_ok);
+            wv[i] = in ? wg[64 * c] : f4{0.f, 0.f, 0.f, 0.f};
           }
 #pragma unroll
           for (int i = 0; i < 2 * kUnroll; ++i) {
@@ -304,23 +362,29 @@ __global__ __launch_bounds__(kTileThreads) void tiled_bwd_kernel(TBParams p) {
   }
 }
 
-__global__ void transpose_kernel(const float* __restrict__ src, float* __restrict__ dst, int rows, int cols) {
-  // dst[c][r] = src[r][c], 32 x 32 tiles through LDS (padded against bank conflicts)
-  __shared__ float tile[32][33];
-  const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 256 threads: ty in [0, 8)
-  for (int i = ty; i < 32; i += 8) {
-    const int rr = r0 + i, cc = c0 + tx;
-    tile[i][tx] = (rr < rows && cc < cols) ? src[(int64_t)rr * cols + cc] : 0.0f;
+// wl[((q 3 nch + cc) 64 + l) 4 + e] = Wh[g H + k][u] with g = cc / nch,
+// k = 64 (cc mod nch) + 4 (l / 4) + e, u = 4 q + l mod 4, and zero where k or u
+// is past H. One thread per float4; lanes 4 b .. 4 b + 3 read 16 contiguous
+// bytes of a row of Wh.
+__global__ void lane_order_kernel(const float* __restrict__ w, float* __restrict__ wl, int H, int nch, int64_t n4) {
+  const int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= n4) return;
+  const int l = (int)(idx & 63);
+  const int64_t qc = idx >> 6;
+  const int nk = 3 * nch;
+  const int q = (int)(qc / nk), cc = (int)(qc - (int64_t)q * nk);
+  const int g = cc / nch, c = cc - g * nch;
+  const int u = 4 * q + (l & 3), k0 = 64 * c + 4 * (l >> 2);
+  f4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int k = k0 + e;
+    v[e] = (u < H && k < H) ? w[(int64_t)(g * H + k) * H + u] : 0.0f;
   }
-  __syncthreads();
-  for (int i = ty; i < 32; i += 8) {
-    const int cc = c0 + i, rr = r0 + tx;
-    if (cc < cols && rr < rows) dst[(int64_t)cc * rows + rr] = tile[tx][i];
-  }
+  reinterpret_cast<f4*>(wl)[idx] = v;
 }
 
-int64_t fwd_lds(int BT, int rs, int hr) { return 4 * (int64_t)BT * (rs + hr); }
+int64_t fwd_lds(int BT, int rs, int hr) { return 4 * ((int64_t)BT * (rs + hr) + (int64_t)kTileWaves * kItemFloats); }
 int64_t bwd_lds(int BT, int rs, int hr) { return 4 * (int64_t)BT * (3 * rs + hr); }
 
 // Rows per workgroup: 4 (one MFMA row block) unless the batch is smaller or the
@@ -396,10 +460,13 @@ int run_tiled_fwd(const gs_args* a, hipStream_t stream, const char* who) {
   return GS_OK;
 }
 
-int64_t tiled_bwd_wt_bytes(int64_t H) { return align256(3 * H * H * 4); }
+int64_t tiled_bwd_wt_bytes(int64_t H) {
+  const int64_t nq = (H + 3) / 4, nch = (H + 63) / 64;
+  return align256(nq * 3 * nch * 64 * 16);
+}
 
-// Step 3 of the dense backward with the batch-tiled kernel: Wh transposed into
-// wt (tiled_bwd_wt_bytes of scratch), then the recurrence.
+// Step 3 of the dense backward with the batch-tiled kernel: Wh in the MFMA
+// operand order into wt (tiled_bwd_wt_bytes of scratch), then the recurrence.
 int run_tiled_bwd_recurrence(const float* w, float* wt, const float* dout, const float* cg, const float* zm,
                              const float* mi, float* dsum, float* dh0, int64_t T, int64_t B, int64_t H,
                              hipStream_t stream, const char* who) {
@@ -409,11 +476,12 @@ int run_tiled_bwd_recurrence(const float* w, float* wt, const float* dout, const
   TilePlan tp;
   int rc = plan_tiled(H, B, true, &tp, who);
   if (rc) return rc;
-  hipLaunchKernelGGL(transpose_kernel, dim3((unsigned)((H + 31) / 32), (unsigned)((3 * H + 31) / 32)), dim3(256), 0,
-                     stream, w, wt, (int)(3 * H), (int)H);
+  const int64_t n4 = ((H + 3) / 4) * 3 * tp.nch * 64;
+  hipLaunchKernelGGL(lane_order_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, stream, w, wt, (int)H,
+                     tp.nch, n4);
   GS_CHECK_HIP(hipGetLastError());
   TBParams p;
-  p.wt = wt;
+  p.wl = wt;
   p.dout = dout;
   p.cg = cg;
   p.zm = zm;
@@ -427,11 +495,11 @@ int run_tiled_bwd_recurrence(const float* w, float* wt, const float* dout, const
   p.nch = tp.nch;
   p.rs = tp.rs;
   p.hr = tp.hr;
-  void (*fn)(TBParams) = (H % 4 == 0) ? tiled_bwd_kernel<true> : tiled_bwd_kernel<false>;
+  void (*fn)(TBParams) = tiled_bwd_kernel;
   if (tp.lds > 65536)
     GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)tp.lds));
   const int64_t nblk = (B + tp.BT - 1) / tp.BT;
-  hipLaunchKernelGGL(fn, dim3((unsigned)nblk), dim3(kTileThreads), (size_t)tp.lds, stream, p);
+  hipLaunchKernelGGL(fn, dim3((unsigned)nblk), dim3(kBwdThreads), (size_t)tp.lds, stream, p);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }

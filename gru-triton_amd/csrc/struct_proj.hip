@@ -30,6 +30,7 @@
 namespace gs {
 
 int bfly_materialize_keep(const float* tw, int nch, int L, int H, float* acts, float* M, hipStream_t stream);
+int bfly_materialize(const float* tw, int nch, int L, int H, float* buf, float* M, hipStream_t stream);
 int bfly_project_grad(const float* tw, int nch, int L, int H, const float* acts, const float* dM, float* gbuf,
                       float* dtw, hipStream_t stream);
 
@@ -65,12 +66,14 @@ __device__ __forceinline__ float block_reduce(float v, float* red) {
 // Backward of one row of a per-row dynamic symmetric fake-quant
 // out_j = clamp(rint(y_j / s)) s with s = max(max_j |y_j|, 1e-8) / qmax, as
 // torch's autograd differentiates FakeQuantizePerChannel + fake_quant_ste:
-// STERound passes g_j, STEClamp never clips (|y_j / s| <= qmax), and the scale
-// is a function of the row, so dL/ds = sum_j g_j (q_j - y_j / s) reaches the
-// row's max through |max| (if |max| >= |min|) and its min through |min| (if
+// STERound passes g_j, STEClamp passes it where rint(y_j / s) lies in
+// [qmin, qmax] (mask m_j; |y_j / s| <= qmax, so only a range with
+// qmin > -qmax clips, on the negative side), and the scale is a function of
+// the row, so dL/ds = sum_j g_j (q_j - m_j y_j / s) reaches the row's max
+// through |max| (if |max| >= |min|) and its min through |min| (if
 // |min| >= |max|), halved on a tie of the two (torch.maximum), shared evenly
 // by equal maxima (amax) or minima (amin), zero when the 1e-8 floor holds
-// (clamp). d may alias g.
+// (clamp). The direct term is m_j g_j. d may alias g.
 __device__ __forceinline__ void rows_dynamic_bwd(const float* y, float s, const float* g, float* d, int cols,
                                                  float qmin, float qmax, float* red) {
   float mx = -__builtin_inff(), mn = __builtin_inff();
@@ -83,12 +86,14 @@ __device__ __forceinline__ void rows_dynamic_bwd(const float* y, float s, const 
   float nmx = 0.f, nmn = 0.f, gs = 0.f;
   for (int k = threadIdx.x; k < cols; k += kSpThreads) {
     const float v = y[k], gk = g[k];
-    const float q = __builtin_fminf(__builtin_fmaxf(__builtin_rintf(v / s), qmin), qmax);
+    const float r = __builtin_rintf(v / s);
+    const float q = __builtin_fminf(__builtin_fmaxf(r, qmin), qmax);
+    const bool keep = r >= qmin && r <= qmax;
     nmx += v == mx ? 1.f : 0.f;
     nmn += v == mn ? 1.f : 0.f;
     {
 #pragma clang fp contract(off)
-      gs += gk * q - gk * v / s;
+      gs += keep ? gk * q - gk * v / s : gk * q;
     }
   }
   nmx = block_reduce<false>(nmx, red);
@@ -104,7 +109,8 @@ __device__ __forceinline__ void rows_dynamic_bwd(const float* y, float s, const 
   const float cmx = dabs * wmx * sgnmx / nmx, cmn = dabs * wmn * sgnmn / nmn;
   for (int k = threadIdx.x; k < cols; k += kSpThreads) {
     const float v = y[k];
-    float dk = g[k];
+    const float r = __builtin_rintf(v / s);
+    float dk = (r >= qmin && r <= qmax) ? g[k] : 0.0f;
     if (v == mx) dk += cmx;
     if (v == mn) dk += cmn;
     d[k] = dk;
@@ -270,6 +276,7 @@ struct SPlan {
   bool any_oq = false, any_rows = false;
   // scratch layout (bytes)
   int64_t map_b = 0, acts_b = 0, gbuf_b = 0, dy_b = 0, xq_b = 0, part_b = 0, colp_b = 0, dm_b = 0;
+  int64_t pp_b = 0;  // forward: two stage planes of the butterfly materialization
   int split = 1;
 };
 
@@ -296,9 +303,12 @@ int validate_oq(const gs_oquant& o, int g, const char* who) {
 
 int plan(int32_t kind, int64_t M, int64_t H, int64_t nblocks, int64_t blksz, int64_t log_n, int64_t nch,
          const gs_quant& qx, const gs_oquant (&oq)[3], bool bwd, SPlan* p, const char* who) {
-  if (M < 1 || H < 1 || M > INT32_MAX / 4 || H > 4096)
-    return set_error(GS_ERR_INVALID, "%s: need 1 <= M < 2^29 and 1 <= H <= 4096; got M=%lld, H=%lld", who, (long long)M,
-                     (long long)H);
+  // M: one workgroup per row in the output-quantizer kernels (256 threads each, fewer than
+  // 2^32 work-items) and one grid row per kDiagRows rows in diag_dw_partial (gridDim.y <= 65535)
+  constexpr int64_t kMaxRows = int64_t(65535) * kDiagRows;
+  if (M < 1 || H < 1 || M > kMaxRows || H > 4096)
+    return set_error(GS_ERR_INVALID, "%s: need 1 <= M <= %lld and 1 <= H <= 4096; got M=%lld, H=%lld", who,
+                     (long long)kMaxRows, (long long)M, (long long)H);
   int rc = validate_quant(qx, "x_quant", who);
   if (rc) return rc;
   for (int g = 0; g < 3; ++g) {
@@ -334,6 +344,7 @@ int plan(int32_t kind, int64_t M, int64_t H, int64_t nblocks, int64_t blksz, int
       p->nch = (int)nch;
       p->map_b = align256((int64_t)3 * H * H * 4);
       p->acts_b = align256((int64_t)3 * (p->nch * p->L + 1) * p->N * H * 4);
+      p->pp_b = align256((int64_t)2 * 3 * p->N * H * 4);
       break;
     default:
       return set_error(GS_ERR_INVALID, "%s: structured input kind must be diagonal, Monarch or butterfly; got %d", who,
@@ -364,7 +375,8 @@ int plan(int32_t kind, int64_t M, int64_t H, int64_t nblocks, int64_t blksz, int
   return GS_OK;
 }
 
-int64_t fwd_scratch(const SPlan& p) { return p.map_b + p.acts_b; }
+// The forward keeps no stage activations (the backward recomputes them).
+int64_t fwd_scratch(const SPlan& p) { return p.map_b + p.pp_b; }
 int64_t bwd_scratch(const SPlan& p) {
   return p.map_b + p.acts_b + p.dm_b + p.gbuf_b + p.dy_b + p.xq_b + p.part_b + p.colp_b;
 }
@@ -413,8 +425,8 @@ int map_forward(const SPlan& p, const float* xq, int64_t ldx, const float* w, co
     return gemm_f32(g, stream, who);
   }
   float* map = reinterpret_cast<float*>(scratch);
-  float* acts = reinterpret_cast<float*>(scratch + p.map_b);
-  int rc = bfly_materialize_keep(w, p.nch, p.L, H, acts, map, stream);
+  float* planes = reinterpret_cast<float*>(scratch + p.map_b);
+  int rc = bfly_materialize(w, p.nch, p.L, H, planes, map, stream);
   if (rc) return rc;
   g.b = map;  // B(k, j) = map[j][k]
   g.ldb = H;

@@ -159,9 +159,17 @@ int gs_butterfly_fwd(const gs_args* args, hipStream_t stream);
  * gs_workspace_bytes(GS_KIND_DENSE, args) is at most 4 MiB (B * H up to about
  * 260,000); larger shapes return GS_ERR_INVALID. The array is cleared by a
  * fill kernel on the first call on each GPU and again before its step tags
- * could wrap. Every call on one GPU shares that GPU's array, so calls that
- * overlap in time on one GPU (two streams, two threads) race; issue them in
- * order on one stream. */
+ * could wrap, as counted on the host over this entry point's calls. Every
+ * call on one GPU shares that GPU's array, so calls that overlap in time on
+ * one GPU (two streams, two threads) race; issue them in order on one stream.
+ * Under HIP graph capture the launch is recorded (make one call outside the
+ * capture first, so that the first-use fill is not part of the graph); each
+ * replay advances the array's device-side tag base by T without the host
+ * counting it, so keep the steps of all replays plus those of the calls below
+ * 2^32 - 2^24 (about 67 million replays of a T = 64 scan), after which tags
+ * could repeat. fault_mirror is this entry point's only fault channel:
+ * gs_workspace_status cannot reach the static array. Above H = 1024 the
+ * batch-tiled kernel runs, which exchanges nothing and uses no array. */
 int gs_dense_fwd_noalloc(const gs_args* args, hipStream_t stream);
 
 /* Same contract as gs_butterfly_fwd, but always runs the general LDS kernel

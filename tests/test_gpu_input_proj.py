@@ -18,6 +18,9 @@ CASES = [
     ((64, 32), 512, 1536, None, None, True),                       # fp32
     ((7,), 13, 30, (0.05, -8, 7), (-127, 127), False),              # odd sizes: scalar loads, no bias
     ((3, 5), 64, 24, None, (-7, 7), True),
+    # asymmetric per-row weight range (scale max|w| / qmax): weights below -100 s clip, and the
+    # clipped-STE mask zeroes their gradient and their part of the scale's gradient
+    ((3, 5), 64, 24, (0.05, -127, 127), (-100, 127), True),
 ]
 
 

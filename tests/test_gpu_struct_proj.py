@@ -28,6 +28,9 @@ pytestmark = pytest.mark.gpu
 
 FROZEN = (0.03, -127, 127)
 ROWS = ("rows", -127, 127)
+# an asymmetric per-row range: the scale is max|y| / 127, so codes below -100 clip
+# (the clipped-STE mask then zeroes their gradient and their scale term)
+ROWS_ASYM = ("rows", -100, 127)
 
 
 def _weights(kind: str, H: int, gen: torch.Generator, nb: int = 4, chains: int = 1) -> torch.Tensor:
@@ -89,6 +92,7 @@ QUANTS = [
     ("frozen", (0.05, -127, 127), (FROZEN, FROZEN, FROZEN)),
     ("rows", None, (ROWS, ROWS, ROWS)),
     ("mixed", (0.05, -127, 127), (None, FROZEN, ROWS)),
+    ("rows_asym", None, (ROWS_ASYM, ROWS, ROWS_ASYM)),
 ]
 
 

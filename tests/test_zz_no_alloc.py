@@ -88,3 +88,33 @@ def test_noalloc_refuses_shapes_beyond_the_static_array(dev):
     out = torch.empty((T, B, H), device=dev)
     with pytest.raises(ValueError, match="static scratch"):
         _call("gs_dense_fwd_noalloc", _args(d, out))
+
+
+def test_noalloc_under_graph_capture_and_replay(dev):
+    """gs_dense_fwd_noalloc captured in a HIP graph (torch.cuda.CUDAGraph):
+    every replay, with eager calls of the same entry point and
+    synchronisations between replays, returns the eager result bit for bit.
+    Each replay's launch advances the device tag base by T, so no replay can
+    accept a word an earlier one left."""
+    cfg = make_config(1, shape=(16, 8, 512), seed=5)
+    d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in cfg.items()}
+    T, B, H = cfg["T"], cfg["B"], cfg["H"]
+    eager = torch.empty((T, B, H), device=dev)
+    _call("gs_dense_fwd_noalloc", _args(d, eager))  # also sets the static array up outside the capture
+    torch.cuda.synchronize(dev)
+    want = eager.cpu()
+    assert (want - O.scan_config(cfg)).abs().max().item() <= FP32_TOL
+    out_g = torch.empty((T, B, H), device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _call("gs_dense_fwd_noalloc", _args(d, out_g))
+    for i in range(4):
+        out_g.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        log(f"[noalloc] replay {i}: {int((out_g.cpu() != want).sum())} elements differ")
+        assert torch.equal(out_g.cpu(), want)
+        again = torch.empty((T, B, H), device=dev)
+        _call("gs_dense_fwd_noalloc", _args(d, again))
+        torch.cuda.synchronize(dev)
+        assert torch.equal(again.cpu(), want)
