@@ -192,6 +192,18 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       const float cr = __builtin_fmaf(kR, gir, bias[0]), cz = __builtin_fmaf(kR, giz, bias[1]), an2 = kN * gin;
       float* hkp = hk + (rbl * 4 + s) * KR + 4 * wave + j;
       const float hprev = *hkp;
+      // flags[1] as staged for this iteration (read as a vector value, made
+      // uniform after the MFMAs): after a give-up the workgroup's outputs are
+      // NaN and it publishes nothing more
+      const int fl_v = REMOTE ? flags[1] : 0;
+      // the step's store addresses
+      float* const outp = p.out + (int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out;
+      uint64_t* const xdst = !REMOTE ? nullptr
+                             : PACK  ? p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb + s) * (p.H / 4) + (unit >> 2)
+                                     : p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * p.H + lane_xh;
+      // the epilogue's LDS reads and the store addresses are issued before the
+      // MFMAs, so that none of them is on the chain after the last one
+      __builtin_amdgcn_sched_barrier(0);
       float a[3][KC];
       lds_a_il<KC>(hst + buf * p.hsz, lane, a[0]);
       f4 acc[3];
@@ -206,9 +218,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
         lv = quant_level(hn, p.qout);
         hn = lv * p.qout.scale;
       }
-      // flags[1] as staged for this iteration: after a give-up the workgroup's
-      // outputs are NaN and it publishes nothing more
-      const int fl = REMOTE ? __builtin_amdgcn_readfirstlane(flags[1]) : 0;
+      const int fl = REMOTE ? __builtin_amdgcn_readfirstlane(fl_v) : 0;
       // bit 0: a poller of this workgroup has seen every workgroup of the group
       // on this XCD (first exchange), so a publish may stay in the XCD's L2
       const bool xcd_local = (fl & 1) != 0;
@@ -229,25 +239,23 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
             const int c2 = __builtin_amdgcn_mov_dpp(c, 0xAA, 0xF, 0xF, true);
             const int c3 = __builtin_amdgcn_mov_dpp(c, 0xFF, 0xF, 0xF, true);
             const uint32_t word = (uint32_t)c0 | ((uint32_t)c1 << 8) | ((uint32_t)c2 << 16) | ((uint32_t)c3 << 24);
-            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb + s) * (p.H / 4) + (unit >> 2);
             if (j == 0) {
               if (xcd_local)
-                st_tagged_xcd(dst, __uint_as_float(word), base + (uint32_t)t + 1u);
+                st_tagged_xcd(xdst, __uint_as_float(word), base + (uint32_t)t + 1u);
               else
-                st_tagged(dst, __uint_as_float(word), base + (uint32_t)t + 1u);
+                st_tagged(xdst, __uint_as_float(word), base + (uint32_t)t + 1u);
             }
           } else if (REMOTE) {
-            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * p.H + lane_xh;
             if (xcd_local)
-              st_tagged_xcd(dst, hq, base + (uint32_t)t + 1u);
+              st_tagged_xcd(xdst, hq, base + (uint32_t)t + 1u);
             else
-              st_tagged(dst, hq, base + (uint32_t)t + 1u);
+              st_tagged(xdst, hq, base + (uint32_t)t + 1u);
           } else {
             hst[(buf ^ 1) * p.hsz + il_index(s, unit - klo)] = hq;  // local mode: RB == 1
           }
         }
       }
-      if (mine) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = dead ? __builtin_nanf("") : hn;
+      if (mine) *outp = dead ? __builtin_nanf("") : hn;
       if constexpr (SAVE) {
         // after the publish, off the step's dependent chain; non-temporal (read once, by the
         // backward)
