@@ -193,32 +193,42 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
 #pragma unroll
   for (int r = 0; r < 4; ++r) d[r] = idx[r] < H ? p.dout[(int64_t)(p.T - 1) * BH + (int64_t)b * H + idx[r]] : 0.0f;
   // The step's inputs (Cg for every gate; Zm, Mi and dout[t-1] for gate r)
-  // are loaded one step ahead, so their memory latency overlaps the layers.
-  float cgv[4], zmv[4], miv[4], dprev[4];
-  auto load_step = [&](int t, float (&c)[4], float (&z)[4], float (&m)[4], float (&dp)[4]) {
-    const int64_t row = (int64_t)t * p.B + b;
+  // sit in two register sets that take turns: a set is refilled, for two
+  // steps ahead, after the stores of the step that used it, so the wait for
+  // one set never covers the other set's loads. (With one set, loaded one
+  // step ahead at the top of the step, the wait before the step's first
+  // product covered the loads just issued, and each step paid a full memory
+  // latency.)
+  struct StepIn {
+    float c[4], z[4], m[4], dp[4];
+  };
+  // Every wave issues the same loads every step, at clamped addresses (the
+  // values a wave does not need are discarded), so that the number of memory
+  // operations between a set's loads and their use does not depend on the
+  // path and the compiler's wait can count the other set's loads.
+  auto load_step = [&](int t, StepIn& in) {
+    const int tc = t < 0 ? 0 : t;
+    const int64_t row = (int64_t)tc * p.B + b;
+    const int64_t rowp = (int64_t)(tc > 0 ? tc - 1 : 0) * p.B + b;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bool ok = idx[r] < H;
-      c[r] = ok ? p.cg[row * 3 * H + g * H + idx[r]] : 0.0f;
-      if (g == 0) {
-        z[r] = ok ? p.zm[row * H + idx[r]] : 0.0f;
-        m[r] = ok ? p.mi[row * H + idx[r]] : 0.0f;
-        dp[r] = (ok && t > 0) ? p.dout[(row - p.B) * H + idx[r]] : 0.0f;
-      }
+      const int ic = ok ? idx[r] : H - 1;
+      const float c = p.cg[row * 3 * H + g * H + ic];
+      const float z = p.zm[row * H + ic];
+      const float m = p.mi[row * H + ic];
+      const float dp = p.dout[rowp * H + ic];
+      in.c[r] = ok ? c : 0.0f;
+      in.z[r] = ok ? z : 0.0f;
+      in.m[r] = ok ? m : 0.0f;
+      in.dp[r] = (ok && tc > 0) ? dp : 0.0f;
     }
   };
-  load_step(p.T - 1, cgv, zmv, miv, dprev);
-  for (int t = p.T - 1; t >= 0; --t) {
+  auto step = [&](int t, StepIn& in) {
     const int64_t row = (int64_t)t * p.B + b;
     float x[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      x[r] = d[r] * cgv[r];
-      if (g == 0 && idx[r] < H) p.dsum[row * H + idx[r]] = d[r];
-    }
-    float ncg[4], nzm[4], nmi[4], ndp[4];
-    if (t > 0) load_step(t - 1, ncg, nzm, nmi, ndp);
+    for (int r = 0; r < 4; ++r) x[r] = d[r] * in.c[r];
     static_for<0, L>([&](auto S) {
       constexpr int s = L - 1 - S;
       if constexpr (L == 10 && s >= 8) {
@@ -254,27 +264,30 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
         {
 #pragma clang fp contract(off)
           via = (x[r] + ghs[1][idx[r]]) + ghs[2][idx[r]];
-          carry = zmv[r] * d[r] + miv[r] * via;
+          carry = in.z[r] * d[r] + in.m[r] * via;
         }
         if (idx[r] < H) {
+          p.dsum[row * H + idx[r]] = d[r];
           if (t == 0)
             p.dh0[(int64_t)b * H + idx[r]] = carry;
           else
-            dv[idx[r]] = dprev[r] + carry;
+            dv[idx[r]] = in.dp[r] + carry;
         }
       }
     }
     lds_barrier();
     if (t > 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        d[r] = idx[r] < H ? dv[idx[r]] : 0.0f;
-        cgv[r] = ncg[r];
-        zmv[r] = nzm[r];
-        miv[r] = nmi[r];
-        dprev[r] = ndp[r];
-      }
+      for (int r = 0; r < 4; ++r) d[r] = idx[r] < H ? dv[idx[r]] : 0.0f;
     }
+    load_step(t - 2, in);  // unconditional (see load_step); past step 0 it reloads step 0
+  };
+  StepIn in0, in1;
+  load_step(p.T - 1, in0);
+  if (p.T > 1) load_step(p.T - 2, in1);
+  for (int t = p.T - 1; t >= 0; t -= 2) {
+    step(t, in0);
+    if (t >= 1) step(t - 1, in1);
   }
 }
 
