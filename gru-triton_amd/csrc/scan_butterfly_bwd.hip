@@ -327,10 +327,30 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
       tpi[s][r] = e.t_pi;
       accd[s][r] = acco[s][r] = 0.0f;
     }
-  for (int64_t v = chunk; v < p.nvec; v += p.nchunk) {
+  // A vector's inputs (its hq row and its gradient row) sit in two register
+  // sets that take turns, each refilled for the vector after next once used,
+  // at clamped addresses so that every iteration issues the same loads; the
+  // wait for one set then never covers the other's loads. (Loaded at the top
+  // of each vector's iteration, every vector paid a full memory latency.)
+  struct VecIn {
+    float h[4], d[4];
+  };
+  auto load_vec = [&](int64_t v, VecIn& in) {
+    const int64_t vc = v < p.nvec ? v : p.nvec - 1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = idx[r] < H;
+      const int ic = ok ? idx[r] : H - 1;
+      const float h = p.hq[vc * H + ic];
+      const float d = g < 2 ? p.dgi[vc * 3 * H + g * H + ic] : p.dghn[vc * H + ic];
+      in.h[r] = ok ? h : 0.0f;
+      in.d[r] = ok ? d : 0.0f;
+    }
+  };
+  auto vec = [&](int64_t v, VecIn& in) {
     float a[L][4], ap[L][4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) a[0][r] = idx[r] < H ? p.hq[v * H + idx[r]] : 0.0f;
+    for (int r = 0; r < 4; ++r) a[0][r] = in.h[r];
     static_for<0, L>([&](auto S) {
       constexpr int s = S;
       partner_of<s>(a[s], ap[s], xch[s & 1], idx);
@@ -343,11 +363,7 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
     });
     float gv[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float d0 = 0.0f;
-      if (idx[r] < H) d0 = g < 2 ? p.dgi[v * 3 * H + g * H + idx[r]] : p.dghn[v * H + idx[r]];
-      gv[r] = d0;
-    }
+    for (int r = 0; r < 4; ++r) gv[r] = in.d[r];
     static_for<0, L>([&](auto S) {
       constexpr int s = L - 1 - S;
 #pragma unroll
@@ -365,6 +381,14 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
       }
     });
     lds_barrier();  // the next vector's exchanges reuse xch
+    load_vec(v + 2 * (int64_t)p.nchunk, in);
+  };
+  VecIn in0, in1;
+  load_vec(chunk, in0);
+  load_vec(chunk + p.nchunk, in1);
+  for (int64_t v = chunk; v < p.nvec; v += 2 * (int64_t)p.nchunk) {
+    vec(v, in0);
+    if (v + p.nchunk < p.nvec) vec(v + p.nchunk, in1);
   }
   float* out = p.part + ((int64_t)g * p.nchunk + chunk) * 2 * L * N;
 #pragma unroll
