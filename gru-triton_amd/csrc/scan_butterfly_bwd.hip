@@ -115,10 +115,27 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_batch(const fl
       tii[s][r] = e.t_ii;
       tip[s][r] = e.t_ip;
     }
-  for (int64_t v = blockIdx.x; v < nvec; v += gridDim.x) {
+  float bias[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) bias[r] = idx[r] < H ? bh[g * H + idx[r]] : 0.0f;
+  // A vector's hq row sits in one of two register sets that take turns, each
+  // refilled for the vector after next once used, at a clamped address so
+  // that every iteration issues the same loads (the wait for one set then
+  // never covers the other's loads)
+  const int64_t stride = gridDim.x;
+  auto load_vec = [&](int64_t v, float (&h)[4]) {
+    const int64_t vc = v < nvec ? v : nvec - 1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = idx[r] < H;
+      const float x = hq[vc * H + (ok ? idx[r] : H - 1)];
+      h[r] = ok ? x : 0.0f;
+    }
+  };
+  auto vec = [&](int64_t v, float (&h)[4]) {
     float x[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = idx[r] < H ? hq[v * H + idx[r]] : 0.0f;
+    for (int r = 0; r < 4; ++r) x[r] = h[r];
     static_for<0, L>([&](auto S) {
       constexpr int s = S;
       float y[4];
@@ -130,8 +147,16 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_batch(const fl
     });
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      if (idx[r] < H) gh[v * 3 * H + g * H + idx[r]] = x[r] + bh[g * H + idx[r]];
+      if (idx[r] < H) gh[v * 3 * H + g * H + idx[r]] = x[r] + bias[r];
     lds_barrier();  // the next vector's exchanges reuse xch
+    load_vec(v + 2 * stride, h);
+  };
+  float h0[4], h1[4];
+  load_vec(blockIdx.x, h0);
+  load_vec(blockIdx.x + stride, h1);
+  for (int64_t v = blockIdx.x; v < nvec; v += 2 * stride) {
+    vec(v, h0);
+    if (v + stride < nvec) vec(v + stride, h1);
   }
 }
 
@@ -401,26 +426,44 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
 }
 
 // dtw[g][0][s][pair][m][*] from the chunk sums of element i = the element
-// with that pair and m.
-__global__ void bfly_twiddle_sum(const float* part, float* dtw, int nchunk, int N, int L) {
+// with that pair and m. A workgroup takes 64 consecutive elements of one
+// gate's [L][N] (coalesced float2 loads); its four waves sum the chunks
+// c = ph mod 4 in a fixed order and the four partial sums are added in a
+// fixed order (deterministic; each thread used to walk all chunks alone,
+// latency bound: 104 us at config 4).
+constexpr int kTwSumPhases = 4;
+__global__ __launch_bounds__(64 * kTwSumPhases) void bfly_twiddle_sum(const float* part, float* dtw, int nchunk,
+                                                                    int N, int L) {
+  __shared__ float2 red[kTwSumPhases][64];
   const int64_t per_gate = (int64_t)L * N;
-  const int64_t n = 3 * per_gate;
-  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
-    const int g = (int)(e / per_gate);
-    const int64_t r = e - g * per_gate;
-    const int s = (int)(r / N), i = (int)(r - (int64_t)s * N);
-    float sd = 0.0f, so = 0.0f;
-    const float* src = part + ((int64_t)g * nchunk * per_gate + r) * 2;
-    for (int c = 0; c < nchunk; ++c) {
-      sd += src[(int64_t)c * per_gate * 2];
-      so += src[(int64_t)c * per_gate * 2 + 1];
+  const int o = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int64_t e = (int64_t)blockIdx.x * 64 + o;
+  const bool ok = e < 3 * per_gate;
+  const int g = ok ? (int)(e / per_gate) : 0;
+  const int64_t r = ok ? e - g * per_gate : 0;
+  float sd = 0.0f, so = 0.0f;
+  if (ok) {
+    const float2* src = reinterpret_cast<const float2*>(part) + ((int64_t)g * nchunk * per_gate + r);
+    for (int c = ph; c < nchunk; c += kTwSumPhases) {
+      const float2 v = src[(int64_t)c * per_gate];
+      sd += v.x;
+      so += v.y;
     }
-    const int m = (i >> s) & 1;
-    const int pair = ((i >> (s + 1)) << s) | (i & ((1 << s) - 1));
-    float* d = dtw + (int64_t)g * L * (N / 2) * 4 + ((int64_t)s * (N / 2) + pair) * 4 + 2 * m;
-    d[m] = sd;
-    d[1 - m] = so;
   }
+  red[ph][o] = make_float2(sd, so);
+  __syncthreads();
+  if (ph != 0 || !ok) return;
+#pragma unroll
+  for (int k = 1; k < kTwSumPhases; ++k) {
+    sd += red[k][o].x;
+    so += red[k][o].y;
+  }
+  const int s = (int)(r / N), i = (int)(r - (int64_t)s * N);
+  const int m = (i >> s) & 1;
+  const int pair = ((i >> (s + 1)) << s) | (i & ((1 << s) - 1));
+  float* d = dtw + (int64_t)g * L * (N / 2) * 4 + ((int64_t)s * (N / 2) + pair) * 4 + 2 * m;
+  d[m] = sd;
+  d[1 - m] = so;
 }
 
 struct NativePlan {
@@ -486,7 +529,7 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   hipLaunchKernelGGL(bfly_twiddle_grad<LOGN>, dim3((unsigned)pl.nchunk, 3), dim3((1 << LOGN) / 4), 0, stream, tp);
   GS_CHECK_HIP(hipGetLastError());
   const int64_t nsum = (int64_t)3 * LOGN * (1 << LOGN);
-  hipLaunchKernelGGL(bfly_twiddle_sum, dim3((unsigned)((nsum + 255) / 256)), dim3(256), 0, stream, part, a->dw_part,
+  hipLaunchKernelGGL(bfly_twiddle_sum, dim3((unsigned)((nsum + 63) / 64)), dim3(64 * kTwSumPhases), 0, stream, part, a->dw_part,
                      pl.nchunk, 1 << LOGN, LOGN);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
