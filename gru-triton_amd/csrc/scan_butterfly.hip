@@ -179,35 +179,52 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
     }
   }
 
-  float x[4], hraw[4], bias[3][4];
+  // The gate epilogue of element r of a lane runs on one of the three gate
+  // waves that hold it (they share a SIMD): r = 0, 1 on the r-gate wave, r = 2
+  // on the z-gate wave, r = 3 on the n-gate wave, so the three waves' epilogue
+  // chains interleave instead of one wave running all four. A wave's owned
+  // elements are its slots: slot 0 is element r0, slot 1 (r-gate wave only)
+  // element 1; the raw h, biases and gate inputs are kept per slot.
+  auto owns = [&](int r) { return r < 2 ? g == 0 : g == r - 1; };
+  const int nslot = g == 0 ? 2 : 1;
+  const int r0 = g == 0 ? 0 : g + 1;
+  const int ie[2] = {idx[r0], idx[1]};
+  float x[4], hraw[2], bias[3][2];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int i = idx[r];
     const float h = (i < H) ? p.h0[(int64_t)b * p.sh0_b + i] : 0.0f;
-    hraw[r] = h;
     x[r] = (i < H && p.qin.on) ? fake_quant(h, p.qin) : h;
+  }
 #pragma unroll
-    for (int q = 0; q < 3; ++q) bias[q][r] = (i < H) ? gate_scale(q) * p.bh[q * H + i] : 0.0f;  // for gru_update_gb
+  for (int k = 0; k < 2; ++k) {
+    const int i = ie[k];
+    hraw[k] = (i < H) ? p.h0[(int64_t)b * p.sh0_b + i] : 0.0f;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) bias[q][k] = (i < H) ? gate_scale(q) * p.bh[q * H + i] : 0.0f;  // for gru_update_gb
   }
 
-  // The gate epilogue of element r of a lane runs on one of the three gate
-  // waves that hold it (they share a SIMD): r = 0, 1 on the r-gate wave, r = 2
-  // on the z-gate wave, r = 3 on the n-gate wave, so the three waves' epilogue
-  // chains interleave instead of one wave running all four.
-  auto owns = [&](int r) { return r < 2 ? g == 0 : g == r - 1; };
-  for (int t = 0; t < p.T; ++t) {
-    // gate inputs of the owned elements (padding elements read element H-1's
-    // and discard their result)
-    float gir[4], giz[4], gin[4];
+  // Gate inputs of the slots sit in two register sets that take turns: a
+  // set is refilled for two steps ahead after the step that used it, with
+  // the same loads every step (clamped step and element; padding elements
+  // read element H-1's and discard the result), so the wait for one set never
+  // covers the other set's loads. (Loaded at the top of the step under the
+  // ownership test, the loads were sunk next to their use in the epilogue,
+  // and each step paid a memory latency there.)
+  struct GiSet {
+    float v[3][2];
+  };
+  const float* gib = p.gi + (int64_t)b * p.sg_b;
+  auto load_gi = [&](int t, GiSet& gs_) {
+    const int tc = t < p.T ? t : p.T - 1;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (owns(r)) {
-        const float* gp = p.gi + (int64_t)t * p.sg_t + (int64_t)b * p.sg_b + min(idx[r], H - 1);
-        gir[r] = gp[0];
-        giz[r] = gp[H];
-        gin[r] = gp[2 * H];
-      }
+    for (int k = 0; k < 2; ++k) {
+      const float* gp = gib + (int64_t)tc * p.sg_t + min(ie[k], H - 1);
+#pragma unroll
+      for (int q = 0; q < 3; ++q) gs_.v[q][k] = gp[q * H];
     }
+  };
+  auto step = [&](int t, GiSet& gs_) {
     int xsel = 0;
     static_for<0, L>([&](auto S) {
       constexpr int s = S;
@@ -253,18 +270,20 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
       if (!owns(r)) ghs[g][idx[r]] = x[r];  // what the owner of r reads
     lds_barrier();
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (!owns(r)) continue;
-      const int i = idx[r];
-      const float ghr = g == 0 ? x[r] : ghs[0][i];
-      const float ghz = g == 1 ? x[r] : ghs[1][i];
-      const float ghn = g == 2 ? x[r] : ghs[2][i];
-      float hn = gru_update_gb(gir[r], giz[r], gin[r], ghr, ghz, ghn, bias[0][r], bias[1][r], bias[2][r], hraw[r]);
+    for (int k = 0; k < 2; ++k) {
+      if (k >= nslot) continue;
+      const int i = ie[k];
+      const float xv = k == 1 ? x[1] : g == 0 ? x[0] : g == 1 ? x[2] : x[3];
+      const float ghr = g == 0 ? xv : ghs[0][i];
+      const float ghz = g == 1 ? xv : ghs[1][i];
+      const float ghn = g == 2 ? xv : ghs[2][i];
+      float hn = gru_update_gb(gs_.v[0][k], gs_.v[1][k], gs_.v[2][k], ghr, ghz, ghn, bias[0][k], bias[1][k],
+                               bias[2][k], hraw[k]);
       if (p.qout.on) hn = fake_quant(hn, p.qout);
       float hq = 0.0f;
       if (i < H) {
         p.out[(int64_t)t * p.so_t + (int64_t)b * p.so_b + i] = hn;
-        hraw[r] = hn;
+        hraw[k] = hn;
         hq = (p.qin.on && p.qin_after_first) ? fake_quant(hn, p.qin) : hn;
       }
       hqs[i] = hq;
@@ -272,6 +291,14 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
     lds_barrier();
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[r] = hqs[idx[r]];
+    load_gi(t + 2, gs_);
+  };
+  GiSet gs0, gs1;
+  load_gi(0, gs0);
+  load_gi(1, gs1);
+  for (int t = 0; t < p.T; t += 2) {
+    step(t, gs0);
+    if (t + 1 < p.T) step(t + 1, gs1);
   }
 }
 
