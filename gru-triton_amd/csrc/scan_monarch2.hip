@@ -249,10 +249,18 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
       const float gir = gs_[0], giz = gs_[U], gin = gs_[2 * U];
       float* hkp = hk + (rbl * 4 + sl) * KS + iec;
       const float hprev = *hkp;
-      // keep these reads ahead of phase 2 (the scheduler would sink them below its MFMAs)
+      // flags[1] as staged for this iteration, read as a vector value and made
+      // uniform after phase 2: after a give-up the workgroup's outputs are NaN
+      // and it publishes nothing more
+      const int fl_v = flags[1];
+      // the step's store addresses
+      const int row = 4 * rb + sl;
+      float* const outp = p.out + (int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out;
+      uint64_t* const xdst = PM > 0 ? p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb + sl) * (H / 4) + b * p.nq + qd
+                                    : p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * H + lane_xh;
+      // keep these reads and addresses ahead of phase 2 (the scheduler would
+      // sink them below its MFMAs, onto the step's chain)
       __builtin_amdgcn_sched_barrier(0);
-      // after a give-up the workgroup's outputs are NaN and it publishes nothing more
-      const int fl = __builtin_amdgcn_readfirstlane(flags[1]);
       // phase 2: L_g[b] times the staged z_g
       float gh[3];
       {
@@ -272,7 +280,7 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
 #pragma unroll
         for (int g = 0; g < 3; ++g) gh[g] = slice_sum(acc[g], sl);
       }
-      const int row = 4 * rb + sl;
+      const int fl = __builtin_amdgcn_readfirstlane(fl_v);
       const bool dead = (fl & 2) != 0;
       if (qok) {
         float hn = gru_update_gb(gir, giz, gin, gh[0], gh[1], gh[2], bias[0], bias[1], bias[2], hprev);
@@ -281,7 +289,6 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
           lv = quant_level(hn, p.qout);
           hn = lv * p.qout.scale;
         }
-        if (row < p.B) p.out[(int64_t)t * p.so_t + (int64_t)(4 * rb) * p.so_b + lane_out] = dead ? __builtin_nanf("") : hn;
         *hkp = hn;
         if (t + 1 < p.T && !dead) {
           float hq = hn;
@@ -299,21 +306,21 @@ __global__ __launch_bounds__(NT) void monarch2_fused_kernel(M2FParams p) {
             const int c2 = __builtin_amdgcn_mov_dpp(c, 0xAA, 0xF, 0xF, true);
             const int c3 = __builtin_amdgcn_mov_dpp(c, 0xFF, 0xF, 0xF, true);
             const uint32_t word = (uint32_t)c0 | ((uint32_t)c1 << 8) | ((uint32_t)c2 << 16) | ((uint32_t)c3 << 24);
-            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb + sl) * (H / 4) + b * p.nq + qd;
             if (j == 0) {
               if (xl)
-                st_tagged_xcd(dst, __uint_as_float(word), tag);
+                st_tagged_xcd(xdst, __uint_as_float(word), tag);
               else
-                st_tagged(dst, __uint_as_float(word), tag);
+                st_tagged(xdst, __uint_as_float(word), tag);
             }
           } else {
-            uint64_t* dst = p.xh + ((int64_t)(t & 1) * p.Bp + 4 * rb) * H + lane_xh;
             if (xl)
-              st_tagged_xcd(dst, hq, tag);
+              st_tagged_xcd(xdst, hq, tag);
             else
-              st_tagged(dst, hq, tag);
+              st_tagged(xdst, hq, tag);
           }
         }
+        // the output store after the publish, off the exchange's chain
+        if (row < p.B) *outp = dead ? __builtin_nanf("") : hn;
       }
       if (lane == 0) __hip_atomic_fetch_add(&flags[0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       lds_barrier();
