@@ -227,10 +227,10 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
   struct StepIn {
     float c[4], z[4], m[4], dp[4];
   };
-  // Every wave issues the same loads every step, at clamped addresses (the
-  // values a wave does not need are discarded), so that the number of memory
-  // operations between a set's loads and their use does not depend on the
-  // path and the compiler's wait can count the other set's loads.
+  // Every wave issues its Cg loads every step, at clamped addresses, first;
+  // the gate-r waves then load Zm, Mi and dout[t-1], which only they use. So
+  // at least a set's Cg loads lie between the other set's loads and their
+  // use on every path, and the compiler's wait can count them.
   auto load_step = [&](int t, StepIn& in) {
     const int tc = t < 0 ? 0 : t;
     const int64_t row = (int64_t)tc * p.B + b;
@@ -240,13 +240,18 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
       const bool ok = idx[r] < H;
       const int ic = ok ? idx[r] : H - 1;
       const float c = p.cg[row * 3 * H + g * H + ic];
-      const float z = p.zm[row * H + ic];
-      const float m = p.mi[row * H + ic];
-      const float dp = p.dout[rowp * H + ic];
       in.c[r] = ok ? c : 0.0f;
-      in.z[r] = ok ? z : 0.0f;
-      in.m[r] = ok ? m : 0.0f;
-      in.dp[r] = (ok && tc > 0) ? dp : 0.0f;
+    }
+    if (g == 0) {
+      // raw values (masked where they are used), so that the loads write the
+      // set's registers directly and nothing waits for them here
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ic = idx[r] < H ? idx[r] : H - 1;
+        in.z[r] = p.zm[row * H + ic];
+        in.m[r] = p.mi[row * H + ic];
+        in.dp[r] = p.dout[rowp * H + ic];
+      }
     }
   };
   auto step = [&](int t, StepIn& in) {
@@ -296,7 +301,7 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
           if (t == 0)
             p.dh0[(int64_t)b * H + idx[r]] = carry;
           else
-            dv[idx[r]] = in.dp[r] + carry;
+            dv[idx[r]] = in.dp[r] + carry;  // t > 0 here, so dout[t-1] was loaded
         }
       }
     }
