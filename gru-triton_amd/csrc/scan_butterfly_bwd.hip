@@ -13,12 +13,12 @@
 // Batch rows never interact, so one workgroup owns one row for all T steps
 // and applies the transposed stages in reverse order in LDS, with no
 // exchange between workgroups. The launcher runs
-//   1. build_prev_state: hq = q_in([h0; out[0..T-2]]);
-//   2. bfly_apply_batch: gh of every (t, b) at once (the forward's stages on hq);
-//   3. the dense backward's coefficient pass;
-//   4. bfly_bwd_kernel: the recurrence, writing D_t and dh0;
-//   5. the dense backward's gradient pass: dgi, dgh_n, per-row dbh;
-//   6. bfly_twiddle_grad: for every (t, b) and gate, the stages run forward on
+//   1. bfly_apply_coef: for every (t, b) at once, hq = q_in(h_{t-1}) and gh
+//      (the forward's stages on hq, kept in LDS), then the dense backward's
+//      coefficient planes from gi, gh and h_{t-1}, and hq;
+//   2. bfly_bwd_kernel: the recurrence, writing D_t and dh0;
+//   3. the dense backward's gradient pass: dgi, dgh_n, per-row dbh;
+//   4. bfly_twiddle_grad: for every (t, b) and gate, the stages run forward on
 //      hq (activations A_j kept in LDS) and dgh runs backward through them
 //      (G_j); stage j's twiddles collect the dots of G_{j+1} with A_j (own
 //      element for the diagonal twiddle, the partner for the other) in
@@ -31,8 +31,6 @@
 
 namespace gs {
 
-int launch_coef(const gs_bwd_args* a, float* cg, float* cgn, float* zm, float* mi, hipStream_t stream,
-                float* hq = nullptr);
 int grad_chunks(int64_t T);
 int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
                 float* dgh, float* chunks, hipStream_t stream, const char* who, SumJob* dbh_sum = nullptr);
@@ -93,20 +91,48 @@ struct Lay {
   static constexpr int WPG = N / 256;  // waves per gate vector
 };
 
-// gh[v][g H + i] = [S_L ... S_1 hq[v]]_i + bh[g H + i] for every vector v:
-// 3 WPG waves, one gate per WPG of them.
+struct CoefParams {
+  const float* tw;
+  const float* bh;
+  const float* gi;   // [T, B, 3H], strides sg_t, sg_b
+  const float* h0;   // [B, H], stride sh0_b
+  const float* out;  // [T, B, H], steps back to back: row m = t B + b at out + m so_b
+  float* hq;         // [T B, H] q_in(h_{t-1})
+  float* cg;         // [T B, 3H] (Cr, Cz, Chn)
+  float* cgn;        // [T B, H]
+  float* zm;         // [T B, H]
+  float* mi;         // [T B, H]
+  int64_t sg_t, sg_b, sh0_b, so_b, nvec;
+  int B, H;
+  Quant qin, qout;
+};
+
+// For every vector v = t B + b: h_{t-1} (h0 at t = 0) and hq = q_in(h_{t-1}),
+// gh_g = [S_L ... S_1 hq]_{:H} + bh_g on 3 WPG waves (one gate per WPG of
+// them), then the dense backward's coefficient planes of every element from
+// gi, gh and h_{t-1} (coef_kernel in scan_dense_bwd.hip, the same arithmetic),
+// and hq for the twiddle gradient. gh only passes through LDS. Element k's
+// coefficients are formed by one of the three waves that hold it: slot r of
+// wave w (elements lane + 64 r + 256 w) goes to gate (r + w) mod 3's wave, so
+// a wave owns slot sa = (g - w) mod 3, and slot 3 as well when sa = 0. Every
+// wave forms two slots; a wave that owns one forms it twice. Lanes past H take
+// element H - 1 in place of theirs (clamped loads, LDS reads and stores), so
+// all lanes holding an address store the same bits there and no store is
+// masked: every iteration issues the same memory operations on every path,
+// and the waits for one register set never cover the stores or the other
+// set's loads.
 template <int LOGN>
-__global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_batch(const float* hq, const float* tw,
-                                                                        const float* bh, float* gh, int64_t nvec,
-                                                                        int H) {
+__global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParams p) {
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
   __shared__ float xch[2][3][N];
+  __shared__ float ghs[2][3][N];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = wv / WPG, w = wv - g * WPG;
+  const int H = p.H;
   int idx[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) idx[r] = lane + 64 * r + 256 * w;
   float tii[L][4], tip[L][4];
-  const float* tw_g = tw + (int64_t)g * L * (N / 2) * 4;
+  const float* tw_g = p.tw + (int64_t)g * L * (N / 2) * 4;
 #pragma unroll
   for (int s = 0; s < L; ++s)
 #pragma unroll
@@ -117,25 +143,55 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_batch(const fl
     }
   float bias[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) bias[r] = idx[r] < H ? bh[g * H + idx[r]] : 0.0f;
-  // A vector's hq row sits in one of two register sets that take turns, each
-  // refilled for the vector after next once used, at a clamped address so
-  // that every iteration issues the same loads (the wait for one set then
-  // never covers the other's loads)
+  for (int r = 0; r < 4; ++r) bias[r] = idx[r] < H ? p.bh[g * H + idx[r]] : 0.0f;
+  const int sa = (g - w % 3 + 3) % 3;
+  const bool two = sa == 0;
+  const int ka = lane + 64 * sa + 256 * w;
+  const int kb = lane + 192 + 256 * w;  // slot 3, used when two
+  const int kac = ka < H ? ka : H - 1, kbc = !two ? kac : kb < H ? kb : H - 1;
+  // A vector's inputs (h_{t-1} at the lane's elements, gi at its coefficient
+  // slots) sit in one of two register sets that take turns, each refilled for
+  // the vector after next once used, at clamped addresses so that every
+  // iteration issues the same loads (the wait for one set then never covers
+  // the other's loads). Values are raw; lanes past H are masked at use.
+  struct VecIn {
+    float h[4], ga[3], gb[3];
+  };
   const int64_t stride = gridDim.x;
-  auto load_vec = [&](int64_t v, float (&h)[4]) {
-    const int64_t vc = v < nvec ? v : nvec - 1;
+  // Rows are addressed through buffer resources built per vector in scalar
+  // registers, with 32-bit per-lane offsets that stay fixed across vectors.
+  auto load_vec = [&](int64_t v, VecIn& in) {
+    const int64_t vc = v < p.nvec ? v : p.nvec - 1;
+    const auto hr = raw_rsrc(vc >= p.B ? p.out + (vc - p.B) * p.so_b : p.h0 + vc * p.sh0_b);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool ok = idx[r] < H;
-      const float x = hq[vc * H + (ok ? idx[r] : H - 1)];
-      h[r] = ok ? x : 0.0f;
+    for (int r = 0; r < 4; ++r) in.h[r] = buf_ld(hr, 4u * (idx[r] < H ? idx[r] : H - 1), 0);
+    const uint32_t t = (uint32_t)vc / (uint32_t)p.B, b = (uint32_t)vc - t * (uint32_t)p.B;  // nvec < 2^31
+    const auto gr = raw_rsrc(p.gi + t * p.sg_t + b * p.sg_b);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      in.ga[q] = buf_ld(gr, 4u * kac, 4u * q * H);
+      in.gb[q] = buf_ld(gr, 4u * kbc, 4u * q * H);
     }
   };
-  auto vec = [&](int64_t v, float (&h)[4]) {
+  auto coef = [&](const float(&gs)[3][N], int64_t v, int k, const float(&gv)[3], float hp) {
+    const GateGrad gg = gru_backward(gv[0], gv[1], gv[2], gs[0][k], gs[1][k], gs[2][k], hp, 1.0f, p.qout);
+    const auto cr = raw_rsrc(p.cg + v * 3 * H);
+    buf_st(cr, 4u * k, 0, gg.dgr);
+    buf_st(cr, 4u * k, 4u * H, gg.dgz);
+    buf_st(cr, 4u * k, 8u * H, gg.dghn);
+    buf_st(raw_rsrc(p.cgn + v * H), 4u * k, 0, gg.dgn);
+    buf_st(raw_rsrc(p.zm + v * H), 4u * k, 0, gg.dh_direct);
+    buf_st(raw_rsrc(p.mi + v * H), 4u * k, 0, (p.qin.on && !quant_keeps(hp, p.qin)) ? 0.0f : 1.0f);
+    buf_st(raw_rsrc(p.hq + v * H), 4u * k, 0, p.qin.on ? fake_quant(hp, p.qin) : hp);
+  };
+  auto vec = [&](int64_t v, VecIn& in, float(&gs)[3][N]) {
+    v = v < p.nvec ? v : p.nvec - 1;  // past the end: vector nvec - 1 again, the same bits to the same places
     float x[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = h[r];
+    for (int r = 0; r < 4; ++r) {
+      const float hp = idx[r] < H ? in.h[r] : 0.0f;
+      x[r] = p.qin.on ? fake_quant(hp, p.qin) : hp;
+    }
     static_for<0, L>([&](auto S) {
       constexpr int s = S;
       float y[4];
@@ -146,17 +202,24 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_batch(const fl
       }
     });
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (idx[r] < H) gh[v * 3 * H + g * H + idx[r]] = x[r] + bias[r];
-    lds_barrier();  // the next vector's exchanges reuse xch
-    load_vec(v + 2 * stride, h);
+    for (int r = 0; r < 4; ++r) gs[g][idx[r]] = x[r] + bias[r];
+    // gs of this vector is read below; its next writer (the vector after
+    // next) first passes the next vector's barrier, which every thread
+    // reaches after these reads. The barrier also orders xch's reuse.
+    lds_barrier();
+    const float hpa = sa == 0 ? in.h[0] : sa == 1 ? in.h[1] : in.h[2];
+    coef(gs, v, kac, in.ga, hpa);
+    coef(gs, v, kbc, in.gb, two ? in.h[3] : hpa);
+    load_vec(v + 2 * stride, in);
   };
-  float h0[4], h1[4];
-  load_vec(blockIdx.x, h0);
-  load_vec(blockIdx.x + stride, h1);
-  for (int64_t v = blockIdx.x; v < nvec; v += 2 * stride) {
-    vec(v, h0);
-    if (v + stride < nvec) vec(v + stride, h1);
+  VecIn in0, in1;
+  load_vec(blockIdx.x, in0);
+  load_vec(blockIdx.x + stride, in1);
+  // both vectors of a pair unconditionally, so that no branch skips memory
+  // operations (see the slots above)
+  for (int64_t v = blockIdx.x; v < p.nvec; v += 2 * stride) {
+    vec(v, in0, ghs[0]);
+    vec(v + stride, in1, ghs[1]);
   }
 }
 
@@ -485,7 +548,7 @@ NativePlan plan_native(const gs_bwd_args* a) {
   if (a->bfly_nblocks != 1 || a->log_n < 8 || a->log_n > 10) return pl;
   const int N = 1 << a->log_n;
   const int64_t H = a->H, TB = a->T * a->B;
-  if (N < H) return pl;
+  if (N < H || TB >= ((int64_t)1 << 31)) return pl;
   pl.nchunk = (int)std::max<int64_t>(1, std::min<int64_t>(TB, 256));
   pl.hq = align256(TB * H * 4);
   pl.cg = align256(TB * 3 * H * 4);
@@ -502,11 +565,28 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   constexpr int NT3 = 3 * (1 << LOGN) / 4;
   const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
   const int64_t TB = (int64_t)T * B;
-  hipLaunchKernelGGL(bfly_apply_batch<LOGN>, dim3((unsigned)std::min<int64_t>(TB, 2048)), dim3(NT3), 0, stream, hq,
-                     a->w, a->bh, cg, TB, H);
+  CoefParams cp;
+  cp.tw = a->w;
+  cp.bh = a->bh;
+  cp.gi = a->gi;
+  cp.h0 = a->h0;
+  cp.out = a->out;
+  cp.hq = hq;
+  cp.cg = cg;
+  cp.cgn = cgn;
+  cp.zm = zm;
+  cp.mi = mi;
+  cp.sg_t = a->sg_t;
+  cp.sg_b = a->sg_b;
+  cp.sh0_b = a->sh0_b;
+  cp.so_b = a->so_b;
+  cp.nvec = TB;
+  cp.B = B;
+  cp.H = H;
+  cp.qin = to_quant(a->q_in);
+  cp.qout = to_quant(a->q_out);
+  hipLaunchKernelGGL(bfly_apply_coef<LOGN>, dim3((unsigned)std::min<int64_t>(TB, 2048)), dim3(NT3), 0, stream, cp);
   GS_CHECK_HIP(hipGetLastError());
-  int rc = launch_coef(a, cg, cgn, zm, mi, stream);
-  if (rc) return rc;
   RecParams rp;
   rp.tw = a->w;
   rp.dout = a->dout;
@@ -520,7 +600,7 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   rp.H = H;
   hipLaunchKernelGGL(bfly_bwd_kernel<LOGN>, dim3((unsigned)B), dim3(NT3), 0, stream, rp);
   GS_CHECK_HIP(hipGetLastError());
-  rc = launch_grad(a, dsum, cg, cgn, dghn, nullptr, chunks, stream, who);
+  int rc = launch_grad(a, dsum, cg, cgn, dghn, nullptr, chunks, stream, who);
   if (rc) return rc;
   TwParams tp;
   tp.tw = a->w;
@@ -572,7 +652,6 @@ extern "C" int gs_butterfly_bwd(const gs_bwd_args* a, hipStream_t stream) {
   rc = check_scratch(a, pl.scratch(), who);
   if (rc) return rc;
 
-  const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
   char* cur = static_cast<char*>(a->scratch);
   auto take = [&](int64_t bytes) {
     char* r = cur;
@@ -589,8 +668,6 @@ extern "C" int gs_butterfly_bwd(const gs_bwd_args* a, hipStream_t stream) {
   float* chunks = take(pl.chunks);
   float* part = take(pl.part);
 
-  rc = build_prev_state(hq, a->h0, a->sh0_b, a->out, a->so_b, T, B, H, to_quant(a->q_in), stream, who);
-  if (rc) return rc;
   switch (a->log_n) {
     case 8: return launch_stages<8>(a, pl, hq, cg, cgn, zm, mi, dsum, dghn, chunks, part, stream, who);
     case 9: return launch_stages<9>(a, pl, hq, cg, cgn, zm, mi, dsum, dghn, chunks, part, stream, who);
