@@ -16,9 +16,9 @@
 //   1. bfly_apply_coef: for every (t, b) at once, hq = q_in(h_{t-1}) and gh
 //      (the forward's stages on hq, kept in LDS), then the dense backward's
 //      coefficient planes from gi, gh and h_{t-1}, and hq;
-//   2. bfly_bwd_kernel: the recurrence, writing D_t and dh0;
-//   3. the dense backward's gradient pass: dgi, dgh_n, per-row dbh;
-//   4. bfly_twiddle_grad: for every (t, b) and gate, the stages run forward on
+//   2. bfly_bwd_kernel: the recurrence, writing dh0 and the gradient planes
+//      as it forms them (dgi, dgh_n) and the per-row dbh sums;
+//   3. bfly_twiddle_grad: for every (t, b) and gate, the stages run forward on
 //      hq (activations A_j kept in LDS) and dgh runs backward through them
 //      (G_j); stage j's twiddles collect the dots of G_{j+1} with A_j (own
 //      element for the diagonal twiddle, the partner for the other) in
@@ -31,9 +31,6 @@
 
 namespace gs {
 
-int grad_chunks(int64_t T);
-int launch_grad(const gs_bwd_args* a, const float* dsum, const float* cg, const float* cgn, float* dghn,
-                float* dgh, float* chunks, hipStream_t stream, const char* who, SumJob* dbh_sum = nullptr);
 int64_t struct_bwd_workspace_bytes(int kind, const gs_bwd_args* a);
 int64_t struct_bwd_scratch_bytes(int kind, const gs_bwd_args* a);
 int run_struct(int kind, const gs_bwd_args* a, hipStream_t stream, const char* who);
@@ -126,7 +123,9 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
   __shared__ float xch[2][3][N];
   __shared__ float ghs[2][3][N];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = wv / WPG, w = wv - g * WPG;
+  // the wave index read into a scalar register, so that per-gate choices are scalar
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = wv / WPG,
+            w = wv - g * WPG;
   const int H = p.H;
   int idx[4];
 #pragma unroll
@@ -227,25 +226,40 @@ struct RecParams {
   const float* tw;
   const float* dout;  // [T, B, H]
   const float* cg;    // [T B, 3H] (Cr, Cz, Chn)
+  const float* cgn;   // [T B, H]
   const float* zm;    // [T B, H]
   const float* mi;    // [T B, H]
-  float* dsum;        // [T B, H] D_t
+  float* dgi;         // [T B, 3H] D_t (Cr, Cz, Cgn)
+  float* dghn;        // [T B, H] D_t Chn
+  float* dbh_part;    // [B, 3H] sum over t of D_t (Cr, Cz, Chn)
   float* dh0;         // [B, H]
   int T, B, H;
 };
 
+// A buffer resource over `bytes` bytes at `base`: an access at a byte offset
+// of `bytes` or more reads 0 or is dropped (the hardware's range check), so
+// a lane past the end stores nothing without a branch around the store.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
+}
+constexpr uint32_t kOffNone = 0x80000000u;  // a byte offset past every bounded_rsrc
+
 // One workgroup per batch row b for all T steps, the forward's wave layout.
-// Per step: each gate's waves form v_g = D_t Cg_t on their elements and run
-// the transposed layers from L-1 down to 0; gates z and n hand their results
-// to the gate-r waves through LDS, which form the carry and D_{t-1} and
-// broadcast it back.
+// Per step: each gate's waves form v_g = D_t Cg_t on their elements, store
+// it as the step's gradient (the dense backward's grad_kernel: dgi_r, dgi_z,
+// and dgh_n with dgi_n = D_t Cgn for gate n; the same products) and add it to
+// the row's dbh sum, then run the transposed layers from L-1 down to 0;
+// gates z and n hand their results to the gate-r waves through LDS, which
+// form the carry and D_{t-1} and broadcast it back.
 template <int LOGN>
 __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams p) {
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
   __shared__ float xch[2][3][N];
   __shared__ float ghs[3][N];
   __shared__ float dv[N];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, g = wv / WPG, w = wv - g * WPG;
+  // the wave index read into a scalar register, so that per-gate choices are scalar
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = wv / WPG,
+            w = wv - g * WPG;
   const int H = p.H, b = blockIdx.x;
   int idx[4];
 #pragma unroll
@@ -277,9 +291,17 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
     }
   }
   const int64_t BH = (int64_t)p.B * H;
+  // Steps run in pairs, t0 and t0 - 1 down to 1 and 0, with no condition
+  // between them (a skippable second step would leave the wait at the top of
+  // the loop unable to count the other set's loads). An odd T starts at the
+  // step t0 = T past the end with D_T = 0: its products are zero, its
+  // gradient stores are dropped (a zero-size store resource), and it forms
+  // D_{T-1} = dout[T-1] + 0 as the carry.
+  const int t0 = (p.T & 1) ? p.T : p.T - 1;
   float d[4];  // D_t of this lane's elements
 #pragma unroll
-  for (int r = 0; r < 4; ++r) d[r] = idx[r] < H ? p.dout[(int64_t)(p.T - 1) * BH + (int64_t)b * H + idx[r]] : 0.0f;
+  for (int r = 0; r < 4; ++r)
+    d[r] = idx[r] < H && t0 < p.T ? p.dout[(int64_t)(p.T - 1) * BH + (int64_t)b * H + idx[r]] : 0.0f;
   // The step's inputs (Cg for every gate; Zm, Mi and dout[t-1] for gate r)
   // sit in two register sets that take turns: a set is refilled, for two
   // steps ahead, after the stores of the step that used it, so the wait for
@@ -290,38 +312,63 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
   struct StepIn {
     float c[4], z[4], m[4], dp[4];
   };
+  // (gate n keeps Cgn in the set's z registers; it never reads Zm.)
   // Every wave issues its Cg loads every step, at clamped addresses, first;
-  // the gate-r waves then load Zm, Mi and dout[t-1], which only they use. So
-  // at least a set's Cg loads lie between the other set's loads and their
-  // use on every path, and the compiler's wait can count them.
+  // the gate-r waves then load Zm, Mi and dout[t-1], and the gate-n waves
+  // Cgn, which only they use. So at least a set's Cg loads lie between the
+  // other set's loads and their use on every path, and the compiler's wait
+  // can count them. Loaded values are masked where they are used, not here:
+  // a select after the load would wait for it.
+  const float* const zs = g == 0 ? p.zm : p.cgn;
   auto load_step = [&](int t, StepIn& in) {
-    const int tc = t < 0 ? 0 : t;
+    const int tc = t < 0 ? 0 : t < p.T ? t : p.T - 1;
     const int64_t row = (int64_t)tc * p.B + b;
-    const int64_t rowp = (int64_t)(tc > 0 ? tc - 1 : 0) * p.B + b;
+    const int64_t rowp = (int64_t)(t > 0 ? t - 1 : 0) * p.B + b;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool ok = idx[r] < H;
-      const int ic = ok ? idx[r] : H - 1;
-      const float c = p.cg[row * 3 * H + g * H + ic];
-      in.c[r] = ok ? c : 0.0f;
+    for (int r = 0; r < 4; ++r) in.c[r] = p.cg[row * 3 * H + g * H + (idx[r] < H ? idx[r] : H - 1)];
+    // raw values (masked where they are used), so that the loads write the
+    // set's registers directly and nothing waits for them here; the z
+    // registers are loaded by one instruction sequence for both gates that
+    // use them (a plane chosen per wave), so no copy merges two loads
+    if (g != 1) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) in.z[r] = zs[row * H + (idx[r] < H ? idx[r] : H - 1)];
     }
     if (g == 0) {
-      // raw values (masked where they are used), so that the loads write the
-      // set's registers directly and nothing waits for them here
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int ic = idx[r] < H ? idx[r] : H - 1;
-        in.z[r] = p.zm[row * H + ic];
         in.m[r] = p.mi[row * H + ic];
         in.dp[r] = p.dout[rowp * H + ic];
       }
     }
   };
+  // per-lane byte offsets of the gradient stores, past the resource's end for
+  // lanes past H
+  uint32_t goff[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) goff[r] = idx[r] < H ? 4u * idx[r] : kOffNone;
+  float dbh[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   auto step = [&](int t, StepIn& in) {
-    const int64_t row = (int64_t)t * p.B + b;
+    const bool real = t < p.T;
+    const int64_t row = (int64_t)(real ? t : p.T - 1) * p.B + b;
+    const uint32_t gbytes = real ? 4u * H : 0u;
     float x[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = d[r] * in.c[r];
+    for (int r = 0; r < 4; ++r) x[r] = real && idx[r] < H ? d[r] * in.c[r] : 0.0f;
+    {
+      const auto gr = bounded_rsrc(p.dgi + row * 3 * H + g * H, gbytes);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dbh[r] += x[r];
+        buf_st(gr, goff[r], 0, g == 2 ? d[r] * in.z[r] : x[r]);
+      }
+      if (g == 2) {
+        const auto nr = bounded_rsrc(p.dghn + row * H, gbytes);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) buf_st(nr, goff[r], 0, x[r]);
+      }
+    }
     static_for<0, L>([&](auto S) {
       constexpr int s = L - 1 - S;
       if constexpr (L == 10 && s >= 8) {
@@ -360,7 +407,6 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
           carry = in.z[r] * d[r] + in.m[r] * via;
         }
         if (idx[r] < H) {
-          p.dsum[row * H + idx[r]] = d[r];
           if (t == 0)
             p.dh0[(int64_t)b * H + idx[r]] = carry;
           else
@@ -376,12 +422,15 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
     load_step(t - 2, in);  // unconditional (see load_step); past step 0 it reloads step 0
   };
   StepIn in0, in1;
-  load_step(p.T - 1, in0);
-  if (p.T > 1) load_step(p.T - 2, in1);
-  for (int t = p.T - 1; t >= 0; t -= 2) {
+  load_step(t0, in0);
+  load_step(t0 - 1, in1);
+  for (int t = t0; t >= 1; t -= 2) {
     step(t, in0);
-    if (t >= 1) step(t - 1, in1);
+    step(t - 1, in1);
   }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    if (idx[r] < H) p.dbh_part[(int64_t)b * 3 * H + g * H + idx[r]] = dbh[r];
 }
 
 struct TwParams {
@@ -537,8 +586,8 @@ __global__ __launch_bounds__(64 * kTwSumPhases) void bfly_twiddle_sum(const floa
 struct NativePlan {
   bool ok = false;
   int nchunk = 0;
-  int64_t hq, cg, plane, chunks, part;
-  int64_t scratch() const { return hq + cg + 5 * plane + chunks + part; }  // no tagged words
+  int64_t hq, cg, plane, part;
+  int64_t scratch() const { return hq + cg + 4 * plane + part; }  // no tagged words
 };
 
 NativePlan plan_native(const gs_bwd_args* a) {
@@ -553,7 +602,6 @@ NativePlan plan_native(const gs_bwd_args* a) {
   pl.hq = align256(TB * H * 4);
   pl.cg = align256(TB * 3 * H * 4);
   pl.plane = align256(TB * H * 4);
-  pl.chunks = align256((int64_t)grad_chunks(a->T) * a->B * 3 * H * 4);
   pl.part = align256((int64_t)3 * pl.nchunk * 2 * a->log_n * N * 4);
   pl.ok = true;
   return pl;
@@ -561,7 +609,7 @@ NativePlan plan_native(const gs_bwd_args* a) {
 
 template <int LOGN>
 int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* cg, float* cgn, float* zm, float* mi,
-                  float* dsum, float* dghn, float* chunks, float* part, hipStream_t stream, const char* who) {
+                  float* dghn, float* part, hipStream_t stream) {
   constexpr int NT3 = 3 * (1 << LOGN) / 4;
   const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
   const int64_t TB = (int64_t)T * B;
@@ -591,17 +639,18 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   rp.tw = a->w;
   rp.dout = a->dout;
   rp.cg = cg;
+  rp.cgn = cgn;
   rp.zm = zm;
   rp.mi = mi;
-  rp.dsum = dsum;
+  rp.dgi = a->dgi;
+  rp.dghn = dghn;
+  rp.dbh_part = a->dbh_part;
   rp.dh0 = a->dh0;
   rp.T = T;
   rp.B = B;
   rp.H = H;
   hipLaunchKernelGGL(bfly_bwd_kernel<LOGN>, dim3((unsigned)B), dim3(NT3), 0, stream, rp);
   GS_CHECK_HIP(hipGetLastError());
-  int rc = launch_grad(a, dsum, cg, cgn, dghn, nullptr, chunks, stream, who);
-  if (rc) return rc;
   TwParams tp;
   tp.tw = a->w;
   tp.hq = hq;
@@ -663,14 +712,12 @@ extern "C" int gs_butterfly_bwd(const gs_bwd_args* a, hipStream_t stream) {
   float* cgn = take(pl.plane);
   float* zm = take(pl.plane);
   float* mi = take(pl.plane);
-  float* dsum = take(pl.plane);
   float* dghn = take(pl.plane);
-  float* chunks = take(pl.chunks);
   float* part = take(pl.part);
 
   switch (a->log_n) {
-    case 8: return launch_stages<8>(a, pl, hq, cg, cgn, zm, mi, dsum, dghn, chunks, part, stream, who);
-    case 9: return launch_stages<9>(a, pl, hq, cg, cgn, zm, mi, dsum, dghn, chunks, part, stream, who);
-    default: return launch_stages<10>(a, pl, hq, cg, cgn, zm, mi, dsum, dghn, chunks, part, stream, who);
+    case 8: return launch_stages<8>(a, pl, hq, cg, cgn, zm, mi, dghn, part, stream);
+    case 9: return launch_stages<9>(a, pl, hq, cg, cgn, zm, mi, dghn, part, stream);
+    default: return launch_stages<10>(a, pl, hq, cg, cgn, zm, mi, dghn, part, stream);
   }
 }
