@@ -26,6 +26,8 @@
 //      bfly_twiddle_sum.
 // Shapes whose LDS needs exceed the device limit fall back to the
 // materialized-map backward (scan_struct_bwd.hip).
+#include <mutex>
+
 #include "gs_gemm.h"
 #include "gs_mfma.h"
 
@@ -233,7 +235,10 @@ struct RecParams {
   float* dghn;        // [T B, H] D_t Chn
   float* dbh_part;    // [B, 3H] sum over t of D_t (Cr, Cz, Chn)
   float* dh0;         // [B, H]
+  float* dcar;        // [B, H] D_{t_lo - 1} handed from one span's launch to the next
   int T, B, H;
+  int t_hi, t_lo;     // this launch's steps, t_hi down to t_lo (an even count)
+  int first;          // t_hi is the first step (dbh starts at 0, D from dout[T-1])
 };
 
 // A buffer resource over `bytes` bytes at `base`: an access at a byte offset
@@ -291,17 +296,21 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
     }
   }
   const int64_t BH = (int64_t)p.B * H;
-  // Steps run in pairs, t0 and t0 - 1 down to 1 and 0, with no condition
-  // between them (a skippable second step would leave the wait at the top of
-  // the loop unable to count the other set's loads). An odd T starts at the
-  // step t0 = T past the end with D_T = 0: its products are zero, its
-  // gradient stores are dropped (a zero-size store resource), and it forms
-  // D_{T-1} = dout[T-1] + 0 as the carry.
-  const int t0 = (p.T & 1) ? p.T : p.T - 1;
+  // Steps run in pairs, from t_hi down to t_lo, with no condition between
+  // them (a skippable second step would leave the wait at the top of the
+  // loop unable to count the other set's loads). An odd T starts at the step
+  // T past the end with D_T = 0: its products are zero, its gradient stores
+  // are dropped (a zero-size store resource), and it forms
+  // D_{T-1} = dout[T-1] + 0 as the carry. A launch covers one span of steps;
+  // the next span's launch continues from D_{t_lo - 1} in dcar and from the
+  // dbh sums so far.
+  const int t0 = p.t_hi;
   float d[4];  // D_t of this lane's elements
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    d[r] = idx[r] < H && t0 < p.T ? p.dout[(int64_t)(p.T - 1) * BH + (int64_t)b * H + idx[r]] : 0.0f;
+  for (int r = 0; r < 4; ++r) {
+    const float* src = p.first ? p.dout + (int64_t)(p.T - 1) * BH + (int64_t)b * H : p.dcar + (int64_t)b * H;
+    d[r] = idx[r] < H && t0 < p.T ? src[idx[r]] : 0.0f;
+  }
   // The step's inputs (Cg for every gate; Zm, Mi and dout[t-1] for gate r)
   // sit in two register sets that take turns: a set is refilled, for two
   // steps ahead, after the stores of the step that used it, so the wait for
@@ -348,7 +357,9 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
   uint32_t goff[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) goff[r] = idx[r] < H ? 4u * idx[r] : kOffNone;
-  float dbh[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float dbh[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) dbh[r] = idx[r] < H && !p.first ? p.dbh_part[(int64_t)b * 3 * H + g * H + idx[r]] : 0.0f;
   auto step = [&](int t, StepIn& in) {
     const bool real = t < p.T;
     const int64_t row = (int64_t)(real ? t : p.T - 1) * p.B + b;
@@ -424,13 +435,17 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
   StepIn in0, in1;
   load_step(t0, in0);
   load_step(t0 - 1, in1);
-  for (int t = t0; t >= 1; t -= 2) {
+  for (int t = t0; t > p.t_lo; t -= 2) {
     step(t, in0);
     step(t - 1, in1);
   }
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-    if (idx[r] < H) p.dbh_part[(int64_t)b * 3 * H + g * H + idx[r]] = dbh[r];
+  for (int r = 0; r < 4; ++r) {
+    if (idx[r] < H) {
+      p.dbh_part[(int64_t)b * 3 * H + g * H + idx[r]] = dbh[r];
+      if (g == 0 && p.t_lo > 0) p.dcar[(int64_t)b * H + idx[r]] = d[r];  // D_{t_lo - 1}
+    }
+  }
 }
 
 struct TwParams {
@@ -439,8 +454,9 @@ struct TwParams {
   const float* dgi;   // [TB, 3H] (r, z parts are dgh's)
   const float* dghn;  // [TB, H]
   float* part;        // [3][nchunk][L][N][2]
-  int64_t nvec;
+  int64_t v_lo, v_hi; // this launch's vectors
   int nchunk, H;
+  int first;          // the first launch writes part; later ones add to it
 };
 
 // Workgroup (chunk, gate) of WPG waves, the forward's lane layout: for
@@ -478,7 +494,7 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
     float h[4], d[4];
   };
   auto load_vec = [&](int64_t v, VecIn& in) {
-    const int64_t vc = v < p.nvec ? v : p.nvec - 1;
+    const int64_t vc = v < p.v_hi ? v : p.v_hi - 1;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bool ok = idx[r] < H;
@@ -526,19 +542,24 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
     load_vec(v + 2 * (int64_t)p.nchunk, in);
   };
   VecIn in0, in1;
-  load_vec(chunk, in0);
-  load_vec(chunk + p.nchunk, in1);
-  for (int64_t v = chunk; v < p.nvec; v += 2 * (int64_t)p.nchunk) {
+  load_vec(p.v_lo + chunk, in0);
+  load_vec(p.v_lo + chunk + p.nchunk, in1);
+  for (int64_t v = p.v_lo + chunk; v < p.v_hi; v += 2 * (int64_t)p.nchunk) {
     vec(v, in0);
-    if (v + p.nchunk < p.nvec) vec(v + p.nchunk, in1);
+    if (v + p.nchunk < p.v_hi) vec(v + p.nchunk, in1);
   }
-  float* out = p.part + ((int64_t)g * p.nchunk + chunk) * 2 * L * N;
+  float2* out = reinterpret_cast<float2*>(p.part) + ((int64_t)g * p.nchunk + chunk) * L * N;
 #pragma unroll
   for (int s = 0; s < L; ++s)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      out[((int64_t)s * N + idx[r]) * 2] = accd[s][r];
-      out[((int64_t)s * N + idx[r]) * 2 + 1] = acco[s][r];
+      float2 o = make_float2(accd[s][r], acco[s][r]);
+      if (!p.first) {
+        const float2 q = out[(int64_t)s * N + idx[r]];
+        o.x += q.x;
+        o.y += q.y;
+      }
+      out[(int64_t)s * N + idx[r]] = o;
     }
 }
 
@@ -586,9 +607,18 @@ __global__ __launch_bounds__(64 * kTwSumPhases) void bfly_twiddle_sum(const floa
 struct NativePlan {
   bool ok = false;
   int nchunk = 0;
-  int64_t hq, cg, plane, part;
-  int64_t scratch() const { return hq + cg + 4 * plane + part; }  // no tagged words
+  int64_t hq, cg, plane, part, dcar;
+  int64_t scratch() const { return hq + cg + 4 * plane + part + dcar; }  // no tagged words
 };
+
+// Twiddle-gradient workgroups per gate. 3 x 64 = 192 one-per-CU workgroups
+// leave 64 of the 256 CUs to the recurrence's one-per-CU row workgroups
+// (B = 64 at the headline shape), so the two run side by side.
+constexpr int kTwChunks = 64;
+// The recurrence runs in up to kSpans launches of an even number of steps
+// each; the twiddle gradient of a span runs on a second stream while the
+// recurrence works on the next span.
+constexpr int kSpans = 8;
 
 NativePlan plan_native(const gs_bwd_args* a) {
   NativePlan pl;
@@ -598,18 +628,46 @@ NativePlan plan_native(const gs_bwd_args* a) {
   const int N = 1 << a->log_n;
   const int64_t H = a->H, TB = a->T * a->B;
   if (N < H || TB >= ((int64_t)1 << 31)) return pl;
-  pl.nchunk = (int)std::max<int64_t>(1, std::min<int64_t>(TB, 256));
+  pl.nchunk = kTwChunks;
   pl.hq = align256(TB * H * 4);
   pl.cg = align256(TB * 3 * H * 4);
   pl.plane = align256(TB * H * 4);
   pl.part = align256((int64_t)3 * pl.nchunk * 2 * a->log_n * N * 4);
+  pl.dcar = align256(a->B * H * 4);
   pl.ok = true;
   return pl;
 }
 
+// A second stream per device for the twiddle gradient, and the events that
+// order it after each span of the recurrence (created on first use with the
+// device current; default priority). `mu` serializes the calls that use
+// them. When they cannot be created, everything runs on the caller's stream.
+struct Side {
+  std::mutex mu;
+  bool tried = false;
+  hipStream_t s = nullptr;
+  hipEvent_t ev[kSpans + 1] = {};
+};
+Side g_side[64];
+
+Side* side_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  Side& sd = g_side[dev];
+  std::lock_guard<std::mutex> lk(sd.mu);
+  if (!sd.tried) {
+    sd.tried = true;
+    bool ok = hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) == hipSuccess;
+    for (int k = 0; ok && k <= kSpans; ++k) ok = hipEventCreateWithFlags(&sd.ev[k], hipEventDisableTiming) == hipSuccess;
+    if (!ok) sd.s = nullptr;
+    (void)hipGetLastError();
+  }
+  return sd.s != nullptr ? &sd : nullptr;
+}
+
 template <int LOGN>
 int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* cg, float* cgn, float* zm, float* mi,
-                  float* dghn, float* part, hipStream_t stream) {
+                  float* dghn, float* part, float* dcar, hipStream_t stream) {
   constexpr int NT3 = 3 * (1 << LOGN) / 4;
   const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
   const int64_t TB = (int64_t)T * B;
@@ -646,25 +704,52 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   rp.dghn = dghn;
   rp.dbh_part = a->dbh_part;
   rp.dh0 = a->dh0;
+  rp.dcar = dcar;
   rp.T = T;
   rp.B = B;
   rp.H = H;
-  hipLaunchKernelGGL(bfly_bwd_kernel<LOGN>, dim3((unsigned)B), dim3(NT3), 0, stream, rp);
-  GS_CHECK_HIP(hipGetLastError());
   TwParams tp;
   tp.tw = a->w;
   tp.hq = hq;
   tp.dgi = a->dgi;
   tp.dghn = dghn;
   tp.part = part;
-  tp.nvec = TB;
   tp.nchunk = pl.nchunk;
   tp.H = H;
-  hipLaunchKernelGGL(bfly_twiddle_grad<LOGN>, dim3((unsigned)pl.nchunk, 3), dim3((1 << LOGN) / 4), 0, stream, tp);
-  GS_CHECK_HIP(hipGetLastError());
+  // Spans of the step range t0 .. 0 (t0 = T - 1, or T for an odd T: see the
+  // recurrence), each an even number of steps, latest first.
+  const int t0 = (T & 1) ? T : T - 1;
+  const int nsteps = t0 + 1;
+  const int span = (((nsteps + kSpans - 1) / kSpans) + 1) & ~1;
+  Side* sd = side_for_current_device();
+  std::unique_lock<std::mutex> lk;
+  if (sd != nullptr) lk = std::unique_lock<std::mutex>(sd->mu);
+  hipStream_t tws = sd != nullptr ? sd->s : stream;
+  int k = 0;
+  for (int hi = t0; hi >= 0; hi -= span, ++k) {
+    const int lo = std::max(hi - span + 1, 0);
+    rp.t_hi = hi;
+    rp.t_lo = lo;
+    rp.first = hi == t0;
+    hipLaunchKernelGGL(bfly_bwd_kernel<LOGN>, dim3((unsigned)B), dim3(NT3), 0, stream, rp);
+    GS_CHECK_HIP(hipGetLastError());
+    if (sd != nullptr) {
+      GS_CHECK_HIP(hipEventRecord(sd->ev[k], stream));
+      GS_CHECK_HIP(hipStreamWaitEvent(tws, sd->ev[k], 0));
+    }
+    tp.v_lo = (int64_t)lo * B;
+    tp.v_hi = (int64_t)(std::min(hi, T - 1) + 1) * B;
+    tp.first = hi == t0;
+    hipLaunchKernelGGL(bfly_twiddle_grad<LOGN>, dim3((unsigned)pl.nchunk, 3), dim3((1 << LOGN) / 4), 0, tws, tp);
+    GS_CHECK_HIP(hipGetLastError());
+  }
+  if (sd != nullptr) {
+    GS_CHECK_HIP(hipEventRecord(sd->ev[kSpans], tws));
+    GS_CHECK_HIP(hipStreamWaitEvent(stream, sd->ev[kSpans], 0));
+  }
   const int64_t nsum = (int64_t)3 * LOGN * (1 << LOGN);
-  hipLaunchKernelGGL(bfly_twiddle_sum, dim3((unsigned)((nsum + 63) / 64)), dim3(64 * kTwSumPhases), 0, stream, part, a->dw_part,
-                     pl.nchunk, 1 << LOGN, LOGN);
+  hipLaunchKernelGGL(bfly_twiddle_sum, dim3((unsigned)((nsum + 63) / 64)), dim3(64 * kTwSumPhases), 0, stream, part,
+                     a->dw_part, pl.nchunk, 1 << LOGN, LOGN);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }
@@ -714,10 +799,11 @@ extern "C" int gs_butterfly_bwd(const gs_bwd_args* a, hipStream_t stream) {
   float* mi = take(pl.plane);
   float* dghn = take(pl.plane);
   float* part = take(pl.part);
+  float* dcar = take(pl.dcar);
 
   switch (a->log_n) {
-    case 8: return launch_stages<8>(a, pl, hq, cg, cgn, zm, mi, dghn, part, stream);
-    case 9: return launch_stages<9>(a, pl, hq, cg, cgn, zm, mi, dghn, part, stream);
-    default: return launch_stages<10>(a, pl, hq, cg, cgn, zm, mi, dghn, part, stream);
+    case 8: return launch_stages<8>(a, pl, hq, cg, cgn, zm, mi, dghn, part, dcar, stream);
+    case 9: return launch_stages<9>(a, pl, hq, cg, cgn, zm, mi, dghn, part, dcar, stream);
+    default: return launch_stages<10>(a, pl, hq, cg, cgn, zm, mi, dghn, part, dcar, stream);
   }
 }

@@ -56,6 +56,8 @@ CASES = [
     (1, (1, 3, 16), None, False), (1, (7, 6, 128), None, False),
     (3, (16, 8, 512), 8, True), (3, (8, 6, 128), 8, False), (3, (5, 9, 96), 3, True),
     (4, (8, 6, 512), None, False), (4, (3, 2, 1000), None, False), (4, (1, 3, 256), None, False),
+    # butterfly: seven spans of the recurrence (the last one short) with the twiddle gradient alongside
+    (4, (37, 3, 256), None, False),
     # N = 1024 with H = N: the recurrence's folded cross-wave layers over every element
     (4, (6, 5, 1024), None, False), (0, (33, 3, 1024), None, False),
     # single-factor Monarch on the block-local path: blksz 16, 32, 64, 128, B not a multiple of the
