@@ -90,17 +90,36 @@ struct Lay {
   static constexpr int WPG = N / 256;  // waves per gate vector
 };
 
+// The planes that only these kernels read (hq and the coefficient planes)
+// hold each row of N elements (zero past H) in lane order: element
+// i = lane + 64 r + 256 w sits at 256 w + 4 lane + r, so a lane's four
+// elements are one 16-byte load.
+// A buffer resource over `bytes` bytes at `base`: an access at a byte offset
+// of `bytes` or more reads 0 or is dropped (the hardware's range check), so
+// a lane past the end stores nothing without a branch around the store.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
+}
+constexpr uint32_t kOffNone = 0x80000000u;  // a byte offset past every bounded_rsrc
+
+// (The four values stay one vector value from the load to their use, so the
+// compiler keeps them in the load's registers.)
+typedef float f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ f4 ld_lane4(const float* row, uint32_t off) {
+  return __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(raw_rsrc(row), (int)off, 0, 0));
+}
+
 struct CoefParams {
   const float* tw;
   const float* bh;
   const float* gi;   // [T, B, 3H], strides sg_t, sg_b
   const float* h0;   // [B, H], stride sh0_b
   const float* out;  // [T, B, H], steps back to back: row m = t B + b at out + m so_b
-  float* hq;         // [T B, H] q_in(h_{t-1})
-  float* cg;         // [T B, 3H] (Cr, Cz, Chn)
-  float* cgn;        // [T B, H]
-  float* zm;         // [T B, H]
-  float* mi;         // [T B, H]
+  float* hq;         // [T B, N] q_in(h_{t-1}), lane order
+  float* cg;         // [T B, 3, N] (Cr, Cz, Chn), lane order
+  float* cgn;        // [T B, N] lane order
+  float* zm;         // [T B, N] lane order
+  float* mi;         // [T B, N] lane order
   int64_t sg_t, sg_b, sh0_b, so_b, nvec;
   int B, H;
   Quant qin, qout;
@@ -114,17 +133,18 @@ struct CoefParams {
 // coefficients are formed by one of the three waves that hold it: slot r of
 // wave w (elements lane + 64 r + 256 w) goes to gate (r + w) mod 3's wave, so
 // a wave owns slot sa = (g - w) mod 3, and slot 3 as well when sa = 0. Every
-// wave forms two slots; a wave that owns one forms it twice. Lanes past H take
-// element H - 1 in place of theirs (clamped loads, LDS reads and stores), so
-// all lanes holding an address store the same bits there and no store is
-// masked: every iteration issues the same memory operations on every path,
-// and the waits for one register set never cover the stores or the other
-// set's loads.
+// wave forms two slots; a wave that owns one forms it twice (the same bits
+// to the same places). Lanes past H read element H - 1's inputs (clamped
+// loads and LDS reads) and store zeros to their own slots of the lane-order
+// planes, so no store is masked: every iteration issues the same memory
+// operations on every path, and the waits for one register set never cover
+// the stores or the other set's loads.
 template <int LOGN>
 __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParams p) {
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
   __shared__ float xch[2][3][N];
   __shared__ float ghs[2][3][N];
+  __shared__ float stg[7][N];  // the vector's seven output rows, element order
   // the wave index read into a scalar register, so that per-gate choices are scalar
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = wv / WPG,
             w = wv - g * WPG;
@@ -150,6 +170,15 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
   const int ka = lane + 64 * sa + 256 * w;
   const int kb = lane + 192 + 256 * w;  // slot 3, used when two
   const int kac = ka < H ? ka : H - 1, kbc = !two ? kac : kb < H ? kb : H - 1;
+  // the slots' elements as staged (a slot past H stages zeros)
+  const int kwa = ka, kwb = two ? kb : ka;
+  const bool oka = ka < H, okb = two ? kb < H : oka;
+  // The staged rows go out in lane order, one 16-byte store per lane and
+  // row: the gate-r waves store Cr, Cz, Chn; the gate-z waves Cgn, Zm; the
+  // gate-n waves Mi, hq; every wave issues three stores (the third of the
+  // gate-z and gate-n waves goes to a zero-size resource and is dropped).
+  const int srow[3] = {g == 0 ? 0 : g == 1 ? 3 : 5, g == 0 ? 1 : g == 1 ? 4 : 6, 2};
+  const uint32_t loff = 16u * (64 * w + lane);
   // A vector's inputs (h_{t-1} at the lane's elements, gi at its coefficient
   // slots) sit in one of two register sets that take turns, each refilled for
   // the vector after next once used, at clamped addresses so that every
@@ -174,16 +203,28 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
       in.gb[q] = buf_ld(gr, 4u * kbc, 4u * q * H);
     }
   };
-  auto coef = [&](const float(&gs)[3][N], int64_t v, int k, const float(&gv)[3], float hp) {
+  auto coef = [&](const float(&gs)[3][N], int k, int kw, bool ok, const float(&gv)[3], float hp) {
     const GateGrad gg = gru_backward(gv[0], gv[1], gv[2], gs[0][k], gs[1][k], gs[2][k], hp, 1.0f, p.qout);
-    const auto cr = raw_rsrc(p.cg + v * 3 * H);
-    buf_st(cr, 4u * k, 0, gg.dgr);
-    buf_st(cr, 4u * k, 4u * H, gg.dgz);
-    buf_st(cr, 4u * k, 8u * H, gg.dghn);
-    buf_st(raw_rsrc(p.cgn + v * H), 4u * k, 0, gg.dgn);
-    buf_st(raw_rsrc(p.zm + v * H), 4u * k, 0, gg.dh_direct);
-    buf_st(raw_rsrc(p.mi + v * H), 4u * k, 0, (p.qin.on && !quant_keeps(hp, p.qin)) ? 0.0f : 1.0f);
-    buf_st(raw_rsrc(p.hq + v * H), 4u * k, 0, p.qin.on ? fake_quant(hp, p.qin) : hp);
+    stg[0][kw] = ok ? gg.dgr : 0.0f;
+    stg[1][kw] = ok ? gg.dgz : 0.0f;
+    stg[2][kw] = ok ? gg.dghn : 0.0f;
+    stg[3][kw] = ok ? gg.dgn : 0.0f;
+    stg[4][kw] = ok ? gg.dh_direct : 0.0f;
+    stg[5][kw] = ok && !(p.qin.on && !quant_keeps(hp, p.qin)) ? 1.0f : 0.0f;
+    stg[6][kw] = !ok ? 0.0f : p.qin.on ? fake_quant(hp, p.qin) : hp;
+  };
+  auto store_rows = [&](int64_t v) {
+    float* const base[3] = {g == 0 ? p.cg + v * 3 * N : g == 1 ? p.cgn + v * N : p.mi + v * N,
+                            g == 0 ? p.cg + (v * 3 + 1) * N : g == 1 ? p.zm + v * N : p.hq + v * N,
+                            p.cg + (v * 3 + 2) * N};
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      typedef int i4 __attribute__((ext_vector_type(4)));
+      const i4 q = {__float_as_int(stg[srow[j]][idx[0]]), __float_as_int(stg[srow[j]][idx[1]]),
+                    __float_as_int(stg[srow[j]][idx[2]]), __float_as_int(stg[srow[j]][idx[3]])};
+      __builtin_amdgcn_raw_buffer_store_b128(q, bounded_rsrc(base[j], j < 2 || g == 0 ? 4u * N : 0u), (int)loff, 0,
+                                             0);
+    }
   };
   auto vec = [&](int64_t v, VecIn& in, float(&gs)[3][N]) {
     v = v < p.nvec ? v : p.nvec - 1;  // past the end: vector nvec - 1 again, the same bits to the same places
@@ -209,8 +250,12 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
     // reaches after these reads. The barrier also orders xch's reuse.
     lds_barrier();
     const float hpa = sa == 0 ? in.h[0] : sa == 1 ? in.h[1] : in.h[2];
-    coef(gs, v, kac, in.ga, hpa);
-    coef(gs, v, kbc, in.gb, two ? in.h[3] : hpa);
+    coef(gs, kac, kwa, oka, in.ga, hpa);
+    coef(gs, kbc, kwb, okb, in.gb, two ? in.h[3] : hpa);
+    // stg is read below; its next writes (the next vector's) come after the
+    // next vector's barrier, which every thread reaches after these reads
+    lds_barrier();
+    store_rows(v);
     load_vec(v + 2 * stride, in);
   };
   VecIn in0, in1;
@@ -227,12 +272,10 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
 struct RecParams {
   const float* tw;
   const float* dout;  // [T, B, H]
-  const float* cg;    // [T B, 3H] (Cr, Cz, Chn)
-  const float* cgn;   // [T B, H]
-  const float* zm;    // [T B, H]
-  const float* mi;    // [T B, H]
-  float* dgi;         // [T B, 3H] D_t (Cr, Cz, Cgn)
-  float* dghn;        // [T B, H] D_t Chn
+  const float* cg;    // [T B, 3, N] (Cr, Cz, Chn), lane order
+  const float* zm;    // [T B, N] lane order
+  const float* mi;    // [T B, N] lane order
+  float* dsum;        // [T B, N] D_t, lane order
   float* dbh_part;    // [B, 3H] sum over t of D_t (Cr, Cz, Chn)
   float* dh0;         // [B, H]
   float* dcar;        // [B, H] D_{t_lo - 1} handed from one span's launch to the next
@@ -241,19 +284,12 @@ struct RecParams {
   int first;          // t_hi is the first step (dbh starts at 0, D from dout[T-1])
 };
 
-// A buffer resource over `bytes` bytes at `base`: an access at a byte offset
-// of `bytes` or more reads 0 or is dropped (the hardware's range check), so
-// a lane past the end stores nothing without a branch around the store.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
-}
-constexpr uint32_t kOffNone = 0x80000000u;  // a byte offset past every bounded_rsrc
 
 // One workgroup per batch row b for all T steps, the forward's wave layout.
-// Per step: each gate's waves form v_g = D_t Cg_t on their elements, store
-// it as the step's gradient (the dense backward's grad_kernel: dgi_r, dgi_z,
-// and dgh_n with dgi_n = D_t Cgn for gate n; the same products) and add it to
-// the row's dbh sum, then run the transposed layers from L-1 down to 0;
+// Per step: the gate-r waves store D_t (the twiddle gradient forms the
+// step's gradients from it); each gate's waves form v_g = D_t Cg_t on their
+// elements and add it to the row's dbh sum, then run the transposed layers
+// from L-1 down to 0;
 // gates z and n hand their results to the gate-r waves through LDS, which
 // form the carry and D_{t-1} and broadcast it back.
 template <int LOGN>
@@ -319,66 +355,52 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
   // product covered the loads just issued, and each step paid a full memory
   // latency.)
   struct StepIn {
-    float c[4], z[4], m[4], dp[4];
+    f4 c, z, m;
+    float dp[4];
   };
-  // (gate n keeps Cgn in the set's z registers; it never reads Zm.)
-  // Every wave issues its Cg loads every step, at clamped addresses, first;
-  // the gate-r waves then load Zm, Mi and dout[t-1], and the gate-n waves
-  // Cgn, which only they use. So at least a set's Cg loads lie between the
-  // other set's loads and their use on every path, and the compiler's wait
-  // can count them. Loaded values are masked where they are used, not here:
-  // a select after the load would wait for it.
-  const float* const zs = g == 0 ? p.zm : p.cgn;
+  // Every wave issues the same memory operations every step, in the same
+  // order: its Cg row, then Zm, Mi and dout[t-1] (which only the gate-r
+  // waves use; the others' loads hit the same lines), and at the start of a
+  // step one store of D_t (a zero-size resource for the waves other than
+  // gate r's: those stores are dropped). The compiler's wait for one set then
+  // counts exactly the operations issued after it, and never covers the
+  // other set's loads. Loaded values are raw: a select after a load would
+  // wait for it.
+  // per-lane byte offsets: of the lane's four elements in the lane-order
+  // planes, and of each element in the [.., H] rows (past the resource's end
+  // for lanes past H: those loads read 0 and those stores are dropped)
+  const uint32_t loff = 16u * (64 * w + lane);
+  uint32_t goff[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) goff[r] = idx[r] < H ? 4u * idx[r] : kOffNone;
   auto load_step = [&](int t, StepIn& in) {
     const int tc = t < 0 ? 0 : t < p.T ? t : p.T - 1;
     const int64_t row = (int64_t)tc * p.B + b;
     const int64_t rowp = (int64_t)(t > 0 ? t - 1 : 0) * p.B + b;
+    in.c = ld_lane4(p.cg + (row * 3 + g) * N, loff);
+    in.z = ld_lane4(p.zm + row * N, loff);
+    in.m = ld_lane4(p.mi + row * N, loff);
+    const auto dr = bounded_rsrc(p.dout + rowp * H, 4u * H);  // 0 past H
 #pragma unroll
-    for (int r = 0; r < 4; ++r) in.c[r] = p.cg[row * 3 * H + g * H + (idx[r] < H ? idx[r] : H - 1)];
-    // raw values (masked where they are used), so that the loads write the
-    // set's registers directly and nothing waits for them here; the z
-    // registers are loaded by one instruction sequence for both gates that
-    // use them (a plane chosen per wave), so no copy merges two loads
-    if (g != 1) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) in.z[r] = zs[row * H + (idx[r] < H ? idx[r] : H - 1)];
-    }
-    if (g == 0) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int ic = idx[r] < H ? idx[r] : H - 1;
-        in.m[r] = p.mi[row * H + ic];
-        in.dp[r] = p.dout[rowp * H + ic];
-      }
-    }
+    for (int r = 0; r < 4; ++r) in.dp[r] = buf_ld(dr, goff[r], 0);
   };
-  // per-lane byte offsets of the gradient stores, past the resource's end for
-  // lanes past H
-  uint32_t goff[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) goff[r] = idx[r] < H ? 4u * idx[r] : kOffNone;
   float dbh[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) dbh[r] = idx[r] < H && !p.first ? p.dbh_part[(int64_t)b * 3 * H + g * H + idx[r]] : 0.0f;
   auto step = [&](int t, StepIn& in) {
     const bool real = t < p.T;
     const int64_t row = (int64_t)(real ? t : p.T - 1) * p.B + b;
-    const uint32_t gbytes = real ? 4u * H : 0u;
+    {
+      typedef int i4 __attribute__((ext_vector_type(4)));
+      const i4 dq = {__float_as_int(d[0]), __float_as_int(d[1]), __float_as_int(d[2]), __float_as_int(d[3])};
+      __builtin_amdgcn_raw_buffer_store_b128(dq, bounded_rsrc(p.dsum + row * N, real && g == 0 ? 4u * N : 0u),
+                                             (int)loff, 0, 0);
+    }
     float x[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = real && idx[r] < H ? d[r] * in.c[r] : 0.0f;
-    {
-      const auto gr = bounded_rsrc(p.dgi + row * 3 * H + g * H, gbytes);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        dbh[r] += x[r];
-        buf_st(gr, goff[r], 0, g == 2 ? d[r] * in.z[r] : x[r]);
-      }
-      if (g == 2) {
-        const auto nr = bounded_rsrc(p.dghn + row * H, gbytes);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) buf_st(nr, goff[r], 0, x[r]);
-      }
+    for (int r = 0; r < 4; ++r) {
+      x[r] = real ? d[r] * in.c[r] : 0.0f;  // Cg is 0 past H
+      dbh[r] += x[r];
     }
     static_for<0, L>([&](auto S) {
       constexpr int s = L - 1 - S;
@@ -417,12 +439,10 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
           via = (x[r] + ghs[1][idx[r]]) + ghs[2][idx[r]];
           carry = in.z[r] * d[r] + in.m[r] * via;
         }
-        if (idx[r] < H) {
-          if (t == 0)
-            p.dh0[(int64_t)b * H + idx[r]] = carry;
-          else
-            dv[idx[r]] = in.dp[r] + carry;  // t > 0 here, so dout[t-1] was loaded
-        }
+        // D_{t-1} = dout[t-1] + carry; at t = 0 the carry is dh0, stored
+        // after the loop (no global store here, so every step issues the
+        // same memory operations)
+        if (idx[r] < H) dv[idx[r]] = t > 0 ? in.dp[r] + carry : carry;
       }
     }
     lds_barrier();
@@ -433,7 +453,10 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
     load_step(t - 2, in);  // unconditional (see load_step); past step 0 it reloads step 0
   };
   StepIn in0, in1;
+  // the two sets' loads issued in this order, as in the loop (the wait at
+  // the top of the loop counts from the entry's order as well)
   load_step(t0, in0);
+  __builtin_amdgcn_sched_barrier(0);
   load_step(t0 - 1, in1);
   for (int t = t0; t > p.t_lo; t -= 2) {
     step(t, in0);
@@ -444,15 +467,18 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
     if (idx[r] < H) {
       p.dbh_part[(int64_t)b * 3 * H + g * H + idx[r]] = dbh[r];
       if (g == 0 && p.t_lo > 0) p.dcar[(int64_t)b * H + idx[r]] = d[r];  // D_{t_lo - 1}
+      if (g == 0 && p.t_lo == 0) p.dh0[(int64_t)b * H + idx[r]] = dv[idx[r]];  // step 0's carry
     }
   }
 }
 
 struct TwParams {
   const float* tw;
-  const float* hq;    // [TB, H]
-  const float* dgi;   // [TB, 3H] (r, z parts are dgh's)
-  const float* dghn;  // [TB, H]
+  const float* hq;    // [TB, N] lane order
+  const float* dsum;  // [TB, N] D, lane order
+  const float* cg;    // [TB, 3, N] (Cr, Cz, Chn), lane order
+  const float* cgn;   // [TB, N] lane order
+  float* dgi;         // [TB, 3H] D (Cr, Cz, Cgn)
   float* part;        // [3][nchunk][L][N][2]
   int64_t v_lo, v_hi; // this launch's vectors
   int nchunk, H;
@@ -460,7 +486,9 @@ struct TwParams {
 };
 
 // Workgroup (chunk, gate) of WPG waves, the forward's lane layout: for
-// vectors v = chunk, chunk + nchunk, ... the layers run forward on hq, each
+// vectors v = chunk, chunk + nchunk, ... the gate's gradient dgh = D Cg is
+// formed and its dgi part stored (dgi_r, dgi_z, and dgi_n = D Cgn for gate n;
+// the dense backward's grad_kernel products), the layers run forward on hq, each
 // lane keeping its elements' activations and their partners' (a, ap) in
 // registers, then dgh runs backward through the transposed layers; each lane
 // accumulates its elements' two twiddle gradients per layer in registers.
@@ -491,19 +519,18 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
   // wait for one set then never covers the other's loads. (Loaded at the top
   // of each vector's iteration, every vector paid a full memory latency.)
   struct VecIn {
-    float h[4], d[4];
+    f4 h, d, c, n;
   };
+  const uint32_t loff = 16u * (64 * w + lane);
+  uint32_t goff[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) goff[r] = idx[r] < H ? 4u * idx[r] : kOffNone;
   auto load_vec = [&](int64_t v, VecIn& in) {
     const int64_t vc = v < p.v_hi ? v : p.v_hi - 1;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool ok = idx[r] < H;
-      const int ic = ok ? idx[r] : H - 1;
-      const float h = p.hq[vc * H + ic];
-      const float d = g < 2 ? p.dgi[vc * 3 * H + g * H + ic] : p.dghn[vc * H + ic];
-      in.h[r] = ok ? h : 0.0f;
-      in.d[r] = ok ? d : 0.0f;
-    }
+    in.h = ld_lane4(p.hq + vc * N, loff);  // lane-order planes: 0 past H
+    in.d = ld_lane4(p.dsum + vc * N, loff);
+    in.c = ld_lane4(p.cg + (vc * 3 + g) * N, loff);
+    in.n = ld_lane4(p.cgn + vc * N, loff);  // used by gate n only
   };
   auto vec = [&](int64_t v, VecIn& in) {
     float a[L][4], ap[L][4];
@@ -520,8 +547,12 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
       }
     });
     float gv[4];
+    const auto gr = bounded_rsrc(p.dgi + v * 3 * H + g * H, 4u * H);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) gv[r] = in.d[r];
+    for (int r = 0; r < 4; ++r) {
+      gv[r] = in.d[r] * in.c[r];
+      buf_st(gr, goff[r], 0, g == 2 ? in.d[r] * in.n[r] : gv[r]);
+    }
     static_for<0, L>([&](auto S) {
       constexpr int s = L - 1 - S;
 #pragma unroll
@@ -543,6 +574,7 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
   };
   VecIn in0, in1;
   load_vec(p.v_lo + chunk, in0);
+  __builtin_amdgcn_sched_barrier(0);  // in0's loads first, as in the loop
   load_vec(p.v_lo + chunk + p.nchunk, in1);
   for (int64_t v = p.v_lo + chunk; v < p.v_hi; v += 2 * (int64_t)p.nchunk) {
     vec(v, in0);
@@ -607,8 +639,8 @@ __global__ __launch_bounds__(64 * kTwSumPhases) void bfly_twiddle_sum(const floa
 struct NativePlan {
   bool ok = false;
   int nchunk = 0;
-  int64_t hq, cg, plane, part, dcar;
-  int64_t scratch() const { return hq + cg + 4 * plane + part + dcar; }  // no tagged words
+  int64_t hq, cg, lplane, part, dcar;
+  int64_t scratch() const { return hq + cg + 4 * lplane + part + dcar; }  // no tagged words
 };
 
 // Twiddle-gradient workgroups per gate. 3 x 64 = 192 one-per-CU workgroups
@@ -629,9 +661,9 @@ NativePlan plan_native(const gs_bwd_args* a) {
   const int64_t H = a->H, TB = a->T * a->B;
   if (N < H || TB >= ((int64_t)1 << 31)) return pl;
   pl.nchunk = kTwChunks;
-  pl.hq = align256(TB * H * 4);
-  pl.cg = align256(TB * 3 * H * 4);
-  pl.plane = align256(TB * H * 4);
+  pl.hq = align256(TB * N * 4);
+  pl.cg = align256(TB * 3 * N * 4);
+  pl.lplane = align256(TB * N * 4);
   pl.part = align256((int64_t)3 * pl.nchunk * 2 * a->log_n * N * 4);
   pl.dcar = align256(a->B * H * 4);
   pl.ok = true;
@@ -667,7 +699,7 @@ Side* side_for_current_device() {
 
 template <int LOGN>
 int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* cg, float* cgn, float* zm, float* mi,
-                  float* dghn, float* part, float* dcar, hipStream_t stream) {
+                  float* dsum, float* part, float* dcar, hipStream_t stream) {
   constexpr int NT3 = 3 * (1 << LOGN) / 4;
   const int T = (int)a->T, B = (int)a->B, H = (int)a->H;
   const int64_t TB = (int64_t)T * B;
@@ -697,11 +729,9 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   rp.tw = a->w;
   rp.dout = a->dout;
   rp.cg = cg;
-  rp.cgn = cgn;
   rp.zm = zm;
   rp.mi = mi;
-  rp.dgi = a->dgi;
-  rp.dghn = dghn;
+  rp.dsum = dsum;
   rp.dbh_part = a->dbh_part;
   rp.dh0 = a->dh0;
   rp.dcar = dcar;
@@ -711,8 +741,10 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   TwParams tp;
   tp.tw = a->w;
   tp.hq = hq;
+  tp.dsum = dsum;
+  tp.cg = cg;
+  tp.cgn = cgn;
   tp.dgi = a->dgi;
-  tp.dghn = dghn;
   tp.part = part;
   tp.nchunk = pl.nchunk;
   tp.H = H;
@@ -794,16 +826,16 @@ extern "C" int gs_butterfly_bwd(const gs_bwd_args* a, hipStream_t stream) {
   };
   float* hq = take(pl.hq);
   float* cg = take(pl.cg);
-  float* cgn = take(pl.plane);
-  float* zm = take(pl.plane);
-  float* mi = take(pl.plane);
-  float* dghn = take(pl.plane);
+  float* cgn = take(pl.lplane);
+  float* zm = take(pl.lplane);
+  float* mi = take(pl.lplane);
+  float* dsum = take(pl.lplane);
   float* part = take(pl.part);
   float* dcar = take(pl.dcar);
 
   switch (a->log_n) {
-    case 8: return launch_stages<8>(a, pl, hq, cg, cgn, zm, mi, dghn, part, dcar, stream);
-    case 9: return launch_stages<9>(a, pl, hq, cg, cgn, zm, mi, dghn, part, dcar, stream);
-    default: return launch_stages<10>(a, pl, hq, cg, cgn, zm, mi, dghn, part, dcar, stream);
+    case 8: return launch_stages<8>(a, pl, hq, cg, cgn, zm, mi, dsum, part, dcar, stream);
+    case 9: return launch_stages<9>(a, pl, hq, cg, cgn, zm, mi, dsum, part, dcar, stream);
+    default: return launch_stages<10>(a, pl, hq, cg, cgn, zm, mi, dsum, part, dcar, stream);
   }
 }
