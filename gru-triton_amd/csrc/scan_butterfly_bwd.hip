@@ -289,15 +289,13 @@ struct RecParams {
 // Per step: the gate-r waves store D_t (the twiddle gradient forms the
 // step's gradients from it); each gate's waves form v_g = D_t Cg_t on their
 // elements and add it to the row's dbh sum, then run the transposed layers
-// from L-1 down to 0;
-// gates z and n hand their results to the gate-r waves through LDS, which
-// form the carry and D_{t-1} and broadcast it back.
+// from L-1 down to 0; the three gates' results meet in LDS, where every wave
+// forms the carry and D_{t-1} for its own elements.
 template <int LOGN>
 __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams p) {
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
   __shared__ float xch[2][3][N];
-  __shared__ float ghs[3][N];
-  __shared__ float dv[N];
+  __shared__ float ghs[2][3][N];
   // the wave index read into a scalar register, so that per-gate choices are scalar
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = wv / WPG,
             w = wv - g * WPG;
@@ -373,21 +371,27 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
   uint32_t goff[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) goff[r] = idx[r] < H ? 4u * idx[r] : kOffNone;
-  auto load_step = [&](int t, StepIn& in) {
+  // (pin: keep the loads in this order; the loop's loads are issued in it,
+  // and the prologue's must be too, since the wait at the top of the loop
+  // counts from the entry's order as well)
+  auto load_step = [&](int t, StepIn& in, auto pin) {
     const int tc = t < 0 ? 0 : t < p.T ? t : p.T - 1;
     const int64_t row = (int64_t)tc * p.B + b;
     const int64_t rowp = (int64_t)(t > 0 ? t - 1 : 0) * p.B + b;
     in.c = ld_lane4(p.cg + (row * 3 + g) * N, loff);
+    if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
     in.z = ld_lane4(p.zm + row * N, loff);
     in.m = ld_lane4(p.mi + row * N, loff);
+    if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
     const auto dr = bounded_rsrc(p.dout + rowp * H, 4u * H);  // 0 past H
 #pragma unroll
     for (int r = 0; r < 4; ++r) in.dp[r] = buf_ld(dr, goff[r], 0);
+    if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
   };
   float dbh[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) dbh[r] = idx[r] < H && !p.first ? p.dbh_part[(int64_t)b * 3 * H + g * H + idx[r]] : 0.0f;
-  auto step = [&](int t, StepIn& in) {
+  auto step = [&](int t, StepIn& in, float(&gs)[3][N]) {
     const bool real = t < p.T;
     const int64_t row = (int64_t)(real ? t : p.T - 1) * p.B + b;
     {
@@ -425,49 +429,42 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
         x[r] = tii[s][r] * x[r] + tpi[s][r] * y[r];
       }
     });
-    if (g != 0) {
+    // Every wave gathers the three gates' results for its elements and forms
+    // D_{t-1} = dout[t-1] + Zm D_t + Mi (sum of the gates) itself (all waves
+    // hold Zm, Mi and dout[t-1]; the same inputs give the same bits), so one
+    // barrier per step serves the gather. At t = 0 the carry is dh0, stored
+    // after the loop. gs alternates between two buffers with the step's
+    // parity: its next writer (two steps on) passes the next step's barrier
+    // first, which every wave reaches after these reads.
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ghs[g][idx[r]] = x[r];
-    }
+    for (int r = 0; r < 4; ++r) gs[g][idx[r]] = x[r];
     lds_barrier();
-    if (g == 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float via, carry;
-        {
+    for (int r = 0; r < 4; ++r) {
+      float via, carry;
+      {
 #pragma clang fp contract(off)
-          via = (x[r] + ghs[1][idx[r]]) + ghs[2][idx[r]];
-          carry = in.z[r] * d[r] + in.m[r] * via;
-        }
-        // D_{t-1} = dout[t-1] + carry; at t = 0 the carry is dh0, stored
-        // after the loop (no global store here, so every step issues the
-        // same memory operations)
-        if (idx[r] < H) dv[idx[r]] = t > 0 ? in.dp[r] + carry : carry;
+        via = (gs[0][idx[r]] + gs[1][idx[r]]) + gs[2][idx[r]];
+        carry = in.z[r] * d[r] + in.m[r] * via;
       }
+      const float dn = t > 0 ? in.dp[r] + carry : carry;
+      d[r] = idx[r] < H ? dn : 0.0f;
     }
-    lds_barrier();
-    if (t > 0) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) d[r] = idx[r] < H ? dv[idx[r]] : 0.0f;
-    }
-    load_step(t - 2, in);  // unconditional (see load_step); past step 0 it reloads step 0
+    load_step(t - 2, in, std::false_type{});  // unconditional; past step 0 it reloads step 0
   };
   StepIn in0, in1;
-  // the two sets' loads issued in this order, as in the loop (the wait at
-  // the top of the loop counts from the entry's order as well)
-  load_step(t0, in0);
-  __builtin_amdgcn_sched_barrier(0);
-  load_step(t0 - 1, in1);
-  for (int t = t0; t > p.t_lo; t -= 2) {
-    step(t, in0);
-    step(t - 1, in1);
+  load_step(t0, in0, std::true_type{});
+  load_step(t0 - 1, in1, std::true_type{});
+  for (int t = t0; t > p.t_lo; t -= 2) {  // t0 is odd (t_hi always is)
+    step(t, in0, ghs[0]);
+    step(t - 1, in1, ghs[1]);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     if (idx[r] < H) {
       p.dbh_part[(int64_t)b * 3 * H + g * H + idx[r]] = dbh[r];
       if (g == 0 && p.t_lo > 0) p.dcar[(int64_t)b * H + idx[r]] = d[r];  // D_{t_lo - 1}
-      if (g == 0 && p.t_lo == 0) p.dh0[(int64_t)b * H + idx[r]] = dv[idx[r]];  // step 0's carry
+      if (g == 0 && p.t_lo == 0) p.dh0[(int64_t)b * H + idx[r]] = d[r];  // step 0's carry
     }
   }
 }
