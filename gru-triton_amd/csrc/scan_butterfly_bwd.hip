@@ -64,9 +64,9 @@ __device__ __forceinline__ ElemTw elem_tw(const float* tw_g, int N, int s, int i
 // s (i ^ 2^s) comes from a DPP move (strides 1-8), an LDS permute (16, 32),
 // another register of the same lane (64, 128) or an LDS exchange between the
 // gate's waves (>= 256, the only case that needs a workgroup barrier).
-template <int S>
+template <int S, bool VX = false>
 __device__ __forceinline__ void partner_of(const float (&x)[4], float (&y)[4], float* xch, const int (&idx)[4]) {
-  if constexpr (S <= 3) {
+  if constexpr (S <= 3 || (VX && S < 6)) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) y[r] = lane_xor_c<1 << S>(x[r]);
   } else if constexpr (S < 6) {
@@ -522,14 +522,28 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
   uint32_t goff[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) goff[r] = idx[r] < H ? 4u * idx[r] : kOffNone;
-  auto load_vec = [&](int64_t v, VecIn& in) {
+  // (pin: keep the loads in this order, as the loop issues them; the wait at
+  // the top of the loop counts from the entry's order as well)
+  auto load_vec = [&](int64_t v, VecIn& in, auto pin) {
     const int64_t vc = v < p.v_hi ? v : p.v_hi - 1;
     in.h = ld_lane4(p.hq + vc * N, loff);  // lane-order planes: 0 past H
+    if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
     in.d = ld_lane4(p.dsum + vc * N, loff);
     in.c = ld_lane4(p.cg + (vc * 3 + g) * N, loff);
     in.n = ld_lane4(p.cgn + vc * N, loff);  // used by gate n only
+    if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
   };
+  // A vector past the end of the span (the second of the last pair) repeats
+  // the span's last vector: its dgi stores put the same bits in the same
+  // places, and its gradient is zeroed, so it adds nothing to the sums. So
+  // both vectors of a pair run unconditionally and no branch skips memory
+  // operations.
   auto vec = [&](int64_t v, VecIn& in) {
+    // (no instruction moves into another vector's code: the scheduler would
+    // otherwise hoist the next vector's products above the wait for its set)
+    __builtin_amdgcn_sched_barrier(0);
+    const bool live = v < p.v_hi;
+    v = live ? v : p.v_hi - 1;
     float a[L][4], ap[L][4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) a[0][r] = in.h[r];
@@ -547,8 +561,9 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
     const auto gr = bounded_rsrc(p.dgi + v * 3 * H + g * H, 4u * H);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      gv[r] = in.d[r] * in.c[r];
-      buf_st(gr, goff[r], 0, g == 2 ? in.d[r] * in.n[r] : gv[r]);
+      const float dg = in.d[r] * in.c[r];
+      buf_st(gr, goff[r], 0, g == 2 ? in.d[r] * in.n[r] : dg);
+      gv[r] = live ? dg : 0.0f;
     }
     static_for<0, L>([&](auto S) {
       constexpr int s = L - 1 - S;
@@ -558,8 +573,10 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
         acco[s][r] += gv[r] * ap[s][r];
       }
       if constexpr (s > 0) {
+        // buffer (s + 1) & 1: never the one the last forward layer (L - 1)
+        // used, whose reads no barrier separates from this write
         float y[4];
-        partner_of<s>(gv, y, xch[S & 1], idx);
+        partner_of<s>(gv, y, xch[(s + 1) & 1], idx);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           gv[r] = tii[s][r] * gv[r] + tpi[s][r] * y[r];
@@ -567,15 +584,14 @@ __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p)
       }
     });
     lds_barrier();  // the next vector's exchanges reuse xch
-    load_vec(v + 2 * (int64_t)p.nchunk, in);
+    load_vec(v + 2 * (int64_t)p.nchunk, in, std::false_type{});
   };
   VecIn in0, in1;
-  load_vec(p.v_lo + chunk, in0);
-  __builtin_amdgcn_sched_barrier(0);  // in0's loads first, as in the loop
-  load_vec(p.v_lo + chunk + p.nchunk, in1);
+  load_vec(p.v_lo + chunk, in0, std::true_type{});
+  load_vec(p.v_lo + chunk + p.nchunk, in1, std::true_type{});
   for (int64_t v = p.v_lo + chunk; v < p.v_hi; v += 2 * (int64_t)p.nchunk) {
     vec(v, in0);
-    if (v + p.nchunk < p.v_hi) vec(v + p.nchunk, in1);
+    vec(v + p.nchunk, in1);
   }
   float2* out = reinterpret_cast<float2*>(p.part) + ((int64_t)g * p.nchunk + chunk) * L * N;
 #pragma unroll
