@@ -132,13 +132,12 @@ struct CoefParams {
 // and hq for the twiddle gradient. gh only passes through LDS. Element k's
 // coefficients are formed by one of the three waves that hold it: slot r of
 // wave w (elements lane + 64 r + 256 w) goes to gate (r + w) mod 3's wave, so
-// a wave owns slot sa = (g - w) mod 3, and slot 3 as well when sa = 0. Every
-// wave forms two slots; a wave that owns one forms it twice (the same bits
-// to the same places). Lanes past H read element H - 1's inputs (clamped
-// loads and LDS reads) and store zeros to their own slots of the lane-order
-// planes, so no store is masked: every iteration issues the same memory
-// operations on every path, and the waits for one register set never cover
-// the stores or the other set's loads.
+// a wave owns slot sa = (g - w) mod 3, and slot 3 as well when sa = 0. The
+// coefficients go to LDS and from there to the lane-order planes, one
+// 16-byte store per lane and row. Lanes past H read element H - 1's inputs
+// (clamped loads and LDS reads) and stage zeros, so every iteration issues
+// the same global memory operations on every path, and the waits for one
+// register set never cover the stores or the other set's loads.
 template <int LOGN>
 __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParams p) {
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
@@ -251,7 +250,7 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
     lds_barrier();
     const float hpa = sa == 0 ? in.h[0] : sa == 1 ? in.h[1] : in.h[2];
     coef(gs, kac, kwa, oka, in.ga, hpa);
-    coef(gs, kbc, kwb, okb, in.gb, two ? in.h[3] : hpa);
+    if (two) coef(gs, kbc, kwb, okb, in.gb, in.h[3]);  // LDS writes only: no memory count depends on it
     // stg is read below; its next writes (the next vector's) come after the
     // next vector's barrier, which every thread reaches after these reads
     lds_barrier();
