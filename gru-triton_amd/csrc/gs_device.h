@@ -227,6 +227,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, kBufDword3);
 }
 
+// A buffer resource over `bytes` bytes at `base`: an access at a byte offset
+// (per-lane offset; the uniform offset is kept 0) of `bytes` or more reads 0
+// or is dropped by the hardware's range check, so a lane past the end of a
+// row loads 0 and stores nothing without a branch around the access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
+}
+constexpr uint32_t kOffNone = 0x80000000u;  // a per-lane byte offset past every bounded_rsrc
+
 __device__ __forceinline__ float buf_ld(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
 }

@@ -94,14 +94,6 @@ struct Lay {
 // hold each row of N elements (zero past H) in lane order: element
 // i = lane + 64 r + 256 w sits at 256 w + 4 lane + r, so a lane's four
 // elements are one 16-byte load.
-// A buffer resource over `bytes` bytes at `base`: an access at a byte offset
-// of `bytes` or more reads 0 or is dropped (the hardware's range check), so
-// a lane past the end stores nothing without a branch around the store.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t bounded_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufDword3);
-}
-constexpr uint32_t kOffNone = 0x80000000u;  // a byte offset past every bounded_rsrc
-
 // (The four values stay one vector value from the load to their use, so the
 // compiler keeps them in the load's registers.)
 typedef float f4 __attribute__((ext_vector_type(4)));
