@@ -135,7 +135,7 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
   __shared__ float xch[2][3][N];
   __shared__ float ghs[2][3][N];
-  __shared__ float stg[7][N];  // the vector's seven output rows, element order
+  __shared__ float stg[2][7][N];  // a vector's seven output rows, element order (two vectors in turn)
   // the wave index read into a scalar register, so that per-gate choices are scalar
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = wv / WPG,
             w = wv - g * WPG;
@@ -153,6 +153,20 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
       tii[s][r] = e.t_ii;
       tip[s][r] = e.t_ip;
     }
+  // N = 1024: layers 8 and 9 (strides 256, 512) run as one exchange with
+  // pre-multiplied coefficients, as the forward register kernel runs them
+  // (scan_butterfly.hip), so gh rounds as the forward's does
+  float c8[4][4];
+  if constexpr (L == 10) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const ElemTw q = elem_tw(tw_g, N, 8, idx[r] ^ 512);
+      c8[0][r] = tii[9][r] * tii[8][r];
+      c8[1][r] = tii[9][r] * tip[8][r];
+      c8[2][r] = tip[9][r] * q.t_ii;
+      c8[3][r] = tip[9][r] * q.t_ip;
+    }
+  }
   float bias[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) bias[r] = idx[r] < H ? p.bh[g * H + idx[r]] : 0.0f;
@@ -194,30 +208,39 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
       in.gb[q] = buf_ld(gr, 4u * kbc, 4u * q * H);
     }
   };
-  auto coef = [&](const float(&gs)[3][N], int k, int kw, bool ok, const float(&gv)[3], float hp) {
+  auto coef = [&](float(&st)[7][N], const float(&gs)[3][N], int k, int kw, bool ok, const float(&gv)[3],
+                  float hp) {
     const GateGrad gg = gru_backward(gv[0], gv[1], gv[2], gs[0][k], gs[1][k], gs[2][k], hp, 1.0f, p.qout);
-    stg[0][kw] = ok ? gg.dgr : 0.0f;
-    stg[1][kw] = ok ? gg.dgz : 0.0f;
-    stg[2][kw] = ok ? gg.dghn : 0.0f;
-    stg[3][kw] = ok ? gg.dgn : 0.0f;
-    stg[4][kw] = ok ? gg.dh_direct : 0.0f;
-    stg[5][kw] = ok && !(p.qin.on && !quant_keeps(hp, p.qin)) ? 1.0f : 0.0f;
-    stg[6][kw] = !ok ? 0.0f : p.qin.on ? fake_quant(hp, p.qin) : hp;
+    st[0][kw] = ok ? gg.dgr : 0.0f;
+    st[1][kw] = ok ? gg.dgz : 0.0f;
+    st[2][kw] = ok ? gg.dghn : 0.0f;
+    st[3][kw] = ok ? gg.dgn : 0.0f;
+    st[4][kw] = ok ? gg.dh_direct : 0.0f;
+    st[5][kw] = ok && !(p.qin.on && !quant_keeps(hp, p.qin)) ? 1.0f : 0.0f;
+    st[6][kw] = !ok ? 0.0f : p.qin.on ? fake_quant(hp, p.qin) : hp;
   };
-  auto store_rows = [&](int64_t v) {
+  // (live false: nothing to store yet; the stores go to zero-size resources)
+  auto store_rows = [&](const float(&st)[7][N], int64_t v, bool live) {
     float* const base[3] = {g == 0 ? p.cg + v * 3 * N : g == 1 ? p.cgn + v * N : p.mi + v * N,
                             g == 0 ? p.cg + (v * 3 + 1) * N : g == 1 ? p.zm + v * N : p.hq + v * N,
                             p.cg + (v * 3 + 2) * N};
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       typedef int i4 __attribute__((ext_vector_type(4)));
-      const i4 q = {__float_as_int(stg[srow[j]][idx[0]]), __float_as_int(stg[srow[j]][idx[1]]),
-                    __float_as_int(stg[srow[j]][idx[2]]), __float_as_int(stg[srow[j]][idx[3]])};
-      __builtin_amdgcn_raw_buffer_store_b128(q, bounded_rsrc(base[j], j < 2 || g == 0 ? 4u * N : 0u), (int)loff, 0,
-                                             0);
+      const i4 q = {__float_as_int(st[srow[j]][idx[0]]), __float_as_int(st[srow[j]][idx[1]]),
+                    __float_as_int(st[srow[j]][idx[2]]), __float_as_int(st[srow[j]][idx[3]])};
+      __builtin_amdgcn_raw_buffer_store_b128(q, bounded_rsrc(base[j], live && (j < 2 || g == 0) ? 4u * N : 0u),
+                                             (int)loff, 0, 0);
     }
   };
-  auto vec = [&](int64_t v, VecIn& in, float(&gs)[3][N]) {
+  // A vector's rows are staged in stg[own] after the gather barrier and
+  // stored by the next vector, after its gather barrier (which orders the
+  // staging writes before those reads); the vector after next stages into
+  // the same buffer only after its own gather barrier, which every thread
+  // reaches after these reads. Two barriers per vector: layers 8-9 and the
+  // gather.
+  auto vec = [&](int64_t v, VecIn& in, float(&gs)[3][N], float(&st)[7][N], const float(&sp)[7][N], int64_t vp,
+                 bool live_prev) {
     v = v < p.nvec ? v : p.nvec - 1;  // past the end: vector nvec - 1 again, the same bits to the same places
     float x[4];
 #pragma unroll
@@ -227,6 +250,20 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
     }
     static_for<0, L>([&](auto S) {
       constexpr int s = S;
+      if constexpr (L == 10 && s >= 8) {
+        if constexpr (s == 8) {
+          float* xs = xch[0][g];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xs[idx[r]] = x[r];
+          lds_barrier();
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = idx[r];
+            x[r] = c8[0][r] * x[r] + c8[1][r] * xs[i ^ 256] + c8[2][r] * xs[i ^ 512] + c8[3][r] * xs[i ^ 768];
+          }
+        }
+        return;  // layer 9 is folded into layer 8's exchange
+      }
       float y[4];
       partner_of<s>(x, y, xch[s & 1][g], idx);
 #pragma unroll
@@ -240,13 +277,10 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
     // next) first passes the next vector's barrier, which every thread
     // reaches after these reads. The barrier also orders xch's reuse.
     lds_barrier();
+    store_rows(sp, vp, live_prev);
     const float hpa = sa == 0 ? in.h[0] : sa == 1 ? in.h[1] : in.h[2];
-    coef(gs, kac, kwa, oka, in.ga, hpa);
-    if (two) coef(gs, kbc, kwb, okb, in.gb, in.h[3]);  // LDS writes only: no memory count depends on it
-    // stg is read below; its next writes (the next vector's) come after the
-    // next vector's barrier, which every thread reaches after these reads
-    lds_barrier();
-    store_rows(v);
+    coef(st, gs, kac, kwa, oka, in.ga, hpa);
+    if (two) coef(st, gs, kbc, kwb, okb, in.gb, in.h[3]);  // LDS writes only: no memory count depends on it
     load_vec(v + 2 * stride, in);
   };
   VecIn in0, in1;
@@ -254,10 +288,14 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
   load_vec(blockIdx.x + stride, in1);
   // both vectors of a pair unconditionally, so that no branch skips memory
   // operations (see the slots above)
-  for (int64_t v = blockIdx.x; v < p.nvec; v += 2 * stride) {
-    vec(v, in0, ghs[0]);
-    vec(v + stride, in1, ghs[1]);
+  int64_t v = blockIdx.x;
+  for (; v < p.nvec; v += 2 * stride) {
+    const int64_t vp = v - stride < p.nvec ? v - stride : p.nvec - 1;
+    vec(v, in0, ghs[0], stg[0], stg[1], vp, v != (int64_t)blockIdx.x);
+    vec(v + stride, in1, ghs[1], stg[1], stg[0], v, true);
   }
+  lds_barrier();
+  store_rows(stg[1], v - stride < p.nvec ? v - stride : p.nvec - 1, v != (int64_t)blockIdx.x);
 }
 
 struct RecParams {
