@@ -88,9 +88,12 @@ def gru_scan_butterfly_backward(gi, h0, twiddles, bh_cat, out, dout, *, h_in_qua
     """Gradients (dgi, dh0, dtwiddles, dbh_cat) of the butterfly scan
     (reference backward: scan_butterfly.py:462-1075).
 
-    ``gs_butterfly_bwd`` materializes the map as a [3H, H] matrix, runs the
-    dense backward with it and carries the matrix gradient back through the
-    twiddle stages; dbh comes back as per-row partials summed here.
+    ``gs_butterfly_bwd`` runs, for one chain of N <= 1024, the stage-wise
+    kernels (coefficient pass, per-row recurrence in spans, twiddle gradient on
+    a second stream of the library's beside the recurrence); for other shapes
+    it materializes the map as a [3H, H] matrix, runs the dense backward with
+    it and carries the matrix gradient back through the twiddle stages. dbh
+    comes back as per-row partials summed here.
     """
     who = "gru_scan_butterfly_backward"
     require_cuda(who, gi=gi, h0=h0, twiddles=twiddles, bh_cat=bh_cat, out=out, dout=dout)

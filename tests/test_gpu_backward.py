@@ -257,3 +257,52 @@ def test_monarch_function_saves_gh_only_where_supported(dev):
                                         Wh_struct2=leaves.get("w2"))
         assert out_ng.grad_fn is None
         assert torch.equal(out_ng, out.detach())
+
+
+@pytest.mark.parametrize("shape", [(9, 4, 256), (6, 3, 1024)])
+def test_butterfly_backward_in_a_graph_and_on_another_stream(dev, shape):
+    """The butterfly backward runs its twiddle gradient on a second stream of
+    its own, ordered by events: captured into a graph (fork and join through
+    those events) and replayed three times, with eager work between the
+    replays, each replay gives bitwise the eager gradients; so does a call on a
+    stream other than the default one."""
+    from gru_qat_amd.scan_butterfly import gru_scan_butterfly_backward
+
+    cfg = _cfg(4, shape, q=COARSE)
+    d = {k: cfg[k].to(dev) for k in ("gi", "h0", "w", "bh")}
+    kw = dict(h_in_quant=cfg["h_in_quant"], h_out_quant=cfg["h_out_quant"])
+    import gru_qat_amd as G
+
+    out = G.gru_scan_butterfly_triton(d["gi"], d["h0"], d["w"], d["bh"], **kw).detach()
+    dout = torch.randn(out.shape, generator=torch.Generator().manual_seed(21)).to(dev)
+    args = (d["gi"], d["h0"], d["w"], d["bh"], out, dout)
+    want = [g.clone() for g in gru_scan_butterfly_backward(*args, **kw)]
+    torch.cuda.synchronize(dev)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        got = gru_scan_butterfly_backward(*args, **kw)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    for name, a, b in zip(("dgi", "dh0", "dtw", "dbh"), got, want):
+        assert torch.equal(a, b), f"{name} differs on another stream"
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        gru_scan_butterfly_backward(*args, **kw)  # warm-up on the capture stream
+        torch.cuda.synchronize(dev)
+        with torch.cuda.graph(g, stream=s):
+            captured = gru_scan_butterfly_backward(*args, **kw)
+    torch.cuda.synchronize(dev)
+    for rep in range(3):
+        for c in captured:
+            c.zero_()
+        g.replay()
+        torch.cuda.synchronize(dev)
+        for name, a, b in zip(("dgi", "dh0", "dtw", "dbh"), captured, want):
+            assert torch.equal(a, b), f"replay {rep}: {name} differs from the eager call"
+        eager = gru_scan_butterfly_backward(*args, **kw)  # eager work between the replays
+        torch.cuda.synchronize(dev)
+        assert torch.equal(eager[0], want[0])
