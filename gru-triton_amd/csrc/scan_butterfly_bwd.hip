@@ -219,7 +219,8 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
     st[5][kw] = ok && !(p.qin.on && !quant_keeps(hp, p.qin)) ? 1.0f : 0.0f;
     st[6][kw] = !ok ? 0.0f : p.qin.on ? fake_quant(hp, p.qin) : hp;
   };
-  // (live false: nothing to store yet; the stores go to zero-size resources)
+  // (live false: nothing to store yet; the stores go to zero-size resources.
+  // The Mi row is stored only when q_in is on; the recurrence reads it only then.)
   auto store_rows = [&](const float(&st)[7][N], int64_t v, bool live) {
     float* const base[3] = {g == 0 ? p.cg + v * 3 * N : g == 1 ? p.cgn + v * N : p.mi + v * N,
                             g == 0 ? p.cg + (v * 3 + 1) * N : g == 1 ? p.zm + v * N : p.hq + v * N,
@@ -229,8 +230,8 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
       typedef int i4 __attribute__((ext_vector_type(4)));
       const i4 q = {__float_as_int(st[srow[j]][idx[0]]), __float_as_int(st[srow[j]][idx[1]]),
                     __float_as_int(st[srow[j]][idx[2]]), __float_as_int(st[srow[j]][idx[3]])};
-      __builtin_amdgcn_raw_buffer_store_b128(q, bounded_rsrc(base[j], live && (j < 2 || g == 0) ? 4u * N : 0u),
-                                             (int)loff, 0, 0);
+      const bool keep = j < 2 ? !(g == 2 && j == 0 && !p.qin.on) : g == 0;
+      __builtin_amdgcn_raw_buffer_store_b128(q, bounded_rsrc(base[j], live && keep ? 4u * N : 0u), (int)loff, 0, 0);
     }
   };
   // A vector's rows are staged in stg[own] after the gather barrier and
@@ -320,7 +321,9 @@ struct RecParams {
 // elements and add it to the row's dbh sum, then run the transposed layers
 // from L-1 down to 0; the three gates' results meet in LDS, where every wave
 // forms the carry and D_{t-1} for its own elements.
-template <int LOGN>
+// MI: q_in is on, so Mi (q_in's mask on h_{t-1}) is read; without q_in it is
+// 1 everywhere (Mi·via = via exactly) and neither loaded nor stored.
+template <int LOGN, bool MI>
 __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams p) {
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
   __shared__ float xch[2][3][N];
@@ -410,7 +413,7 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
     in.c = ld_lane4(p.cg + (row * 3 + g) * N, loff);
     if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
     in.z = ld_lane4(p.zm + row * N, loff);
-    in.m = ld_lane4(p.mi + row * N, loff);
+    if constexpr (MI) in.m = ld_lane4(p.mi + row * N, loff);
     if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
     const auto dr = bounded_rsrc(p.dout + rowp * H, 4u * H);  // 0 past H
 #pragma unroll
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
       {
 #pragma clang fp contract(off)
         via = (gs[0][idx[r]] + gs[1][idx[r]]) + gs[2][idx[r]];
-        carry = in.z[r] * d[r] + in.m[r] * via;
+        carry = in.z[r] * d[r] + (MI ? in.m[r] * via : via);
       }
       const float dn = t > 0 ? in.dp[r] + carry : carry;
       d[r] = idx[r] < H ? dn : 0.0f;
@@ -805,7 +808,10 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
     rp.t_hi = hi;
     rp.t_lo = lo;
     rp.first = hi == t0;
-    hipLaunchKernelGGL(bfly_bwd_kernel<LOGN>, dim3((unsigned)B), dim3(NT3), 0, stream, rp);
+    if (cp.qin.on)
+      hipLaunchKernelGGL((bfly_bwd_kernel<LOGN, true>), dim3((unsigned)B), dim3(NT3), 0, stream, rp);
+    else
+      hipLaunchKernelGGL((bfly_bwd_kernel<LOGN, false>), dim3((unsigned)B), dim3(NT3), 0, stream, rp);
     GS_CHECK_HIP(hipGetLastError());
     if (sd != nullptr) {
       GS_CHECK_HIP(hipEventRecord(sd->ev[k], stream));
