@@ -802,6 +802,19 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   std::unique_lock<std::mutex> lk;
   if (sd != nullptr) lk = std::unique_lock<std::mutex>(sd->mu);
   hipStream_t tws = sd != nullptr ? sd->s : stream;
+  // Once the second stream has work of this call, the caller's stream waits
+  // for all of it on every way out, an error return included, so that nothing
+  // of this call runs after the caller may reuse its buffers.
+  bool forked = false;
+  struct Join {
+    Side* sd;
+    hipStream_t stream;
+    const bool& forked;
+    ~Join() {
+      if (sd == nullptr || !forked) return;
+      if (hipEventRecord(sd->ev[kSpans], sd->s) == hipSuccess) (void)hipStreamWaitEvent(stream, sd->ev[kSpans], 0);
+    }
+  } join{sd, stream, forked};
   int k = 0;
   for (int hi = t0; hi >= 0; hi -= span, ++k) {
     const int lo = std::max(hi - span + 1, 0);
@@ -816,6 +829,7 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
     if (sd != nullptr) {
       GS_CHECK_HIP(hipEventRecord(sd->ev[k], stream));
       GS_CHECK_HIP(hipStreamWaitEvent(tws, sd->ev[k], 0));
+      forked = true;
     }
     tp.v_lo = (int64_t)lo * B;
     tp.v_hi = (int64_t)(std::min(hi, T - 1) + 1) * B;
@@ -826,6 +840,7 @@ int launch_stages(const gs_bwd_args* a, const NativePlan& pl, float* hq, float* 
   if (sd != nullptr) {
     GS_CHECK_HIP(hipEventRecord(sd->ev[kSpans], tws));
     GS_CHECK_HIP(hipStreamWaitEvent(stream, sd->ev[kSpans], 0));
+    forked = false;  // joined
   }
   const int64_t nsum = (int64_t)3 * LOGN * (1 << LOGN);
   hipLaunchKernelGGL(bfly_twiddle_sum, dim3((unsigned)((nsum + 63) / 64)), dim3(64 * kTwSumPhases), 0, stream, part,
