@@ -263,7 +263,11 @@ int gs_dense_bwd_tiled(const gs_bwd_args* args, hipStream_t stream);
  * is materialized as a [3H, H] matrix and run through the dense backward (its
  * recurrence persistent up to H = 1024, batch-tiled beyond), and its [3H, H]
  * gradient is carried onto the structured parameters (dw_part, and dw2_part for
- * a two-factor Monarch): H <= 8192 for Monarch, 2^log_n <= 4096 for butterfly. */
+ * a two-factor Monarch): H <= 8192 for Monarch, 2^log_n <= 4096 for butterfly.
+ * The stage-wise butterfly backward runs its twiddle gradient on a stream the
+ * library creates per device (non-blocking, default priority), ordered by
+ * events in both directions: every write of the call is complete in `stream`'s
+ * order, and under graph capture that stream forks from and joins `stream`. */
 int gs_monarch_bwd(const gs_bwd_args* args, hipStream_t stream);
 int gs_butterfly_bwd(const gs_bwd_args* args, hipStream_t stream);
 
