@@ -19,7 +19,9 @@
 // quantizers as int8 symmetric min_max observers), items t1, t2 the dense
 // training forward (gs_dense_fwd also storing gh through gs_args.gh_save),
 // items s1, s2 the dense backward given that saved gh (gs_bwd_args.gh_saved),
-// t5 and s5 the same for the single-factor Monarch configuration, and
+// t5 and s5 the same for the single-factor Monarch configuration, i2 the
+// int8-QAT dense configuration with Wh fake-quantized per row and passed with
+// its codes (gs_quantize_rows, gs_weight_codes, gs_dense_fwd_i8w), and
 // "proj" times the input projection at the benchmark shape (x [2048, 512],
 // Wi_cat [1536, 512], int8 x and per-row weight fake-quant) forward and
 // backward.
@@ -159,7 +161,7 @@ int run_copy(int mib, int launches) {
   return 0;
 }
 
-enum Mode { kForward, kBackward, kCalibrate, kTrainForward, kSavedBackward };
+enum Mode { kForward, kBackward, kCalibrate, kTrainForward, kSavedBackward, kInt8Weights };
 
 int run_config(int idx, int launches, int warmup, Mode mode) {
   const bool backward = mode == kBackward || mode == kSavedBackward;
@@ -216,6 +218,44 @@ int run_config(int idx, int launches, int warmup, Mode mode) {
     const gs_quant q = {1, 1.0f / 127.0f, -127, 127};
     a.q_in = q;
     a.q_out = q;
+  }
+  int8_t* wcodes = nullptr;
+  float* wscale = nullptr;
+  if (mode == kInt8Weights) {
+    if (idx != 2) {
+      fprintf(stderr, "gs_bench: i%d: int8 weight codes are an option of configuration 2 only\n", idx);
+      return 2;
+    }
+    // Wh fake-quantized per row (int8, qmax 127), then its codes recovered from it
+    float* wq = nullptr;
+    int32_t* exact = nullptr;
+    CHECK(hipMalloc(&wq, sizeof(float) * 3 * H * H));
+    CHECK(hipMalloc(&wcodes, 3 * H * H));
+    CHECK(hipMalloc(&wscale, sizeof(float) * 3 * H));
+    CHECK(hipMalloc(&exact, sizeof(int32_t) * 3 * H));
+    gs_rows_args r;
+    memset(&r, 0, sizeof r);
+    r.w = a.w;
+    r.scale = wscale;
+    r.w_q = wq;
+    r.rows = 3 * H;
+    r.cols = H;
+    r.qmin = -127;
+    r.qmax = 127;
+    if (gs_quantize_rows(&r, nullptr) != GS_OK ||
+        gs_weight_codes(wq, 3 * H, H, wcodes, wscale, exact, nullptr) != GS_OK) {
+      fprintf(stderr, "gs_bench: weight codes: %s\n", gs_last_error());
+      return 1;
+    }
+    std::vector<int32_t> ex(3 * H);
+    CHECK(hipMemcpy(ex.data(), exact, sizeof(int32_t) * 3 * H, hipMemcpyDeviceToHost));
+    if (std::count(ex.begin(), ex.end(), 1) != 3 * H) {
+      fprintf(stderr, "gs_bench: a fake-quantized row was not recovered as int8 codes\n");
+      return 1;
+    }
+    CHECK(hipFree(exact));
+    owned.push_back(wq);
+    a.w = wq;
   }
   int64_t need = gs_workspace_bytes(kind, &a);
   if (need < 0) {
@@ -337,7 +377,7 @@ int run_config(int idx, int launches, int warmup, Mode mode) {
   auto forward = [&] {
     switch (kind) {
       case GS_KIND_DIAGONAL: rc = gs_diagonal_fwd(&a, st); break;
-      case GS_KIND_DENSE: rc = gs_dense_fwd(&a, st); break;
+      case GS_KIND_DENSE: rc = wcodes ? gs_dense_fwd_i8w(&a, wcodes, wscale, st) : gs_dense_fwd(&a, st); break;
       case GS_KIND_MONARCH: rc = gs_monarch_fwd(&a, st); break;
       default: rc = gs_butterfly_fwd(&a, st); break;
     }
@@ -380,6 +420,7 @@ int run_config(int idx, int launches, int warmup, Mode mode) {
              mode == kBackward        ? "backward"
              : mode == kSavedBackward ? "backward_saved_gh"
              : mode == kTrainForward  ? "train_forward"
+             : mode == kInt8Weights   ? "int8_weight_codes"
                                       : "calibration");
     report(name, idx, ms, T, B, H);
   } else {
@@ -387,6 +428,8 @@ int run_config(int idx, int launches, int warmup, Mode mode) {
   }
   CHECK(hipFree(ws));
   if (gh) CHECK(hipFree(gh));
+  if (wcodes) CHECK(hipFree(wcodes));
+  if (wscale) CHECK(hipFree(wscale));
   if (b.scratch) CHECK(hipFree(b.scratch));
   if (o.scratch) CHECK(hipFree(o.scratch));
   if (stats) CHECK(hipFree(stats));
@@ -485,7 +528,8 @@ int run_proj(int launches, int warmup) {
 int main(int argc, char** argv) {
   if (argc < 2) {
     fprintf(stderr, "usage: gs_bench <items: configs 0..5, b0..b5 (backward), c0..c5 (calibration), "
-                    "t1, t2, t5 (training forward), s1, s2, s5 (backward on the saved gh), proj, copy; "
+                    "t1, t2, t5 (training forward), s1, s2, s5 (backward on the saved gh), i2 (int8 weight "
+                    "codes), proj, copy; "
                     "comma-separated> "
                     "[launches] [warmup]\n");
     return 2;
@@ -507,6 +551,7 @@ int main(int argc, char** argv) {
                         : tok[0] == 'c' ? kCalibrate
                         : tok[0] == 't' ? kTrainForward
                         : tok[0] == 's' ? kSavedBackward
+                        : tok[0] == 'i' ? kInt8Weights
                                         : kForward;
       const char* num = mode == kForward ? tok : tok + 1;
       char* end = nullptr;

@@ -219,6 +219,77 @@ __device__ __forceinline__ void mfma3(const float (&a)[3][KC], const float (&wr)
 }
 
 
+// ---- int8 weight codes (v_mfma_i32_4x4x4_16b_i8) ------------------------------------
+// Same lane layout as the fp32 chains, with 4 consecutive k per block packed
+// as 4 bytes (byte e = k offset e): instruction q of a chain covers, in block
+// b, k = 64 q + 4 b + e, which is what KC fp32 instructions m = 4 q + e cover
+// (kmap), so the 16 block partials and reduce16 are those of the fp32 chains.
+
+typedef int i4 __attribute__((ext_vector_type(4)));
+
+// Int8 staging layout of a 4-row operand block: word c (k = 4 c .. 4 c + 3 of
+// row r, one byte each) at 4 c + ((r + c / 16) mod 4). A lane's operand reads
+// (row l % 4, word 16 q + l / 4) then cover 64 consecutive words per q, and a
+// poller's stores of one row (lane l: word c = l + 64 i) 64 distinct banks.
+__device__ __forceinline__ int i8_index(int r, int c) { return 4 * c + ((r + (c >> 4)) & 3); }
+
+// A operand of lane l from an int8 staging block: a[q] = word 16 q + l / 4 of row l % 4.
+template <int KC>
+__device__ __forceinline__ void lds_a_i8(const int* blk, int lane, int (&a)[KC / 4]) {
+  const int* b = blk + 4 * (lane >> 2);
+#pragma unroll
+  for (int q = 0; q < KC / 4; ++q) a[q] = b[64 * q + (((lane & 3) + q) & 3)];
+}
+
+// Int8 codes of a quad's 12 weight rows: wi[g][q] packs codes[(g H + o) H + k .. k + 3]
+// for o = o0 + j, k = 64 q + 4 kb4; zero where o >= H or k >= H. H % 4 == 0 and
+// codes 4-byte aligned, so each is one aligned 32-bit load.
+template <int KC>
+__device__ __forceinline__ void load_wi(const int8_t* codes, int H, int o0, int j, int kb4, bool ok_quad,
+                                        int (&wi)[3][KC / 4]) {
+  const int o = o0 + j;
+  const bool ok = ok_quad && o < H;
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    const int8_t* row = codes + ((int64_t)g * H + (ok ? o : 0)) * H;
+#pragma unroll
+    for (int q = 0; q < KC / 4; ++q) {
+      const int k = 64 * q + 4 * kb4;
+      wi[g][q] = (ok && k < H) ? *reinterpret_cast<const int*>(row + k) : 0;
+    }
+  }
+}
+
+// Three int8 MFMA chains (one per gate) on a shared A operand, two accumulators
+// each when the chain has two or more instructions. Sums are exact (|code| <= 128,
+// K <= 1024: at most 2^24).
+template <int KC>
+__device__ __forceinline__ void mfma3_i8(const int (&a)[KC / 4], const int (&wi)[3][KC / 4], i4 (&acc)[3]) {
+  constexpr int NQ = KC / 4;
+  constexpr int NA = NQ >= 2 ? 2 : 1;
+  i4 part[NA][3];
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+#pragma unroll
+    for (int g = 0; g < 3; ++g) part[i][g] = i4{0, 0, 0, 0};
+#pragma unroll
+  for (int q = 0; q < NQ; q += NA) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+#pragma unroll
+      for (int g = 0; g < 3; ++g) part[i][g] = __builtin_amdgcn_mfma_i32_4x4x4i8(a[q + i], wi[g][q + i], part[i][g], 0, 0, 0);
+  }
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+    acc[g] = part[0][g];
+    if constexpr (NA == 2) acc[g] += part[1][g];
+  }
+}
+
+// The 16 block partials of an int8 chain as floats: exact, since every partial
+// and every sum reduce16 forms is an integer of magnitude at most 2^24.
+__device__ __forceinline__ f4 i4_to_f4(i4 v) { return f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]}; }
+
 // ---- host side --------------------------------------------------------------------
 
 struct DevInfo {

@@ -53,6 +53,43 @@ __global__ __launch_bounds__(kRowThreads) void weight_quant_rows(const float* w,
   if (threadIdx.x == 0) scale_out[row] = scale;
 }
 
+// One wave per row of an already fake-quantized weight w [rows, cols]: finds a
+// scale s for which every element is fl(c * s) with an integer code |c| <= 127
+// (the candidates are fl(max|w| / 127) and its neighbours up to two ulps away,
+// the scales weight_quant_rows' rule can have produced), then writes s, the
+// codes and exact[row] = 1; exact[row] = 0 (codes 0) when no candidate fits.
+__global__ __launch_bounds__(64) void recover_codes_rows(const float* w, int cols, int8_t* codes, float* scale_out,
+                                                         int32_t* exact) {
+  const int64_t row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const float* src = w + row * cols;
+  float m = 0.0f;
+  for (int k = lane; k < cols; k += 64) m = fmaxf(m, fabsf(src[k]));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  bool found = m == 0.0f;  // an all-zero row: codes 0 at any scale
+  float s = 1.0f;
+  const float s0 = m / 127.0f;
+  for (int d = 0; d < 5 && !found; ++d) {
+    const int step = d == 0 ? 0 : (d & 1) ? (d + 1) / 2 : -(d / 2);  // 0, +1, -1, +2, -2 ulps
+    const float sc = __int_as_float(__float_as_int(s0) + step);
+    bool ok = sc > 0.0f && sc < __builtin_inff();
+    for (int k = lane; k < cols && ok; k += 64) {
+      const float c = __builtin_rintf(src[k] / sc);
+      ok = fabsf(c) <= 127.0f && c * sc == src[k];
+    }
+    if (__all(ok)) {
+      found = true;
+      s = sc;
+    }
+  }
+  for (int k = lane; k < cols; k += 64) codes[row * cols + k] = found ? (int8_t)__builtin_rintf(src[k] / s) : 0;
+  if (lane == 0) {
+    scale_out[row] = s;
+    exact[row] = found ? 1 : 0;
+  }
+}
+
 // dx[m][i] = 0 where q_x clipped x[m][i].
 __global__ void mask_clipped(float* dx, int64_t sdx, const float* x, int64_t sx, int rows, int cols, Quant q) {
   const int64_t n = (int64_t)rows * cols;
@@ -255,6 +292,21 @@ extern "C" int gs_quantize_rows(const gs_rows_args* a, hipStream_t stream) {
                      a->qmax);
   hipLaunchKernelGGL(weight_quant_rows, dim3((unsigned)a->rows), dim3(kRowThreads), 0, stream, a->w, (int)a->cols,
                      (float)a->qmin, (float)a->qmax, a->w_q, a->scale, a->codes);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
+
+extern "C" int gs_weight_codes(const float* w, int64_t rows, int64_t cols, int8_t* codes, float* scale,
+                               int32_t* exact, hipStream_t stream) {
+  using namespace gs;
+  clear_error();
+  const char* who = "gs_weight_codes";
+  if (rows < 1 || cols < 1 || rows > INT32_MAX || cols > (1 << 24))
+    return set_error(GS_ERR_INVALID, "%s: rows and cols must be in [1, 2^31) and [1, 2^24]; got %lld, %lld", who,
+                     (long long)rows, (long long)cols);
+  if (!w || !codes || !scale || !exact)
+    return set_error(GS_ERR_INVALID, "%s: w, codes, scale and exact must be non-NULL", who);
+  hipLaunchKernelGGL(recover_codes_rows, dim3((unsigned)rows), dim3(64), 0, stream, w, (int)cols, codes, scale, exact);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }

@@ -49,6 +49,8 @@ struct DParams {
   const float* bh;
   float* out;
   float* gh_save;  // SAVE instances: [T, B, 3H] q_in(h_{t-1}) Wh^T as the step computed it (no bias)
+  const int8_t* wq;  // I8 instances: int8 codes of Wh [3H, H], w == fl(code * wsc[row])
+  const float* wsc;  // I8 instances: the code scale of each of Wh's 3H rows
   uint64_t* xh;  // remote mode: [2][Bp][H] tagged q_in(h_t)
   uint64_t* xw;  // remote mode: [nwg] tagged XCD ids
   Ctrl ctrl;
@@ -76,8 +78,16 @@ __host__ __device__ constexpr int dense_remote_units(int KC) { return 4 * (KC >=
 // LDS row stride of a row of n floats that a wave reads as 4 rows x 4 units.
 __host__ __device__ constexpr int row_stride_pad(int n) { return n % 16 == 0 ? n + 4 : n; }
 
-template <int KIND, int KC, int NT, bool REMOTE, bool PACK = false, bool SAVE = false>
+// Int8 weights (I8, dense remote mode with the packed exchange, q_in on and
+// the published levels in q_in's scale): Wh arrives as per-row int8 codes and
+// scales, every A operand (q_in(h0) and each exchanged q_in(h_t)) is a level
+// times that scale, so the step's products run on v_mfma_i32_4x4x4_16b_i8 over
+// the levels and codes (exact integer sums, a quarter of the fp32 chain's
+// instructions) and gh = sum * (code scale * level scale). The operand block
+// is staged as int8 levels (i8_index) instead of floats.
+template <int KIND, int KC, int NT, bool REMOTE, bool PACK = false, bool SAVE = false, bool I8 = false>
 __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
+  static_assert(!I8 || (KIND == kDense && REMOTE && PACK && !SAVE), "int8 weights: dense, remote, packed exchange");
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -117,8 +127,14 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
                                                       // bit 1: a wait of this workgroup gave up
   // The compute waves' Wh slice is loaded first, so that its latency overlaps
   // the LDS clear and the prologue (T = 1 and 64: 0.6 and 1.8 us less).
-  float wr[3][KC];
-  if (!poller) load_w<KC>(p.w, p.nb, p.bs, blk_g, o0, j, kb4, quad_ok, wr);
+  float wr[3][I8 ? 1 : KC];
+  int wi[3][I8 ? KC / 4 : 1];
+  if (!poller) {
+    if constexpr (I8)
+      load_wi<KC>(p.wq, p.H, o0, j, kb4, quad_ok, wi);
+    else
+      load_w<KC>(p.w, p.nb, p.bs, blk_g, o0, j, kb4, quad_ok, wr);
+  }
   const int lds_floats = 2 * p.hsz + p.RB * 4 * KR + (REMOTE ? 8 * GR + 4 : 0);
   for (int i = threadIdx.x; i < lds_floats; i += blockDim.x) lds[i] = 0.0f;
 
@@ -134,12 +150,18 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
     for (int w = threadIdx.x; w < 4 * p.bs; w += blockDim.x) {
       const int r = w / p.bs, k = w - r * p.bs;
       const int row = 4 * rb + r;
-      float v = 0.0f;
-      if (row < p.B) {
-        v = p.h0[(int64_t)row * p.sh0_b + klo + k];
-        if (p.qin.on) v = fake_quant(v, p.qin);
+      if constexpr (I8) {
+        // the level of q_in(h0) (q_in is on in every I8 launch)
+        const int lv = row < p.B ? (int)quant_level(p.h0[(int64_t)row * p.sh0_b + klo + k], p.qin) : 0;
+        reinterpret_cast<int8_t*>(hst)[4 * i8_index(r, k >> 2) + (k & 3)] = (int8_t)lv;
+      } else {
+        float v = 0.0f;
+        if (row < p.B) {
+          v = p.h0[(int64_t)row * p.sh0_b + klo + k];
+          if (p.qin.on) v = fake_quant(v, p.qin);
+        }
+        hst[il_index(r, k)] = v;
       }
-      hst[il_index(r, k)] = v;
     }
     for (int w = threadIdx.x; w < nrbm * 4 * U; w += blockDim.x) {
       const int rbl = w / (4 * U), rem = w - rbl * 4 * U, r = rem / U, u = rem - r * U;
@@ -167,6 +189,12 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
     float bias[3];
 #pragma unroll
     for (int g = 0; g < 3; ++g) bias[g] = unit_ok ? (g == 2 ? kN : kR) * p.bh[g * p.H + unit] : 0.0f;
+    // I8: gh = integer sum * (row's code scale * level scale)
+    float gsc[3] = {0.0f, 0.0f, 0.0f};
+    if constexpr (I8) {
+#pragma unroll
+      for (int g = 0; g < 3; ++g) gsc[g] = unit_ok ? p.wsc[g * p.H + unit] * p.pscale : 0.0f;
+    }
     // lane parts of the out / exchange-word offsets (row = 4 rb + s)
     const int64_t lane_out = (int64_t)s * p.so_b + unit;
     const int64_t lane_xh = (int64_t)s * p.H + unit;
@@ -204,13 +232,22 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
       // the epilogue's LDS reads and the store addresses are issued before the
       // MFMAs, so that none of them is on the chain after the last one
       __builtin_amdgcn_sched_barrier(0);
-      float a[3][KC];
-      lds_a_il<KC>(hst + buf * p.hsz, lane, a[0]);
-      f4 acc[3];
-      mfma3<KC, true>(a, wr, acc);
       float gh[3];
+      if constexpr (I8) {
+        int ai[KC / 4];
+        lds_a_i8<KC>(reinterpret_cast<const int*>(hst + buf * p.hsz), lane, ai);
+        i4 acc[3];
+        mfma3_i8<KC>(ai, wi, acc);
 #pragma unroll
-      for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
+        for (int g = 0; g < 3; ++g) gh[g] = reduce16(i4_to_f4(acc[g]), s) * gsc[g];
+      } else {
+        float a[3][KC];
+        lds_a_il<KC>(hst + buf * p.hsz, lane, a[0]);
+        f4 acc[3];
+        mfma3<KC, true>(a, wr, acc);
+#pragma unroll
+        for (int g = 0; g < 3; ++g) gh[g] = reduce16(acc[g], s);
+      }
       float hn = gru_update_l2(__builtin_fmaf(kR, gh[0], cr), __builtin_fmaf(kR, gh[1], cz),
                                __builtin_fmaf(kN, gh[2], bias[2]), an2, hprev);
       float lv = 0.0f;  // level of the published value (packed exchange)
@@ -307,12 +344,17 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
         float* hs = hst + (nx & 1) * p.hsz;
         if (t2 == 0) {
           for (int k = lane + 64 * part; k < p.bs; k += 64 * NPR) {
-            float v = 0.0f;
-            if (row < p.B) {
-              v = p.h0[(int64_t)row * p.sh0_b + klo + k];
-              if (p.qin.on) v = fake_quant(v, p.qin);
+            if constexpr (I8) {
+              const int lv = row < p.B ? (int)quant_level(p.h0[(int64_t)row * p.sh0_b + klo + k], p.qin) : 0;
+              reinterpret_cast<int8_t*>(hs)[4 * i8_index(pr, k >> 2) + (k & 3)] = (int8_t)lv;
+            } else {
+              float v = 0.0f;
+              if (row < p.B) {
+                v = p.h0[(int64_t)row * p.sh0_b + klo + k];
+                if (p.qin.on) v = fake_quant(v, p.qin);
+              }
+              hs[il_index(pr, k)] = v;
             }
-            hs[il_index(pr, k)] = v;
           }
         } else {
           {
@@ -335,10 +377,15 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
               for (int m = 0; m < PMW; ++m) {
                 if ((valid >> m) & 1u) {
                   const uint32_t x = (uint32_t)v[m];
-                  f4 q;
+                  if constexpr (I8) {
+                    // levels + 128 -> two's-complement int8 levels
+                    reinterpret_cast<int*>(hs)[i8_index(pr, w0 + lane + 64 * m)] = (int)(x ^ 0x80808080u);
+                  } else {
+                    f4 q;
 #pragma unroll
-                  for (int e = 0; e < 4; ++e) q[e] = __builtin_fmaf((float)((x >> (8 * e)) & 0xffu), p.pscale, p.pbias);
-                  *reinterpret_cast<f4*>(hs + il_index(pr, 4 * (w0 + lane + 64 * m))) = q;
+                    for (int e = 0; e < 4; ++e) q[e] = __builtin_fmaf((float)((x >> (8 * e)) & 0xffu), p.pscale, p.pbias);
+                    *reinterpret_cast<f4*>(hs + il_index(pr, 4 * (w0 + lane + 64 * m))) = q;
+                  }
                 }
               }
             } else {
@@ -365,23 +412,25 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
 
 typedef void (*DFn)(DParams);
 
-template <int KIND, bool REMOTE, bool PACK = false, bool SAVE = false>
+template <int KIND, bool REMOTE, bool PACK = false, bool SAVE = false, bool I8 = false>
 DFn pick_kernel(int KC, int* nt) {
   // Remote instances add 4 pollers_per_row(KC) poller waves to 4 compute
   // waves (KC >= 16) or to up to 12 (KC <= 8); local instances hold up to 16
   // compute waves.
   switch (KC) {
-    case 4: *nt = 1024; return scan_kernel<KIND, 4, 1024, REMOTE, PACK, SAVE>;
-    case 8: *nt = 1024; return scan_kernel<KIND, 8, 1024, REMOTE, PACK, SAVE>;
-    case 16: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 16, REMOTE ? 768 : 256, REMOTE, PACK, SAVE>;
-    case 32: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 32, REMOTE ? 768 : 256, REMOTE, PACK, SAVE>;
-    case 64: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 64, REMOTE ? 512 : 256, REMOTE, PACK, SAVE>;
+    case 4: *nt = 1024; return scan_kernel<KIND, 4, 1024, REMOTE, PACK, SAVE, I8>;
+    case 8: *nt = 1024; return scan_kernel<KIND, 8, 1024, REMOTE, PACK, SAVE, I8>;
+    case 16: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 16, REMOTE ? 768 : 256, REMOTE, PACK, SAVE, I8>;
+    case 32: *nt = REMOTE ? 768 : 256; return scan_kernel<KIND, 32, REMOTE ? 768 : 256, REMOTE, PACK, SAVE, I8>;
+    case 64: *nt = REMOTE ? 512 : 256; return scan_kernel<KIND, 64, REMOTE ? 512 : 256, REMOTE, PACK, SAVE, I8>;
     default: return nullptr;
   }
 }
 
-// save: the dense instances that also write gh_t (the training forward)
-DFn pick(int kind, bool remote, int KC, int* nt, bool pack = false, bool save = false) {
+// save: the dense instances that also write gh_t (the training forward);
+// i8: the int8-weight instances (dense, remote, packed, no save)
+DFn pick(int kind, bool remote, int KC, int* nt, bool pack = false, bool save = false, bool i8 = false) {
+  if (i8) return pick_kernel<kDense, true, true, false, true>(KC, nt);
   if (kind == kDense && save) {
     if (remote && pack) return pick_kernel<kDense, true, true, true>(KC, nt);
     return remote ? pick_kernel<kDense, true, false, true>(KC, nt) : pick_kernel<kDense, false, false, true>(KC, nt);
@@ -449,13 +498,19 @@ int plan_dense(int kind, const gs_args* a, DPlan* pl, const char* who) {
   return GS_OK;
 }
 
-int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
+// codes / scales: int8 codes of Wh and their row scales (gs_dense_fwd_i8w), or
+// NULL; used when the launch qualifies for the int8-weight instances.
+int run(int kind, const gs_args* a, hipStream_t stream, const char* who, const int8_t* codes = nullptr,
+        const float* scales = nullptr) {
   DPlan pl;
   int rc = plan_dense(kind, a, &pl, who);
   if (rc) return rc;
   rc = check_workspace(a, kCtrlBytes + pl.xh_bytes + pl.xw_bytes, who);
   if (rc) return rc;
-  DFn fn = pick(kind, pl.remote, pl.KC, &pl.nt, pl.pack, a->gh_save != nullptr);
+  // every A operand must be a q_in level in the published levels' scale
+  const bool i8 = codes != nullptr && kind == kDense && pl.pack && a->gh_save == nullptr && a->q_in.enabled &&
+                  a->q_in.scale == pl.pscale && a->q_in.qmin >= -128 && a->q_in.qmax <= 127;
+  DFn fn = pick(kind, pl.remote, pl.KC, &pl.nt, pl.pack, a->gh_save != nullptr, i8);
   const int threads = 64 * (pl.nwc + (pl.remote ? 4 * pollers_per_row(pl.KC) : 0));
   const int per_set = pl.P * (kind == kMonarch1 ? pl.nb : 1);
 
@@ -484,6 +539,8 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who) {
   p.bh = a->bh;
   p.out = a->out;
   p.gh_save = a->gh_save;
+  p.wq = i8 ? codes : nullptr;
+  p.wsc = i8 ? scales : nullptr;
   char* ws = static_cast<char*>(a->workspace);
   p.ctrl = ctrl_of(ws, a->fault_mirror);
   p.xh = reinterpret_cast<uint64_t*>(ws + kCtrlBytes);
@@ -547,6 +604,20 @@ extern "C" int gs_dense_fwd(const gs_args* a, hipStream_t stream) {
   if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
   if (gs::dense_uses_tiled(a)) return gs::run_tiled_fwd(a, stream, who);
   return gs::run(gs::kDense, a, stream, who);
+}
+
+extern "C" int gs_dense_fwd_i8w(const gs_args* a, const int8_t* w_codes, const float* w_scale, hipStream_t stream) {
+  gs::clear_error();
+  const char* who = "gs_dense_fwd_i8w";
+  int rc = gs::validate_common(a, who, true);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
+  if (w_codes == nullptr || w_scale == nullptr)
+    return gs::set_error(GS_ERR_INVALID, "%s: w_codes and w_scale are required", who);
+  if (reinterpret_cast<uintptr_t>(w_codes) % 4 != 0)
+    return gs::set_error(GS_ERR_INVALID, "%s: w_codes must be 4-byte aligned", who);
+  if (gs::dense_uses_tiled(a)) return gs::run_tiled_fwd(a, stream, who);
+  return gs::run(gs::kDense, a, stream, who, w_codes, w_scale);
 }
 
 extern "C" int gs_monarch_fwd(const gs_args* a, hipStream_t stream) {

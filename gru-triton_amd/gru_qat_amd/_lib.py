@@ -12,6 +12,7 @@ import ctypes
 import os
 import struct
 import threading
+import weakref
 from typing import Callable, Optional, Tuple
 
 import torch
@@ -34,6 +35,8 @@ KIND_DENSE_TILED = 5  # size queries of the batch-tiled dense entry points
 EXPORTS = (
     "gs_dense_fwd",
     "gs_dense_fwd_tiled",
+    "gs_dense_fwd_i8w",
+    "gs_weight_codes",
     "gs_dense_fwd_noalloc",
     "gs_diagonal_fwd",
     "gs_monarch_fwd",
@@ -67,7 +70,7 @@ EXPORTS = (
     "gs_abi_version",
 )
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 QuantTuple = Optional[Tuple[float, int, int]]
 
@@ -395,6 +398,9 @@ def load() -> ctypes.CDLL:
         lib.gs_hidden_map_grad.restype = ctypes.c_int
         lib.gs_quantize_rows.argtypes = [ctypes.POINTER(GsRowsArgs), ctypes.c_void_p]
         lib.gs_quantize_rows.restype = ctypes.c_int
+        lib.gs_weight_codes.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        lib.gs_weight_codes.restype = ctypes.c_int
         lib.gs_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsArgs)]
         lib.gs_workspace_bytes.restype = ctypes.c_int64
         lib.gs_bwd_workspace_bytes.argtypes = [ctypes.c_int, ctypes.POINTER(GsBwdArgs)]
@@ -611,14 +617,49 @@ _NEED: dict = {}  # workspace bytes per (kind, sizes, quant) of the tagged kinds
 
 
 def _raw_entry(lib: ctypes.CDLL, fn_name: str):
-    """The entry point as a function of (packed gs_args bytes, stream handle)."""
+    """The entry point as a function of (packed gs_args bytes, stream handle), or
+    for gs_dense_fwd_i8w of (packed gs_args bytes, codes, scales, stream handle)."""
     fn = _RAW_FN.get(fn_name)
     if fn is None:
         fn = lib[fn_name]  # an independent function object: its argtypes do not touch getattr(lib, ...)
-        fn.argtypes = [ctypes.c_char_p, ctypes.c_void_p]
+        if fn_name == "gs_dense_fwd_i8w":
+            fn.argtypes = [ctypes.c_char_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        else:
+            fn.argtypes = [ctypes.c_char_p, ctypes.c_void_p]
         fn.restype = ctypes.c_int
         _RAW_FN[fn_name] = fn
     return fn
+
+
+# id(w) -> (weak reference to w, (data_ptr, _version), result); the entry goes
+# when w does. (A WeakKeyDictionary would compare two tensors with ==.)
+_CODES_CACHE: dict = {}
+
+
+def weight_codes(w: torch.Tensor) -> Optional[Tuple[torch.Tensor, torch.Tensor]]:
+    """Per-row int8 codes [rows, cols] and scales [rows] whose fp32 products
+    reproduce the fake-quantized weight w [rows, cols] (fp32 on the GPU) element
+    for element (``gs_weight_codes``), or None when a row is not such a product.
+    Found once per version of w: the verdict costs one device-to-host read, and
+    a frozen weight is not written again (any in-place write bumps ``_version``)."""
+    key = (w.data_ptr(), w._version)
+    hit = _CODES_CACHE.get(id(w))
+    if hit is not None and hit[0]() is w and hit[1] == key:
+        return hit[2]
+    lib = _lib if _lib is not None else load()
+    rows, cols = w.shape
+    src = w.contiguous()
+    codes = torch.empty((rows, cols), dtype=torch.int8, device=w.device)
+    scale = torch.empty(rows, dtype=torch.float32, device=w.device)
+    exact = torch.empty(rows, dtype=torch.int32, device=w.device)
+    with torch.cuda.device(w.device):
+        rc = lib.gs_weight_codes(src.data_ptr(), rows, cols, codes.data_ptr(), scale.data_ptr(), exact.data_ptr(),
+                                 current_stream_handle(w.device))
+    raise_for(rc, lib)
+    res = (codes, scale) if bool(exact.all()) else None
+    wid = id(w)
+    _CODES_CACHE[wid] = (weakref.ref(w, lambda _r, wid=wid: _CODES_CACHE.pop(wid, None)), key, res)
+    return res
 
 
 def _qfields(q: QuantTuple, name: str) -> tuple:
@@ -635,7 +676,7 @@ def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: to
            w2: Optional[torch.Tensor], bh: torch.Tensor, out: torch.Tensor,
            h_in_quant: QuantTuple, h_out_quant: QuantTuple, nblocks: int = 0, blksz: int = 0,
            log_n: int = 0, bfly_nblocks: int = 0, gh_save: Optional[torch.Tensor] = None,
-           contiguous: bool = False) -> None:
+           contiguous: bool = False, w_codes: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> None:
     """Fill gs_args from fp32 device tensors and call the entry point on the
     current torch stream of gi's device. contiguous: the caller guarantees that
     gi, h0 and out are contiguous (the wrappers make them so), which fixes their
@@ -676,16 +717,17 @@ def launch(kind: int, fn_name: str, *, gi: torch.Tensor, h0: torch.Tensor, w: to
                 raise_for(need, lib)
             _NEED[key] = need
     dev = gi.device
+    codes = (w_codes[0].data_ptr(), w_codes[1].data_ptr()) if w_codes is not None else None
     if dev.index == torch.cuda.current_device():
-        rc = _launch_current(lib, fn_name, ptrs, sizes, qi, qo, gh_ptr, dev, need, T if tagged else 0)
+        rc = _launch_current(lib, fn_name, ptrs, sizes, qi, qo, gh_ptr, dev, need, T if tagged else 0, codes)
     else:
         with torch.cuda.device(dev):
-            rc = _launch_current(lib, fn_name, ptrs, sizes, qi, qo, gh_ptr, dev, need, T if tagged else 0)
+            rc = _launch_current(lib, fn_name, ptrs, sizes, qi, qo, gh_ptr, dev, need, T if tagged else 0, codes)
     raise_for(rc, lib)
 
 
 def _launch_current(lib: ctypes.CDLL, fn_name: str, ptrs: tuple, sizes: tuple, qi: tuple, qo: tuple, gh_ptr: int,
-                    dev: torch.device, need: int, steps: int) -> int:
+                    dev: torch.device, need: int, steps: int, codes: Optional[tuple] = None) -> int:
     handle = current_stream_handle(dev)
     ws = workspace(dev, handle, need, steps=steps)
     mirror = 0
@@ -695,6 +737,8 @@ def _launch_current(lib: ctypes.CDLL, fn_name: str, ptrs: tuple, sizes: tuple, q
         _order_after_previous(dev, handle, lambda: torch.cuda.current_stream(dev))
         mirror = m[0].data_ptr()
     a = GS_ARGS.pack(*ptrs, ws.data_ptr(), ws.numel(), mirror, *sizes, *qi, *qo, gh_ptr)
+    if codes is not None:
+        return _raw_entry(lib, fn_name)(a, codes[0], codes[1], handle)
     return _raw_entry(lib, fn_name)(a, handle)
 
 

@@ -41,12 +41,25 @@ from . import _lib
 from ._common import QuantTuple, check_common, check_quant, cuda_f32, require_cuda, require_f32, save_gh_default
 
 
+def _int8_codes_apply(H: int, h_in_quant: QuantTuple) -> bool:
+    """Whether gs_dense_fwd_i8w would run its int8-weight kernel for this shape
+    and hidden quant (the persistent kernel exchanging q_in levels that fit a
+    byte), so that finding the codes is worth its device-to-host read."""
+    return (h_in_quant is not None and 64 < H <= 1024 and H % 4 == 0 and int(h_in_quant[1]) >= -128
+            and int(h_in_quant[2]) <= 127)
+
+
 def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.Tensor,
                    bh_cat: torch.Tensor, h_in_quant: QuantTuple, h_out_quant: QuantTuple,
-                   gh_save: Optional[torch.Tensor] = None, tiled: bool = False) -> torch.Tensor:
+                   gh_save: Optional[torch.Tensor] = None, tiled: bool = False,
+                   int8_codes: bool = False) -> torch.Tensor:
     """Runs gs_dense_fwd (tiled: gs_dense_fwd_tiled); with gh_save ([T, B, 3H]
     contiguous fp32) the kernel also stores every step's q_in(h_{t-1}) Wh^T (gh_t
-    without bh) there for the backward."""
+    without bh) there for the backward. int8_codes (forwards that need no
+    gradient): when Wh_cat is a per-row int8 fake-quantized weight (its codes
+    found once per version of the tensor, ``_lib.weight_codes``) and the hidden
+    quant makes the exchanged state int8 levels, gs_dense_fwd_i8w runs the step's
+    products on the int8 MFMA."""
     if not cuda_f32(gi, h0, Wh_cat, bh_cat):
         require_cuda(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
         require_f32(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
@@ -60,9 +73,15 @@ def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.T
     Wh_cat = Wh_cat.contiguous()
     bh_cat = bh_cat.contiguous()
     out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
+    codes = None
+    if int8_codes and not tiled and gh_save is None and _int8_codes_apply(H, h_in_quant):
+        codes = _lib.weight_codes(Wh_cat)
     if tiled:
         _lib.launch(_lib.KIND_DENSE_TILED, "gs_dense_fwd_tiled", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat,
                     out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, gh_save=gh_save, contiguous=True)
+    elif codes is not None:
+        _lib.launch(_lib.KIND_DENSE, "gs_dense_fwd_i8w", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat, out=out,
+                    h_in_quant=h_in_quant, h_out_quant=h_out_quant, contiguous=True, w_codes=codes)
     else:
         _lib.launch(_lib.KIND_DENSE, "gs_dense_fwd", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat, out=out,
                     h_in_quant=h_in_quant, h_out_quant=h_out_quant, gh_save=gh_save, contiguous=True)
@@ -80,7 +99,8 @@ def gru_scan_forward_persistent(
     **_ignored_tiling: Any,
 ) -> torch.Tensor:
     """Forward of the dense scan; returns out [T, B, H] (h_T = out[-1])."""
-    return _dense_forward("gru_scan_forward_persistent", gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant)
+    return _dense_forward("gru_scan_forward_persistent", gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant,
+                          int8_codes=True)
 
 
 def gru_scan_forward(
@@ -155,7 +175,8 @@ def _function_forward(ctx: Any, tiled: bool, gi, h0, Wh_cat, bh_cat, h_in_quant,
         T, B, G3 = gi.shape
         gh = torch.empty((T, B, G3), device=gi.device, dtype=torch.float32)
     who = "gru_scan_forward" if tiled else "gru_scan_forward_persistent"
-    out = _dense_forward(who, gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant, gh_save=gh, tiled=tiled)
+    out = _dense_forward(who, gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant, gh_save=gh, tiled=tiled,
+                         int8_codes=not any(ctx.needs_input_grad[:4]))
     ctx.save_for_backward(gi, h0, Wh_cat, bh_cat, out, gh)
     ctx.h_in_quant = check_quant(h_in_quant, "h_in_quant")
     ctx.h_out_quant = check_quant(h_out_quant, "h_out_quant")

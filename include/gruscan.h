@@ -62,7 +62,7 @@
 extern "C" {
 #endif
 
-#define GS_ABI_VERSION 4
+#define GS_ABI_VERSION 5
 
 #define GS_OK 0
 #define GS_ERR_INVALID (-1)  /* bad pointer, shape, stride or quant parameter (Python: ValueError) */
@@ -144,6 +144,20 @@ int gs_dense_fwd(const gs_args* args, hipStream_t stream);
  * bit-identical outputs; gs_dense_fwd is the faster of the two there (each step here
  * streams all 3 H^2 weights through one CU). gh_save as for gs_dense_fwd. */
 int gs_dense_fwd_tiled(const gs_args* args, hipStream_t stream);
+
+/* Dense forward with Wh also given as per-row int8 codes: w_codes [3H, H] int8
+ * (4-byte aligned) and w_scale [3H], such that args->w[i][k] is the fp32 product
+ * w_codes[i][k] * w_scale[i] for every element (gs_weight_codes recovers them from a
+ * fake-quantized Wh_cat). Same contract and results' tolerance as gs_dense_fwd, which
+ * it replaces for the frozen-int8 configuration of gru_scan_persistent
+ * (scan.py:1667-1685, the weight fake-quanted per row as in quantizers.py:188-199):
+ * when the persistent kernel exchanges int8 levels (q_in on, its levels in
+ * [-128, 127], H a multiple of 4, 64 < H <= 1024) and gh_save is NULL, the step's
+ * products run on the int8 MFMA over the h levels and the weight codes, whose
+ * integer sums are exact, and gh = sum * (w_scale[i] * q_in scale): within an fp32
+ * rounding of each product of gs_dense_fwd's fp32 chains, which round every partial
+ * sum. Every other launch is gs_dense_fwd's, codes unused. */
+int gs_dense_fwd_i8w(const gs_args* args, const int8_t* w_codes, const float* w_scale, hipStream_t stream);
 
 int gs_diagonal_fwd(const gs_args* args, hipStream_t stream);
 int gs_monarch_fwd(const gs_args* args, hipStream_t stream);
@@ -434,6 +448,15 @@ typedef struct gs_rows_args {
 } gs_rows_args;
 
 int gs_quantize_rows(const gs_rows_args* args, hipStream_t stream);
+
+/* The inverse for an already fake-quantized weight w [rows, cols] (contiguous): for
+ * each row, a scale s among fl(max|w| / 127) and its neighbours within two ulps such
+ * that every element is the fp32 product c * s of an integer code |c| <= 127 (what
+ * gs_quantize_rows' w_q holds for qmax = 127). Writes scale[r], codes[r][:] and
+ * exact[r] = 1, or exact[r] = 0 (codes 0) when no candidate reproduces the row.
+ * No counterpart in the reference; it feeds gs_dense_fwd_i8w. */
+int gs_weight_codes(const float* w, int64_t rows, int64_t cols, int8_t* codes, float* scale, int32_t* exact,
+                    hipStream_t stream);
 
 /* ---- dense form of a hidden map --------------------------------------------------
  * Writes the hidden map of any kind as the dense matrix m [3H, H] (rows r, z,
