@@ -23,7 +23,9 @@ Per kind:
   host_us_per_call  host time of one call with the queue kept ahead of the
                GPU (wrapper, C entry point and HIP launch; best of 3 x 50);
   roofline     algorithmic bytes or FLOPs per launch / kernel_ms against the
-               MI355X peak (HBM 8 TB/s; fp32 MFMA 157.3 TFLOP/s);
+               MI355X peak (HBM 8 TB/s; fp32 MFMA 157.3 TFLOP/s; for the int8
+               QAT configuration, whose products run on the int8 MFMA, dense
+               int8 5.0 POP/s);
   cpu_baseline the oracle (the reference's per-step PyTorch CPU path) timed on
                this host's cores on a bounded sample.
 
@@ -50,13 +52,17 @@ for _p in (ROOT, os.path.join(ROOT, "gru-triton_amd")):
 
 HBM_PEAK_GBS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+INT8_MFMA_PEAK_TOPS = 5000.0  # dense int8 MFMA
 
 # Algorithmic work per launch at the benchmark shapes (bytes: gi + out + hidden
 # weights + h0 + bias; FLOPs: the hidden projection only).
 WORK = {
     0: {"bytes": 16_855_040, "flops": 3 * 64 * 32 * 512, "bound": "hbm"},
     1: {"bytes": 19_994_624, "flops": 3_221_225_472, "bound": "mfma"},
-    2: {"bytes": 19_994_624, "flops": 3_221_225_472, "bound": "mfma"},
+    # int8 QAT: the products run on the int8 MFMA over the h levels and Wh's per-row
+    # int8 codes (gs_dense_fwd_i8w), so Wh is 3 H^2 code bytes + 3H scales and the
+    # peak is int8's
+    2: {"bytes": 17_641_472, "flops": 3_221_225_472, "bound": "mfma", "int8": True},
     3: {"bytes": 17_635_328, "flops": 805_306_368, "bound": "mfma"},
     4: {"bytes": 537_391_104, "flops": 3_019_898_880, "bound": "hbm"},
     # single-factor Monarch (not a BASELINE.json configuration): 2 T B 3H blksz flops;
@@ -83,6 +89,9 @@ def roofline(idx: int, kernel_ms: float) -> dict:
         return {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic}
     achieved = w["flops"] / (kernel_ms * 1e-3) / 1e12
+    if w.get("int8"):
+        return {"bound": "mfma", "achieved": round(achieved, 4), "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",
+                "frac": round(achieved / INT8_MFMA_PEAK_TOPS, 6), "traffic": traffic}
     return {"bound": "mfma", "achieved": round(achieved, 4), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 5), "traffic": traffic}
 
