@@ -290,6 +290,25 @@ __device__ __forceinline__ void mfma3_i8(const int (&a)[KC / 4], const int (&wi)
 // and every sum reduce16 forms is an integer of magnitude at most 2^24.
 __device__ __forceinline__ f4 i4_to_f4(i4 v) { return f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]}; }
 
+// reduce16 in integers, for chains whose sums may exceed 2^24 (K > 1024): the
+// exact sum for row s = (l >> 2) & 3, unit l & 3, in lane l. Where every sum
+// stays within 2^24 the float of it equals reduce16(i4_to_f4(acc), s).
+__device__ __forceinline__ int reduce16_i(i4 acc, int s) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    acc[c] += __builtin_amdgcn_mov_dpp(acc[c], 0x128, 0xF, 0xF, true);  // row_ror:8
+    acc[c] += __builtin_amdgcn_mov_dpp(acc[c], 0x124, 0xF, 0xF, true);  // row_ror:4
+  }
+  const int lo = (s & 1) ? acc[1] : acc[0];
+  const int hi = (s & 1) ? acc[3] : acc[2];
+  const int x = (s & 2) ? hi : lo;
+  typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+  const u2 a = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+  const int y = (int)(a[0] + a[1]);
+  const u2 b = __builtin_amdgcn_permlane32_swap((unsigned)y, (unsigned)y, false, false);
+  return (int)(b[0] + b[1]);
+}
+
 // ---- host side --------------------------------------------------------------------
 
 struct DevInfo {
@@ -354,7 +373,28 @@ inline int resident_groups(const void* fn, int threads, size_t lds, int per_grou
 constexpr int64_t kPersistentMaxH = 1024;
 inline bool dense_uses_tiled(const gs_args* a) { return a->H > kPersistentMaxH; }
 int64_t tiled_max_h();
-int run_tiled_fwd(const gs_args* a, hipStream_t stream, const char* who);
+int run_tiled_fwd(const gs_args* a, hipStream_t stream, const char* who, const int8_t* codes = nullptr,
+                  const float* scales = nullptr);
+
+// The dense forwards run their int8-weight instances (v_mfma_i32_4x4x4_16b_i8
+// over q_in levels and Wh's int8 codes) when every A operand is a q_in level
+// that fits a byte, rows of codes load as 16-byte words, the persistent kernel
+// is in remote mode (H > 64) and no gh is saved. The rule is the same for the
+// persistent and the batch-tiled kernel, so the two give the same outputs.
+inline bool dense_i8_applies(const gs_args* a) {
+  return a->q_in.enabled && a->q_in.qmin >= -128 && a->q_in.qmax <= 127 && a->H > 64 && a->H % 16 == 0 &&
+         a->gh_save == nullptr;
+}
+
+// Arguments of the int8-weight entry points: both arrays given, the codes
+// 16-byte aligned (the batch-tiled kernel loads 16 codes per lane).
+inline int check_codes(const int8_t* codes, const float* scales, const char* who) {
+  if (codes == nullptr || scales == nullptr)
+    return set_error(GS_ERR_INVALID, "%s: w_codes and w_scale are required", who);
+  if ((reinterpret_cast<uintptr_t>(codes) & 15u) != 0)
+    return set_error(GS_ERR_INVALID, "%s: w_codes must be 16-byte aligned", who);
+  return GS_OK;
+}
 int64_t tiled_bwd_wt_bytes(int64_t H);
 int run_tiled_bwd_recurrence(const float* w, float* wt, const float* dout, const float* cg, const float* zm,
                              const float* mi, float* dsum, float* dh0, int64_t T, int64_t B, int64_t H,

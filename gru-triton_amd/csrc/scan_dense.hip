@@ -507,9 +507,9 @@ int run(int kind, const gs_args* a, hipStream_t stream, const char* who, const i
   if (rc) return rc;
   rc = check_workspace(a, kCtrlBytes + pl.xh_bytes + pl.xw_bytes, who);
   if (rc) return rc;
-  // every A operand must be a q_in level in the published levels' scale
-  const bool i8 = codes != nullptr && kind == kDense && pl.pack && a->gh_save == nullptr && a->q_in.enabled &&
-                  a->q_in.scale == pl.pscale && a->q_in.qmin >= -128 && a->q_in.qmax <= 127;
+  // every A operand must be a q_in level in the published levels' scale (with q_in on,
+  // the packed exchange publishes q_in's levels)
+  const bool i8 = codes != nullptr && kind == kDense && dense_i8_applies(a) && pl.pack && a->q_in.scale == pl.pscale;
   DFn fn = pick(kind, pl.remote, pl.KC, &pl.nt, pl.pack, a->gh_save != nullptr, i8);
   const int threads = 64 * (pl.nwc + (pl.remote ? 4 * pollers_per_row(pl.KC) : 0));
   const int per_set = pl.P * (kind == kMonarch1 ? pl.nb : 1);
@@ -612,11 +612,9 @@ extern "C" int gs_dense_fwd_i8w(const gs_args* a, const int8_t* w_codes, const f
   int rc = gs::validate_common(a, who, true);
   if (rc) return rc;
   if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
-  if (w_codes == nullptr || w_scale == nullptr)
-    return gs::set_error(GS_ERR_INVALID, "%s: w_codes and w_scale are required", who);
-  if (reinterpret_cast<uintptr_t>(w_codes) % 4 != 0)
-    return gs::set_error(GS_ERR_INVALID, "%s: w_codes must be 4-byte aligned", who);
-  if (gs::dense_uses_tiled(a)) return gs::run_tiled_fwd(a, stream, who);
+  rc = gs::check_codes(w_codes, w_scale, who);
+  if (rc) return rc;
+  if (gs::dense_uses_tiled(a)) return gs::run_tiled_fwd(a, stream, who, w_codes, w_scale);
   return gs::run(gs::kDense, a, stream, who, w_codes, w_scale);
 }
 

@@ -51,6 +51,10 @@ struct TFParams {
   const float* bh;
   float* out;
   float* gh_save;  // SAVE: [T, B, 3H] q_in(h_{t-1}) Wh^T (no bias)
+  const int8_t* wq;  // I8: int8 codes of Wh [3H, H], w == fl(code * wsc[row])
+  const float* wsc;  // I8: the code scale of each of Wh's 3H rows
+  float pscale;      // I8: q_in's scale (the staged state is q_in levels)
+  int rsi;           // I8: LDS row stride of the staged levels, words (16 mod 64)
   int64_t sg_t, sg_b, sh0_b, so_t, so_b;
   int T, B, H;
   int BT;   // batch rows per workgroup
@@ -79,8 +83,19 @@ constexpr int kItemLoads = 6;         // 12 rows, 2 per load instruction
 // 4 addresses per float4 and spills at 3
 template <bool VEC> constexpr int kFwdDepth = VEC ? 3 : 2;
 
-template <bool VEC, bool SAVE>
+// Int8 weights (I8): the products of gs_dense_fwd_i8w's persistent instance
+// (scan_dense.hip) on the same item pipeline. The state is staged as q_in
+// levels (word c of a row holds k = 4 c .. 4 c + 3, one byte each), an item is
+// 512 k of the quad's 12 code rows (the same 6 KiB of 16-byte loads and the
+// same staging buffer as 128 k of fp32), and each 64-k chunk is one
+// v_mfma_i32_4x4x4_16b_i8 per gate. The integer sums are exact, reduced in
+// integers, and gh = sum * (row scale * q_in scale): bit for bit the persistent
+// instance's gh wherever it runs (K <= 1024, sums within 2^24).
+template <bool VEC, bool SAVE, bool I8 = false>
 __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
+  static_assert(!I8 || (VEC && !SAVE), "int8 weights: 16-byte code loads, no saved gh");
+  constexpr int IK = I8 ? 4 * kItemK : kItemK;  // k per item
+  constexpr int ICH = IK / 64;                  // 64-k chunks per item
   extern __shared__ float lds[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -93,14 +108,29 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
   float* hraw = hq + BT * rs;        // [BT][hr] raw h_{t-1}
   float* wbuf = hraw + BT * hr + wave * kItemFloats;  // this wave's weight staging buffer
 
-  for (int i = threadIdx.x; i < BT * rs; i += kTileThreads) {
-    const int rr = i / rs, k = i - rr * rs, row = row0 + rr;
-    float v = 0.0f;
-    if (k < H && row < p.B) {
-      v = p.h0[(int64_t)row * p.sh0_b + k];
-      if (p.qin.on) v = fake_quant(v, p.qin);
+  int* hqi = reinterpret_cast<int*>(hq);  // I8: [BT][rsi] staged q_in levels, zero from H on
+  if constexpr (I8) {
+    for (int i = threadIdx.x; i < BT * p.rsi; i += kTileThreads) {
+      const int rr = i / p.rsi, c = i - rr * p.rsi, row = row0 + rr;
+      uint32_t wd = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int k = 4 * c + e;
+        if (k < H && row < p.B)
+          wd |= ((uint32_t)(int)quant_level(p.h0[(int64_t)row * p.sh0_b + k], p.qin) & 0xffu) << (8 * e);
+      }
+      hqi[i] = (int)wd;
     }
-    hq[i] = v;
+  } else {
+    for (int i = threadIdx.x; i < BT * rs; i += kTileThreads) {
+      const int rr = i / rs, k = i - rr * rs, row = row0 + rr;
+      float v = 0.0f;
+      if (k < H && row < p.B) {
+        v = p.h0[(int64_t)row * p.sh0_b + k];
+        if (p.qin.on) v = fake_quant(v, p.qin);
+      }
+      hq[i] = v;
+    }
   }
   for (int i = threadIdx.x; i < BT * hr; i += kTileThreads) {
     const int rr = i / hr, k = i - rr * hr, row = row0 + rr;
@@ -112,6 +142,7 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
   const int nq = (H + 3) >> 2;
   const bool a_ok = r < BT;
   const float* arow = hq + (a_ok ? r : 0) * rs + 4 * kb;
+  const int* arowi = hqi + (a_ok ? r : 0) * p.rsi + kb;  // I8: word 16 c of chunk c
   const int64_t HH = (int64_t)H * H;
   const int row = row0 + s;
   const bool row_ok = lead && s < BT && row < p.B;
@@ -121,25 +152,32 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
   const int kl = 4 * (lane & 31), rh = lane >> 5;
   float* wst = wbuf + rh * kItemRS + kl;        // + 2 i kItemRS for load instruction i
   const float* wop = wbuf + j * kItemRS + 4 * kb;  // + 4 g kItemRS + 64 c for gate g, chunk c
+  const int* wopi = reinterpret_cast<const int*>(wbuf) + j * kItemRS + kb;  // I8: + 4 g kItemRS + 16 c
   const int myq = wave < nq ? (nq - 1 - wave) / kTileWaves + 1 : 0;
-  const int nbat = (H + kItemK - 1) / kItemK;   // items per quad
+  const int nbat = (H + IK - 1) / IK;   // items per quad
   const int nit = myq * nbat;
   for (int t = 0; t < p.T; ++t) {
     const float* git = p.gi + (int64_t)t * p.sg_t + (int64_t)row_c * p.sg_b;
-    // Item (q, b): k in [b kItemK, (b + 1) kItemK) of quad q's 12 rows, loaded
-    // coalesced into registers; also the quad's gate inputs and biases (raw).
+    // Item (q, b): k in [b IK, (b + 1) IK) of quad q's 12 rows, loaded
+    // coalesced into registers; also the quad's gate inputs and biases (raw),
+    // and for I8 the rows' code scales times q_in's scale.
     struct Item {
       f4 w[kItemLoads];
-      float g[3], bb[3];
+      float g[3], bb[3], sc[I8 ? 3 : 1];
     };
     auto load = [&](int q, int b, Item& it) {
 #pragma unroll
       for (int i = 0; i < kItemLoads; ++i) {
         const int rr = 2 * i + rh, g = rr >> 2, u = 4 * q + (rr & 3);
-        const int k = b * kItemK + kl;
+        const int k = b * IK + (I8 ? 4 * kl : kl);  // I8: byte k, 16 codes a lane
         const bool ok = u < H && k < H;
         const int64_t off = g * HH + (int64_t)(u < H ? u : H - 1) * H + k;
-        if constexpr (VEC) {
+        if constexpr (I8) {
+          typedef int i4v __attribute__((ext_vector_type(4)));
+          const i4v v = *reinterpret_cast<const i4v*>(p.wq + (ok ? off : 0));
+          const f4 bits = __builtin_bit_cast(f4, v);  // staged as raw words
+          it.w[i] = ok ? bits : f4{0.f, 0.f, 0.f, 0.f};
+        } else if constexpr (VEC) {
           const f4 v = *reinterpret_cast<const f4*>(p.w + (ok ? off : 0));
           it.w[i] = ok ? v : f4{0.f, 0.f, 0.f, 0.f};
         } else {
@@ -156,9 +194,11 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
       for (int g = 0; g < 3; ++g) {
         it.g[g] = git[g * H + uc];
         it.bb[g] = p.bh[g * H + uc];
+        if constexpr (I8) it.sc[g] = p.wsc[g * H + uc] * p.pscale;
       }
     };
     f4 p0[3], p1[3];
+    i4 n0[3], n1[3];  // I8 accumulators
     // one item: stage its weights, its MFMAs, and after a quad's last item the
     // reduction and the gate epilogue (the staging buffer is this wave's alone,
     // and a wave's LDS accesses complete in order, so no barrier is needed)
@@ -167,26 +207,46 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
       for (int i = 0; i < kItemLoads; ++i) *reinterpret_cast<f4*>(wst + 2 * i * kItemRS) = it.w[i];
       if (b == 0) {
 #pragma unroll
-        for (int g = 0; g < 3; ++g) p0[g] = p1[g] = f4{0.f, 0.f, 0.f, 0.f};
+        for (int g = 0; g < 3; ++g) {
+          p0[g] = p1[g] = f4{0.f, 0.f, 0.f, 0.f};
+          n0[g] = n1[g] = i4{0, 0, 0, 0};
+        }
       }
 #pragma unroll
-      for (int ci = 0; ci < kItemK / 64; ++ci) {
-        const int c = b * (kItemK / 64) + ci;
+      for (int ci = 0; ci < ICH; ++ci) {
+        const int c = b * ICH + ci;
         if (c >= p.nch) break;  // uniform
-        const f4 a = a_ok ? *reinterpret_cast<const f4*>(arow + 64 * c) : f4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (I8) {
+          const int a = a_ok ? arowi[16 * c] : 0;
 #pragma unroll
-        for (int g = 0; g < 3; ++g) {
-          const f4 wv = *reinterpret_cast<const f4*>(wop + 4 * g * kItemRS + 64 * ci);
-          p0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[0], wv[0], p0[g], 0, 0, 0);
-          p1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[1], wv[1], p1[g], 0, 0, 0);
-          p0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[2], wv[2], p0[g], 0, 0, 0);
-          p1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[3], wv[3], p1[g], 0, 0, 0);
+          for (int g = 0; g < 3; ++g) {
+            const int wv = wopi[4 * g * kItemRS + 16 * ci];
+            if (ci & 1)
+              n1[g] = __builtin_amdgcn_mfma_i32_4x4x4i8(a, wv, n1[g], 0, 0, 0);
+            else
+              n0[g] = __builtin_amdgcn_mfma_i32_4x4x4i8(a, wv, n0[g], 0, 0, 0);
+          }
+        } else {
+          const f4 a = a_ok ? *reinterpret_cast<const f4*>(arow + 64 * c) : f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int g = 0; g < 3; ++g) {
+            const f4 wv = *reinterpret_cast<const f4*>(wop + 4 * g * kItemRS + 64 * ci);
+            p0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[0], wv[0], p0[g], 0, 0, 0);
+            p1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[1], wv[1], p1[g], 0, 0, 0);
+            p0[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[2], wv[2], p0[g], 0, 0, 0);
+            p1[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(a[3], wv[3], p1[g], 0, 0, 0);
+          }
         }
       }
       if (b != nbat - 1) return;
       float gh[3];
 #pragma unroll
-      for (int g = 0; g < 3; ++g) gh[g] = reduce16(p0[g] + p1[g], s);
+      for (int g = 0; g < 3; ++g) {
+        if constexpr (I8)
+          gh[g] = (float)reduce16_i(n0[g] + n1[g], s) * it.sc[g];
+        else
+          gh[g] = reduce16(p0[g] + p1[g], s);
+      }
       const int u = 4 * q + j;
       if (row_ok && u < H) {
         float* hp = hraw + s * hr + u;
@@ -224,11 +284,24 @@ __global__ __launch_bounds__(kTileThreads) void tiled_fwd_kernel(TFParams p) {
     }
     lds_barrier();
     if (t + 1 < p.T) {
-      for (int i = threadIdx.x; i < BT * H; i += kTileThreads) {
-        const int rr = i / H, k = i - rr * H;
-        float v = hraw[rr * hr + k];
-        if (p.qin_after_first) v = fake_quant(v, p.qin);
-        hq[rr * rs + k] = v;
+      if constexpr (I8) {
+        // q_in levels of the new state (of q_out's value when q_in repeats q_out: the same level)
+        const int nw = H >> 2;
+        for (int i = threadIdx.x; i < BT * nw; i += kTileThreads) {
+          const int rr = i / nw, c = i - rr * nw;
+          const float* hv = hraw + rr * hr + 4 * c;
+          uint32_t wd = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wd |= ((uint32_t)(int)quant_level(hv[e], p.qin) & 0xffu) << (8 * e);
+          hqi[rr * p.rsi + c] = (int)wd;
+        }
+      } else {
+        for (int i = threadIdx.x; i < BT * H; i += kTileThreads) {
+          const int rr = i / H, k = i - rr * H;
+          float v = hraw[rr * hr + k];
+          if (p.qin_after_first) v = fake_quant(v, p.qin);
+          hq[rr * rs + k] = v;
+        }
       }
       lds_barrier();
     }
@@ -418,7 +491,10 @@ int plan_tiled(int64_t H, int64_t B, bool bwd, TilePlan* tp, const char* who) {
 // is larger; the backward's three staged gate rows set the common limit).
 int64_t tiled_max_h() { return 8192; }
 
-int run_tiled_fwd(const gs_args* a, hipStream_t stream, const char* who) {
+// codes / scales: Wh's int8 codes and row scales (gs_dense_fwd_i8w,
+// gs_dense_fwd_tiled_i8w), or NULL; used when the launch qualifies.
+int run_tiled_fwd(const gs_args* a, hipStream_t stream, const char* who, const int8_t* codes,
+                  const float* scales) {
   if (a->H > tiled_max_h())
     return set_error(GS_ERR_INVALID, "%s: hidden size %lld exceeds the supported maximum of %lld", who,
                      (long long)a->H, (long long)tiled_max_h());
@@ -450,8 +526,14 @@ int run_tiled_fwd(const gs_args* a, hipStream_t stream, const char* who) {
   // float4 weight loads: rows of a multiple of 4 floats from a 16-byte aligned base
   const bool vec = a->H % 4 == 0 && (reinterpret_cast<uintptr_t>(a->w) & 15u) == 0;
   const bool save = a->gh_save != nullptr;
-  void (*fn)(TFParams) = vec ? (save ? tiled_fwd_kernel<true, true> : tiled_fwd_kernel<true, false>)
-                             : (save ? tiled_fwd_kernel<false, true> : tiled_fwd_kernel<false, false>);
+  const bool i8 = codes != nullptr && dense_i8_applies(a) && (reinterpret_cast<uintptr_t>(codes) & 15u) == 0;
+  p.wq = i8 ? codes : nullptr;
+  p.wsc = i8 ? scales : nullptr;
+  p.pscale = a->q_in.scale;
+  p.rsi = 64 * ((tp.nch + 3) / 4) + 16;
+  void (*fn)(TFParams) = i8    ? tiled_fwd_kernel<true, false, true>
+                         : vec ? (save ? tiled_fwd_kernel<true, true> : tiled_fwd_kernel<true, false>)
+                               : (save ? tiled_fwd_kernel<false, true> : tiled_fwd_kernel<false, false>);
   if (tp.lds > 65536)
     GS_CHECK_HIP(hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)tp.lds));
   const int64_t nblk = (a->B + tp.BT - 1) / tp.BT;
@@ -513,4 +595,16 @@ extern "C" int gs_dense_fwd_tiled(const gs_args* a, hipStream_t stream) {
   if (rc) return rc;
   if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
   return gs::run_tiled_fwd(a, stream, who);
+}
+
+extern "C" int gs_dense_fwd_tiled_i8w(const gs_args* a, const int8_t* w_codes, const float* w_scale,
+                                      hipStream_t stream) {
+  gs::clear_error();
+  const char* who = "gs_dense_fwd_tiled_i8w";
+  int rc = gs::validate_common(a, who, true);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the dense kind", who);
+  rc = gs::check_codes(w_codes, w_scale, who);
+  if (rc) return rc;
+  return gs::run_tiled_fwd(a, stream, who, w_codes, w_scale);
 }

@@ -36,6 +36,7 @@ EXPORTS = (
     "gs_dense_fwd",
     "gs_dense_fwd_tiled",
     "gs_dense_fwd_i8w",
+    "gs_dense_fwd_tiled_i8w",
     "gs_weight_codes",
     "gs_dense_fwd_noalloc",
     "gs_diagonal_fwd",
@@ -618,11 +619,11 @@ _NEED: dict = {}  # workspace bytes per (kind, sizes, quant) of the tagged kinds
 
 def _raw_entry(lib: ctypes.CDLL, fn_name: str):
     """The entry point as a function of (packed gs_args bytes, stream handle), or
-    for gs_dense_fwd_i8w of (packed gs_args bytes, codes, scales, stream handle)."""
+    for the int8-weight entry points of (packed gs_args bytes, codes, scales, stream handle)."""
     fn = _RAW_FN.get(fn_name)
     if fn is None:
         fn = lib[fn_name]  # an independent function object: its argtypes do not touch getattr(lib, ...)
-        if fn_name == "gs_dense_fwd_i8w":
+        if fn_name in ("gs_dense_fwd_i8w", "gs_dense_fwd_tiled_i8w"):
             fn.argtypes = [ctypes.c_char_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         else:
             fn.argtypes = [ctypes.c_char_p, ctypes.c_void_p]

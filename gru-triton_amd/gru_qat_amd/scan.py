@@ -42,10 +42,12 @@ from ._common import QuantTuple, check_common, check_quant, cuda_f32, require_cu
 
 
 def _int8_codes_apply(H: int, h_in_quant: QuantTuple) -> bool:
-    """Whether gs_dense_fwd_i8w would run its int8-weight kernel for this shape
-    and hidden quant (the persistent kernel exchanging q_in levels that fit a
-    byte), so that finding the codes is worth its device-to-host read."""
-    return (h_in_quant is not None and 64 < H <= 1024 and H % 4 == 0 and int(h_in_quant[1]) >= -128
+    """Whether the int8-weight entry points (gs_dense_fwd_i8w,
+    gs_dense_fwd_tiled_i8w) run their int8-MFMA kernels for this shape and
+    hidden quant (every A operand a q_in level that fits a byte, H > 64 and a
+    multiple of 16), so that finding the codes is worth its device-to-host read.
+    The rule is the library's dense_i8_applies."""
+    return (h_in_quant is not None and H > 64 and H % 16 == 0 and int(h_in_quant[1]) >= -128
             and int(h_in_quant[2]) <= 127)
 
 
@@ -57,9 +59,10 @@ def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.T
     contiguous fp32) the kernel also stores every step's q_in(h_{t-1}) Wh^T (gh_t
     without bh) there for the backward. int8_codes (forwards that need no
     gradient): when Wh_cat is a per-row int8 fake-quantized weight (its codes
-    found once per version of the tensor, ``_lib.weight_codes``) and the hidden
-    quant makes the exchanged state int8 levels, gs_dense_fwd_i8w runs the step's
-    products on the int8 MFMA."""
+    found once per version of the tensor, ``_lib.weight_codes``) and every A
+    operand is a q_in level that fits a byte, gs_dense_fwd_i8w (tiled:
+    gs_dense_fwd_tiled_i8w) runs the step's products on the int8 MFMA; the two
+    kernels then agree bit for bit as their fp32 forms do."""
     if not cuda_f32(gi, h0, Wh_cat, bh_cat):
         require_cuda(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
         require_f32(who, gi=gi, h0=h0, Wh_cat=Wh_cat, bh_cat=bh_cat)
@@ -74,9 +77,12 @@ def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.T
     bh_cat = bh_cat.contiguous()
     out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
     codes = None
-    if int8_codes and not tiled and gh_save is None and _int8_codes_apply(H, h_in_quant):
+    if int8_codes and gh_save is None and _int8_codes_apply(H, h_in_quant):
         codes = _lib.weight_codes(Wh_cat)
-    if tiled:
+    if tiled and codes is not None:
+        _lib.launch(_lib.KIND_DENSE_TILED, "gs_dense_fwd_tiled_i8w", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat,
+                    out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, contiguous=True, w_codes=codes)
+    elif tiled:
         _lib.launch(_lib.KIND_DENSE_TILED, "gs_dense_fwd_tiled", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat,
                     out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, gh_save=gh_save, contiguous=True)
     elif codes is not None:
@@ -114,7 +120,8 @@ def gru_scan_forward(
 ) -> torch.Tensor:
     """Same contract as the reference's barrier-free launcher (scan.py:1688-1765):
     the batch-tiled kernel, no co-residency requirement, any H up to 8192."""
-    return _dense_forward("gru_scan_forward", gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant, tiled=True)
+    return _dense_forward("gru_scan_forward", gi, h0, Wh_cat, bh_cat, h_in_quant, h_out_quant, tiled=True,
+                          int8_codes=True)
 
 
 def gru_scan_backward_persistent(gi, h0, Wh_cat, bh_cat, out, dout, *, h_in_quant=None, h_out_quant=None,

@@ -146,18 +146,25 @@ int gs_dense_fwd(const gs_args* args, hipStream_t stream);
 int gs_dense_fwd_tiled(const gs_args* args, hipStream_t stream);
 
 /* Dense forward with Wh also given as per-row int8 codes: w_codes [3H, H] int8
- * (4-byte aligned) and w_scale [3H], such that args->w[i][k] is the fp32 product
+ * (16-byte aligned) and w_scale [3H], such that args->w[i][k] is the fp32 product
  * w_codes[i][k] * w_scale[i] for every element (gs_weight_codes recovers them from a
  * fake-quantized Wh_cat). Same contract and results' tolerance as gs_dense_fwd, which
  * it replaces for the frozen-int8 configuration of gru_scan_persistent
  * (scan.py:1667-1685, the weight fake-quanted per row as in quantizers.py:188-199):
- * when the persistent kernel exchanges int8 levels (q_in on, its levels in
- * [-128, 127], H a multiple of 4, 64 < H <= 1024) and gh_save is NULL, the step's
- * products run on the int8 MFMA over the h levels and the weight codes, whose
- * integer sums are exact, and gh = sum * (w_scale[i] * q_in scale): within an fp32
- * rounding of each product of gs_dense_fwd's fp32 chains, which round every partial
- * sum. Every other launch is gs_dense_fwd's, codes unused. */
+ * when every A operand is a q_in level in [-128, 127] (q_in on), H > 64 is a multiple
+ * of 16 and gh_save is NULL, the step's products run on the int8 MFMA over the h
+ * levels and the weight codes, whose integer sums are exact, and gh = sum *
+ * (w_scale[i] * q_in scale): within an fp32 rounding of each product of gs_dense_fwd's
+ * fp32 chains, which round every partial sum. Every other launch is gs_dense_fwd's,
+ * codes unused. H > 1024 runs gs_dense_fwd_tiled_i8w's kernel. */
 int gs_dense_fwd_i8w(const gs_args* args, const int8_t* w_codes, const float* w_scale, hipStream_t stream);
+
+/* gs_dense_fwd_tiled with the int8 codes of gs_dense_fwd_i8w (reference gru_scan_forward,
+ * scan.py:1688-1765, on frozen int8 weights): the batch-tiled kernel reads the codes
+ * instead of the fp32 weights every step (a quarter of the bytes) and runs the same
+ * int8 products under the same rule, so it returns gs_dense_fwd_i8w's outputs bit for
+ * bit up to H = 1024. No counterpart in the reference beyond that entry point. */
+int gs_dense_fwd_tiled_i8w(const gs_args* args, const int8_t* w_codes, const float* w_scale, hipStream_t stream);
 
 int gs_diagonal_fwd(const gs_args* args, hipStream_t stream);
 int gs_monarch_fwd(const gs_args* args, hipStream_t stream);

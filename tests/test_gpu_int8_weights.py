@@ -5,11 +5,13 @@ fake-quantized per row as quantizers.py:188-199 does)
 hands the scan a weight whose every element is the fp32 product of an int8 code
 and its row's scale. gru_scan_forward_persistent then finds those codes once
 per version of the tensor and runs the step's products on the int8 MFMA over the
-exchanged h levels and the codes. Checked here: the codes reproduce the weight
+exchanged h levels and the codes; gru_scan_forward (the batch-tiled kernel)
+does the same on its own pipeline. Checked here: the codes reproduce the weight
 bit for bit, rows that are not such products are refused, the int8 path meets
 the oracle's parity bar (codes bit-exact away from rounding boundaries) in
-every hidden-quant arrangement it serves, and every launch it does not serve
-returns gs_dense_fwd's result bit for bit.
+every hidden-quant arrangement it serves, the persistent and batch-tiled int8
+forwards agree bit for bit, and every launch the int8 path does not serve
+returns the fp32 kernels' result bit for bit.
 """
 
 from __future__ import annotations
@@ -82,8 +84,10 @@ CASES = [
     ((16, 8, 128), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
     ((9, 5, 1024), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
     ((12, 37, 256), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
-    ((7, 3, 68), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
-    ((20, 6, 300), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
+    ((7, 3, 80), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
+    ((20, 6, 304), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
+    ((6, 5, 1536), Q_INT8_HIDDEN, Q_INT8_HIDDEN),  # H > 1024: the batch-tiled int8 kernel
+    ((5, 3, 2048), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
     ((16, 8, 512), Q_INT8_HIDDEN, None),
     ((16, 8, 512), Q_INT8_HIDDEN, Q_OTHER),
     ((10, 9, 256), Q_OTHER, Q_INT8_HIDDEN),
@@ -97,13 +101,13 @@ def _cfg(shape, q_in, q_out):
     return cfg
 
 
-def _both(cfg, dev):
+def _both(cfg, dev, tiled=False):
     import gru_qat_amd.scan as S
 
     d = to_dev(cfg, dev)
     args = (d["gi"], d["h0"], d["w"], d["bh"], cfg["h_in_quant"], cfg["h_out_quant"])
-    fp32 = S._dense_forward("fp32 products", *args, int8_codes=False)
-    i8 = S._dense_forward("int8 products", *args, int8_codes=True)
+    fp32 = S._dense_forward("fp32 products", *args, int8_codes=False, tiled=tiled)
+    i8 = S._dense_forward("int8 products", *args, int8_codes=True, tiled=tiled)
     return fp32, i8
 
 
@@ -134,13 +138,40 @@ def test_int8_products_match_the_oracle(dev, shape, q_in, q_out):
 
 
 @pytest.mark.parametrize("shape,q_in,q_out", [
+    ((64, 32, 512), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
+    ((12, 37, 256), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
+    ((9, 5, 1024), Q_INT8_HIDDEN, Q_INT8_HIDDEN),
+    ((16, 8, 512), Q_INT8_HIDDEN, None),
+    ((16, 8, 512), Q_INT8_HIDDEN, Q_OTHER),
+    ((10, 9, 256), Q_OTHER, Q_INT8_HIDDEN),
+])
+def test_tiled_int8_bit_identical_to_persistent(dev, shape, q_in, q_out):
+    """gru_scan_forward and gru_scan_forward_persistent on int8 weights: the
+    batch-tiled and persistent int8 instances form the same exact integer sums
+    and the same gate arithmetic."""
+    import gru_qat_amd as G
+
+    cfg = _cfg(shape, q_in, q_out)
+    d = to_dev(cfg, dev)
+    kw = dict(h_in_quant=q_in, h_out_quant=q_out)
+    a = G.gru_scan_forward(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    b = G.gru_scan_forward_persistent(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    log(f"[int8w] tiled vs persistent {shape}: {int((a != b).sum())} elements differ")
+    assert torch.equal(a, b)
+    fp32_t, i8_t = _both(cfg, dev, tiled=True)
+    assert torch.equal(i8_t, a)
+
+
+@pytest.mark.parametrize("shape,q_in,q_out", [
     ((16, 8, 512), None, Q_INT8_HIDDEN),   # q_in off: h0 is not a level
     ((8, 4, 64), Q_INT8_HIDDEN, Q_INT8_HIDDEN),  # one workgroup: no exchange
+    ((8, 4, 68), Q_INT8_HIDDEN, Q_INT8_HIDDEN),  # H not a multiple of 16
     ((8, 4, 512), (1.0 / 500, -500, 500), (1.0 / 500, -500, 500)),  # levels wider than a byte
 ])
-def test_launches_outside_the_int8_path_are_unchanged(dev, shape, q_in, q_out):
+@pytest.mark.parametrize("tiled", [False, True])
+def test_launches_outside_the_int8_path_are_unchanged(dev, shape, q_in, q_out, tiled):
     cfg = _cfg(shape, q_in, q_out)
-    fp32, i8 = _both(cfg, dev)
+    fp32, i8 = _both(cfg, dev, tiled=tiled)
     assert torch.equal(fp32, i8)
 
 
@@ -160,8 +191,8 @@ def _entry(dev, cfg, codes, scale, name="gs_dense_fwd_i8w"):
                     out.data_ptr(), ws.data_ptr(), ws.numel(), None, T, B, H, d["gi"].stride(0), d["gi"].stride(1),
                     d["h0"].stride(0), out.stride(0), out.stride(1), 0, 0, 0, 0,
                     _lib.make_quant(cfg["h_in_quant"], "q"), _lib.make_quant(cfg["h_out_quant"], "q"), None)
-    fn = lib["gs_dense_fwd_i8w"] if name == "gs_dense_fwd_i8w" else lib[name]
-    if name == "gs_dense_fwd_i8w":
+    fn = lib[name]
+    if name.endswith("_i8w"):
         fn.argtypes = [ctypes.POINTER(_lib.GsArgs), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         rc = fn(ctypes.byref(a), codes, scale, ctypes.c_void_p(_lib.current_stream_handle(dev)))
     else:
@@ -171,19 +202,20 @@ def _entry(dev, cfg, codes, scale, name="gs_dense_fwd_i8w"):
     return rc, out, lib
 
 
-def test_entry_point_through_the_c_abi(dev):
-    """gs_dense_fwd_i8w called directly: the int8 path on a config-2 input
-    agrees with the Python route; NULL codes and a misaligned code pointer are
-    refused before any launch."""
+@pytest.mark.parametrize("name", ["gs_dense_fwd_i8w", "gs_dense_fwd_tiled_i8w"])
+def test_entry_point_through_the_c_abi(dev, name):
+    """The int8-weight entry points called directly: on a config-2 input they
+    agree with the Python route; NULL codes and a code pointer that is not
+    16-byte aligned are refused before any launch."""
     from gru_qat_amd import _lib
 
     cfg = make_config(2, shape=(16, 8, 256))
     codes, scale = _codes(cfg["w"].to(dev))
-    rc, out, lib = _entry(dev, cfg, codes.data_ptr(), scale.data_ptr())
+    rc, out, lib = _entry(dev, cfg, codes.data_ptr(), scale.data_ptr(), name)
     assert rc == 0
     _, i8 = _both(cfg, dev)
     assert torch.equal(out, i8)
-    rc, _, _ = _entry(dev, cfg, None, scale.data_ptr())
+    rc, _, _ = _entry(dev, cfg, None, scale.data_ptr(), name)
     assert rc == _lib.GS_ERR_INVALID and b"w_codes" in lib.gs_last_error()
-    rc, _, _ = _entry(dev, cfg, codes.data_ptr() + 1, scale.data_ptr())
+    rc, _, _ = _entry(dev, cfg, codes.data_ptr() + 4, scale.data_ptr(), name)
     assert rc == _lib.GS_ERR_INVALID and b"aligned" in lib.gs_last_error()

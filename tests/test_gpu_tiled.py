@@ -66,18 +66,17 @@ def test_gru_scan_by_name_matches_oracle(dev, fn, shape):
 def test_gru_scan_qat_matches_oracle(dev, shape):
     """Frozen int8 hidden fake-quant through gru_scan (reference
     test_triton_qat_matches_pytorch, tests/test_triton_scan.py:291-380):
-    codes bit-exact away from rounding boundaries. The batch-tiled forward is
-    bit for bit the persistent kernel's fp32 products; the public persistent
-    forward runs this configuration's int8 weights on the int8 MFMA
-    (test_gpu_int8_weights.py) and is held to the oracle here."""
+    codes bit-exact away from rounding boundaries. This configuration's weights
+    are int8 codes, so at H = 512 both forwards run their int8-MFMA instances
+    (test_gpu_int8_weights.py), which agree bit for bit as the fp32 ones do."""
     cfg = make_config(2, shape=shape)
     d = to_dev(cfg, dev)
     import gru_qat_amd as G
-    import gru_qat_amd.scan as S
 
-    q_in, q_out = cfg["h_in_quant"], cfg["h_out_quant"]
-    out_t = G.gru_scan_forward(d["gi"], d["h0"], d["w"], d["bh"], h_in_quant=q_in, h_out_quant=q_out)
-    out_p = S._dense_forward("fp32 products", d["gi"], d["h0"], d["w"], d["bh"], q_in, q_out, int8_codes=False)
+    out_t = G.gru_scan_forward(d["gi"], d["h0"], d["w"], d["bh"], h_in_quant=cfg["h_in_quant"],
+                               h_out_quant=cfg["h_out_quant"])
+    out_p = G.gru_scan_forward_persistent(d["gi"], d["h0"], d["w"], d["bh"], h_in_quant=cfg["h_in_quant"],
+                                          h_out_quant=cfg["h_out_quant"])
     assert torch.equal(out_t, out_p)
     assert_quant_parity(cfg, dev, free_bound=2.0)
 
