@@ -90,8 +90,10 @@ def roofline(idx: int, kernel_ms: float) -> dict:
                 "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic}
     achieved = w["flops"] / (kernel_ms * 1e-3) / 1e12
     if w.get("int8"):
+        # also against the fp32 MFMA peak, the bound of the same products in fp32
         return {"bound": "mfma", "achieved": round(achieved, 4), "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",
-                "frac": round(achieved / INT8_MFMA_PEAK_TOPS, 6), "traffic": traffic}
+                "frac": round(achieved / INT8_MFMA_PEAK_TOPS, 6), "traffic": traffic,
+                "frac_of_fp32_mfma_peak": round(achieved / FP32_MFMA_PEAK_TFLOPS, 5)}
     return {"bound": "mfma", "achieved": round(achieved, 4), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 5), "traffic": traffic}
 

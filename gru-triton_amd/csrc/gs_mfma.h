@@ -1,8 +1,8 @@
 // Building blocks shared by the MFMA scan kernels (dense, single- and
 // two-factor Monarch): the 4x4x1 MFMA chains over a wave's quad of hidden
-// units, the 16-way K-slice reduction, weight-slice loads and LDS operand
-// reads, the workgroup barrier used between exchange stages, and host-side
-// device queries.
+// units (fp32, and int8 over int8 weight codes), the 16-way K-slice
+// reduction, weight-slice loads and LDS operand reads, the workgroup barrier
+// used between exchange stages, and host-side device queries.
 //
 // MFMA layout (v_mfma_f32_4x4x1_16b_f32, checked on the device): lane l
 // supplies A[block l/4][row l%4] and B[block l/4][col l%4]; D block b, row v,

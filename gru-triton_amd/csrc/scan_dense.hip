@@ -1,4 +1,5 @@
-// Dense and single-factor Monarch GRU scan forward on fp32 MFMA (gfx950).
+// Dense and single-factor Monarch GRU scan forward on fp32 MFMA (gfx950), and
+// the dense forward on int8 MFMA when Wh comes as per-row int8 codes (I8).
 //
 // References (LarocheC/gru-triton src/gru_qat/triton_kernels/):
 //   dense    scan.py:76-210 (persistent kernel), scan.py:213-293 (launcher)
