@@ -642,11 +642,15 @@ def weight_codes(w: torch.Tensor) -> Optional[Tuple[torch.Tensor, torch.Tensor]]
     reproduce the fake-quantized weight w [rows, cols] (fp32 on the GPU) element
     for element (``gs_weight_codes``), or None when a row is not such a product.
     Found once per version of w: the verdict costs one device-to-host read, and
-    a frozen weight is not written again (any in-place write bumps ``_version``)."""
+    a frozen weight is not written again (any in-place write bumps ``_version``).
+    Under HIP graph capture, where that read cannot happen, an uncached weight
+    gets None (the fp32 kernels); a call before the capture caches it."""
     key = (w.data_ptr(), w._version)
     hit = _CODES_CACHE.get(id(w))
     if hit is not None and hit[0]() is w and hit[1] == key:
         return hit[2]
+    if torch.cuda.is_current_stream_capturing():
+        return None
     lib = _lib if _lib is not None else load()
     rows, cols = w.shape
     src = w.contiguous()
