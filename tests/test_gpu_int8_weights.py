@@ -162,6 +162,23 @@ def test_tiled_int8_bit_identical_to_persistent(dev, shape, q_in, q_out):
     assert torch.equal(i8_t, a)
 
 
+@pytest.mark.parametrize("shape", [(1, 1, 80), (2, 3, 96), (5, 1, 112), (3, 5, 1040), (1, 33, 256),
+                                   (4, 7, 1056), (3, 2, 128)])
+def test_int8_edge_shapes(dev, shape):
+    """Odd batch tiles and row blocks, T = 1, H just past a KC step or past the
+    persistent limit: the two int8 forwards agree bit for bit (H <= 1024) and
+    meet the quant bar."""
+    import gru_qat_amd as G
+
+    cfg = _cfg(shape, Q_INT8_HIDDEN, Q_INT8_HIDDEN)
+    d = to_dev(cfg, dev)
+    kw = dict(h_in_quant=Q_INT8_HIDDEN, h_out_quant=Q_INT8_HIDDEN)
+    a = G.gru_scan_forward(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    b = G.gru_scan_forward_persistent(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    assert torch.equal(a, b)
+    assert_quant_parity(cfg, dev, free_bound=2.0)
+
+
 @pytest.mark.parametrize("shape,q_in,q_out", [
     ((16, 8, 512), None, Q_INT8_HIDDEN),   # q_in off: h0 is not a level
     ((8, 4, 64), Q_INT8_HIDDEN, Q_INT8_HIDDEN),  # one workgroup: no exchange
