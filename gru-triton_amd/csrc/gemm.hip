@@ -262,6 +262,97 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_kernel(GemmArgs g) {
     }
 }
 
+// ---- int8 NT product (gemm_i8_nt) -----------------------------------------------
+// A 64 x 64 tile of C per workgroup of 4 waves, each wave 2 x 2 tiles of
+// v_mfma_i32_16x16x64_i8; K advances by 64, double-buffered through LDS. Each
+// thread loads 16 consecutive k (16 bytes) of one row of each operand and
+// stores them with one 16-byte LDS write; a row holds 64 bytes in a stride of
+// 20 words, so the 16 rows that a 16-lane pass of the operand reads start on
+// distinct 4-bank groups (20 r mod 64) and the 16-byte reads are free of
+// conflicts. MFMA operand layout: lane l supplies the 16 bytes of row l % 16
+// at k-group l / 16 for A and for B alike, so whatever k the hardware assigns
+// a byte, A's and B's bytes at one position are the same k; D VGPR v of lane
+// l is C[4 (l / 16) + v][l % 16].
+constexpr int kI8Tile = 64, kI8BK = 64, kI8RowWords = 20;
+typedef int i4v __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kGemmThreads) void gemm_i8_nt_kernel(GemmI8Args g) {
+  __shared__ __attribute__((aligned(16))) int As[2][kI8Tile * kI8RowWords];
+  __shared__ __attribute__((aligned(16))) int Bs[2][kI8Tile * kI8RowWords];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wy = wave >> 1, wx = wave & 1;
+  const int i0 = blockIdx.x * kI8Tile, j0 = blockIdx.y * kI8Tile;
+  // loader: row lr of the tile, k = 16 lk .. 16 lk + 15 of the slice
+  const int lr = threadIdx.x >> 2, lk = threadIdx.x & 3;
+  const int ra = i0 + lr, rb = j0 + lr;
+  const bool oka = ra < g.M, okb = rb < g.N;
+  const int8_t* pa = g.a + (int64_t)(oka ? ra : 0) * g.lda + 16 * lk;
+  const int8_t* pb = g.b + (int64_t)(okb ? rb : 0) * g.ldb + 16 * lk;
+  i4v va, vb;
+  auto load = [&](int k0) {
+    const bool in = k0 + 16 * lk < g.K;  // K % 16 == 0: 16 bytes wholly inside or outside
+    va = (oka && in) ? *reinterpret_cast<const i4v*>(pa + k0) : i4v{0, 0, 0, 0};
+    vb = (okb && in) ? *reinterpret_cast<const i4v*>(pb + k0) : i4v{0, 0, 0, 0};
+  };
+  auto stage = [&](int buf) {
+    *reinterpret_cast<i4v*>(&As[buf][lr * kI8RowWords + 4 * lk]) = va;
+    *reinterpret_cast<i4v*>(&Bs[buf][lr * kI8RowWords + 4 * lk]) = vb;
+  };
+  i4v acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = i4v{0, 0, 0, 0};
+  const int r16 = lane & 15, kg = lane >> 4;
+  int buf = 0;
+  load(0);
+  stage(0);
+  __syncthreads();
+  for (int k0 = 0; k0 < g.K; k0 += kI8BK) {
+    const bool more = k0 + kI8BK < g.K;
+    if (more) load(k0 + kI8BK);
+    i4v a[2], b[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      a[t] = *reinterpret_cast<const i4v*>(&As[buf][(32 * wy + 16 * t + r16) * kI8RowWords + 4 * kg]);
+      b[t] = *reinterpret_cast<const i4v*>(&Bs[buf][(32 * wx + 16 * t + r16) * kI8RowWords + 4 * kg]);
+    }
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < 2; ++tj) acc[ti][tj] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[ti], b[tj], acc[ti][tj], 0, 0, 0);
+    if (more) stage(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+#pragma unroll
+  for (int tj = 0; tj < 2; ++tj) {
+    const int j = j0 + 32 * wx + 16 * tj + r16;
+    if (j >= g.N) continue;
+    const float sc = g.sa * g.b_scale[j];
+    const float bias = g.bias ? g.bias[j] : 0.0f;
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = i0 + 32 * wy + 16 * ti + 4 * kg + v;
+        if (i < g.M) g.c[(int64_t)i * g.ldc + j] = (float)acc[ti][tj][v] * sc + bias;
+      }
+  }
+}
+
+__global__ void quant_codes_kernel(float* dst_q, int8_t* codes, const float* src, int64_t ld, int rows, int cols,
+                                   Quant q) {
+  const int64_t n = (int64_t)rows * cols;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = e / cols;
+    const int i = (int)(e - m * cols);
+    const float lv = quant_level(src[m * ld + i], q);
+    if (dst_q != nullptr) dst_q[e] = lv * q.scale;
+    codes[e] = (int8_t)(int)lv;
+  }
+}
+
 __global__ void sum_partials_kernel(float* dst, const float* src, int64_t n, int parts, int64_t stride) {
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
     float s = src[e];
@@ -393,6 +484,31 @@ int gemm_f32(const GemmArgs& g, hipStream_t stream, const char* who) {
   const dim3 grid((unsigned)((g.M + BM - 1) / BM), (unsigned)((g.N + BN - 1) / BN),
                   (unsigned)(g.batch * g.ksplit));
   hipLaunchKernelGGL(fn, grid, dim3(kGemmThreads), 0, stream, g);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
+
+bool gemm_i8_applies(const GemmI8Args& g) {
+  return g.K >= 1 && g.K <= 65536 && g.K % 16 == 0 && g.lda % 16 == 0 && g.ldb % 16 == 0 && aligned16(g.a) &&
+         aligned16(g.b) && g.b_scale != nullptr;
+}
+
+int gemm_i8_nt(const GemmI8Args& g, hipStream_t stream, const char* who) {
+  if (g.M < 1 || g.N < 1 || !gemm_i8_applies(g))
+    return set_error(GS_ERR_INVALID, "%s: int8 GEMM operands out of its contract (M=%d, N=%d, K=%d)", who, g.M, g.N,
+                     g.K);
+  const dim3 grid((unsigned)((g.M + kI8Tile - 1) / kI8Tile), (unsigned)((g.N + kI8Tile - 1) / kI8Tile));
+  hipLaunchKernelGGL(gemm_i8_nt_kernel, grid, dim3(kGemmThreads), 0, stream, g);
+  GS_CHECK_HIP(hipGetLastError());
+  return GS_OK;
+}
+
+int quant_copy_codes(float* dst_q, int8_t* codes, const float* src, int64_t ld, int rows, int cols, const Quant& q,
+                     hipStream_t stream, const char* who) {
+  (void)who;
+  const int64_t n = (int64_t)rows * cols;
+  hipLaunchKernelGGL(quant_codes_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 8192)), dim3(256), 0,
+                     stream, dst_q, codes, src, ld, rows, cols, q);
   GS_CHECK_HIP(hipGetLastError());
   return GS_OK;
 }

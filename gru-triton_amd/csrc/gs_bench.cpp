@@ -480,6 +480,13 @@ int run_proj(int launches, int warmup) {
   p.sgi = N;
   p.q_x = gs_quant{1, 0.02f, -127, 127};
   p.q_w = gs_quant{1, 1.0f, -127, 127};
+  // int8 scratch: x's levels and the weight's codes (the int8 product)
+  int8_t* xc = nullptr;
+  int8_t* wc = nullptr;
+  CHECK(hipMalloc(&xc, (size_t)M * I));
+  CHECK(hipMalloc(&wc, (size_t)N * I));
+  p.x_codes = xc;
+  p.w_codes = wc;
   gs_proj_bwd_args q;
   memset(&q, 0, sizeof q);
   q.x = x;
@@ -518,6 +525,8 @@ int run_proj(int launches, int warmup) {
   report("input_projection", -1, time_launches(fwd, launches, warmup, st), 64, 32, 512);
   report("input_projection_backward", -1, time_launches(bwd, launches, warmup, st), 64, 32, 512);
   CHECK(hipFree(ws));
+  CHECK(hipFree(xc));
+  CHECK(hipFree(wc));
   for (float* o : owned) CHECK(hipFree(o));
   CHECK(hipStreamDestroy(st));
   return 0;

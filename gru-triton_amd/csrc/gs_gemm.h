@@ -37,6 +37,33 @@ struct GemmArgs {
 // Launches the product on `stream`. Every element of C (of every split) is written.
 int gemm_f32(const GemmArgs& g, hipStream_t stream, const char* who);
 
+// NT product of int8 operands on the int8 MFMA:
+//   C[i, j] = float(sum_k a[i lda + k] b[j ldb + k]) * (sa * b_scale[j]) (+ bias[j])
+// with a the levels of a per-tensor fake-quant of scale sa and b per-row codes
+// of scale b_scale[j] (int8, rows 16-byte aligned: K, lda and ldb multiples of
+// 16). The integer sums are exact (K <= 65536: no int32 overflow), so C is
+// within an fp32 rounding of each product of gemm_f32 on the fake-quantized
+// operands.
+struct GemmI8Args {
+  const int8_t* a = nullptr;
+  int64_t lda = 0;
+  float sa = 1.0f;
+  const int8_t* b = nullptr;
+  int64_t ldb = 0;
+  const float* b_scale = nullptr;
+  const float* bias = nullptr;
+  float* c = nullptr;
+  int64_t ldc = 0;
+  int M = 0, N = 0, K = 0;
+};
+bool gemm_i8_applies(const GemmI8Args& g);
+int gemm_i8_nt(const GemmI8Args& g, hipStream_t stream, const char* who);
+
+// dst_q[m][i] = fake_quant(src[m ld + i], q) (dst_q contiguous [rows, cols], or
+// NULL) and codes[m][i] its level (int8, contiguous), for q's range in a byte.
+int quant_copy_codes(float* dst_q, int8_t* codes, const float* src, int64_t ld, int rows, int cols, const Quant& q,
+                     hipStream_t stream, const char* who);
+
 // dst[e] = sum_{s < parts} src[s * stride + e] for e < n.
 int sum_partials(float* dst, const float* src, int64_t n, int parts, int64_t stride, hipStream_t stream,
                  const char* who);

@@ -150,10 +150,38 @@ extern "C" int gs_input_proj(const gs_proj_args* a, hipStream_t stream) {
     if (!(a->q_w.qmax > 0) || a->q_w.qmin > a->q_w.qmax)
       return set_error(GS_ERR_INVALID, "%s: weight quant needs qmax > 0 and qmin <= qmax; got [%d, %d]", who,
                        a->q_w.qmin, a->q_w.qmax);
+    // the codes too when the int8 product may run (int8 scratch given, byte range)
+    int8_t* codes = a->w_codes != nullptr && a->q_w.qmin >= -128 && a->q_w.qmax <= 127 ? a->w_codes : nullptr;
     hipLaunchKernelGGL(weight_quant_rows, dim3((unsigned)a->N), dim3(kRowThreads), 0, stream, a->w, (int)a->I,
-                       (float)a->q_w.qmin, (float)a->q_w.qmax, a->w_q, a->w_scale, nullptr);
+                       (float)a->q_w.qmin, (float)a->q_w.qmax, a->w_q, a->w_scale, codes);
     GS_CHECK_HIP(hipGetLastError());
     w = a->w_q;
+  }
+  // Both operands int8 (the int8 QAT layer: q_x and the per-row weight quant
+  // with byte ranges) and the int8 scratch given: the pre-passes write x's
+  // levels and the weight's codes, and the product runs on the int8 MFMA, exact
+  // integer sums scaled once (gemm_i8_nt).
+  const bool i8 = a->q_x.enabled && a->q_x.qmin >= -128 && a->q_x.qmax <= 127 && a->q_w.enabled &&
+                  a->q_w.qmin >= -128 && a->q_w.qmax <= 127 && a->x_codes != nullptr && a->w_codes != nullptr;
+  if (i8) {
+    GemmI8Args h;
+    h.a = a->x_codes;
+    h.lda = a->I;
+    h.sa = a->q_x.scale;
+    h.b = a->w_codes;
+    h.ldb = a->I;
+    h.b_scale = a->w_scale;
+    h.bias = a->bias;
+    h.c = a->gi;
+    h.ldc = a->sgi;
+    h.M = (int)a->M;
+    h.N = (int)a->N;
+    h.K = (int)a->I;
+    if (gemm_i8_applies(h)) {
+      rc = quant_copy_codes(a->x_q, a->x_codes, a->x, a->sx, (int)a->M, (int)a->I, to_quant(a->q_x), stream, who);
+      if (rc) return rc;
+      return gemm_i8_nt(h, stream, who);
+    }
   }
   GemmArgs g;
   g.a = a->x;

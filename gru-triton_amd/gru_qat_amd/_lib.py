@@ -167,6 +167,8 @@ class GsProjArgs(ctypes.Structure):
         ("sgi", ctypes.c_int64),
         ("q_x", GsQuant),
         ("q_w", GsQuant),
+        ("x_codes", ctypes.c_void_p),
+        ("w_codes", ctypes.c_void_p),
     ]
 
 

@@ -8,7 +8,9 @@ gate weight through its per-channel quantizer, quantizers.py:188-199) and
 ``gi = F.linear(xq, Wi_cat, bi_cat)``. Here the three steps are one call of
 ``gs_input_proj`` (libgruscan.so): the per-row weight fake-quant, then one
 fp32 MFMA GEMM that fake-quantizes x as it loads it and adds the bias in its
-epilogue. The backward (``gs_input_proj_bwd``) follows torch's autograd of
+epilogue; with both quantizers int8 (the QAT layer) the product runs instead on
+the int8 MFMA over x's levels and the weight's codes (exact integer sums, within
+an fp32 rounding of each product of the fp32 GEMM). The backward (``gs_input_proj_bwd``) follows torch's autograd of
 fake_quant_ste (ste.py:65-95): straight through the rounding, clipped at the
 clamp, x's frozen scale constant, and the per-row weight scales (computed from
 the weight, not detached, in the reference's dynamic weight quantizer)
@@ -65,9 +67,16 @@ def _project(x2: torch.Tensor, Wi_cat: torch.Tensor, bi_cat: Optional[torch.Tens
         a.q_w = _lib.GsQuant(1, 1.0, int(w_quant[0]), int(w_quant[1]))
     else:
         a.q_w = _lib.make_quant(None, "w_quant")
+    codes = None
+    if (x_quant is not None and w_quant is not None and I % 16 == 0 and int(x_quant[1]) >= -128
+            and int(x_quant[2]) <= 127 and w_quant[0] >= -128 and w_quant[1] <= 127):
+        # int8 scratch for x's levels and the weight's codes: the product then runs on the int8 MFMA
+        codes = torch.empty((M + N) * I, device=x2.device, dtype=torch.int8)
+        a.x_codes, a.w_codes = codes.data_ptr(), codes.data_ptr() + M * I
     with _lib.on_device(x2.device):
         rc = lib.gs_input_proj(ctypes.byref(a), ctypes.c_void_p(_lib.current_stream_handle(x2.device)))
     _lib.raise_for(rc, lib)
+    del codes  # the caching allocator keeps it until the stream's work is done
     return gi, w_used, scales, xq
 
 

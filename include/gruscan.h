@@ -307,7 +307,13 @@ int64_t gs_bwd_scratch_bytes(int kind, const gs_bwd_args* args);
  * symmetric fake-quant of w (FakeQuantizePerChannel, quantizers.py:188-199:
  * scale[n] = max(max_i |w[n][i]|, 1e-8) / qmax, quantizers.py:124-134), or w
  * itself when q_w is off. One fp32 MFMA GEMM with the x fake-quant applied as
- * the operand is loaded and the bias added in its epilogue.
+ * the operand is loaded and the bias added in its epilogue. When both quants are
+ * on with ranges in a byte (the int8 QAT layer), I is a multiple of 16 up to 65536
+ * and the caller passes the int8 scratch x_codes and w_codes (16-byte aligned), the
+ * pre-passes write q_x's levels and the weight's codes there and the product runs on
+ * the int8 MFMA instead: exact integer sums, gi = sum * (q_x scale * scale[n]) +
+ * bias[n], within an fp32 rounding of each product of the fp32 GEMM. No
+ * counterpart in the reference for the two scratch fields (ABI version 5).
  */
 typedef struct gs_proj_args {
   const float* x;     /* [M, I] rows (M = T B), row stride sx                        */
@@ -322,6 +328,8 @@ typedef struct gs_proj_args {
   int64_t sx, sgi;
   gs_quant q_x;       /* per-tensor fake-quant of x                                  */
   gs_quant q_w;       /* per-row weight fake-quant: enabled, qmin, qmax (scale unused) */
+  int8_t* x_codes;    /* [M, I] int8 scratch for q_x's levels, or NULL (see above)    */
+  int8_t* w_codes;    /* [N, I] int8 scratch for the weight's codes, or NULL          */
 } gs_proj_args;
 
 int gs_input_proj(const gs_proj_args* args, hipStream_t stream);

@@ -1,6 +1,7 @@
 """The input projection (gs_input_proj / gs_input_proj_bwd) against the
 oracle's restatement of the reference's gi producer (gru_layer.py:249-255):
-forward within 1e-4 x max(1, |gi|) (fp32 sums over I), the per-row weight
+forward within 1e-4 x max(1, |gi|) (fp32 sums over I, or exact int8 sums
+when both quantizers are int8 and I is a multiple of 16), the per-row weight
 codes and scales bit-exact, and the straight-through gradients within
 1e-4 x max(1, |ref|)."""
 
@@ -21,6 +22,10 @@ CASES = [
     # asymmetric per-row weight range (scale max|w| / qmax): weights below -100 s clip, and the
     # clipped-STE mask zeroes their gradient and their part of the scale's gradient
     ((3, 5), 64, 24, (0.05, -127, 127), (-100, 127), True),
+    # int8 x and weight with I a multiple of 16: the product on the int8 MFMA (exact integer sums),
+    # at tile tails (M = 5 and 18 rows, N = 7 and 100 columns) and the full int8 level range
+    ((2, 9), 1024, 100, (0.03, -128, 127), (-127, 127), True),
+    ((5,), 48, 7, (0.05, -127, 127), (-100, 127), False),
 ]
 
 
