@@ -123,28 +123,81 @@ __global__ __launch_bounds__(kGenericThreads) void butterfly_generic_kernel(BPar
 // Each lane keeps the two twiddles of each of its 4 elements for all L stages
 // in registers (8L values), loaded
 // once. The gate epilogue for element i runs on one of the three gate waves
-// that hold i (see owns() below), which reads the other gates' gh from LDS and
-// broadcasts the next q_in(h) back.
+// that hold i (see owns() below), or at N = 1024 for r = 1 on a fourth wave of
+// the SIMD (EW), which reads the other gates' gh from LDS and broadcasts the
+// next q_in(h) back.
 // ---------------------------------------------------------------------------------
+// EW (N = 1024): a fourth wave per SIMD, with no butterfly of its own, runs
+// the gate epilogue of element r = 1 of its lanes, so every wave of a SIMD
+// runs one epilogue chain per step.
 template <int LOGN>
-__global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BParams p) {
+constexpr bool bfly_ew() { return LOGN == 10; }
+template <int LOGN>
+constexpr int bfly_threads() { return bfly_ew<LOGN>() ? 4 * (1 << LOGN) / 4 : 3 * (1 << LOGN) / 4; }
+
+template <int LOGN>
+__global__ __launch_bounds__(bfly_threads<LOGN>()) void butterfly_reg_kernel(BParams p) {
   constexpr int N = 1 << LOGN;
   constexpr int L = LOGN;
   constexpr int WPG = N / 256;
+  constexpr bool EW = bfly_ew<LOGN>();
   __shared__ float xch[2][3][N];
   __shared__ float ghs[3][N];
   __shared__ float hqs[N];
 
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  const int g = wv / WPG;
-  const int w = wv - g * WPG;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool ewave = EW && wv >= 3 * WPG;
+  const int g = ewave ? 3 : wv / WPG;
+  const int w = ewave ? wv - 3 * WPG : wv - g * WPG;
   const int b = blockIdx.x;
   const int H = p.H;
 
   int idx[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) idx[r] = lane + 64 * r + 256 * w;
+
+  if constexpr (EW) {
+    if (ewave) {
+      // element r = 1 of the lane: the three barriers of each gate-wave step
+      // (layers 8-9, gather, h), with the epilogue between the second and third
+      const int i = idx[1];
+      const bool in = i < H;
+      float hr = in ? p.h0[(int64_t)b * p.sh0_b + i] : 0.0f;
+      float bs[3];
+#pragma unroll
+      for (int q = 0; q < 3; ++q) bs[q] = in ? gate_scale(q) * p.bh[q * H + i] : 0.0f;
+      const float* gp0 = p.gi + (int64_t)b * p.sg_b + min(i, H - 1);
+      float ga[3], gb[3];
+      auto load = [&](int t, float (&gv)[3]) {
+        const int tc = t < p.T ? t : p.T - 1;
+#pragma unroll
+        for (int q = 0; q < 3; ++q) gv[q] = gp0[(int64_t)tc * p.sg_t + q * H];
+      };
+      auto estep = [&](int t, float (&gv)[3]) {
+        lds_barrier();  // layers 8-9
+        lds_barrier();  // gather
+        float hn = gru_update_gb(gv[0], gv[1], gv[2], ghs[0][i], ghs[1][i], ghs[2][i], bs[0], bs[1], bs[2], hr);
+        if (p.qout.on) hn = fake_quant(hn, p.qout);
+        float hq = 0.0f;
+        if (in) {
+          p.out[(int64_t)t * p.so_t + (int64_t)b * p.so_b + i] = hn;
+          hr = hn;
+          hq = (p.qin.on && p.qin_after_first) ? fake_quant(hn, p.qin) : hn;
+        }
+        hqs[i] = hq;
+        lds_barrier();  // h
+        load(t + 2, gv);
+      };
+      load(0, ga);
+      load(1, gb);
+      for (int t = 0; t < p.T; t += 2) {
+        estep(t, ga);
+        if (t + 1 < p.T) estep(t + 1, gb);
+      }
+      return;
+    }
+  }
 
   auto twiddles = [&](int i, int s, float& self, float& partner) {
     const int m = (i >> s) & 1;
@@ -180,13 +233,14 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void butterfly_reg_kernel(BPar
   }
 
   // The gate epilogue of element r of a lane runs on one of the three gate
-  // waves that hold it (they share a SIMD): r = 0, 1 on the r-gate wave, r = 2
-  // on the z-gate wave, r = 3 on the n-gate wave, so the three waves' epilogue
-  // chains interleave instead of one wave running all four. A wave's owned
-  // elements are its slots: slot 0 is element r0, slot 1 (r-gate wave only)
-  // element 1; the raw h, biases and gate inputs are kept per slot.
-  auto owns = [&](int r) { return r < 2 ? g == 0 : g == r - 1; };
-  const int nslot = g == 0 ? 2 : 1;
+  // waves that hold it (they share a SIMD): r = 0, 1 on the r-gate wave (r = 1
+  // on the epilogue wave with EW), r = 2 on the z-gate wave, r = 3 on the
+  // n-gate wave, so the waves' epilogue chains interleave instead of one wave
+  // running all four. A wave's owned elements are its slots: slot 0 is element
+  // r0, slot 1 (r-gate wave only, without EW) element 1; the raw h, biases and
+  // gate inputs are kept per slot.
+  auto owns = [&](int r) { return r < 2 ? (EW ? r == 0 && g == 0 : g == 0) : g == r - 1; };
+  const int nslot = (!EW && g == 0) ? 2 : 1;
   const int r0 = g == 0 ? 0 : g + 1;
   const int ie[2] = {idx[r0], idx[1]};
   float x[4], hraw[2], bias[3][2];
@@ -352,7 +406,7 @@ extern "C" int gs_butterfly_fwd(const gs_args* a, hipStream_t stream) {
 
   const dim3 grid((unsigned)a->B);
   if (p.nchains == 1 && p.logn == 10) {
-    hipLaunchKernelGGL(butterfly_reg_kernel<10>, grid, dim3(768), 0, stream, p);
+    hipLaunchKernelGGL(butterfly_reg_kernel<10>, grid, dim3(bfly_threads<10>()), 0, stream, p);
   } else if (p.nchains == 1 && p.logn == 9) {
     hipLaunchKernelGGL(butterfly_reg_kernel<9>, grid, dim3(384), 0, stream, p);
   } else if (p.nchains == 1 && p.logn == 8) {
