@@ -71,14 +71,14 @@ def _dense_forward(who: str, gi: torch.Tensor, h0: torch.Tensor, Wh_cat: torch.T
         raise ValueError(f"Wh_cat shape must be (3H, H)=({3 * H}, {H}); got {tuple(Wh_cat.shape)}")
     h_in_quant = check_quant(h_in_quant, "h_in_quant")
     h_out_quant = check_quant(h_out_quant, "h_out_quant")
+    codes = None
+    if int8_codes and gh_save is None and _int8_codes_apply(H, h_in_quant):
+        codes = _lib.weight_codes(Wh_cat)  # keyed on the caller's tensor, contiguous or not
     gi = gi.contiguous()
     h0 = h0.contiguous()
     Wh_cat = Wh_cat.contiguous()
     bh_cat = bh_cat.contiguous()
     out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
-    codes = None
-    if int8_codes and gh_save is None and _int8_codes_apply(H, h_in_quant):
-        codes = _lib.weight_codes(Wh_cat)
     if tiled and codes is not None:
         _lib.launch(_lib.KIND_DENSE_TILED, "gs_dense_fwd_tiled_i8w", gi=gi, h0=h0, w=Wh_cat, w2=None, bh=bh_cat,
                     out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, contiguous=True, w_codes=codes)
