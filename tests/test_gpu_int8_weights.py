@@ -236,3 +236,20 @@ def test_entry_point_through_the_c_abi(dev, name):
     assert rc == _lib.GS_ERR_INVALID and b"w_codes" in lib.gs_last_error()
     rc, _, _ = _entry(dev, cfg, codes.data_ptr() + 4, scale.data_ptr(), name)
     assert rc == _lib.GS_ERR_INVALID and b"aligned" in lib.gs_last_error()
+
+
+def test_non_contiguous_weight(dev):
+    """A non-contiguous Wh_cat (same values) finds the same codes, cached on the
+    caller's tensor, and gives the contiguous weight's outputs bit for bit."""
+    import gru_qat_amd as G
+
+    cfg = make_config(2, shape=(8, 4, 256))
+    d = to_dev(cfg, dev)
+    w_nc = d["w"].t().contiguous().t()
+    assert not w_nc.is_contiguous()
+    kw = dict(h_in_quant=cfg["h_in_quant"], h_out_quant=cfg["h_out_quant"])
+    a = G.gru_scan_forward_persistent(d["gi"], d["h0"], d["w"], d["bh"], **kw)
+    b = G.gru_scan_forward_persistent(d["gi"], d["h0"], w_nc, d["bh"], **kw)
+    assert torch.equal(a, b)
+    first = _codes(w_nc)
+    assert first is not None and _codes(w_nc) is first
