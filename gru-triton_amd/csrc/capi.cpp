@@ -133,6 +133,7 @@ int check_scratch(const gs_bwd_args* a, int64_t need, const char* who) {
 // Defined in the kernel translation units.
 namespace gs {
 int64_t dense_workspace_bytes(const gs_args* a);
+int64_t circulant_workspace_bytes(const gs_args* a);
 int64_t monarch_workspace_bytes(const gs_args* a);
 int64_t dense_bwd_workspace_bytes(const gs_bwd_args* a, bool tiled);
 int64_t dense_bwd_scratch_bytes(const gs_bwd_args* a, bool tiled);
@@ -155,6 +156,8 @@ int64_t gs_workspace_bytes(int kind, const gs_args* a) {
       return 0;
     case GS_KIND_MONARCH:
       return gs::monarch_workspace_bytes(a);
+    case GS_KIND_CIRCULANT:
+      return gs::circulant_workspace_bytes(a);
     case GS_KIND_DIAGONAL:
     case GS_KIND_BUTTERFLY:
       return gs::kCtrlBytes;

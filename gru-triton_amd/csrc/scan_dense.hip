@@ -35,7 +35,30 @@
 namespace gs {
 namespace {
 
-enum : int { kDense = 0, kMonarch1 = 1 };
+// kCirculant: the dense scan of a circulant map, Wh_cat[g H + o][k] =
+// col_g[(o - k) mod H], each compute wave forming its weight slice from the
+// gate columns (Wh_circ [3, H]) instead of loading a materialized map: the
+// same weights, so the same products as kDense on that map.
+enum : int { kDense = 0, kMonarch1 = 1, kCirculant = 2 };
+
+// The weight slice of a quad from circulant columns: as load_w on the
+// materialized map, wr[g][m] = col[g H + (o - k) mod H] for o = o0 + j,
+// k = kmap(m, kb4); zero where o >= H or k >= H.
+template <int KC>
+__device__ __forceinline__ void load_w_circ(const float* col, int H, int o0, int j, int kb4, bool ok_quad,
+                                            float (&wr)[3][KC]) {
+  const int o = o0 + j;
+  const bool ok = ok_quad && o < H;
+#pragma unroll
+  for (int g = 0; g < 3; ++g) {
+#pragma unroll
+    for (int m = 0; m < KC; ++m) {
+      const int k = kmap(m, kb4);
+      const int d = o - k;
+      wr[g][m] = (ok && k < H) ? col[g * H + (d < 0 ? d + H : d)] : 0.0f;
+    }
+  }
+}
 // Remote mode: poller waves per batch row. Two for KC = 16 and 32, each
 // polling half of the row (measured 2 % faster than one at config 1: fewer
 // words per lane shorten a poll round); one for KC <= 8, whose workgroups
@@ -119,7 +142,7 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   // consecutive units: row strides that are not multiples of 16 floats put
   // the four rows on different banks of each 32-lane pass. Dense remote mode
   // has U = 4 nwc fixed by KC (16 or 48), so its strides are constants.
-  constexpr int UD = (KIND == kDense && REMOTE) ? dense_remote_units(KC) : 0;
+  constexpr int UD = ((KIND == kDense || KIND == kCirculant) && REMOTE) ? dense_remote_units(KC) : 0;
   const int KR = UD ? row_stride_pad(UD) : p.kr, GR = UD ? row_stride_pad(3 * UD) : p.gr;
   float* hk = hst + 2 * p.hsz;       // [RB][4][KR]  raw h of this workgroup's units
   float* gst = hk + p.RB * 4 * KR;   // [2][4][GR]   staged gi, [3][U] per row (remote mode)
@@ -133,6 +156,8 @@ __global__ __launch_bounds__(NT) void scan_kernel(DParams p) {
   if (!poller) {
     if constexpr (I8)
       load_wi<KC>(p.wq, p.H, o0, j, kb4, quad_ok, wi);
+    else if constexpr (KIND == kCirculant)
+      load_w_circ<KC>(p.w, p.H, o0, j, kb4, quad_ok, wr);
     else
       load_w<KC>(p.w, p.nb, p.bs, blk_g, o0, j, kb4, quad_ok, wr);
   }
@@ -436,6 +461,10 @@ DFn pick(int kind, bool remote, int KC, int* nt, bool pack = false, bool save = 
     if (remote && pack) return pick_kernel<kDense, true, true, true>(KC, nt);
     return remote ? pick_kernel<kDense, true, false, true>(KC, nt) : pick_kernel<kDense, false, false, true>(KC, nt);
   }
+  if (kind == kCirculant) {
+    if (remote && pack) return pick_kernel<kCirculant, true, true>(KC, nt);
+    return remote ? pick_kernel<kCirculant, true>(KC, nt) : pick_kernel<kCirculant, false>(KC, nt);
+  }
   if (kind == kDense && remote && pack) return pick_kernel<kDense, true, true>(KC, nt);
   if (kind == kDense) return remote ? pick_kernel<kDense, true>(KC, nt) : pick_kernel<kDense, false>(KC, nt);
   return remote ? pick_kernel<kMonarch1, true>(KC, nt) : pick_kernel<kMonarch1, false>(KC, nt);
@@ -450,7 +479,7 @@ struct DPlan {
 };
 
 int plan_dense(int kind, const gs_args* a, DPlan* pl, const char* who) {
-  if (kind == kDense) {
+  if (kind == kDense || kind == kCirculant) {
     pl->nb = 1;
     pl->bs = (int)a->H;
   } else {
@@ -479,14 +508,15 @@ int plan_dense(int kind, const gs_args* a, DPlan* pl, const char* who) {
   // Packed exchange when the published value is a fake-quant level in
   // [-128, 127] (q_in after q_out, or q_out when q_in repeats it or is off).
   const gs_quant& qp = (a->q_in.enabled && !same_quant(a->q_in, a->q_out)) ? a->q_in : a->q_out;
-  pl->pack = kind == kDense && pl->remote && a->H % 4 == 0 && qp.enabled && qp.qmin >= -128 && qp.qmax <= 127;
+  pl->pack = (kind == kDense || kind == kCirculant) && pl->remote && a->H % 4 == 0 && qp.enabled &&
+             qp.qmin >= -128 && qp.qmax <= 127;
   pl->pscale = pl->pack ? qp.scale : 1.0f;
   pick(kind, pl->remote, pl->KC, &pl->nt, pl->pack);
   pl->nrb = (int)((a->B + 3) / 4);
   pl->Bp = 4 * pl->nrb;
   pl->hsz = 64 * pl->KC;
   const int U = 4 * pl->nwc;
-  if (kind == kDense && pl->remote && U != dense_remote_units(pl->KC))
+  if ((kind == kDense || kind == kCirculant) && pl->remote && U != dense_remote_units(pl->KC))
     return set_error(GS_ERR_INVALID, "%s: dense remote plan has %d units per workgroup, kernel assumes %d", who, U,
                      dense_remote_units(pl->KC));
   pl->kr = row_stride_pad(U);
@@ -590,6 +620,8 @@ int64_t ws_bytes(int kind, const gs_args* a) {
 
 int64_t dense_workspace_bytes(const gs_args* a) { return ws_bytes(kDense, a); }
 
+int64_t circulant_workspace_bytes(const gs_args* a) { return ws_bytes(kCirculant, a); }
+
 int64_t monarch_workspace_bytes(const gs_args* a) {
   if (a->w2) return monarch2_workspace_bytes(a);
   return monarch1_local_ok(a) ? kCtrlBytes : ws_bytes(kMonarch1, a);
@@ -617,6 +649,19 @@ extern "C" int gs_dense_fwd_i8w(const gs_args* a, const int8_t* w_codes, const f
   if (rc) return rc;
   if (gs::dense_uses_tiled(a)) return gs::run_tiled_fwd(a, stream, who, w_codes, w_scale);
   return gs::run(gs::kDense, a, stream, who, w_codes, w_scale);
+}
+
+extern "C" int gs_circulant_fwd(const gs_args* a, hipStream_t stream) {
+  gs::clear_error();
+  const char* who = "gs_circulant_fwd";
+  int rc = gs::validate_common(a, who);
+  if (rc) return rc;
+  if (a->w2 != nullptr) return gs::set_error(GS_ERR_INVALID, "%s: w2 must be NULL for the circulant kind", who);
+  if (gs::dense_uses_tiled(a))
+    return gs::set_error(GS_ERR_INVALID,
+                         "%s: H=%lld exceeds 1024; run gs_dense_fwd on the map gs_hidden_map_dense writes", who,
+                         (long long)a->H);
+  return gs::run(gs::kCirculant, a, stream, who);
 }
 
 extern "C" int gs_monarch_fwd(const gs_args* a, hipStream_t stream) {

@@ -41,6 +41,7 @@ EXPORTS = (
     "gs_dense_fwd_noalloc",
     "gs_diagonal_fwd",
     "gs_monarch_fwd",
+    "gs_circulant_fwd",
     "gs_butterfly_fwd",
     "gs_butterfly_fwd_generic",
     "gs_diagonal_bwd",
@@ -614,7 +615,7 @@ def _check_gh(name: str, gh: torch.Tensor, gi: torch.Tensor) -> None:
 # building a ctypes Structure field by field cost the host about 4 us a call.
 GS_ARGS = struct.Struct("<9Q12q" "ifii" "ifii" "Q")
 _QOFF = (0, 1.0, -(2**31), 2**31 - 1)
-_TAGGED = (KIND_DENSE, KIND_MONARCH)
+_TAGGED = (KIND_DENSE, KIND_MONARCH, KIND_CIRCULANT)
 _RAW_FN: dict = {}
 _NEED: dict = {}  # workspace bytes per (kind, sizes, quant) of the tagged kinds
 

@@ -21,6 +21,7 @@ from typing import Any, Tuple, cast
 
 import torch
 
+from . import _lib
 from ._common import QuantTuple, check_common, check_quant, require_cuda, require_f32
 from .observe import hidden_map_dense, hidden_map_grad
 from .scan import gru_scan_backward_persistent, gru_scan_forward_persistent
@@ -51,8 +52,19 @@ def _check(who: str, gi, h0, Wh_circ, bh_cat) -> int:
 
 def gru_scan_circulant_forward(gi, h0, Wh_circ, bh_cat, *, h_in_quant: QuantTuple = None,
                                h_out_quant: QuantTuple = None) -> torch.Tensor:
-    """Forward only; returns out [T, B, H]."""
+    """Forward only; returns out [T, B, H]. Up to H = 1024 the persistent kernel forms the
+    circulant rows itself from Wh_circ (``gs_circulant_fwd``); above, the dense scan runs on
+    the materialized map. Either way the outputs equal the dense scan's on that map."""
     H = _check("gru_scan_circulant_forward", gi, h0, Wh_circ, bh_cat)
+    if H <= 1024:
+        h_in_quant = check_quant(h_in_quant, "h_in_quant")
+        h_out_quant = check_quant(h_out_quant, "h_out_quant")
+        T, B = gi.shape[0], gi.shape[1]
+        gi, h0, bh_cat = gi.contiguous(), h0.contiguous(), bh_cat.contiguous()
+        out = torch.empty((T, B, H), device=gi.device, dtype=gi.dtype)
+        _lib.launch(_lib.KIND_CIRCULANT, "gs_circulant_fwd", gi=gi, h0=h0, w=Wh_circ.contiguous(), w2=None,
+                    bh=bh_cat, out=out, h_in_quant=h_in_quant, h_out_quant=h_out_quant, contiguous=True)
+        return out
     M = hidden_map_dense("circulant", Wh_circ.contiguous(), H)
     return gru_scan_forward_persistent(gi, h0, M, bh_cat, h_in_quant=h_in_quant, h_out_quant=h_out_quant)
 

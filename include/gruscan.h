@@ -77,8 +77,10 @@ extern "C" {
  * y = irfft(rfft(col) * rfft(x)), i.e. y[i] = sum_j col[(i - j) mod H] x[j]): w is Wh_circ
  * [3, H], each gate's first column col. The reference runs this kind on its per-step loop
  * (gru_layer.py:109-113); here it is the dense scan on the circulant matrices:
- * gs_hidden_map_dense(GS_KIND_CIRCULANT) writes them, gs_dense_fwd / gs_dense_bwd run the
- * scan, and gs_hidden_map_grad folds the dense weight gradient back onto col. */
+ * gs_circulant_fwd (H <= 1024) forms them from col inside the persistent kernel; above
+ * that, and for the backward, gs_hidden_map_dense(GS_KIND_CIRCULANT) writes them,
+ * gs_dense_fwd / gs_dense_bwd run the scan, and gs_hidden_map_grad folds the dense
+ * weight gradient back onto col. */
 #define GS_KIND_CIRCULANT 4
 /* Size queries only (gs_workspace_bytes, gs_bwd_workspace_bytes, gs_bwd_scratch_bytes): the
  * batch-tiled dense entry points gs_dense_fwd_tiled / gs_dense_bwd_tiled. */
@@ -168,6 +170,15 @@ int gs_dense_fwd_tiled_i8w(const gs_args* args, const int8_t* w_codes, const flo
 
 int gs_diagonal_fwd(const gs_args* args, hipStream_t stream);
 int gs_monarch_fwd(const gs_args* args, hipStream_t stream);
+
+/* Circulant forward (GS_KIND_CIRCULANT; the reference's _CirculantLinear hidden map,
+ * structure.py:220-240, which it scans on its per-step loop, gru_layer.py:109-113): w is
+ * Wh_circ [3, H]. The persistent dense kernel with each compute wave forming its rows of
+ * the circulant map from col, so its outputs equal gs_dense_fwd's on the map
+ * gs_hidden_map_dense writes, bit for bit, without that map in memory. H <= 1024 (above,
+ * run gs_dense_fwd on the written map); a workspace of gs_workspace_bytes(GS_KIND_CIRCULANT)
+ * bytes; gh_save must be NULL. */
+int gs_circulant_fwd(const gs_args* args, hipStream_t stream);
 int gs_butterfly_fwd(const gs_args* args, hipStream_t stream);
 
 /* Dense forward that allocates nothing and takes no workspace. No counterpart

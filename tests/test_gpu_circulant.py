@@ -37,6 +37,31 @@ def test_circulant_map_and_fold(dev, H):
         assert torch.allclose(dcol, ref, atol=1e-5)
 
 
+@pytest.mark.parametrize("shape", [(8, 4, 64), (5, 3, 7), (1, 1, 1), (9, 5, 100), (4, 33, 256), (3, 2, 1024),
+                                   (64, 32, 512)])
+@pytest.mark.parametrize("q", [None, Q_INT8_HIDDEN, "in_only", (0.02, -500, 500)])
+def test_circulant_kernel_equals_dense_on_the_map(dev, shape, q):
+    """gs_circulant_fwd forms each wave's rows of the circulant map from the
+    columns: the same weights in the same products as the dense scan on the
+    map gs_hidden_map_dense writes, so the outputs are equal bit for bit (local
+    and remote modes, fp32 and packed int8 exchange, 8-byte words for levels
+    wider than a byte)."""
+    from gru_qat_amd.scan import gru_scan_forward_persistent
+    from gru_qat_amd.scan_circulant import gru_scan_circulant_forward
+
+    T, B, H = shape
+    g = torch.Generator().manual_seed(H + B)
+    gi = (torch.randn(T, B, 3 * H, generator=g)).to(dev)
+    h0 = (torch.randn(B, H, generator=g) * 0.3).to(dev)
+    col = (torch.randn(3, H, generator=g) / H ** 0.5).to(dev)
+    bh = (torch.randn(3 * H, generator=g) * 0.1).to(dev)
+    qi, qo = (q, q) if q != "in_only" else (Q_INT8_HIDDEN, None)
+    a = gru_scan_circulant_forward(gi, h0, col, bh, h_in_quant=qi, h_out_quant=qo)
+    b = gru_scan_forward_persistent(gi, h0, hidden_map_dense("circulant", col, H), bh, h_in_quant=qi,
+                                    h_out_quant=qo)
+    assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("shape", [(8, 4, 64), (5, 3, 7), (1, 1, 1), (9, 5, 100), (4, 33, 256), (3, 2, 1024)])
 def test_circulant_fp32(dev, shape):
     assert_fp32_parity(small_cfg(6, shape), dev)
