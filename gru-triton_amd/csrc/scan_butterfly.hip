@@ -141,7 +141,7 @@ __global__ __launch_bounds__(bfly_threads<LOGN>()) void butterfly_reg_kernel(BPa
   constexpr int L = LOGN;
   constexpr int WPG = N / 256;
   constexpr bool EW = bfly_ew<LOGN>();
-  __shared__ float xch[2][3][N];
+  __shared__ __attribute__((aligned(16))) float xch[2][3][N];
   __shared__ float ghs[3][N];
   __shared__ float hqs[N];
 
@@ -297,15 +297,17 @@ __global__ __launch_bounds__(bfly_threads<LOGN>()) void butterfly_reg_kernel(BPa
         for (int r = 0; r < 4; ++r) y[r] = x[r ^ (1 << (s - 6))];
       } else if constexpr (L == 10) {
         if constexpr (s == 8) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) xch[0][g][idx[r]] = x[r];
+          // lane-major exchange: a lane's four elements r of wave w sit at
+          // [w][lane][r], so its partners at i ^ 256, i ^ 512, i ^ 768 (the
+          // same lane and r of waves w ^ 1, w ^ 2, w ^ 3) are three 16-byte reads
+          typedef float f4l __attribute__((ext_vector_type(4)));
+          *reinterpret_cast<f4l*>(&xch[0][g][256 * w + 4 * lane]) = f4l{x[0], x[1], x[2], x[3]};
           lds_barrier();
+          const f4l p1 = *reinterpret_cast<const f4l*>(&xch[0][g][256 * (w ^ 1) + 4 * lane]);
+          const f4l p2 = *reinterpret_cast<const f4l*>(&xch[0][g][256 * (w ^ 2) + 4 * lane]);
+          const f4l p3 = *reinterpret_cast<const f4l*>(&xch[0][g][256 * (w ^ 3) + 4 * lane]);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float* xs = xch[0][g];
-            const int i = idx[r];
-            x[r] = c8[0][r] * x[r] + c8[1][r] * xs[i ^ 256] + c8[2][r] * xs[i ^ 512] + c8[3][r] * xs[i ^ 768];
-          }
+          for (int r = 0; r < 4; ++r) x[r] = c8[0][r] * x[r] + c8[1][r] * p1[r] + c8[2][r] * p2[r] + c8[3][r] * p3[r];
         }
         return;  // stage 9 is folded into stage 8
       } else {
