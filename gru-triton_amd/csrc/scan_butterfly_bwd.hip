@@ -76,11 +76,15 @@ __device__ __forceinline__ void partner_of(const float (&x)[4], float (&y)[4], f
 #pragma unroll
     for (int r = 0; r < 4; ++r) y[r] = x[r ^ (1 << (S - 6))];
   } else {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) xch[idx[r]] = x[r];
+    // lane-major exchange buffer: element r of lane l of wave w at 256 w + 4 l + r,
+    // so a lane writes its four elements and reads its partners' (the same lane and
+    // r of wave w ^ 2^(S-8)) with one 16-byte access each
+    const int w = idx[0] >> 8, l = idx[0] & 63;
+    *reinterpret_cast<f4*>(xch + 256 * w + 4 * l) = f4{x[0], x[1], x[2], x[3]};
     lds_barrier();
+    const f4 v = *reinterpret_cast<const f4*>(xch + 256 * (w ^ (1 << (S - 8))) + 4 * l);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) y[r] = xch[idx[r] ^ (1 << S)];
+    for (int r = 0; r < 4; ++r) y[r] = v[r];
   }
 }
 
@@ -133,7 +137,7 @@ struct CoefParams {
 template <int LOGN>
 __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParams p) {
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
-  __shared__ float xch[2][3][N];
+  __shared__ __attribute__((aligned(16))) float xch[2][3][N];
   __shared__ float ghs[2][3][N];
   __shared__ float stg[2][7][N];  // a vector's seven output rows, element order (two vectors in turn)
   // the wave index read into a scalar register, so that per-gate choices are scalar
@@ -253,15 +257,17 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_apply_coef(CoefParam
       constexpr int s = S;
       if constexpr (L == 10 && s >= 8) {
         if constexpr (s == 8) {
+          // lane-major (partner_of): the partners at i ^ 256, ^ 512, ^ 768 are the
+          // same lane and r of waves w ^ 1, ^ 2, ^ 3
           float* xs = xch[0][g];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) xs[idx[r]] = x[r];
+          const int w = idx[0] >> 8, l = idx[0] & 63;
+          *reinterpret_cast<f4*>(xs + 256 * w + 4 * l) = f4{x[0], x[1], x[2], x[3]};
           lds_barrier();
+          const f4 p1 = *reinterpret_cast<const f4*>(xs + 256 * (w ^ 1) + 4 * l);
+          const f4 p2 = *reinterpret_cast<const f4*>(xs + 256 * (w ^ 2) + 4 * l);
+          const f4 p3 = *reinterpret_cast<const f4*>(xs + 256 * (w ^ 3) + 4 * l);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = idx[r];
-            x[r] = c8[0][r] * x[r] + c8[1][r] * xs[i ^ 256] + c8[2][r] * xs[i ^ 512] + c8[3][r] * xs[i ^ 768];
-          }
+          for (int r = 0; r < 4; ++r) x[r] = c8[0][r] * x[r] + c8[1][r] * p1[r] + c8[2][r] * p2[r] + c8[3][r] * p3[r];
         }
         return;  // layer 9 is folded into layer 8's exchange
       }
@@ -326,7 +332,7 @@ struct RecParams {
 template <int LOGN, bool MI>
 __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams p) {
   constexpr int N = Lay<LOGN>::N, WPG = Lay<LOGN>::WPG, L = LOGN;
-  __shared__ float xch[2][3][N];
+  __shared__ __attribute__((aligned(16))) float xch[2][3][N];
   __shared__ float ghs[2][3][N];
   // the wave index read into a scalar register, so that per-gate choices are scalar
   const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), g = wv / WPG,
@@ -442,15 +448,17 @@ __global__ __launch_bounds__(3 * (1 << LOGN) / 4) void bfly_bwd_kernel(RecParams
       constexpr int s = L - 1 - S;
       if constexpr (L == 10 && s >= 8) {
         if constexpr (s == 9) {
+          // lane-major, as in the coefficient pass
           float* xs = xch[0][g];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) xs[idx[r]] = x[r];
+          const int w = idx[0] >> 8, l = idx[0] & 63;
+          *reinterpret_cast<f4*>(xs + 256 * w + 4 * l) = f4{x[0], x[1], x[2], x[3]};
           lds_barrier();
+          const f4 p1 = *reinterpret_cast<const f4*>(xs + 256 * (w ^ 1) + 4 * l);
+          const f4 p2 = *reinterpret_cast<const f4*>(xs + 256 * (w ^ 2) + 4 * l);
+          const f4 p3 = *reinterpret_cast<const f4*>(xs + 256 * (w ^ 3) + 4 * l);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = idx[r];
-            x[r] = ((c89[0][r] * x[r] + c89[1][r] * xs[i ^ 512]) + c89[2][r] * xs[i ^ 256]) + c89[3][r] * xs[i ^ 768];
-          }
+          for (int r = 0; r < 4; ++r)
+            x[r] = ((c89[0][r] * x[r] + c89[1][r] * p2[r]) + c89[2][r] * p1[r]) + c89[3][r] * p3[r];
         }
         return;  // layer 8 is folded into layer 9's exchange
       }
@@ -524,7 +532,7 @@ struct TwParams {
 template <int LOGN>
 __global__ __launch_bounds__((1 << LOGN) / 4) void bfly_twiddle_grad(TwParams p) {
   constexpr int N = Lay<LOGN>::N, L = LOGN;
-  __shared__ float xch[2][N];
+  __shared__ __attribute__((aligned(16))) float xch[2][N];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int chunk = blockIdx.x, g = blockIdx.y, H = p.H;
   int idx[4];
