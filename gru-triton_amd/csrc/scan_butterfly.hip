@@ -117,9 +117,10 @@ __global__ __launch_bounds__(kGenericThreads) void butterfly_generic_kernel(BPar
 // i = l + 64*r + 256*w for r = 0..3. Stages with stride < 64 swap across
 // lanes: strides 1, 2, 4 and 8 with DPP moves that fold into the multiply
 // (stride 4 needs one extra move), 16 and 32 with ds_bpermute, which keeps
-// them off the VALU, the bound at three waves per SIMD (moving them to the
-// permlane swaps measured 5 % slower). Strides 64 and 128 pair registers
-// inside a lane, strides >= 256 go through LDS between the gate's waves.
+// them off the VALU (moving them to the permlane swaps measured 5 % slower at
+// three waves per SIMD, 15 % with the epilogue wave). Strides 64 and 128 pair
+// registers inside a lane, strides >= 256 go through LDS between the gate's
+// waves (at N = 1024 in lane-major order: see the layer 8 exchange).
 // Each lane keeps the two twiddles of each of its 4 elements for all L stages
 // in registers (8L values), loaded
 // once. The gate epilogue for element i runs on one of the three gate waves
@@ -289,7 +290,7 @@ __global__ __launch_bounds__(bfly_threads<LOGN>()) void butterfly_reg_kernel(BPa
         for (int r = 0; r < 4; ++r) y[r] = lane_xor_c<1 << s>(x[r]);
       } else if constexpr (s < 6) {
         // strides 16, 32: through the LDS crossbar, which keeps these moves
-        // off the VALU (the kernel's bound at three waves per SIMD)
+        // off the VALU
 #pragma unroll
         for (int r = 0; r < 4; ++r) y[r] = lane_xor(x[r], 1 << s);
       } else if constexpr (s < 8) {
